@@ -1,0 +1,265 @@
+"""ctypes wrapper of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker the GPU kernels are compared against.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module. Function names mirror the reference's
+(crates/unltd-tensor/src/quants.rs, kernels.rs); reference panics surface as
+OracleError with the same status classes as the product library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+QK_K = 256
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34}
+BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32}
+STATUS = {1: "LEN", 2: "BLOCK_MULTIPLE", 3: "DTYPE", 4: "ALLOC"}
+
+Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i4", (16,))],
+                     align=True)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what}: {STATUS.get(code, code)}")
+        self.code = code
+        self.kind = STATUS.get(code, str(code))
+
+
+def build() -> str:
+    """Compile liboracle.so with its Makefile (gcc)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        P = C.c_void_p
+        S = C.c_size_t
+        L.or_f16_to_f32.argtypes = [C.c_uint16]
+        L.or_f16_to_f32.restype = C.c_float
+        L.or_scale_min_k4.argtypes = [P, C.c_int, P, P]
+        L.or_pairwise_sum_f64.argtypes = [P, S, P]
+        L.or_pairwise_sum_f64.restype = C.c_double
+        for n in ("or_dot_f32", "or_dot_q4_k", "or_dot_q6_k", "or_dot_q8_0"):
+            getattr(L, n).argtypes = [P, P, S]
+            getattr(L, n).restype = C.c_double
+        L.or_row_bytes.argtypes = [C.c_int, S]
+        L.or_row_bytes.restype = S
+        for n in ("or_gemv_quant", "or_gemv_quant_q8k"):
+            getattr(L, n).argtypes = [P, S, P, S, P, S, S, S, C.c_int]
+            getattr(L, n).restype = C.c_int
+        for n in ("or_gemv_quant_mt", "or_gemv_quant_q8k_mt"):
+            getattr(L, n).argtypes = [P, S, P, S, P, S, S, S, C.c_int, C.c_int]
+            getattr(L, n).restype = C.c_int
+        L.or_nearest_int.argtypes = [C.c_float]
+        L.or_nearest_int.restype = C.c_int32
+        L.or_quantize_q8_k.argtypes = [P, P, S]
+        L.or_quantize_q8_k.restype = C.c_int
+        for n in ("or_dot_q4_k_q8_k", "or_dot_q6_k_q8_k"):
+            getattr(L, n).argtypes = [P, S, P]
+            getattr(L, n).restype = C.c_float
+        for n in ("or_dequantize_q4_k", "or_dequantize_q6_k", "or_dequantize_q8_0"):
+            getattr(L, n).argtypes = [P, S, P, S]
+            getattr(L, n).restype = C.c_int
+        L.or_unpack_q4_k.argtypes = [P, S, P, P, P, P, P]
+        L.or_unpack_q6_k.argtypes = [P, S, P, P, P]
+        L.or_unpack_q8_0.argtypes = [P, S, P, P]
+        L.or_swiglu.argtypes = [P, P, P, S]
+        L.or_silu.argtypes = [P, P, S]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise OracleError(rc, what)
+
+
+def f16_to_f32(h: int) -> np.float32:
+    return np.float32(lib().or_f16_to_f32(h))
+
+
+def f16_to_f32_array(h: np.ndarray) -> np.ndarray:
+    f = lib().or_f16_to_f32
+    return np.array([f(int(v)) for v in h.ravel()], dtype=np.float32).reshape(h.shape)
+
+
+def scale_min_k4(s: bytes, g: int):
+    s = np.frombuffer(bytes(s), dtype=np.uint8)
+    sc = np.zeros(1, np.uint8)
+    m = np.zeros(1, np.uint8)
+    lib().or_scale_min_k4(_p(s), g, _p(sc), _p(m))
+    return int(sc[0]), int(m[0])
+
+
+def pairwise_sum_f64(v) -> float:
+    v = np.ascontiguousarray(v, dtype=np.float64)
+    scratch = np.empty(max(len(v), 1), np.float64)
+    return lib().or_pairwise_sum_f64(_p(v), len(v), _p(scratch))
+
+
+def _u8(w) -> np.ndarray:
+    return np.ascontiguousarray(np.frombuffer(bytes(w), dtype=np.uint8)
+                                if isinstance(w, (bytes, bytearray)) else w, dtype=np.uint8)
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def dot_f32(x, w) -> float:
+    x, w = _f32(x), _f32(w)
+    assert len(x) == len(w)
+    return lib().or_dot_f32(_p(x), _p(w), len(x))
+
+
+def dot_q4_k(x, w) -> float:
+    x, w = _f32(x), _u8(w)
+    assert len(x) % QK_K == 0 and len(w) == len(x) // QK_K * 144
+    return lib().or_dot_q4_k(_p(x), _p(w), len(x))
+
+
+def dot_q6_k(x, w) -> float:
+    x, w = _f32(x), _u8(w)
+    assert len(x) % QK_K == 0 and len(w) == len(x) // QK_K * 210
+    return lib().or_dot_q6_k(_p(x), _p(w), len(x))
+
+
+def dot_q8_0(x, w) -> float:
+    x, w = _f32(x), _u8(w)
+    assert len(x) % 32 == 0 and len(w) == len(x) // 32 * 34
+    return lib().or_dot_q8_0(_p(x), _p(w), len(x))
+
+
+def row_bytes(dtype: int, n: int) -> int:
+    return lib().or_row_bytes(dtype, n)
+
+
+def gemv_quant(out: np.ndarray, x, w, dim_in: int, dim_out: int, dtype: int,
+               nthreads: int = 1) -> None:
+    x, w = _f32(x), _u8(w)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    rc = lib().or_gemv_quant_mt(_p(out), out.size, _p(x), x.size, _p(w), w.size,
+                                dim_in, dim_out, dtype, nthreads)
+    _check(rc, "gemv_quant")
+
+
+def gemv_quant_q8k(out: np.ndarray, x, w, dim_in: int, dim_out: int, dtype: int,
+                   nthreads: int = 1) -> None:
+    x, w = _f32(x), _u8(w)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    rc = lib().or_gemv_quant_q8k_mt(_p(out), out.size, _p(x), x.size, _p(w), w.size,
+                                    dim_in, dim_out, dtype, nthreads)
+    _check(rc, "gemv_quant_q8k")
+
+
+def nearest_int(f: float) -> int:
+    return lib().or_nearest_int(f)
+
+
+def quantize_q8_k(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(max(len(x) // QK_K, 1), dtype=Q8K_DTYPE)
+    _check(lib().or_quantize_q8_k(_p(out), _p(x), len(x)), "quantize_q8_k")
+    return out[: len(x) // QK_K]
+
+
+def dot_q4_k_q8_k(xq: np.ndarray, w) -> float:
+    w = _u8(w)
+    assert len(w) == len(xq) * 144
+    return float(np.float32(lib().or_dot_q4_k_q8_k(_p(xq), len(xq), _p(w))))
+
+
+def dot_q6_k_q8_k(xq: np.ndarray, w) -> float:
+    w = _u8(w)
+    assert len(w) == len(xq) * 210
+    return float(np.float32(lib().or_dot_q6_k_q8_k(_p(xq), len(xq), _p(w))))
+
+
+def _dequant(fn, out: np.ndarray, w, what):
+    w = _u8(w)
+    _check(getattr(lib(), fn)(_p(out), out.size, _p(w), w.size), what)
+
+
+def dequantize_q4_k(out: np.ndarray, w) -> None:
+    _dequant("or_dequantize_q4_k", out, w, "dequantize_q4_k")
+
+
+def dequantize_q6_k(out: np.ndarray, w) -> None:
+    _dequant("or_dequantize_q6_k", out, w, "dequantize_q6_k")
+
+
+def dequantize_q8_0(out: np.ndarray, w) -> None:
+    _dequant("or_dequantize_q8_0", out, w, "dequantize_q8_0")
+
+
+def dequantize(dtype: int, w, n: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    {Q4_K: dequantize_q4_k, Q6_K: dequantize_q6_k, Q8_0: dequantize_q8_0}[dtype](out, w)
+    return out
+
+
+def unpack_q4_k(w):
+    w = _u8(w)
+    nb = len(w) // 144
+    q = np.zeros(nb * 256, np.uint8)
+    sc = np.zeros(nb * 8, np.uint8)
+    m = np.zeros(nb * 8, np.uint8)
+    d = np.zeros(nb, np.float32)
+    dmin = np.zeros(nb, np.float32)
+    lib().or_unpack_q4_k(_p(w), nb, _p(q), _p(sc), _p(m), _p(d), _p(dmin))
+    return q, sc, m, d, dmin
+
+
+def unpack_q6_k(w):
+    w = _u8(w)
+    nb = len(w) // 210
+    q = np.zeros(nb * 256, np.uint8)
+    sc = np.zeros(nb * 16, np.int8)
+    d = np.zeros(nb, np.float32)
+    lib().or_unpack_q6_k(_p(w), nb, _p(q), _p(sc), _p(d))
+    return q, sc, d
+
+
+def unpack_q8_0(w):
+    w = _u8(w)
+    nb = len(w) // 34
+    q = np.zeros(nb * 32, np.int8)
+    d = np.zeros(nb, np.float32)
+    lib().or_unpack_q8_0(_p(w), nb, _p(q), _p(d))
+    return q, d
+
+
+def swiglu(gate, up) -> np.ndarray:
+    g, u = _f32(gate), _f32(up)
+    out = np.zeros(len(g), np.float32)
+    lib().or_swiglu(_p(out), _p(g), _p(u), len(g))
+    return out
+
+
+def silu(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(len(x), np.float32)
+    lib().or_silu(_p(out), _p(x), len(x))
+    return out
