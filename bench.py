@@ -1,0 +1,401 @@
+"""Benchmark of the quantized linear-layer path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+
+Headline workload (one "step" = one pass over one batch):
+    Q6_K output-projection GEMV, 152064 x 4096 (510,935,040 weight bytes),
+    gemv_quant semantics, weights and activations resident in HBM.
+    value = algorithmic bytes (weights + 4K + 4N) per step / wall time per
+    step, in GB/s; roofline.achieved uses HIP-event kernel time.
+Secondary workloads (reported under "extra", not the headline):
+    Q4_K GEMV 4096 x 4096 (rotated over 64 copies so the 256 MB MALL cannot
+    serve it), fused FFN gate/up Q4_K 12288 x 4096 + SwiGLU + down Q6_K
+    4096 x 12288 and a Q8_0 4096 x 4096 projection (rotated), the Q4_K prefill
+    GEMM N=12288 K=4096 over M in {1, 8, 32, 128, 512}, bit-exact
+    gemv_quant_q8k on the head, and the decode step of a synthetic 9B hybrid
+    (all quantized linear layers back-to-back, replayed as one HIP graph).
+cpu_baseline: the CPU oracle (a C restatement of the reference's scalar
+kernels) on the same head weights, timed on this host.
+Data are synthetic (seeded random GGUF blocks, N(0,1) activations).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "unltd-inference_amd")]
+
+import uq  # noqa: E402
+import uq.synth as S  # noqa: E402
+
+METRIC = "Q4_K/Q6_K GEMV achieved HBM GB/s (% of peak); decode-step linear-layer tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------- HIP plumbing
+class Hip:
+    """HIP runtime calls the timing needs (events, streams, graphs)."""
+
+    def __init__(self):
+        uq.lib()  # loads libamdhip64 into the process
+        self.h = C.CDLL("libamdhip64.so")
+        P = C.c_void_p
+        self.h.hipEventCreate.argtypes = [C.POINTER(P)]
+        self.h.hipEventRecord.argtypes = [P, P]
+        self.h.hipEventSynchronize.argtypes = [P]
+        self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), P, P]
+        self.h.hipStreamCreate.argtypes = [C.POINTER(P)]
+        self.h.hipStreamSynchronize.argtypes = [P]
+        self.h.hipStreamBeginCapture.argtypes = [P, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [P, C.POINTER(P)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(P), P, P, P, C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [P, P]
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def event(self):
+        e = C.c_void_p()
+        self.ok(self.h.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e
+
+    def stream(self):
+        s = C.c_void_p()
+        self.ok(self.h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        return s
+
+    def sync(self):
+        self.ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def record(self, e, s=None):
+        self.ok(self.h.hipEventRecord(e, s), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self.ok(self.h.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = C.c_float()
+        self.ok(self.h.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def capture(self, s, fn):
+        self.ok(self.h.hipStreamBeginCapture(s, 0), "hipStreamBeginCapture")
+        fn()
+        g = C.c_void_p()
+        self.ok(self.h.hipStreamEndCapture(s, C.byref(g)), "hipStreamEndCapture")
+        ge = C.c_void_p()
+        self.ok(self.h.hipGraphInstantiate(C.byref(ge), g, None, None, 0), "hipGraphInstantiate")
+        return ge
+
+    def launch_graph(self, ge, s):
+        self.ok(self.h.hipGraphLaunch(ge, s), "hipGraphLaunch")
+
+
+def timed(hip, fn, steps, warmup, stream=None):
+    """Run warmup untimed steps, then exactly `steps` timed ones bracketed by
+    device synchronisation; returns (wall_s, event_ms) for the whole region."""
+    for _ in range(warmup):
+        fn()
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        fn()
+    hip.record(e1, stream)
+    hip.sync()
+    wall = time.perf_counter() - t0
+    return wall, hip.elapsed_ms(e0, e1)
+
+
+def gemv_bytes(dtype, K, N):
+    return S.row_bytes(dtype, K) * N + 4 * K + 4 * N
+
+
+# ----------------------------------------------------------- workloads
+def bench_head(hip, steps, warmup):
+    K, N = 4096, 152064
+    log("head: generating Q6_K 152064 x 4096")
+    w = S.weights(S.Q6_K, N, K, seed=S.seed_for(1))
+    x = S.activations(K, seed=S.seed_for(1))
+    W = uq.Weights(w, uq.DType.Q6K, K, N)
+    dx, dy = uq.DeviceArray.from_numpy(x), uq.DeviceArray(4 * N)
+    nbytes = gemv_bytes(S.Q6_K, K, N)
+    wall, ev = timed(hip, lambda: uq.gemv(W, dx, dy), steps, warmup)
+    res = {"bytes": nbytes, "wall_s": wall, "event_ms": ev, "steps": steps,
+           "gbs_wall": nbytes * steps / wall / 1e9, "gbs_event": nbytes * steps / (ev * 1e-3) / 1e9,
+           "us_per_call": ev * 1e3 / steps}
+    wall8, ev8 = timed(hip, lambda: uq.gemv_q8k(W, dx, dy), steps, warmup)
+    res["q8k"] = {"us_per_call": ev8 * 1e3 / steps, "gbs_event": nbytes * steps / (ev8 * 1e-3) / 1e9}
+    return res, w, x, W
+
+
+def rotated(hip, make_step, ncopies, steps, warmup):
+    wall, ev = timed(hip, make_step, steps * ncopies, warmup * ncopies)
+    return wall, ev
+
+
+def bench_q4k_small(hip, steps, warmup):
+    K, N, copies = 4096, 4096, 64
+    w = S.weights(S.Q4_K, N, K, seed=S.seed_for(0))
+    x = S.activations(K, seed=S.seed_for(0))
+    Ws = [uq.Weights(w, uq.DType.Q4K, K, N) for _ in range(copies)]
+    dx, dy = uq.DeviceArray.from_numpy(x), uq.DeviceArray(4 * N)
+    state = {"i": 0}
+
+    def step():
+        uq.gemv(Ws[state["i"] % copies], dx, dy)
+        state["i"] += 1
+
+    wall, ev = timed(hip, step, steps * copies, warmup)
+    n = steps * copies
+    nbytes = gemv_bytes(S.Q4_K, K, N)
+    for W in Ws:
+        W.free()
+    return {"config": "Q4_K GEMV 4096x4096, 64 rotated copies (605 MB)", "bytes": nbytes,
+            "us_per_call": ev * 1e3 / n, "gbs_event": nbytes * n / (ev * 1e-3) / 1e9,
+            "gbs_wall": nbytes * n / wall / 1e9}
+
+
+def bench_ffn(hip, steps, warmup):
+    n, nff, copies = 4096, 12288, 6
+    g = S.weights(S.Q4_K, nff, n, seed=S.seed_for(2, 1))
+    u = S.weights(S.Q4_K, nff, n, seed=S.seed_for(2, 2))
+    d = S.weights(S.Q6_K, n, nff, seed=S.seed_for(2, 3))
+    q = S.weights(S.Q8_0, n, n, seed=S.seed_for(2, 4))
+    x = S.activations(n, seed=S.seed_for(2))
+    sets = [(uq.Weights(g, uq.DType.Q4K, n, nff), uq.Weights(u, uq.DType.Q4K, n, nff),
+             uq.Weights(d, uq.DType.Q6K, nff, n), uq.Weights(q, uq.DType.Q8_0, n, n)) for _ in range(copies)]
+    dx, dh, dy, dq = (uq.DeviceArray.from_numpy(x), uq.DeviceArray(4 * nff), uq.DeviceArray(4 * n),
+                      uq.DeviceArray(4 * n))
+    state = {"i": 0}
+
+    def step():
+        G, U, D, Q = sets[state["i"] % copies]
+        uq.ffn_swiglu(G, U, D, dx, dh, dy)
+        uq.gemv(Q, dx, dq)
+        state["i"] += 1
+
+    wall, ev = timed(hip, step, steps * copies, warmup)
+    k = steps * copies
+    wbytes = 2 * g.size + d.size + q.size
+    act = 4 * n + 2 * 4 * nff + 4 * n + 4 * n + 4 * n  # x, h written+read, y, q8_0 x and y
+    for s in sets:
+        for W in s:
+            W.free()
+    return {"config": "FFN gate/up Q4_K 12288x4096 + SwiGLU, down Q6_K 4096x12288, + Q8_0 4096x4096; "
+                      "6 rotated copies (694 MB)",
+            "weight_bytes": wbytes, "us_per_step": ev * 1e3 / k,
+            "gbs_event": (wbytes + act) * k / (ev * 1e-3) / 1e9}
+
+
+def bench_gemm(hip, steps, warmup):
+    K, N = 4096, 12288
+    w = S.weights(S.Q4_K, N, K, seed=S.seed_for(3))
+    W = uq.Weights(w, uq.DType.Q4K, K, N)
+    X = S.activations(K, seed=S.seed_for(3), rows=512)
+    dx, dy = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * 512 * N)
+    out = {}
+    for M in (1, 8, 32, 128, 512):
+        st = max(2, steps // (1 if M < 128 else 4))
+        wall, ev = timed(hip, lambda: uq.gemm(W, M, dx, dy), st, max(1, warmup // 2))
+        t = ev * 1e-3 / st
+        out[str(M)] = {"us": t * 1e6, "tflops": 2 * M * N * K / t / 1e12,
+                       "frac_bf16_peak": 2 * M * N * K / t / 1e12 / BF16_PEAK_TFLOPS,
+                       "weight_gbs": w.size / t / 1e9}
+    W.free()
+    return {"config": "Q4_K prefill GEMM N=12288 K=4096, M sweep", "by_m": out}
+
+
+def decode_layers():
+    """Synthetic Qwen3.5-style hybrid 9B: 32 layers, hidden 4096; layer il is
+    full attention when (il+1) % 4 == 0 (qwen35.rs:289-291), else GatedDeltaNet.
+    Attention-block projections and ffn_down of the 8 attention layers are
+    Q6_K, everything else Q4_K; Q6_K head with vocab 152064."""
+    n, nff = 4096, 12288
+    layers = []
+    for il in range(32):
+        attn = (il + 1) % 4 == 0
+        dt = S.Q6_K if attn else S.Q4_K
+        if attn:
+            proj = [("attn_q", dt, n, 8192), ("attn_k", dt, n, 1024), ("attn_v", dt, n, 1024),
+                    ("attn_output", dt, n, n)]
+        else:
+            proj = [("attn_qkv", S.Q4_K, n, 8192), ("attn_gate", S.Q4_K, n, n), ("ssm_beta", S.Q4_K, n, 32),
+                    ("ssm_alpha", S.Q4_K, n, 32), ("ssm_out", S.Q4_K, n, n)]
+        ffn = [("ffn_gate", S.Q4_K, n, nff), ("ffn_up", S.Q4_K, n, nff), ("ffn_down", dt, nff, n)]
+        layers.append((attn, proj, ffn))
+    return layers
+
+
+def bench_decode(hip, steps, warmup, head_w=None, head_h=None):
+    n, nff = 4096, 12288
+    layers = decode_layers()
+    cache = {}
+
+    def host_bytes(dt, K, N):
+        key = (dt, K, N)
+        if key not in cache:
+            cache[key] = S.weights(dt, N, K, seed=S.seed_for(4, len(cache) + 1))
+        return cache[key]
+
+    total = 0
+    built = []
+    for attn, proj, ffn in layers:
+        P = []
+        for name, dt, K, N in proj + ffn:
+            b = host_bytes(dt, K, N)
+            P.append(uq.Weights(b, dt, K, N))
+            total += b.size
+        built.append((attn, P))
+    head = head_h if head_h is not None else uq.Weights(S.weights(S.Q6_K, 152064, n, seed=S.seed_for(1)),
+                                                         uq.DType.Q6K, n, 152064)
+    total += S.row_bytes(S.Q6_K, n) * 152064
+    x = uq.DeviceArray.from_numpy(S.activations(n, seed=S.seed_for(4)))
+    bufs = {k: uq.DeviceArray(4 * v) for k, v in
+            (("a", 8192), ("b", 4096), ("c", 1024), ("d", 1024), ("e", 32), ("f", 32), ("o", 4096),
+             ("h", nff), ("logits", 152064))}
+    s = hip.stream()
+
+    def chain():
+        for attn, P in built:
+            if attn:
+                q, k, v, o, g, u, d = P
+                uq.gemv(q, x, bufs["a"], s)
+                uq.gemv(k, x, bufs["c"], s)
+                uq.gemv(v, x, bufs["d"], s)
+                uq.gemv(o, bufs["a"], bufs["o"], s)  # first 4096 of q stand in for the attention output
+            else:
+                qkv, z, beta, alpha, out, g, u, d = P
+                uq.gemv(qkv, x, bufs["a"], s)
+                uq.gemv(z, x, bufs["b"], s)
+                uq.gemv(beta, x, bufs["e"], s)
+                uq.gemv(alpha, x, bufs["f"], s)
+                uq.gemv(out, bufs["b"], bufs["o"], s)
+            uq.ffn_swiglu(g, u, d, bufs["o"], bufs["h"], x, s)
+        uq.gemv(head, x, bufs["logits"], s)
+
+    graph = hip.capture(s, chain)
+    wall, ev = timed(hip, lambda: hip.launch_graph(graph, s), steps, warmup, s)
+    t = ev * 1e-3 / steps
+    launches = sum(4 + 2 if a else 5 + 2 for a, _ in built) + 1
+    res = {"config": "decode step, synthetic hybrid 9B (32 layers, 24 GDN + 8 attention, FFN 12288, "
+                     "Q6_K head 152064), all quantized linear layers in one HIP graph",
+           "weight_bytes_per_token": total, "launches": launches, "ms_per_token": t * 1e3,
+           "tok_s": 1.0 / t, "gbs": total / t / 1e9, "frac_hbm_peak": total / t / 1e9 / HBM_PEAK_GBS,
+           "tok_s_wall": steps / wall}
+    for _, P in built:
+        for W in P:
+            W.free()
+    return res
+
+
+def cpu_baseline(w, x):
+    """The oracle (C restatement of quants.rs's scalar kernels) on the first
+    third of the head, 1 thread, median of 3; plus all cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    K, rows = 4096, 152064 // 3
+    ws = w[: rows * S.row_bytes(S.Q6_K, K)]
+    out = np.zeros(rows, np.float32)
+    nbytes = gemv_bytes(S.Q6_K, K, rows)
+
+    def rate(fn, nt, reps):
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn(out, x, ws, K, rows, S.Q6_K, nthreads=nt)
+            ts.append(time.perf_counter() - t)
+        return nbytes / statistics.median(ts) / 1e9
+
+    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    ncpu = min(ncpu, 16)
+    q8k_1 = rate(O.gemv_quant_q8k, 1, 3)
+    exact_1 = rate(O.gemv_quant, 1, 3)
+    q8k_all = rate(O.gemv_quant_q8k, ncpu, 3)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": q8k_1, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"gemv_quant_q8k (the reference forward's path) over rows 0..{rows} of the same "
+                      f"Q6_K head, C restatement of quants.rs built -O2 -ffp-contract=off, median of 3",
+            "gemv_quant_exact_1core_gbs": exact_1, "q8k_all_cores_gbs": q8k_all, "all_cores": ncpu,
+            "cpu_model": cpu, "nproc": os.cpu_count()}
+
+
+def load_traffic():
+    p = os.path.join(PROFILES, "q6k_head_gemv_counters.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of: head,q4k,ffn,gemm,decode")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path runs on a single "
+              f"MI355X; see DESIGN.md for how it would shard).", file=sys.stderr)
+        sys.exit(2)
+    hip = Hip()
+    log("device:", uq.device_name())
+    only = set(filter(None, a.only.split(",")))
+    head, w, x, W = bench_head(hip, a.steps, a.warmup)
+    extra = {"head_q8k_bit_exact": head["q8k"]}
+    if not a.quick:
+        for name, fn in (("q4k", bench_q4k_small), ("ffn", bench_ffn), ("gemm", bench_gemm)):
+            if not only or name in only:
+                log("bench:", name)
+                extra[name] = fn(hip, a.steps, a.warmup)
+        if not only or "decode" in only:
+            log("bench: decode")
+            extra["decode"] = bench_decode(hip, max(5, a.steps // 2), 2, head_h=W)
+    cpu = None if a.no_cpu else cpu_baseline(w, x)
+    ach = head["gbs_event"]
+    line = {
+        "metric": METRIC, "value": head["gbs_wall"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": head["wall_s"] * 1e3 / a.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8-dot4+f32",
+        "data": "synthetic (seeded random GGUF blocks, N(0,1) activations)",
+        "config": {"workload": "Q6_K output-projection GEMV 152064x4096 (gemv_quant semantics)",
+                   "dim_out": 152064, "dim_in": 4096, "weight_bytes": 510935040,
+                   "algorithmic_bytes_per_step": head["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ach / HBM_PEAK_GBS, "traffic": load_traffic()},
+        "cpu_baseline": cpu,
+        "extra": extra,
+        "host": platform.node(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

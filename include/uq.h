@@ -1,0 +1,172 @@
+/*
+ * uq.h -- C ABI of the MI355X quantized linear-layer library (libuq.so).
+ *
+ * Drop-in boundary for unltd-tensor's quantized-matmul operator API
+ * (crates/unltd-tensor/src/lib.rs:128-131 re-exports, quants.rs bodies).
+ * Every entry point below cites the reference function it replaces.
+ *
+ * Conventions
+ *  - Weights are GGUF tensors: [dim_out] rows, each row dim_in weights packed
+ *    in blocks of the row's dtype, row-major, block bytes unchanged
+ *    (quants.rs:414-421). dtype values are ggml type ids (min_forward.rs:39-48).
+ *  - The reference panics on bad arguments (assert_eq!/panic!); here every
+ *    panic class is a uq_status code, and uq_last_error() returns the
+ *    message of the calling thread's last failure. No entry point aborts.
+ *  - Host-pointer entry points (uq_gemv_quant, ...) take the reference's
+ *    slices as (pointer, length) pairs, copy to the current HIP device, run,
+ *    and copy back. They are reentrant (thread-safe, one HIP stream per
+ *    calling thread).
+ *  - Device entry points take device pointers and a hipStream_t (void*; NULL
+ *    = the null stream). They are asynchronous on that stream and allocate
+ *    no device memory. Weights live behind a uq_weights handle whose bytes
+ *    are copied to HBM unchanged.
+ *  - Numerics: uq_gemv_quant / uq_gemv / uq_gemm / uq_ffn_swiglu follow
+ *    gemv_quant's semantics (f32 result of the exact dequantized weights times
+ *    f32 x; matched within |y-r| <= 1e-4 + 1e-3*|r|). uq_gemv_quant_q8k /
+ *    uq_gemv_q8k, uq_quantize_q8_k, the dequantize and unpack exports are
+ *    bit-exact with the reference.
+ */
+#ifndef UQ_H
+#define UQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, DType mapping of dtype_of (min_forward.rs:39-48). */
+typedef enum uq_dtype {
+    UQ_F32 = 0,
+    UQ_F16 = 1, /* recognised, no dot kernel (gemv_quant panics, quants.rs:446) */
+    UQ_Q8_0 = 8,
+    UQ_Q4_K = 12,
+    UQ_Q6_K = 14
+} uq_dtype;
+
+typedef enum uq_status {
+    UQ_OK = 0,
+    UQ_ERR_LEN = 1,            /* assert_eq!(len ...): quants.rs:430-452, :482-505, :535-539 */
+    UQ_ERR_BLOCK_MULTIPLE = 2, /* dim_in % 256 != 0: quants.rs:435-439 (min_forward.rs:55-66) */
+    UQ_ERR_DTYPE = 3,          /* unsupported dtype panic: quants.rs:446, :497-499 */
+    UQ_ERR_ARG = 4,            /* null pointer, bad handle, size out of range */
+    UQ_ERR_HIP = 5,            /* HIP runtime failure (message in uq_last_error) */
+    UQ_ERR_NO_DEVICE = 6       /* no usable gfx950 device */
+} uq_status;
+
+/* Q8_K activation block, quants.rs:235-242 ({f32 d; i8 qs[256]; i32 bsums[16]}). */
+typedef struct uq_q8k_block {
+    float d;
+    int8_t qs[256];
+    int32_t bsums[16];
+} uq_q8k_block;
+
+/* Message of the calling thread's last failing call ("" if none). */
+const char *uq_last_error(void);
+/* Static name of a status code. */
+const char *uq_status_name(uq_status s);
+/* Bytes of one row of dim_in weights (min_forward.rs:52-80); 0 if refused. */
+size_t uq_row_bytes(uq_dtype dtype, size_t dim_in);
+
+/* ===================== host-pointer mirrors of unltd-tensor ============== */
+
+/* gemv_quant (quants.rs:422-466): out[j] = (f32) dot(x[..dim_in], row_j).
+ * F32, Q4_K, Q6_K as the reference; Q8_0 accepted (GGUF closed form) where
+ * the reference panics. x_len >= dim_in (x may be longer, :431). */
+uq_status uq_gemv_quant(float *out, size_t out_len, const float *x, size_t x_len,
+                        const uint8_t *w, size_t w_len, size_t dim_in,
+                        size_t dim_out, uq_dtype dtype);
+
+/* gemv_quant_q8k (quants.rs:474-515): x quantized to Q8_K once, each row dotted
+ * with dot_q4_k_q8_k / dot_q6_k_q8_k. Q4_K and Q6_K only. Bit-exact. */
+uq_status uq_gemv_quant_q8k(float *out, size_t out_len, const float *x,
+                            size_t x_len, const uint8_t *w, size_t w_len,
+                            size_t dim_in, size_t dim_out, uq_dtype dtype);
+
+/* quantize_q8_k (quants.rs:250-290): x_len % 256 == 0, out_blocks == x_len/256. */
+uq_status uq_quantize_q8_k(uq_q8k_block *out, size_t out_blocks, const float *x,
+                           size_t x_len);
+
+/* dequantize_q4_k (quants.rs:534-567): w_len == out_len/256*144, bit-exact. */
+uq_status uq_dequantize_q4_k(float *out, size_t out_len, const uint8_t *w,
+                             size_t w_len);
+/* Q6_K to f32: w = d*(sc*q), the exact product dot_q6_k forms (quants.rs:195);
+ * no reference function exists, bit-exact with that product. */
+uq_status uq_dequantize_q6_k(float *out, size_t out_len, const uint8_t *w,
+                             size_t w_len);
+/* Q8_0 to f32: w = d*q (GGUF closed form; no reference kernel). */
+uq_status uq_dequantize_q8_0(float *out, size_t out_len, const uint8_t *w,
+                             size_t w_len);
+
+/* Integer unpack of the element maps (quants.rs:146-151 for Q4_K, :185-194 for
+ * Q6_K): per block 256 quants (Q4_K nibble 0..15; Q6_K raw 6-bit 0..63, the
+ * reference's q is raw-32), the per-group scales and the f32 block scales
+ * (f16_to_f32, quants.rs:44-72). Debug exports for bit-exact checks. */
+uq_status uq_unpack_q4_k(const uint8_t *w, size_t nblocks, uint8_t *q,
+                         uint8_t *sc, uint8_t *m, float *d, float *dmin);
+uq_status uq_unpack_q6_k(const uint8_t *w, size_t nblocks, uint8_t *q,
+                         int8_t *sc, float *d);
+uq_status uq_unpack_q8_0(const uint8_t *w, size_t nblocks, int8_t *q, float *d);
+
+/* f16_to_f32 (quants.rs:44-72) over an array, on the device; bit-exact
+ * including the reference's quiet-NaN canonicalisation. */
+uq_status uq_f16_to_f32(float *out, const uint16_t *h, size_t n);
+
+/* swiglu (kernels.rs:174-182): out = (g/(1+expf(-g)))*u, f32. */
+uq_status uq_swiglu(float *out, const float *gate, const float *up, size_t n);
+
+/* ========================= device-resident API ========================== */
+
+typedef struct uq_weights_s *uq_weights;
+
+/* Copy one GGUF tensor's bytes to HBM unchanged. nbytes must equal
+ * uq_row_bytes(dtype, dim_in) * dim_out (checked like gemv_quant, :448-452).
+ * Uploads to the current HIP device. */
+uq_status uq_weights_upload(uq_weights *out, const void *bytes, size_t nbytes,
+                            uq_dtype dtype, size_t dim_in, size_t dim_out);
+uq_status uq_weights_free(uq_weights w);
+/* Shape of a handle (any pointer may be NULL). */
+uq_status uq_weights_info(uq_weights w, uq_dtype *dtype, size_t *dim_in,
+                          size_t *dim_out, size_t *nbytes);
+
+/* d_y[dim_out] = W . d_x[dim_in] with gemv_quant semantics (quants.rs:422-466). */
+uq_status uq_gemv(uq_weights w, const float *d_x, float *d_y, void *stream);
+
+/* d_y = gemv_quant_q8k(W, d_x) (quants.rs:474-515), bit-exact. */
+uq_status uq_gemv_q8k(uq_weights w, const float *d_x, float *d_y, void *stream);
+
+/* Batched prefill: d_y[m][dim_out] = W . d_x[m][dim_in] for m < m_rows, with
+ * gemv_quant semantics per row (the reference feeds prefill tokens one at a
+ * time, greedy.rs:55-65; each row equals gemv_quant of that token). */
+uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
+                  void *stream);
+
+/* Gated FFN of one token (qwen35_forward.rs:713-768): d_h = swiglu(gate.x, up.x)
+ * (kernels.rs:174-182) computed in the GEMV epilogue, then d_y = down.d_h.
+ * gate/up: [n_ff][n]; down: [n][n_ff]. d_h holds n_ff floats. */
+uq_status uq_ffn_swiglu(uq_weights gate, uq_weights up, uq_weights down,
+                        const float *d_x, float *d_h, float *d_y, void *stream);
+
+/* Device f32 dequantization of a whole handle into d_out[dim_out*dim_in]
+ * (dequantize_q4_k semantics, bit-exact; Q6_K/Q8_0 closed forms). */
+uq_status uq_dequantize(uq_weights w, float *d_out, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Device memory and stream plumbing for callers without their own HIP
+ * binding (the Rust FFI crate, the ctypes tests). Thin wrappers over the
+ * HIP runtime of the current device.
+ * --------------------------------------------------------------------- */
+uq_status uq_device_count(int *n);
+uq_status uq_device_name(char *buf, size_t len);
+uq_status uq_malloc(void **d_ptr, size_t nbytes);
+uq_status uq_free(void *d_ptr);
+uq_status uq_memcpy_htod(void *d_dst, const void *src, size_t nbytes, void *stream);
+uq_status uq_memcpy_dtoh(void *dst, const void *d_src, size_t nbytes, void *stream);
+uq_status uq_memcpy_dtod(void *d_dst, const void *d_src, size_t nbytes, void *stream);
+uq_status uq_stream_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* UQ_H */

@@ -1,0 +1,85 @@
+"""libuq.so without a GPU: it loads, exports every symbol include/uq.h
+declares, refuses bad arguments with the reference's panic classes before
+touching a device, and fails loudly (no CPU fallback) when no GPU exists."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import uq
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "uq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(uq_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = uq.lib()
+    names = declared_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(uq.SIGNATURES), set(names) ^ set(uq.SIGNATURES)
+
+
+def test_row_bytes():  # min_forward.rs:270-282
+    assert uq.row_bytes(uq.DType.F32, 4096) == 16384
+    assert uq.row_bytes(uq.DType.Q4K, 4096) == 16 * 144
+    assert uq.row_bytes(uq.DType.Q6K, 4096) == 16 * 210
+    assert uq.row_bytes(uq.DType.Q8_0, 64) == 2 * 34
+    assert uq.row_bytes(uq.DType.Q4K, 4097) == 0 and uq.row_bytes(uq.DType.Q8_0, 33) == 0
+
+
+def _raises(kind, fn, *a):
+    with pytest.raises(uq.UqError) as e:
+        fn(*a)
+    assert e.value.kind == kind, str(e.value)
+
+
+def test_gemv_quant_argument_errors_mirror_reference_panics():  # quants.rs:430-452
+    w = np.zeros(144 * 2, np.uint8)
+    x = np.zeros(256, np.float32)
+    _raises("LEN", uq.gemv_quant, np.zeros(3, np.float32), x, w, 256, 2, uq.DType.Q4K)
+    _raises("LEN", uq.gemv_quant, np.zeros(2, np.float32), x[:100], w, 256, 2, uq.DType.Q4K)
+    _raises("BLOCK_MULTIPLE", uq.gemv_quant, np.zeros(2, np.float32), x, w, 128, 2, uq.DType.Q4K)
+    _raises("DTYPE", uq.gemv_quant, np.zeros(2, np.float32), x, w, 256, 2, uq.DType.F16)
+    _raises("LEN", uq.gemv_quant, np.zeros(2, np.float32), x, w[:-1], 256, 2, uq.DType.Q4K)
+    _raises("BLOCK_MULTIPLE", uq.gemv_quant, np.zeros(1, np.float32), x, np.zeros(34, np.uint8), 16, 1,
+            uq.DType.Q8_0)
+
+
+def test_gemv_quant_q8k_argument_errors():  # quants.rs:482-505
+    w = np.zeros(144 * 2, np.uint8)
+    x = np.zeros(256, np.float32)
+    _raises("DTYPE", uq.gemv_quant_q8k, np.zeros(2, np.float32), x, w, 256, 2, uq.DType.F32)
+    _raises("DTYPE", uq.gemv_quant_q8k, np.zeros(2, np.float32), x, w, 256, 2, uq.DType.Q8_0)
+    _raises("BLOCK_MULTIPLE", uq.gemv_quant_q8k, np.zeros(2, np.float32), x, w, 128, 2, uq.DType.Q4K)
+    _raises("LEN", uq.gemv_quant_q8k, np.zeros(1, np.float32), x, w, 256, 2, uq.DType.Q4K)
+
+
+def test_dequant_and_quantize_argument_errors():  # quants.rs:535-539, :251-255
+    _raises("LEN", uq.dequantize_q4_k, np.zeros(512, np.float32), np.zeros(144, np.uint8))
+    _raises("LEN", uq.dequantize_q4_k, np.zeros(300, np.float32), np.zeros(144, np.uint8))
+    _raises("LEN", uq.dequantize_q6_k, np.zeros(256, np.float32), np.zeros(209, np.uint8))
+    _raises("BLOCK_MULTIPLE", uq.quantize_q8_k, np.zeros(100, np.float32))
+
+
+def test_empty_shapes_need_no_device():
+    out = np.zeros(0, np.float32)
+    uq.gemv_quant(out, np.zeros(256, np.float32), np.zeros(0, np.uint8), 256, 0, uq.DType.Q4K)
+    out = np.full(3, 7.0, np.float32)
+    uq.gemv_quant(out, np.zeros(0, np.float32), np.zeros(0, np.uint8), 0, 3, uq.DType.Q4K)
+    assert np.all(out == 0.0)  # empty dot = 0 (pairwise_sum of nothing, kernels.rs:41)
+
+
+@pytest.mark.skipif(uq.device_count() > 0, reason="a GPU is present")
+def test_compute_fails_loudly_without_gpu():
+    x = np.zeros(256, np.float32)
+    w = np.zeros(144, np.uint8)
+    _raises("NO_DEVICE", uq.gemv_quant, np.zeros(1, np.float32), x, w, 256, 1, uq.DType.Q4K)
+    _raises("NO_DEVICE", uq.Weights, w, uq.DType.Q4K, 256, 1)

@@ -1,0 +1,65 @@
+"""Build recipe for libuq.so (gfx950) and libuq_emu.so (host emulation).
+
+    python unltd-inference_amd/build.py
+
+libuq.so: every csrc/*.hip plus uq_abi.cpp, compiled by hipcc for gfx950
+  only, -O3, FP contraction off (FMAs are written explicitly), f32
+  denormals kept, packed-FP32 instructions disabled.
+libuq_emu.so: csrc/uq_emu.cpp with g++: the kernels' per-lane code run on
+  the CPU, used by the CPU test-suite.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libuq.so")
+EMU = os.path.join(HERE, "libuq_emu.so")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
+                    if "packed-fp32-ops" not in l)  # host pass ignores the device feature
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def build_lib(verbose: bool = False) -> str:
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + [os.path.join(CSRC, "uq_abi.cpp")]
+    tmp = LIB + ".tmp"
+    _run(["hipcc", *HIPCC_FLAGS, "-x", "hip", *srcs, "-o", tmp], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_emu(verbose: bool = False) -> str:
+    tmp = EMU + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+          "-Wall", os.path.join(CSRC, "uq_emu.cpp"), "-o", tmp], verbose)
+    os.replace(tmp, EMU)
+    return EMU
+
+
+def build(verbose: bool = False):
+    return build_lib(verbose), build_emu(verbose)
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,485 @@
+// Decode GEMV kernels for gfx950 (bandwidth-bound, no MFMA).
+//
+// gemv_kernel      gemv_quant semantics (quants.rs:422-466): y = W x, f32
+//                  result of the exact dequantized weights times f32 x.
+// gemv_q8k_kernel  gemv_quant_q8k (quants.rs:474-515), bit-exact: x is
+//                  quantized to Q8_K in the workgroup, each block's eight
+//                  i32 lanes come from integer dots, and the f32 epilogue
+//                  replays the reference's operation order per row.
+//
+// Common structure: a workgroup of 4 waves prepares the activations in LDS
+// once; each wave then walks rows (stride = all waves of the grid). In a
+// row every lane owns the same 64-weight task (uq_policies.h), so its
+// activation data is read from LDS once and stays in VGPRs while the next
+// row's weights are prefetched with 128-bit loads. Row sums are reduced
+// across the wave with DPP.
+#include "uq_device.h"
+#include "uq_internal.h"
+#include "uq_policies.h"
+
+namespace uq {
+
+namespace {
+
+constexpr int WAVES = 4;
+constexpr int TPB = 64 * WAVES;
+constexpr size_t kLdsCap = 64 * 1024;
+
+int num_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+// ---------------------------- gemv_quant -----------------------------------
+__host__ __device__ inline size_t planes_bytes(int K) {
+    return 3 * (size_t)K + (size_t)(K / 32) * 4 + (size_t)(K / 16) * 4;
+}
+
+__device__ inline XPlanes planes_at(uint8_t *lds, int K) {
+    XPlanes P;
+    P.p0 = (uint32_t *)lds;
+    P.p1 = (uint32_t *)(lds + K);
+    P.p2 = (uint32_t *)(lds + 2 * K);
+    P.scale = (float *)(lds + 3 * K);
+    P.xs16 = (int *)(lds + 3 * K + (K / 32) * 4);
+    return P;
+}
+
+__device__ inline float swiglu1(float g, float u) {
+    // kernels.rs:174-182: (t / (1 + expf(-t))) * up, all f32
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+}
+
+// PAIR: W and W2 (gate, up) share x; writes swiglu(W x, W2 x).
+template <class F, bool CACHED, bool PAIR>
+__global__ __launch_bounds__(TPB) void gemv_kernel(const uint8_t *__restrict__ W,
+                                                   const uint8_t *__restrict__ W2,
+                                                   size_t row_bytes, int K, int N,
+                                                   const float *__restrict__ x,
+                                                   float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const XPlanes P = planes_at(lds, K);
+    prep_x_planes(x, K, P);
+    __syncthreads();
+    const XPlanesView PV{P.p0, P.p1, P.p2, P.scale, P.xs16};
+
+    const int lane = threadIdx.x & 63;
+    const int ntask = F::ntasks(K);
+    const typename F::LC c = F::lane_consts(lane);
+    const int wave = blockIdx.x * WAVES + (threadIdx.x >> 6);
+    const int nwave = gridDim.x * WAVES;
+
+    if (CACHED) {
+        const bool active = lane < ntask;
+        typename F::XS xs;
+        if (active) F::load_x(xs, PV, lane, c);
+        int row = wave;
+        if (row >= N) return;
+        typename F::Frag cur{}, cur2{}, nxt{}, nxt2{};
+        if (active) {
+            cur = F::load_w(W + (size_t)row * row_bytes, lane, c);
+            if (PAIR) cur2 = F::load_w(W2 + (size_t)row * row_bytes, lane, c);
+        }
+        for (; row < N; row += nwave) {
+            const int nrow = row + nwave;
+            if (active && nrow < N) {
+                nxt = F::load_w(W + (size_t)nrow * row_bytes, lane, c);
+                if (PAIR) nxt2 = F::load_w(W2 + (size_t)nrow * row_bytes, lane, c);
+            }
+            float g = 0.0f, u = 0.0f;
+            if (active) {
+                g = F::dot(cur, xs, c);
+                if (PAIR) u = F::dot(cur2, xs, c);
+            }
+            g = wave_sum(g);
+            if (PAIR) {
+                u = wave_sum(u);
+                if (lane == 0) y[row] = swiglu1(g, u);
+            } else if (lane == 0) {
+                y[row] = g;
+            }
+            cur = nxt;
+            if (PAIR) cur2 = nxt2;
+        }
+    } else {
+        for (int row = wave; row < N; row += nwave) {
+            const uint8_t *R = W + (size_t)row * row_bytes;
+            float g = 0.0f, u = 0.0f;
+            for (int t = lane; t < ntask; t += 64) {
+                typename F::XS xs;
+                F::load_x(xs, PV, t, c);
+                g += F::dot(F::load_w(R, t, c), xs, c);
+                if (PAIR) u += F::dot(F::load_w(W2 + (size_t)row * row_bytes, t, c), xs, c);
+            }
+            g = wave_sum(g);
+            if (PAIR) {
+                u = wave_sum(u);
+                if (lane == 0) y[row] = swiglu1(g, u);
+            } else if (lane == 0) {
+                y[row] = g;
+            }
+        }
+    }
+}
+
+// Generic fallback (F32 rows, Q8_0 with K % 64 != 0, K beyond the LDS
+// budget): one wave per row, f32 dequantization and FMA.
+__device__ __forceinline__ float deq_elem(uq_dtype dt, const uint8_t *row, int e) {
+    if (dt == UQ_F32) return ((const float *)row)[e];
+    if (dt == UQ_Q8_0) {
+        const uint8_t *b = row + (e >> 5) * BQ8_0;
+        return f16_bits_exact(b[0] | (b[1] << 8)) * (float)(int8_t)b[2 + (e & 31)];
+    }
+    if (dt == UQ_Q4_K) {
+        const uint8_t *b = row + (e >> 8) * BQ4K;
+        const int l = e & 255, g = l >> 5;
+        const uint8_t *s = b + 4;
+        uint32_t sc, m;
+        if (g < 4) {
+            sc = s[g] & 63;
+            m = s[g + 4] & 63;
+        } else {
+            sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+            m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+        }
+        const uint8_t byte = b[16 + 32 * (g >> 1) + (l & 31)];
+        const uint32_t nib = (g & 1) ? (byte >> 4) : (byte & 0xF);
+        return (f16_bits_exact(b[0] | (b[1] << 8)) * (float)sc) * (float)nib -
+               f16_bits_exact(b[2] | (b[3] << 8)) * (float)m;
+    }
+    const uint8_t *b = row + (e >> 8) * BQ6K;
+    const int l = e & 255;
+    const uint8_t byte = b[64 * (l / 128) + (l % 64)];
+    const int nib = ((l / 64) % 2 == 0) ? (byte & 0xF) : (byte >> 4);
+    const int hi2 = (b[128 + (l % 32) + 32 * (l / 128)] >> (2 * ((l % 128) / 32))) & 3;
+    return f16_bits_exact(b[208] | (b[209] << 8)) *
+           ((float)(int8_t)b[192 + l / 16] * (float)((nib | (hi2 << 4)) - 32));
+}
+
+__global__ __launch_bounds__(TPB) void gemv_generic_kernel(uq_dtype dt, const uint8_t *__restrict__ W,
+                                                           const uint8_t *__restrict__ W2,
+                                                           size_t row_bytes, int K, int N,
+                                                           const float *__restrict__ x,
+                                                           float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    for (int row = blockIdx.x * WAVES + (threadIdx.x >> 6); row < N; row += gridDim.x * WAVES) {
+        const uint8_t *R = W + (size_t)row * row_bytes;
+        float g = 0.0f, u = 0.0f;
+        for (int e = lane; e < K; e += 64) {
+            g = fmaf(x[e], deq_elem(dt, R, e), g);
+            if (W2) u = fmaf(x[e], deq_elem(dt, W2 + (size_t)row * row_bytes, e), u);
+        }
+        g = wave_sum(g);
+        if (W2) {
+            u = wave_sum(u);
+            if (lane == 0) y[row] = swiglu1(g, u);
+        } else if (lane == 0) {
+            y[row] = g;
+        }
+    }
+}
+
+template <class F, bool PAIR>
+hipError_t launch_fast(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out;
+    const size_t lds = planes_bytes(K);
+    // >= 2 rows per wave so the prep is amortised; at most 4 workgroups per CU
+    int grid = (N + 2 * WAVES - 1) / (2 * WAVES);
+    const int cap = num_cus() * 4;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    if (F::ntasks(K) <= 64)
+        hipLaunchKernelGGL((gemv_kernel<F, true, PAIR>), dim3(grid), dim3(TPB), lds, s, w.bytes, w2,
+                           w.row_bytes, K, N, x, y);
+    else
+        hipLaunchKernelGGL((gemv_kernel<F, false, PAIR>), dim3(grid), dim3(TPB), lds, s, w.bytes, w2,
+                           w.row_bytes, K, N, x, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_any(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out;
+    if (N == 0) return hipSuccess;
+    const bool pair = w2 != nullptr, fits = planes_bytes(K) <= kLdsCap;
+    if (fits && w.dtype == UQ_Q4_K)
+        return pair ? launch_fast<Q4K, true>(w, w2, x, y, s) : launch_fast<Q4K, false>(w, w2, x, y, s);
+    if (fits && w.dtype == UQ_Q6_K)
+        return pair ? launch_fast<Q6K, true>(w, w2, x, y, s) : launch_fast<Q6K, false>(w, w2, x, y, s);
+    if (fits && w.dtype == UQ_Q8_0 && K % 64 == 0)
+        return pair ? launch_fast<Q80, true>(w, w2, x, y, s) : launch_fast<Q80, false>(w, w2, x, y, s);
+    int grid = (N + WAVES - 1) / WAVES;
+    if (grid > num_cus() * 8) grid = num_cus() * 8;
+    hipLaunchKernelGGL(gemv_generic_kernel, dim3(grid), dim3(TPB), 0, s, w.dtype, w.bytes, w2,
+                       w.row_bytes, K, N, x, y);
+    return hipGetLastError();
+}
+
+// ---------------------------- gemv_quant_q8k -------------------------------
+// quantize_q8_k (quants.rs:250-290) of one 256-block by one wave into LDS:
+// q = 64 dwords of qs, bs = 16 bsums, *d = block scale.
+__device__ void quantize_block_lds(const float *__restrict__ c, int lane, uint32_t *q, int *bs, float *dq) {
+    float v[4];
+    float am = 0.0f, mx = 0.0f;
+    int idx = 0x7FFFFFFF;
+    for (int i = 0; i < 4; i++) {
+        v[i] = c[lane * 4 + i];
+        const float a = fabsf(v[i]);
+        if (a > am) {
+            am = a;
+            mx = v[i];
+            idx = lane * 4 + i;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {  // first strict argmax of |x|
+        const float oam = __shfl_xor(am, off);
+        const float omx = __shfl_xor(mx, off);
+        const int oidx = __shfl_xor(idx, off);
+        if (oam > am || (oam == am && oidx < idx)) {
+            am = oam;
+            mx = omx;
+            idx = oidx;
+        }
+    }
+    uint32_t packed = 0;
+    int s = 0;
+    if (am != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, mx);
+        for (int i = 0; i < 4; i++) {
+            const float val = __fadd_rn(__fmul_rn(iscale, v[i]), 12582912.0f);
+            int qv = (int)(__float_as_uint(val) & 0x007FFFFFu) - 0x00400000;
+            qv = qv < 127 ? qv : 127;
+            packed |= ((uint32_t)qv & 0xFF) << (8 * i);
+            s += qv;
+        }
+        if (lane == 0) *dq = __fdiv_rn(1.0f, iscale);
+    } else if (lane == 0) {
+        *dq = 0.0f;
+    }
+    q[lane] = packed;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((lane & 3) == 0) bs[lane >> 2] = s;
+}
+
+struct Q8KLayout {
+    size_t xq, d8, region, total;  // byte offsets
+    int R;                         // rows per epilogue batch
+};
+
+template <class F>
+__host__ __device__ inline Q8KLayout q8k_layout(int K) {
+    const int nblk = K >> 8, ntask = 4 * nblk;
+    const int dw = F::kDw;
+    Q8KLayout L;
+    L.xq = 0;
+    L.d8 = (size_t)ntask * dw * 4;
+    L.region = (L.d8 + (size_t)nblk * 4 + 15) & ~(size_t)15;
+    int R = (int)(32768 / ((size_t)WAVES * nblk * 40));
+    L.R = R < 1 ? 1 : (R > 8 ? 8 : R);
+    const size_t prep = (size_t)K + (size_t)(K / 16) * 4;
+    const size_t recs = (size_t)WAVES * L.R * nblk * 40;
+    L.total = L.region + (prep > recs ? prep : recs);
+    return L;
+}
+
+template <class F, bool CACHED>
+__global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                       int K, int N, const float *__restrict__ x,
+                                                       float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const Q8KLayout L = q8k_layout<F>(K);
+    const int nblk = K >> 8, ntask = 4 * nblk, R = L.R;
+    uint32_t *xq = (uint32_t *)(lds + L.xq);
+    float *d8 = (float *)(lds + L.d8);
+    uint32_t *qtmp = (uint32_t *)(lds + L.region);
+    int *bst = (int *)(lds + L.region + K);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+
+    for (int b = wid; b < nblk; b += WAVES) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    __syncthreads();
+    for (int t = threadIdx.x; t < ntask; t += TPB)
+        F::build_task(xq + (size_t)t * F::kDw, qtmp + 64 * (t >> 2), bst + 16 * (t >> 2), t & 3);
+    __syncthreads();  // the prep region becomes the per-wave record area
+
+    uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)wid * R * nblk * 10;
+    const typename F::LC c = F::lane_consts(lane);
+    const int wave = blockIdx.x * WAVES + wid, nwave = gridDim.x * WAVES;
+    const int iters = (ntask + 63) / 64;
+    typename F::XS xs0;
+    if (CACHED && lane < ntask) F::load_x(xs0, xq, lane);
+
+    int slot = 0;
+    for (int row = wave; row < N; row += nwave) {
+        const uint8_t *Rw = W + (size_t)row * row_bytes;
+        for (int it = 0; it < iters; it++) {
+            const int t = lane + 64 * it;
+            int S[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
+            uint32_t h = 0;
+            if (t < ntask) {
+                typename F::XS xsl;
+                if (!CACHED) F::load_x(xsl, xq, t);
+                const typename F::Frag f = F::load_w(Rw, t, c);
+                F::dot(f, CACHED ? xs0 : xsl, c, S, M);
+                h = F::hdr(f);
+            }
+            // the four tasks of a block are one lane quad: sum them
+#pragma unroll
+            for (int k = 0; k < 8; k++) S[k] = group4_sum_i(S[k]);
+            if (F::kMin) M = group4_sum_i(M);
+            if (t < ntask) {
+                const int q = t & 3;
+                uint32_t *r = rec + ((size_t)slot * nblk + (t >> 2)) * 10;
+                r[2 * q] = (uint32_t)S[2 * q];
+                r[2 * q + 1] = (uint32_t)S[2 * q + 1];
+                if (q == 0) {
+                    r[8] = (uint32_t)M;
+                    r[9] = h;
+                }
+            }
+        }
+        slot++;
+        if (slot == R || row + nwave >= N) {
+            // epilogue (quants.rs:343-358 / :402-411): lane (r, k) replays
+            // sums[k] += d*sumi[k] over the blocks in order; k = 0 also
+            // replays sumf -= dmin*minsum; then s = sumf + sums[0] + ... + sums[7].
+            __builtin_amdgcn_wave_barrier();
+            const int r = lane >> 3, k = lane & 7;
+            float sums = 0.0f, sumf = 0.0f;
+            if (r < slot) {
+                for (int kb = 0; kb < nblk; kb++) {
+                    const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
+                    const uint32_t hw = rr[9];
+                    const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                    sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
+                    if (F::kMin && k == 0) {
+                        const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                        sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
+                    }
+                }
+            }
+            float s = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) s = __fadd_rn(s, __shfl(sums, (lane & ~7) + kk));
+            if (k == 0 && r < slot) y[row - (slot - 1 - r) * nwave] = s;
+            __builtin_amdgcn_wave_barrier();
+            slot = 0;
+        }
+    }
+}
+
+// Any K (multiple of 256) the fast kernel cannot hold: one thread per row
+// running the reference loop verbatim on the workgroup's Q8_K blocks.
+__global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, const uint8_t *__restrict__ W,
+                                                               size_t row_bytes, int K, int N,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int nblk = K >> 8;
+    uint32_t *q = (uint32_t *)lds;
+    int *bs = (int *)(lds + K);
+    float *d8 = (float *)(lds + K + (K / 16) * 4);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    for (int b = wid; b < nblk; b += WAVES) quantize_block_lds(x + 256 * b, lane, q + 64 * b, bs + 16 * b, d8 + b);
+    __syncthreads();
+    const int8_t *qs = (const int8_t *)q;
+    for (int row = blockIdx.x * TPB + threadIdx.x; row < N; row += gridDim.x * TPB) {
+        const uint8_t *Rw = W + (size_t)row * row_bytes;
+        float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sumf = 0.0f;
+        for (int b = 0; b < nblk; b++) {
+            int sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            const int8_t *q8 = qs + 256 * b;
+            if (dt == UQ_Q4_K) {
+                const uint8_t *blk = Rw + (size_t)b * BQ4K;
+                const uint8_t *s = blk + 4;
+                int sc[8], m[8];
+                for (int g = 0; g < 8; g++) {
+                    if (g < 4) {
+                        sc[g] = s[g] & 63;
+                        m[g] = s[g + 4] & 63;
+                    } else {
+                        sc[g] = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+                        m[g] = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+                    }
+                }
+                for (int e = 0; e < 256; e++) {
+                    const int pos = e % 64;
+                    const uint8_t byte = blk[16 + 32 * (e / 64) + pos % 32];
+                    const int a = pos < 32 ? (byte & 0xF) : (byte >> 4);
+                    sumi[e % 8] += sc[e / 32] * a * q8[e];
+                }
+                const float d = __fmul_rn(d8[b], f16_bits_exact(blk[0] | (blk[1] << 8)));
+                for (int k = 0; k < 8; k++) sums[k] = __fadd_rn(sums[k], __fmul_rn(d, (float)sumi[k]));
+                int minsum = 0;
+                for (int g = 0; g < 16; g++) minsum += bs[16 * b + g] * m[g / 2];
+                const float dmin = __fmul_rn(f16_bits_exact(blk[2] | (blk[3] << 8)), d8[b]);
+                sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)minsum));
+            } else {
+                const uint8_t *blk = Rw + (size_t)b * BQ6K;
+                for (int e = 0; e < 256; e++) {
+                    const int pos = e % 128;
+                    const uint8_t byte = blk[64 * (e / 128) + pos % 64];
+                    const int nib = pos < 64 ? (byte & 0xF) : (byte >> 4);
+                    const int hi2 = (blk[128 + 32 * (e / 128) + pos % 32] >> (2 * (pos / 32))) & 3;
+                    sumi[e % 8] += (int)(int8_t)blk[192 + e / 16] * ((nib | (hi2 << 4)) - 32) * q8[e];
+                }
+                const float d = __fmul_rn(d8[b], f16_bits_exact(blk[208] | (blk[209] << 8)));
+                for (int k = 0; k < 8; k++) sums[k] = __fadd_rn(sums[k], __fmul_rn(d, (float)sumi[k]));
+            }
+        }
+        float s = sumf;
+        for (int k = 0; k < 8; k++) s = __fadd_rn(s, sums[k]);
+        y[row] = s;
+    }
+}
+
+template <class F>
+hipError_t launch_q8k_fast(const WeightsView &w, const float *x, float *y, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out;
+    const Q8KLayout L = q8k_layout<F>(K);
+    int grid = (N + 2 * WAVES - 1) / (2 * WAVES);
+    const int cap = num_cus() * 4;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    if (F::ntasks(K) <= 64)
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, true>), dim3(grid), dim3(TPB), L.total, s, w.bytes,
+                           w.row_bytes, K, N, x, y);
+    else
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, false>), dim3(grid), dim3(TPB), L.total, s, w.bytes,
+                           w.row_bytes, K, N, x, y);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const WeightsView &w, const float *x, float *y, hipStream_t s) {
+    return launch_any(w, nullptr, x, y, s);
+}
+
+hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, const float *x, float *h,
+                                 hipStream_t s) {
+    return launch_any(g, u.bytes, x, h, s);
+}
+
+hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out;
+    if (N == 0) return hipSuccess;
+    if (w.dtype == UQ_Q4_K && q8k_layout<Q4KQ8>(K).total <= kLdsCap) return launch_q8k_fast<Q4KQ8>(w, x, y, s);
+    if (w.dtype == UQ_Q6_K && q8k_layout<Q6KQ8>(K).total <= kLdsCap) return launch_q8k_fast<Q6KQ8>(w, x, y, s);
+    const size_t lds = (size_t)K + (size_t)(K / 16) * 4 + (size_t)(K / 256) * 4;
+    if (lds > kLdsCap) return hipErrorInvalidValue;
+    int grid = (N + TPB - 1) / TPB;
+    if (grid > num_cus() * 4) grid = num_cus() * 4;
+    hipLaunchKernelGGL(gemv_q8k_generic_kernel, dim3(grid), dim3(TPB), lds, s, w.dtype, w.bytes,
+                       w.row_bytes, K, N, x, y);
+    return hipGetLastError();
+}
+
+}  // namespace uq

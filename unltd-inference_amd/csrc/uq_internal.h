@@ -1,0 +1,68 @@
+// Internal declarations shared by the C-ABI host code and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/uq.h"
+
+// Device copies of weights carry this many bytes of zero padding after the
+// tensor, so that dword windows of the last block (Q6_K scales/d, Q8_0 pairs)
+// never read past the allocation.
+#define UQ_WEIGHT_PAD 256
+
+struct uq_weights_s {
+    uint32_t magic;
+    int device;
+    uq_dtype dtype;
+    size_t dim_in, dim_out, row_bytes, nbytes;
+    uint8_t *d_bytes;  // nbytes + UQ_WEIGHT_PAD, 256-byte aligned
+};
+#define UQ_WEIGHTS_MAGIC 0x55515754u
+
+namespace uq {
+
+// Block geometry (quants.rs:33-39, gguf.rs:202).
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int BQ4K = 144;
+constexpr int BQ6K = 210;
+constexpr int BQ8_0 = 34;
+
+struct WeightsView {
+    const uint8_t *bytes;
+    uq_dtype dtype;
+    int dim_in, dim_out;
+    size_t row_bytes;
+};
+
+inline WeightsView view(const uq_weights_s &w) {
+    return WeightsView{w.d_bytes, w.dtype, (int)w.dim_in, (int)w.dim_out, w.row_bytes};
+}
+
+// ---- launchers (each returns the launch error; no allocation) -------------
+hipError_t launch_unpack(uq_dtype dt, const uint8_t *w, size_t nblocks, void *q,
+                         void *sc, uint8_t *m, float *d, float *dmin, hipStream_t s);
+hipError_t launch_dequant(uq_dtype dt, const uint8_t *w, size_t nelem, float *out,
+                          hipStream_t s);
+hipError_t launch_f16_to_f32(const uint16_t *h, size_t n, float *out, hipStream_t s);
+hipError_t launch_swiglu(const float *g, const float *u, size_t n, float *out,
+                         hipStream_t s);
+hipError_t launch_quantize_q8k(const float *x, size_t n, uq_q8k_block *out,
+                               hipStream_t s);
+
+// y = W x with gemv_quant semantics.
+hipError_t launch_gemv(const WeightsView &w, const float *x, float *y, hipStream_t s);
+// h = swiglu(G x, U x); G and U share dtype and shape.
+hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u,
+                                 const float *x, float *h, hipStream_t s);
+// y = gemv_quant_q8k(W, x), bit-exact.
+hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y,
+                           hipStream_t s);
+// Y[m] = W X[m] for m < M.
+hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y,
+                       hipStream_t s);
+
+}  // namespace uq

@@ -1,0 +1,440 @@
+// Per-lane "task" policies of the decode GEMV kernels, one per block format.
+//
+// A wave walks rows; in every row each lane owns the same 64-weight slice
+// (a task), so its activation data is fetched from LDS once and kept in
+// VGPRs. A policy defines, for one task:
+//   XS    the lane's activation data (from the per-workgroup LDS prep)
+//   Frag  the weight bytes it loads per row (128-bit loads)
+//   LC    lane constants
+//   dot   the task's contribution to the row.
+// Everything here is a pure function of registers and memory reads, compiled
+// for gfx950 and, for the CPU emulation tests, for the host (uq_bits.h).
+//
+// Two families:
+//   Q4K, Q6K, Q80    gemv_quant semantics (quants.rs:422-466); activations as
+//                    three signed byte planes of a 24-bit fixed-point form,
+//                    integer v_dot4 MACs, f32 scale application.
+//   Q4KQ8, Q6KQ8     gemv_quant_q8k semantics (quants.rs:474-515), bit-exact:
+//                    Q8_K activations, the reference's eight i32 lanes
+//                    sumi[e % 8] built from transposed bytes.
+#pragma once
+
+#include "uq_bits.h"
+
+namespace uq {
+
+constexpr int kBQ4K = 144, kBQ6K = 210, kBQ8_0 = 34;
+
+// Activation planes as prepared in LDS (see prep_x_planes).
+struct XPlanesView {
+    const uint32_t *p0, *p1, *p2;  // K/4 dwords: signed base-256 digits b0, b1, b2
+    const float *scale;            // K/32 power-of-two run scales
+    const int *xs16;               // K/16 sums of X over 16-element half-runs
+};
+
+template <int N>
+UQ_HD void copy_dw(uint32_t (&dst)[N], const uint32_t *src) {
+    for (int i = 0; i < N; i++) dst[i] = src[i];
+}
+
+// ============================ Q4_K ==========================================
+// Task t: block kb = t/4, group pair p = t%4 = lane%4: qs bytes [32p, 32p+32).
+// Low nibble of qs byte 32p+l is element 64p+l (group 2p), high nibble is
+// element 64p+32+l (group 2p+1) (quants.rs:146-151).
+struct Q4K {
+    struct XS {
+        uint32_t X[3][16];
+        float slo, shi, xslo, xshi;
+    };
+    struct Frag {
+        u4 h, qa, qb;
+    };
+    // scale_min_k4 (quants.rs:92-102) for groups 2p, 2p+1 as lane-constant
+    // bit fields of the scale dwords S0 = s[0..3], S1 = s[4..7], S2 = s[8..11]:
+    //   g < 4: sc = S0.bits[8g, +6), m = S1.bits[8g, +6)
+    //   g >= 4 (g' = g-4): sc = S2.bits[8g', +4) | S0.bits[8g'+6, +2) << 4
+    //                      m  = S2.bits[8g'+4, +4) | S1.bits[8g'+6, +2) << 4
+    struct LC {
+        int p;
+        bool hi;
+        uint32_t shA0, shA1, shC0, shC1, shB0, shB1, wA, wB;
+    };
+    static constexpr int kTasksPerBlock = 4;
+    UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    UQ_HD static LC lane_consts(int lane) {
+        LC c;
+        c.p = lane & 3;
+        c.hi = c.p >= 2;
+        const int g0 = 2 * c.p, g1 = g0 + 1;
+        if (!c.hi) {
+            c.shA0 = 8 * g0; c.shA1 = 8 * g1; c.shC0 = 8 * g0; c.shC1 = 8 * g1;
+            c.shB0 = 0; c.shB1 = 0; c.wA = 6; c.wB = 0;
+        } else {
+            const int h0 = g0 - 4, h1 = g1 - 4;
+            c.shA0 = 8 * h0; c.shA1 = 8 * h1; c.shC0 = 8 * h0 + 4; c.shC1 = 8 * h1 + 4;
+            c.shB0 = 8 * h0 + 6; c.shB1 = 8 * h1 + 6; c.wA = 4; c.wB = 2;
+        }
+        return c;
+    }
+    UQ_HD static void scales(const u4 &h, const LC &c, uint32_t &sc0, uint32_t &sc1, uint32_t &m0,
+                             uint32_t &m1) {
+        const uint32_t S0 = h.y, S1 = h.z, S2 = h.w;
+        const uint32_t srcA = c.hi ? S2 : S0, srcC = c.hi ? S2 : S1;
+        sc0 = ubfe(srcA, c.shA0, c.wA) | (ubfe(S0, c.shB0, c.wB) << 4);
+        sc1 = ubfe(srcA, c.shA1, c.wA) | (ubfe(S0, c.shB1, c.wB) << 4);
+        m0 = ubfe(srcC, c.shC0, c.wA) | (ubfe(S1, c.shB0, c.wB) << 4);
+        m1 = ubfe(srcC, c.shC1, c.wA) | (ubfe(S1, c.shB1, c.wB) << 4);
+    }
+    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &c) {
+        const int kb = task >> 2;
+        const int dw = kb * 64 + c.p * 16;
+        copy_dw(s.X[0], P.p0 + dw);
+        copy_dw(s.X[1], P.p1 + dw);
+        copy_dw(s.X[2], P.p2 + dw);
+        const int run = kb * 8 + 2 * c.p;
+        s.slo = P.scale[run];
+        s.shi = P.scale[run + 1];
+        s.xslo = s.slo * (float)(P.xs16[2 * run] + P.xs16[2 * run + 1]);
+        s.xshi = s.shi * (float)(P.xs16[2 * run + 2] + P.xs16[2 * run + 3]);
+    }
+    UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
+        const uint8_t *B = row + (size_t)(task >> 2) * kBQ4K;
+        Frag f;
+        f.h = ld4(B);
+        f.qa = ld4(B + 16 + 32 * c.p);
+        f.qb = ld4(B + 32 + 32 * c.p);
+        return f;
+    }
+    UQ_HD static float dot(const Frag &f, const XS &s, const LC &c) {
+        const uint32_t Q[8] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w, f.qb.x, f.qb.y, f.qb.z, f.qb.w};
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        for (int i = 0; i < 8; i++) {
+            const uint32_t lo = Q[i] & 0x0F0F0F0Fu, hi = (Q[i] >> 4) & 0x0F0F0F0Fu;
+            a0 = sdot4(lo, s.X[0][i], a0);
+            a1 = sdot4(lo, s.X[1][i], a1);
+            a2 = sdot4(lo, s.X[2][i], a2);
+            b0 = sdot4(hi, s.X[0][8 + i], b0);
+            b1 = sdot4(hi, s.X[1][8 + i], b1);
+            b2 = sdot4(hi, s.X[2][8 + i], b2);
+        }
+        uint32_t sc0, sc1, m0, m1;
+        scales(f.h, c, sc0, sc1, m0, m1);
+        const float d = f16_lo(f.h.x), dmin = f16_hi(f.h.x);
+        float r = (d * (float)sc0) * (s.slo * combine3(a0, a1, a2));
+        r = fmaf(d * (float)sc1, s.shi * combine3(b0, b1, b2), r);
+        r = fmaf(-(dmin * (float)m0), s.xslo, r);
+        r = fmaf(-(dmin * (float)m1), s.xshi, r);
+        return r;
+    }
+};
+
+// ============================ Q6_K ==========================================
+// Task t: block kb = t/4, half h = (t/2)%2, column half u = t%2. Quarter j
+// (0..3) holds elements 128h + 32j + 16u + l, l < 16:
+//   low 4 bits: ql byte 64h + 16u + l (j = 0, 2) or 64h + 32 + 16u + l
+//               (j = 1, 3); low nibble for j < 2, high for j >= 2
+//   high 2 bits: bits 2j..2j+1 of qh byte 32h + 16u + l
+//   scale: int8 at 192 + 8h + 2j + u; d: f16 at 208 (quants.rs:185-195).
+// Blocks are 2-byte aligned, so every 16-byte field is loaded as a
+// dword-aligned 20-byte window and realigned with v_alignbyte.
+struct Q6KWindows {
+    u4 a, b, c, e;
+    uint32_t a4, b4, c4, e4, sh;
+};
+UQ_HD Q6KWindows q6k_windows(const uint8_t *B, int h, int u) {
+    Q6KWindows f;
+    f.sh = (uint32_t)((uintptr_t)B & 3);
+    const uint8_t *B4 = B - f.sh;
+    const int oa = 64 * h + 16 * u, oc = 128 + 32 * h + 16 * u;
+    f.a = ld4(B4 + oa);
+    f.a4 = ld1(B4 + oa + 16);
+    f.b = ld4(B4 + oa + 32);
+    f.b4 = ld1(B4 + oa + 48);
+    f.c = ld4(B4 + oc);
+    f.c4 = ld1(B4 + oc + 16);
+    f.e = ld4(B4 + 192);  // scales (+ d in e4); may read 2 bytes past the
+    f.e4 = ld1(B4 + 208); // block: device copies carry tail padding
+    return f;
+}
+UQ_HD void align4(uint32_t (&o)[4], const u4 &v, uint32_t v4, uint32_t sh) {
+    o[0] = alignbyte(v.y, v.x, sh);
+    o[1] = alignbyte(v.z, v.y, sh);
+    o[2] = alignbyte(v.w, v.z, sh);
+    o[3] = alignbyte(v4, v.w, sh);
+}
+// int8 scale of quarter j for lane half u: byte 8h + 2j + u of the scales,
+// i.e. dword 2h + j/2 (E[0..3] are the realigned scale dwords), byte 2(j%2)+u
+UQ_HD int q6k_scale(const uint32_t (&E)[4], int h, int u, int j) {
+    const uint32_t w = E[2 * h + (j >> 1)];
+    return sbfe((int)w, 8 * (2 * (j & 1) + u), 8);
+}
+
+struct Q6K {
+    struct XS {
+        uint32_t X[3][16];
+        int P32[3][4];  // 32 * (sum of the plane's signed digits) per quarter
+        float s[4];
+    };
+    typedef Q6KWindows Frag;
+    struct LC {
+        int h, u;
+    };
+    static constexpr int kTasksPerBlock = 4;
+    UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    UQ_HD static LC lane_consts(int lane) { return LC{(lane >> 1) & 1, lane & 1}; }
+    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &c) {
+        const int kb = task >> 2;
+        for (int j = 0; j < 4; j++) {
+            const int dw = kb * 64 + c.h * 32 + j * 8 + c.u * 4;
+            int q0 = 0, q1 = 0, q2 = 0;
+            for (int i = 0; i < 4; i++) {
+                s.X[0][4 * j + i] = P.p0[dw + i];
+                s.X[1][4 * j + i] = P.p1[dw + i];
+                s.X[2][4 * j + i] = P.p2[dw + i];
+                q0 = sdot4(P.p0[dw + i], 0x01010101u, q0);
+                q1 = sdot4(P.p1[dw + i], 0x01010101u, q1);
+                q2 = sdot4(P.p2[dw + i], 0x01010101u, q2);
+            }
+            s.P32[0][j] = 32 * q0;
+            s.P32[1][j] = 32 * q1;
+            s.P32[2][j] = 32 * q2;
+            s.s[j] = P.scale[kb * 8 + c.h * 4 + j];
+        }
+    }
+    UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
+        return q6k_windows(row + (size_t)(task >> 2) * kBQ6K, c.h, c.u);
+    }
+    // raw 6-bit quants of quarter j (0..63 per byte)
+    UQ_HD static uint32_t raw6(const uint32_t (&A)[4], const uint32_t (&Bq)[4], const uint32_t (&C)[4],
+                               int j, int i) {
+        if (j == 0) return (A[i] & 0x0F0F0F0Fu) | ((C[i] << 4) & 0x30303030u);
+        if (j == 1) return (Bq[i] & 0x0F0F0F0Fu) | ((C[i] << 2) & 0x30303030u);
+        if (j == 2) return ((A[i] >> 4) & 0x0F0F0F0Fu) | (C[i] & 0x30303030u);
+        return ((Bq[i] >> 4) & 0x0F0F0F0Fu) | ((C[i] >> 2) & 0x30303030u);
+    }
+    UQ_HD static float dot(const Frag &f, const XS &s, const LC &c) {
+        uint32_t A[4], Bq[4], C[4], E[4];
+        align4(A, f.a, f.a4, f.sh);
+        align4(Bq, f.b, f.b4, f.sh);
+        align4(C, f.c, f.c4, f.sh);
+        align4(E, f.e, f.e4, f.sh);
+        const float d = f16_lo(f.e4 >> (8 * f.sh));
+        float t = 0.0f;
+        for (int j = 0; j < 4; j++) {
+            int D0 = 0, D1 = 0, D2 = 0;
+            for (int i = 0; i < 4; i++) {
+                const uint32_t q = raw6(A, Bq, C, j, i);
+                D0 = sdot4(q, s.X[0][4 * j + i], D0);
+                D1 = sdot4(q, s.X[1][4 * j + i], D1);
+                D2 = sdot4(q, s.X[2][4 * j + i], D2);
+            }
+            // sum((raw-32)*X) = sum(raw*X) - 32*sum(X), plane by plane
+            D0 -= s.P32[0][j];
+            D1 -= s.P32[1][j];
+            D2 -= s.P32[2][j];
+            const float sc = (float)q6k_scale(E, c.h, c.u, j);
+            t = fmaf(sc * s.s[j], combine3(D0, D1, D2), t);
+        }
+        return d * t;
+    }
+};
+
+// ============================ Q8_0 ==========================================
+// Task t: blocks 2t, 2t+1 (68 bytes, dword aligned when K % 64 == 0):
+// d0 | q0[32] | d1 | q1[32] (ggml block_q8_0: f16 d, int8 qs[32]).
+struct Q80 {
+    struct XS {
+        uint32_t X[3][16];
+        float s0, s1;
+    };
+    struct Frag {
+        u4 w0, w1, w2, w3;
+        uint32_t w4;
+    };
+    struct LC {
+        int unused;
+    };
+    static constexpr int kTasksPerBlock = 0;
+    UQ_HD static int ntasks(int K) { return K >> 6; }
+    UQ_HD static LC lane_consts(int) { return LC{0}; }
+    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &) {
+        const int dw = task * 16;
+        copy_dw(s.X[0], P.p0 + dw);
+        copy_dw(s.X[1], P.p1 + dw);
+        copy_dw(s.X[2], P.p2 + dw);
+        s.s0 = P.scale[2 * task];
+        s.s1 = P.scale[2 * task + 1];
+    }
+    UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &) {
+        const uint8_t *B = row + (size_t)task * (2 * kBQ8_0);
+        Frag f;
+        f.w0 = ld4(B);
+        f.w1 = ld4(B + 16);
+        f.w2 = ld4(B + 32);
+        f.w3 = ld4(B + 48);
+        f.w4 = ld1(B + 64);
+        return f;
+    }
+    UQ_HD static float dot(const Frag &f, const XS &s, const LC &) {
+        const uint32_t w[17] = {f.w0.x, f.w0.y, f.w0.z, f.w0.w, f.w1.x, f.w1.y, f.w1.z, f.w1.w,
+                                f.w2.x, f.w2.y, f.w2.z, f.w2.w, f.w3.x, f.w3.y, f.w3.z, f.w3.w, f.w4};
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q0 = alignbyte(w[i + 1], w[i], 2);  // bytes 2..33
+            const uint32_t q1 = w[9 + i];                       // bytes 36..67
+            a0 = sdot4(q0, s.X[0][i], a0);
+            a1 = sdot4(q0, s.X[1][i], a1);
+            a2 = sdot4(q0, s.X[2][i], a2);
+            b0 = sdot4(q1, s.X[0][8 + i], b0);
+            b1 = sdot4(q1, s.X[1][8 + i], b1);
+            b2 = sdot4(q1, s.X[2][8 + i], b2);
+        }
+        const float d0 = f16_lo(w[0]), d1 = f16_hi(w[8]);
+        const float r = (d0 * s.s0) * combine3(a0, a1, a2);
+        return fmaf(d1 * s.s1, combine3(b0, b1, b2), r);
+    }
+};
+
+// =================== gemv_quant_q8k: Q8_K activations ========================
+// Layout of the prepared Q8_K activations (row-independent), per block kb:
+//   Q4_K: for each p, 20 dwords: X8lo[k] = q8 bytes of elements
+//         64p + k + {0,8,16,24}, X8hi[k] = the same + 32 (k = 0..7),
+//         then bsums pair sums {bs[4p]+bs[4p+1], bs[4p+2]+bs[4p+3]}, 2 pad.
+//   Q6_K: for each task (h,u), 32 dwords: per quarter j and b = 0..3,
+//         Xlo = {x(b), x(8+b), 0, 0}, Xhi = {0, 0, x(4+b), x(12+b)} where
+//         x(l) = q8 of element 128h + 32j + 16u + l.
+// A task's result is the reference's per-block i32 lanes restricted to its
+// elements: S[k] = sum over its elements e with e % 8 == k of
+// sc(e)*a(e)*q8(e), plus (Q4_K) its share of minsum = sum bsums[g]*m[g/2]
+// (quants.rs:337-350, :390-401). Integer sums are order-free, so the sum of
+// the four tasks of a block is the reference's sumi[k] exactly.
+constexpr int kQ4Q8Dw = 20;  // dwords per (block, p)
+constexpr int kQ6Q8Dw = 32;  // dwords per (block, task)
+
+struct Q4KQ8 {
+    struct XS {
+        uint32_t lo[8], hi[8];
+        int bslo, bshi;
+    };
+    typedef Q4K::Frag Frag;
+    typedef Q4K::LC LC;
+    static constexpr int kTasksPerBlock = 4;
+    static constexpr int kDw = kQ4Q8Dw;
+    static constexpr bool kMin = true;  // has the dmin*minsum term
+    // block header dword: f16 d (low) | f16 dmin (high)
+    UQ_HD static uint32_t hdr(const Frag &f) { return f.h.x; }
+    UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    UQ_HD static LC lane_consts(int lane) { return Q4K::lane_consts(lane); }
+    UQ_HD static void load_x(XS &s, const uint32_t *xq, int task) {
+        const uint32_t *p = xq + (size_t)task * kQ4Q8Dw;
+        copy_dw(s.lo, p);
+        copy_dw(s.hi, p + 8);
+        s.bslo = (int)p[16];
+        s.bshi = (int)p[17];
+    }
+    UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) { return Q4K::load_w(row, task, c); }
+    // S[0..7] and M for this task
+    UQ_HD static void dot(const Frag &f, const XS &s, const LC &c, int (&S)[8], int &M) {
+        uint32_t T[8], t4[4];
+        transpose4(f.qa.x, f.qa.z, f.qb.x, f.qb.z, t4);  // bytes l = k, 8+k, 16+k, 24+k (k < 4)
+        T[0] = t4[0]; T[1] = t4[1]; T[2] = t4[2]; T[3] = t4[3];
+        transpose4(f.qa.y, f.qa.w, f.qb.y, f.qb.w, t4);  // l = 4+b, 12+b, 20+b, 28+b
+        T[4] = t4[0]; T[5] = t4[1]; T[6] = t4[2]; T[7] = t4[3];
+        uint32_t sc0, sc1, m0, m1;
+        Q4K::scales(f.h, c, sc0, sc1, m0, m1);
+        for (int k = 0; k < 8; k++) {
+            const int dl = sdot4(T[k] & 0x0F0F0F0Fu, s.lo[k], 0);
+            const int dh = sdot4((T[k] >> 4) & 0x0F0F0F0Fu, s.hi[k], 0);
+            S[k] = (int)sc0 * dl + (int)sc1 * dh;
+        }
+        M = (int)m0 * s.bslo + (int)m1 * s.bshi;
+    }
+    // Build the (block, p) record from the block's 256 Q8_K bytes (64 dwords)
+    // and bsums.
+    UQ_HD static void build(uint32_t *dst, const uint32_t *qblk, const int *bs, int p) {
+        uint32_t t4[4];
+        for (int half = 0; half < 2; half++) {
+            const uint32_t *L = qblk + 16 * p + 8 * half;  // elements 64p + 32*half + 0..31
+            uint32_t *o = dst + 8 * half;
+            transpose4(L[0], L[2], L[4], L[6], t4);
+            o[0] = t4[0]; o[1] = t4[1]; o[2] = t4[2]; o[3] = t4[3];
+            transpose4(L[1], L[3], L[5], L[7], t4);
+            o[4] = t4[0]; o[5] = t4[1]; o[6] = t4[2]; o[7] = t4[3];
+        }
+        dst[16] = (uint32_t)(bs[4 * p] + bs[4 * p + 1]);
+        dst[17] = (uint32_t)(bs[4 * p + 2] + bs[4 * p + 3]);
+        dst[18] = 0;
+        dst[19] = 0;
+    }
+    // record of task `sub` (= p) of a block
+    UQ_HD static void build_task(uint32_t *dst, const uint32_t *qblk, const int *bs, int sub) {
+        build(dst, qblk, bs, sub);
+    }
+};
+
+struct Q6KQ8 {
+    struct XS {
+        uint32_t X[32];
+    };
+    typedef Q6KWindows Frag;
+    typedef Q6K::LC LC;
+    static constexpr int kTasksPerBlock = 4;
+    static constexpr int kDw = kQ6Q8Dw;
+    static constexpr bool kMin = false;
+    // f16 d bits of the block
+    UQ_HD static uint32_t hdr(const Frag &f) { return (f.e4 >> (8 * f.sh)) & 0xFFFFu; }
+    UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    UQ_HD static LC lane_consts(int lane) { return Q6K::lane_consts(lane); }
+    UQ_HD static void load_x(XS &s, const uint32_t *xq, int task) {
+        copy_dw(s.X, xq + (size_t)task * kQ6Q8Dw);
+    }
+    UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) { return Q6K::load_w(row, task, c); }
+    // 4*(raw-32) as signed bytes: raw placed in bits 2..7, top bit flipped
+    UQ_HD static uint32_t sq6(const uint32_t (&A)[4], const uint32_t (&Bq)[4], const uint32_t (&C)[4],
+                              int j, int i) {
+        uint32_t lo4, hi2;
+        if (j == 0) { lo4 = A[i] << 2; hi2 = C[i] << 6; }
+        else if (j == 1) { lo4 = Bq[i] << 2; hi2 = C[i] << 4; }
+        else if (j == 2) { lo4 = A[i] >> 2; hi2 = C[i] << 2; }
+        else { lo4 = Bq[i] >> 2; hi2 = C[i]; }
+        return ((lo4 & 0x3C3C3C3Cu) | (hi2 & 0xC0C0C0C0u)) ^ 0x80808080u;
+    }
+    UQ_HD static void dot(const Frag &f, const XS &s, const LC &c, int (&S)[8], int &M) {
+        uint32_t A[4], Bq[4], C[4], E[4];
+        align4(A, f.a, f.a4, f.sh);
+        align4(Bq, f.b, f.b4, f.sh);
+        align4(C, f.c, f.c4, f.sh);
+        align4(E, f.e, f.e4, f.sh);
+        for (int k = 0; k < 8; k++) S[k] = 0;
+        for (int j = 0; j < 4; j++) {
+            const uint32_t q0 = sq6(A, Bq, C, j, 0), q1 = sq6(A, Bq, C, j, 1);
+            const uint32_t q2 = sq6(A, Bq, C, j, 2), q3 = sq6(A, Bq, C, j, 3);
+            uint32_t T[4];
+            transpose4(q0, q2, q1, q3, T);  // T[b] = {l=b, l=8+b, l=4+b, l=12+b}
+            const int sc = q6k_scale(E, c.h, c.u, j);
+            for (int b = 0; b < 4; b++) {
+                S[b] += sc * sdot4(T[b], s.X[8 * j + 2 * b], 0);
+                S[4 + b] += sc * sdot4(T[b], s.X[8 * j + 2 * b + 1], 0);
+            }
+        }
+        for (int k = 0; k < 8; k++) S[k] >>= 2;  // products carried 4*(raw-32): exact
+        M = 0;
+    }
+    UQ_HD static void build(uint32_t *dst, const uint32_t *qblk, int h, int u) {
+        for (int j = 0; j < 4; j++) {
+            const uint32_t *x = qblk + 32 * h + 8 * j + 4 * u;  // elements 128h+32j+16u + 4i
+            uint32_t T[4];
+            transpose4(x[0], x[2], x[1], x[3], T);
+            for (int b = 0; b < 4; b++) {
+                dst[8 * j + 2 * b] = T[b] & 0x0000FFFFu;
+                dst[8 * j + 2 * b + 1] = T[b] & 0xFFFF0000u;
+            }
+        }
+    }
+    // record of task `sub` = 2h + u of a block
+    UQ_HD static void build_task(uint32_t *dst, const uint32_t *qblk, const int *, int sub) {
+        build(dst, qblk, sub >> 1, sub & 1);
+    }
+};
+
+}  // namespace uq
