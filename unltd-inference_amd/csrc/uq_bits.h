@@ -125,9 +125,5 @@ UQ_HD void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (
     t[3] = perm(cd_hi, ab_hi, 0x07060302u);
 }
 
-// sum of q*X over X = b2*65536 + b1*256 + b0 from the three plane dots
-UQ_HD float combine3(int d0, int d1, int d2) {
-    return fmaf((float)d2, 65536.0f, (float)(d1 * 256 + d0));
-}
 
 }  // namespace uq

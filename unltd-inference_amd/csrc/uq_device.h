@@ -69,31 +69,59 @@ __device__ __forceinline__ int group4_sum_i(int v) {
     return v;
 }
 
+// f64 DPP: the two halves move together
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// Same fixed tree as wave_sum, in f64.
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    v += dpp_d<0x142, 0xA>(v);
+    v += dpp_d<0x143, 0xC>(v);
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), 63),
+                            __builtin_amdgcn_readlane(__double2loint(v), 63));
+}
+
+__device__ __forceinline__ double group8_sum_d(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    return v;
+}
+
 // ---------------------------------------------------------------------------
-// Activation digit planes.
-// Each run of 32 activations gets a power-of-two scale s = 2^(ex-22), where
-// 2^(ex-1) <= max|x| < 2^ex, and the integers X = rint(x / s) (|X| <= 2^22,
-// exact scaling, round-half-even). X is split into three signed base-256
-// digits, X = b2*65536 + b1*256 + b0 with b0, b1, b2 in [-128, 127], stored
-// as three byte planes so that v_dot4_i32_i8 multiplies them with packed
-// weight quants exactly. ΣX over each 16-element half-run is kept as an
-// exact int32. Error per activation <= s/2 <= max|x| * 2^-22. Non-finite
+// Activation digit planes (layout read by uq_policies.h).
+// Each run of 32 activations gets a power-of-two scale s = 2^(ex-30), where
+// 2^(ex-1) <= max|x| < 2^ex, and the integers X = rint(x / s) (|X| <= 2^30,
+// exact scaling, round-half-even). X is split into four signed base-256
+// digits X = b3*2^24 + b2*2^16 + b1*2^8 + b0 (b0..b2 in [-128,127], b3 in
+// [-64,64]) stored as byte planes, so v_dot4_i32_i8 multiplies them with
+// packed weight quants exactly. The run sum s*sum(X) is kept as an exact
+// double. Error per activation <= s/2 <= max|x_run| * 2^-30. Non-finite
 // activations are outside this path's contract (outputs unspecified).
 // ---------------------------------------------------------------------------
+constexpr int kXPlanes = 4;
 struct XPlanes {
-    uint32_t *p0, *p1, *p2;  // K/4 dwords each
-    float *scale;            // K/32 run scales s
-    int *xs16;               // K/16 half-run sums of X
+    uint32_t *p[kXPlanes];  // K/4 dwords each
+    float *scale;           // K/32 run scales s
+    double *xsum;           // K/32 run sums s*sum(X)
 };
 
-__device__ __forceinline__ void digits3(int X, uint32_t &b0, uint32_t &b1, uint32_t &b2) {
-    int d0 = (int)(int8_t)(X & 0xFF);
-    int X1 = (X - d0) >> 8;
-    int d1 = (int)(int8_t)(X1 & 0xFF);
-    int d2 = (X1 - d1) >> 8;
-    b0 = (uint32_t)d0 & 0xFF;
-    b1 = (uint32_t)d1 & 0xFF;
-    b2 = (uint32_t)d2 & 0xFF;
+__device__ __forceinline__ uint32_t digits4(int X, int &b1, int &b2, int &b3) {
+    const int d0 = (int)(int8_t)(X & 0xFF);
+    const int X1 = (X - d0) >> 8;
+    b1 = (int)(int8_t)(X1 & 0xFF);
+    const int X2 = (X1 - b1) >> 8;
+    b2 = (int)(int8_t)(X2 & 0xFF);
+    b3 = (X2 - b2) >> 8;
+    return (uint32_t)d0 & 0xFF;
 }
 
 // All threads of the block cooperate; K % 32 == 0. Each group of 8 lanes
@@ -101,31 +129,31 @@ __device__ __forceinline__ void digits3(int X, uint32_t &b0, uint32_t &b1, uint3
 // active together because runs are aligned to 8-lane groups.
 __device__ __forceinline__ void prep_x_planes(const float *__restrict__ x, int K, XPlanes P) {
     for (int base = threadIdx.x * 4; base < K; base += blockDim.x * 4) {
-        float v0 = x[base], v1 = x[base + 1], v2 = x[base + 2], v3 = x[base + 3];
-        float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+        const float v[4] = {x[base], x[base + 1], x[base + 2], x[base + 3]};
+        float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
         am = group8_max(am);
         int ex = 0;
         if (am > 0.0f) (void)frexpf(am, &ex);
-        const int sh = 22 - ex;
-        int X0 = 0, X1 = 0, X2 = 0, X3 = 0;
-        if (am > 0.0f) {
-            X0 = (int)rintf(ldexpf(v0, sh));
-            X1 = (int)rintf(ldexpf(v1, sh));
-            X2 = (int)rintf(ldexpf(v2, sh));
-            X3 = (int)rintf(ldexpf(v3, sh));
+        uint32_t w[kXPlanes] = {0, 0, 0, 0};
+        double xs = 0.0;
+        for (int i = 0; i < 4; i++) {
+            const int X = am > 0.0f ? (int)rintf(ldexpf(v[i], 30 - ex)) : 0;
+            int b1, b2, b3;
+            const uint32_t b0 = digits4(X, b1, b2, b3);
+            w[0] |= b0 << (8 * i);
+            w[1] |= ((uint32_t)b1 & 0xFF) << (8 * i);
+            w[2] |= ((uint32_t)b2 & 0xFF) << (8 * i);
+            w[3] |= ((uint32_t)b3 & 0xFF) << (8 * i);
+            xs += (double)X;
         }
-        uint32_t a0, a1, a2, c0, c1, c2, e0, e1, e2, f0, f1, f2;
-        digits3(X0, a0, a1, a2);
-        digits3(X1, c0, c1, c2);
-        digits3(X2, e0, e1, e2);
-        digits3(X3, f0, f1, f2);
         const int dw = base >> 2;
-        P.p0[dw] = a0 | (c0 << 8) | (e0 << 16) | (f0 << 24);
-        P.p1[dw] = a1 | (c1 << 8) | (e1 << 16) | (f1 << 24);
-        P.p2[dw] = a2 | (c2 << 8) | (e2 << 16) | (f2 << 24);
-        int s4 = group4_sum_i(X0 + X1 + X2 + X3);
-        if ((threadIdx.x & 3) == 0) P.xs16[base >> 4] = s4;
-        if ((threadIdx.x & 7) == 0) P.scale[base >> 5] = am > 0.0f ? ldexpf(1.0f, ex - 22) : 0.0f;
+        for (int q = 0; q < kXPlanes; q++) P.p[q][dw] = w[q];
+        xs = group8_sum_d(xs);
+        if ((threadIdx.x & 7) == 0) {
+            const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
+            P.scale[base >> 5] = s;
+            P.xsum[base >> 5] = xs * (double)s;
+        }
     }
 }
 

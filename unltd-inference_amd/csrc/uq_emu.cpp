@@ -19,63 +19,56 @@ namespace {
 
 // prep_x_planes (uq_device.h) for the whole vector
 struct HostPlanes {
-    std::vector<uint32_t> p0, p1, p2;
+    std::vector<uint32_t> p[kPlanes];
     std::vector<float> scale;
-    std::vector<int> xs16;
-    XPlanesView view() const { return XPlanesView{p0.data(), p1.data(), p2.data(), scale.data(), xs16.data()}; }
+    std::vector<double> xsum;
+    XPlanesView view() const {
+        return XPlanesView{{p[0].data(), p[1].data(), p[2].data(), p[3].data()}, scale.data(), xsum.data()};
+    }
 };
-
-void digits3(int X, uint32_t &b0, uint32_t &b1, uint32_t &b2) {
-    const int d0 = (int)(int8_t)(X & 0xFF);
-    const int X1 = (X - d0) >> 8;
-    const int d1 = (int)(int8_t)(X1 & 0xFF);
-    const int d2 = (X1 - d1) >> 8;
-    b0 = (uint32_t)d0 & 0xFF;
-    b1 = (uint32_t)d1 & 0xFF;
-    b2 = (uint32_t)d2 & 0xFF;
-}
 
 HostPlanes prep_planes(const float *x, int K) {
     HostPlanes P;
-    P.p0.assign(K / 4, 0);
-    P.p1.assign(K / 4, 0);
-    P.p2.assign(K / 4, 0);
+    for (int q = 0; q < kPlanes; q++) P.p[q].assign(K / 4, 0);
     P.scale.assign(K / 32, 0.0f);
-    P.xs16.assign(K / 16, 0);
+    P.xsum.assign(K / 32, 0.0);
     for (int run = 0; run < K / 32; run++) {
         const float *v = x + 32 * run;
         float am = 0.0f;
         for (int i = 0; i < 32; i++) am = std::fmax(am, std::fabs(v[i]));
         int ex = 0;
         if (am > 0.0f) (void)std::frexp(am, &ex);
-        int X[32];
-        for (int i = 0; i < 32; i++) X[i] = am > 0.0f ? (int)std::rint(std::ldexp(v[i], 22 - ex)) : 0;
-        for (int q = 0; q < 8; q++) {
-            uint32_t w0 = 0, w1 = 0, w2 = 0;
-            for (int b = 0; b < 4; b++) {
-                uint32_t b0, b1, b2;
-                digits3(X[4 * q + b], b0, b1, b2);
-                w0 |= b0 << (8 * b);
-                w1 |= b1 << (8 * b);
-                w2 |= b2 << (8 * b);
+        double part[8];
+        for (int g = 0; g < 8; g++) {
+            uint32_t w[kPlanes] = {0, 0, 0, 0};
+            double xs = 0.0;
+            for (int i = 0; i < 4; i++) {
+                const int X = am > 0.0f ? (int)std::rint(std::ldexp(v[4 * g + i], 30 - ex)) : 0;
+                const int d0 = (int)(int8_t)(X & 0xFF), X1 = (X - d0) >> 8;
+                const int d1 = (int)(int8_t)(X1 & 0xFF), X2 = (X1 - d1) >> 8;
+                const int d2 = (int)(int8_t)(X2 & 0xFF), d3 = (X2 - d2) >> 8;
+                const int dd[4] = {d0, d1, d2, d3};
+                for (int q = 0; q < kPlanes; q++) w[q] |= ((uint32_t)dd[q] & 0xFF) << (8 * i);
+                xs += (double)X;
             }
-            P.p0[8 * run + q] = w0;
-            P.p1[8 * run + q] = w1;
-            P.p2[8 * run + q] = w2;
+            for (int q = 0; q < kPlanes; q++) P.p[q][8 * run + g] = w[q];
+            part[g] = xs;
         }
-        for (int h = 0; h < 2; h++) {
-            int s = 0;
-            for (int i = 0; i < 16; i++) s += X[16 * h + i];
-            P.xs16[2 * run + h] = s;
-        }
-        P.scale[run] = am > 0.0f ? std::ldexp(1.0f, ex - 22) : 0.0f;
+        // group8_sum_d: quad_perm 1,0,3,2 / 2,3,0,1 / row_half_mirror, lane 0
+        double t[8];
+        for (int i = 0; i < 8; i++) t[i] = part[i] + part[i ^ 1];
+        for (int i = 0; i < 8; i++) part[i] = t[i] + t[i ^ 2];
+        const double xs = part[0] + part[7];
+        const float s = am > 0.0f ? std::ldexp(1.0f, ex - 30) : 0.0f;
+        P.scale[run] = s;
+        P.xsum[run] = xs * (double)s;
     }
     return P;
 }
 
-// wave_sum (uq_device.h): the DPP tree, lane 63's value
-float wave_sum64(const float *in) {
-    float v[64], t[64];
+// wave_sum_d (uq_device.h): the DPP tree, lane 63's value
+double wave_sum64(const double *in) {
+    double v[64], t[64];
     std::memcpy(v, in, sizeof v);
     for (int i = 0; i < 64; i++) t[i] = v[i] + v[i ^ 1];
     std::memcpy(v, t, sizeof v);
@@ -87,10 +80,10 @@ float wave_sum64(const float *in) {
     std::memcpy(v, t, sizeof v);
     for (int i = 0; i < 64; i++) {
         const int row = i >> 4;
-        t[i] = v[i] + ((row == 1 || row == 3) ? v[(row - 1) * 16 + 15] : 0.0f);
+        t[i] = v[i] + ((row == 1 || row == 3) ? v[(row - 1) * 16 + 15] : 0.0);
     }
     std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + ((i >> 4) >= 2 ? v[31] : 0.0f);
+    for (int i = 0; i < 64; i++) t[i] = v[i] + ((i >> 4) >= 2 ? v[31] : 0.0);
     return t[63];
 }
 
@@ -101,10 +94,10 @@ void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int 
     const int ntask = F::ntasks(K);
     for (int row = 0; row < N; row++) {
         const uint8_t *R = W + (size_t)row * row_bytes;
-        float part[64];
+        double part[64];
         for (int lane = 0; lane < 64; lane++) {
             const typename F::LC c = F::lane_consts(lane);
-            float g = 0.0f;
+            double g = 0.0;
             for (int t = lane; t < ntask; t += 64) {
                 typename F::XS xs;
                 F::load_x(xs, PV, t, c);
@@ -112,7 +105,7 @@ void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int 
             }
             part[lane] = g;
         }
-        y[row] = wave_sum64(part);
+        y[row] = (float)wave_sum64(part);
     }
 }
 

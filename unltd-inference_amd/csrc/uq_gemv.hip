@@ -39,17 +39,17 @@ int num_cus() {
 }
 
 // ---------------------------- gemv_quant -----------------------------------
+// LDS: 4 digit planes (K bytes each), then K/32 run sums (f64), then K/32
+// run scales (f32)
 __host__ __device__ inline size_t planes_bytes(int K) {
-    return 3 * (size_t)K + (size_t)(K / 32) * 4 + (size_t)(K / 16) * 4;
+    return 4 * (size_t)K + (size_t)(K / 32) * 8 + (size_t)(K / 32) * 4;
 }
 
 __device__ inline XPlanes planes_at(uint8_t *lds, int K) {
     XPlanes P;
-    P.p0 = (uint32_t *)lds;
-    P.p1 = (uint32_t *)(lds + K);
-    P.p2 = (uint32_t *)(lds + 2 * K);
-    P.scale = (float *)(lds + 3 * K);
-    P.xs16 = (int *)(lds + 3 * K + (K / 32) * 4);
+    for (int q = 0; q < kXPlanes; q++) P.p[q] = (uint32_t *)(lds + (size_t)q * K);
+    P.xsum = (double *)(lds + 4 * (size_t)K);
+    P.scale = (float *)(lds + 4 * (size_t)K + (size_t)(K / 32) * 8);
     return P;
 }
 
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(const uint8_t *__restrict__ W
     const XPlanes P = planes_at(lds, K);
     prep_x_planes(x, K, P);
     __syncthreads();
-    const XPlanesView PV{P.p0, P.p1, P.p2, P.scale, P.xs16};
+    const XPlanesView PV{{P.p[0], P.p[1], P.p[2], P.p[3]}, P.scale, P.xsum};
 
     const int lane = threadIdx.x & 63;
     const int ntask = F::ntasks(K);
@@ -94,17 +94,17 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(const uint8_t *__restrict__ W
                 nxt = F::load_w(W + (size_t)nrow * row_bytes, lane, c);
                 if (PAIR) nxt2 = F::load_w(W2 + (size_t)nrow * row_bytes, lane, c);
             }
-            float g = 0.0f, u = 0.0f;
+            double g = 0.0, u = 0.0;
             if (active) {
                 g = F::dot(cur, xs, c);
                 if (PAIR) u = F::dot(cur2, xs, c);
             }
-            g = wave_sum(g);
+            g = wave_sum_d(g);
             if (PAIR) {
-                u = wave_sum(u);
-                if (lane == 0) y[row] = swiglu1(g, u);
+                u = wave_sum_d(u);
+                if (lane == 0) y[row] = swiglu1((float)g, (float)u);
             } else if (lane == 0) {
-                y[row] = g;
+                y[row] = (float)g;
             }
             cur = nxt;
             if (PAIR) cur2 = nxt2;
@@ -112,26 +112,28 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(const uint8_t *__restrict__ W
     } else {
         for (int row = wave; row < N; row += nwave) {
             const uint8_t *R = W + (size_t)row * row_bytes;
-            float g = 0.0f, u = 0.0f;
+            double g = 0.0, u = 0.0;
             for (int t = lane; t < ntask; t += 64) {
                 typename F::XS xs;
                 F::load_x(xs, PV, t, c);
                 g += F::dot(F::load_w(R, t, c), xs, c);
                 if (PAIR) u += F::dot(F::load_w(W2 + (size_t)row * row_bytes, t, c), xs, c);
             }
-            g = wave_sum(g);
+            g = wave_sum_d(g);
             if (PAIR) {
-                u = wave_sum(u);
-                if (lane == 0) y[row] = swiglu1(g, u);
+                u = wave_sum_d(u);
+                if (lane == 0) y[row] = swiglu1((float)g, (float)u);
             } else if (lane == 0) {
-                y[row] = g;
+                y[row] = (float)g;
             }
         }
     }
 }
 
 // Generic fallback (F32 rows, Q8_0 with K % 64 != 0, K beyond the LDS
-// budget): one wave per row, f32 dequantization and FMA.
+// budget): one wave per row, f32 dequantization (exact: one rounding for
+// Q4_K, none for Q6_K/Q8_0/F32, quants.rs:129-131, :170) and f64
+// accumulation of the exact products x*w.
 __device__ __forceinline__ float deq_elem(uq_dtype dt, const uint8_t *row, int e) {
     if (dt == UQ_F32) return ((const float *)row)[e];
     if (dt == UQ_Q8_0) {
@@ -172,17 +174,17 @@ __global__ __launch_bounds__(TPB) void gemv_generic_kernel(uq_dtype dt, const ui
     const int lane = threadIdx.x & 63;
     for (int row = blockIdx.x * WAVES + (threadIdx.x >> 6); row < N; row += gridDim.x * WAVES) {
         const uint8_t *R = W + (size_t)row * row_bytes;
-        float g = 0.0f, u = 0.0f;
+        double g = 0.0, u = 0.0;
         for (int e = lane; e < K; e += 64) {
-            g = fmaf(x[e], deq_elem(dt, R, e), g);
-            if (W2) u = fmaf(x[e], deq_elem(dt, W2 + (size_t)row * row_bytes, e), u);
+            g = fma((double)x[e], (double)deq_elem(dt, R, e), g);
+            if (W2) u = fma((double)x[e], (double)deq_elem(dt, W2 + (size_t)row * row_bytes, e), u);
         }
-        g = wave_sum(g);
+        g = wave_sum_d(g);
         if (W2) {
-            u = wave_sum(u);
-            if (lane == 0) y[row] = swiglu1(g, u);
+            u = wave_sum_d(u);
+            if (lane == 0) y[row] = swiglu1((float)g, (float)u);
         } else if (lane == 0) {
-            y[row] = g;
+            y[row] = (float)g;
         }
     }
 }

@@ -12,8 +12,10 @@
 //
 // Two families:
 //   Q4K, Q6K, Q80    gemv_quant semantics (quants.rs:422-466); activations as
-//                    three signed byte planes of a 24-bit fixed-point form,
-//                    integer v_dot4 MACs, f32 scale application.
+//                    four signed byte planes of a 31-bit fixed-point form,
+//                    exact integer v_dot4 MACs, scale application and
+//                    accumulation in f64 (full rate on CDNA4), so the row
+//                    result carries the reference's f64 accuracy.
 //   Q4KQ8, Q6KQ8     gemv_quant_q8k semantics (quants.rs:474-515), bit-exact:
 //                    Q8_K activations, the reference's eight i32 lanes
 //                    sumi[e % 8] built from transposed bytes.
@@ -25,11 +27,15 @@ namespace uq {
 
 constexpr int kBQ4K = 144, kBQ6K = 210, kBQ8_0 = 34;
 
-// Activation planes as prepared in LDS (see prep_x_planes).
+// Activation planes as prepared in LDS (see prep_x_planes): each run of 32
+// activations has a power-of-two scale s and integers X = rint(x/s),
+// |X| <= 2^30, stored as four signed base-256 digit planes
+// X = b3*2^24 + b2*2^16 + b1*2^8 + b0.
+constexpr int kPlanes = 4;
 struct XPlanesView {
-    const uint32_t *p0, *p1, *p2;  // K/4 dwords: signed base-256 digits b0, b1, b2
-    const float *scale;            // K/32 power-of-two run scales
-    const int *xs16;               // K/16 sums of X over 16-element half-runs
+    const uint32_t *p[kPlanes];  // K/4 dwords per plane
+    const float *scale;          // K/32 run scales s
+    const double *xsum;          // K/32 run sums s*sum(X), exact
 };
 
 template <int N>
@@ -37,14 +43,26 @@ UQ_HD void copy_dw(uint32_t (&dst)[N], const uint32_t *src) {
     for (int i = 0; i < N; i++) dst[i] = src[i];
 }
 
+// sum(q*X) of a group from its four exact plane dots, as an exact double:
+// (D3*256 + D2)*65536 + (D1*256 + D0); both halves fit int32 for <= 32
+// elements of |q| <= 128 (|D| <= 2^19), the result fits 53 bits.
+UQ_HD double plane_sum(int d0, int d1, int d2, int d3) {
+    return fma((double)(d3 * 256 + d2), 65536.0, (double)(d1 * 256 + d0));
+}
+
 // ============================ Q4_K ==========================================
 // Task t: block kb = t/4, group pair p = t%4 = lane%4: qs bytes [32p, 32p+32).
 // Low nibble of qs byte 32p+l is element 64p+l (group 2p), high nibble is
 // element 64p+32+l (group 2p+1) (quants.rs:146-151).
+// Row contribution, exactly as the reference's per-element weights
+// w = (d*sc)*q - dmin*m (quants.rs:151) summed over the task:
+//   sum_g (d*sc_g*s_g) * sum(q*X) - (dmin*m_g) * (s_g*sum(X)),
+// with the integer sums exact and the accumulation in f64.
 struct Q4K {
     struct XS {
-        uint32_t X[3][16];
-        float slo, shi, xslo, xshi;
+        uint32_t X[kPlanes][16];
+        float slo, shi;
+        double xslo, xshi;  // s*sum(X) of groups 2p, 2p+1
     };
     struct Frag {
         u4 h, qa, qb;
@@ -88,14 +106,12 @@ struct Q4K {
     UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &c) {
         const int kb = task >> 2;
         const int dw = kb * 64 + c.p * 16;
-        copy_dw(s.X[0], P.p0 + dw);
-        copy_dw(s.X[1], P.p1 + dw);
-        copy_dw(s.X[2], P.p2 + dw);
+        for (int q = 0; q < kPlanes; q++) copy_dw(s.X[q], P.p[q] + dw);
         const int run = kb * 8 + 2 * c.p;
         s.slo = P.scale[run];
         s.shi = P.scale[run + 1];
-        s.xslo = s.slo * (float)(P.xs16[2 * run] + P.xs16[2 * run + 1]);
-        s.xshi = s.shi * (float)(P.xs16[2 * run + 2] + P.xs16[2 * run + 3]);
+        s.xslo = P.xsum[run];
+        s.xshi = P.xsum[run + 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
         const uint8_t *B = row + (size_t)(task >> 2) * kBQ4K;
@@ -105,25 +121,24 @@ struct Q4K {
         f.qb = ld4(B + 32 + 32 * c.p);
         return f;
     }
-    UQ_HD static float dot(const Frag &f, const XS &s, const LC &c) {
+    UQ_HD static double dot(const Frag &f, const XS &s, const LC &c) {
         const uint32_t Q[8] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w, f.qb.x, f.qb.y, f.qb.z, f.qb.w};
-        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        int a[kPlanes] = {0, 0, 0, 0}, b[kPlanes] = {0, 0, 0, 0};
         for (int i = 0; i < 8; i++) {
             const uint32_t lo = Q[i] & 0x0F0F0F0Fu, hi = (Q[i] >> 4) & 0x0F0F0F0Fu;
-            a0 = sdot4(lo, s.X[0][i], a0);
-            a1 = sdot4(lo, s.X[1][i], a1);
-            a2 = sdot4(lo, s.X[2][i], a2);
-            b0 = sdot4(hi, s.X[0][8 + i], b0);
-            b1 = sdot4(hi, s.X[1][8 + i], b1);
-            b2 = sdot4(hi, s.X[2][8 + i], b2);
+            for (int q = 0; q < kPlanes; q++) {
+                a[q] = sdot4(lo, s.X[q][i], a[q]);
+                b[q] = sdot4(hi, s.X[q][8 + i], b[q]);
+            }
         }
         uint32_t sc0, sc1, m0, m1;
         scales(f.h, c, sc0, sc1, m0, m1);
         const float d = f16_lo(f.h.x), dmin = f16_hi(f.h.x);
-        float r = (d * (float)sc0) * (s.slo * combine3(a0, a1, a2));
-        r = fmaf(d * (float)sc1, s.shi * combine3(b0, b1, b2), r);
-        r = fmaf(-(dmin * (float)m0), s.xslo, r);
-        r = fmaf(-(dmin * (float)m1), s.xshi, r);
+        // d*sc and dmin*m are exact in f32 (<= 17 significant bits)
+        double r = (double)((d * (float)sc0) * s.slo) * plane_sum(a[0], a[1], a[2], a[3]);
+        r = fma((double)((d * (float)sc1) * s.shi), plane_sum(b[0], b[1], b[2], b[3]), r);
+        r = fma(-(double)(dmin * (float)m0), s.xslo, r);
+        r = fma(-(double)(dmin * (float)m1), s.xshi, r);
         return r;
     }
 };
@@ -169,10 +184,12 @@ UQ_HD int q6k_scale(const uint32_t (&E)[4], int h, int u, int j) {
     return sbfe((int)w, 8 * (2 * (j & 1) + u), 8);
 }
 
+// Row contribution: sum_j d*sc_j*s_j * sum((raw-32)*X) over each quarter,
+// the reference's w = d*(sc*q) with q = raw-32 (quants.rs:193-195).
 struct Q6K {
     struct XS {
-        uint32_t X[3][16];
-        int P32[3][4];  // 32 * (sum of the plane's signed digits) per quarter
+        uint32_t X[kPlanes][16];
+        int Clo[4], Chi[4];  // 32*(P1*256+P0), 32*(P3*256+P2): plane digit sums
         float s[4];
     };
     typedef Q6KWindows Frag;
@@ -186,18 +203,14 @@ struct Q6K {
         const int kb = task >> 2;
         for (int j = 0; j < 4; j++) {
             const int dw = kb * 64 + c.h * 32 + j * 8 + c.u * 4;
-            int q0 = 0, q1 = 0, q2 = 0;
-            for (int i = 0; i < 4; i++) {
-                s.X[0][4 * j + i] = P.p0[dw + i];
-                s.X[1][4 * j + i] = P.p1[dw + i];
-                s.X[2][4 * j + i] = P.p2[dw + i];
-                q0 = sdot4(P.p0[dw + i], 0x01010101u, q0);
-                q1 = sdot4(P.p1[dw + i], 0x01010101u, q1);
-                q2 = sdot4(P.p2[dw + i], 0x01010101u, q2);
-            }
-            s.P32[0][j] = 32 * q0;
-            s.P32[1][j] = 32 * q1;
-            s.P32[2][j] = 32 * q2;
+            int sum[kPlanes] = {0, 0, 0, 0};
+            for (int q = 0; q < kPlanes; q++)
+                for (int i = 0; i < 4; i++) {
+                    s.X[q][4 * j + i] = P.p[q][dw + i];
+                    sum[q] = sdot4(P.p[q][dw + i], 0x01010101u, sum[q]);
+                }
+            s.Clo[j] = 32 * (sum[1] * 256 + sum[0]);
+            s.Chi[j] = 32 * (sum[3] * 256 + sum[2]);
             s.s[j] = P.scale[kb * 8 + c.h * 4 + j];
         }
     }
@@ -212,39 +225,37 @@ struct Q6K {
         if (j == 2) return ((A[i] >> 4) & 0x0F0F0F0Fu) | (C[i] & 0x30303030u);
         return ((Bq[i] >> 4) & 0x0F0F0F0Fu) | ((C[i] >> 2) & 0x30303030u);
     }
-    UQ_HD static float dot(const Frag &f, const XS &s, const LC &c) {
+    UQ_HD static double dot(const Frag &f, const XS &s, const LC &c) {
         uint32_t A[4], Bq[4], C[4], E[4];
         align4(A, f.a, f.a4, f.sh);
         align4(Bq, f.b, f.b4, f.sh);
         align4(C, f.c, f.c4, f.sh);
         align4(E, f.e, f.e4, f.sh);
         const float d = f16_lo(f.e4 >> (8 * f.sh));
-        float t = 0.0f;
+        double t = 0.0;
         for (int j = 0; j < 4; j++) {
-            int D0 = 0, D1 = 0, D2 = 0;
+            int D[kPlanes] = {0, 0, 0, 0};
             for (int i = 0; i < 4; i++) {
                 const uint32_t q = raw6(A, Bq, C, j, i);
-                D0 = sdot4(q, s.X[0][4 * j + i], D0);
-                D1 = sdot4(q, s.X[1][4 * j + i], D1);
-                D2 = sdot4(q, s.X[2][4 * j + i], D2);
+                for (int p = 0; p < kPlanes; p++) D[p] = sdot4(q, s.X[p][4 * j + i], D[p]);
             }
-            // sum((raw-32)*X) = sum(raw*X) - 32*sum(X), plane by plane
-            D0 -= s.P32[0][j];
-            D1 -= s.P32[1][j];
-            D2 -= s.P32[2][j];
-            const float sc = (float)q6k_scale(E, c.h, c.u, j);
-            t = fmaf(sc * s.s[j], combine3(D0, D1, D2), t);
+            // sum((raw-32)*X) = sum(raw*X) - 32*sum(X), per half of the planes
+            const int lo = D[1] * 256 + D[0] - s.Clo[j];
+            const int hi = D[3] * 256 + D[2] - s.Chi[j];
+            const double S = fma((double)hi, 65536.0, (double)lo);
+            // d*sc*s is exact in f32 (<= 19 significant bits)
+            t = fma((double)(d * (float)q6k_scale(E, c.h, c.u, j) * s.s[j]), S, t);
         }
-        return d * t;
+        return t;
     }
 };
 
 // ============================ Q8_0 ==========================================
 // Task t: blocks 2t, 2t+1 (68 bytes, dword aligned when K % 64 == 0):
-// d0 | q0[32] | d1 | q1[32] (ggml block_q8_0: f16 d, int8 qs[32]).
+// d0 | q0[32] | d1 | q1[32] (ggml block_q8_0: f16 d, int8 qs[32]); w = d*q.
 struct Q80 {
     struct XS {
-        uint32_t X[3][16];
+        uint32_t X[kPlanes][16];
         float s0, s1;
     };
     struct Frag {
@@ -259,9 +270,7 @@ struct Q80 {
     UQ_HD static LC lane_consts(int) { return LC{0}; }
     UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &) {
         const int dw = task * 16;
-        copy_dw(s.X[0], P.p0 + dw);
-        copy_dw(s.X[1], P.p1 + dw);
-        copy_dw(s.X[2], P.p2 + dw);
+        for (int q = 0; q < kPlanes; q++) copy_dw(s.X[q], P.p[q] + dw);
         s.s0 = P.scale[2 * task];
         s.s1 = P.scale[2 * task + 1];
     }
@@ -275,23 +284,21 @@ struct Q80 {
         f.w4 = ld1(B + 64);
         return f;
     }
-    UQ_HD static float dot(const Frag &f, const XS &s, const LC &) {
+    UQ_HD static double dot(const Frag &f, const XS &s, const LC &) {
         const uint32_t w[17] = {f.w0.x, f.w0.y, f.w0.z, f.w0.w, f.w1.x, f.w1.y, f.w1.z, f.w1.w,
                                 f.w2.x, f.w2.y, f.w2.z, f.w2.w, f.w3.x, f.w3.y, f.w3.z, f.w3.w, f.w4};
-        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        int a[kPlanes] = {0, 0, 0, 0}, b[kPlanes] = {0, 0, 0, 0};
         for (int i = 0; i < 8; i++) {
             const uint32_t q0 = alignbyte(w[i + 1], w[i], 2);  // bytes 2..33
             const uint32_t q1 = w[9 + i];                       // bytes 36..67
-            a0 = sdot4(q0, s.X[0][i], a0);
-            a1 = sdot4(q0, s.X[1][i], a1);
-            a2 = sdot4(q0, s.X[2][i], a2);
-            b0 = sdot4(q1, s.X[0][8 + i], b0);
-            b1 = sdot4(q1, s.X[1][8 + i], b1);
-            b2 = sdot4(q1, s.X[2][8 + i], b2);
+            for (int q = 0; q < kPlanes; q++) {
+                a[q] = sdot4(q0, s.X[q][i], a[q]);
+                b[q] = sdot4(q1, s.X[q][8 + i], b[q]);
+            }
         }
         const float d0 = f16_lo(w[0]), d1 = f16_hi(w[8]);
-        const float r = (d0 * s.s0) * combine3(a0, a1, a2);
-        return fmaf(d1 * s.s1, combine3(b0, b1, b2), r);
+        const double r = (double)(d0 * s.s0) * plane_sum(a[0], a[1], a[2], a[3]);
+        return fma((double)(d1 * s.s1), plane_sum(b[0], b[1], b[2], b[3]), r);
     }
 };
 
