@@ -10,11 +10,11 @@
 #include <cstdint>
 #include <cstring>
 
-#if defined(__HIP_DEVICE_COMPILE__)
-#include <hip/hip_runtime.h>
-#define UQ_HD __device__ __forceinline__
-#else
 #include <cmath>
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define UQ_HD __host__ __device__ __forceinline__
+#else
 #define UQ_HD inline
 #endif
 

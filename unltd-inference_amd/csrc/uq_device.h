@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "uq_policies.h"
+
 namespace uq {
 
 // ---------------------------------------------------------------------------
@@ -97,62 +99,66 @@ __device__ __forceinline__ double group8_sum_d(double v) {
 }
 
 // ---------------------------------------------------------------------------
-// Activation digit planes (layout read by uq_policies.h).
-// Each run of 32 activations gets a power-of-two scale s = 2^(ex-30), where
-// 2^(ex-1) <= max|x| < 2^ex, and the integers X = rint(x / s) (|X| <= 2^30,
-// exact scaling, round-half-even). X is split into four signed base-256
-// digits X = b3*2^24 + b2*2^16 + b1*2^8 + b0 (b0..b2 in [-128,127], b3 in
-// [-64,64]) stored as byte planes, so v_dot4_i32_i8 multiplies them with
-// packed weight quants exactly. The run sum s*sum(X) is kept as an exact
-// double. Error per activation <= s/2 <= max|x_run| * 2^-30. Non-finite
-// activations are outside this path's contract (outputs unspecified).
+// Activation prep into the layout of uq_policies.h (XView): one thread per
+// element-dword w (4 activations); a run of 128 activations is one aligned
+// group of 32 lanes. The loop is padded to whole runs so every lane of a run
+// takes part in its reductions; padding elements are zero and not stored.
+// Error per activation <= s/2 <= max|x_run| * 2^-30. Non-finite activations
+// are outside this path's contract (outputs unspecified).
 // ---------------------------------------------------------------------------
-constexpr int kXPlanes = 4;
-struct XPlanes {
-    uint32_t *p[kXPlanes];  // K/4 dwords each
-    float *scale;           // K/32 run scales s
-    double *xsum;           // K/32 run sums s*sum(X)
+struct XLayout {
+    uint32_t *xq;
+    int *aux;
+    float *scale;
+    double *gsum;
+    int NT;
 };
 
-__device__ __forceinline__ uint32_t digits4(int X, int &b1, int &b2, int &b3) {
-    const int d0 = (int)(int8_t)(X & 0xFF);
-    const int X1 = (X - d0) >> 8;
-    b1 = (int)(int8_t)(X1 & 0xFF);
-    const int X2 = (X1 - b1) >> 8;
-    b2 = (int)(int8_t)(X2 & 0xFF);
-    b3 = (X2 - b2) >> 8;
-    return (uint32_t)d0 & 0xFF;
-}
+__device__ __forceinline__ uint32_t digit(int v) { return (uint32_t)v & 0xFFu; }
 
-// All threads of the block cooperate; K % 32 == 0. Each group of 8 lanes
-// handles one run (4 activations per lane). Lanes of a run are always
-// active together because runs are aligned to 8-lane groups.
-__device__ __forceinline__ void prep_x_planes(const float *__restrict__ x, int K, XPlanes P) {
-    for (int base = threadIdx.x * 4; base < K; base += blockDim.x * 4) {
-        const float v[4] = {x[base], x[base + 1], x[base + 2], x[base + 3]};
+template <class F>
+__device__ __forceinline__ void prep_x(const float *__restrict__ x, int K, XLayout L) {
+    const int nw = K >> 2;
+    const int nw_pad = (nw + 31) & ~31;
+    for (int w = threadIdx.x; w < ((nw_pad + blockDim.x - 1) / blockDim.x) * blockDim.x; w += blockDim.x) {
+        const bool in = w < nw;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (in)
+            for (int i = 0; i < 4; i++) v[i] = x[4 * w + i];
         float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        am = group8_max(am);
+        for (int off = 16; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
         int ex = 0;
         if (am > 0.0f) (void)frexpf(am, &ex);
-        uint32_t w[kXPlanes] = {0, 0, 0, 0};
+        uint32_t pl[4] = {0, 0, 0, 0};
         double xs = 0.0;
         for (int i = 0; i < 4; i++) {
             const int X = am > 0.0f ? (int)rintf(ldexpf(v[i], 30 - ex)) : 0;
-            int b1, b2, b3;
-            const uint32_t b0 = digits4(X, b1, b2, b3);
-            w[0] |= b0 << (8 * i);
-            w[1] |= ((uint32_t)b1 & 0xFF) << (8 * i);
-            w[2] |= ((uint32_t)b2 & 0xFF) << (8 * i);
-            w[3] |= ((uint32_t)b3 & 0xFF) << (8 * i);
+            const int d0 = (int)(int8_t)(X & 0xFF), X1 = (X - d0) >> 8;
+            const int d1 = (int)(int8_t)(X1 & 0xFF), X2 = (X1 - d1) >> 8;
+            const int d2 = (int)(int8_t)(X2 & 0xFF), d3 = (X2 - d2) >> 8;
+            pl[0] |= digit(d0) << (8 * i);
+            pl[1] |= digit(d1) << (8 * i);
+            pl[2] |= digit(d2) << (8 * i);
+            pl[3] |= digit(d3) << (8 * i);
             xs += (double)X;
         }
-        const int dw = base >> 2;
-        for (int q = 0; q < kXPlanes; q++) P.p[q][dw] = w[q];
+        const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
+        int t, i;
+        F::xmap(w, t, i);
+        if (in)
+            for (int q = 0; q < 4; q++) L.xq[xq_index(q, i, t, L.NT)] = pl[q];
         xs = group8_sum_d(xs);
-        if ((threadIdx.x & 7) == 0) {
-            const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
-            P.scale[base >> 5] = s;
-            P.xsum[base >> 5] = xs * (double)s;
+        if (in && (w & 7) == 0) L.gsum[w >> 3] = xs * (double)s;
+        if (in && (w & 31) == 0) L.scale[w >> 5] = s;
+        if constexpr (F::kAux) {
+            int P[4];
+            for (int q = 0; q < 4; q++) P[q] = group4_sum_i(sdot4(pl[q], 0x01010101u, 0));
+            if (in && (w & 3) == 0) {
+                int lo, hi;
+                F::aux_of(P, lo, hi);
+                L.aux[aux_index(i >> 2, t, L.NT)] = lo;
+                L.aux[aux_index(4 + (i >> 2), t, L.NT)] = hi;
+            }
         }
     }
 }

@@ -17,53 +17,82 @@ using namespace uq;
 
 namespace {
 
-// prep_x_planes (uq_device.h) for the whole vector
-struct HostPlanes {
-    std::vector<uint32_t> p[kPlanes];
+// prep_x<F> (uq_device.h) for the whole vector, same layout
+template <class F>
+struct HostLayout {
+    std::vector<uint32_t> xq;
+    std::vector<int> aux;
     std::vector<float> scale;
-    std::vector<double> xsum;
-    XPlanesView view() const {
-        return XPlanesView{{p[0].data(), p[1].data(), p[2].data(), p[3].data()}, scale.data(), xsum.data()};
-    }
+    std::vector<double> gsum;
+    int NT = 0;
+    XView view() const { return XView{xq.data(), aux.data(), scale.data(), gsum.data(), NT}; }
 };
 
-HostPlanes prep_planes(const float *x, int K) {
-    HostPlanes P;
-    for (int q = 0; q < kPlanes; q++) P.p[q].assign(K / 4, 0);
-    P.scale.assign(K / 32, 0.0f);
-    P.xsum.assign(K / 32, 0.0);
-    for (int run = 0; run < K / 32; run++) {
-        const float *v = x + 32 * run;
+template <class F>
+HostLayout<F> prep_layout(const float *x, int K) {
+    HostLayout<F> L;
+    L.NT = round_tasks(F::ntasks(K));
+    L.xq.assign((size_t)L.NT * 64, 0);
+    L.aux.assign((size_t)L.NT * 8, 0);
+    const int nw = K / 4, nruns = (nw + 31) / 32;
+    L.scale.assign(nruns, 0.0f);
+    L.gsum.assign(K / 32, 0.0);
+    for (int run = 0; run < nruns; run++) {
         float am = 0.0f;
-        for (int i = 0; i < 32; i++) am = std::fmax(am, std::fabs(v[i]));
+        for (int w = 32 * run; w < 32 * run + 32 && w < nw; w++)
+            for (int i = 0; i < 4; i++) am = std::fmax(am, std::fabs(x[4 * w + i]));
         int ex = 0;
         if (am > 0.0f) (void)std::frexp(am, &ex);
-        double part[8];
-        for (int g = 0; g < 8; g++) {
-            uint32_t w[kPlanes] = {0, 0, 0, 0};
-            double xs = 0.0;
+        const float s = am > 0.0f ? std::ldexp(1.0f, ex - 30) : 0.0f;
+        L.scale[run] = s;
+        double part[32];
+        int P[32][kPlanes];
+        for (int k = 0; k < 32; k++) {
+            const int w = 32 * run + k;
+            part[k] = 0.0;
+            for (int q = 0; q < kPlanes; q++) P[k][q] = 0;
+            if (w >= nw) continue;
+            uint32_t pl[kPlanes] = {0, 0, 0, 0};
             for (int i = 0; i < 4; i++) {
-                const int X = am > 0.0f ? (int)std::rint(std::ldexp(v[4 * g + i], 30 - ex)) : 0;
+                const int X = am > 0.0f ? (int)std::rint(std::ldexp(x[4 * w + i], 30 - ex)) : 0;
                 const int d0 = (int)(int8_t)(X & 0xFF), X1 = (X - d0) >> 8;
                 const int d1 = (int)(int8_t)(X1 & 0xFF), X2 = (X1 - d1) >> 8;
                 const int d2 = (int)(int8_t)(X2 & 0xFF), d3 = (X2 - d2) >> 8;
                 const int dd[4] = {d0, d1, d2, d3};
-                for (int q = 0; q < kPlanes; q++) w[q] |= ((uint32_t)dd[q] & 0xFF) << (8 * i);
-                xs += (double)X;
+                for (int q = 0; q < kPlanes; q++) pl[q] |= ((uint32_t)dd[q] & 0xFF) << (8 * i);
+                part[k] += (double)X;
             }
-            for (int q = 0; q < kPlanes; q++) P.p[q][8 * run + g] = w[q];
-            part[g] = xs;
+            int t, i;
+            F::xmap(w, t, i);
+            for (int q = 0; q < kPlanes; q++) {
+                L.xq[xq_index(q, i, t, L.NT)] = pl[q];
+                P[k][q] = sdot4(pl[q], 0x01010101u, 0);
+            }
         }
-        // group8_sum_d: quad_perm 1,0,3,2 / 2,3,0,1 / row_half_mirror, lane 0
-        double t[8];
-        for (int i = 0; i < 8; i++) t[i] = part[i] + part[i ^ 1];
-        for (int i = 0; i < 8; i++) part[i] = t[i] + t[i ^ 2];
-        const double xs = part[0] + part[7];
-        const float s = am > 0.0f ? std::ldexp(1.0f, ex - 30) : 0.0f;
-        P.scale[run] = s;
-        P.xsum[run] = xs * (double)s;
+        // group8_sum_d: quad_perm 1,0,3,2 / 2,3,0,1 / row_half_mirror, lane 0 of 8
+        for (int g = 0; g < 4; g++) {
+            const int w0 = 32 * run + 8 * g;
+            if (w0 >= nw) continue;
+            double *pp = part + 8 * g, t1[8], t2[8];
+            for (int i = 0; i < 8; i++) t1[i] = pp[i] + pp[i ^ 1];
+            for (int i = 0; i < 8; i++) t2[i] = t1[i] + t1[i ^ 2];
+            L.gsum[w0 / 8] = (t2[0] + t2[7]) * (double)s;
+        }
+        if constexpr (F::kAux) {
+            for (int k = 0; k < 32; k += 4) {
+                const int w = 32 * run + k;
+                if (w >= nw) continue;
+                int Ps[kPlanes];
+                for (int q = 0; q < kPlanes; q++) Ps[q] = P[k][q] + P[k + 1][q] + P[k + 2][q] + P[k + 3][q];
+                int t, i, lo, hi;
+                F::xmap(w, t, i);
+                F::aux_of(Ps, lo, hi);
+                L.aux[aux_index(i >> 2, t, L.NT)] = lo;
+                L.aux[aux_index(4 + (i >> 2), t, L.NT)] = hi;
+            }
+        }
     }
-    return P;
+    return L;
 }
 
 // wave_sum_d (uq_device.h): the DPP tree, lane 63's value
@@ -89,8 +118,8 @@ double wave_sum64(const double *in) {
 
 template <class F>
 void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int K, int N) {
-    const HostPlanes P = prep_planes(x, K);
-    const XPlanesView PV = P.view();
+    const HostLayout<F> L = prep_layout<F>(x, K);
+    const XView PV = L.view();
     const int ntask = F::ntasks(K);
     for (int row = 0; row < N; row++) {
         const uint8_t *R = W + (size_t)row * row_bytes;

@@ -13,6 +13,9 @@
 // activation data is read from LDS once and stays in VGPRs while the next
 // row's weights are prefetched with 128-bit loads. Row sums are reduced
 // across the wave with DPP.
+#include <map>
+#include <mutex>
+
 #include "uq_device.h"
 #include "uq_internal.h"
 #include "uq_policies.h"
@@ -23,6 +26,10 @@ namespace {
 
 constexpr int WAVES = 4;
 constexpr int TPB = 64 * WAVES;
+#ifndef UQ_GEMV_DEPTH
+#define UQ_GEMV_DEPTH 1
+#endif
+constexpr int kDepth = UQ_GEMV_DEPTH;  // rows of weights in flight per wave
 constexpr size_t kLdsCap = 64 * 1024;
 
 int num_cus() {
@@ -39,18 +46,27 @@ int num_cus() {
 }
 
 // ---------------------------- gemv_quant -----------------------------------
-// LDS: 4 digit planes (K bytes each), then K/32 run sums (f64), then K/32
-// run scales (f32)
-__host__ __device__ inline size_t planes_bytes(int K) {
-    return 4 * (size_t)K + (size_t)(K / 32) * 8 + (size_t)(K / 32) * 4;
+// LDS of the activation layout (uq_policies.h): planes 4*16*NT dwords, aux
+// 8*NT ints (Q6_K), K/128 run scales, K/32 group sums.
+template <class F>
+__host__ __device__ inline size_t x_lds_bytes(int K) {
+    const size_t NT = round_tasks(F::ntasks(K));
+    return NT * 256 + (F::kAux ? NT * 32 : 0) + (size_t)(K / 128 + 1) * 4 + (size_t)(K / 32) * 8;
 }
 
-__device__ inline XPlanes planes_at(uint8_t *lds, int K) {
-    XPlanes P;
-    for (int q = 0; q < kXPlanes; q++) P.p[q] = (uint32_t *)(lds + (size_t)q * K);
-    P.xsum = (double *)(lds + 4 * (size_t)K);
-    P.scale = (float *)(lds + 4 * (size_t)K + (size_t)(K / 32) * 8);
-    return P;
+template <class F>
+__device__ inline XLayout x_layout_at(uint8_t *lds, int K) {
+    XLayout L;
+    L.NT = round_tasks(F::ntasks(K));
+    size_t o = 0;
+    L.gsum = (double *)(lds + o);  // 8-byte aligned first
+    o += (size_t)(K / 32) * 8;
+    L.xq = (uint32_t *)(lds + o);
+    o += (size_t)L.NT * 256;
+    L.aux = (int *)(lds + o);
+    o += F::kAux ? (size_t)L.NT * 32 : 0;
+    L.scale = (float *)(lds + o);
+    return L;
 }
 
 __device__ inline float swiglu1(float g, float u) {
@@ -58,73 +74,93 @@ __device__ inline float swiglu1(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-// PAIR: W and W2 (gate, up) share x; writes swiglu(W x, W2 x).
-template <class F, bool CACHED, bool PAIR>
-__global__ __launch_bounds__(TPB) void gemv_kernel(const uint8_t *__restrict__ W,
-                                                   const uint8_t *__restrict__ W2,
-                                                   size_t row_bytes, int K, int N,
-                                                   const float *__restrict__ x,
-                                                   float *__restrict__ y) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const XPlanes P = planes_at(lds, K);
-    prep_x_planes(x, K, P);
-    __syncthreads();
-    const XPlanesView PV{{P.p[0], P.p[1], P.p[2], P.p[3]}, P.scale, P.xsum};
+#ifdef UQ_GEMV_WAVES_PER_EU
+#define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(UQ_GEMV_WAVES_PER_EU)))
+#else
+#define UQ_GEMV_OCC
+#endif
 
+// One unit = one task of one row. A wave walks the units of its rows in
+// order (the tasks of row 0, then row 1, ...); a ring of kDepth units keeps
+// that many weight loads in flight, each slot reloaded right after it is
+// consumed (no register copies), and the first kDepth units are issued
+// before the activation prep so their HBM latency overlaps it.
+// XREG (one task per lane) keeps the lane's activation digits in VGPRs;
+// otherwise they are read from LDS for every unit.
+// PAIR: W and W2 (gate, up) share x; writes swiglu(W x, W2 x).
+template <class F, bool PAIR, bool XREG>
+__global__ __launch_bounds__(TPB) UQ_GEMV_OCC void gemv_kernel(const uint8_t *__restrict__ W,
+                                                               const uint8_t *__restrict__ W2,
+                                                               size_t row_bytes, int K, int N,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int ntask = F::ntasks(K);
+    const int T = (ntask + 63) >> 6;  // tasks per lane per row
     const typename F::LC c = F::lane_consts(lane);
     const int wave = blockIdx.x * WAVES + (threadIdx.x >> 6);
     const int nwave = gridDim.x * WAVES;
+    const int U = (wave < N ? (N - 1 - wave) / nwave + 1 : 0) * T;
 
-    if (CACHED) {
-        const bool active = lane < ntask;
-        typename F::XS xs;
-        if (active) F::load_x(xs, PV, lane, c);
-        int row = wave;
-        if (row >= N) return;
-        typename F::Frag cur{}, cur2{}, nxt{}, nxt2{};
-        if (active) {
-            cur = F::load_w(W + (size_t)row * row_bytes, lane, c);
-            if (PAIR) cur2 = F::load_w(W2 + (size_t)row * row_bytes, lane, c);
+    typename F::Frag f[kDepth], f2[kDepth];
+    int pr = 0, pt = 0;  // next unit to load: row index, task iteration
+    auto issue = [&](typename F::Frag &dst, typename F::Frag &dst2) {
+        const int t = lane + 64 * pt;
+        const size_t off = (size_t)(wave + pr * nwave) * row_bytes;
+        if (t < ntask) {
+            dst = F::load_w(W + off, t, c);
+            if (PAIR) dst2 = F::load_w(W2 + off, t, c);
         }
-        for (; row < N; row += nwave) {
-            const int nrow = row + nwave;
-            if (active && nrow < N) {
-                nxt = F::load_w(W + (size_t)nrow * row_bytes, lane, c);
-                if (PAIR) nxt2 = F::load_w(W2 + (size_t)nrow * row_bytes, lane, c);
-            }
-            double g = 0.0, u = 0.0;
-            if (active) {
-                g = F::dot(cur, xs, c);
-                if (PAIR) u = F::dot(cur2, xs, c);
-            }
-            g = wave_sum_d(g);
-            if (PAIR) {
-                u = wave_sum_d(u);
-                if (lane == 0) y[row] = swiglu1((float)g, (float)u);
-            } else if (lane == 0) {
-                y[row] = (float)g;
-            }
-            cur = nxt;
-            if (PAIR) cur2 = nxt2;
+        if (++pt == T) {
+            pt = 0;
+            ++pr;
         }
-    } else {
-        for (int row = wave; row < N; row += nwave) {
-            const uint8_t *R = W + (size_t)row * row_bytes;
-            double g = 0.0, u = 0.0;
-            for (int t = lane; t < ntask; t += 64) {
-                typename F::XS xs;
-                F::load_x(xs, PV, t, c);
-                g += F::dot(F::load_w(R, t, c), xs, c);
-                if (PAIR) u += F::dot(F::load_w(W2 + (size_t)row * row_bytes, t, c), xs, c);
+    };
+#pragma unroll
+    for (int d = 0; d < kDepth; d++)
+        if (d < U) issue(f[d], f2[d]);
+
+    const XLayout L = x_layout_at<F>(lds, K);
+    prep_x<F>(x, K, L);
+    __syncthreads();
+    if (U == 0) return;
+    const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
+    typename F::XS xr;
+    if (XREG && lane < ntask) F::load_x(xr, PV, lane, c);
+
+    double g = 0.0, u = 0.0;
+    int cr = 0, ct = 0;  // unit being consumed
+    for (int u0 = 0; u0 < U; u0 += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; d++) {
+            if (u0 + d >= U) break;  // wave-uniform
+            const int t = lane + 64 * ct;
+            if (t < ntask) {
+                if (XREG) {
+                    g += F::dot(f[d], xr, c);
+                    if (PAIR) u += F::dot(f2[d], xr, c);
+                } else {
+                    typename F::XS xs;
+                    F::load_x(xs, PV, t, c);
+                    g += F::dot(f[d], xs, c);
+                    if (PAIR) u += F::dot(f2[d], xs, c);
+                }
             }
-            g = wave_sum_d(g);
-            if (PAIR) {
-                u = wave_sum_d(u);
-                if (lane == 0) y[row] = swiglu1((float)g, (float)u);
-            } else if (lane == 0) {
-                y[row] = (float)g;
+            if (u0 + d + kDepth < U) issue(f[d], f2[d]);
+            if (++ct == T) {
+                const int row = wave + cr * nwave;
+                g = wave_sum_d(g);
+                if (PAIR) {
+                    u = wave_sum_d(u);
+                    if (lane == 0) y[row] = swiglu1((float)g, (float)u);
+                } else if (lane == 0) {
+                    y[row] = (float)g;
+                }
+                g = 0.0;
+                u = 0.0;
+                ct = 0;
+                ++cr;
             }
         }
     }
@@ -189,33 +225,62 @@ __global__ __launch_bounds__(TPB) void gemv_generic_kernel(uq_dtype dt, const ui
     }
 }
 
+// Workgroups for a row-walking kernel: exactly the number that are resident
+// at once (occupancy from VGPRs/LDS), so no workgroup waits for a second
+// round, then trimmed so every wave walks the same number of rows.
+int blocks_per_cu(const void *kernel, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, size_t>, int> cache;
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find({kernel, lds});
+    if (it != cache.end()) return it->second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, TPB, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    cache[{kernel, lds}] = per_cu;
+    return per_cu;
+}
+
+int resident_grid(const void *kernel, size_t lds, int N) {
+    int per_cu = blocks_per_cu(kernel, lds);
+#ifdef UQ_WG_PER_CU
+    per_cu = UQ_WG_PER_CU;
+#endif
+    const int max_waves = num_cus() * per_cu * WAVES;
+    const int rows_per_wave = (N + max_waves - 1) / max_waves;
+    const int waves = (N + rows_per_wave - 1) / rows_per_wave;
+    return (waves + WAVES - 1) / WAVES;
+}
+
+#ifndef UQ_GEMV_XREG
+#define UQ_GEMV_XREG 1
+#endif
+
 template <class F, bool PAIR>
 hipError_t launch_fast(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
-    const size_t lds = planes_bytes(K);
-    // >= 2 rows per wave so the prep is amortised; at most 4 workgroups per CU
-    int grid = (N + 2 * WAVES - 1) / (2 * WAVES);
-    const int cap = num_cus() * 4;
-    if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
-    if (F::ntasks(K) <= 64)
-        hipLaunchKernelGGL((gemv_kernel<F, true, PAIR>), dim3(grid), dim3(TPB), lds, s, w.bytes, w2,
-                           w.row_bytes, K, N, x, y);
-    else
-        hipLaunchKernelGGL((gemv_kernel<F, false, PAIR>), dim3(grid), dim3(TPB), lds, s, w.bytes, w2,
-                           w.row_bytes, K, N, x, y);
+    const size_t lds = x_lds_bytes<F>(K);
+    if (UQ_GEMV_XREG && F::ntasks(K) <= 64) {
+        const void *k = (const void *)gemv_kernel<F, PAIR, true>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, true>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds, s,
+                           w.bytes, w2, w.row_bytes, K, N, x, y);
+    } else {
+        const void *k = (const void *)gemv_kernel<F, PAIR, false>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, false>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds, s,
+                           w.bytes, w2, w.row_bytes, K, N, x, y);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_any(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
     if (N == 0) return hipSuccess;
-    const bool pair = w2 != nullptr, fits = planes_bytes(K) <= kLdsCap;
-    if (fits && w.dtype == UQ_Q4_K)
+    const bool pair = w2 != nullptr;
+    if (w.dtype == UQ_Q4_K && x_lds_bytes<Q4K>(K) <= kLdsCap)
         return pair ? launch_fast<Q4K, true>(w, w2, x, y, s) : launch_fast<Q4K, false>(w, w2, x, y, s);
-    if (fits && w.dtype == UQ_Q6_K)
+    if (w.dtype == UQ_Q6_K && x_lds_bytes<Q6K>(K) <= kLdsCap)
         return pair ? launch_fast<Q6K, true>(w, w2, x, y, s) : launch_fast<Q6K, false>(w, w2, x, y, s);
-    if (fits && w.dtype == UQ_Q8_0 && K % 64 == 0)
+    if (w.dtype == UQ_Q8_0 && K % 64 == 0 && x_lds_bytes<Q80>(K) <= kLdsCap)
         return pair ? launch_fast<Q80, true>(w, w2, x, y, s) : launch_fast<Q80, false>(w, w2, x, y, s);
     int grid = (N + WAVES - 1) / WAVES;
     if (grid > num_cus() * 8) grid = num_cus() * 8;
@@ -446,16 +511,15 @@ template <class F>
 hipError_t launch_q8k_fast(const WeightsView &w, const float *x, float *y, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
     const Q8KLayout L = q8k_layout<F>(K);
-    int grid = (N + 2 * WAVES - 1) / (2 * WAVES);
-    const int cap = num_cus() * 4;
-    if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
-    if (F::ntasks(K) <= 64)
-        hipLaunchKernelGGL((gemv_q8k_kernel<F, true>), dim3(grid), dim3(TPB), L.total, s, w.bytes,
-                           w.row_bytes, K, N, x, y);
-    else
-        hipLaunchKernelGGL((gemv_q8k_kernel<F, false>), dim3(grid), dim3(TPB), L.total, s, w.bytes,
-                           w.row_bytes, K, N, x, y);
+    if (F::ntasks(K) <= 64) {
+        const void *k = (const void *)gemv_q8k_kernel<F, true>;
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, true>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total, s,
+                           w.bytes, w.row_bytes, K, N, x, y);
+    } else {
+        const void *k = (const void *)gemv_q8k_kernel<F, false>;
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, false>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total, s,
+                           w.bytes, w.row_bytes, K, N, x, y);
+    }
     return hipGetLastError();
 }
 

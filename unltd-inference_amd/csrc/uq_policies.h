@@ -27,20 +27,51 @@ namespace uq {
 
 constexpr int kBQ4K = 144, kBQ6K = 210, kBQ8_0 = 34;
 
-// Activation planes as prepared in LDS (see prep_x_planes): each run of 32
-// activations has a power-of-two scale s and integers X = rint(x/s),
-// |X| <= 2^30, stored as four signed base-256 digit planes
-// X = b3*2^24 + b2*2^16 + b1*2^8 + b0.
+// Activation layout, shared by the device prep (uq_device.h), the kernels
+// and the CPU emulation.
+//  * Runs of 128 activations share a power-of-two scale s (2^(ex-1) <=
+//    max|x_run| < 2^ex, s = 2^(ex-30)); X = rint(x/s), |X| <= 2^30, is held
+//    as four signed base-256 digit planes X = b3*2^24 + b2*2^16 + b1*2^8 + b0.
+//  * Every task (one lane's 64-element slice of a row, see the policies)
+//    owns 16 dwords per plane. They are stored task-major,
+//        xq[((q*4 + i/4) * NT + t) * 4 + i%4]   (plane q, dword i, task t),
+//    NT = tasks rounded up to 64, so when the 64 lanes of a wave read dwords
+//    4*i4..4*i4+3 of their tasks they read 64 consecutive 16-byte slots: one
+//    ds_read_b128 without bank conflicts.
+//  * A task covers exactly half a run: its scale is scale[t/2].
+//  * gsum[g] = s * sum(X) over each 32-element group g (Q4_K mins), exact.
+//  * aux: per task 8 ints stored the same way (Q6_K: 32 * the digit sums of
+//    each quarter, see Q6K).
 constexpr int kPlanes = 4;
-struct XPlanesView {
-    const uint32_t *p[kPlanes];  // K/4 dwords per plane
-    const float *scale;          // K/32 run scales s
-    const double *xsum;          // K/32 run sums s*sum(X), exact
+constexpr int kRunLen = 128;
+struct XView {
+    const uint32_t *xq;
+    const int *aux;
+    const float *scale;
+    const double *gsum;
+    int NT;
 };
-
 template <int N>
 UQ_HD void copy_dw(uint32_t (&dst)[N], const uint32_t *src) {
     for (int i = 0; i < N; i++) dst[i] = src[i];
+}
+
+UQ_HD int round_tasks(int ntask) { return (ntask + 63) & ~63; }
+UQ_HD size_t xq_index(int q, int i, int t, int NT) {
+    return ((size_t)(q * 4 + (i >> 2)) * NT + t) * 4 + (i & 3);
+}
+UQ_HD size_t aux_index(int k, int t, int NT) { return ((size_t)(k >> 2) * NT + t) * 4 + (k & 3); }
+
+UQ_HD void load_planes(uint32_t (&X)[kPlanes][16], const XView &V, int t) {
+    for (int q = 0; q < kPlanes; q++)
+        for (int i4 = 0; i4 < 4; i4++) {
+            u4 v;  // 16-byte slot (the layout keeps every slot 16-byte aligned)
+            __builtin_memcpy(&v, __builtin_assume_aligned(V.xq + xq_index(q, 4 * i4, t, V.NT), 16), 16);
+            X[q][4 * i4] = v.x;
+            X[q][4 * i4 + 1] = v.y;
+            X[q][4 * i4 + 2] = v.z;
+            X[q][4 * i4 + 3] = v.w;
+        }
 }
 
 // sum(q*X) of a group from its four exact plane dots, as an exact double:
@@ -53,16 +84,17 @@ UQ_HD double plane_sum(int d0, int d1, int d2, int d3) {
 // ============================ Q4_K ==========================================
 // Task t: block kb = t/4, group pair p = t%4 = lane%4: qs bytes [32p, 32p+32).
 // Low nibble of qs byte 32p+l is element 64p+l (group 2p), high nibble is
-// element 64p+32+l (group 2p+1) (quants.rs:146-151).
-// Row contribution, exactly as the reference's per-element weights
-// w = (d*sc)*q - dmin*m (quants.rs:151) summed over the task:
-//   sum_g (d*sc_g*s_g) * sum(q*X) - (dmin*m_g) * (s_g*sum(X)),
-// with the integer sums exact and the accumulation in f64.
+// element 64p+32+l (group 2p+1) (quants.rs:146-151). The task's 64
+// activations are contiguous: element-dword w = 16t + i.
+// Row contribution, the reference's per-element w = (d*sc)*q - dmin*m
+// (quants.rs:151) summed over the task:
+//   d*s*(sc0*sum0(q*X) + sc1*sum1(q*X)) - dmin*(m0*gsum0 + m1*gsum1),
+// integer sums exact, the rest in f64.
 struct Q4K {
     struct XS {
         uint32_t X[kPlanes][16];
-        float slo, shi;
-        double xslo, xshi;  // s*sum(X) of groups 2p, 2p+1
+        float s;
+        double gs0, gs1;
     };
     struct Frag {
         u4 h, qa, qb;
@@ -77,8 +109,13 @@ struct Q4K {
         bool hi;
         uint32_t shA0, shA1, shC0, shC1, shB0, shB1, wA, wB;
     };
-    static constexpr int kTasksPerBlock = 4;
+    static constexpr bool kAux = false;
     UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    // element-dword w -> (task, dword within task)
+    UQ_HD static void xmap(int w, int &t, int &i) {
+        t = w >> 4;
+        i = w & 15;
+    }
     UQ_HD static LC lane_consts(int lane) {
         LC c;
         c.p = lane & 3;
@@ -103,15 +140,11 @@ struct Q4K {
         m0 = ubfe(srcC, c.shC0, c.wA) | (ubfe(S1, c.shB0, c.wB) << 4);
         m1 = ubfe(srcC, c.shC1, c.wA) | (ubfe(S1, c.shB1, c.wB) << 4);
     }
-    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &c) {
-        const int kb = task >> 2;
-        const int dw = kb * 64 + c.p * 16;
-        for (int q = 0; q < kPlanes; q++) copy_dw(s.X[q], P.p[q] + dw);
-        const int run = kb * 8 + 2 * c.p;
-        s.slo = P.scale[run];
-        s.shi = P.scale[run + 1];
-        s.xslo = P.xsum[run];
-        s.xshi = P.xsum[run + 1];
+    UQ_HD static void load_x(XS &s, const XView &V, int t, const LC &) {
+        load_planes(s.X, V, t);
+        s.s = V.scale[t >> 1];
+        s.gs0 = V.gsum[2 * t];
+        s.gs1 = V.gsum[2 * t + 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
         const uint8_t *B = row + (size_t)(task >> 2) * kBQ4K;
@@ -134,12 +167,11 @@ struct Q4K {
         uint32_t sc0, sc1, m0, m1;
         scales(f.h, c, sc0, sc1, m0, m1);
         const float d = f16_lo(f.h.x), dmin = f16_hi(f.h.x);
-        // d*sc and dmin*m are exact in f32 (<= 17 significant bits)
-        double r = (double)((d * (float)sc0) * s.slo) * plane_sum(a[0], a[1], a[2], a[3]);
-        r = fma((double)((d * (float)sc1) * s.shi), plane_sum(b[0], b[1], b[2], b[3]), r);
-        r = fma(-(double)(dmin * (float)m0), s.xslo, r);
-        r = fma(-(double)(dmin * (float)m1), s.xshi, r);
-        return r;
+        const double main = fma((double)(int)sc0, plane_sum(a[0], a[1], a[2], a[3]),
+                                (double)(int)sc1 * plane_sum(b[0], b[1], b[2], b[3]));
+        const double mins = fma((double)(int)m0, s.gs0, (double)(int)m1 * s.gs1);
+        // d*s is exact in f32 (a power-of-two scaling of d)
+        return fma((double)(d * s.s), main, -(double)dmin * mins);
     }
 };
 
@@ -150,6 +182,7 @@ struct Q4K {
 //               (j = 1, 3); low nibble for j < 2, high for j >= 2
 //   high 2 bits: bits 2j..2j+1 of qh byte 32h + 16u + l
 //   scale: int8 at 192 + 8h + 2j + u; d: f16 at 208 (quants.rs:185-195).
+// Task dword 4j + i' holds elements 256kb + 128h + 32j + 16u + 4i'.
 // Blocks are 2-byte aligned, so every 16-byte field is loaded as a
 // dword-aligned 20-byte window and realigned with v_alignbyte.
 struct Q6KWindows {
@@ -184,35 +217,33 @@ UQ_HD int q6k_scale(const uint32_t (&E)[4], int h, int u, int j) {
     return sbfe((int)w, 8 * (2 * (j & 1) + u), 8);
 }
 
-// Row contribution: sum_j d*sc_j*s_j * sum((raw-32)*X) over each quarter,
+// Row contribution: d*s * sum_j sc_j * sum((raw-32)*X) over each quarter,
 // the reference's w = d*(sc*q) with q = raw-32 (quants.rs:193-195).
+// aux holds, per task and quarter j, C[j] = 32*(P1*256 + P0) and
+// C[4+j] = 32*(P3*256 + P2) where Pq is the sum of plane q's digits over the
+// quarter, so sum((raw-32)*X) = (D3*256+D2 - C[4+j])*65536 + (D1*256+D0 - C[j]).
 struct Q6K {
     struct XS {
         uint32_t X[kPlanes][16];
-        int Clo[4], Chi[4];  // 32*(P1*256+P0), 32*(P3*256+P2): plane digit sums
-        float s[4];
+        int C[8];
+        float s;
     };
     typedef Q6KWindows Frag;
     struct LC {
         int h, u;
     };
-    static constexpr int kTasksPerBlock = 4;
+    static constexpr bool kAux = true;
     UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
+    UQ_HD static void xmap(int w, int &t, int &i) {
+        const int kb = w >> 6, r = w & 63;
+        t = 4 * kb + 2 * (r >> 5) + ((r >> 2) & 1);
+        i = 4 * ((r >> 3) & 3) + (r & 3);
+    }
     UQ_HD static LC lane_consts(int lane) { return LC{(lane >> 1) & 1, lane & 1}; }
-    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &c) {
-        const int kb = task >> 2;
-        for (int j = 0; j < 4; j++) {
-            const int dw = kb * 64 + c.h * 32 + j * 8 + c.u * 4;
-            int sum[kPlanes] = {0, 0, 0, 0};
-            for (int q = 0; q < kPlanes; q++)
-                for (int i = 0; i < 4; i++) {
-                    s.X[q][4 * j + i] = P.p[q][dw + i];
-                    sum[q] = sdot4(P.p[q][dw + i], 0x01010101u, sum[q]);
-                }
-            s.Clo[j] = 32 * (sum[1] * 256 + sum[0]);
-            s.Chi[j] = 32 * (sum[3] * 256 + sum[2]);
-            s.s[j] = P.scale[kb * 8 + c.h * 4 + j];
-        }
+    UQ_HD static void load_x(XS &s, const XView &V, int t, const LC &) {
+        load_planes(s.X, V, t);
+        for (int k = 0; k < 8; k++) s.C[k] = V.aux[aux_index(k, t, V.NT)];
+        s.s = V.scale[t >> 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
         return q6k_windows(row + (size_t)(task >> 2) * kBQ6K, c.h, c.u);
@@ -239,14 +270,16 @@ struct Q6K {
                 const uint32_t q = raw6(A, Bq, C, j, i);
                 for (int p = 0; p < kPlanes; p++) D[p] = sdot4(q, s.X[p][4 * j + i], D[p]);
             }
-            // sum((raw-32)*X) = sum(raw*X) - 32*sum(X), per half of the planes
-            const int lo = D[1] * 256 + D[0] - s.Clo[j];
-            const int hi = D[3] * 256 + D[2] - s.Chi[j];
-            const double S = fma((double)hi, 65536.0, (double)lo);
-            // d*sc*s is exact in f32 (<= 19 significant bits)
-            t = fma((double)(d * (float)q6k_scale(E, c.h, c.u, j) * s.s[j]), S, t);
+            const int lo = D[1] * 256 + D[0] - s.C[j];
+            const int hi = D[3] * 256 + D[2] - s.C[4 + j];
+            t = fma((double)q6k_scale(E, c.h, c.u, j), fma((double)hi, 65536.0, (double)lo), t);
         }
-        return t;
+        return (double)(d * s.s) * t;
+    }
+    // aux of one quarter from its plane-digit sums (used by the prep)
+    UQ_HD static void aux_of(const int (&P)[kPlanes], int &lo, int &hi) {
+        lo = 32 * (P[1] * 256 + P[0]);
+        hi = 32 * (P[3] * 256 + P[2]);
     }
 };
 
@@ -256,7 +289,7 @@ struct Q6K {
 struct Q80 {
     struct XS {
         uint32_t X[kPlanes][16];
-        float s0, s1;
+        float s;
     };
     struct Frag {
         u4 w0, w1, w2, w3;
@@ -265,14 +298,16 @@ struct Q80 {
     struct LC {
         int unused;
     };
-    static constexpr int kTasksPerBlock = 0;
+    static constexpr bool kAux = false;
     UQ_HD static int ntasks(int K) { return K >> 6; }
+    UQ_HD static void xmap(int w, int &t, int &i) {
+        t = w >> 4;
+        i = w & 15;
+    }
     UQ_HD static LC lane_consts(int) { return LC{0}; }
-    UQ_HD static void load_x(XS &s, const XPlanesView &P, int task, const LC &) {
-        const int dw = task * 16;
-        for (int q = 0; q < kPlanes; q++) copy_dw(s.X[q], P.p[q] + dw);
-        s.s0 = P.scale[2 * task];
-        s.s1 = P.scale[2 * task + 1];
+    UQ_HD static void load_x(XS &s, const XView &V, int t, const LC &) {
+        load_planes(s.X, V, t);
+        s.s = V.scale[t >> 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &) {
         const uint8_t *B = row + (size_t)task * (2 * kBQ8_0);
@@ -297,8 +332,9 @@ struct Q80 {
             }
         }
         const float d0 = f16_lo(w[0]), d1 = f16_hi(w[8]);
-        const double r = (double)(d0 * s.s0) * plane_sum(a[0], a[1], a[2], a[3]);
-        return fma((double)(d1 * s.s1), plane_sum(b[0], b[1], b[2], b[3]), r);
+        const double r = fma((double)d0, plane_sum(a[0], a[1], a[2], a[3]),
+                             (double)d1 * plane_sum(b[0], b[1], b[2], b[3]));
+        return (double)s.s * r;
     }
 };
 
