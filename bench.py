@@ -135,11 +135,12 @@ def bench_head(hip, steps, warmup):
     W = uq.Weights(w, uq.DType.Q6K, K, N)
     dx, dy = uq.DeviceArray.from_numpy(x), uq.DeviceArray(4 * N)
     nbytes = gemv_bytes(S.Q6_K, K, N)
-    wall, ev = timed(hip, lambda: uq.gemv(W, dx, dy), steps, warmup)
+    s = hip.stream()  # events are recorded on the stream the kernels run on
+    wall, ev = timed(hip, lambda: uq.gemv(W, dx, dy, s), steps, warmup, s)
     res = {"bytes": nbytes, "wall_s": wall, "event_ms": ev, "steps": steps,
            "gbs_wall": nbytes * steps / wall / 1e9, "gbs_event": nbytes * steps / (ev * 1e-3) / 1e9,
            "us_per_call": ev * 1e3 / steps}
-    wall8, ev8 = timed(hip, lambda: uq.gemv_q8k(W, dx, dy), steps, warmup)
+    wall8, ev8 = timed(hip, lambda: uq.gemv_q8k(W, dx, dy, s), steps, warmup, s)
     res["q8k"] = {"us_per_call": ev8 * 1e3 / steps, "gbs_event": nbytes * steps / (ev8 * 1e-3) / 1e9}
     return res, w, x, W
 
@@ -344,12 +345,28 @@ def cpu_baseline(w, x):
 
 
 def load_traffic():
-    p = os.path.join(PROFILES, "q6k_head_gemv_counters.json")
+    """HBM bytes per launch of the head GEMV from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's
+    reading for a device-to-device copy of known size)."""
+    p = os.path.join(PROFILES, "q6k_head_gemv_counters.md")
     try:
         with open(p) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
     except (OSError, ValueError):
-        return None
+        pass
+    return None
+
+
+def copy_calibration(nbytes=1 << 30):
+    """One device-to-device copy of a known size, so a counter run
+    (FETCH_SIZE / WRITE_SIZE) has a reference dispatch to scale by."""
+    a, b = uq.DeviceArray(nbytes), uq.DeviceArray(nbytes)
+    for _ in range(2):
+        uq.lib().uq_memcpy_dtod(b.ptr, a.ptr, nbytes, None)
+    uq.synchronize()
+    log(f"copy calibration: 2 device-to-device copies of {nbytes} bytes")
 
 
 def main():
@@ -360,6 +377,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: head,q4k,ffn,gemm,decode")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run two 1 GiB device copies (reference dispatches for counter runs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path runs on a single "
@@ -367,6 +386,8 @@ def main():
         sys.exit(2)
     hip = Hip()
     log("device:", uq.device_name())
+    if a.copy_calibration:
+        copy_calibration()
     only = set(filter(None, a.only.split(",")))
     head, w, x, W = bench_head(hip, a.steps, a.warmup)
     extra = {"head_q8k_bit_exact": head["q8k"]}
@@ -383,7 +404,7 @@ def main():
     line = {
         "metric": METRIC, "value": head["gbs_wall"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": head["wall_s"] * 1e3 / a.steps, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "i8-dot4+f32",
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8-dot4/f64",
         "data": "synthetic (seeded random GGUF blocks, N(0,1) activations)",
         "config": {"workload": "Q6_K output-projection GEMV 152064x4096 (gemv_quant semantics)",
                    "dim_out": 152064, "dim_in": 4096, "weight_bytes": 510935040,
