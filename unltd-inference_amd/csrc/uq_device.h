@@ -99,6 +99,40 @@ __device__ __forceinline__ double group8_sum_d(double v) {
 }
 
 // ---------------------------------------------------------------------------
+// Transposed reduction of four rows at once. Lane l holds v[r], its partial
+// sum of row r. v_permlane32_swap exchanges the upper 32 lanes of its first
+// operand with the lower 32 lanes of its second, so one swap and one add per
+// pair (v[0], v[2]) leave row 0 summed over lanes l, l+32 in the lower half
+// and row 2 in the upper half; v_permlane16_swap does the same between
+// 16-lane rows. A DPP xor tree over 16 lanes finishes. On return every lane
+// of 16-lane row r (lanes 16r..16r+15) holds the same value
+//     sum over i < 16 of (v_i + v_{i+32}) + (v_{i+16} + v_{i+48})
+// of row r, combined by the xor tree (1, 2, then half-mirror, mirror).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double swap32_add(double a, double b) {
+    const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)__double2loint(a),
+                                                     (unsigned)__double2loint(b), false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)__double2hiint(a),
+                                                     (unsigned)__double2hiint(b), false, false);
+    return __hiloint2double((int)hi[0], (int)lo[0]) + __hiloint2double((int)hi[1], (int)lo[1]);
+}
+__device__ __forceinline__ double swap16_add(double a, double b) {
+    const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)__double2loint(a),
+                                                     (unsigned)__double2loint(b), false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)__double2hiint(a),
+                                                     (unsigned)__double2hiint(b), false, false);
+    return __hiloint2double((int)hi[0], (int)lo[0]) + __hiloint2double((int)hi[1], (int)lo[1]);
+}
+__device__ __forceinline__ double reduce4_rows(const double (&v)[4]) {
+    double z = swap16_add(swap32_add(v[0], v[2]), swap32_add(v[1], v[3]));
+    z += dpp_d<0xB1>(z);   // xor 1
+    z += dpp_d<0x4E>(z);   // xor 2
+    z += dpp_d<0x141>(z);  // row_half_mirror (quads uniform: xor 4)
+    z += dpp_d<0x140>(z);  // row_mirror (halves uniform: xor 8)
+    return z;
+}
+
+// ---------------------------------------------------------------------------
 // Activation prep into the layout of uq_policies.h (XView): one thread per
 // element-dword w (4 activations); a run of 128 activations is one aligned
 // group of 32 lanes. The loop is padded to whole runs so every lane of a run

@@ -95,25 +95,20 @@ HostLayout<F> prep_layout(const float *x, int K) {
     return L;
 }
 
-// wave_sum_d (uq_device.h): the DPP tree, lane 63's value
-double wave_sum64(const double *in) {
-    double v[64], t[64];
-    std::memcpy(v, in, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + v[i ^ 1];
-    std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + v[i ^ 2];
-    std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + v[(i & ~7) | (7 - (i & 7))];
-    std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + v[(i & ~15) | (15 - (i & 15))];
-    std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) {
-        const int row = i >> 4;
-        t[i] = v[i] + ((row == 1 || row == 3) ? v[(row - 1) * 16 + 15] : 0.0);
-    }
-    std::memcpy(v, t, sizeof v);
-    for (int i = 0; i < 64; i++) t[i] = v[i] + ((i >> 4) >= 2 ? v[31] : 0.0);
-    return t[63];
+// reduce4_rows (uq_device.h) for one row: lane pairs (i, i+32), then
+// (i, i+16), then the 16-lane xor tree; every lane of the result row holds
+// the same value, taken here from lane 0.
+double row_sum64(const double *v) {
+    double q[16], t[16];
+    for (int i = 0; i < 16; i++) q[i] = (v[i] + v[i + 32]) + (v[i + 16] + v[i + 48]);
+    for (int i = 0; i < 16; i++) t[i] = q[i] + q[i ^ 1];
+    std::memcpy(q, t, sizeof q);
+    for (int i = 0; i < 16; i++) t[i] = q[i] + q[i ^ 2];
+    std::memcpy(q, t, sizeof q);
+    for (int i = 0; i < 16; i++) t[i] = q[i] + q[(i & ~7) | (7 - (i & 7))];
+    std::memcpy(q, t, sizeof q);
+    for (int i = 0; i < 16; i++) t[i] = q[i] + q[15 - i];
+    return t[0];
 }
 
 template <class F>
@@ -134,7 +129,7 @@ void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int 
             }
             part[lane] = g;
         }
-        y[row] = (float)wave_sum64(part);
+        y[row] = (float)row_sum64(part);
     }
 }
 

@@ -26,10 +26,6 @@ namespace {
 
 constexpr int WAVES = 4;
 constexpr int TPB = 64 * WAVES;
-#ifndef UQ_GEMV_DEPTH
-#define UQ_GEMV_DEPTH 1
-#endif
-constexpr int kDepth = UQ_GEMV_DEPTH;  // rows of weights in flight per wave
 constexpr size_t kLdsCap = 64 * 1024;
 
 int num_cus() {
@@ -74,51 +70,59 @@ __device__ inline float swiglu1(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-#ifdef UQ_GEMV_WAVES_PER_EU
-#define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(UQ_GEMV_WAVES_PER_EU)))
-#else
-#define UQ_GEMV_OCC
-#endif
+// Register budget: the single GEMV kernels that keep x in VGPRs run NW/4
+// waves per SIMD (one workgroup of NW waves per CU), so the allocator is held
+// to 512/(NW/4) VGPRs; the gate/up pair (twice the weight fragments) and the
+// LDS-streaming kernels are left to the allocator.
+#define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(PAIR || !XREG ? 1 : NW / 4)))
 
-// One unit = one task of one row. A wave walks the units of its rows in
-// order (the tasks of row 0, then row 1, ...); a ring of kDepth units keeps
-// that many weight loads in flight, each slot reloaded right after it is
-// consumed (no register copies), and the first kDepth units are issued
-// before the activation prep so their HBM latency overlaps it.
-// XREG (one task per lane) keeps the lane's activation digits in VGPRs;
-// otherwise they are read from LDS for every unit.
+// One unit = one task of one row. A wave owns rows wave, wave + nwave, ...
+// and walks their units in order (the tasks of a row, then the next row); a
+// ring of D units keeps that many weight loads in flight, each slot reloaded
+// right after it is consumed, and the first D units are issued before the
+// activation prep so their HBM latency overlaps it. Rows are taken four at a
+// time: a lane accumulates its four partial sums, then one transposed
+// reduction (reduce4_rows) yields all four row sums.
+// XREG (one task per lane, K <= 4096) keeps the lane's activation digits in
+// VGPRs; otherwise they are read from LDS for every unit (then D == 1).
 // PAIR: W and W2 (gate, up) share x; writes swiglu(W x, W2 x).
-template <class F, bool PAIR, bool XREG>
-__global__ __launch_bounds__(TPB) UQ_GEMV_OCC void gemv_kernel(const uint8_t *__restrict__ W,
+template <class F, bool PAIR, bool XREG, int D, int NW>
+__global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const uint8_t *__restrict__ W,
                                                                const uint8_t *__restrict__ W2,
                                                                size_t row_bytes, int K, int N,
                                                                const float *__restrict__ x,
                                                                float *__restrict__ y) {
+    static_assert(D == 1 || D == 2 || D == 4, "ring depth divides the 4-row batch");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int ntask = F::ntasks(K);
-    const int T = (ntask + 63) >> 6;  // tasks per lane per row
+    const int T = XREG ? 1 : (ntask + 63) >> 6;  // tasks per lane per row
     const typename F::LC c = F::lane_consts(lane);
-    const int wave = blockIdx.x * WAVES + (threadIdx.x >> 6);
-    const int nwave = gridDim.x * WAVES;
-    const int U = (wave < N ? (N - 1 - wave) / nwave + 1 : 0) * T;
+    const int wave = blockIdx.x * NW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int nwave = gridDim.x * NW;
+    const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
+    const int U = nrows * T;  // units of this wave
+    const size_t stride = (size_t)nwave * row_bytes;
 
-    typename F::Frag f[kDepth], f2[kDepth];
-    int pr = 0, pt = 0;  // next unit to load: row index, task iteration
+    typename F::Frag f[D], f2[D];
+    const uint8_t *pw = W + (size_t)wave * row_bytes;    // row of the next unit to load
+    const uint8_t *pw2 = W2 + (size_t)wave * row_bytes;  // (PAIR only)
+    int pt = 0, issued = 0;
     auto issue = [&](typename F::Frag &dst, typename F::Frag &dst2) {
         const int t = lane + 64 * pt;
-        const size_t off = (size_t)(wave + pr * nwave) * row_bytes;
         if (t < ntask) {
-            dst = F::load_w(W + off, t, c);
-            if (PAIR) dst2 = F::load_w(W2 + off, t, c);
+            dst = F::load_w(pw, t, c);
+            if (PAIR) dst2 = F::load_w(pw2, t, c);
         }
         if (++pt == T) {
             pt = 0;
-            ++pr;
+            pw += stride;
+            if (PAIR) pw2 += stride;
         }
+        ++issued;
     };
 #pragma unroll
-    for (int d = 0; d < kDepth; d++)
+    for (int d = 0; d < D; d++)
         if (d < U) issue(f[d], f2[d]);
 
     const XLayout L = x_layout_at<F>(lds, K);
@@ -129,39 +133,41 @@ __global__ __launch_bounds__(TPB) UQ_GEMV_OCC void gemv_kernel(const uint8_t *__
     typename F::XS xr;
     if (XREG && lane < ntask) F::load_x(xr, PV, lane, c);
 
-    double g = 0.0, u = 0.0;
-    int cr = 0, ct = 0;  // unit being consumed
-    for (int u0 = 0; u0 < U; u0 += kDepth) {
+    for (int rb = 0; rb < nrows; rb += 4) {
+        double g[4], u[4];
 #pragma unroll
-        for (int d = 0; d < kDepth; d++) {
-            if (u0 + d >= U) break;  // wave-uniform
-            const int t = lane + 64 * ct;
-            if (t < ntask) {
-                if (XREG) {
-                    g += F::dot(f[d], xr, c);
-                    if (PAIR) u += F::dot(f2[d], xr, c);
-                } else {
-                    typename F::XS xs;
-                    F::load_x(xs, PV, t, c);
-                    g += F::dot(f[d], xs, c);
-                    if (PAIR) u += F::dot(f2[d], xs, c);
+        for (int r = 0; r < 4; r++) {
+            g[r] = 0.0;
+            u[r] = 0.0;
+            if (rb + r >= nrows) continue;  // wave-uniform
+            if (XREG) {
+                // one unit per row; its slot is the row's place in the ring
+                typename F::Frag &cur = f[r % D], &cur2 = f2[r % D];
+                if (lane < ntask) {
+                    g[r] = F::dot(cur, xr, c);
+                    if (PAIR) u[r] = F::dot(cur2, xr, c);
+                }
+                if (issued < U) issue(cur, cur2);
+            } else {
+                for (int tt = 0; tt < T; tt++) {
+                    const int t = lane + 64 * tt;
+                    if (t < ntask) {
+                        typename F::XS xs;
+                        F::load_x(xs, PV, t, c);
+                        g[r] += F::dot(f[0], xs, c);
+                        if (PAIR) u[r] += F::dot(f2[0], xs, c);
+                    }
+                    if (issued < U) issue(f[0], f2[0]);
                 }
             }
-            if (u0 + d + kDepth < U) issue(f[d], f2[d]);
-            if (++ct == T) {
-                const int row = wave + cr * nwave;
-                g = wave_sum_d(g);
-                if (PAIR) {
-                    u = wave_sum_d(u);
-                    if (lane == 0) y[row] = swiglu1((float)g, (float)u);
-                } else if (lane == 0) {
-                    y[row] = (float)g;
-                }
-                g = 0.0;
-                u = 0.0;
-                ct = 0;
-                ++cr;
-            }
+        }
+        const double G = reduce4_rows(g);
+        double Uu = 0.0;
+        if (PAIR) Uu = reduce4_rows(u);
+        const int r = lane >> 4;
+        if ((lane & 15) == 0 && rb + r < nrows) {
+            const int row = wave + (rb + r) * nwave;
+            y[row] = PAIR ? swiglu1((float)G, (float)Uu) : (float)G;
         }
     }
 }
@@ -228,46 +234,50 @@ __global__ __launch_bounds__(TPB) void gemv_generic_kernel(uq_dtype dt, const ui
 // Workgroups for a row-walking kernel: exactly the number that are resident
 // at once (occupancy from VGPRs/LDS), so no workgroup waits for a second
 // round, then trimmed so every wave walks the same number of rows.
-int blocks_per_cu(const void *kernel, size_t lds) {
+int blocks_per_cu(const void *kernel, size_t lds, int tpb) {
     static std::mutex mu;
     static std::map<std::pair<const void *, size_t>, int> cache;
     std::lock_guard<std::mutex> g(mu);
     auto it = cache.find({kernel, lds});
     if (it != cache.end()) return it->second;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, TPB, lds) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, tpb, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     cache[{kernel, lds}] = per_cu;
     return per_cu;
 }
 
-int resident_grid(const void *kernel, size_t lds, int N) {
-    int per_cu = blocks_per_cu(kernel, lds);
+int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
+    int per_cu = blocks_per_cu(kernel, lds, 64 * nw);
 #ifdef UQ_WG_PER_CU
     per_cu = UQ_WG_PER_CU;
 #endif
-    const int max_waves = num_cus() * per_cu * WAVES;
+    const int max_waves = num_cus() * per_cu * nw;
     const int rows_per_wave = (N + max_waves - 1) / max_waves;
     const int waves = (N + rows_per_wave - 1) / rows_per_wave;
-    return (waves + WAVES - 1) / WAVES;
+    return (waves + nw - 1) / nw;
 }
 
-#ifndef UQ_GEMV_XREG
-#define UQ_GEMV_XREG 1
-#endif
+// Launch shape of the x-in-VGPR kernels, per format: one workgroup per CU
+// (NW waves) so the activation prep runs once per CU, with D units in flight
+// per wave. Q6_K: 12 waves (3 per SIMD, <= 168 VGPRs) with two units in
+// flight; Q4_K and Q8_0: 16 waves (4 per SIMD, <= 128 VGPRs), one unit.
+template <class F> struct Shape { static constexpr int NW = 16, D = 1; };
+template <> struct Shape<Q6K> { static constexpr int NW = 12, D = 2; };
 
 template <class F, bool PAIR>
 hipError_t launch_fast(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
     const size_t lds = x_lds_bytes<F>(K);
-    if (UQ_GEMV_XREG && F::ntasks(K) <= 64) {
-        const void *k = (const void *)gemv_kernel<F, PAIR, true>;
-        hipLaunchKernelGGL((gemv_kernel<F, PAIR, true>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds, s,
-                           w.bytes, w2, w.row_bytes, K, N, x, y);
+    if (F::ntasks(K) <= 64) {
+        constexpr int NW = PAIR ? WAVES : Shape<F>::NW, D = PAIR ? 1 : Shape<F>::D;
+        const void *k = (const void *)gemv_kernel<F, PAIR, true, D, NW>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW>), dim3(resident_grid(k, lds, N, NW)),
+                           dim3(64 * NW), lds, s, w.bytes, w2, w.row_bytes, K, N, x, y);
     } else {
-        const void *k = (const void *)gemv_kernel<F, PAIR, false>;
-        hipLaunchKernelGGL((gemv_kernel<F, PAIR, false>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds, s,
-                           w.bytes, w2, w.row_bytes, K, N, x, y);
+        const void *k = (const void *)gemv_kernel<F, PAIR, false, 1, WAVES>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, false, 1, WAVES>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds,
+                           s, w.bytes, w2, w.row_bytes, K, N, x, y);
     }
     return hipGetLastError();
 }

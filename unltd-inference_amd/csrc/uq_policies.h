@@ -40,7 +40,7 @@ constexpr int kBQ4K = 144, kBQ6K = 210, kBQ8_0 = 34;
 //    ds_read_b128 without bank conflicts.
 //  * A task covers exactly half a run: its scale is scale[t/2].
 //  * gsum[g] = s * sum(X) over each 32-element group g (Q4_K mins), exact.
-//  * aux: per task 8 ints stored the same way (Q6_K: 32 * the digit sums of
+//  * aux: per task 8 ints stored the same way (Q6_K: -32 * the digit sums of
 //    each quarter, see Q6K).
 constexpr int kPlanes = 4;
 constexpr int kRunLen = 128;
@@ -74,12 +74,10 @@ UQ_HD void load_planes(uint32_t (&X)[kPlanes][16], const XView &V, int t) {
         }
 }
 
-// sum(q*X) of a group from its four exact plane dots, as an exact double:
-// (D3*256 + D2)*65536 + (D1*256 + D0); both halves fit int32 for <= 32
-// elements of |q| <= 128 (|D| <= 2^19), the result fits 53 bits.
-UQ_HD double plane_sum(int d0, int d1, int d2, int d3) {
-    return fma((double)(d3 * 256 + d2), 65536.0, (double)(d1 * 256 + d0));
-}
+// A group's sum(q*X) is formed from its four plane dots Dq as the exact
+// double (D3*256 + D2)*65536 + (D1*256 + D0). Each bracket is one int32
+// accumulator chain (dots of plane 3, times 256, dots of plane 2), which fits
+// for <= 32 elements of |q| <= 128 (|Dq| <= 2^19); the result fits 53 bits.
 
 // ============================ Q4_K ==========================================
 // Task t: block kb = t/4, group pair p = t%4 = lane%4: qs bytes [32p, 32p+32).
@@ -147,28 +145,44 @@ struct Q4K {
         s.gs1 = V.gsum[2 * t + 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
-        const uint8_t *B = row + (size_t)(task >> 2) * kBQ4K;
+        const uint32_t ob = (uint32_t)(task >> 2) * (uint32_t)kBQ4K, oq = ob + (uint32_t)(16 + 32 * c.p);
         Frag f;
-        f.h = ld4(B);
-        f.qa = ld4(B + 16 + 32 * c.p);
-        f.qb = ld4(B + 32 + 32 * c.p);
+        f.h = ldu4(row + ob);
+        f.qa = ldu4(row + oq);
+        f.qb = ldu4(row + oq + 16);
         return f;
     }
     UQ_HD static double dot(const Frag &f, const XS &s, const LC &c) {
         const uint32_t Q[8] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w, f.qb.x, f.qb.y, f.qb.z, f.qb.w};
-        int a[kPlanes] = {0, 0, 0, 0}, b[kPlanes] = {0, 0, 0, 0};
+        uint32_t lo[8], hi[8];
         for (int i = 0; i < 8; i++) {
-            const uint32_t lo = Q[i] & 0x0F0F0F0Fu, hi = (Q[i] >> 4) & 0x0F0F0F0Fu;
-            for (int q = 0; q < kPlanes; q++) {
-                a[q] = sdot4(lo, s.X[q][i], a[q]);
-                b[q] = sdot4(hi, s.X[q][8 + i], b[q]);
-            }
+            lo[i] = Q[i] & 0x0F0F0F0Fu;
+            hi[i] = (Q[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        // Per group the two halves D3*256 + D2 and D1*256 + D0 of the plane
+        // dots, each one accumulator chain shifted by 8 bits between planes.
+        int ah = 0, al = 0, bh = 0, bl = 0;
+        for (int i = 0; i < 8; i++) {
+            ah = sdot4(lo[i], s.X[3][i], ah);
+            al = sdot4(lo[i], s.X[1][i], al);
+            bh = sdot4(hi[i], s.X[3][8 + i], bh);
+            bl = sdot4(hi[i], s.X[1][8 + i], bl);
+        }
+        ah *= 256;
+        al *= 256;
+        bh *= 256;
+        bl *= 256;
+        for (int i = 0; i < 8; i++) {
+            ah = sdot4(lo[i], s.X[2][i], ah);
+            al = sdot4(lo[i], s.X[0][i], al);
+            bh = sdot4(hi[i], s.X[2][8 + i], bh);
+            bl = sdot4(hi[i], s.X[0][8 + i], bl);
         }
         uint32_t sc0, sc1, m0, m1;
         scales(f.h, c, sc0, sc1, m0, m1);
         const float d = f16_lo(f.h.x), dmin = f16_hi(f.h.x);
-        const double main = fma((double)(int)sc0, plane_sum(a[0], a[1], a[2], a[3]),
-                                (double)(int)sc1 * plane_sum(b[0], b[1], b[2], b[3]));
+        const double main = fma((double)(int)sc0, fma((double)ah, 65536.0, (double)al),
+                                (double)(int)sc1 * fma((double)bh, 65536.0, (double)bl));
         const double mins = fma((double)(int)m0, s.gs0, (double)(int)m1 * s.gs1);
         // d*s is exact in f32 (a power-of-two scaling of d)
         return fma((double)(d * s.s), main, -(double)dmin * mins);
@@ -183,52 +197,44 @@ struct Q4K {
 //   high 2 bits: bits 2j..2j+1 of qh byte 32h + 16u + l
 //   scale: int8 at 192 + 8h + 2j + u; d: f16 at 208 (quants.rs:185-195).
 // Task dword 4j + i' holds elements 256kb + 128h + 32j + 16u + 4i'.
-// Blocks are 2-byte aligned, so every 16-byte field is loaded as a
-// dword-aligned 20-byte window and realigned with v_alignbyte.
-struct Q6KWindows {
-    u4 a, b, c, e;
-    uint32_t a4, b4, c4, e4, sh;
+// Blocks are 2-byte aligned; the loads are unaligned 128-bit / 32-bit loads.
+struct Q6KFrag {
+    u4 a, b, c;      // ql[64h+16u, +16), ql[64h+32+16u, +16), qh[32h+16u, +16)
+    uint32_t s0, s1; // scale bytes 192+8h+u + {0, 2} and + {4, 6}
+    uint32_t dw;     // f16 d in the low half
 };
-UQ_HD Q6KWindows q6k_windows(const uint8_t *B, int h, int u) {
-    Q6KWindows f;
-    f.sh = (uint32_t)((uintptr_t)B & 3);
-    const uint8_t *B4 = B - f.sh;
-    const int oa = 64 * h + 16 * u, oc = 128 + 32 * h + 16 * u;
-    f.a = ld4(B4 + oa);
-    f.a4 = ld1(B4 + oa + 16);
-    f.b = ld4(B4 + oa + 32);
-    f.b4 = ld1(B4 + oa + 48);
-    f.c = ld4(B4 + oc);
-    f.c4 = ld1(B4 + oc + 16);
-    f.e = ld4(B4 + 192);  // scales (+ d in e4); may read 2 bytes past the
-    f.e4 = ld1(B4 + 208); // block: device copies carry tail padding
+// Block at row + ob. Addresses are a row pointer plus 32-bit lane offsets so
+// the device loads take the scalar-base + vector-offset form.
+UQ_HD Q6KFrag q6k_load(const uint8_t *row, uint32_t ob, int h, int u) {
+    const uint32_t oa = ob + (uint32_t)(64 * h + 16 * u), oc = ob + (uint32_t)(128 + 32 * h + 16 * u),
+                   os = ob + (uint32_t)(192 + 8 * h + u);
+    Q6KFrag f;
+    f.a = ldu4(row + oa);
+    f.b = ldu4(row + oa + 32);
+    f.c = ldu4(row + oc);
+    f.s0 = ldu1(row + os);
+    f.s1 = ldu1(row + os + 4);
+    f.dw = ldu1(row + ob + 208);  // reads 2 bytes past the block: device copies carry tail padding
     return f;
 }
-UQ_HD void align4(uint32_t (&o)[4], const u4 &v, uint32_t v4, uint32_t sh) {
-    o[0] = alignbyte(v.y, v.x, sh);
-    o[1] = alignbyte(v.z, v.y, sh);
-    o[2] = alignbyte(v.w, v.z, sh);
-    o[3] = alignbyte(v4, v.w, sh);
-}
-// int8 scale of quarter j for lane half u: byte 8h + 2j + u of the scales,
-// i.e. dword 2h + j/2 (E[0..3] are the realigned scale dwords), byte 2(j%2)+u
-UQ_HD int q6k_scale(const uint32_t (&E)[4], int h, int u, int j) {
-    const uint32_t w = E[2 * h + (j >> 1)];
-    return sbfe((int)w, 8 * (2 * (j & 1) + u), 8);
+// int8 scale of quarter j
+UQ_HD int q6k_scale(const Q6KFrag &f, int j) {
+    return sbfe((int)(j < 2 ? f.s0 : f.s1), 16 * (j & 1), 8);
 }
 
 // Row contribution: d*s * sum_j sc_j * sum((raw-32)*X) over each quarter,
 // the reference's w = d*(sc*q) with q = raw-32 (quants.rs:193-195).
-// aux holds, per task and quarter j, C[j] = 32*(P1*256 + P0) and
-// C[4+j] = 32*(P3*256 + P2) where Pq is the sum of plane q's digits over the
-// quarter, so sum((raw-32)*X) = (D3*256+D2 - C[4+j])*65536 + (D1*256+D0 - C[j]).
+// aux holds, per task and quarter j, C[j] = -32*(P1*256 + P0) and
+// C[4+j] = -32*(P3*256 + P2) where Pq is the sum of plane q's digits over the
+// quarter, so sum((raw-32)*X) = ((D3*256 + C[4+j]) + D2)*65536 + (D1*256 + C[j]) + D0
+// with every bracket an exact int32 chain.
 struct Q6K {
     struct XS {
         uint32_t X[kPlanes][16];
         int C[8];
         float s;
     };
-    typedef Q6KWindows Frag;
+    typedef Q6KFrag Frag;
     struct LC {
         int h, u;
     };
@@ -246,40 +252,41 @@ struct Q6K {
         s.s = V.scale[t >> 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) {
-        return q6k_windows(row + (size_t)(task >> 2) * kBQ6K, c.h, c.u);
+        return q6k_load(row, (uint32_t)(task >> 2) * (uint32_t)kBQ6K, c.h, c.u);
     }
     // raw 6-bit quants of quarter j (0..63 per byte)
-    UQ_HD static uint32_t raw6(const uint32_t (&A)[4], const uint32_t (&Bq)[4], const uint32_t (&C)[4],
-                               int j, int i) {
-        if (j == 0) return (A[i] & 0x0F0F0F0Fu) | ((C[i] << 4) & 0x30303030u);
-        if (j == 1) return (Bq[i] & 0x0F0F0F0Fu) | ((C[i] << 2) & 0x30303030u);
-        if (j == 2) return ((A[i] >> 4) & 0x0F0F0F0Fu) | (C[i] & 0x30303030u);
-        return ((Bq[i] >> 4) & 0x0F0F0F0Fu) | ((C[i] >> 2) & 0x30303030u);
+    UQ_HD static uint32_t raw6(const Frag &f, int j, int i) {
+        const uint32_t A = (&f.a.x)[i], Bq = (&f.b.x)[i], C = (&f.c.x)[i];
+        if (j == 0) return (A & 0x0F0F0F0Fu) | ((C << 4) & 0x30303030u);
+        if (j == 1) return (Bq & 0x0F0F0F0Fu) | ((C << 2) & 0x30303030u);
+        if (j == 2) return ((A >> 4) & 0x0F0F0F0Fu) | (C & 0x30303030u);
+        return ((Bq >> 4) & 0x0F0F0F0Fu) | ((C >> 2) & 0x30303030u);
     }
-    UQ_HD static double dot(const Frag &f, const XS &s, const LC &c) {
-        uint32_t A[4], Bq[4], C[4], E[4];
-        align4(A, f.a, f.a4, f.sh);
-        align4(Bq, f.b, f.b4, f.sh);
-        align4(C, f.c, f.c4, f.sh);
-        align4(E, f.e, f.e4, f.sh);
-        const float d = f16_lo(f.e4 >> (8 * f.sh));
+    UQ_HD static double dot(const Frag &f, const XS &s, const LC &) {
+        const float d = f16_lo(f.dw);
         double t = 0.0;
         for (int j = 0; j < 4; j++) {
-            int D[kPlanes] = {0, 0, 0, 0};
+            uint32_t q[4];
+            for (int i = 0; i < 4; i++) q[i] = raw6(f, j, i);
+            int hi = 0, lo = 0;
             for (int i = 0; i < 4; i++) {
-                const uint32_t q = raw6(A, Bq, C, j, i);
-                for (int p = 0; p < kPlanes; p++) D[p] = sdot4(q, s.X[p][4 * j + i], D[p]);
+                hi = sdot4(q[i], s.X[3][4 * j + i], hi);
+                lo = sdot4(q[i], s.X[1][4 * j + i], lo);
             }
-            const int lo = D[1] * 256 + D[0] - s.C[j];
-            const int hi = D[3] * 256 + D[2] - s.C[4 + j];
-            t = fma((double)q6k_scale(E, c.h, c.u, j), fma((double)hi, 65536.0, (double)lo), t);
+            hi = hi * 256 + s.C[4 + j];
+            lo = lo * 256 + s.C[j];
+            for (int i = 0; i < 4; i++) {
+                hi = sdot4(q[i], s.X[2][4 * j + i], hi);
+                lo = sdot4(q[i], s.X[0][4 * j + i], lo);
+            }
+            t = fma((double)q6k_scale(f, j), fma((double)hi, 65536.0, (double)lo), t);
         }
         return (double)(d * s.s) * t;
     }
     // aux of one quarter from its plane-digit sums (used by the prep)
     UQ_HD static void aux_of(const int (&P)[kPlanes], int &lo, int &hi) {
-        lo = 32 * (P[1] * 256 + P[0]);
-        hi = 32 * (P[3] * 256 + P[2]);
+        lo = -32 * (P[1] * 256 + P[0]);
+        hi = -32 * (P[3] * 256 + P[2]);
     }
 };
 
@@ -292,8 +299,8 @@ struct Q80 {
         float s;
     };
     struct Frag {
-        u4 w0, w1, w2, w3;
-        uint32_t w4;
+        uint32_t h0, h1;  // f16 d0 in the low half of dword 0; d1 in the high half of dword 8
+        u4 a0, a1, b0, b1; // q0 = bytes 2..33, q1 = bytes 36..67 (unaligned loads)
     };
     struct LC {
         int unused;
@@ -310,30 +317,39 @@ struct Q80 {
         s.s = V.scale[t >> 1];
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &) {
-        const uint8_t *B = row + (size_t)task * (2 * kBQ8_0);
+        const uint8_t *B = row + (uint32_t)task * (uint32_t)(2 * kBQ8_0);
         Frag f;
-        f.w0 = ld4(B);
-        f.w1 = ld4(B + 16);
-        f.w2 = ld4(B + 32);
-        f.w3 = ld4(B + 48);
-        f.w4 = ld1(B + 64);
+        f.h0 = ldu1(B);
+        f.a0 = ldu4(B + 2);
+        f.a1 = ldu4(B + 18);
+        f.h1 = ldu1(B + 32);
+        f.b0 = ldu4(B + 36);
+        f.b1 = ldu4(B + 52);
         return f;
     }
     UQ_HD static double dot(const Frag &f, const XS &s, const LC &) {
-        const uint32_t w[17] = {f.w0.x, f.w0.y, f.w0.z, f.w0.w, f.w1.x, f.w1.y, f.w1.z, f.w1.w,
-                                f.w2.x, f.w2.y, f.w2.z, f.w2.w, f.w3.x, f.w3.y, f.w3.z, f.w3.w, f.w4};
-        int a[kPlanes] = {0, 0, 0, 0}, b[kPlanes] = {0, 0, 0, 0};
+        const uint32_t q0[8] = {f.a0.x, f.a0.y, f.a0.z, f.a0.w, f.a1.x, f.a1.y, f.a1.z, f.a1.w};
+        const uint32_t q1[8] = {f.b0.x, f.b0.y, f.b0.z, f.b0.w, f.b1.x, f.b1.y, f.b1.z, f.b1.w};
+        int ah = 0, al = 0, bh = 0, bl = 0;
         for (int i = 0; i < 8; i++) {
-            const uint32_t q0 = alignbyte(w[i + 1], w[i], 2);  // bytes 2..33
-            const uint32_t q1 = w[9 + i];                       // bytes 36..67
-            for (int q = 0; q < kPlanes; q++) {
-                a[q] = sdot4(q0, s.X[q][i], a[q]);
-                b[q] = sdot4(q1, s.X[q][8 + i], b[q]);
-            }
+            ah = sdot4(q0[i], s.X[3][i], ah);
+            al = sdot4(q0[i], s.X[1][i], al);
+            bh = sdot4(q1[i], s.X[3][8 + i], bh);
+            bl = sdot4(q1[i], s.X[1][8 + i], bl);
         }
-        const float d0 = f16_lo(w[0]), d1 = f16_hi(w[8]);
-        const double r = fma((double)d0, plane_sum(a[0], a[1], a[2], a[3]),
-                             (double)d1 * plane_sum(b[0], b[1], b[2], b[3]));
+        ah *= 256;
+        al *= 256;
+        bh *= 256;
+        bl *= 256;
+        for (int i = 0; i < 8; i++) {
+            ah = sdot4(q0[i], s.X[2][i], ah);
+            al = sdot4(q0[i], s.X[0][i], al);
+            bh = sdot4(q1[i], s.X[2][8 + i], bh);
+            bl = sdot4(q1[i], s.X[0][8 + i], bl);
+        }
+        const float d0 = f16_lo(f.h0), d1 = f16_hi(f.h1);
+        const double r = fma((double)d0, fma((double)ah, 65536.0, (double)al),
+                             (double)d1 * fma((double)bh, 65536.0, (double)bl));
         return (double)s.s * r;
     }
 };
@@ -419,13 +435,13 @@ struct Q6KQ8 {
     struct XS {
         uint32_t X[32];
     };
-    typedef Q6KWindows Frag;
+    typedef Q6KFrag Frag;
     typedef Q6K::LC LC;
     static constexpr int kTasksPerBlock = 4;
     static constexpr int kDw = kQ6Q8Dw;
     static constexpr bool kMin = false;
     // f16 d bits of the block
-    UQ_HD static uint32_t hdr(const Frag &f) { return (f.e4 >> (8 * f.sh)) & 0xFFFFu; }
+    UQ_HD static uint32_t hdr(const Frag &f) { return f.dw & 0xFFFFu; }
     UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
     UQ_HD static LC lane_consts(int lane) { return Q6K::lane_consts(lane); }
     UQ_HD static void load_x(XS &s, const uint32_t *xq, int task) {
@@ -433,28 +449,23 @@ struct Q6KQ8 {
     }
     UQ_HD static Frag load_w(const uint8_t *row, int task, const LC &c) { return Q6K::load_w(row, task, c); }
     // 4*(raw-32) as signed bytes: raw placed in bits 2..7, top bit flipped
-    UQ_HD static uint32_t sq6(const uint32_t (&A)[4], const uint32_t (&Bq)[4], const uint32_t (&C)[4],
-                              int j, int i) {
+    UQ_HD static uint32_t sq6(const Frag &f, int j, int i) {
+        const uint32_t A = (&f.a.x)[i], Bq = (&f.b.x)[i], C = (&f.c.x)[i];
         uint32_t lo4, hi2;
-        if (j == 0) { lo4 = A[i] << 2; hi2 = C[i] << 6; }
-        else if (j == 1) { lo4 = Bq[i] << 2; hi2 = C[i] << 4; }
-        else if (j == 2) { lo4 = A[i] >> 2; hi2 = C[i] << 2; }
-        else { lo4 = Bq[i] >> 2; hi2 = C[i]; }
+        if (j == 0) { lo4 = A << 2; hi2 = C << 6; }
+        else if (j == 1) { lo4 = Bq << 2; hi2 = C << 4; }
+        else if (j == 2) { lo4 = A >> 2; hi2 = C << 2; }
+        else { lo4 = Bq >> 2; hi2 = C; }
         return ((lo4 & 0x3C3C3C3Cu) | (hi2 & 0xC0C0C0C0u)) ^ 0x80808080u;
     }
-    UQ_HD static void dot(const Frag &f, const XS &s, const LC &c, int (&S)[8], int &M) {
-        uint32_t A[4], Bq[4], C[4], E[4];
-        align4(A, f.a, f.a4, f.sh);
-        align4(Bq, f.b, f.b4, f.sh);
-        align4(C, f.c, f.c4, f.sh);
-        align4(E, f.e, f.e4, f.sh);
+    UQ_HD static void dot(const Frag &f, const XS &s, const LC &, int (&S)[8], int &M) {
         for (int k = 0; k < 8; k++) S[k] = 0;
         for (int j = 0; j < 4; j++) {
-            const uint32_t q0 = sq6(A, Bq, C, j, 0), q1 = sq6(A, Bq, C, j, 1);
-            const uint32_t q2 = sq6(A, Bq, C, j, 2), q3 = sq6(A, Bq, C, j, 3);
+            const uint32_t q0 = sq6(f, j, 0), q1 = sq6(f, j, 1);
+            const uint32_t q2 = sq6(f, j, 2), q3 = sq6(f, j, 3);
             uint32_t T[4];
             transpose4(q0, q2, q1, q3, T);  // T[b] = {l=b, l=8+b, l=4+b, l=12+b}
-            const int sc = q6k_scale(E, c.h, c.u, j);
+            const int sc = q6k_scale(f, j);
             for (int b = 0; b < 4; b++) {
                 S[b] += sc * sdot4(T[b], s.X[8 * j + 2 * b], 0);
                 S[4 + b] += sc * sdot4(T[b], s.X[8 * j + 2 * b + 1], 0);
