@@ -18,8 +18,8 @@
  *    calling thread).
  *  - Device entry points take device pointers and a hipStream_t (void*; NULL
  *    = the null stream). They are asynchronous on that stream and allocate
- *    no device memory. Weights live behind a uq_weights handle whose bytes
- *    are copied to HBM unchanged.
+ *    no device memory, except uq_gemm (see there). Weights live behind a
+ *    uq_weights handle whose bytes are copied to HBM unchanged.
  *  - Numerics: uq_gemv_quant / uq_gemv / uq_gemm / uq_ffn_swiglu follow
  *    gemv_quant's semantics (f32 result of the exact dequantized weights times
  *    f32 x; matched within |y-r| <= 1e-4 + 1e-3*|r|). uq_gemv_quant_q8k /
@@ -138,7 +138,11 @@ uq_status uq_gemv_q8k(uq_weights w, const float *d_x, float *d_y, void *stream);
 
 /* Batched prefill: d_y[m][dim_out] = W . d_x[m][dim_in] for m < m_rows, with
  * gemv_quant semantics per row (the reference feeds prefill tokens one at a
- * time, greedy.rs:55-65; each row equals gemv_quant of that token). */
+ * time, greedy.rs:55-65; each row equals gemv_quant of that token).
+ * Q4_K with m_rows >= 16 and dim_out % 256 == 0 runs on the f16 MFMA and
+ * uses a library-owned device workspace of about 4*m_rows*dim_in bytes per
+ * (device, stream), allocated on first use and grown when a call needs more
+ * (growing synchronizes the stream). Other shapes run as m_rows GEMVs. */
 uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                   void *stream);
 

@@ -291,6 +291,57 @@ def test_device_api_gemm_rows_equal_gemv_quant(dtype, M):
         assert_close(Y[m], ref, what=f"gemm row {m}")
 
 
+def _gemm_check(K, N, M, X, seed, what):
+    w = S.weights(S.Q4_K, N, K, seed=seed)
+    W = uq.Weights(w, uq.DType.Q4K, K, N)
+    dx, dy = uq.DeviceArray.from_numpy(np.ascontiguousarray(X, np.float32)), uq.DeviceArray(4 * M * N)
+    uq.gemm(W, M, dx, dy)
+    Y = dy.download(np.float32, M * N).reshape(M, N)
+    worst = 0.0
+    for m in range(M):
+        ref = np.zeros(N, np.float32)
+        O.gemv_quant(ref, X[m], w, K, N, S.Q4_K, nthreads=NT)
+        err = np.abs(Y[m].astype(np.float64) - ref)
+        worst = max(worst, float(np.max(err / (1e-4 + 1e-3 * np.abs(ref.astype(np.float64))))))
+        assert_close(Y[m], ref, what=f"{what} row {m}")
+    return worst
+
+
+@pytest.mark.parametrize("K,N,M", [(4096, 256, 130), (768, 512, 40), (4096, 256, 16), (256, 768, 257),
+                                   (512, 384, 20)])
+def test_gemm_mfma_q4k_rows_equal_gemv_quant(K, N, M):
+    """The MFMA prefill path (Q4_K, M >= 16, N % 256 == 0; N = 384 takes the
+    GEMV path): masked M tails, K not a multiple of 1024, several N tiles;
+    every row within the gemv_quant tolerance."""
+    X = S.activations(K, seed=K + M, rows=M).reshape(M, K)
+    worst = _gemm_check(K, N, M, X, seed=N + M, what=f"gemm {M}x{N}x{K}")
+    print(f"worst err/tol {worst:.3g}")
+
+
+def test_gemm_mfma_q4k_dynamic_range():
+    """Rows of very different magnitude (1e-4 .. 1e4) and rows whose elements
+    span many binades: the per-row power-of-two scale and the f16 hi/lo
+    split keep every row within tolerance."""
+    K, N, M = 1024, 256, 16
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    X *= (10.0 ** rng.uniform(-4, 4, size=(M, 1))).astype(np.float32)
+    X[::3] *= (10.0 ** rng.uniform(-6, 0, size=(len(X[::3]), K))).astype(np.float32)
+    X[5] = 0.0
+    X[7, :] = 0.0
+    X[7, 100] = 3.0e4
+    _gemm_check(K, N, M, X, seed=99, what="gemm dynamic range")
+
+
+def test_gemm_mfma_workspace_regrows_between_calls():
+    """Two calls on one stream, the second with a larger M (the workspace
+    grows), then a smaller one again."""
+    K, N = 512, 256
+    for M, seed in ((8, 1), (200, 2), (5, 3)):
+        X = S.activations(K, seed=seed, rows=M).reshape(M, K)
+        _gemm_check(K, N, M, X, seed=seed, what=f"gemm M={M}")
+
+
 def test_device_dequantize_handle():
     K, N = 4096, 256
     w = S.weights(S.Q4_K, N, K, seed=5)
