@@ -133,6 +133,17 @@ uq_status uq_weights_info(uq_weights w, uq_dtype *dtype, size_t *dim_in,
 /* d_y[dim_out] = W . d_x[dim_in] with gemv_quant semantics (quants.rs:422-466). */
 uq_status uq_gemv(uq_weights w, const float *d_x, float *d_y, void *stream);
 
+/* Several projections of one activation vector in one launch:
+ * d_y[i] = W[i] . d_x for i < count (count <= UQ_GEMV_BATCH_MAX), e.g. the
+ * q, k and v projections of a token. All W[i] share dtype and dim_in.
+ * gemv_quant semantics; every d_y[i] equals what uq_gemv(W[i]) writes, bit
+ * for bit. No reference counterpart (the reference calls gemv_quant_q8k once
+ * per projection, qwen35_forward.rs:365-401); it saves the per-launch
+ * activation preparation of the small projections. */
+#define UQ_GEMV_BATCH_MAX 8
+uq_status uq_gemv_batch(const uq_weights *w, float *const *d_y, size_t count,
+                        const float *d_x, void *stream);
+
 /* d_y = gemv_quant_q8k(W, d_x) (quants.rs:474-515), bit-exact. */
 uq_status uq_gemv_q8k(uq_weights w, const float *d_x, float *d_y, void *stream);
 

@@ -4,6 +4,8 @@ touching a device, and fails loudly (no CPU fallback) when no GPU exists."""
 import os
 import re
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -83,3 +85,17 @@ def test_compute_fails_loudly_without_gpu():
     w = np.zeros(144, np.uint8)
     _raises("NO_DEVICE", uq.gemv_quant, np.zeros(1, np.float32), x, w, 256, 1, uq.DType.Q4K)
     _raises("NO_DEVICE", uq.Weights, w, uq.DType.Q4K, 256, 1)
+
+
+def test_gemv_batch_argument_errors():
+    """uq_gemv_batch validates before touching a device: null tables, count
+    above UQ_GEMV_BATCH_MAX, invalid handles."""
+    L = uq.lib()
+    P = C.c_void_p
+    hs = (P * 9)()
+    ys = (P * 9)()
+    assert uq.STATUS[L.uq_gemv_batch(None, ys, 1, None, None)] == "ARG"
+    assert uq.STATUS[L.uq_gemv_batch(hs, None, 1, None, None)] == "ARG"
+    assert L.uq_gemv_batch(hs, ys, 0, None, None) == 0  # nothing to do
+    assert uq.STATUS[L.uq_gemv_batch(hs, ys, 9, None, None)] == "ARG"
+    assert uq.STATUS[L.uq_gemv_batch(hs, ys, 2, None, None)] == "ARG"  # null handles

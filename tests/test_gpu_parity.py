@@ -364,3 +364,39 @@ def test_device_api_errors():
     with pytest.raises(uq.UqError) as e:
         uq.Weights(w[:-1], uq.DType.Q8_0, 64, 4)
     assert e.value.kind == "LEN"
+
+
+@pytest.mark.parametrize("dtype,K,ns", [(S.Q4_K, 4096, (8192, 4096, 32, 32)), (S.Q6_K, 4096, (8192, 1024, 1024)),
+                                        (S.Q4_K, 12288, (4096, 7)), (S.Q8_0, 4096, (100, 4096))])
+def test_gemv_batch_equals_separate_gemvs(dtype, K, ns):
+    """uq_gemv_batch: one launch over several weight tensors sharing x writes
+    exactly what separate uq_gemv calls write (same per-row arithmetic), and
+    each is within the gemv_quant tolerance of the oracle."""
+    x = S.activations(K, seed=K + len(ns))
+    dx = uq.DeviceArray.from_numpy(x)
+    ws = [S.weights(dtype, n, K, seed=17 * i + n) for i, n in enumerate(ns)]
+    Ws = [uq.Weights(w, dtype, K, n) for w, n in zip(ws, ns)]
+    yb = [uq.DeviceArray(4 * n) for n in ns]
+    ys = [uq.DeviceArray(4 * n) for n in ns]
+    uq.gemv_batch(Ws, dx, yb)
+    for W, y in zip(Ws, ys):
+        uq.gemv(W, dx, y)
+    for w, n, a, b in zip(ws, ns, yb, ys):
+        got, sep = a.download(np.float32, n), b.download(np.float32, n)
+        assert_bitwise(got, sep, what=f"batch vs separate n={n}")
+        ref = np.zeros(n, np.float32)
+        O.gemv_quant(ref, x, w, K, n, dtype, nthreads=NT)
+        assert_close(got, ref, what=f"batch n={n}")
+
+
+def test_gemv_batch_rejects_mixed_shapes():
+    K = 4096
+    a = uq.Weights(S.weights(S.Q4_K, 8, K, seed=1), uq.DType.Q4K, K, 8)
+    b = uq.Weights(S.weights(S.Q6_K, 8, K, seed=2), uq.DType.Q6K, K, 8)
+    c = uq.Weights(S.weights(S.Q4_K, 8, 2 * K, seed=3), uq.DType.Q4K, 2 * K, 8)
+    dx = uq.DeviceArray.from_numpy(S.activations(2 * K, seed=4))
+    ys = [uq.DeviceArray(32), uq.DeviceArray(32)]
+    for pair in ((a, b), (a, c)):
+        with pytest.raises(uq.UqError) as e:
+            uq.gemv_batch(list(pair), dx, ys)
+        assert e.value.kind == "LEN"

@@ -419,6 +419,30 @@ uq_status uq_gemv(uq_weights wh, const float *d_x, float *d_y, void *stream) {
     return UQ_OK;
 }
 
+uq_status uq_gemv_batch(const uq_weights *whs, float *const *d_y, size_t count, const float *d_x, void *stream) {
+    if (!whs || !d_y) return fail(UQ_ERR_ARG, "gemv_batch: null argument");
+    if (count == 0) return UQ_OK;
+    if (count > UQ_GEMV_BATCH_MAX) return fail(UQ_ERR_ARG, "gemv_batch: count %zu above %d", count, UQ_GEMV_BATCH_MAX);
+    uq::WeightsView v[UQ_GEMV_BATCH_MAX];
+    uq_weights_s *first = nullptr;
+    for (size_t i = 0; i < count; i++) {
+        uq_weights_s *w = handle(whs[i]);
+        if (!w) return fail(UQ_ERR_ARG, "gemv_batch: invalid handle %zu", i);
+        if (!first) first = w;
+        if (w->dtype != first->dtype || w->dim_in != first->dim_in)
+            return fail(UQ_ERR_LEN, "gemv_batch: weights %zu differ from weights 0 in dtype or dim_in", i);
+        if (w->device != first->device) return fail(UQ_ERR_ARG, "gemv_batch: weights on different devices");
+        if (w->dim_out && !d_y[i]) return fail(UQ_ERR_ARG, "gemv_batch: null output %zu", i);
+        v[i] = uq::view(*w);
+    }
+    if (!d_x && first->dim_in) return fail(UQ_ERR_ARG, "gemv_batch: null device pointer");
+    size_t rows = 0;
+    for (size_t i = 0; i < count; i++) rows += v[i].dim_out;
+    if (rows > (size_t)INT_MAX) return fail(UQ_ERR_ARG, "gemv_batch: more than INT_MAX rows");
+    UQ_HIP(uq::launch_gemv_batch(v, (int)count, d_x, d_y, (hipStream_t)stream), "gemv_batch launch");
+    return UQ_OK;
+}
+
 uq_status uq_gemv_q8k(uq_weights wh, const float *d_x, float *d_y, void *stream) {
     uq_weights_s *w = handle(wh);
     if (!w) return fail(UQ_ERR_ARG, "gemv_q8k: invalid handle");

@@ -76,6 +76,24 @@ __device__ inline float swiglu1(float g, float u) {
 // LDS-streaming kernels are left to the allocator.
 #define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(PAIR || !XREG ? 1 : NW / 4)))
 
+// Rows of up to kMaxSegs weight tensors that share x (and dtype, K), laid
+// end to end: global row R belongs to segment s with start[s] <= R <
+// start[s+1]; its bytes are at w[s] (w2[s] for the gate/up pair) and its
+// result goes to y[s]. A single GEMV is one segment.
+constexpr int kMaxSegs = 8;
+struct Segs {
+    int n;
+    int start[kMaxSegs + 1];
+    const uint8_t *w[kMaxSegs];
+    const uint8_t *w2[kMaxSegs];
+    float *y[kMaxSegs];
+};
+__device__ __forceinline__ int seg_of(const Segs &S, int R) {
+    int s = 0;
+    for (int i = 1; i < kMaxSegs; i++) s += (i < S.n && R >= S.start[i]) ? 1 : 0;
+    return s;
+}
+
 // One unit = one task of one row. A wave owns rows wave, wave + nwave, ...
 // and walks their units in order (the tasks of a row, then the next row); a
 // ring of D units keeps that many weight loads in flight, each slot reloaded
@@ -86,12 +104,9 @@ __device__ inline float swiglu1(float g, float u) {
 // XREG (one task per lane, K <= 4096) keeps the lane's activation digits in
 // VGPRs; otherwise they are read from LDS for every unit (then D == 1).
 // PAIR: W and W2 (gate, up) share x; writes swiglu(W x, W2 x).
-template <class F, bool PAIR, bool XREG, int D, int NW>
-__global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const uint8_t *__restrict__ W,
-                                                               const uint8_t *__restrict__ W2,
-                                                               size_t row_bytes, int K, int N,
-                                                               const float *__restrict__ x,
-                                                               float *__restrict__ y) {
+template <class F, bool PAIR, bool XREG, int D, int NW, bool MULTI>
+__global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S, size_t row_bytes, int K,
+                                                               const float *__restrict__ x) {
     static_assert(D == 1 || D == 2 || D == 4, "ring depth divides the 4-row batch");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -100,24 +115,36 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const uint8_t
     const typename F::LC c = F::lane_consts(lane);
     const int wave = blockIdx.x * NW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
     const int nwave = gridDim.x * NW;
+    const int N = S.start[S.n];
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
     const int U = nrows * T;  // units of this wave
-    const size_t stride = (size_t)nwave * row_bytes;
 
     typename F::Frag f[D], f2[D];
-    const uint8_t *pw = W + (size_t)wave * row_bytes;    // row of the next unit to load
-    const uint8_t *pw2 = W2 + (size_t)wave * row_bytes;  // (PAIR only)
-    int pt = 0, issued = 0;
+    // single tensor: row pointers advance by a fixed stride; several: each
+    // row's segment is looked up (wave-uniform, scalar)
+    const size_t stride = (size_t)nwave * row_bytes;
+    const uint8_t *pw = S.w[0] + (size_t)wave * row_bytes;
+    const uint8_t *pw2 = PAIR ? S.w2[0] + (size_t)wave * row_bytes : nullptr;
+    int pr = 0, pt = 0, issued = 0;  // next unit to load: row index, task iteration
     auto issue = [&](typename F::Frag &dst, typename F::Frag &dst2) {
         const int t = lane + 64 * pt;
+        if (MULTI) {
+            const int R = wave + pr * nwave, sg = __builtin_amdgcn_readfirstlane(seg_of(S, R));
+            const size_t off = (size_t)(R - S.start[sg]) * row_bytes;
+            pw = S.w[sg] + off;
+            if (PAIR) pw2 = S.w2[sg] + off;
+        }
         if (t < ntask) {
             dst = F::load_w(pw, t, c);
             if (PAIR) dst2 = F::load_w(pw2, t, c);
         }
         if (++pt == T) {
             pt = 0;
-            pw += stride;
-            if (PAIR) pw2 += stride;
+            ++pr;
+            if (!MULTI) {
+                pw += stride;
+                if (PAIR) pw2 += stride;
+            }
         }
         ++issued;
     };
@@ -166,8 +193,75 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const uint8_t
         if (PAIR) Uu = reduce4_rows(u);
         const int r = lane >> 4;
         if ((lane & 15) == 0 && rb + r < nrows) {
-            const int row = wave + (rb + r) * nwave;
-            y[row] = PAIR ? swiglu1((float)G, (float)Uu) : (float)G;
+            const int R = wave + (rb + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
+            S.y[sg][R - S.start[sg]] = PAIR ? swiglu1((float)G, (float)Uu) : (float)G;
+        }
+    }
+}
+
+// K > 4096 (several tasks per lane and row): rows are still taken four at a
+// time, and the loop runs task-outer, row-inner: a lane reads its task's
+// activation digits from LDS once and applies them to the four rows, whose
+// weight fragments for that task are one load unit (issued right after the
+// previous unit is consumed, the first before the prep). Summation per lane
+// is over tasks in order, then reduce4_rows, as in gemv_kernel.
+constexpr int KT_NW = 8;  // 2 waves per SIMD, one workgroup per CU
+template <class F, bool MULTI>
+__global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kt_kernel(
+    const Segs S, size_t row_bytes, int K, const float *__restrict__ x) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int ntask = F::ntasks(K);
+    const int T = (ntask + 63) >> 6;
+    const typename F::LC c = F::lane_consts(lane);
+    const int wave = blockIdx.x * KT_NW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int nwave = gridDim.x * KT_NW;
+    const int N = S.start[S.n];
+    const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
+    const int nb = (nrows + 3) >> 2;
+
+    typename F::Frag f[4];
+    int ib = 0, it = 0;  // next unit to load: batch, task
+    auto issue = [&]() {
+        const int t = lane + 64 * it;
+        for (int r = 0; r < 4; r++) {
+            const int i = 4 * ib + r;
+            if (i < nrows && t < ntask) {
+                const int R = wave + i * nwave, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(S, R)) : 0;
+                f[r] = F::load_w(S.w[sg] + (size_t)(R - S.start[sg]) * row_bytes, t, c);
+            }
+        }
+        if (++it == T) {
+            it = 0;
+            ++ib;
+        }
+    };
+    if (nb > 0) issue();
+
+    const XLayout L = x_layout_at<F>(lds, K);
+    prep_x<F>(x, K, L);
+    __syncthreads();
+    if (nb == 0) return;
+    const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
+
+    for (int b = 0; b < nb; b++) {
+        double g[4] = {0.0, 0.0, 0.0, 0.0};
+        for (int tt = 0; tt < T; tt++) {
+            const int t = lane + 64 * tt;
+            if (t < ntask) {
+                typename F::XS xs;
+                F::load_x(xs, PV, t, c);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (4 * b + r < nrows) g[r] += F::dot(f[r], xs, c);  // wave-uniform row test
+            }
+            if (ib < nb) issue();
+        }
+        const double G = reduce4_rows(g);
+        const int r = lane >> 4;
+        if ((lane & 15) == 0 && 4 * b + r < nrows) {
+            const int R = wave + (4 * b + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
+            S.y[sg][R - S.start[sg]] = (float)G;
         }
     }
 }
@@ -265,38 +359,64 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 template <class F> struct Shape { static constexpr int NW = 16, D = 1; };
 template <> struct Shape<Q6K> { static constexpr int NW = 12, D = 2; };
 
-template <class F, bool PAIR>
-hipError_t launch_fast(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out;
+template <class F, bool PAIR, bool MULTI>
+hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+    const int N = S.start[S.n];
     const size_t lds = x_lds_bytes<F>(K);
     if (F::ntasks(K) <= 64) {
         constexpr int NW = PAIR ? WAVES : Shape<F>::NW, D = PAIR ? 1 : Shape<F>::D;
-        const void *k = (const void *)gemv_kernel<F, PAIR, true, D, NW>;
-        hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW>), dim3(resident_grid(k, lds, N, NW)),
-                           dim3(64 * NW), lds, s, w.bytes, w2, w.row_bytes, K, N, x, y);
+        const void *k = (const void *)gemv_kernel<F, PAIR, true, D, NW, MULTI>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW, MULTI>), dim3(resident_grid(k, lds, N, NW)),
+                           dim3(64 * NW), lds, s, S, row_bytes, K, x);
+    } else if constexpr (!PAIR) {
+        const void *k = (const void *)gemv_kt_kernel<F, MULTI>;
+        hipLaunchKernelGGL((gemv_kt_kernel<F, MULTI>), dim3(resident_grid(k, lds, N, KT_NW)), dim3(64 * KT_NW), lds,
+                           s, S, row_bytes, K, x);
     } else {
-        const void *k = (const void *)gemv_kernel<F, PAIR, false, 1, WAVES>;
-        hipLaunchKernelGGL((gemv_kernel<F, PAIR, false, 1, WAVES>), dim3(resident_grid(k, lds, N)), dim3(TPB), lds,
-                           s, w.bytes, w2, w.row_bytes, K, N, x, y);
+        const void *k = (const void *)gemv_kernel<F, PAIR, false, 1, WAVES, MULTI>;
+        hipLaunchKernelGGL((gemv_kernel<F, PAIR, false, 1, WAVES, MULTI>), dim3(resident_grid(k, lds, N)), dim3(TPB),
+                           lds, s, S, row_bytes, K, x);
     }
     return hipGetLastError();
 }
+template <class F, bool PAIR>
+hipError_t launch_fast(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+    if (PAIR || S.n == 1) return launch_fast_m<F, PAIR, false>(S, row_bytes, K, x, s);
+    return launch_fast_m<F, false, true>(S, row_bytes, K, x, s);
+}
 
-hipError_t launch_any(const WeightsView &w, const uint8_t *w2, const float *x, float *y, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out;
-    if (N == 0) return hipSuccess;
-    const bool pair = w2 != nullptr;
-    if (w.dtype == UQ_Q4_K && x_lds_bytes<Q4K>(K) <= kLdsCap)
-        return pair ? launch_fast<Q4K, true>(w, w2, x, y, s) : launch_fast<Q4K, false>(w, w2, x, y, s);
-    if (w.dtype == UQ_Q6_K && x_lds_bytes<Q6K>(K) <= kLdsCap)
-        return pair ? launch_fast<Q6K, true>(w, w2, x, y, s) : launch_fast<Q6K, false>(w, w2, x, y, s);
-    if (w.dtype == UQ_Q8_0 && K % 64 == 0 && x_lds_bytes<Q80>(K) <= kLdsCap)
-        return pair ? launch_fast<Q80, true>(w, w2, x, y, s) : launch_fast<Q80, false>(w, w2, x, y, s);
-    int grid = (N + WAVES - 1) / WAVES;
-    if (grid > num_cus() * 8) grid = num_cus() * 8;
-    hipLaunchKernelGGL(gemv_generic_kernel, dim3(grid), dim3(TPB), 0, s, w.dtype, w.bytes, w2,
-                       w.row_bytes, K, N, x, y);
-    return hipGetLastError();
+// All segments share dtype, K and row_bytes; pair = S.w2 holds the up rows.
+hipError_t launch_segs(uq_dtype dt, int K, size_t row_bytes, const Segs &S, bool pair, const float *x,
+                       hipStream_t s) {
+    if (S.start[S.n] == 0) return hipSuccess;
+    if (dt == UQ_Q4_K && x_lds_bytes<Q4K>(K) <= kLdsCap)
+        return pair ? launch_fast<Q4K, true>(S, row_bytes, K, x, s) : launch_fast<Q4K, false>(S, row_bytes, K, x, s);
+    if (dt == UQ_Q6_K && x_lds_bytes<Q6K>(K) <= kLdsCap)
+        return pair ? launch_fast<Q6K, true>(S, row_bytes, K, x, s) : launch_fast<Q6K, false>(S, row_bytes, K, x, s);
+    if (dt == UQ_Q8_0 && K % 64 == 0 && x_lds_bytes<Q80>(K) <= kLdsCap)
+        return pair ? launch_fast<Q80, true>(S, row_bytes, K, x, s) : launch_fast<Q80, false>(S, row_bytes, K, x, s);
+    for (int i = 0; i < S.n; i++) {
+        const int N = S.start[i + 1] - S.start[i];
+        if (N == 0) continue;
+        int grid = (N + WAVES - 1) / WAVES;
+        if (grid > num_cus() * 8) grid = num_cus() * 8;
+        hipLaunchKernelGGL(gemv_generic_kernel, dim3(grid), dim3(TPB), 0, s, dt, S.w[i], pair ? S.w2[i] : nullptr,
+                           row_bytes, K, N, x, S.y[i]);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+Segs one_seg(const WeightsView &w, const uint8_t *w2, float *y) {
+    Segs S{};
+    S.n = 1;
+    S.start[0] = 0;
+    S.start[1] = w.dim_out;
+    S.w[0] = w.bytes;
+    S.w2[0] = w2;
+    S.y[0] = y;
+    return S;
 }
 
 // ---------------------------- gemv_quant_q8k -------------------------------
@@ -536,12 +656,26 @@ hipError_t launch_q8k_fast(const WeightsView &w, const float *x, float *y, hipSt
 }  // namespace
 
 hipError_t launch_gemv(const WeightsView &w, const float *x, float *y, hipStream_t s) {
-    return launch_any(w, nullptr, x, y, s);
+    return launch_segs(w.dtype, w.dim_in, w.row_bytes, one_seg(w, nullptr, y), false, x, s);
+}
+
+hipError_t launch_gemv_batch(const WeightsView *w, int n, const float *x, float *const *y, hipStream_t s) {
+    static_assert(kMaxSegs == UQ_GEMV_BATCH_MAX, "segment table size");
+    Segs S{};
+    S.n = n;
+    S.start[0] = 0;
+    for (int i = 0; i < n; i++) {
+        S.w[i] = w[i].bytes;
+        S.w2[i] = nullptr;
+        S.y[i] = y[i];
+        S.start[i + 1] = S.start[i] + w[i].dim_out;
+    }
+    return launch_segs(w[0].dtype, w[0].dim_in, w[0].row_bytes, S, false, x, s);
 }
 
 hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, const float *x, float *h,
                                  hipStream_t s) {
-    return launch_any(g, u.bytes, x, h, s);
+    return launch_segs(g.dtype, g.dim_in, g.row_bytes, one_seg(g, u.bytes, h), true, x, s);
 }
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {

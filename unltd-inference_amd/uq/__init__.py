@@ -66,6 +66,7 @@ SIGNATURES = {
     "uq_weights_free": ([_P], _I),
     "uq_weights_info": ([_P, C.POINTER(_I), C.POINTER(_S), C.POINTER(_S), C.POINTER(_S)], _I),
     "uq_gemv": ([_P, _P, _P, _P], _I),
+    "uq_gemv_batch": ([_P, _P, _S, _P, _P], _I),
     "uq_gemv_q8k": ([_P, _P, _P, _P], _I),
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
@@ -270,6 +271,17 @@ class Weights:
 
 def gemv(w: Weights, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
     _check(lib().uq_gemv(w.h, d_x.ptr, d_y.ptr, stream))
+
+
+GEMV_BATCH_MAX = 8
+
+
+def gemv_batch(ws, d_x: DeviceArray, d_ys, stream=None) -> None:
+    """d_ys[i] = ws[i] . d_x for every i, in one launch (same dtype and dim_in)."""
+    n = len(ws)
+    hs = (_P * max(n, 1))(*[w.h for w in ws])
+    ys = (_P * max(n, 1))(*[y.ptr for y in d_ys])
+    _check(lib().uq_gemv_batch(hs, ys, n, d_x.ptr, stream))
 
 
 def gemv_q8k(w: Weights, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
