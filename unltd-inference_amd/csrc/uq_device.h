@@ -150,15 +150,28 @@ struct XLayout {
 
 __device__ __forceinline__ uint32_t digit(int v) { return (uint32_t)v & 0xFFu; }
 
+// The first element-dword of each thread can be loaded early (prep_x_first)
+// so its latency overlaps the kernel's first weight loads.
+__device__ __forceinline__ float4 prep_x_first(const float *__restrict__ x, int K) {
+    const int w = threadIdx.x;
+    return w < (K >> 2) ? *(const float4 *)(x + 4 * w) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <class F>
-__device__ __forceinline__ void prep_x(const float *__restrict__ x, int K, XLayout L) {
+__device__ __forceinline__ void prep_x(const float *__restrict__ x, int K, XLayout L, float4 first) {
     const int nw = K >> 2;
     const int nw_pad = (nw + 31) & ~31;
     for (int w = threadIdx.x; w < ((nw_pad + blockDim.x - 1) / blockDim.x) * blockDim.x; w += blockDim.x) {
         const bool in = w < nw;
         float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (in)
+        if (w == (int)threadIdx.x) {
+            v[0] = first.x;
+            v[1] = first.y;
+            v[2] = first.z;
+            v[3] = first.w;
+        } else if (in) {
             for (int i = 0; i < 4; i++) v[i] = x[4 * w + i];
+        }
         float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
         for (int off = 16; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
         int ex = 0;

@@ -74,7 +74,7 @@ __device__ inline float swiglu1(float g, float u) {
 // waves per SIMD (one workgroup of NW waves per CU), so the allocator is held
 // to 512/(NW/4) VGPRs; the gate/up pair (twice the weight fragments) and the
 // LDS-streaming kernels are left to the allocator.
-#define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(PAIR || !XREG ? 1 : NW / 4)))
+#define UQ_GEMV_OCC __attribute__((amdgpu_waves_per_eu(!XREG || NW < 8 ? 1 : NW / 4)))
 
 // Rows of up to kMaxSegs weight tensors that share x (and dtype, K), laid
 // end to end: global row R belongs to segment s with start[s] <= R <
@@ -119,6 +119,7 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
     const int U = nrows * T;  // units of this wave
 
+    const float4 x_first = prep_x_first(x, K);
     typename F::Frag f[D], f2[D];
     // single tensor: row pointers advance by a fixed stride; several: each
     // row's segment is looked up (wave-uniform, scalar)
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
         if (d < U) issue(f[d], f2[d]);
 
     const XLayout L = x_layout_at<F>(lds, K);
-    prep_x<F>(x, K, L);
+    prep_x<F>(x, K, L, x_first);
     __syncthreads();
     if (U == 0) return;
     const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
@@ -220,6 +221,7 @@ __global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(2)))
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
     const int nb = (nrows + 3) >> 2;
 
+    const float4 x_first = prep_x_first(x, K);
     typename F::Frag f[4];
     int ib = 0, it = 0;  // next unit to load: batch, task
     auto issue = [&]() {
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(2)))
     if (nb > 0) issue();
 
     const XLayout L = x_layout_at<F>(lds, K);
-    prep_x<F>(x, K, L);
+    prep_x<F>(x, K, L, x_first);
     __syncthreads();
     if (nb == 0) return;
     const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
@@ -356,7 +358,19 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 // (NW waves) so the activation prep runs once per CU, with D units in flight
 // per wave. Q6_K: 12 waves (3 per SIMD, <= 168 VGPRs) with two units in
 // flight; Q4_K and Q8_0: 16 waves (4 per SIMD, <= 128 VGPRs), one unit.
-template <class F> struct Shape { static constexpr int NW = 16, D = 1; };
+#ifndef UQ_Q4K_NW
+#define UQ_Q4K_NW 16
+#endif
+#ifndef UQ_Q4K_D
+#define UQ_Q4K_D 1
+#endif
+#ifndef UQ_PAIR_NW
+#define UQ_PAIR_NW 4
+#endif
+#ifndef UQ_PAIR_D
+#define UQ_PAIR_D 1
+#endif
+template <class F> struct Shape { static constexpr int NW = UQ_Q4K_NW, D = UQ_Q4K_D; };
 template <> struct Shape<Q6K> { static constexpr int NW = 12, D = 2; };
 
 template <class F, bool PAIR, bool MULTI>
@@ -364,7 +378,7 @@ hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x,
     const int N = S.start[S.n];
     const size_t lds = x_lds_bytes<F>(K);
     if (F::ntasks(K) <= 64) {
-        constexpr int NW = PAIR ? WAVES : Shape<F>::NW, D = PAIR ? 1 : Shape<F>::D;
+        constexpr int NW = PAIR ? UQ_PAIR_NW : Shape<F>::NW, D = PAIR ? UQ_PAIR_D : Shape<F>::D;
         const void *k = (const void *)gemv_kernel<F, PAIR, true, D, NW, MULTI>;
         hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW, MULTI>), dim3(resident_grid(k, lds, N, NW)),
                            dim3(64 * NW), lds, s, S, row_bytes, K, x);
