@@ -147,6 +147,12 @@ uq_status uq_gemv_batch(const uq_weights *w, float *const *d_y, size_t count,
 /* d_y = gemv_quant_q8k(W, d_x) (quants.rs:474-515), bit-exact. */
 uq_status uq_gemv_q8k(uq_weights w, const float *d_x, float *d_y, void *stream);
 
+/* uq_gemv_batch with gemv_quant_q8k semantics (Q4_K / Q6_K): every d_y[i]
+ * equals gemv_quant_q8k(W[i], d_x) bit for bit. No reference counterpart
+ * (one gemv_quant_q8k call per projection, qwen35_forward.rs:365-401). */
+uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count,
+                            const float *d_x, void *stream);
+
 /* Batched prefill: d_y[m][dim_out] = W . d_x[m][dim_in] for m < m_rows, with
  * gemv_quant semantics per row (the reference feeds prefill tokens one at a
  * time, greedy.rs:55-65; each row equals gemv_quant of that token).
@@ -162,6 +168,19 @@ uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
  * gate/up: [n_ff][n]; down: [n][n_ff]. d_h holds n_ff floats. */
 uq_status uq_ffn_swiglu(uq_weights gate, uq_weights up, uq_weights down,
                         const float *d_x, float *d_h, float *d_y, void *stream);
+
+/* The reference FFN (qwen35_forward.rs:735-765) bit for bit on the device:
+ * d_g = gemv_quant_q8k(gate, d_x), d_u = gemv_quant_q8k(up, d_x) (one
+ * launch), d_h = swiglu(d_g, d_u) (kernels.rs:174-182), d_y =
+ * gemv_quant_q8k(down, d_h). gate/up: [n_ff][n]; down: [n][n_ff]; Q4_K or
+ * Q6_K. d_g, d_u, d_h hold n_ff floats (the reference's g, u, sw). */
+uq_status uq_ffn_swiglu_q8k(uq_weights gate, uq_weights up, uq_weights down,
+                            const float *d_x, float *d_g, float *d_u, float *d_h,
+                            float *d_y, void *stream);
+
+/* swiglu (kernels.rs:174-182) on device arrays: d_out = (g/(1+expf(-g)))*u. */
+uq_status uq_swiglu_d(float *d_out, const float *d_gate, const float *d_up, size_t n,
+                      void *stream);
 
 /* Device f32 dequantization of a whole handle into d_out[dim_out*dim_in]
  * (dequantize_q4_k semantics, bit-exact; Q6_K/Q8_0 closed forms). */

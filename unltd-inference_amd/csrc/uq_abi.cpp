@@ -419,27 +419,73 @@ uq_status uq_gemv(uq_weights wh, const float *d_x, float *d_y, void *stream) {
     return UQ_OK;
 }
 
-uq_status uq_gemv_batch(const uq_weights *whs, float *const *d_y, size_t count, const float *d_x, void *stream) {
-    if (!whs || !d_y) return fail(UQ_ERR_ARG, "gemv_batch: null argument");
-    if (count == 0) return UQ_OK;
-    if (count > UQ_GEMV_BATCH_MAX) return fail(UQ_ERR_ARG, "gemv_batch: count %zu above %d", count, UQ_GEMV_BATCH_MAX);
-    uq::WeightsView v[UQ_GEMV_BATCH_MAX];
+// Shared validation of the batched GEMV entry points: fills v[0..count).
+static uq_status batch_views(const char *fn, const uq_weights *whs, float *const *d_y, size_t count,
+                             const float *d_x, bool q8k, uq::WeightsView *v) {
+    if (!whs || !d_y) return fail(UQ_ERR_ARG, "%s: null argument", fn);
+    if (count > UQ_GEMV_BATCH_MAX) return fail(UQ_ERR_ARG, "%s: count %zu above %d", fn, count, UQ_GEMV_BATCH_MAX);
     uq_weights_s *first = nullptr;
+    size_t rows = 0;
     for (size_t i = 0; i < count; i++) {
         uq_weights_s *w = handle(whs[i]);
-        if (!w) return fail(UQ_ERR_ARG, "gemv_batch: invalid handle %zu", i);
+        if (!w) return fail(UQ_ERR_ARG, "%s: invalid handle %zu", fn, i);
         if (!first) first = w;
+        if (q8k && w->dtype != UQ_Q4_K && w->dtype != UQ_Q6_K)
+            return fail(UQ_ERR_DTYPE, "%s: dtype %s does not use the Q8_K dot", fn, dtype_name(w->dtype));
         if (w->dtype != first->dtype || w->dim_in != first->dim_in)
-            return fail(UQ_ERR_LEN, "gemv_batch: weights %zu differ from weights 0 in dtype or dim_in", i);
-        if (w->device != first->device) return fail(UQ_ERR_ARG, "gemv_batch: weights on different devices");
-        if (w->dim_out && !d_y[i]) return fail(UQ_ERR_ARG, "gemv_batch: null output %zu", i);
+            return fail(UQ_ERR_LEN, "%s: weights %zu differ from weights 0 in dtype or dim_in", fn, i);
+        if (w->device != first->device) return fail(UQ_ERR_ARG, "%s: weights on different devices", fn);
+        if (w->dim_out && !d_y[i]) return fail(UQ_ERR_ARG, "%s: null output %zu", fn, i);
         v[i] = uq::view(*w);
+        rows += w->dim_out;
     }
-    if (!d_x && first->dim_in) return fail(UQ_ERR_ARG, "gemv_batch: null device pointer");
-    size_t rows = 0;
-    for (size_t i = 0; i < count; i++) rows += v[i].dim_out;
-    if (rows > (size_t)INT_MAX) return fail(UQ_ERR_ARG, "gemv_batch: more than INT_MAX rows");
+    if (first && !d_x && first->dim_in) return fail(UQ_ERR_ARG, "%s: null device pointer", fn);
+    if (rows > (size_t)INT_MAX) return fail(UQ_ERR_ARG, "%s: more than INT_MAX rows", fn);
+    return UQ_OK;
+}
+
+uq_status uq_gemv_batch(const uq_weights *whs, float *const *d_y, size_t count, const float *d_x, void *stream) {
+    uq::WeightsView v[UQ_GEMV_BATCH_MAX];
+    uq_status st = batch_views("gemv_batch", whs, d_y, count, d_x, false, v);
+    if (st != UQ_OK || count == 0) return st;
     UQ_HIP(uq::launch_gemv_batch(v, (int)count, d_x, d_y, (hipStream_t)stream), "gemv_batch launch");
+    return UQ_OK;
+}
+
+uq_status uq_gemv_q8k_batch(const uq_weights *whs, float *const *d_y, size_t count, const float *d_x,
+                            void *stream) {
+    uq::WeightsView v[UQ_GEMV_BATCH_MAX];
+    uq_status st = batch_views("gemv_q8k_batch", whs, d_y, count, d_x, true, v);
+    if (st != UQ_OK || count == 0) return st;
+    UQ_HIP(uq::launch_gemv_q8k_batch(v, (int)count, d_x, d_y, (hipStream_t)stream), "gemv_q8k_batch launch");
+    return UQ_OK;
+}
+
+uq_status uq_swiglu_d(float *d_out, const float *d_gate, const float *d_up, size_t n, void *stream) {
+    if (n == 0) return UQ_OK;
+    if (!d_out || !d_gate || !d_up) return fail(UQ_ERR_ARG, "swiglu_d: null device pointer");
+    UQ_HIP(uq::launch_swiglu(d_gate, d_up, n, d_out, (hipStream_t)stream), "swiglu_d launch");
+    return UQ_OK;
+}
+
+uq_status uq_ffn_swiglu_q8k(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_g, float *d_u,
+                            float *d_h, float *d_y, void *stream) {
+    uq_weights_s *g = handle(gh), *u = handle(uh), *dn = handle(dh);
+    if (!g || !u || !dn) return fail(UQ_ERR_ARG, "ffn_swiglu_q8k: invalid handle");
+    for (uq_weights_s *w : {g, u, dn})
+        if (w->dtype != UQ_Q4_K && w->dtype != UQ_Q6_K)
+            return fail(UQ_ERR_DTYPE, "ffn_swiglu_q8k: dtype %s does not use the Q8_K dot", dtype_name(w->dtype));
+    if (g->dtype != u->dtype || g->dim_in != u->dim_in || g->dim_out != u->dim_out)
+        return fail(UQ_ERR_LEN, "ffn_swiglu_q8k: gate and up differ in dtype or shape");
+    if (dn->dim_in != g->dim_out)
+        return fail(UQ_ERR_LEN, "ffn_swiglu_q8k: down dim_in %zu != n_ff %zu", dn->dim_in, g->dim_out);
+    if (!d_x || !d_g || !d_u || !d_h || !d_y) return fail(UQ_ERR_ARG, "ffn_swiglu_q8k: null device pointer");
+    const hipStream_t s = (hipStream_t)stream;
+    const uq::WeightsView gu[2] = {uq::view(*g), uq::view(*u)};
+    float *const gy[2] = {d_g, d_u};
+    UQ_HIP(uq::launch_gemv_q8k_batch(gu, 2, d_x, gy, s), "ffn_q8k gate/up launch");
+    UQ_HIP(uq::launch_swiglu(d_g, d_u, g->dim_out, d_h, s), "ffn_q8k swiglu launch");
+    UQ_HIP(uq::launch_gemv_q8k(uq::view(*dn), d_h, d_y, s), "ffn_q8k down launch");
     return UQ_OK;
 }
 

@@ -135,14 +135,12 @@ __global__ void f16_kernel(const uint16_t *__restrict__ h, size_t n, float *__re
         out[t] = f16_bits_exact(h[t]);
 }
 
-// swiglu (kernels.rs:174-182): s = t/(1+expf(-t)); out = s*u.
+// swiglu (kernels.rs:174-182): s = t/(1+expf(-t)); out = s*u (swiglu1).
 __global__ void swiglu_kernel(const float *__restrict__ g, const float *__restrict__ u, size_t n,
                               float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n;
-         t += (size_t)gridDim.x * blockDim.x) {
-        const float v = g[t];
-        out[t] = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, expf(-v))), u[t]);
-    }
+         t += (size_t)gridDim.x * blockDim.x)
+        out[t] = swiglu1(g[t], u[t]);
 }
 
 // quantize_q8_k (quants.rs:250-290), one wave per 256-block, 4 values/lane.

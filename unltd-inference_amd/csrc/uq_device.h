@@ -35,6 +35,18 @@ __device__ __forceinline__ float f16_bits_exact(uint32_t h) {
 }
 
 // ---------------------------------------------------------------------------
+// swiglu (kernels.rs:174-182): (t / (1 + expf(-t))) * up, all f32. The
+// reference's expf is the platform libm's; here the exponential is evaluated
+// in f64 and rounded once, i.e. correctly rounded except for arguments whose
+// exact result lies within about 2^-29 ulp of a rounding midpoint, so it
+// agrees with a correctly rounding (or nearly correctly rounding) libm expf.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float expf_cr(float v) { return (float)exp((double)v); }
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_cr(-g))), u);
+}
+
+// ---------------------------------------------------------------------------
 // Wave64 reductions with DPP (row_mirror / row_bcast); the result is
 // returned to every lane. Summation tree is fixed, so results are
 // deterministic.

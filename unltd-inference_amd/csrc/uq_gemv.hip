@@ -65,11 +65,6 @@ __device__ inline XLayout x_layout_at(uint8_t *lds, int K) {
     return L;
 }
 
-__device__ inline float swiglu1(float g, float u) {
-    // kernels.rs:174-182: (t / (1 + expf(-t))) * up, all f32
-    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-}
-
 // Register budget: the single GEMV kernels that keep x in VGPRs run NW/4
 // waves per SIMD (one workgroup of NW waves per CU), so the allocator is held
 // to 512/(NW/4) VGPRs; the gate/up pair (twice the weight fragments) and the
@@ -501,10 +496,9 @@ __host__ __device__ inline Q8KLayout q8k_layout(int K) {
     return L;
 }
 
-template <class F, bool CACHED>
-__global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                       int K, int N, const float *__restrict__ x,
-                                                       float *__restrict__ y) {
+template <class F, bool CACHED, bool MULTI>
+__global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_bytes, int K,
+                                                       const float *__restrict__ x) {
     extern __shared__ __align__(16) uint8_t lds[];
     const Q8KLayout L = q8k_layout<F>(K);
     const int nblk = K >> 8, ntask = 4 * nblk, R = L.R;
@@ -527,9 +521,11 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const uint8_t *__restrict
     typename F::XS xs0;
     if (CACHED && lane < ntask) F::load_x(xs0, xq, lane);
 
+    const int N = S.start[S.n];
     int slot = 0;
     for (int row = wave; row < N; row += nwave) {
-        const uint8_t *Rw = W + (size_t)row * row_bytes;
+        const int sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(S, row)) : 0;
+        const uint8_t *Rw = S.w[sg] + (size_t)(row - S.start[sg]) * row_bytes;
         for (int it = 0; it < iters; it++) {
             const int t = lane + 64 * it;
             int S[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
@@ -579,7 +575,10 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const uint8_t *__restrict
             float s = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) s = __fadd_rn(s, __shfl(sums, (lane & ~7) + kk));
-            if (k == 0 && r < slot) y[row - (slot - 1 - r) * nwave] = s;
+            if (k == 0 && r < slot) {
+                const int Rr = row - (slot - 1 - r) * nwave, so = MULTI ? seg_of(S, Rr) : 0;
+                S.y[so][Rr - S.start[so]] = s;
+            }
             __builtin_amdgcn_wave_barrier();
             slot = 0;
         }
@@ -651,20 +650,58 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
     }
 }
 
-template <class F>
-hipError_t launch_q8k_fast(const WeightsView &w, const float *x, float *y, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out;
+template <class F, bool MULTI>
+hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+    const int N = S.start[S.n];
     const Q8KLayout L = q8k_layout<F>(K);
     if (F::ntasks(K) <= 64) {
-        const void *k = (const void *)gemv_q8k_kernel<F, true>;
-        hipLaunchKernelGGL((gemv_q8k_kernel<F, true>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total, s,
-                           w.bytes, w.row_bytes, K, N, x, y);
+        const void *k = (const void *)gemv_q8k_kernel<F, true, MULTI>;
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, true, MULTI>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total,
+                           s, S, row_bytes, K, x);
     } else {
-        const void *k = (const void *)gemv_q8k_kernel<F, false>;
-        hipLaunchKernelGGL((gemv_q8k_kernel<F, false>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total, s,
-                           w.bytes, w.row_bytes, K, N, x, y);
+        const void *k = (const void *)gemv_q8k_kernel<F, false, MULTI>;
+        hipLaunchKernelGGL((gemv_q8k_kernel<F, false, MULTI>), dim3(resident_grid(k, L.total, N)), dim3(TPB),
+                           L.total, s, S, row_bytes, K, x);
     }
     return hipGetLastError();
+}
+
+// gemv_quant_q8k over a segment table (all segments share dtype and K).
+hipError_t launch_q8k_segs(uq_dtype dt, int K, size_t row_bytes, const Segs &S, const float *x, hipStream_t s) {
+    if (S.start[S.n] == 0) return hipSuccess;
+    const bool multi = S.n > 1;
+    if (dt == UQ_Q4_K && q8k_layout<Q4KQ8>(K).total <= kLdsCap)
+        return multi ? launch_q8k_fast_m<Q4KQ8, true>(S, row_bytes, K, x, s)
+                     : launch_q8k_fast_m<Q4KQ8, false>(S, row_bytes, K, x, s);
+    if (dt == UQ_Q6_K && q8k_layout<Q6KQ8>(K).total <= kLdsCap)
+        return multi ? launch_q8k_fast_m<Q6KQ8, true>(S, row_bytes, K, x, s)
+                     : launch_q8k_fast_m<Q6KQ8, false>(S, row_bytes, K, x, s);
+    const size_t lds = (size_t)K + (size_t)(K / 16) * 4 + (size_t)(K / 256) * 4;
+    if (lds > kLdsCap) return hipErrorInvalidValue;
+    for (int i = 0; i < S.n; i++) {
+        const int N = S.start[i + 1] - S.start[i];
+        if (N == 0) continue;
+        int grid = (N + TPB - 1) / TPB;
+        if (grid > num_cus() * 4) grid = num_cus() * 4;
+        hipLaunchKernelGGL(gemv_q8k_generic_kernel, dim3(grid), dim3(TPB), lds, s, dt, S.w[i], row_bytes, K, N, x,
+                           S.y[i]);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+Segs batch_segs(const WeightsView *w, int n, float *const *y) {
+    Segs S{};
+    S.n = n;
+    S.start[0] = 0;
+    for (int i = 0; i < n; i++) {
+        S.w[i] = w[i].bytes;
+        S.w2[i] = nullptr;
+        S.y[i] = y[i];
+        S.start[i + 1] = S.start[i] + w[i].dim_out;
+    }
+    return S;
 }
 
 }  // namespace
@@ -675,16 +712,11 @@ hipError_t launch_gemv(const WeightsView &w, const float *x, float *y, hipStream
 
 hipError_t launch_gemv_batch(const WeightsView *w, int n, const float *x, float *const *y, hipStream_t s) {
     static_assert(kMaxSegs == UQ_GEMV_BATCH_MAX, "segment table size");
-    Segs S{};
-    S.n = n;
-    S.start[0] = 0;
-    for (int i = 0; i < n; i++) {
-        S.w[i] = w[i].bytes;
-        S.w2[i] = nullptr;
-        S.y[i] = y[i];
-        S.start[i + 1] = S.start[i] + w[i].dim_out;
-    }
-    return launch_segs(w[0].dtype, w[0].dim_in, w[0].row_bytes, S, false, x, s);
+    return launch_segs(w[0].dtype, w[0].dim_in, w[0].row_bytes, batch_segs(w, n, y), false, x, s);
+}
+
+hipError_t launch_gemv_q8k_batch(const WeightsView *w, int n, const float *x, float *const *y, hipStream_t s) {
+    return launch_q8k_segs(w[0].dtype, w[0].dim_in, w[0].row_bytes, batch_segs(w, n, y), x, s);
 }
 
 hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, const float *x, float *h,
@@ -693,17 +725,7 @@ hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, con
 }
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out;
-    if (N == 0) return hipSuccess;
-    if (w.dtype == UQ_Q4_K && q8k_layout<Q4KQ8>(K).total <= kLdsCap) return launch_q8k_fast<Q4KQ8>(w, x, y, s);
-    if (w.dtype == UQ_Q6_K && q8k_layout<Q6KQ8>(K).total <= kLdsCap) return launch_q8k_fast<Q6KQ8>(w, x, y, s);
-    const size_t lds = (size_t)K + (size_t)(K / 16) * 4 + (size_t)(K / 256) * 4;
-    if (lds > kLdsCap) return hipErrorInvalidValue;
-    int grid = (N + TPB - 1) / TPB;
-    if (grid > num_cus() * 4) grid = num_cus() * 4;
-    hipLaunchKernelGGL(gemv_q8k_generic_kernel, dim3(grid), dim3(TPB), lds, s, w.dtype, w.bytes,
-                       w.row_bytes, K, N, x, y);
-    return hipGetLastError();
+    return launch_q8k_segs(w.dtype, w.dim_in, w.row_bytes, one_seg(w, nullptr, y), x, s);
 }
 
 }  // namespace uq

@@ -58,6 +58,8 @@ hipError_t launch_gemv(const WeightsView &w, const float *x, float *y, hipStream
 // y[i] = W[i] x for i < n (n <= UQ_GEMV_BATCH_MAX), one launch; all W[i]
 // share dtype and dim_in.
 hipError_t launch_gemv_batch(const WeightsView *w, int n, const float *x, float *const *y, hipStream_t s);
+// gemv_quant_q8k of several tensors sharing x (same dtype and dim_in).
+hipError_t launch_gemv_q8k_batch(const WeightsView *w, int n, const float *x, float *const *y, hipStream_t s);
 // h = swiglu(G x, U x); G and U share dtype and shape.
 hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u,
                                  const float *x, float *h, hipStream_t s);

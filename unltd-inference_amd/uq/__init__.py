@@ -67,6 +67,9 @@ SIGNATURES = {
     "uq_weights_info": ([_P, C.POINTER(_I), C.POINTER(_S), C.POINTER(_S), C.POINTER(_S)], _I),
     "uq_gemv": ([_P, _P, _P, _P], _I),
     "uq_gemv_batch": ([_P, _P, _S, _P, _P], _I),
+    "uq_gemv_q8k_batch": ([_P, _P, _S, _P, _P], _I),
+    "uq_ffn_swiglu_q8k": ([_P, _P, _P, _P, _P, _P, _P, _P, _P], _I),
+    "uq_swiglu_d": ([_P, _P, _P, _S, _P], _I),
     "uq_gemv_q8k": ([_P, _P, _P, _P], _I),
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
@@ -282,6 +285,23 @@ def gemv_batch(ws, d_x: DeviceArray, d_ys, stream=None) -> None:
     hs = (_P * max(n, 1))(*[w.h for w in ws])
     ys = (_P * max(n, 1))(*[y.ptr for y in d_ys])
     _check(lib().uq_gemv_batch(hs, ys, n, d_x.ptr, stream))
+
+
+def gemv_q8k_batch(ws, d_x: DeviceArray, d_ys, stream=None) -> None:
+    """d_ys[i] = gemv_quant_q8k(ws[i], d_x) for every i, in one launch."""
+    n = len(ws)
+    hs = (_P * max(n, 1))(*[w.h for w in ws])
+    ys = (_P * max(n, 1))(*[y.ptr for y in d_ys])
+    _check(lib().uq_gemv_q8k_batch(hs, ys, n, d_x.ptr, stream))
+
+
+def ffn_swiglu_q8k(gate: Weights, up: Weights, down: Weights, d_x: DeviceArray, d_g: DeviceArray,
+                   d_u: DeviceArray, d_h: DeviceArray, d_y: DeviceArray, stream=None) -> None:
+    _check(lib().uq_ffn_swiglu_q8k(gate.h, up.h, down.h, d_x.ptr, d_g.ptr, d_u.ptr, d_h.ptr, d_y.ptr, stream))
+
+
+def swiglu_d(d_out: DeviceArray, d_gate: DeviceArray, d_up: DeviceArray, n: int, stream=None) -> None:
+    _check(lib().uq_swiglu_d(d_out.ptr, d_gate.ptr, d_up.ptr, n, stream))
 
 
 def gemv_q8k(w: Weights, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
