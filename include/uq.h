@@ -52,7 +52,19 @@ typedef enum uq_status {
     UQ_ERR_DTYPE = 3,          /* unsupported dtype panic: quants.rs:446, :497-499 */
     UQ_ERR_ARG = 4,            /* null pointer, bad handle, size out of range */
     UQ_ERR_HIP = 5,            /* HIP runtime failure (message in uq_last_error) */
-    UQ_ERR_NO_DEVICE = 6       /* no usable gfx950 device */
+    UQ_ERR_NO_DEVICE = 6,      /* no usable gfx950 device */
+    UQ_ERR_TOKEN = 7,          /* token id >= vocab: LoadError::corrupt of embed, min_forward.rs:168-173 */
+    /* GGUF loader (uq_gguf.h); LoadError variants of unltd-core/src/lib.rs:19-96 */
+    UQ_ERR_FILE = 8,           /* BadFile: corrupt or truncated file */
+    UQ_ERR_MAGIC = 9,          /* BadMagic */
+    UQ_ERR_VERSION = 10,       /* UnsupportedVersion */
+    UQ_ERR_TENSOR_BOUNDS = 11, /* TensorOutOfBounds */
+    UQ_ERR_TENSOR_OVERLAP = 12,/* TensorOverlap */
+    UQ_ERR_TENSOR_ALIGN = 13,  /* MisalignedTensor */
+    UQ_ERR_GGML_TYPE = 14,     /* UnknownGgmlType */
+    UQ_ERR_MISSING_TENSOR = 15,/* MissingTensor */
+    UQ_ERR_ELEMENT_COUNT = 16, /* ElementCount */
+    UQ_ERR_IO = 17             /* Io */
 } uq_status;
 
 /* Q8_K activation block, quants.rs:235-242 ({f32 d; i8 qs[256]; i32 bsums[16]}). */
@@ -185,6 +197,17 @@ uq_status uq_swiglu_d(float *d_out, const float *d_gate, const float *d_up, size
 /* Device f32 dequantization of a whole handle into d_out[dim_out*dim_in]
  * (dequantize_q4_k semantics, bit-exact; Q6_K/Q8_0 closed forms). */
 uq_status uq_dequantize(uq_weights w, float *d_out, void *stream);
+
+/* Embedding lookup, embed (min_forward.rs:160-184): for r < n_tokens,
+ * d_out[r*dim_in .. (r+1)*dim_in) = row tokens[r] of w, copied (F32) or
+ * dequantized bit-exactly as dequantize_q4_k (Q4_K). Q6_K / Q8_0 rows use
+ * the closed forms of uq_dequantize_q6_k / _q8_0 (the reference refuses them
+ * when it opens the model). tokens is a HOST array: every id is checked
+ * against w's dim_out (the vocabulary) before any launch, and the first id
+ * out of range fails with UQ_ERR_TOKEN, as the reference returns an error
+ * rather than clamping. The ids travel in the kernel arguments (256 per
+ * launch), so the call allocates nothing. n_tokens == 0 is a no-op. */
+uq_status uq_embed(uq_weights w, const uint32_t *tokens, size_t n_tokens, float *d_out, void *stream);
 
 /* ------------------------------------------------------------------------
  * Device memory and stream plumbing for callers without their own HIP

@@ -1,6 +1,7 @@
-"""libuq.so without a GPU: it loads, exports every symbol include/uq.h
-declares, refuses bad arguments with the reference's panic classes before
+"""libuq.so without a GPU: it loads, exports every symbol include/*.h
+declare, refuses bad arguments with the reference's panic classes before
 touching a device, and fails loudly (no CPU fallback) when no GPU exists."""
+import glob
 import os
 import re
 
@@ -11,13 +12,15 @@ import pytest
 
 import uq
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "uq.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include")
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(uq_\w+)\s*\(", text)))
+    names = set()
+    for h in sorted(glob.glob(os.path.join(INCLUDE, "*.h"))):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(uq_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():

@@ -354,6 +354,91 @@ def test_device_dequantize_handle():
     assert_bitwise(d.download(np.float32, K * N), ref, "device dequantize")
 
 
+# ------------------------------------------------- embedding GET_ROWS (f4)
+
+def _embed_ref(dtype, w, K, tokens):
+    """embed (min_forward.rs:160-184) restated with the oracle: each token's
+    row dequantized by itself (F32 rows copied)."""
+    rb = uq.row_bytes(dtype, K)
+    out = np.zeros((len(tokens), K), np.float32)
+    for r, t in enumerate(tokens):
+        row = w[t * rb:(t + 1) * rb]
+        if dtype == S.F32:
+            out[r] = row.view(np.float32)
+        else:
+            out[r] = O.dequantize(dtype, row, K)
+    return out
+
+
+@pytest.mark.parametrize("dtype,K,V,n", [(S.Q4_K, 4096, 1000, 300), (S.Q4_K, 256, 3, 7), (S.F32, 1000, 50, 9),
+                                         (S.Q6_K, 4096, 64, 20), (S.Q8_0, 2048, 64, 20)])
+def test_embed_rows_bit_exact(dtype, K, V, n):
+    rng = np.random.default_rng(K + V + n)
+    if dtype == S.F32:
+        w = rng.standard_normal(V * K).astype(np.float32).view(np.uint8)
+    else:
+        w = S.weights(dtype, V, K, seed=V)
+    # first, last, repeated ids and a run that crosses the 256-id launch chunk
+    tokens = np.concatenate([[0, V - 1, 1 % V, 1 % V], rng.integers(0, V, max(0, n - 4))]).astype(np.uint32)[:n]
+    W = uq.Weights(w, dtype, K, V)
+    d = uq.DeviceArray(4 * n * K)
+    uq.embed(W, tokens, d)
+    uq.synchronize()
+    got = d.download(np.float32, n * K).reshape(n, K)
+    assert_bitwise(got, _embed_ref(dtype, w, K, tokens), f"embed dtype={dtype} K={K} n={n}")
+
+
+def test_embed_refuses_out_of_vocab_before_writing():
+    K, V = 256, 10
+    w = S.weights(S.Q4_K, V, K, seed=2)
+    W = uq.Weights(w, S.Q4_K, K, V)
+    d = uq.DeviceArray(4 * 3 * K)
+    sentinel = np.full(3 * K, 7.0, np.float32)
+    d.upload(sentinel)
+    with pytest.raises(uq.UqError) as e:
+        uq.embed(W, [1, V, 2], d)
+    assert e.value.kind == "TOKEN" and "10" in str(e.value)
+    uq.embed(W, [], d)  # no tokens: no-op
+    uq.synchronize()
+    assert_bitwise(d.download(np.float32, 3 * K), sentinel, "untouched after refusal")
+
+
+# --------------------------------------------------- GGUF -> HBM loader (f2)
+
+def test_gguf_file_to_hbm_gemv_and_embed(tmp_path):
+    """A GGUF file written byte by byte, mapped by uq_gguf_open, its tensors
+    uploaded unchanged: the GEMVs and the embedding lookup on the uploaded
+    handles equal the oracle on the file's bytes."""
+    from uq import gguf as G
+    K, V, N = 4096, 512, 1024
+    emb = S.weights(S.Q4_K, V, K, seed=41)
+    head = S.weights(S.Q6_K, V, K, seed=42)
+    up = S.weights(S.Q4_K, N, K, seed=43)
+    path = tmp_path / "tiny.gguf"
+    path.write_bytes(G.write([("general.architecture", G.STRING, "qwen35")],
+                             [("token_embd.weight", [K, V], S.Q4_K, emb), ("output.weight", [K, V], S.Q6_K, head),
+                              ("blk.0.ffn_up.weight", [K, N], S.Q4_K, up)]))
+    with G.Gguf.open(path) as g:
+        assert g.check("blk.0.ffn_up.weight", K * N, [uq.DType.Q4K]) == uq.DType.Q4K
+        Wh, Wu, We = g.upload("output.weight"), g.upload("blk.0.ffn_up.weight"), g.upload("token_embd.weight")
+    assert (Wh.dtype, Wh.dim_in, Wh.dim_out) == (S.Q6_K, K, V) and (Wu.dim_in, Wu.dim_out) == (K, N)
+    x = S.activations(K, seed=44)
+    dx = uq.DeviceArray.from_numpy(x)
+    for W, w, n in ((Wh, head, V), (Wu, up, N)):
+        dy = uq.DeviceArray(4 * n)
+        uq.gemv_q8k(W, dx, dy)
+        uq.synchronize()
+        ref = np.zeros(n, np.float32)
+        O.gemv_quant_q8k(ref, x, w, K, n, W.dtype, nthreads=NT)
+        assert_bitwise(dy.download(np.float32, n), ref, f"gguf-loaded gemv_q8k dtype={W.dtype}")
+    toks = np.array([3, V - 1, 0, 3], np.uint32)
+    de = uq.DeviceArray(4 * len(toks) * K)
+    uq.embed(We, toks, de)
+    uq.synchronize()
+    assert_bitwise(de.download(np.float32, len(toks) * K).reshape(len(toks), K),
+                   _embed_ref(S.Q4_K, emb, K, toks), "gguf-loaded embed")
+
+
 def test_device_api_errors():
     w = S.weights(S.Q8_0, 4, 64, seed=1)
     W = uq.Weights(w, uq.DType.Q8_0, 64, 4)

@@ -22,6 +22,20 @@ uq_status fail(uq_status s, const char *fmt, ...) {
     return s;
 }
 
+}  // namespace
+
+uq_status uq::set_error(uq_status s, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return s;
+}
+
+namespace {
+
 uq_status hip_fail(hipError_t e, const char *what) {
     return fail(UQ_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
@@ -229,6 +243,17 @@ const char *uq_status_name(uq_status s) {
     case UQ_ERR_ARG: return "UQ_ERR_ARG";
     case UQ_ERR_HIP: return "UQ_ERR_HIP";
     case UQ_ERR_NO_DEVICE: return "UQ_ERR_NO_DEVICE";
+    case UQ_ERR_TOKEN: return "UQ_ERR_TOKEN";
+    case UQ_ERR_FILE: return "UQ_ERR_FILE";
+    case UQ_ERR_MAGIC: return "UQ_ERR_MAGIC";
+    case UQ_ERR_VERSION: return "UQ_ERR_VERSION";
+    case UQ_ERR_TENSOR_BOUNDS: return "UQ_ERR_TENSOR_BOUNDS";
+    case UQ_ERR_TENSOR_OVERLAP: return "UQ_ERR_TENSOR_OVERLAP";
+    case UQ_ERR_TENSOR_ALIGN: return "UQ_ERR_TENSOR_ALIGN";
+    case UQ_ERR_GGML_TYPE: return "UQ_ERR_GGML_TYPE";
+    case UQ_ERR_MISSING_TENSOR: return "UQ_ERR_MISSING_TENSOR";
+    case UQ_ERR_ELEMENT_COUNT: return "UQ_ERR_ELEMENT_COUNT";
+    case UQ_ERR_IO: return "UQ_ERR_IO";
     default: return "UQ_ERR_UNKNOWN";
     }
 }
@@ -536,6 +561,20 @@ uq_status uq_dequantize(uq_weights wh, float *d_out, void *stream) {
     }
     UQ_HIP(uq::launch_dequant(w->dtype, w->d_bytes, w->dim_in * w->dim_out, d_out, (hipStream_t)stream),
            "dequantize launch");
+    return UQ_OK;
+}
+
+uq_status uq_embed(uq_weights wh, const uint32_t *tokens, size_t n_tokens, float *d_out, void *stream) {
+    uq_weights_s *w = handle(wh);
+    if (!w) return fail(UQ_ERR_ARG, "embed: invalid handle");
+    if (n_tokens == 0) return UQ_OK;
+    if (!tokens || !d_out) return fail(UQ_ERR_ARG, "embed: null pointer");
+    for (size_t r = 0; r < n_tokens; r++)
+        if (tokens[r] >= w->dim_out)
+            return fail(UQ_ERR_TOKEN, "embed: token %u out of the vocabulary (0..%zu)", tokens[r], w->dim_out);
+    UQ_HIP(uq::launch_embed(w->dtype, w->d_bytes, w->row_bytes, (int)w->dim_in, tokens, n_tokens, d_out,
+                            (hipStream_t)stream),
+           "embed launch");
     return UQ_OK;
 }
 

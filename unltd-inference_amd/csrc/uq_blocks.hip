@@ -87,46 +87,75 @@ __global__ void unpack_q8_0_kernel(const uint8_t *__restrict__ w, size_t nblocks
 
 // dequantize_q4_k (quants.rs:534-567): d1 = d*sc, m1 = min*m in f32, then
 // y = d1*q - m1; d1*q is exact (<= 21 significant bits) so one rounding.
-__global__ void dequant_q4k_kernel(const uint8_t *__restrict__ w, size_t n, float *__restrict__ out) {
-    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n;
-         t += (size_t)gridDim.x * blockDim.x) {
-        const size_t b = t >> 8;
-        const int e = (int)(t & 255), g = e >> 5;
-        const uint8_t *blk = w + b * BQ4K;
-        const float dd = f16_bits_exact(f16_at(blk));
-        const float mn = f16_bits_exact(f16_at(blk + 2));
-        uint32_t sc, m;
-        scale_min_k4(blk + 4, g, sc, m);
-        const float d1 = __fmul_rn(dd, (float)sc);
-        const float m1 = __fmul_rn(mn, (float)m);
-        const uint8_t byte = blk[16 + 32 * (g >> 1) + (e & 31)];
-        const uint32_t nib = (g & 1) ? (byte >> 4) : (byte & 0xF);
-        out[t] = __fsub_rn(__fmul_rn(d1, (float)nib), m1);
-    }
+// Element e (0..255) of the block at blk.
+__device__ __forceinline__ float deq_q4k(const uint8_t *blk, int e) {
+    const int g = e >> 5;
+    const float dd = f16_bits_exact(f16_at(blk));
+    const float mn = f16_bits_exact(f16_at(blk + 2));
+    uint32_t sc, m;
+    scale_min_k4(blk + 4, g, sc, m);
+    const float d1 = __fmul_rn(dd, (float)sc);
+    const float m1 = __fmul_rn(mn, (float)m);
+    const uint8_t byte = blk[16 + 32 * (g >> 1) + (e & 31)];
+    const uint32_t nib = (g & 1) ? (byte >> 4) : (byte & 0xF);
+    return __fsub_rn(__fmul_rn(d1, (float)nib), m1);
 }
 
 // Q6_K: d*(sc*q), the exact product of dot_q6_k (quants.rs:195).
+__device__ __forceinline__ float deq_q6k(const uint8_t *blk, int e) {
+    const uint8_t byte = blk[64 * (e / 128) + (e % 64)];
+    const int nib = ((e / 64) % 2 == 0) ? (byte & 0xF) : (byte >> 4);
+    const int hi2 = (blk[128 + (e % 32) + 32 * (e / 128)] >> (2 * ((e % 128) / 32))) & 3;
+    const int q = (nib | (hi2 << 4)) - 32;
+    const float sc = (float)(int8_t)blk[192 + e / 16];
+    return __fmul_rn(f16_bits_exact(f16_at(blk + 208)), __fmul_rn(sc, (float)q));
+}
+
+// Q8_0 (GGUF closed form): d*q, exact. Element e (0..31) of the block at blk.
+__device__ __forceinline__ float deq_q80(const uint8_t *blk, int e) {
+    return __fmul_rn(f16_bits_exact(f16_at(blk)), (float)(int8_t)blk[2 + e]);
+}
+
+// Element e of a row of dtype DT (e < dim_in).
+template <uq_dtype DT>
+__device__ __forceinline__ float deq_row(const uint8_t *row, int e) {
+    if constexpr (DT == UQ_Q4_K) return deq_q4k(row + (size_t)(e >> 8) * BQ4K, e & 255);
+    else if constexpr (DT == UQ_Q6_K) return deq_q6k(row + (size_t)(e >> 8) * BQ6K, e & 255);
+    else if constexpr (DT == UQ_Q8_0) return deq_q80(row + (size_t)(e >> 5) * BQ8_0, e & 31);
+    else return ((const float *)row)[e];
+}
+
+__global__ void dequant_q4k_kernel(const uint8_t *__restrict__ w, size_t n, float *__restrict__ out) {
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n;
+         t += (size_t)gridDim.x * blockDim.x)
+        out[t] = deq_q4k(w + (t >> 8) * BQ4K, (int)(t & 255));
+}
+
 __global__ void dequant_q6k_kernel(const uint8_t *__restrict__ w, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n;
-         t += (size_t)gridDim.x * blockDim.x) {
-        const size_t b = t >> 8;
-        const int e = (int)(t & 255);
-        const uint8_t *blk = w + b * BQ6K;
-        const uint8_t byte = blk[64 * (e / 128) + (e % 64)];
-        const int nib = ((e / 64) % 2 == 0) ? (byte & 0xF) : (byte >> 4);
-        const int hi2 = (blk[128 + (e % 32) + 32 * (e / 128)] >> (2 * ((e % 128) / 32))) & 3;
-        const int q = (nib | (hi2 << 4)) - 32;
-        const float sc = (float)(int8_t)blk[192 + e / 16];
-        out[t] = __fmul_rn(f16_bits_exact(f16_at(blk + 208)), __fmul_rn(sc, (float)q));
-    }
+         t += (size_t)gridDim.x * blockDim.x)
+        out[t] = deq_q6k(w + (t >> 8) * BQ6K, (int)(t & 255));
 }
 
 __global__ void dequant_q8_0_kernel(const uint8_t *__restrict__ w, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n;
-         t += (size_t)gridDim.x * blockDim.x) {
-        const uint8_t *blk = w + (t >> 5) * BQ8_0;
-        out[t] = __fmul_rn(f16_bits_exact(f16_at(blk)), (float)(int8_t)blk[2 + (t & 31)]);
-    }
+         t += (size_t)gridDim.x * blockDim.x)
+        out[t] = deq_q80(w + (t >> 5) * BQ8_0, (int)(t & 31));
+}
+
+// Embedding lookup (embed, min_forward.rs:160-184): row r of out is row
+// tok.id[r] of w, dequantized. The ids travel in the kernel arguments (one
+// chunk of up to kEmbedChunk tokens per launch, validated by the host), so
+// the lookup needs no device buffer of its own. grid = (ceil(dim_in/256),
+// tokens in the chunk); one thread per output element.
+template <uq_dtype DT>
+__global__ void __launch_bounds__(TPB)
+embed_kernel(const uint8_t *__restrict__ w, size_t row_bytes, int dim_in, EmbedIds tok, float *__restrict__ out) {
+    const int e = blockIdx.x * TPB + threadIdx.x;
+    if (e >= dim_in) return;
+    const int r = blockIdx.y;
+    const uint8_t *row = w + (size_t)tok.id[r] * row_bytes;
+    out[(size_t)r * dim_in + e] = deq_row<DT>(row, e);
 }
 
 __global__ void f16_kernel(const uint16_t *__restrict__ h, size_t n, float *__restrict__ out) {
@@ -232,6 +261,27 @@ hipError_t launch_dequant(uq_dtype dt, const uint8_t *w, size_t n, float *out, h
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_embed(uq_dtype dt, const uint8_t *w, size_t row_bytes, int dim_in, const uint32_t *ids,
+                        size_t n, float *out, hipStream_t s) {
+    for (size_t c = 0; c < n; c += kEmbedChunk) {
+        const size_t m = n - c < (size_t)kEmbedChunk ? n - c : (size_t)kEmbedChunk;
+        EmbedIds tok;
+        for (size_t i = 0; i < m; i++) tok.id[i] = ids[c + i];
+        const dim3 g((unsigned)((dim_in + TPB - 1) / TPB), (unsigned)m), b(TPB);
+        float *o = out + c * (size_t)dim_in;
+        switch (dt) {
+        case UQ_F32: hipLaunchKernelGGL(embed_kernel<UQ_F32>, g, b, 0, s, w, row_bytes, dim_in, tok, o); break;
+        case UQ_Q4_K: hipLaunchKernelGGL(embed_kernel<UQ_Q4_K>, g, b, 0, s, w, row_bytes, dim_in, tok, o); break;
+        case UQ_Q6_K: hipLaunchKernelGGL(embed_kernel<UQ_Q6_K>, g, b, 0, s, w, row_bytes, dim_in, tok, o); break;
+        case UQ_Q8_0: hipLaunchKernelGGL(embed_kernel<UQ_Q8_0>, g, b, 0, s, w, row_bytes, dim_in, tok, o); break;
+        default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_f16_to_f32(const uint16_t *h, size_t n, float *out, hipStream_t s) {

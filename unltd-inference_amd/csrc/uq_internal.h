@@ -31,6 +31,9 @@ constexpr int BQ4K = 144;
 constexpr int BQ6K = 210;
 constexpr int BQ8_0 = 34;
 
+// Records the calling thread's error message (uq_last_error) and returns s.
+uq_status set_error(uq_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
 struct WeightsView {
     const uint8_t *bytes;
     uq_dtype dtype;
@@ -45,6 +48,13 @@ inline WeightsView view(const uq_weights_s &w) {
 // ---- launchers (each returns the launch error; no allocation) -------------
 hipError_t launch_unpack(uq_dtype dt, const uint8_t *w, size_t nblocks, void *q,
                          void *sc, uint8_t *m, float *d, float *dmin, hipStream_t s);
+// Token ids of one embedding launch, passed by value in the kernel arguments.
+constexpr int kEmbedChunk = 256;
+struct EmbedIds {
+    uint32_t id[kEmbedChunk];
+};
+hipError_t launch_embed(uq_dtype dt, const uint8_t *w, size_t row_bytes, int dim_in, const uint32_t *ids,
+                        size_t n, float *out, hipStream_t s);
 hipError_t launch_dequant(uq_dtype dt, const uint8_t *w, size_t nelem, float *out,
                           hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t *h, size_t n, float *out, hipStream_t s);

@@ -30,7 +30,9 @@ class DType(enum.IntEnum):
     Q6K = 14
 
 
-STATUS = {0: "OK", 1: "LEN", 2: "BLOCK_MULTIPLE", 3: "DTYPE", 4: "ARG", 5: "HIP", 6: "NO_DEVICE"}
+STATUS = {0: "OK", 1: "LEN", 2: "BLOCK_MULTIPLE", 3: "DTYPE", 4: "ARG", 5: "HIP", 6: "NO_DEVICE", 7: "TOKEN",
+          8: "FILE", 9: "MAGIC", 10: "VERSION", 11: "TENSOR_BOUNDS", 12: "TENSOR_OVERLAP", 13: "TENSOR_ALIGN",
+          14: "GGML_TYPE", 15: "MISSING_TENSOR", 16: "ELEMENT_COUNT", 17: "IO"}
 
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i4", (16,))], align=True)
 assert Q8K_DTYPE.itemsize == 324
@@ -74,6 +76,7 @@ SIGNATURES = {
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
     "uq_dequantize": ([_P, _P, _P], _I),
+    "uq_embed": ([_P, _P, _S, _P, _P], _I),
     "uq_device_count": ([C.POINTER(_I)], _I),
     "uq_device_name": ([C.c_char_p, _S], _I),
     "uq_malloc": ([C.POINTER(_P), _S], _I),
@@ -82,6 +85,22 @@ SIGNATURES = {
     "uq_memcpy_dtoh": ([_P, _P, _S, _P], _I),
     "uq_memcpy_dtod": ([_P, _P, _S, _P], _I),
     "uq_stream_synchronize": ([_P], _I),
+    # include/uq_gguf.h
+    "uq_gguf_open": ([C.c_char_p, C.POINTER(_P)], _I),
+    "uq_gguf_parse": ([_P, _S, C.POINTER(_P)], _I),
+    "uq_gguf_close": ([_P], _I),
+    "uq_gguf_header": ([_P, _P, _P, _P, _P, _P], _I),
+    "uq_gguf_tensor_at": ([_P, C.c_uint64, _P], _I),
+    "uq_gguf_find": ([_P, C.c_char_p, _P], _I),
+    "uq_gguf_tensor_bytes": ([_P, C.c_char_p, _P, _P], _I),
+    "uq_gguf_tensor_checked": ([_P, C.c_char_p, C.c_uint64, _P, _P], _I),
+    "uq_gguf_check": ([_P, C.c_char_p, C.c_uint64, C.c_uint64, _P], _I),
+    "uq_gguf_upload": ([_P, C.c_char_p, C.POINTER(_P)], _I),
+    "uq_gguf_kv_at": ([_P, C.c_uint64, _P], _I),
+    "uq_gguf_kv_find": ([_P, C.c_char_p, _P], _I),
+    "uq_gguf_kv_string": ([_P, C.c_uint64, C.c_uint64, _P, _P], _I),
+    "uq_gguf_type_blocksize": ([C.c_uint32, _P, _P], _I),
+    "uq_gguf_type_name": ([C.c_uint32, C.c_char_p, _S], _I),
 }
 
 
@@ -102,7 +121,7 @@ def lib():
 
 def _check(rc: int):
     if rc != 0:
-        raise UqError(rc, lib().uq_last_error().decode())
+        raise UqError(rc, lib().uq_last_error().decode("utf-8", "replace"))
 
 
 def _ptr(a: np.ndarray | None):
@@ -260,6 +279,15 @@ class Weights:
         _check(lib().uq_weights_upload(C.byref(h), _ptr(b), b.size, int(dtype), dim_in, dim_out))
         self.h, self.dtype, self.dim_in, self.dim_out, self.nbytes = h, int(dtype), dim_in, dim_out, b.size
 
+    @classmethod
+    def from_handle(cls, h: C.c_void_p) -> "Weights":
+        """Adopt a handle made by the library (e.g. uq_gguf_upload)."""
+        self = cls.__new__(cls)
+        dt, di, do, nb = C.c_int(), C.c_size_t(), C.c_size_t(), C.c_size_t()
+        _check(lib().uq_weights_info(h, C.byref(dt), C.byref(di), C.byref(do), C.byref(nb)))
+        self.h, self.dtype, self.dim_in, self.dim_out, self.nbytes = h, dt.value, di.value, do.value, nb.value
+        return self
+
     def free(self):
         if self.h:
             _check(lib().uq_weights_free(self.h))
@@ -319,6 +347,12 @@ def ffn_swiglu(gate: Weights, up: Weights, down: Weights, d_x: DeviceArray, d_h:
 
 def dequantize(w: Weights, d_out: DeviceArray, stream=None) -> None:
     _check(lib().uq_dequantize(w.h, d_out.ptr, stream))
+
+
+def embed(w: Weights, tokens, d_out: DeviceArray, stream=None) -> None:
+    """min_forward.rs:160-184: rows tokens[r] of w into d_out[r*dim_in:]."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    _check(lib().uq_embed(w.h, t.ctypes.data_as(C.c_void_p), t.size, d_out.ptr, stream))
 
 
 def synchronize(stream=None) -> None:
