@@ -49,11 +49,18 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
 // ---------------------------------------------------------------------------
 // Wave64 reductions with DPP (row_mirror / row_bcast); the result is
 // returned to every lane. Summation tree is fixed, so results are
-// deterministic.
+// deterministic. Every DPP read uses bound_ctrl (a lane whose source is out
+// of range or inactive reads 0, which is what the old value 0 gave), so the
+// compiler folds each move into the consuming add/max as one DPP
+// instruction.
 // ---------------------------------------------------------------------------
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xF, 0xF, true);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -66,6 +73,21 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Maximum over each aligned group of 32 lanes, returned to all of them:
+// DPP within 16-lane rows (xor 1, xor 2, then half-mirror and mirror, which
+// act as xor 4 and xor 8 once quads and halves are uniform), then
+// v_permlane16_swap pairs rows 0-1 and 2-3. No LDS round trip.
+// Operates on the bit patterns of non-negative floats, which order like
+// unsigned integers (NaN is outside the callers' contract).
+__device__ __forceinline__ uint32_t group32_max_bits(uint32_t v) {
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x140>(v));
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return max((uint32_t)r[0], (uint32_t)r[1]);
+}
+
 // xor-shuffle within aligned groups of 2/4/8 lanes (quad_perm / half mirror)
 __device__ __forceinline__ float group8_max(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
@@ -75,7 +97,7 @@ __device__ __forceinline__ float group8_max(float v) {
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp_int(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
 __device__ __forceinline__ int group4_sum_i(int v) {
     v += dpp_int<0xB1>(v);
@@ -86,8 +108,8 @@ __device__ __forceinline__ int group4_sum_i(int v) {
 // f64 DPP: the two halves move together
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ double dpp_d(double v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xF, false);
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xF, true);
     return __hiloint2double(hi, lo);
 }
 
@@ -147,10 +169,9 @@ __device__ __forceinline__ double reduce4_rows(const double (&v)[4]) {
 // ---------------------------------------------------------------------------
 // Activation prep into the layout of uq_policies.h (XView): one thread per
 // element-dword w (4 activations); a run of 128 activations is one aligned
-// group of 32 lanes. The loop is padded to whole runs so every lane of a run
-// takes part in its reductions; padding elements are zero and not stored.
-// Error per activation <= s/2 <= max|x_run| * 2^-30. Non-finite activations
-// are outside this path's contract (outputs unspecified).
+// group of 32 lanes. Error per activation <= s/2 <= max|x_run| * 2^-30.
+// Non-finite activations are outside this path's contract (outputs
+// unspecified).
 // ---------------------------------------------------------------------------
 struct XLayout {
     uint32_t *xq;
@@ -160,7 +181,6 @@ struct XLayout {
     int NT;
 };
 
-__device__ __forceinline__ uint32_t digit(int v) { return (uint32_t)v & 0xFFu; }
 
 // The first element-dword of each thread can be loaded early (prep_x_first)
 // so its latency overlaps the kernel's first weight loads.
@@ -169,56 +189,77 @@ __device__ __forceinline__ float4 prep_x_first(const float *__restrict__ x, int 
     return w < (K >> 2) ? *(const float4 *)(x + 4 * w) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// One element-dword w (activations f, zero beyond K) into the layout.
+// X = rint(x * 2^(30-ex)) is split into signed base-256 digits with the bias
+// trick: the bytes of X + 0x80808080 are the digits plus 128 (|X| <= 2^30, so
+// the sum neither wraps nor borrows), a 4x4 byte transpose (v_perm) turns the
+// four elements' bytes into the four planes, and xor 0x80 per byte removes
+// the bias.
 template <class F>
+__device__ __forceinline__ void prep_dword(int w, int nw, float4 f, XLayout L) {
+    const bool in = w < nw;
+    const uint32_t ab = max(max(__float_as_uint(f.x) & 0x7FFFFFFFu, __float_as_uint(f.y) & 0x7FFFFFFFu),
+                            max(__float_as_uint(f.z) & 0x7FFFFFFFu, __float_as_uint(f.w) & 0x7FFFFFFFu));
+    const float am = __uint_as_float(group32_max_bits(ab));
+    const int ex = am > 0.0f ? __builtin_amdgcn_frexp_expf(am) : 0;  // am = m * 2^ex, m in [0.5, 1)
+    const int X0 = (int)rintf(ldexpf(f.x, 30 - ex)), X1 = (int)rintf(ldexpf(f.y, 30 - ex));
+    const int X2 = (int)rintf(ldexpf(f.z, 30 - ex)), X3 = (int)rintf(ldexpf(f.w, 30 - ex));
+    const uint32_t u0 = (uint32_t)X0 + 0x80808080u, u1 = (uint32_t)X1 + 0x80808080u;
+    const uint32_t u2 = (uint32_t)X2 + 0x80808080u, u3 = (uint32_t)X3 + 0x80808080u;
+    const uint32_t a_lo = __builtin_amdgcn_perm(u1, u0, 0x05010400u), a_hi = __builtin_amdgcn_perm(u1, u0, 0x07030602u);
+    const uint32_t b_lo = __builtin_amdgcn_perm(u3, u2, 0x05010400u), b_hi = __builtin_amdgcn_perm(u3, u2, 0x07030602u);
+    const uint32_t pl[4] = {__builtin_amdgcn_perm(b_lo, a_lo, 0x05040100u) ^ 0x80808080u,
+                            __builtin_amdgcn_perm(b_lo, a_lo, 0x07060302u) ^ 0x80808080u,
+                            __builtin_amdgcn_perm(b_hi, a_hi, 0x05040100u) ^ 0x80808080u,
+                            __builtin_amdgcn_perm(b_hi, a_hi, 0x07060302u) ^ 0x80808080u};
+    const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
+    int t, i;
+    F::xmap(w, t, i);
+    if (in) {
+        uint32_t *dst = L.xq + xq_index(0, i, t, L.NT);
+        const size_t plane = (size_t)16 * L.NT;  // dwords between planes
+        for (int q = 0; q < 4; q++) dst[q * plane] = pl[q];
+    }
+    double xs = ((double)X0 + (double)X1) + ((double)X2 + (double)X3);
+    xs = group8_sum_d(xs);
+    if (in && (w & 7) == 0) L.gsum[w >> 3] = xs * (double)s;
+    if (in && (w & 31) == 0) L.scale[w >> 5] = s;
+    if constexpr (F::kAux) {
+        int P[4];
+        for (int q = 0; q < 4; q++) P[q] = group4_sum_i(sdot4(pl[q], 0x01010101u, 0));
+        if (in && (w & 3) == 0) {
+            int lo, hi;
+            F::aux_of(P, lo, hi);
+            L.aux[aux_index(i >> 2, t, L.NT)] = lo;
+            L.aux[aux_index(4 + (i >> 2), t, L.NT)] = hi;
+        }
+    }
+}
+
+// The loop is padded to whole runs so every lane of a run takes part in its
+// reductions; padding elements are zero and not stored. A thread's
+// element-dwords are loaded CHUNK at a time, all before any is processed, so
+// their latencies overlap instead of adding up.
+// TPB is the workgroup size (a multiple of 64).
+template <class F, int TPB, int CHUNK = 4>
 __device__ __forceinline__ void prep_x(const float *__restrict__ x, int K, XLayout L, float4 first) {
     const int nw = K >> 2;
     const int nw_pad = (nw + 31) & ~31;
-    for (int w = threadIdx.x; w < ((nw_pad + blockDim.x - 1) / blockDim.x) * blockDim.x; w += blockDim.x) {
-        const bool in = w < nw;
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (w == (int)threadIdx.x) {
-            v[0] = first.x;
-            v[1] = first.y;
-            v[2] = first.z;
-            v[3] = first.w;
-        } else if (in) {
-            for (int i = 0; i < 4; i++) v[i] = x[4 * w + i];
+    const int iters = (nw_pad + TPB - 1) / TPB;
+    for (int base = 0; base < iters; base += CHUNK) {
+        float4 v[CHUNK];
+#pragma unroll
+        for (int j = 0; j < CHUNK; j++) {
+            const int w = threadIdx.x + (base + j) * TPB;
+            v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (base + j == 0)
+                v[j] = first;
+            else if (base + j < iters && w < nw)
+                v[j] = *(const float4 *)(x + 4 * w);
         }
-        float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        for (int off = 16; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
-        int ex = 0;
-        if (am > 0.0f) (void)frexpf(am, &ex);
-        uint32_t pl[4] = {0, 0, 0, 0};
-        double xs = 0.0;
-        for (int i = 0; i < 4; i++) {
-            const int X = am > 0.0f ? (int)rintf(ldexpf(v[i], 30 - ex)) : 0;
-            const int d0 = (int)(int8_t)(X & 0xFF), X1 = (X - d0) >> 8;
-            const int d1 = (int)(int8_t)(X1 & 0xFF), X2 = (X1 - d1) >> 8;
-            const int d2 = (int)(int8_t)(X2 & 0xFF), d3 = (X2 - d2) >> 8;
-            pl[0] |= digit(d0) << (8 * i);
-            pl[1] |= digit(d1) << (8 * i);
-            pl[2] |= digit(d2) << (8 * i);
-            pl[3] |= digit(d3) << (8 * i);
-            xs += (double)X;
-        }
-        const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
-        int t, i;
-        F::xmap(w, t, i);
-        if (in)
-            for (int q = 0; q < 4; q++) L.xq[xq_index(q, i, t, L.NT)] = pl[q];
-        xs = group8_sum_d(xs);
-        if (in && (w & 7) == 0) L.gsum[w >> 3] = xs * (double)s;
-        if (in && (w & 31) == 0) L.scale[w >> 5] = s;
-        if constexpr (F::kAux) {
-            int P[4];
-            for (int q = 0; q < 4; q++) P[q] = group4_sum_i(sdot4(pl[q], 0x01010101u, 0));
-            if (in && (w & 3) == 0) {
-                int lo, hi;
-                F::aux_of(P, lo, hi);
-                L.aux[aux_index(i >> 2, t, L.NT)] = lo;
-                L.aux[aux_index(4 + (i >> 2), t, L.NT)] = hi;
-            }
-        }
+#pragma unroll
+        for (int j = 0; j < CHUNK; j++)
+            if (base + j < iters) prep_dword<F>(threadIdx.x + (base + j) * TPB, nw, v[j], L);
     }
 }
 

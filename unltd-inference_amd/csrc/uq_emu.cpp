@@ -111,25 +111,43 @@ double row_sum64(const double *v) {
     return t[0];
 }
 
+// A row is reduced as the kernel that runs it does: lane sums over the
+// lane's tasks, then row_sum64 (gemv_kernel, gemv_kt_kernel); or, when the
+// row runs K-split (kslices), row_sum64 per slice of 64 tasks and the slice
+// sums added in slice order (gemv_ks_kernel).
 template <class F>
 void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int K, int N) {
     const HostLayout<F> L = prep_layout<F>(x, K);
     const XView PV = L.view();
     const int ntask = F::ntasks(K);
+    const int ks = kslices<F>(K);
     for (int row = 0; row < N; row++) {
         const uint8_t *R = W + (size_t)row * row_bytes;
         double part[64];
-        for (int lane = 0; lane < 64; lane++) {
-            const typename F::LC c = F::lane_consts(lane);
-            double g = 0.0;
-            for (int t = lane; t < ntask; t += 64) {
-                typename F::XS xs;
-                F::load_x(xs, PV, t, c);
-                g += F::dot(F::load_w(R, t, c), xs, c);
+        auto lane_sums = [&](int t0, int t1, int step) {
+            for (int lane = 0; lane < 64; lane++) {
+                const typename F::LC c = F::lane_consts(lane);
+                double g = 0.0;
+                for (int t = t0 + lane; t < t1; t += step) {
+                    typename F::XS xs;
+                    F::load_x(xs, PV, t, c);
+                    g += F::dot(F::load_w(R, t, c), xs, c);
+                }
+                part[lane] = g;
             }
-            part[lane] = g;
+        };
+        if (ks) {
+            double acc = 0.0;
+            for (int s = 0; s < ks; s++) {
+                lane_sums(64 * s, 64 * s + 64 < ntask ? 64 * s + 64 : ntask, 64);
+                const double p = row_sum64(part);
+                acc = s == 0 ? p : acc + p;
+            }
+            y[row] = (float)acc;
+        } else {
+            lane_sums(0, ntask, 64);
+            y[row] = (float)row_sum64(part);
         }
-        y[row] = (float)row_sum64(part);
     }
 }
 

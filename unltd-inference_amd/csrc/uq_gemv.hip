@@ -26,7 +26,6 @@ namespace {
 
 constexpr int WAVES = 4;
 constexpr int TPB = 64 * WAVES;
-constexpr size_t kLdsCap = 64 * 1024;
 
 int num_cus() {
     static int n = 0;
@@ -42,13 +41,6 @@ int num_cus() {
 }
 
 // ---------------------------- gemv_quant -----------------------------------
-// LDS of the activation layout (uq_policies.h): planes 4*16*NT dwords, aux
-// 8*NT ints (Q6_K), K/128 run scales, K/32 group sums.
-template <class F>
-__host__ __device__ inline size_t x_lds_bytes(int K) {
-    const size_t NT = round_tasks(F::ntasks(K));
-    return NT * 256 + (F::kAux ? NT * 32 : 0) + (size_t)(K / 128 + 1) * 4 + (size_t)(K / 32) * 8;
-}
 
 template <class F>
 __device__ inline XLayout x_layout_at(uint8_t *lds, int K) {
@@ -149,7 +141,7 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
         if (d < U) issue(f[d], f2[d]);
 
     const XLayout L = x_layout_at<F>(lds, K);
-    prep_x<F>(x, K, L, x_first);
+    prep_x<F, 64 * NW>(x, K, L, x_first);
     __syncthreads();
     if (U == 0) return;
     const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
@@ -198,12 +190,24 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
 // K > 4096 (several tasks per lane and row): rows are still taken four at a
 // time, and the loop runs task-outer, row-inner: a lane reads its task's
 // activation digits from LDS once and applies them to the four rows, whose
-// weight fragments for that task are one load unit (issued right after the
-// previous unit is consumed, the first before the prep). Summation per lane
-// is over tasks in order, then reduce4_rows, as in gemv_kernel.
-constexpr int KT_NW = 8;  // 2 waves per SIMD, one workgroup per CU
+// weight fragments for that task are one load unit. Units run batch-major,
+// task-minor; a ring of KT_DEPTH units is in flight, each slot reloaded as
+// soon as it is consumed, and the first KT_DEPTH units are issued before the
+// prep. Summation per lane is over tasks in order, then reduce4_rows, as in
+// gemv_kernel.
+#ifndef UQ_KT_NW
+#define UQ_KT_NW 8
+#endif
+#ifndef UQ_KT_DEPTH
+#define UQ_KT_DEPTH 1
+#endif
+#ifndef UQ_KT_WPE
+#define UQ_KT_WPE 2
+#endif
+constexpr int KT_NW = UQ_KT_NW;        // waves per workgroup, one workgroup per CU
+constexpr int KT_DEPTH = UQ_KT_DEPTH;  // units in flight per wave
 template <class F, bool MULTI>
-__global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kt_kernel(
+__global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(UQ_KT_WPE))) void gemv_kt_kernel(
     const Segs S, size_t row_bytes, int K, const float *__restrict__ x) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -215,50 +219,137 @@ __global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(2)))
     const int N = S.start[S.n];
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
     const int nb = (nrows + 3) >> 2;
+    const int U = nb * T;
 
     const float4 x_first = prep_x_first(x, K);
-    typename F::Frag f[4];
-    int ib = 0, it = 0;  // next unit to load: batch, task
-    auto issue = [&]() {
-        const int t = lane + 64 * it;
+    typename F::Frag f[KT_DEPTH][4];
+    int iu = 0;  // next unit to load
+    auto issue = [&](typename F::Frag(&dst)[4]) {
+        const int b = iu / T, t = lane + 64 * (iu - b * T);
         for (int r = 0; r < 4; r++) {
-            const int i = 4 * ib + r;
+            const int i = 4 * b + r;
             if (i < nrows && t < ntask) {
                 const int R = wave + i * nwave, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(S, R)) : 0;
-                f[r] = F::load_w(S.w[sg] + (size_t)(R - S.start[sg]) * row_bytes, t, c);
+                dst[r] = F::load_w(S.w[sg] + (size_t)(R - S.start[sg]) * row_bytes, t, c);
             }
         }
-        if (++it == T) {
-            it = 0;
-            ++ib;
-        }
+        ++iu;
     };
-    if (nb > 0) issue();
+#pragma unroll
+    for (int d = 0; d < KT_DEPTH; d++)
+        if (iu < U) issue(f[d]);
 
     const XLayout L = x_layout_at<F>(lds, K);
-    prep_x<F>(x, K, L, x_first);
+    prep_x<F, 64 * KT_NW, 8>(x, K, L, x_first);
     __syncthreads();
-    if (nb == 0) return;
+    if (U == 0) return;
     const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
 
-    for (int b = 0; b < nb; b++) {
-        double g[4] = {0.0, 0.0, 0.0, 0.0};
-        for (int tt = 0; tt < T; tt++) {
-            const int t = lane + 64 * tt;
+    double g[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int u0 = 0; u0 < U; u0 += KT_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < KT_DEPTH; d++) {
+            const int u = u0 + d;
+            if (u >= U) break;  // wave-uniform
+            const int b = u / T, tt = u - b * T, t = lane + 64 * tt;
             if (t < ntask) {
                 typename F::XS xs;
                 F::load_x(xs, PV, t, c);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    if (4 * b + r < nrows) g[r] += F::dot(f[r], xs, c);  // wave-uniform row test
+                    if (4 * b + r < nrows) g[r] += F::dot(f[d][r], xs, c);  // wave-uniform row test
             }
-            if (ib < nb) issue();
+            if (iu < U) issue(f[d]);
+            if (tt == T - 1) {
+                const double G = reduce4_rows(g);
+                const int r = lane >> 4;
+                if ((lane & 15) == 0 && 4 * b + r < nrows) {
+                    const int R = wave + (4 * b + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
+                    S.y[sg][R - S.start[sg]] = (float)G;
+                }
+                for (int q = 0; q < 4; q++) g[q] = 0.0;
+            }
         }
-        const double G = reduce4_rows(g);
-        const int r = lane >> 4;
-        if ((lane & 15) == 0 && 4 * b + r < nrows) {
-            const int R = wave + (4 * b + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
-            S.y[sg][R - S.start[sg]] = (float)G;
+    }
+}
+
+// 4096 < K <= 16384 (KS = 2..4 slices of 64 tasks): K is split across the
+// waves of a workgroup. Wave w owns slice s = w % KS (tasks 64s + lane) and
+// row group gi = w / KS; the KS waves of a group walk the same rows (four at
+// a time, like gemv_kernel), each keeping its slice's activation digits in
+// VGPRs, so every wave has one load unit per row and up to KS_D rows in
+// flight. The slice sums of a 4-row batch (reduce4_rows) meet in LDS and
+// the slice-0 wave adds them in slice order:
+//     y = ((p_0 + p_1) + p_2) + p_3,  p_s = reduce4_rows over slice s.
+// Every wave of the workgroup runs the same number of batches (those of its
+// first group, which has the most rows), so the per-batch barrier is uniform.
+#ifndef UQ_KS_D
+#define UQ_KS_D 4  // rows in flight per wave (Q4_K, Q8_0)
+#endif
+#ifndef UQ_KS_D6
+#define UQ_KS_D6 2  // Q6_K (larger fragments; 4 would spill at 3 waves per SIMD)
+#endif
+
+template <class F, int KS, bool MULTI>
+__global__ __launch_bounds__(64 * KS_NW) __attribute__((amdgpu_waves_per_eu(3))) void gemv_ks_kernel(
+    const Segs S, size_t row_bytes, int K, const float *__restrict__ x) {
+    static_assert(KS >= 2 && KS <= 4 && KS_NW % KS == 0, "slices per workgroup");
+    constexpr int KS_D = F::kAux ? UQ_KS_D6 : UQ_KS_D;  // kAux: Q6_K
+    static_assert(KS_D == 1 || KS_D == 2 || KS_D == 4, "ring depth divides the 4-row batch");
+    constexpr int NG = KS_NW / KS;  // row groups per workgroup
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sl = wv % KS, gi = wv / KS;
+    const int ntask = F::ntasks(K);
+    const int t = 64 * sl + lane;
+    const bool act = t < ntask;
+    const typename F::LC c = F::lane_consts(lane);
+    const int G = blockIdx.x * NG + gi, nG = gridDim.x * NG;  // row group: rows G, G + nG, ...
+    const int N = S.start[S.n];
+    const int nrows = G < N ? (N - 1 - G) / nG + 1 : 0;
+    const int G0 = blockIdx.x * NG;
+    const int nb = G0 < N ? ((N - 1 - G0) / nG + 1 + 3) >> 2 : 0;  // batches of the workgroup's first group
+
+    const float4 x_first = prep_x_first(x, K);
+    typename F::Frag f[KS_D];
+    int pr = 0;  // next row index to load
+    auto issue = [&](typename F::Frag &dst) {
+        if (pr < nrows && act) {
+            const int R = G + pr * nG, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(S, R)) : 0;
+            dst = F::load_w(S.w[sg] + (size_t)(R - S.start[sg]) * row_bytes, t, c);
+        }
+        ++pr;
+    };
+#pragma unroll
+    for (int d = 0; d < KS_D; d++) issue(f[d]);
+
+    const XLayout L = x_layout_at<F>(lds, K);
+    double *part = (double *)(lds + ks_part_offset<F>(K));  // [2][NG][KS][4]
+    prep_x<F, 64 * KS_NW>(x, K, L, x_first);
+    __syncthreads();
+    const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
+    typename F::XS xr;
+    if (act) F::load_x(xr, PV, t, c);
+
+    for (int b = 0; b < nb; b++) {
+        double g[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            g[r] = 0.0;
+            typename F::Frag &cur = f[r % KS_D];
+            if (4 * b + r < nrows && act) g[r] = F::dot(cur, xr, c);  // row test is wave-uniform
+            issue(cur);
+        }
+        const double P = reduce4_rows(g);
+        double *pb = part + (size_t)(b & 1) * NG * KS * 4;
+        if ((lane & 15) == 0) pb[(gi * KS + sl) * 4 + (lane >> 4)] = P;
+        __syncthreads();
+        if (sl == 0 && lane < 4 && 4 * b + lane < nrows) {
+            double v = pb[(gi * KS) * 4 + lane];
+            for (int q = 1; q < KS; q++) v += pb[(gi * KS + q) * 4 + lane];
+            const int R = G + (4 * b + lane) * nG, sg = MULTI ? seg_of(S, R) : 0;
+            S.y[sg][R - S.start[sg]] = (float)v;
         }
     }
 }
@@ -352,7 +443,8 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 // Launch shape of the x-in-VGPR kernels, per format: one workgroup per CU
 // (NW waves) so the activation prep runs once per CU, with D units in flight
 // per wave. Q6_K: 12 waves (3 per SIMD, <= 168 VGPRs) with two units in
-// flight; Q4_K and Q8_0: 16 waves (4 per SIMD, <= 128 VGPRs), one unit.
+// flight; Q4_K and Q8_0: 16 waves (4 per SIMD, <= 128 VGPRs), one unit; the
+// gate/up pair: 12 waves, one unit (two fragments).
 #ifndef UQ_Q4K_NW
 #define UQ_Q4K_NW 16
 #endif
@@ -360,7 +452,7 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 #define UQ_Q4K_D 1
 #endif
 #ifndef UQ_PAIR_NW
-#define UQ_PAIR_NW 4
+#define UQ_PAIR_NW 12
 #endif
 #ifndef UQ_PAIR_D
 #define UQ_PAIR_D 1
@@ -378,9 +470,29 @@ hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x,
         hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW, MULTI>), dim3(resident_grid(k, lds, N, NW)),
                            dim3(64 * NW), lds, s, S, row_bytes, K, x);
     } else if constexpr (!PAIR) {
-        const void *k = (const void *)gemv_kt_kernel<F, MULTI>;
-        hipLaunchKernelGGL((gemv_kt_kernel<F, MULTI>), dim3(resident_grid(k, lds, N, KT_NW)), dim3(64 * KT_NW), lds,
-                           s, S, row_bytes, K, x);
+        const int ks = kslices<F>(K);
+        const size_t lds_ks = ks_lds_bytes<F>(K);
+        if (ks) {
+            auto go = [&](auto kern, int nslice) {
+                // one workgroup per CU (as resident), KS_NW / nslice row groups each
+                const int ng = KS_NW / nslice;
+                const int max_groups = num_cus() * blocks_per_cu((const void *)kern, lds_ks, 64 * KS_NW) * ng;
+                const int rows_per_group = (N + max_groups - 1) / max_groups;
+                const int groups = (N + rows_per_group - 1) / rows_per_group;
+                hipLaunchKernelGGL(kern, dim3((groups + ng - 1) / ng), dim3(64 * KS_NW), lds_ks, s, S, row_bytes, K,
+                                   x);
+            };
+            if (ks == 2)
+                go(gemv_ks_kernel<F, 2, MULTI>, 2);
+            else if (ks == 3)
+                go(gemv_ks_kernel<F, 3, MULTI>, 3);
+            else
+                go(gemv_ks_kernel<F, 4, MULTI>, 4);
+        } else {
+            const void *k = (const void *)gemv_kt_kernel<F, MULTI>;
+            hipLaunchKernelGGL((gemv_kt_kernel<F, MULTI>), dim3(resident_grid(k, lds, N, KT_NW)), dim3(64 * KT_NW),
+                               lds, s, S, row_bytes, K, x);
+        }
     } else {
         const void *k = (const void *)gemv_kernel<F, PAIR, false, 1, WAVES, MULTI>;
         hipLaunchKernelGGL((gemv_kernel<F, PAIR, false, 1, WAVES, MULTI>), dim3(resident_grid(k, lds, N)), dim3(TPB),

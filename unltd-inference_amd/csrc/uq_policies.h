@@ -62,6 +62,37 @@ UQ_HD size_t xq_index(int q, int i, int t, int NT) {
 }
 UQ_HD size_t aux_index(int k, int t, int NT) { return ((size_t)(k >> 2) * NT + t) * 4 + (k & 3); }
 
+// LDS budget of one GEMV workgroup (the default dynamic LDS limit).
+constexpr size_t kLdsCap = 64 * 1024;
+
+// LDS of the activation layout: planes 4*16*NT dwords, aux 8*NT ints
+// (Q6_K), K/128 run scales, K/32 group sums.
+template <class F>
+UQ_HD size_t x_lds_bytes(int K) {
+    const size_t NT = round_tasks(F::ntasks(K));
+    return NT * 256 + (F::kAux ? NT * 32 : 0) + (size_t)(K / 128 + 1) * 4 + (size_t)(K / 32) * 8;
+}
+
+// Rows of more than 64 tasks (K > 4096) run K-split: slices of 64 tasks, one
+// per wave of a KS_NW-wave workgroup, whose per-slice row sums meet in LDS
+// after the activation layout (16-byte aligned, two batches of KS_NW * 4
+// doubles). kslices is the slice count, or 0 when the rows do not take
+// that path (one slice, more than 4, or beyond the LDS budget).
+constexpr int KS_NW = 12;
+template <class F>
+UQ_HD size_t ks_part_offset(int K) {
+    return (x_lds_bytes<F>(K) + 15) & ~(size_t)15;
+}
+template <class F>
+UQ_HD size_t ks_lds_bytes(int K) {
+    return ks_part_offset<F>(K) + 2 * (size_t)KS_NW * 4 * sizeof(double);
+}
+template <class F>
+UQ_HD int kslices(int K) {
+    const int ks = (F::ntasks(K) + 63) / 64;
+    return ks >= 2 && ks <= 4 && ks_lds_bytes<F>(K) <= kLdsCap ? ks : 0;
+}
+
 UQ_HD void load_planes(uint32_t (&X)[kPlanes][16], const XView &V, int t) {
     for (int q = 0; q < kPlanes; q++)
         for (int i4 = 0; i4 < 4; i4++) {
