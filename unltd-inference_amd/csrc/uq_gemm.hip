@@ -411,13 +411,7 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ntm = (M + GM - 1) / GM, ntn = N / GN;
     const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
-    static bool lds_set = false;  // opt in to more than 64 KB of dynamic LDS (once per process)
-    if (!lds_set) {
-        if ((e = hipFuncSetAttribute((const void *)gemm_q4k_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)sizeof(GemmLds))) != hipSuccess)
-            return e;
-        lds_set = true;
-    }
+    if ((e = allow_lds((const void *)gemm_q4k_kernel, sizeof(GemmLds))) != hipSuccess) return e;
     hipLaunchKernelGGL(gemm_q4k_kernel, dim3(grid), dim3(GTPB), sizeof(GemmLds), s, w.bytes, w.row_bytes, K, N, M,
                        ws, ntn, Y);
     return hipGetLastError();

@@ -14,6 +14,7 @@
 // row's weights are prefetched with 128-bit loads. Row sums are reduced
 // across the wave with DPP.
 #include <map>
+#include <type_traits>
 #include <mutex>
 
 #include "uq_device.h"
@@ -184,6 +185,138 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
             const int R = wave + (rb + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
             S.y[sg][R - S.start[sg]] = PAIR ? swiglu1((float)G, (float)Uu) : (float)G;
         }
+    }
+}
+
+// Streaming variant of the x-in-VGPR kernel for single tensors (K <= 4096):
+// a row is fetched with fully coalesced direct-to-LDS loads
+// (global_load_lds_dwordx4: lane i of an instruction writes 16 bytes at
+// slot + 16i) into a per-wave ring of S row slots, and each lane then reads
+// its task's fragment from the slot. Blocks are laid out at a 16-byte
+// aligned pitch (Stage::BP; Q6_K's 210-byte blocks get 224), so chunk k of a
+// row is global bytes [blk*210 + 16j, +16) for k = 14*blk + j, and every LDS
+// read is aligned. The in-flight row bytes live in LDS, not in VGPRs.
+// Synchronisation is per wave: before reading row i the wave waits (vmcnt)
+// until at most the ops issued after row i's loads are outstanding: the
+// loads of the S-1 later rows (NI instructions each) and the y stores made
+// in between; at the tail, where fewer rows follow, it waits for all.
+template <class F> struct Stage;
+template <> struct Stage<Q6K> {
+    static constexpr int BC = 14, BP = 224, BB = kBQ6K;  // chunks per block, LDS pitch, block bytes
+    __device__ static Q6KFrag frag(const uint8_t *blk, const Q6K::LC &c) {
+        Q6KFrag f;
+        f.a = *(const u4 *)(blk + 64 * c.h + 16 * c.u);
+        f.b = *(const u4 *)(blk + 64 * c.h + 32 + 16 * c.u);
+        f.c = *(const u4 *)(blk + 128 + 32 * c.h + 16 * c.u);
+        // scale bytes 8h+u, +2 (s0) and +4, +6 (s1) in bytes 0 and 2, as q6k_load
+        f.s0 = *(const uint32_t *)(blk + 192 + 8 * c.h) >> (8 * c.u);
+        f.s1 = *(const uint32_t *)(blk + 196 + 8 * c.h) >> (8 * c.u);
+        f.dw = *(const uint32_t *)(blk + 208);
+        return f;
+    }
+};
+template <> struct Stage<Q4K> {
+    static constexpr int BC = 9, BP = 144, BB = kBQ4K;
+    __device__ static Q4K::Frag frag(const uint8_t *blk, const Q4K::LC &c) {
+        Q4K::Frag f;
+        f.h = *(const u4 *)blk;
+        f.qa = *(const u4 *)(blk + 16 + 32 * c.p);
+        f.qb = *(const u4 *)(blk + 32 + 32 * c.p);
+        return f;
+    }
+};
+
+// 16 bytes per lane from global g into LDS at dst + 16 * lane (dst
+// wave-uniform).
+// The loads carry the nontemporal hint (cache policy NT = 2): every weight
+// byte is read once, and these full-line coalesced loads then stream at a
+// markedly higher rate (measured: Q6_K head 101 -> 89 us).
+#ifndef UQ_STREAM_CPOL
+#define UQ_STREAM_CPOL 2
+#endif
+__device__ __forceinline__ void lds_dma16(const uint8_t *g, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 16, 0, UQ_STREAM_CPOL);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class F, int NI, int NW, int S>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
+gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, size_t row_bytes, int K,
+                   const float *__restrict__ x) {
+    static_assert(S == 1 || S == 2 || S == 4, "ring depth divides the 4-row batch");
+    using St = Stage<F>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = blockIdx.x * NW + wv, nwave = gridDim.x * NW;
+    const int ntask = F::ntasks(K);
+    const int nchunk = (K >> 8) * St::BC;
+    const typename F::LC c = F::lane_consts(lane);
+    const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
+    uint8_t *ring = lds + ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)wv * S * NI * 1024;
+
+    uint32_t goff[NI];
+    bool gval[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) {
+        const int k = lane + 64 * m, b = k / St::BC;
+        gval[m] = k < nchunk;
+        goff[m] = (uint32_t)(b * St::BB + 16 * (k - b * St::BC));
+    }
+    auto issue = [&](int i, int slot) {
+        if (i < nrows) {  // wave-uniform
+            const uint8_t *row = W + (size_t)(wave + i * nwave) * row_bytes;
+#pragma unroll
+            for (int m = 0; m < NI; m++)
+                if (gval[m]) lds_dma16(row + goff[m], ring + (slot * NI + m) * 1024);
+        }
+    };
+
+    const float4 x_first = prep_x_first(x, K);
+#pragma unroll
+    for (int sl = 0; sl < S; sl++) issue(sl, sl);
+    const XLayout L = x_layout_at<F>(lds, K);
+    prep_x<F, 64 * NW>(x, K, L, x_first);
+    __syncthreads();
+    if (nrows == 0) return;
+    const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
+    typename F::XS xr;
+    if (lane < ntask) F::load_x(xr, PV, lane, c);
+    const uint8_t *myblk = ring + (lane >> 2) * St::BP;
+
+    for (int rb = 0; rb < nrows; rb += 4) {
+        double g[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            g[r] = 0.0;
+            const int i = rb + r;
+            if (i >= nrows) continue;  // wave-uniform
+            // ops issued after row i's loads: the later rows' loads, and the
+            // one y store of the batch that ended among steps i-S .. i-1
+            const bool store_between = i >= S && (S == 4 || (S == 2 ? r <= 1 : r == 0));
+            if (i + S - 1 < nrows) {
+                if (store_between)
+                    wait_vm<(S - 1) * NI + 1>();
+                else
+                    wait_vm<(S - 1) * NI>();
+            } else {
+                wait_vm<0>();
+            }
+            typename F::Frag f{};
+            if (lane < ntask) f = St::frag(myblk + (r % S) * NI * 1024, c);
+            // the slot's LDS reads have returned before its next loads land in it
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(i + S, r % S);
+            if (lane < ntask) g[r] = F::dot(f, xr, c);
+        }
+        const double G = reduce4_rows(g);
+        const int r = lane >> 4;
+        if ((lane & 15) == 0 && rb + r < nrows) y[wave + (rb + r) * nwave] = (float)G;
     }
 }
 
@@ -458,12 +591,59 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 #define UQ_PAIR_D 1
 #endif
 template <class F> struct Shape { static constexpr int NW = UQ_Q4K_NW, D = UQ_Q4K_D; };
-template <> struct Shape<Q6K> { static constexpr int NW = 12, D = 2; };
+#ifndef UQ_Q6K_NW
+#define UQ_Q6K_NW 12
+#endif
+#ifndef UQ_Q6K_D
+#define UQ_Q6K_D 2
+#endif
+template <> struct Shape<Q6K> { static constexpr int NW = UQ_Q6K_NW, D = UQ_Q6K_D; };
+
+// Launch shape of the streaming kernel (one workgroup per CU, SNW waves,
+// SS rows per wave in flight), measured on the 152064 x 4096 Q6_K head and
+// the 4096 / 12288 x 4096 Q4_K projections.
+#ifndef UQ_STREAM_Q6K_NW
+#define UQ_STREAM_Q6K_NW 12
+#endif
+#ifndef UQ_STREAM_Q6K_S
+#define UQ_STREAM_Q6K_S 1
+#endif
+#ifndef UQ_STREAM_Q4K_NW
+#define UQ_STREAM_Q4K_NW 16
+#endif
+#ifndef UQ_STREAM_Q4K_S
+#define UQ_STREAM_Q4K_S 1
+#endif
+template <class F> struct StreamShape { static constexpr int NW = UQ_STREAM_Q4K_NW, S = UQ_STREAM_Q4K_S; };
+template <> struct StreamShape<Q6K> { static constexpr int NW = UQ_STREAM_Q6K_NW, S = UQ_STREAM_Q6K_S; };
+
+template <class F, int NI>
+hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+    constexpr int SNW = StreamShape<F>::NW, SS = StreamShape<F>::S;
+    const int N = S.start[S.n];
+    const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * NI * 1024;
+    const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS>;
+    const hipError_t e = allow_lds(k, l);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS>), dim3(resident_grid(k, l, N, SNW)), dim3(64 * SNW), l, s,
+                       S.w[0], S.y[0], N, row_bytes, K, x);
+    return hipGetLastError();
+}
 
 template <class F, bool PAIR, bool MULTI>
 hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const size_t lds = x_lds_bytes<F>(K);
+    // single Q4_K / Q6_K tensors with K <= 4096 stream through LDS
+    if constexpr (!PAIR && !MULTI && (std::is_same<F, Q6K>::value || std::is_same<F, Q4K>::value)) {
+        if (F::ntasks(K) <= 64) {
+            const int ni = ((K >> 8) * Stage<F>::BC + 63) / 64;
+            if (ni == 4) return launch_stream<F, 4>(S, row_bytes, K, x, s);
+            if (ni == 3) return launch_stream<F, 3>(S, row_bytes, K, x, s);
+            if (ni == 2) return launch_stream<F, 2>(S, row_bytes, K, x, s);
+            return launch_stream<F, 1>(S, row_bytes, K, x, s);
+        }
+    }
     if (F::ntasks(K) <= 64) {
         constexpr int NW = PAIR ? UQ_PAIR_NW : Shape<F>::NW, D = PAIR ? UQ_PAIR_D : Shape<F>::D;
         const void *k = (const void *)gemv_kernel<F, PAIR, true, D, NW, MULTI>;
@@ -838,6 +1018,22 @@ hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, con
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {
     return launch_q8k_segs(w.dtype, w.dim_in, w.row_bytes, one_seg(w, nullptr, y), x, s);
+}
+
+// Dynamic LDS above 64 KB must be allowed per kernel and device, once.
+hipError_t allow_lds(const void *kernel, size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    static std::mutex mu;
+    static std::map<std::pair<const void *, int>, size_t> done;
+    std::lock_guard<std::mutex> g(mu);
+    size_t &have = done[{kernel, dev}];
+    if (have >= lds) return hipSuccess;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) have = lds;
+    return e;
 }
 
 }  // namespace uq

@@ -31,6 +31,10 @@ constexpr int BQ4K = 144;
 constexpr int BQ6K = 210;
 constexpr int BQ8_0 = 34;
 
+// Allows kernel to take lds bytes of dynamic LDS (above the 64 KB default)
+// on the current device; a no-op after the first call per kernel and device.
+hipError_t allow_lds(const void *kernel, size_t lds);
+
 // Records the calling thread's error message (uq_last_error) and returns s.
 uq_status set_error(uq_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
