@@ -379,7 +379,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path runs on a single "
-              f"MI355X; see DESIGN.md for how it would shard).", file=sys.stderr)
+              f"MI355X; the row-sharded design is documented with the sources).", file=sys.stderr)
         sys.exit(2)
     hip = Hip()
     log("device:", uq.device_name())
