@@ -81,6 +81,25 @@ __device__ __forceinline__ int seg_of(const Segs &S, int R) {
     for (int i = 1; i < kMaxSegs; i++) s += (i < S.n && R >= S.start[i]) ? 1 : 0;
     return s;
 }
+// Output address of global row R; R must be wave-uniform, so the segment
+// table is read with scalar loads (a per-lane index into the kernel
+// arguments would become vector loads and a full vmcnt drain).
+template <bool MULTI>
+__device__ __forceinline__ float *y_of(const Segs &S, int R) {
+    const int sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(S, R)) : 0;
+    return S.y[sg] + (R - S.start[sg]);
+}
+// The store of a 4-row batch: lane 16r writes row r's value v; the four
+// row addresses are formed wave-uniformly first.
+template <bool MULTI>
+__device__ __forceinline__ void store4(const Segs &S, int lane, int R0, int nwave, int nvalid, float v) {
+    float *p[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) p[r] = r < nvalid ? y_of<MULTI>(S, R0 + r * nwave) : nullptr;
+    const int r = lane >> 4;
+    float *q = r == 0 ? p[0] : r == 1 ? p[1] : r == 2 ? p[2] : p[3];
+    if ((lane & 15) == 0 && r < nvalid) *q = v;
+}
 
 // One unit = one task of one row. A wave owns rows wave, wave + nwave, ...
 // and walks their units in order (the tasks of a row, then the next row); a
@@ -180,11 +199,8 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
         const double G = reduce4_rows(g);
         double Uu = 0.0;
         if (PAIR) Uu = reduce4_rows(u);
-        const int r = lane >> 4;
-        if ((lane & 15) == 0 && rb + r < nrows) {
-            const int R = wave + (rb + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
-            S.y[sg][R - S.start[sg]] = PAIR ? swiglu1((float)G, (float)Uu) : (float)G;
-        }
+        store4<MULTI>(S, lane, wave + rb * nwave, nwave, nrows - rb,
+                      PAIR ? swiglu1((float)G, (float)Uu) : (float)G);
     }
 }
 
@@ -244,12 +260,15 @@ __device__ __forceinline__ void wait_vm() {
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <class F, int NI, int NW, int S>
+// PAIR: each row unit is a gate row and an up row (2*NI loads, two slots'
+// worth of LDS); MULTI: the row's tensor is looked up in the segment table.
+template <class F, int NI, int NW, int S, bool PAIR, bool MULTI>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
-gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, size_t row_bytes, int K,
-                   const float *__restrict__ x) {
+gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
     static_assert(S == 1 || S == 2 || S == 4, "ring depth divides the 4-row batch");
     using St = Stage<F>;
+    constexpr int NT = PAIR ? 2 : 1;   // tensors per row unit
+    constexpr int UNIT = NT * NI;      // loads (and KB of LDS) per row unit
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -257,8 +276,9 @@ gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, 
     const int ntask = F::ntasks(K);
     const int nchunk = (K >> 8) * St::BC;
     const typename F::LC c = F::lane_consts(lane);
+    const int N = Sg.start[Sg.n];
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
-    uint8_t *ring = lds + ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)wv * S * NI * 1024;
+    uint8_t *ring = lds + ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)wv * S * UNIT * 1024;
 
     uint32_t goff[NI];
     bool gval[NI];
@@ -270,10 +290,15 @@ gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, 
     }
     auto issue = [&](int i, int slot) {
         if (i < nrows) {  // wave-uniform
-            const uint8_t *row = W + (size_t)(wave + i * nwave) * row_bytes;
+            const int R = wave + i * nwave, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(Sg, R)) : 0;
+            const size_t off = (size_t)(R - Sg.start[sg]) * row_bytes;
 #pragma unroll
-            for (int m = 0; m < NI; m++)
-                if (gval[m]) lds_dma16(row + goff[m], ring + (slot * NI + m) * 1024);
+            for (int t = 0; t < NT; t++) {
+                const uint8_t *row = (t == 0 ? Sg.w[sg] : Sg.w2[sg]) + off;
+#pragma unroll
+                for (int m = 0; m < NI; m++)
+                    if (gval[m]) lds_dma16(row + goff[m], ring + (slot * UNIT + t * NI + m) * 1024);
+            }
         }
     };
 
@@ -290,10 +315,11 @@ gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, 
     const uint8_t *myblk = ring + (lane >> 2) * St::BP;
 
     for (int rb = 0; rb < nrows; rb += 4) {
-        double g[4];
+        double g[4], u[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             g[r] = 0.0;
+            u[r] = 0.0;
             const int i = rb + r;
             if (i >= nrows) continue;  // wave-uniform
             // ops issued after row i's loads: the later rows' loads, and the
@@ -301,22 +327,31 @@ gemv_stream_kernel(const uint8_t *__restrict__ W, float *__restrict__ y, int N, 
             const bool store_between = i >= S && (S == 4 || (S == 2 ? r <= 1 : r == 0));
             if (i + S - 1 < nrows) {
                 if (store_between)
-                    wait_vm<(S - 1) * NI + 1>();
+                    wait_vm<(S - 1) * UNIT + 1>();
                 else
-                    wait_vm<(S - 1) * NI>();
+                    wait_vm<(S - 1) * UNIT>();
             } else {
                 wait_vm<0>();
             }
-            typename F::Frag f{};
-            if (lane < ntask) f = St::frag(myblk + (r % S) * NI * 1024, c);
+            typename F::Frag f{}, f2{};
+            const uint8_t *b0 = myblk + (r % S) * UNIT * 1024;
+            if (lane < ntask) {
+                f = St::frag(b0, c);
+                if (PAIR) f2 = St::frag(b0 + NI * 1024, c);
+            }
             // the slot's LDS reads have returned before its next loads land in it
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             issue(i + S, r % S);
-            if (lane < ntask) g[r] = F::dot(f, xr, c);
+            if (lane < ntask) {
+                g[r] = F::dot(f, xr, c);
+                if (PAIR) u[r] = F::dot(f2, xr, c);
+            }
         }
         const double G = reduce4_rows(g);
-        const int r = lane >> 4;
-        if ((lane & 15) == 0 && rb + r < nrows) y[wave + (rb + r) * nwave] = (float)G;
+        double Uu = 0.0;
+        if (PAIR) Uu = reduce4_rows(u);
+        store4<MULTI>(Sg, lane, wave + rb * nwave, nwave, nrows - rb,
+                      PAIR ? swiglu1((float)G, (float)Uu) : (float)G);
     }
 }
 
@@ -395,11 +430,7 @@ __global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(UQ_K
             if (iu < U) issue(f[d]);
             if (tt == T - 1) {
                 const double G = reduce4_rows(g);
-                const int r = lane >> 4;
-                if ((lane & 15) == 0 && 4 * b + r < nrows) {
-                    const int R = wave + (4 * b + r) * nwave, sg = MULTI ? seg_of(S, R) : 0;
-                    S.y[sg][R - S.start[sg]] = (float)G;
-                }
+                store4<MULTI>(S, lane, wave + 4 * b * nwave, nwave, nrows - 4 * b, (float)G);
                 for (int q = 0; q < 4; q++) g[q] = 0.0;
             }
         }
@@ -478,11 +509,16 @@ __global__ __launch_bounds__(64 * KS_NW) __attribute__((amdgpu_waves_per_eu(3)))
         double *pb = part + (size_t)(b & 1) * NG * KS * 4;
         if ((lane & 15) == 0) pb[(gi * KS + sl) * 4 + (lane >> 4)] = P;
         __syncthreads();
-        if (sl == 0 && lane < 4 && 4 * b + lane < nrows) {
-            double v = pb[(gi * KS) * 4 + lane];
-            for (int q = 1; q < KS; q++) v += pb[(gi * KS + q) * 4 + lane];
-            const int R = G + (4 * b + lane) * nG, sg = MULTI ? seg_of(S, R) : 0;
-            S.y[sg][R - S.start[sg]] = (float)v;
+        if (sl == 0) {
+            double v = 0.0;
+            if (lane < 4) {
+                v = pb[(gi * KS) * 4 + lane];
+                for (int q = 1; q < KS; q++) v += pb[(gi * KS + q) * 4 + lane];
+            }
+            // lane 16r stores row r: move lane r's sum there
+            v = __hiloint2double(__builtin_amdgcn_ds_bpermute(4 * (lane >> 4), __double2hiint(v)),
+                                 __builtin_amdgcn_ds_bpermute(4 * (lane >> 4), __double2loint(v)));
+            store4<MULTI>(S, lane, G + 4 * b * nG, nG, nrows - 4 * b, (float)v);
         }
     }
 }
@@ -614,19 +650,25 @@ template <> struct Shape<Q6K> { static constexpr int NW = UQ_Q6K_NW, D = UQ_Q6K_
 #ifndef UQ_STREAM_Q4K_S
 #define UQ_STREAM_Q4K_S 1
 #endif
+#ifndef UQ_STREAM_PAIR_NW
+#define UQ_STREAM_PAIR_NW 12
+#endif
+#ifndef UQ_STREAM_ON
+#define UQ_STREAM_ON 1
+#endif
 template <class F> struct StreamShape { static constexpr int NW = UQ_STREAM_Q4K_NW, S = UQ_STREAM_Q4K_S; };
 template <> struct StreamShape<Q6K> { static constexpr int NW = UQ_STREAM_Q6K_NW, S = UQ_STREAM_Q6K_S; };
 
-template <class F, int NI>
+template <class F, int NI, bool PAIR, bool MULTI>
 hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
-    constexpr int SNW = StreamShape<F>::NW, SS = StreamShape<F>::S;
+    constexpr int SNW = PAIR ? UQ_STREAM_PAIR_NW : StreamShape<F>::NW, SS = PAIR ? 1 : StreamShape<F>::S;
     const int N = S.start[S.n];
-    const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * NI * 1024;
-    const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS>;
+    const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * (PAIR ? 2 : 1) * NI * 1024;
+    const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>;
     const hipError_t e = allow_lds(k, l);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS>), dim3(resident_grid(k, l, N, SNW)), dim3(64 * SNW), l, s,
-                       S.w[0], S.y[0], N, row_bytes, K, x);
+    hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>), dim3(resident_grid(k, l, N, SNW)),
+                       dim3(64 * SNW), l, s, S, row_bytes, K, x);
     return hipGetLastError();
 }
 
@@ -634,14 +676,14 @@ template <class F, bool PAIR, bool MULTI>
 hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const size_t lds = x_lds_bytes<F>(K);
-    // single Q4_K / Q6_K tensors with K <= 4096 stream through LDS
-    if constexpr (!PAIR && !MULTI && (std::is_same<F, Q6K>::value || std::is_same<F, Q4K>::value)) {
-        if (F::ntasks(K) <= 64) {
+    // Q4_K / Q6_K rows with K <= 4096 stream through LDS
+    if constexpr (std::is_same<F, Q6K>::value || std::is_same<F, Q4K>::value) {
+        if (F::ntasks(K) <= 64 && UQ_STREAM_ON) {
             const int ni = ((K >> 8) * Stage<F>::BC + 63) / 64;
-            if (ni == 4) return launch_stream<F, 4>(S, row_bytes, K, x, s);
-            if (ni == 3) return launch_stream<F, 3>(S, row_bytes, K, x, s);
-            if (ni == 2) return launch_stream<F, 2>(S, row_bytes, K, x, s);
-            return launch_stream<F, 1>(S, row_bytes, K, x, s);
+            if (ni == 4) return launch_stream<F, 4, PAIR, MULTI>(S, row_bytes, K, x, s);
+            if (ni == 3) return launch_stream<F, 3, PAIR, MULTI>(S, row_bytes, K, x, s);
+            if (ni == 2) return launch_stream<F, 2, PAIR, MULTI>(S, row_bytes, K, x, s);
+            return launch_stream<F, 1, PAIR, MULTI>(S, row_bytes, K, x, s);
         }
     }
     if (F::ntasks(K) <= 64) {
