@@ -1,0 +1,100 @@
+/*
+ * uq_ops.h -- per-layer non-linear kernels of libuq.so, the functions of
+ * crates/unltd-tensor/src/kernels.rs that the Qwen3.5 forward runs between
+ * its quantized projections, so activations can stay in HBM from one layer
+ * to the next.
+ *
+ * Each function has a host-pointer mirror with the reference's arguments
+ * (slices as pointer + length; panics as uq_status codes, UQ_ERR_LEN for the
+ * length asserts) and a device form (suffix _d: device pointers, several
+ * rows per call, asynchronous on the given stream, no allocation).
+ *
+ * Numerics (checked against the oracle):
+ *  - rmsnorm, l2_norm_rows, ssm_conv, gdn_fused_step (given exp(gate)) and
+ *    the softmax denominator follow the reference's f32 / f64 steps and
+ *    summation orders exactly; the sequential f64 sums of rmsnorm and
+ *    l2_norm_rows are proven equal through a rounding bound, or replayed.
+ *  - exp / log are the f64 functions rounded once to f32 (correctly rounded
+ *    but for rare near-midpoint arguments); the reference calls the
+ *    platform libm, so sigmoid, silu, softplus, softmax and the gdn decay
+ *    agree with it within 1-2 ulp.
+ *  - the rope rotations use the device's f64 sin / cos; results agree with
+ *    the reference except when its libm and the device differ in the last
+ *    f64 bit in a way that changes the f32 rounding.
+ */
+#ifndef UQ_OPS_H
+#define UQ_OPS_H
+
+#include "uq.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* rmsnorm (kernels.rs:61-78): out = (x * scale) * w, scale = 1/sqrtf(mean(x^2) + eps).
+ * Panics: len(out) != len(x), len(x) != len(w). */
+uq_status uq_rmsnorm(float *out, size_t out_len, const float *x, size_t x_len, const float *w, size_t w_len,
+                     float eps);
+/* rows rows of n, each normalised with the same w[n]. */
+uq_status uq_rmsnorm_d(float *d_out, const float *d_x, const float *d_w, size_t n, size_t rows, float eps,
+                       void *stream);
+
+/* l2_norm_rows (kernels.rs:236-256), in place over len/dim rows.
+ * Panics: len % dim != 0. */
+uq_status uq_l2_norm_rows(float *data, size_t len, size_t dim, float eps);
+uq_status uq_l2_norm_rows_d(float *d_data, size_t len, size_t dim, float eps, void *stream);
+
+/* softmax (kernels.rs:157-168). Panics: len(out) != len(x). The device
+ * form takes rows of n <= 8192 (UQ_ERR_ARG above). */
+uq_status uq_softmax(float *out, size_t out_len, const float *x, size_t x_len, float scale);
+uq_status uq_softmax_d(float *d_out, const float *d_x, size_t n, size_t rows, float scale, void *stream);
+
+/* sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228).
+ * Panics: len(out) != len(x). */
+uq_status uq_sigmoid(float *out, size_t out_len, const float *x, size_t x_len);
+uq_status uq_silu(float *out, size_t out_len, const float *x, size_t x_len);
+uq_status uq_softplus(float *out, size_t out_len, const float *x, size_t x_len);
+uq_status uq_sigmoid_d(float *d_out, const float *d_x, size_t n, void *stream);
+uq_status uq_silu_d(float *d_out, const float *d_x, size_t n, void *stream);
+uq_status uq_softplus_d(float *d_out, const float *d_x, size_t n, void *stream);
+
+/* ssm_conv (kernels.rs:265-305): x is [ncs, channels], kernel [d_conv,
+ * channels], out [n_t, channels] with n_t = ncs - (d_conv - 1).
+ * Panics: len(x) % channels, ncs < d_conv, len(kernel), len(out). */
+uq_status uq_ssm_conv(float *out, size_t out_len, const float *x, size_t x_len, const float *kernel,
+                      size_t kernel_len, size_t d_conv, size_t channels);
+uq_status uq_ssm_conv_d(float *d_out, const float *d_x, size_t x_len, const float *d_kernel, size_t d_conv,
+                        size_t channels, void *stream);
+
+/* gdn_fused_step (kernels.rs:316-375) of one head: state is dim x dim,
+ * S[i][j] at i*dim + j. Panics: len(k), len(v), len(out) != dim = len(q),
+ * len(state) != dim*dim. */
+uq_status uq_gdn_fused_step(float *state, size_t state_len, float *out, size_t out_len, const float *q,
+                            size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len, float gate,
+                            float beta, float scale);
+/* heads heads at once: state [heads][dim][dim], q/k/v/out [heads][dim],
+ * gate/beta [heads] (the caller maps q/k heads to v heads, as the
+ * reference's caller does). */
+uq_status uq_gdn_fused_step_d(float *d_state, float *d_out, const float *d_q, const float *d_k, const float *d_v,
+                              const float *d_gate, const float *d_beta, size_t dim, size_t heads, float scale,
+                              void *stream);
+
+/* rope_apply_llama (kernels.rs:109-125) and rope_apply_neox (:131-148), in
+ * place. Panics: len(x) odd, len(freqs) < len(x)/2. */
+uq_status uq_rope_llama(float *x, size_t x_len, const float *freqs, size_t freqs_len, size_t pos);
+uq_status uq_rope_neox(float *x, size_t x_len, const float *freqs, size_t freqs_len, size_t pos);
+/* rows rows of n at the same position; d_freqs holds n/2 values. */
+uq_status uq_rope_llama_d(float *d_x, size_t n, size_t rows, const float *d_freqs, size_t pos, void *stream);
+uq_status uq_rope_neox_d(float *d_x, size_t n, size_t rows, const float *d_freqs, size_t pos, void *stream);
+
+/* rope_apply_imrope (kernels.rs:381-400), in place. Panics: n_rot odd,
+ * n_rot > len(x). */
+uq_status uq_rope_imrope(float *x, size_t x_len, size_t n_rot, double theta_scale, size_t pos);
+uq_status uq_rope_imrope_d(float *d_x, size_t n, size_t rows, size_t n_rot, double theta_scale, size_t pos,
+                           void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UQ_OPS_H */

@@ -9,7 +9,8 @@
  * Every function restates one function of the reference, cited file:line
  * (paths relative to the reference repository root):
  *   crates/unltd-tensor/src/quants.rs   -- block decode, dots, GEMV, Q8_K
- *   crates/unltd-tensor/src/kernels.rs  -- pairwise_sum_f64, swiglu, silu
+ *   crates/unltd-tensor/src/kernels.rs  -- pairwise_sum_f64, swiglu, silu, and
+ *                                          the per-layer ops (oracle_ops.c)
  *   crates/unltd-generation/src/min_forward.rs -- dtype ids, row bytes
  * Functions marked "closed form" have no reference kernel (Q8_0 decode, Q6_K
  * and Q8_0 f32 dequantization, integer unpack exports); they follow the GGUF
@@ -118,6 +119,27 @@ int or_unpack_q8_0(const uint8_t *w, size_t nblocks, int8_t *q, float *d);
 void or_swiglu(float *out, const float *gate, const float *up, size_t n);
 /* kernels.rs:207-212 */
 void or_silu(float *out, const float *x, size_t n);
+
+/* Per-layer non-linear kernels (oracle_ops.c), kernels.rs: */
+/* :61-78 rmsnorm: sequential f64 sum of f32 squares, f32 scale */
+int or_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps);
+/* :236-256 l2_norm_rows, in place over len/dim rows */
+int or_l2_norm_rows(float *data, size_t len, size_t dim, float eps);
+/* :157-168 softmax: f32 exp, pairwise f64 denominator, f64 division */
+int or_softmax(float *out, const float *x, size_t n, float scale);
+/* :198-203 sigmoid; :217-228 softplus */
+void or_sigmoid(float *out, const float *x, size_t n);
+void or_softplus(float *out, const float *x, size_t n);
+/* :265-305 ssm_conv */
+int or_ssm_conv(float *out, size_t out_len, const float *x, size_t x_len, const float *kernel,
+                size_t kernel_len, size_t d_conv, size_t channels);
+/* :316-375 gdn_fused_step; state is dim x dim, row i = product dim */
+int or_gdn_fused_step(float *state, float *out, const float *q, const float *k, const float *v, size_t dim,
+                      float gate, float beta, float scale);
+/* :109-125, :131-148, :381-400 */
+int or_rope_llama(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
+int or_rope_neox(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
+int or_rope_imrope(float *x, size_t n, size_t n_rot, double theta_scale, size_t pos);
 
 #ifdef __cplusplus
 }

@@ -263,3 +263,98 @@ def silu(x) -> np.ndarray:
     out = np.zeros(len(x), np.float32)
     lib().or_silu(_p(out), _p(x), len(x))
     return out
+
+
+# ------------------------------------------------ per-layer ops (oracle_ops.c)
+
+def _fn(name, argtypes, restype=C.c_int):
+    f = getattr(lib(), name)
+    f.argtypes = argtypes
+    f.restype = restype
+    return f
+
+
+def _ok(rc, what):
+    if rc != 0:
+        raise ValueError(f"{what}: oracle status {rc}")
+
+
+_P, _S = C.c_void_p, C.c_size_t
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """kernels.rs:61-78"""
+    x, w = _f32(x), _f32(w)
+    out = np.zeros(len(x), np.float32)
+    _ok(_fn("or_rmsnorm", [_P, _P, _P, _S, C.c_float])(_p(out), _p(x), _p(w), len(x), eps), "rmsnorm")
+    return out
+
+
+def l2_norm_rows(data, dim: int, eps: float) -> np.ndarray:
+    """kernels.rs:236-256 (returns a normalised copy)"""
+    d = _f32(data).copy()
+    _ok(_fn("or_l2_norm_rows", [_P, _S, _S, C.c_float])(_p(d), len(d), dim, eps), "l2_norm_rows")
+    return d
+
+
+def softmax(x, scale: float) -> np.ndarray:
+    """kernels.rs:157-168"""
+    x = _f32(x)
+    out = np.zeros(len(x), np.float32)
+    _ok(_fn("or_softmax", [_P, _P, _S, C.c_float])(_p(out), _p(x), len(x), scale), "softmax")
+    return out
+
+
+def sigmoid(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(len(x), np.float32)
+    _fn("or_sigmoid", [_P, _P, _S], None)(_p(out), _p(x), len(x))
+    return out
+
+
+def softplus(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(len(x), np.float32)
+    _fn("or_softplus", [_P, _P, _S], None)(_p(out), _p(x), len(x))
+    return out
+
+
+def ssm_conv(x, kernel, d_conv: int, channels: int) -> np.ndarray:
+    """kernels.rs:265-305; out[t*channels + c]"""
+    x, k = _f32(x), _f32(kernel)
+    n_t = len(x) // channels - (d_conv - 1)
+    out = np.zeros(max(n_t, 0) * channels, np.float32)
+    _ok(_fn("or_ssm_conv", [_P, _S, _P, _S, _P, _S, _S, _S])(_p(out), len(out), _p(x), len(x), _p(k), len(k),
+                                                             d_conv, channels), "ssm_conv")
+    return out
+
+
+def gdn_fused_step(state, q, k, v, gate: float, beta: float, scale: float):
+    """kernels.rs:316-375; returns (new state, out)"""
+    st = _f32(state).copy()
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros(len(q), np.float32)
+    _ok(_fn("or_gdn_fused_step", [_P, _P, _P, _P, _P, _S, C.c_float, C.c_float, C.c_float])(
+        _p(st), _p(out), _p(q), _p(k), _p(v), len(q), gate, beta, scale), "gdn_fused_step")
+    return st, out
+
+
+def rope_llama(x, freqs, pos: int) -> np.ndarray:
+    """kernels.rs:109-125 (returns a rotated copy)"""
+    y, f = _f32(x).copy(), _f32(freqs)
+    _ok(_fn("or_rope_llama", [_P, _S, _P, _S, _S])(_p(y), len(y), _p(f), len(f), pos), "rope_llama")
+    return y
+
+
+def rope_neox(x, freqs, pos: int) -> np.ndarray:
+    """kernels.rs:131-148"""
+    y, f = _f32(x).copy(), _f32(freqs)
+    _ok(_fn("or_rope_neox", [_P, _S, _P, _S, _S])(_p(y), len(y), _p(f), len(f), pos), "rope_neox")
+    return y
+
+
+def rope_imrope(x, n_rot: int, theta_scale: float, pos: int) -> np.ndarray:
+    """kernels.rs:381-400"""
+    y = _f32(x).copy()
+    _ok(_fn("or_rope_imrope", [_P, _S, _S, C.c_double, _S])(_p(y), len(y), n_rot, theta_scale, pos), "rope_imrope")
+    return y

@@ -102,3 +102,29 @@ def test_gemv_batch_argument_errors():
     assert L.uq_gemv_batch(hs, ys, 0, None, None) == 0  # nothing to do
     assert uq.STATUS[L.uq_gemv_batch(hs, ys, 9, None, None)] == "ARG"
     assert uq.STATUS[L.uq_gemv_batch(hs, ys, 2, None, None)] == "ARG"  # null handles
+
+
+def test_ops_argument_errors_mirror_reference_panics():  # kernels.rs asserts, before any device work
+    from uq import ops
+    f = np.zeros(4, np.float32)
+    L = uq.lib()
+    P = lambda a: a.ctypes.data_as(C.c_void_p)
+    assert uq.STATUS[L.uq_rmsnorm(P(f), 3, P(f), 4, P(f), 4, 0.0)] == "LEN"
+    assert uq.STATUS[L.uq_rmsnorm(P(f), 4, P(f), 4, P(f), 3, 0.0)] == "LEN"
+    assert uq.STATUS[L.uq_softmax(P(f), 3, P(f), 4, 1.0)] == "LEN"
+    assert uq.STATUS[L.uq_sigmoid(P(f), 3, P(f), 4)] == "LEN"
+    assert uq.STATUS[L.uq_l2_norm_rows(P(f), 4, 3, 1e-6)] == "LEN"
+    assert uq.STATUS[L.uq_ssm_conv(P(f), 2, P(f), 3, P(f), 4, 2, 2)] == "LEN"       # len(x) % channels
+    assert uq.STATUS[L.uq_ssm_conv(P(f), 2, P(f), 4, P(f), 4, 4, 2)] == "LEN"       # window shorter than kernel
+    assert uq.STATUS[L.uq_ssm_conv(P(f), 2, P(f), 4, P(f), 3, 2, 2)] == "LEN"       # len(kernel)
+    assert uq.STATUS[L.uq_ssm_conv(P(f), 3, P(f), 4, P(f), 4, 2, 2)] == "LEN"       # len(out)
+    assert uq.STATUS[L.uq_gdn_fused_step(P(f), 4, P(f), 2, P(f), 2, P(f), 1, P(f), 2, 0.0, 1.0, 1.0)] == "LEN"
+    assert uq.STATUS[L.uq_gdn_fused_step(P(f), 3, P(f), 2, P(f), 2, P(f), 2, P(f), 2, 0.0, 1.0, 1.0)] == "LEN"
+    assert uq.STATUS[L.uq_rope_llama(P(f), 3, P(f), 4, 1)] == "LEN"
+    assert uq.STATUS[L.uq_rope_neox(P(f), 4, P(f), 1, 1)] == "LEN"
+    assert uq.STATUS[L.uq_rope_imrope(P(f), 4, 3, 0.5, 1)] == "LEN"
+    assert uq.STATUS[L.uq_rope_imrope(P(f), 4, 6, 0.5, 1)] == "LEN"
+    if uq.device_count() == 0:
+        with pytest.raises(uq.UqError) as e:
+            ops.rmsnorm(f, f, 1e-6)
+        assert e.value.kind == "NO_DEVICE"

@@ -1,0 +1,209 @@
+"""GPU parity of the per-layer ops (include/uq_ops.h) against the oracle.
+
+Bars (see uq_ops.h):
+  * bit-exact: rmsnorm, l2_norm_rows (including inputs whose mean sits on an
+    f32 rounding boundary, which take the sequential replay), ssm_conv,
+    gdn_fused_step with exp(gate) exact, and the rope rotations;
+  * within 2 ulp of the oracle's C library expf / logf: sigmoid, silu,
+    softplus, softmax and gdn_fused_step with a general gate; nearly all
+    elements bit-equal (the device's exp / log are correctly rounded, the C
+    library's are not always).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import uq
+from uq import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+
+
+def assert_bitwise(got, ref, what):
+    g, r = bits(got), bits(ref)
+    bad = np.nonzero(g != r)[0]
+    assert bad.size == 0, f"{what}: {bad.size} differ, first {bad[:5].tolist()}"
+
+
+def assert_ulp(got, ref, max_ulp, min_equal, what):
+    g, r = bits(got), bits(ref)
+    d = np.abs(g - r)
+    assert d.max() <= max_ulp, f"{what}: max ulp {d.max()} at {int(np.argmax(d))}"
+    frac = float(np.mean(d == 0))
+    assert frac >= min_equal, f"{what}: only {frac:.4f} bit-equal"
+
+
+def dev(a):
+    return uq.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 12288])
+def test_rmsnorm_bit_exact(n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 40.0], n)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    assert_bitwise(ops.rmsnorm(x, w, 1e-6), O.rmsnorm(x, w, 1e-6), f"rmsnorm n={n}")
+
+
+def test_rmsnorm_rows_on_device_and_the_boundary_replay():
+    rng = np.random.default_rng(5)
+    n, rows = 4096, 9
+    X = rng.standard_normal((rows, n)).astype(np.float32)
+    # row 8: mean = 2^-10 (1 + 2^-24) exactly, the midpoint between two f32 values,
+    # so the tree-sum bound cannot decide and the sequential loop runs
+    X[8] = 0.0
+    X[8, 4092:] = [1.0, 1.0, 1.0, np.nextafter(np.float32(1.0), np.float32(2.0))]
+    w = rng.standard_normal(n).astype(np.float32)
+    dx, dw, dy = dev(X), dev(w), uq.DeviceArray(4 * n * rows)
+    ops.rmsnorm_d(dy, dx, dw, n, rows, 1e-6)
+    uq.synchronize()
+    got = dy.download(np.float32, n * rows).reshape(rows, n)
+    for r in range(rows):
+        assert_bitwise(got[r], O.rmsnorm(X[r], w, 1e-6), f"rmsnorm row {r}")
+    # the small case of the midpoint: [1, 1, 1, 1+2^-23] with eps 0
+    x4 = np.array([1.0, 1.0, 1.0, np.nextafter(np.float32(1.0), np.float32(2.0))], np.float32)
+    assert_bitwise(ops.rmsnorm(x4, np.ones(4, np.float32), 0.0), O.rmsnorm(x4, np.ones(4, np.float32), 0.0),
+                   "rmsnorm midpoint")
+
+
+def test_l2_norm_rows_bit_exact_and_boundary():
+    rng = np.random.default_rng(6)
+    dim, rows = 128, 64
+    X = (rng.standard_normal(rows * dim) * 3).astype(np.float32)
+    X[:dim] = 0.0
+    X[dim - 4:dim] = [1.0, 1.0, 1.0, np.nextafter(np.float32(1.0), np.float32(2.0))]  # sum = 4 + 2^-22: f32 midpoint
+    assert_bitwise(ops.l2_norm_rows(X, dim, 1e-6), O.l2_norm_rows(X, dim, 1e-6), "l2_norm_rows host")
+    d = dev(X)
+    ops.l2_norm_rows_d(d, len(X), dim, 1e-6)
+    uq.synchronize()
+    assert_bitwise(d.download(np.float32, len(X)), O.l2_norm_rows(X, dim, 1e-6), "l2_norm_rows device")
+
+
+@pytest.mark.parametrize("n", [1, 3, 1000, 8192])
+def test_softmax_within_2_ulp(n):
+    rng = np.random.default_rng(n + 1)
+    x = (rng.standard_normal(n) * 5).astype(np.float32)
+    assert_ulp(ops.softmax(x, 0.125), O.softmax(x, 0.125), 2, 0.99, f"softmax n={n}")
+
+
+def test_softmax_reference_case_and_device_rows():
+    assert_bitwise(ops.softmax([1000.0, 1001.0, 1002.0], 1.0), O.softmax([1000.0, 1001.0, 1002.0], 1.0), "kat")
+    rng = np.random.default_rng(8)
+    n, rows = 777, 16
+    X = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    dx, dy = dev(X), uq.DeviceArray(4 * n * rows)
+    ops.softmax_d(dy, dx, n, rows, 0.5)
+    uq.synchronize()
+    got = dy.download(np.float32, n * rows).reshape(rows, n)
+    for r in range(rows):
+        assert_ulp(got[r], O.softmax(X[r], 0.5), 2, 0.99, f"softmax row {r}")
+
+
+def unary_cr(name, x):
+    """The device's method: each f32 exp / log is the f64 function rounded
+    once to f32; the other steps are single f32 operations."""
+    f = np.float32
+    x = np.asarray(x, np.float32)
+    if name == "softplus":
+        e = np.exp(x.astype(np.float64)).astype(f)
+        return np.where(x > f(20), x, np.log((f(1) + e).astype(np.float64)).astype(f))
+    e = np.exp(-x.astype(np.float64)).astype(f)
+    return (f(1) if name == "sigmoid" else x) / (f(1) + e)
+
+
+@pytest.mark.parametrize("name", ["sigmoid", "silu", "softplus"])
+def test_unary_within_2_ulp(name):
+    """Within 2 ulp of the oracle (the C library's expf / logf, as the
+    reference calls them); glibc's logf is not correctly rounded for about
+    0.75% of the arguments of softplus here, so bit-equality with the oracle
+    is only required of 99%. Against the correctly rounded f64 model of the
+    device's own method the bar is bit-equality but for rare near-midpoint
+    arguments."""
+    rng = np.random.default_rng(9)
+    x = np.concatenate([rng.uniform(-30, 30, 200000), [0.0, -0.0, 1.0, -1.0, 20.0, 20.5, -88.0, 88.0]]).astype(np.float32)
+    ref, cr = getattr(O, name)(x), unary_cr(name, x)
+    got = getattr(ops, name)(x)
+    assert_ulp(got, ref, 2, 0.99, f"{name} host")
+    assert_ulp(got, cr, 1, 0.9999, f"{name} host vs f64 model")
+    d, y = dev(x), uq.DeviceArray(4 * len(x))
+    ops.unary_d(name, y, d, len(x))
+    uq.synchronize()
+    got = y.download(np.float32, len(x))
+    assert_ulp(got, ref, 2, 0.99, f"{name} device")
+    assert_ulp(got, cr, 1, 0.9999, f"{name} device vs f64 model")
+
+
+@pytest.mark.parametrize("d_conv,channels,n_t", [(4, 8192, 1), (4, 8192, 7), (2, 2, 2)])
+def test_ssm_conv_bit_exact(d_conv, channels, n_t):
+    rng = np.random.default_rng(channels + n_t)
+    x = rng.standard_normal((d_conv - 1 + n_t) * channels).astype(np.float32)
+    k = rng.standard_normal(d_conv * channels).astype(np.float32)
+    ref = O.ssm_conv(x, k, d_conv, channels)
+    assert_bitwise(ops.ssm_conv(x, k, d_conv, channels), ref, "ssm_conv host")
+    dx, dk, dy = dev(x), dev(k), uq.DeviceArray(4 * len(ref))
+    ops.ssm_conv_d(dy, dx, len(x), dk, d_conv, channels)
+    uq.synchronize()
+    assert_bitwise(dy.download(np.float32, len(ref)), ref, "ssm_conv device")
+
+
+def test_gdn_fused_step_heads():
+    rng = np.random.default_rng(10)
+    dim, heads = 128, 8
+    S = (rng.standard_normal((heads, dim, dim)) * 0.1).astype(np.float32)
+    q, k, v = (rng.standard_normal((heads, dim)).astype(np.float32) for _ in range(3))
+    k /= np.linalg.norm(k, axis=1, keepdims=True)
+    gate = np.zeros(heads, np.float32)  # exp(0) = 1 on both sides: bit-exact
+    gate[4:] = rng.uniform(-2, 0, 4)    # general gates: exp may differ by an ulp
+    beta = rng.uniform(0, 1, heads).astype(np.float32)
+    ds, dq, dk, dv, dg, db = dev(S), dev(q), dev(k), dev(v), dev(gate), dev(beta)
+    dout = uq.DeviceArray(4 * heads * dim)
+    ops.gdn_fused_step_d(ds, dout, dq, dk, dv, dg, db, dim, heads, 0.0884)
+    uq.synchronize()
+    gs = ds.download(np.float32, heads * dim * dim).reshape(heads, dim * dim)
+    go = dout.download(np.float32, heads * dim).reshape(heads, dim)
+    for h in range(heads):
+        rs, ro = O.gdn_fused_step(S[h].reshape(-1), q[h], k[h], v[h], float(gate[h]), float(beta[h]), 0.0884)
+        if h < 4:
+            assert_bitwise(gs[h], rs, f"gdn state head {h}")
+            assert_bitwise(go[h], ro, f"gdn out head {h}")
+        else:
+            np.testing.assert_allclose(gs[h], rs, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(go[h], ro, rtol=1e-4, atol=1e-5)
+    # one head through the host mirror
+    rs, ro = O.gdn_fused_step(S[0].reshape(-1), q[0], k[0], v[0], 0.0, float(beta[0]), 0.5)
+    hs, ho = ops.gdn_fused_step(S[0].reshape(-1), q[0], k[0], v[0], 0.0, float(beta[0]), 0.5)
+    assert_bitwise(hs, rs, "gdn host state")
+    assert_bitwise(ho, ro, "gdn host out")
+
+
+@pytest.mark.parametrize("kind", ["llama", "neox"])
+def test_rope_freq(kind):
+    rng = np.random.default_rng(11)
+    n, rows, pos = 256, 32, 1234
+    freqs = (10000.0 ** (-np.arange(n // 2) * 2.0 / n)).astype(np.float32)
+    X = rng.standard_normal((rows, n)).astype(np.float32)
+    ref = np.stack([getattr(O, f"rope_{kind}")(X[r], freqs, pos) for r in range(rows)])
+    assert_ulp(getattr(ops, f"rope_{kind}")(X[0], freqs, pos), ref[0], 1, 0.999, f"rope {kind} host")
+    d, df = dev(X), dev(freqs)
+    ops.rope_d(kind, d, n, rows, df, pos)
+    uq.synchronize()
+    assert_ulp(d.download(np.float32, n * rows), ref.reshape(-1), 1, 0.999, f"rope {kind} device")
+
+
+def test_rope_imrope():
+    rng = np.random.default_rng(12)
+    n, n_rot, rows, pos = 256, 64, 24, 4321
+    theta = float(np.float32(10000.0) ** np.float32(-2.0 / n_rot))
+    X = rng.standard_normal((rows, n)).astype(np.float32)
+    ref = np.stack([O.rope_imrope(X[r], n_rot, theta, pos) for r in range(rows)])
+    assert_ulp(ops.rope_imrope(X[0], n_rot, theta, pos), ref[0], 1, 0.999, "imrope host")
+    d = dev(X)
+    ops.rope_imrope_d(d, n, rows, n_rot, theta, pos)
+    uq.synchronize()
+    assert_ulp(d.download(np.float32, n * rows), ref.reshape(-1), 1, 0.999, "imrope device")
+    kat = ops.rope_imrope([1.0, 99.0, 0.0, 99.0, 7.0, 8.0], 4, 0.01, 1)
+    assert_bitwise(kat, O.rope_imrope([1.0, 99.0, 0.0, 99.0, 7.0, 8.0], 4, 0.01, 1), "imrope kat")

@@ -230,6 +230,14 @@ uq_status host_unpack(uq_dtype dt, const uint8_t *w, size_t nblocks, void *q, vo
 
 }  // namespace
 
+uq_status uq::host_stream(hipStream_t *s) {
+    const uq_status st = check_device();
+    return st ? st : thread_stream(s);
+}
+
+uq_status uq::hip_error(hipError_t e, const char *what) { return hip_fail(e, what); }
+
+
 extern "C" {
 
 const char *uq_last_error(void) { return g_err.c_str(); }

@@ -35,6 +35,24 @@ constexpr int BQ8_0 = 34;
 // on the current device; a no-op after the first call per kernel and device.
 hipError_t allow_lds(const void *kernel, size_t lds);
 
+// Per-layer non-linear ops (uq_ops.hip).
+hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s);
+hipError_t launch_l2norm(float *data, int dim, int rows, float eps, hipStream_t s);
+int softmax_max_len();
+hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s);
+hipError_t launch_unary(int op, const float *x, size_t n, float *out, hipStream_t s);  // 0 sigmoid, 1 silu, 2 softplus
+hipError_t launch_ssm_conv(float *out, const float *x, const float *kern, int d_conv, int channels, int n_t,
+                           hipStream_t s);
+hipError_t launch_gdn_step(float *state, float *out, const float *q, const float *k, const float *v, const float *gate,
+                           const float *beta, int dim, int heads, float scale, hipStream_t s);
+hipError_t launch_rope_freq(int mode, float *x, int rows, int n, const float *freqs, size_t pos, hipStream_t s);
+hipError_t launch_rope_imrope(float *x, int rows, int n, int n_rot, double theta_scale, size_t pos, hipStream_t s);
+
+// For host-pointer entry points: checks for a gfx950 device and returns the
+// calling thread's stream (uq_abi.cpp).
+uq_status host_stream(hipStream_t *s);
+uq_status hip_error(hipError_t e, const char *what);
+
 // Records the calling thread's error message (uq_last_error) and returns s.
 uq_status set_error(uq_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 

@@ -1,0 +1,305 @@
+// Per-layer non-linear kernels of the forward (crates/unltd-tensor/src/
+// kernels.rs), on device so activations stay in HBM between layers. Each
+// kernel follows the reference's arithmetic step for step: f32 steps as
+// separate IEEE operations (built -ffp-contract=off, with explicit _rn
+// intrinsics where the order matters), f64 sums in the reference's order.
+//
+// Sequential f64 sums (rmsnorm, l2_norm_rows) are formed as a tree sum S
+// plus a rigorous bound: for n non-negative terms the sequential sum and S
+// both lie within (n + log2 n + 2) * 2^-53 * S of the exact sum, so when
+// both ends of [S - e, S + e] round to the same f32 result (rounding is
+// monotonic), that is the reference's result. Otherwise (probability about
+// n * 2^-29 per row) one lane replays the sequential loop.
+//
+// Transcendentals: f32 exp / log are evaluated in f64 and rounded once
+// (correctly rounded but for rare near-midpoint arguments), and the rope
+// angles use the f64 sin / cos of the device library; the reference uses
+// the platform libm, so those results agree within about 1 ulp.
+#include "uq_device.h"
+#include "uq_internal.h"
+
+namespace uq {
+
+namespace {
+
+constexpr int OPS_TPB = 256;
+
+__device__ __forceinline__ float logf_cr(float v) { return (float)log((double)v); }
+
+// Correctly rounded f32 square root: the f64 root (correctly rounded) rounded
+// to f32 is the correctly rounded f32 root, since 53 >= 2 * 24 + 2. The f32
+// hardware root alone (v_sqrt_f32) is accurate to 1 ulp only.
+__device__ __forceinline__ float sqrtf_cr(float v) { return (float)__dsqrt_rn((double)v); }
+
+// Sum over the workgroup (f64, fixed tree), returned to every thread.
+template <int TPB>
+__device__ double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < TPB / 64; i++) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+__device__ float block_max_f(float v, float *red) {
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, red[i]);
+    __syncthreads();
+    return t;
+}
+
+// The f32 result of a sequential f64 sum of the n non-negative values
+// sq[i] (f32 squares), mapped through finish(): finish(lo) == finish(hi)
+// proves the result; otherwise thread 0 replays the loop. Every thread
+// returns the same value.
+template <int TPB, class Finish>
+__device__ float seq_sum_f32(const float *__restrict__ sq_src, int n, double S, Finish finish, float *bcast) {
+    const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
+    const float a = finish(S - e), b = finish(S + e);
+    if (a == b) return a;
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int i = 0; i < n; i++) s += (double)__fmul_rn(sq_src[i], sq_src[i]);
+        *bcast = finish(s);
+    }
+    __syncthreads();
+    const float r = *bcast;
+    __syncthreads();
+    return r;
+}
+
+// rmsnorm (kernels.rs:61-78), one workgroup per row of n.
+__global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
+                                                          const float *__restrict__ w, int n, float eps) {
+    __shared__ double red[OPS_TPB / 64];
+    __shared__ float bc;
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = out + (size_t)blockIdx.x * n;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += OPS_TPB) s += (double)__fmul_rn(xr[i], xr[i]);
+    const double S = block_sum_d<OPS_TPB>(s, red);
+    const double dn = (double)n;
+    const float mean = seq_sum_f32<OPS_TPB>(xr, n, S, [dn](double v) { return (float)(v / dn); }, &bc);
+    const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
+    for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+}
+
+// l2_norm_rows (kernels.rs:236-256), in place, one workgroup per row.
+__global__ __launch_bounds__(OPS_TPB) void l2norm_kernel(float *__restrict__ data, int dim, float eps) {
+    __shared__ double red[OPS_TPB / 64];
+    __shared__ float bc;
+    float *r = data + (size_t)blockIdx.x * dim;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < dim; i += OPS_TPB) s += (double)__fmul_rn(r[i], r[i]);
+    const double S = block_sum_d<OPS_TPB>(s, red);
+    const float sum32 = seq_sum_f32<OPS_TPB>(r, dim, S, [](double v) { return (float)v; }, &bc);
+    const float scale = __fdiv_rn(1.0f, fmaxf(sqrtf_cr(sum32), eps));
+    for (int i = threadIdx.x; i < dim; i += OPS_TPB) r[i] = __fmul_rn(r[i], scale);
+}
+
+// softmax (kernels.rs:157-168), one workgroup per row of n <= kSoftmaxMax:
+// the denominator is pairwise_sum_f64 (kernels.rs:27-42) level by level in
+// LDS, pairs (2i, 2i+1) with an odd tail carried up.
+constexpr int kSoftmaxMax = 8192;
+__global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *__restrict__ out, const float *__restrict__ x, int n,
+                                                          float scale) {
+    __shared__ double lv[kSoftmaxMax / 2];
+    __shared__ float red[OPS_TPB / 64];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = out + (size_t)blockIdx.x * n;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += OPS_TPB) m = fmaxf(m, xr[i]);
+    m = block_max_f(m, red);
+    auto ex = [&](int i) { return expf_cr(__fmul_rn(__fsub_rn(xr[i], m), scale)); };
+    // level 1 straight from the exponentials
+    int len = (n + 1) / 2;
+    for (int p = threadIdx.x; p < len; p += OPS_TPB)
+        lv[p] = 2 * p + 1 < n ? (double)ex(2 * p) + (double)ex(2 * p + 1) : (double)ex(2 * p);
+    __syncthreads();
+    while (len > 1) {
+        const int nl = (len + 1) / 2;
+        double v[kSoftmaxMax / 2 / OPS_TPB];
+        int c = 0;
+        for (int p = threadIdx.x; p < nl; p += OPS_TPB, c++) v[c] = 2 * p + 1 < len ? lv[2 * p] + lv[2 * p + 1] : lv[2 * p];
+        __syncthreads();
+        c = 0;
+        for (int p = threadIdx.x; p < nl; p += OPS_TPB, c++) lv[p] = v[c];
+        __syncthreads();
+        len = nl;
+    }
+    const double sum = n == 1 ? (double)ex(0) : lv[0];
+    for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
+}
+
+// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
+__global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, float *__restrict__ out) {
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
+        const float v = x[t];
+        float r;
+        if (op == 0)
+            r = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v)));
+        else if (op == 1)
+            r = __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v)));
+        else
+            r = v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v)));
+        out[t] = r;
+    }
+}
+
+// ssm_conv (kernels.rs:265-305): out[t*channels + c], sequential f32 sum.
+__global__ void ssm_conv_kernel(float *__restrict__ out, const float *__restrict__ x, const float *__restrict__ kern,
+                                int d_conv, int channels, int n_t) {
+    const size_t total = (size_t)n_t * channels;
+    for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total; o += (size_t)gridDim.x * blockDim.x) {
+        const int t = (int)(o / channels), c = (int)(o % channels);
+        float s = 0.0f;
+        for (int tau = 0; tau < d_conv; tau++)
+            s = __fadd_rn(s, __fmul_rn(x[(size_t)(t + tau) * channels + c], kern[(size_t)tau * channels + c]));
+        out[o] = s;
+    }
+}
+
+// gdn_fused_step (kernels.rs:316-375), one workgroup per head, thread j
+// owns column j of the head's dim x dim state: every step of the
+// reference touches column j only through S[:, j], k, q, v[j], so the
+// column is processed alone, with its f64 dots in the reference's order.
+__global__ void gdn_step_kernel(float *__restrict__ state, float *__restrict__ out, const float *__restrict__ q,
+                                const float *__restrict__ k, const float *__restrict__ v,
+                                const float *__restrict__ gate, const float *__restrict__ beta, int dim,
+                                float scale) {
+    const int h = blockIdx.x;
+    float *S = state + (size_t)h * dim * dim;
+    const float *qh = q + (size_t)h * dim, *kh = k + (size_t)h * dim, *vh = v + (size_t)h * dim;
+    const float g_exp = expf_cr(gate[h]), bt = beta[h];
+    for (int j = threadIdx.x; j < dim; j += blockDim.x) {
+        double sum = 0.0;
+        for (int i = 0; i < dim; i++) {
+            const float sv = __fmul_rn(S[(size_t)i * dim + j], g_exp);
+            S[(size_t)i * dim + j] = sv;
+            sum += (double)__fmul_rn(sv, kh[i]);
+        }
+        const float d = __fmul_rn(__fsub_rn(vh[j], (float)sum), bt);
+        double o = 0.0;
+        for (int i = 0; i < dim; i++) {
+            const float sv = __fadd_rn(S[(size_t)i * dim + j], __fmul_rn(kh[i], d));
+            S[(size_t)i * dim + j] = sv;
+            o += (double)__fmul_rn(sv, qh[i]);
+        }
+        out[(size_t)h * dim + j] = __fmul_rn((float)o, scale);
+    }
+}
+
+// The rope rotation (kernels.rs:121-123): f64 sin/cos, fma, rounded to f32.
+__device__ __forceinline__ void rotate_pair(float *a, float *b, double angle) {
+    double s, c;
+    sincos(angle, &s, &c);
+    const double x0 = (double)*a, x1 = (double)*b;
+    *a = (float)fma(c, x0, -(s * x1));
+    *b = (float)fma(s, x0, c * x1);
+}
+
+// mode 0: llama pairs (2i, 2i+1); 1: neox pairs (i, i + n/2); each over
+// rows of n; one thread per pair.
+__global__ void rope_freq_kernel(int mode, float *__restrict__ x, int rows, int n, const float *__restrict__ freqs,
+                                 double pos) {
+    const int half = n / 2;
+    const size_t total = (size_t)rows * half;
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(t / half), i = (int)(t % half);
+        float *xr = x + (size_t)r * n;
+        const double angle = pos * (double)freqs[i];
+        if (mode == 0)
+            rotate_pair(&xr[2 * i], &xr[2 * i + 1], angle);
+        else
+            rotate_pair(&xr[i], &xr[i + half], angle);
+    }
+}
+
+// rope_apply_imrope (kernels.rs:381-400): pair ic rotates when ic % 3 == 0
+// by pos * theta^ic, the product formed by the reference's running
+// multiplication (one f64 rounding per pair before it).
+__global__ void rope_imrope_kernel(float *__restrict__ x, int rows, int n, int n_rot, double theta_scale, double pos) {
+    const int half = n_rot / 2, nrot3 = (half + 2) / 3;
+    const size_t total = (size_t)rows * nrot3;
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(t / nrot3), ic = 3 * (int)(t % nrot3);
+        double angle = pos;
+        for (int i = 0; i < ic; i++) angle *= theta_scale;
+        float *xr = x + (size_t)r * n;
+        rotate_pair(&xr[ic], &xr[ic + half], angle);
+    }
+}
+
+inline unsigned ops_grid(size_t n) {
+    const size_t g = (n + OPS_TPB - 1) / OPS_TPB;
+    return (unsigned)(g < 65535u * 32u ? (g ? g : 1) : 65535u * 32u);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_l2norm(float *data, int dim, int rows, float eps, hipStream_t s) {
+    if (rows == 0 || dim == 0) return hipSuccess;
+    hipLaunchKernelGGL(l2norm_kernel, dim3(rows), dim3(OPS_TPB), 0, s, data, dim, eps);
+    return hipGetLastError();
+}
+
+int softmax_max_len() { return kSoftmaxMax; }
+
+hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (n > kSoftmaxMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_unary(int op, const float *x, size_t n, float *out, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(unary_kernel, dim3(ops_grid(n)), dim3(OPS_TPB), 0, s, op, x, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_ssm_conv(float *out, const float *x, const float *kern, int d_conv, int channels, int n_t,
+                           hipStream_t s) {
+    if (n_t == 0 || channels == 0) return hipSuccess;
+    hipLaunchKernelGGL(ssm_conv_kernel, dim3(ops_grid((size_t)n_t * channels)), dim3(OPS_TPB), 0, s, out, x, kern,
+                       d_conv, channels, n_t);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_step(float *state, float *out, const float *q, const float *k, const float *v, const float *gate,
+                           const float *beta, int dim, int heads, float scale, hipStream_t s) {
+    if (heads == 0 || dim == 0) return hipSuccess;
+    const int tpb = dim >= 256 ? 256 : ((dim + 63) / 64) * 64;
+    hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_freq(int mode, float *x, int rows, int n, const float *freqs, size_t pos, hipStream_t s) {
+    if (rows == 0 || n < 2) return hipSuccess;
+    hipLaunchKernelGGL(rope_freq_kernel, dim3(ops_grid((size_t)rows * (n / 2))), dim3(OPS_TPB), 0, s, mode, x, rows,
+                       n, freqs, (double)pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_imrope(float *x, int rows, int n, int n_rot, double theta_scale, size_t pos, hipStream_t s) {
+    if (rows == 0 || n_rot < 2) return hipSuccess;
+    const int nrot3 = (n_rot / 2 + 2) / 3;
+    hipLaunchKernelGGL(rope_imrope_kernel, dim3(ops_grid((size_t)rows * nrot3)), dim3(OPS_TPB), 0, s, x, rows, n,
+                       n_rot, theta_scale, (double)pos);
+    return hipGetLastError();
+}
+
+}  // namespace uq

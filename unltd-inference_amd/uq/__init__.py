@@ -101,6 +101,29 @@ SIGNATURES = {
     "uq_gguf_kv_string": ([_P, C.c_uint64, C.c_uint64, _P, _P], _I),
     "uq_gguf_type_blocksize": ([C.c_uint32, _P, _P], _I),
     "uq_gguf_type_name": ([C.c_uint32, C.c_char_p, _S], _I),
+    # include/uq_ops.h
+    "uq_rmsnorm": ([_P, _S, _P, _S, _P, _S, C.c_float], _I),
+    "uq_rmsnorm_d": ([_P, _P, _P, _S, _S, C.c_float, _P], _I),
+    "uq_l2_norm_rows": ([_P, _S, _S, C.c_float], _I),
+    "uq_l2_norm_rows_d": ([_P, _S, _S, C.c_float, _P], _I),
+    "uq_softmax": ([_P, _S, _P, _S, C.c_float], _I),
+    "uq_softmax_d": ([_P, _P, _S, _S, C.c_float, _P], _I),
+    "uq_sigmoid": ([_P, _S, _P, _S], _I),
+    "uq_silu": ([_P, _S, _P, _S], _I),
+    "uq_softplus": ([_P, _S, _P, _S], _I),
+    "uq_sigmoid_d": ([_P, _P, _S, _P], _I),
+    "uq_silu_d": ([_P, _P, _S, _P], _I),
+    "uq_softplus_d": ([_P, _P, _S, _P], _I),
+    "uq_ssm_conv": ([_P, _S, _P, _S, _P, _S, _S, _S], _I),
+    "uq_ssm_conv_d": ([_P, _P, _S, _P, _S, _S, _P], _I),
+    "uq_gdn_fused_step": ([_P, _S, _P, _S, _P, _S, _P, _S, _P, _S, C.c_float, C.c_float, C.c_float], _I),
+    "uq_gdn_fused_step_d": ([_P, _P, _P, _P, _P, _P, _P, _S, _S, C.c_float, _P], _I),
+    "uq_rope_llama": ([_P, _S, _P, _S, _S], _I),
+    "uq_rope_neox": ([_P, _S, _P, _S, _S], _I),
+    "uq_rope_llama_d": ([_P, _S, _S, _P, _S, _P], _I),
+    "uq_rope_neox_d": ([_P, _S, _S, _P, _S, _P], _I),
+    "uq_rope_imrope": ([_P, _S, _S, C.c_double, _S], _I),
+    "uq_rope_imrope_d": ([_P, _S, _S, _S, C.c_double, _S, _P], _I),
 }
 
 
