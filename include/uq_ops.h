@@ -44,8 +44,8 @@ uq_status uq_rmsnorm_d(float *d_out, const float *d_x, const float *d_w, size_t 
 uq_status uq_l2_norm_rows(float *data, size_t len, size_t dim, float eps);
 uq_status uq_l2_norm_rows_d(float *d_data, size_t len, size_t dim, float eps, void *stream);
 
-/* softmax (kernels.rs:157-168). Panics: len(out) != len(x). The device
- * form takes rows of n <= 8192 (UQ_ERR_ARG above). */
+/* softmax (kernels.rs:157-168). Panics: len(out) != len(x). Rows of up to
+ * 2^24 values (UQ_ERR_ARG above); the device form may run in place. */
 uq_status uq_softmax(float *out, size_t out_len, const float *x, size_t x_len, float scale);
 uq_status uq_softmax_d(float *d_out, const float *d_x, size_t n, size_t rows, float scale, void *stream);
 
@@ -92,6 +92,27 @@ uq_status uq_rope_neox_d(float *d_x, size_t n, size_t rows, const float *d_freqs
 uq_status uq_rope_imrope(float *x, size_t x_len, size_t n_rot, double theta_scale, size_t pos);
 uq_status uq_rope_imrope_d(float *d_x, size_t n, size_t rows, size_t n_rot, double theta_scale, size_t pos,
                            void *stream);
+
+/* The causal attention of one decode position, step 5 of attn_layer
+ * (qwen35_forward.rs:639-671): for each q head h, with kv head
+ * h / (n_head / n_head_kv),
+ *   scores[p] = (f32) dot_f32(q_h, K[p][kv])   (f64 products, pairwise sum)
+ *   soft_h    = softmax(scores, kq_scale)
+ *   out_h[i]  = (f32) sum over p, in order, of (f64) soft_h[p] * V[p][kv][i].
+ * q and out are [n_head][head_dim]; the caches hold rows [p][n_head_kv]
+ * [head_dim], as the reference's k_cache / v_cache slots; soft [n_head]
+ * [n_ctx] receives the weights. Bit-exact with the reference (softmax's
+ * expf aside, as softmax). Limits: head_dim in {64, 128, 256, 512},
+ * n_head / n_head_kv <= 8, 1 <= n_ctx <= 2^24 (UQ_ERR_ARG otherwise).
+ * Panics of the host form: len(q), len(out) != n_head * head_dim,
+ * len(k_cache) or len(v_cache) < n_ctx * n_head_kv * head_dim (the
+ * reference's cache slices). */
+uq_status uq_attn_decode(float *out, size_t out_len, const float *q, size_t q_len, const float *k_cache,
+                         size_t k_len, const float *v_cache, size_t v_len, size_t n_ctx, size_t n_head,
+                         size_t n_head_kv, size_t head_dim, float kq_scale);
+uq_status uq_attn_decode_d(float *d_out, float *d_soft, const float *d_q, const float *d_k_cache,
+                           const float *d_v_cache, size_t n_ctx, size_t n_head, size_t n_head_kv, size_t head_dim,
+                           float kq_scale, void *stream);
 
 #ifdef __cplusplus
 }

@@ -140,6 +140,11 @@ int or_gdn_fused_step(float *state, float *out, const float *q, const float *k, 
 int or_rope_llama(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
 int or_rope_neox(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
 int or_rope_imrope(float *x, size_t n, size_t n_rot, double theta_scale, size_t pos);
+/* qwen35_forward.rs:639-671: causal attention of one decode position.
+ * q and out are [n_head][hd]; the caches are [n_ctx][n_head_kv][hd]; soft
+ * [n_head][n_ctx] receives each head's softmax weights. */
+int or_attn_decode(float *out, float *soft, const float *q, const float *k_cache, const float *v_cache, size_t n_ctx,
+                   size_t n_head, size_t n_head_kv, size_t hd, float kq_scale);
 
 #ifdef __cplusplus
 }

@@ -353,6 +353,16 @@ def rope_neox(x, freqs, pos: int) -> np.ndarray:
     return y
 
 
+def attn_decode(q, k_cache, v_cache, n_ctx: int, n_head: int, n_head_kv: int, hd: int, kq_scale: float):
+    """qwen35_forward.rs:639-671; returns (out [n_head*hd], soft [n_head*n_ctx])"""
+    q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)
+    out = np.zeros(n_head * hd, np.float32)
+    soft = np.zeros(n_head * n_ctx, np.float32)
+    _ok(_fn("or_attn_decode", [_P, _P, _P, _P, _P, _S, _S, _S, _S, C.c_float])(
+        _p(out), _p(soft), _p(q), _p(kc), _p(vc), n_ctx, n_head, n_head_kv, hd, kq_scale), "attn_decode")
+    return out, soft
+
+
 def rope_imrope(x, n_rot: int, theta_scale: float, pos: int) -> np.ndarray:
     """kernels.rs:381-400"""
     y = _f32(x).copy()

@@ -152,3 +152,32 @@ int or_rope_imrope(float *x, size_t n, size_t n_rot, double theta_scale, size_t 
     }
     return OR_OK;
 }
+
+/* qwen35_forward.rs:639-671, step 5 of attn_layer: q head h reads kv head
+ * h / (n_head / n_head_kv); scores[p] = (f32) dot_f32(q_h, K[p]) (f64
+ * products, pairwise sum); soft = softmax(scores, kq_scale); out_h[i] =
+ * (f32) of the sequential f64 sum over p of soft[p] * V[p][i]. */
+int or_attn_decode(float *out, float *soft, const float *q, const float *k_cache, const float *v_cache, size_t n_ctx,
+                   size_t n_head, size_t n_head_kv, size_t hd, float kq_scale) {
+    if (n_head_kv == 0 || n_head % n_head_kv || n_ctx == 0) return OR_ERR_LEN;
+    const size_t group = n_head / n_head_kv, kv_len = n_head_kv * hd;
+    float *scores = malloc(n_ctx * sizeof(float));
+    if (!scores) return OR_ERR_ALLOC;
+    for (size_t h = 0; h < n_head; h++) {
+        const size_t kv = h / group;
+        float *sh = soft + h * n_ctx;
+        for (size_t p = 0; p < n_ctx; p++) scores[p] = (float)or_dot_f32(q + h * hd, k_cache + p * kv_len + kv * hd, hd);
+        const int rc = or_softmax(sh, scores, n_ctx, kq_scale);
+        if (rc != OR_OK) {
+            free(scores);
+            return rc;
+        }
+        for (size_t i = 0; i < hd; i++) {
+            double sum = 0.0;
+            for (size_t p = 0; p < n_ctx; p++) sum += (double)sh[p] * (double)v_cache[p * kv_len + kv * hd + i];
+            out[h * hd + i] = (float)sum;
+        }
+    }
+    free(scores);
+    return OR_OK;
+}

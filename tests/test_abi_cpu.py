@@ -124,6 +124,16 @@ def test_ops_argument_errors_mirror_reference_panics():  # kernels.rs asserts, b
     assert uq.STATUS[L.uq_rope_neox(P(f), 4, P(f), 1, 1)] == "LEN"
     assert uq.STATUS[L.uq_rope_imrope(P(f), 4, 3, 0.5, 1)] == "LEN"
     assert uq.STATUS[L.uq_rope_imrope(P(f), 4, 6, 0.5, 1)] == "LEN"
+    # attention: shape limits, then the slice lengths
+    g = np.zeros(256, np.float32)
+    assert uq.STATUS[L.uq_attn_decode(P(g), 128, P(g), 128, P(g), 64, P(g), 64, 1, 2, 3, 64, 1.0)] == "ARG"  # 2 % 3
+    assert uq.STATUS[L.uq_attn_decode(P(g), 96, P(g), 96, P(g), 96, P(g), 96, 1, 1, 1, 96, 1.0)] == "ARG"   # head_dim
+    assert uq.STATUS[L.uq_attn_decode(P(g), 64, P(g), 64, P(g), 64, P(g), 64, 0, 1, 1, 64, 1.0)] == "ARG"   # n_ctx 0
+    assert uq.STATUS[L.uq_attn_decode(P(g), 64, P(g), 32, P(g), 64, P(g), 64, 1, 1, 1, 64, 1.0)] == "LEN"   # len(q)
+    assert uq.STATUS[L.uq_attn_decode(P(g), 64, P(g), 64, P(g), 63, P(g), 64, 1, 1, 1, 64, 1.0)] == "LEN"   # len(k)
+    assert uq.STATUS[L.uq_attn_decode(P(g), 64, P(g), 64, P(g), 64, P(g), 127, 2, 1, 1, 64, 1.0)] == "LEN"  # len(v)
+    assert uq.STATUS[L.uq_attn_decode(P(g), 63, P(g), 64, P(g), 64, P(g), 64, 1, 1, 1, 64, 1.0)] == "LEN"   # len(out)
+    assert uq.STATUS[L.uq_attn_decode_d(P(g), P(g), P(g), P(g), P(g), 1, 18, 2, 64, 1.0, None)] == "ARG"  # group 9
     if uq.device_count() == 0:
         with pytest.raises(uq.UqError) as e:
             ops.rmsnorm(f, f, 1e-6)

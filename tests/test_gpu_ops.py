@@ -115,6 +115,23 @@ def unary_cr(name, x):
     return (f(1) if name == "sigmoid" else x) / (f(1) + e)
 
 
+@pytest.mark.parametrize("n", [8193, 16384, 16385, 40000])
+def test_softmax_rows_beyond_one_chunk(n):
+    """Rows longer than the 8192-value LDS chunk: the denominator is the tree
+    over chunk sums, which must equal the pairwise tree over the whole row."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 4).astype(np.float32)
+    assert_ulp(ops.softmax(x, 0.3), O.softmax(x, 0.3), 2, 0.99, f"softmax n={n}")
+    # in place on the device, two rows
+    X = np.stack([x, x[::-1]]).astype(np.float32)
+    d = dev(X)
+    ops.softmax_d(d, d, n, 2, 0.3)
+    uq.synchronize()
+    got = d.download(np.float32, 2 * n).reshape(2, n)
+    assert_ulp(got[0], O.softmax(X[0], 0.3), 2, 0.99, "softmax in place row 0")
+    assert_ulp(got[1], O.softmax(X[1], 0.3), 2, 0.99, "softmax in place row 1")
+
+
 @pytest.mark.parametrize("name", ["sigmoid", "silu", "softplus"])
 def test_unary_within_2_ulp(name):
     """Within 2 ulp of the oracle (the C library's expf / logf, as the
@@ -207,3 +224,65 @@ def test_rope_imrope():
     assert_ulp(d.download(np.float32, n * rows), ref.reshape(-1), 1, 0.999, "imrope device")
     kat = ops.rope_imrope([1.0, 99.0, 0.0, 99.0, 7.0, 8.0], 4, 0.01, 1)
     assert_bitwise(kat, O.rope_imrope([1.0, 99.0, 0.0, 99.0, 7.0, 8.0], 4, 0.01, 1), "imrope kat")
+
+
+def attn_case(seed, n_ctx, nh, nhkv, hd, spare=0):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal((n_ctx + spare) * nhkv * hd).astype(np.float32)
+    vc = rng.standard_normal((n_ctx + spare) * nhkv * hd).astype(np.float32)
+    return q, kc, vc
+
+
+def check_attn(q, kc, vc, n_ctx, nh, nhkv, hd, scale, what, bit_exact_soft=False):
+    ref, rsoft = O.attn_decode(q, kc, vc, n_ctx, nh, nhkv, hd, scale)
+    dq, dk, dv = dev(q), dev(kc), dev(vc)
+    dout, dsoft = uq.DeviceArray(4 * nh * hd), uq.DeviceArray(4 * nh * n_ctx)
+    ops.attn_decode_d(dout, dsoft, dq, dk, dv, n_ctx, nh, nhkv, hd, scale)
+    uq.synchronize()
+    got, soft = dout.download(np.float32, nh * hd), dsoft.download(np.float32, nh * n_ctx)
+    if bit_exact_soft:
+        assert_bitwise(soft, rsoft, f"{what} soft")
+        assert_bitwise(got, ref, f"{what} out")
+    else:
+        # softmax's expf may differ from the C library's by an ulp; where the
+        # weights agree bit for bit, out must too
+        assert_ulp(soft, rsoft, 2, 0.99, f"{what} soft")
+        for h in range(nh):
+            if np.array_equal(bits(soft[h * n_ctx:(h + 1) * n_ctx]), bits(rsoft[h * n_ctx:(h + 1) * n_ctx])):
+                assert_bitwise(got[h * hd:(h + 1) * hd], ref[h * hd:(h + 1) * hd], f"{what} head {h}")
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+    return got
+
+
+@pytest.mark.parametrize("n_ctx,nh,nhkv,hd", [(1, 16, 4, 256), (7, 16, 4, 256), (300, 16, 4, 256),
+                                              (2049, 16, 4, 256), (33, 8, 8, 64), (100, 16, 2, 128),
+                                              (65, 8, 1, 512)])
+def test_attn_decode_matches_the_reference_loop(n_ctx, nh, nhkv, hd):
+    q, kc, vc = attn_case(n_ctx * 7 + hd, n_ctx, nh, nhkv, hd, spare=3)  # caches longer than n_ctx, as in a session
+    check_attn(q, kc, vc, n_ctx, nh, nhkv, hd, 1.0 / np.sqrt(hd), f"attn n_ctx={n_ctx} hd={hd}")
+    if n_ctx == 300:
+        out = ops.attn_decode(q, kc, vc, n_ctx, nh, nhkv, hd, 1.0 / np.sqrt(hd))
+        ref, _ = O.attn_decode(q, kc, vc, n_ctx, nh, nhkv, hd, 1.0 / np.sqrt(hd))
+        np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_attn_decode_order_adversaries_take_the_replay():
+    """Equal keys (weights exactly 1/n_ctx, so bit-exact) and value columns
+    with cancellation: [2^62, 1, -2^62, 1] sums to 0.25 only in sequential
+    order, so the parallel bound cannot decide and the lane replays; the
+    pairwise score adversary of dot_f32 gives weights [0.5, 0.5]."""
+    hd, n_ctx = 64, 4
+    q = np.ones(hd, np.float32)
+    kc = np.ones(n_ctx * hd, np.float32)
+    col = np.array([2.0 ** 62, 1.0, -(2.0 ** 62), 1.0], np.float32)
+    vc = np.repeat(col, hd).astype(np.float32)
+    vc[1::2] *= -1.0  # half the columns sum to -0.25 ... mixed signs across lanes
+    got = check_attn(q, kc, vc, n_ctx, 1, 1, hd, 1.0, "adversary", bit_exact_soft=True)
+    assert set(np.abs(got).tolist()) == {0.25}
+    kq = np.zeros(2 * hd, np.float32)
+    kq[:4] = [2.0 ** 60, 1.0, -(2.0 ** 60), 1.0]
+    vv = np.concatenate([np.ones(hd), np.zeros(hd)]).astype(np.float32)
+    got = check_attn(q, kq, vv, 2, 1, 1, hd, 1.0, "score adversary", bit_exact_soft=True)
+    assert got.tolist() == [0.5] * hd
+

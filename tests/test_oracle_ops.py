@@ -243,3 +243,70 @@ def test_rope_imrope_angle_is_the_running_product():
             exp[ic], exp[ic + n_rot // 2] = _rot(x[ic], x[ic + n_rot // 2], angle)
         angle *= theta
     assert bits(got).tolist() == bits(exp).tolist()
+
+
+def _attn_f64(q, kc, vc, n_ctx, nh, nhkv, hd, scale):
+    """A float64 restatement for closeness (not bit-level) checks."""
+    G = nh // nhkv
+    K = kc[: n_ctx * nhkv * hd].reshape(n_ctx, nhkv, hd).astype(np.float64)
+    V = vc[: n_ctx * nhkv * hd].reshape(n_ctx, nhkv, hd).astype(np.float64)
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        s = K[:, h // G, :] @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ V[:, h // G, :]
+    return out.reshape(-1)
+
+
+def test_attn_decode_single_position_returns_v_of_the_heads_kv():  # qwen35_forward.rs:639-671
+    """n_ctx = 1: soft = [1.0] and out_h = V[kv(h)] exactly; kv(h) = h / group
+    (consecutive heads share a kv head, not h % n_head_kv)."""
+    rng = np.random.default_rng(20)
+    nh, nhkv, hd = 4, 2, 8
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal(nhkv * hd).astype(np.float32)
+    vc = rng.standard_normal(nhkv * hd).astype(np.float32)
+    out, soft = O.attn_decode(q, kc, vc, 1, nh, nhkv, hd, 0.125)
+    assert soft.tolist() == [1.0] * nh
+    V = vc.reshape(nhkv, hd)
+    assert bits(out).tolist() == bits(np.concatenate([V[0], V[0], V[1], V[1]])).tolist()
+
+
+def test_attn_decode_value_sum_is_sequential_in_position():
+    """Equal keys give soft = 1/4 exactly; the column [2^62, 1, -2^62, 1]
+    then sums to 0.25 in the reference's sequential order (the pairwise
+    order, or the reversed one, gives 0)."""
+    hd, n_ctx = 4, 4
+    q = np.ones(hd, np.float32)
+    kc = np.ones(n_ctx * hd, np.float32)
+    col = [2.0 ** 62, 1.0, -(2.0 ** 62), 1.0]
+    vc = np.array([[c] * hd for c in col], np.float32).reshape(-1)
+    out, soft = O.attn_decode(q, kc, vc, n_ctx, 1, 1, hd, 1.0)
+    assert soft.tolist() == [0.25] * 4
+    assert out.tolist() == [0.25] * hd
+
+
+def test_attn_decode_scores_use_the_pairwise_dot():
+    """Key 0's products [2^60, 1, -2^60, 1] sum to 0 in the pairwise tree
+    (1 sequentially); key 1 scores 0: the weights are [0.5, 0.5] only if the
+    score is dot_f32's pairwise sum."""
+    hd = 4
+    q = np.ones(hd, np.float32)
+    kc = np.array([2.0 ** 60, 1.0, -(2.0 ** 60), 1.0, 0, 0, 0, 0], np.float32)
+    vc = np.array([1.0] * hd + [0.0] * hd, np.float32)
+    out, soft = O.attn_decode(q, kc, vc, 2, 1, 1, hd, 1.0)
+    assert soft.tolist() == [0.5, 0.5]
+    assert out.tolist() == [0.5] * hd
+
+
+def test_attn_decode_close_to_float64_attention():
+    rng = np.random.default_rng(21)
+    for n_ctx, nh, nhkv, hd in [(1, 2, 1, 16), (7, 4, 2, 32), (50, 8, 2, 64)]:
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        kc = rng.standard_normal(n_ctx * nhkv * hd).astype(np.float32)
+        vc = rng.standard_normal(n_ctx * nhkv * hd).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        out, soft = O.attn_decode(q, kc, vc, n_ctx, nh, nhkv, hd, scale)
+        np.testing.assert_allclose(out, _attn_f64(q, kc, vc, n_ctx, nh, nhkv, hd, scale), rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(soft.reshape(nh, n_ctx).sum(axis=1), 1.0, rtol=1e-6)
+

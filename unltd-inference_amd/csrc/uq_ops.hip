@@ -63,7 +63,7 @@ template <int TPB, class Finish>
 __device__ float seq_sum_f32(const float *__restrict__ sq_src, int n, double S, Finish finish, float *bcast) {
     const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
     const float a = finish(S - e), b = finish(S + e);
-    if (a == b) return a;
+    if (__float_as_uint(a) == __float_as_uint(b)) return a;  // -0 and +0 differ: replay
     if (threadIdx.x == 0) {
         double s = 0.0;
         for (int i = 0; i < n; i++) s += (double)__fmul_rn(sq_src[i], sq_src[i]);
@@ -104,28 +104,14 @@ __global__ __launch_bounds__(OPS_TPB) void l2norm_kernel(float *__restrict__ dat
     for (int i = threadIdx.x; i < dim; i += OPS_TPB) r[i] = __fmul_rn(r[i], scale);
 }
 
-// softmax (kernels.rs:157-168), one workgroup per row of n <= kSoftmaxMax:
-// the denominator is pairwise_sum_f64 (kernels.rs:27-42) level by level in
-// LDS, pairs (2i, 2i+1) with an odd tail carried up.
-constexpr int kSoftmaxMax = 8192;
-__global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *__restrict__ out, const float *__restrict__ x, int n,
-                                                          float scale) {
-    __shared__ double lv[kSoftmaxMax / 2];
-    __shared__ float red[OPS_TPB / 64];
-    const float *xr = x + (size_t)blockIdx.x * n;
-    float *yr = out + (size_t)blockIdx.x * n;
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += OPS_TPB) m = fmaxf(m, xr[i]);
-    m = block_max_f(m, red);
-    auto ex = [&](int i) { return expf_cr(__fmul_rn(__fsub_rn(xr[i], m), scale)); };
-    // level 1 straight from the exponentials
-    int len = (n + 1) / 2;
-    for (int p = threadIdx.x; p < len; p += OPS_TPB)
-        lv[p] = 2 * p + 1 < n ? (double)ex(2 * p) + (double)ex(2 * p + 1) : (double)ex(2 * p);
-    __syncthreads();
+// Pairwise tree (kernels.rs:27-42) of lv[0, len) in LDS, level by level:
+// pairs (2i, 2i+1), an odd tail carried up. Every thread takes part;
+// returns lv[0] to all (len <= 2 * OPS_TPB * kTreeRegs).
+constexpr int kTreeRegs = 16;
+__device__ double lds_tree(double *lv, int len) {
     while (len > 1) {
         const int nl = (len + 1) / 2;
-        double v[kSoftmaxMax / 2 / OPS_TPB];
+        double v[kTreeRegs];
         int c = 0;
         for (int p = threadIdx.x; p < nl; p += OPS_TPB, c++) v[c] = 2 * p + 1 < len ? lv[2 * p] + lv[2 * p + 1] : lv[2 * p];
         __syncthreads();
@@ -134,7 +120,44 @@ __global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *__restrict__ ou
         __syncthreads();
         len = nl;
     }
-    const double sum = n == 1 ? (double)ex(0) : lv[0];
+    const double r = lv[0];
+    __syncthreads();
+    return r;
+}
+
+// softmax (kernels.rs:157-168), one workgroup per row, in place allowed.
+// The denominator is pairwise_sum_f64 over the row. For a chunk size C that
+// is a power of two, level log2(C) of that tree holds the trees of the full
+// C-chunks followed by the tree of the remainder (whose node is always the
+// carried odd tail below that level), so the row sum is the pairwise tree
+// over the chunk sums: each chunk is reduced in LDS, then the chunk sums.
+constexpr int kSmChunk = 2 * OPS_TPB * kTreeRegs;  // 8192
+constexpr int kSmMaxChunks = 2048;
+static_assert((kSmChunk & (kSmChunk - 1)) == 0, "chunk trees must be nodes of the row tree");
+__global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const float *x, int n, float scale) {
+    __shared__ double lv[kSmChunk / 2];
+    __shared__ double cs[kSmMaxChunks];
+    __shared__ float red[OPS_TPB / 64];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = out + (size_t)blockIdx.x * n;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += OPS_TPB) m = fmaxf(m, xr[i]);
+    m = block_max_f(m, red);
+    auto ex = [&](int i) { return expf_cr(__fmul_rn(__fsub_rn(xr[i], m), scale)); };
+    const int nch = (n + kSmChunk - 1) / kSmChunk;
+    for (int c = 0; c < nch; c++) {
+        const int base = c * kSmChunk, cl = min(kSmChunk, n - base);
+        const int len = (cl + 1) / 2;  // level 1 straight from the exponentials
+        for (int p = threadIdx.x; p < len; p += OPS_TPB) {
+            const int i = base + 2 * p;
+            lv[p] = 2 * p + 1 < cl ? (double)ex(i) + (double)ex(i + 1) : (double)ex(i);
+        }
+        __syncthreads();
+        const double t = lds_tree(lv, len);
+        if (threadIdx.x == 0) cs[c] = t;
+    }
+    __syncthreads();
+    const double sum = lds_tree(cs, nch);
     for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
 }
 
@@ -237,6 +260,112 @@ __global__ void rope_imrope_kernel(float *__restrict__ x, int rows, int n, int n
     }
 }
 
+// ---- decode attention (qwen35_forward.rs:639-671) ----
+// Caches are [n_ctx][n_head_kv][hd] f32; q head h reads kv head h / group
+// (group = n_head / n_head_kv, consecutive heads share a kv head).
+
+// Pairwise sum (kernels.rs:21-42) of 64 * E values, lane l holding values
+// [E*l, E*l + E). For a power-of-two count the tree adds adjacent nodes
+// level by level: the lane-local tree, then the xor butterfly over lanes
+// (both lanes of a pair form the same node: f64 addition is commutative).
+template <int E>
+__device__ double wave_pairwise(double (&t)[E]) {
+#pragma unroll
+    for (int w = E; w > 1; w /= 2)
+#pragma unroll
+        for (int j = 0; j < w / 2; j++) t[j] = t[2 * j] + t[2 * j + 1];
+    double s = t[0];
+#pragma unroll
+    for (int off = 1; off < 64; off *= 2) s = s + __shfl_xor(s, off);
+    return s;
+}
+
+constexpr int kAttnMaxGroup = 8;
+constexpr int kScoresPPB = 32;  // positions per workgroup (8 per wave)
+
+// scores[h][p] = (f32) dot_f32(q_h, K[p][kv]) for the group's heads; one
+// wave per position, E = hd / 64 values per lane.
+template <int E>
+__global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict__ scores, const float *__restrict__ q,
+                                                              const float *__restrict__ kc, int n_ctx, int n_head_kv,
+                                                              int group) {
+    constexpr int HD = 64 * E;
+    __shared__ float qs[kAttnMaxGroup * HD];
+    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int t = threadIdx.x; t < group * HD; t += OPS_TPB) qs[t] = q[(size_t)kv * group * HD + t];
+    __syncthreads();
+    const size_t kv_len = (size_t)n_head_kv * HD;
+    const int p1 = min(n_ctx, (int)(blockIdx.x + 1) * kScoresPPB);
+    for (int p = blockIdx.x * kScoresPPB + w; p < p1; p += OPS_TPB / 64) {
+        const float *kr = kc + (size_t)p * kv_len + (size_t)kv * HD + lane * E;
+        float kx[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) kx[e] = kr[e];
+        for (int g = 0; g < group; g++) {
+            double t[E];
+#pragma unroll
+            for (int e = 0; e < E; e++) t[e] = (double)qs[g * HD + lane * E + e] * (double)kx[e];
+            const double sc = wave_pairwise<E>(t);
+            if (lane == 0) scores[(size_t)(kv * group + g) * n_ctx + p] = (float)sc;
+        }
+    }
+}
+
+// out[h][i] = (f32) of the sequential f64 sum over p of soft[h][p] * V[p][i]
+// (every product exact in f64). Lane = column i, the waves split p; the
+// partial sums S and absolute sums A meet in LDS. Any summation order of
+// n terms lies within gamma_n * A of the exact sum, so the sequential sum
+// lies in [S - e, S + e], e = (n + 66) 2^-52 A (with room for the rounding
+// of e and S +- e); when both ends round to the same f32 (same bits) that
+// is the reference's value, else the lane replays the sequential loop.
+constexpr int kPvWaves = 8;
+__global__ __launch_bounds__(kPvWaves * 64) void attn_pv_kernel(float *__restrict__ out, const float *__restrict__ soft,
+                                                                const float *__restrict__ vc, int n_ctx, int n_head_kv,
+                                                                int hd, int group) {
+    __shared__ double part[2][kPvWaves][kAttnMaxGroup][64];
+    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int i = blockIdx.x * 64 + lane;
+    const size_t kv_len = (size_t)n_head_kv * hd;
+    const float *vcol = vc + (size_t)kv * hd + i;
+    const float *sr = soft + (size_t)kv * group * n_ctx;
+    double S[kAttnMaxGroup], A[kAttnMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kAttnMaxGroup; g++) S[g] = A[g] = 0.0;
+    for (int p = w; p < n_ctx; p += kPvWaves) {
+        const double v = (double)vcol[(size_t)p * kv_len];
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; g++)
+            if (g < group) {
+                const double t = (double)sr[(size_t)g * n_ctx + p] * v;
+                S[g] += t;
+                A[g] += fabs(t);
+            }
+    }
+#pragma unroll
+    for (int g = 0; g < kAttnMaxGroup; g++) {
+        part[0][w][g][lane] = S[g];
+        part[1][w][g][lane] = A[g];
+    }
+    __syncthreads();
+    if (w < group) {
+        const int g = w;
+        double st = 0.0, at = 0.0;
+        for (int u = 0; u < kPvWaves; u++) {
+            st += part[0][u][g][lane];
+            at += part[1][u][g][lane];
+        }
+        const double e = (double)(n_ctx + 66) * 0x1p-52 * at;
+        const float lo = (float)(st - e), hi = (float)(st + e);
+        float r = lo;
+        if (__float_as_uint(lo) != __float_as_uint(hi)) {
+            double q = 0.0;
+            for (int p = 0; p < n_ctx; p++) q += (double)sr[(size_t)g * n_ctx + p] * (double)vcol[(size_t)p * kv_len];
+            r = (float)q;
+        }
+        out[(size_t)(kv * group + g) * hd + i] = r;
+    }
+}
+
 inline unsigned ops_grid(size_t n) {
     const size_t g = (n + OPS_TPB - 1) / OPS_TPB;
     return (unsigned)(g < 65535u * 32u ? (g ? g : 1) : 65535u * 32u);
@@ -256,11 +385,11 @@ hipError_t launch_l2norm(float *data, int dim, int rows, float eps, hipStream_t 
     return hipGetLastError();
 }
 
-int softmax_max_len() { return kSoftmaxMax; }
+int softmax_max_len() { return kSmChunk * kSmMaxChunks; }
 
 hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
-    if (n > kSoftmaxMax) return hipErrorInvalidValue;
+    if (n > softmax_max_len()) return hipErrorInvalidValue;
     hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale);
     return hipGetLastError();
 }
@@ -299,6 +428,30 @@ hipError_t launch_rope_imrope(float *x, int rows, int n, int n_rot, double theta
     const int nrot3 = (n_rot / 2 + 2) / 3;
     hipLaunchKernelGGL(rope_imrope_kernel, dim3(ops_grid((size_t)rows * nrot3)), dim3(OPS_TPB), 0, s, x, rows, n,
                        n_rot, theta_scale, (double)pos);
+    return hipGetLastError();
+}
+
+bool attn_shape_ok(int hd, int group) {
+    return (hd == 64 || hd == 128 || hd == 256 || hd == 512) && group >= 1 && group <= kAttnMaxGroup;
+}
+
+hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
+                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s) {
+    if (n_ctx <= 0 || n_head_kv <= 0) return hipSuccess;
+    if (!attn_shape_ok(hd, group) || n_ctx > softmax_max_len()) return hipErrorInvalidValue;
+    const dim3 gs((n_ctx + kScoresPPB - 1) / kScoresPPB, n_head_kv);
+    switch (hd) {
+        case 64: hipLaunchKernelGGL(attn_scores_kernel<1>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
+        case 128: hipLaunchKernelGGL(attn_scores_kernel<2>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
+        case 256: hipLaunchKernelGGL(attn_scores_kernel<4>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
+        default: hipLaunchKernelGGL(attn_scores_kernel<8>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_pv_kernel, dim3(hd / 64, n_head_kv), dim3(kPvWaves * 64), 0, s, out, soft, vc, n_ctx,
+                       n_head_kv, hd, group);
     return hipGetLastError();
 }
 

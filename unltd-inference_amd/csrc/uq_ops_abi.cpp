@@ -312,3 +312,48 @@ uq_status uq_rope_imrope_d(float *d_x, size_t n, size_t rows, size_t n_rot, doub
 }
 
 }  // extern "C"
+
+namespace {
+uq_status attn_shape(const char *fn, size_t n_ctx, size_t n_head, size_t n_head_kv, size_t head_dim) {
+    if (n_head_kv == 0 || n_head == 0 || n_head % n_head_kv)
+        return set_error(UQ_ERR_ARG, "%s: n_head %zu is not a multiple of n_head_kv %zu", fn, n_head, n_head_kv);
+    if (n_head / n_head_kv > 8 || head_dim > 512 || !uq::attn_shape_ok((int)head_dim, (int)(n_head / n_head_kv)))
+        return set_error(UQ_ERR_ARG, "%s: head_dim %zu / group %zu outside {64,128,256,512} / 1..8", fn, head_dim,
+                         n_head / n_head_kv);
+    if (n_ctx == 0 || n_ctx > (size_t)uq::softmax_max_len())
+        return set_error(UQ_ERR_ARG, "%s: n_ctx %zu outside 1..%d", fn, n_ctx, uq::softmax_max_len());
+    if (n_head > 65536) return too_big(fn, n_head);
+    return UQ_OK;
+}
+}  // namespace
+
+uq_status uq_attn_decode(float *out, size_t out_len, const float *q, size_t q_len, const float *k_cache,
+                         size_t k_len, const float *v_cache, size_t v_len, size_t n_ctx, size_t n_head,
+                         size_t n_head_kv, size_t head_dim, float kq_scale) {
+    if (uq_status st = attn_shape("attn_decode", n_ctx, n_head, n_head_kv, head_dim)) return st;
+    const size_t nq = n_head * head_dim, cache = n_ctx * n_head_kv * head_dim;
+    if (q_len != nq) return set_error(UQ_ERR_LEN, "attn_decode: len(q) %zu != %zu", q_len, nq);
+    if (k_len < cache) return set_error(UQ_ERR_LEN, "attn_decode: len(k_cache) %zu < %zu", k_len, cache);
+    if (v_len < cache) return set_error(UQ_ERR_LEN, "attn_decode: len(v_cache) %zu < %zu", v_len, cache);
+    if (out_len != nq) return set_error(UQ_ERR_LEN, "attn_decode: len(out) %zu != %zu", out_len, nq);
+    if (!out || !q || !k_cache || !v_cache) return set_error(UQ_ERR_ARG, "attn_decode: null pointer");
+    HostCall h("attn_decode");
+    float *dq = h.in(q, nq), *dk = h.in(k_cache, cache), *dv = h.in(v_cache, cache);
+    float *dy = h.out(nq), *ds = h.out(n_head * n_ctx);
+    if (h.status()) return h.status();
+    h.launched(uq::launch_attn_decode(dy, ds, dq, dk, dv, (int)n_ctx, (int)n_head_kv, (int)head_dim,
+                                      (int)(n_head / n_head_kv), kq_scale, h.stream()));
+    h.back(out, dy, nq);
+    return h.finish();
+}
+
+uq_status uq_attn_decode_d(float *d_out, float *d_soft, const float *d_q, const float *d_k_cache,
+                           const float *d_v_cache, size_t n_ctx, size_t n_head, size_t n_head_kv, size_t head_dim,
+                           float kq_scale, void *stream) {
+    if (uq_status st = attn_shape("attn_decode_d", n_ctx, n_head, n_head_kv, head_dim)) return st;
+    if (!d_out || !d_soft || !d_q || !d_k_cache || !d_v_cache)
+        return set_error(UQ_ERR_ARG, "attn_decode_d: null device pointer");
+    return hip_st(uq::launch_attn_decode(d_out, d_soft, d_q, d_k_cache, d_v_cache, (int)n_ctx, (int)n_head_kv,
+                                         (int)head_dim, (int)(n_head / n_head_kv), kq_scale, (hipStream_t)stream),
+                  "attn_decode_d");
+}

@@ -124,6 +124,8 @@ SIGNATURES = {
     "uq_rope_neox_d": ([_P, _S, _S, _P, _S, _P], _I),
     "uq_rope_imrope": ([_P, _S, _S, C.c_double, _S], _I),
     "uq_rope_imrope_d": ([_P, _S, _S, _S, C.c_double, _S, _P], _I),
+    "uq_attn_decode": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _S, C.c_float], _I),
+    "uq_attn_decode_d": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, C.c_float, _P], _I),
 }
 
 

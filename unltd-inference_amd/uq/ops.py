@@ -128,3 +128,22 @@ def rope_imrope(x, n_rot: int, theta_scale: float, pos: int) -> np.ndarray:
 
 def rope_imrope_d(d_x: DeviceArray, n: int, rows: int, n_rot: int, theta_scale: float, pos: int, stream=None):
     _check(lib().uq_rope_imrope_d(d_x.ptr, n, rows, n_rot, theta_scale, pos, stream))
+
+
+def attn_decode(q, k_cache, v_cache, n_ctx: int, n_head: int, n_head_kv: int, head_dim: int,
+                kq_scale: float) -> np.ndarray:
+    """qwen35_forward.rs:639-671 (step 5 of attn_layer): the attention of one
+    decode position over n_ctx cached positions; returns out [n_head*head_dim]."""
+    q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)
+    out = np.zeros(n_head * head_dim, np.float32)
+    _check(lib().uq_attn_decode(_ptr(out), len(out), _ptr(q), len(q), _ptr(kc), len(kc), _ptr(vc), len(vc),
+                                n_ctx, n_head, n_head_kv, head_dim, kq_scale))
+    return out
+
+
+def attn_decode_d(d_out: DeviceArray, d_soft: DeviceArray, d_q: DeviceArray, d_k_cache: DeviceArray,
+                  d_v_cache: DeviceArray, n_ctx: int, n_head: int, n_head_kv: int, head_dim: int, kq_scale: float,
+                  stream=None):
+    _check(lib().uq_attn_decode_d(d_out.ptr, d_soft.ptr, d_q.ptr, d_k_cache.ptr, d_v_cache.ptr, n_ctx, n_head,
+                                  n_head_kv, head_dim, kq_scale, stream))
+
