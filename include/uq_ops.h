@@ -1,8 +1,9 @@
 /*
- * uq_ops.h -- per-layer non-linear kernels of libuq.so, the functions of
- * crates/unltd-tensor/src/kernels.rs that the Qwen3.5 forward runs between
- * its quantized projections, so activations can stay in HBM from one layer
- * to the next.
+ * uq_ops.h -- per-layer kernels of libuq.so: every public function of
+ * crates/unltd-tensor/src/kernels.rs (the ones the Qwen3.5 forward runs
+ * between its quantized projections, and the rest of that file's surface)
+ * plus the decode attention of qwen35_forward.rs, so activations can stay in
+ * HBM from one layer to the next.
  *
  * Each function has a host-pointer mirror with the reference's arguments
  * (slices as pointer + length; panics as uq_status codes, UQ_ERR_LEN for the
@@ -92,6 +93,30 @@ uq_status uq_rope_neox_d(float *d_x, size_t n, size_t rows, const float *d_freqs
 uq_status uq_rope_imrope(float *x, size_t x_len, size_t n_rot, double theta_scale, size_t pos);
 uq_status uq_rope_imrope_d(float *d_x, size_t n, size_t rows, size_t n_rot, double theta_scale, size_t pos,
                            void *stream);
+
+/* gelu_tanh (kernels.rs:185-194), in f64 with the device's tanh: within
+ * 1 ulp of the reference (its libm tanh may differ in the last f64 bit).
+ * Panics: len(out) != len(x). */
+uq_status uq_gelu_tanh(float *out, size_t out_len, const float *x, size_t x_len);
+uq_status uq_gelu_tanh_d(float *d_out, const float *d_x, size_t n, void *stream);
+
+/* matmul_f32_acc (kernels.rs:87-101): acc[m][n] += a[m][k] @ b[k][n], each
+ * element f32((f64)acc + pairwise f64 sum of the exact products), bit-exact.
+ * Panics: len(a) != m*k, len(b) != k*n, len(acc) != m*n. k <= 2^18
+ * (UQ_ERR_ARG above). */
+uq_status uq_matmul_f32_acc(float *acc, size_t acc_len, const float *a, size_t a_len, const float *b, size_t b_len,
+                            size_t m, size_t k, size_t n);
+uq_status uq_matmul_f32_acc_d(float *d_acc, const float *d_a, const float *d_b, size_t m, size_t k, size_t n,
+                              void *stream);
+
+/* embedding_lookup (kernels.rs:402-422): row copies of an f32 table.
+ * Panics: len(table) % dim, len(out) != len(ids) * dim (UQ_ERR_LEN); an id
+ * past the table is UQ_ERR_TOKEN, checked for every id before any copy.
+ * The device form takes the ids from host memory, as uq_embed does. */
+uq_status uq_embedding_lookup(float *out, size_t out_len, const float *table, size_t table_len, const uint32_t *ids,
+                              size_t n_ids, size_t dim);
+uq_status uq_embedding_lookup_d(float *d_out, const float *d_table, size_t table_len, const uint32_t *ids,
+                                size_t n_ids, size_t dim, void *stream);
 
 /* The causal attention of one decode position, step 5 of attn_layer
  * (qwen35_forward.rs:639-671): for each q head h, with kv head

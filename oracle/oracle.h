@@ -39,7 +39,8 @@ enum {
     OR_ERR_LEN = 1,            /* assert_eq!(len ...) failed            */
     OR_ERR_BLOCK_MULTIPLE = 2, /* dim_in % QK_K != 0 (or % 32 for Q8_0) */
     OR_ERR_DTYPE = 3,          /* panic!("... sin dot implementado")     */
-    OR_ERR_ALLOC = 4
+    OR_ERR_ALLOC = 4,
+    OR_ERR_RANGE = 5           /* assert!(id in range) failed            */
 };
 
 #define OR_QK_K 256
@@ -140,6 +141,13 @@ int or_gdn_fused_step(float *state, float *out, const float *q, const float *k, 
 int or_rope_llama(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
 int or_rope_neox(float *x, size_t n, const float *freqs, size_t nfreq, size_t pos);
 int or_rope_imrope(float *x, size_t n, size_t n_rot, double theta_scale, size_t pos);
+/* kernels.rs:87-101: acc[m][n] = f32((f64)acc + pairwise f64 sum of a*b over k). */
+int or_matmul_f32_acc(float *acc, const float *a, const float *b, size_t m, size_t k, size_t n);
+/* kernels.rs:185-194 */
+void or_gelu_tanh(float *out, const float *x, size_t n);
+/* kernels.rs:402-422: OR_ERR_LEN for the length asserts, OR_ERR_RANGE for an id past the table. */
+int or_embedding_lookup(float *out, size_t out_len, const float *table, size_t table_len, const uint32_t *ids,
+                        size_t n_ids, size_t dim);
 /* qwen35_forward.rs:639-671: causal attention of one decode position.
  * q and out are [n_head][hd]; the caches are [n_ctx][n_head_kv][hd]; soft
  * [n_head][n_ctx] receives each head's softmax weights. */

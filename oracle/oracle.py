@@ -353,6 +353,31 @@ def rope_neox(x, freqs, pos: int) -> np.ndarray:
     return y
 
 
+def matmul_f32_acc(acc, a, b, m: int, k: int, n: int) -> np.ndarray:
+    """kernels.rs:87-101; returns the updated copy of acc"""
+    out, a, b = _f32(acc).copy(), _f32(a), _f32(b)
+    _ok(_fn("or_matmul_f32_acc", [_P, _P, _P, _S, _S, _S])(_p(out), _p(a), _p(b), m, k, n), "matmul_f32_acc")
+    return out
+
+
+def gelu_tanh(x) -> np.ndarray:
+    """kernels.rs:185-194"""
+    x = _f32(x)
+    out = np.zeros(len(x), np.float32)
+    _fn("or_gelu_tanh", [_P, _P, _S], None)(_p(out), _p(x), len(x))
+    return out
+
+
+def embedding_lookup(table, ids, dim: int) -> np.ndarray:
+    """kernels.rs:402-422"""
+    t = _f32(table)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.zeros(len(ids) * dim, np.float32)
+    _ok(_fn("or_embedding_lookup", [_P, _S, _P, _S, _P, _S, _S])(_p(out), len(out), _p(t), len(t), _p(ids), len(ids),
+                                                                 dim), "embedding_lookup")
+    return out
+
+
 def attn_decode(q, k_cache, v_cache, n_ctx: int, n_head: int, n_head_kv: int, hd: int, kq_scale: float):
     """qwen35_forward.rs:639-671; returns (out [n_head*hd], soft [n_head*n_ctx])"""
     q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)

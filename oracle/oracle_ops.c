@@ -181,3 +181,41 @@ int or_attn_decode(float *out, float *soft, const float *q, const float *k_cache
     free(scores);
     return OR_OK;
 }
+
+/* kernels.rs:87-101: products in f64, pairwise sum, accumulate in f64, one f32 rounding */
+int or_matmul_f32_acc(float *acc, const float *a, const float *b, size_t m, size_t k, size_t n) {
+    double *prods = malloc((2 * k + 1) * sizeof(double));
+    if (!prods) return OR_ERR_ALLOC;
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++) {
+            for (size_t l = 0; l < k; l++) prods[l] = (double)a[i * k + l] * (double)b[l * n + j];
+            const double sum = or_pairwise_sum_f64(prods, k, prods + k);
+            acc[i * n + j] = (float)((double)acc[i * n + j] + sum);
+        }
+    free(prods);
+    return OR_OK;
+}
+
+/* kernels.rs:185-194: 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3))) in f64, left to right */
+void or_gelu_tanh(float *out, const float *x, size_t n) {
+    const double s2pi = 0.7978845608028654, c = 0.044715;
+    for (size_t i = 0; i < n; i++) {
+        const double t = (double)x[i];
+        const double inner = s2pi * (t + c * t * t * t);
+        out[i] = (float)(0.5 * t * (1.0 + tanh(inner)));
+    }
+}
+
+/* kernels.rs:402-422: row copies; the length asserts first, then each id in order */
+int or_embedding_lookup(float *out, size_t out_len, const float *table, size_t table_len, const uint32_t *ids,
+                        size_t n_ids, size_t dim) {
+    if (dim == 0 || table_len % dim) return OR_ERR_LEN;
+    if (out_len != n_ids * dim) return OR_ERR_LEN;
+    for (size_t r = 0; r < n_ids; r++) {
+        const size_t src = (size_t)ids[r] * dim;
+        if (src + dim > table_len) return OR_ERR_RANGE;
+        memcpy(out + r * dim, table + src, dim * sizeof(float));
+    }
+    return OR_OK;
+}
+

@@ -134,6 +134,16 @@ def test_ops_argument_errors_mirror_reference_panics():  # kernels.rs asserts, b
     assert uq.STATUS[L.uq_attn_decode(P(g), 64, P(g), 64, P(g), 64, P(g), 127, 2, 1, 1, 64, 1.0)] == "LEN"  # len(v)
     assert uq.STATUS[L.uq_attn_decode(P(g), 63, P(g), 64, P(g), 64, P(g), 64, 1, 1, 1, 64, 1.0)] == "LEN"   # len(out)
     assert uq.STATUS[L.uq_attn_decode_d(P(g), P(g), P(g), P(g), P(g), 1, 18, 2, 64, 1.0, None)] == "ARG"  # group 9
+    # matmul_f32_acc: len(a), len(b), len(acc) in that order; gelu; embedding_lookup
+    assert uq.STATUS[L.uq_matmul_f32_acc(P(f), 4, P(f), 5, P(f), 7, 2, 3, 2)] == "LEN"
+    assert uq.STATUS[L.uq_matmul_f32_acc(P(f), 3, P(g), 6, P(g), 7, 2, 3, 2)] == "LEN"
+    assert uq.STATUS[L.uq_matmul_f32_acc(P(f), 3, P(g), 6, P(g), 6, 2, 3, 2)] == "LEN"
+    assert uq.STATUS[L.uq_gelu_tanh(P(f), 3, P(f), 4)] == "LEN"
+    ids = np.array([0, 99], np.uint32)
+    assert uq.STATUS[L.uq_embedding_lookup(P(f), 4, P(g), 7, P(ids), 2, 2)] == "LEN"    # len(table) % dim
+    assert uq.STATUS[L.uq_embedding_lookup(P(f), 3, P(g), 6, P(ids), 2, 2)] == "LEN"    # len(out)
+    assert uq.STATUS[L.uq_embedding_lookup(P(f), 4, P(g), 6, P(ids), 2, 2)] == "TOKEN"  # id 99 past 3 rows
+    assert uq.STATUS[L.uq_embedding_lookup_d(P(f), P(g), 6, P(ids), 2, 2, None)] == "TOKEN"
     if uq.device_count() == 0:
         with pytest.raises(uq.UqError) as e:
             ops.rmsnorm(f, f, 1e-6)

@@ -286,3 +286,53 @@ def test_attn_decode_order_adversaries_take_the_replay():
     got = check_attn(q, kq, vv, 2, 1, 1, hd, 1.0, "score adversary", bit_exact_soft=True)
     assert got.tolist() == [0.5] * hd
 
+
+def test_gelu_tanh_within_1_ulp():
+    rng = np.random.default_rng(23)
+    x = np.concatenate([rng.uniform(-8, 8, 100000), [0.0, -0.0, 1.0, -1.0, 30.0, -30.0]]).astype(np.float32)
+    ref = O.gelu_tanh(x)
+    assert_ulp(ops.gelu_tanh(x), ref, 1, 0.999, "gelu_tanh host")
+    d, y = dev(x), uq.DeviceArray(4 * len(x))
+    ops.unary_d("gelu_tanh", y, d, len(x))
+    uq.synchronize()
+    assert_ulp(y.download(np.float32, len(x)), ref, 1, 0.999, "gelu_tanh device")
+    assert ops.gelu_tanh([0.0, 1.0])[0] == 0.0
+
+
+@pytest.mark.parametrize("m,k,n", [(2, 3, 2), (1, 4, 1), (5, 1000, 7), (3, 4097, 2), (2, 4096 * 3 + 65, 3),
+                                   (1, 64 ** 3, 1), (4, 0, 3)])
+def test_matmul_f32_acc_bit_exact(m, k, n):
+    """Wide exponents make the f64 sums order-sensitive: any order but the
+    pairwise tree (including across the 64- and 4096-chunks) shows in f32."""
+    rng = np.random.default_rng(m * 1000 + k + n)
+    if (m, k, n) == (2, 3, 2):
+        a, b = np.arange(1, 7, dtype=np.float32), np.arange(7, 13, dtype=np.float32)
+    elif (m, k, n) == (1, 4, 1):
+        a, b = np.array([1e19, 1.0, -1e19, 1.0], np.float32), np.ones(4, np.float32)
+    else:
+        a = (rng.standard_normal(m * k) * 2.0 ** rng.integers(-24, 24, m * k)).astype(np.float32)
+        b = rng.standard_normal(k * n).astype(np.float32)
+    acc = rng.standard_normal(m * n).astype(np.float32) if k > 4 else np.zeros(m * n, np.float32)
+    ref = O.matmul_f32_acc(acc, a, b, m, k, n)
+    assert_bitwise(ops.matmul_f32_acc(acc, a, b, m, k, n), ref, f"matmul host {m}x{k}x{n}")
+    dacc, da, db = dev(acc), dev(a if k else np.zeros(1)), dev(b if k else np.zeros(1))
+    ops.matmul_f32_acc_d(dacc, da, db, m, k, n)
+    uq.synchronize()
+    assert_bitwise(dacc.download(np.float32, m * n), ref, f"matmul device {m}x{k}x{n}")
+
+
+def test_embedding_lookup_rows_bit_exact():
+    rng = np.random.default_rng(24)
+    vocab, dim = 1000, 384
+    table = rng.standard_normal(vocab * dim).astype(np.float32)
+    ids = rng.integers(0, vocab, 300).astype(np.uint32)  # crosses the 256-id launch chunk
+    ref = O.embedding_lookup(table, ids, dim)
+    assert_bitwise(ops.embedding_lookup(table, ids, dim), ref, "embedding_lookup host")
+    dt, dy = dev(table), uq.DeviceArray(4 * len(ref))
+    ops.embedding_lookup_d(dy, dt, len(table), ids, dim)
+    uq.synchronize()
+    assert_bitwise(dy.download(np.float32, len(ref)), ref, "embedding_lookup device")
+    with pytest.raises(uq.UqError) as e:
+        ops.embedding_lookup(table, [0, vocab], dim)
+    assert e.value.kind == "TOKEN"
+

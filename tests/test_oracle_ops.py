@@ -310,3 +310,47 @@ def test_attn_decode_close_to_float64_attention():
         np.testing.assert_allclose(out, _attn_f64(q, kc, vc, n_ctx, nh, nhkv, hd, scale), rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(soft.reshape(nh, n_ctx).sum(axis=1), 1.0, rtol=1e-6)
 
+
+def test_matmul_exact_acc_semantics_and_order_adversary():  # kernels.rs:488-511
+    a = [1.0, 2.0, 3.0, 4.0, 5.0, 6.0]
+    b = [7.0, 8.0, 9.0, 10.0, 11.0, 12.0]
+    acc = O.matmul_f32_acc(np.zeros(4), a, b, 2, 3, 2)
+    assert acc.tolist() == [58.0, 64.0, 139.0, 154.0]
+    assert O.matmul_f32_acc(acc, a, b, 2, 3, 2).tolist() == [116.0, 128.0, 278.0, 308.0]
+    assert O.matmul_f32_acc([0.0], [1e19, 1.0, -1e19, 1.0], [1.0] * 4, 1, 4, 1).tolist() == [0.0]
+
+
+def test_matmul_is_pairwise_then_one_rounding():
+    rng = np.random.default_rng(22)
+    m, k, n = 3, 37, 2
+    a = (rng.standard_normal(m * k) * 2.0 ** rng.integers(-20, 20, m * k)).astype(np.float32)
+    b = rng.standard_normal(k * n).astype(np.float32)
+    acc0 = rng.standard_normal(m * n).astype(np.float32)
+    got = O.matmul_f32_acc(acc0, a, b, m, k, n)
+    A, B = a.reshape(m, k).astype(np.float64), b.reshape(k, n).astype(np.float64)
+    for i in range(m):
+        for j in range(n):
+            s = _pairwise([A[i, l] * B[l, j] for l in range(k)])
+            assert bits([got[i * n + j]]).tolist() == bits([np.float32(float(acc0[i * n + j]) + s)]).tolist()
+
+
+def test_gelu_tanh_hand_values():  # kernels.rs:612-623
+    out = O.gelu_tanh([0.0, 1.0])
+    assert out[0] == 0.0
+    S, Cc, t = 0.7978845608028654, 0.044715, 1.0
+    e = f32(0.5 * t * (1.0 + math.tanh(S * (t + Cc * t * t * t))))
+    assert bits(out[1:]).tolist() == bits([e]).tolist() and abs(out[1] - 0.84119199) < 1e-5
+    x = np.linspace(-6, 6, 101).astype(np.float32)
+    ref = [f32(0.5 * float(v) * (1.0 + math.tanh(S * (float(v) + Cc * float(v) * float(v) * float(v))))) for v in x]
+    assert bits(O.gelu_tanh(x)).tolist() == bits(ref).tolist()
+
+
+def test_embedding_lookup_copies_rows_and_refuses_out_of_range():  # kernels.rs:780-798
+    table = np.array([i * 10.0 + (i % 3) for i in range(12)], np.float32)
+    out = O.embedding_lookup(table, [0, 3, 1], 3)
+    assert out.tolist() == table[0:3].tolist() + table[9:12].tolist() + table[3:6].tolist()
+    with pytest.raises(ValueError, match="status 5"):
+        O.embedding_lookup(np.zeros(6, np.float32), [0, 99], 2)
+    with pytest.raises(ValueError, match="status 1"):
+        O.embedding_lookup(np.zeros(7, np.float32), [0], 2)
+

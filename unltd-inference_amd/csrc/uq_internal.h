@@ -47,6 +47,9 @@ hipError_t launch_gdn_step(float *state, float *out, const float *q, const float
                            const float *beta, int dim, int heads, float scale, hipStream_t s);
 hipError_t launch_rope_freq(int mode, float *x, int rows, int n, const float *freqs, size_t pos, hipStream_t s);
 hipError_t launch_rope_imrope(float *x, int rows, int n, int n_rot, double theta_scale, size_t pos, hipStream_t s);
+// matmul_f32_acc, k <= matmul_max_k()
+int matmul_max_k();
+hipError_t launch_matmul_acc(float *acc, const float *a, const float *b, int m, int k, int n, hipStream_t s);
 // decode attention: hd in {64, 128, 256, 512}, 1 <= group <= 8
 bool attn_shape_ok(int hd, int group);
 hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const floa
     for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
 }
 
-// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
+// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228), gelu_tanh (:185-194)
 __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
         const float v = x[t];
@@ -170,8 +170,13 @@ __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, floa
             r = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v)));
         else if (op == 1)
             r = __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v)));
-        else
+        else if (op == 2)
             r = v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v)));
+        else {  // gelu_tanh (kernels.rs:185-194), f64 left to right
+            const double d = (double)v;
+            const double inner = 0.7978845608028654 * (d + 0.044715 * d * d * d);
+            r = (float)(0.5 * d * (1.0 + tanh(inner)));
+        }
         out[t] = r;
     }
 }
@@ -258,6 +263,56 @@ __global__ void rope_imrope_kernel(float *__restrict__ x, int rows, int n, int n
         float *xr = x + (size_t)r * n;
         rotate_pair(&xr[ic], &xr[ic + half], angle);
     }
+}
+
+// The pairwise tree (kernels.rs:27-42) of len <= 64 values held one per
+// lane, level by level: lane i forms node i from lanes 2i and 2i+1, an odd
+// tail carried up. Returned to every lane.
+__device__ double wave_tree(double v, int len) {
+    const int lane = threadIdx.x & 63;
+    while (len > 1) {
+        const double a = __shfl(v, (2 * lane) & 63), b = __shfl(v, (2 * lane + 1) & 63);
+        v = 2 * lane + 1 < len ? a + b : a;
+        len = (len + 1) >> 1;
+    }
+    return __shfl(v, 0);
+}
+
+// The pairwise tree of leaf(0), ..., leaf(n - 1), n <= 64^3, by one wave.
+// Chunks of 64 and of 4096 (powers of two) are nodes of the tree, with the
+// remainder's own tree as the carried last node, so the tree is the tree
+// over the chunk sums, level after level.
+constexpr int kWaveTreeMax = 64 * 64 * 64;
+template <class Leaf>
+__device__ double wave_pairwise_n(Leaf leaf, int n) {
+    const int lane = threadIdx.x & 63;
+    double l2 = 0.0;
+    int m2 = 0;
+    for (int b2 = 0; b2 < n; b2 += 4096, m2++) {
+        const int n2 = min(4096, n - b2);
+        double l1 = 0.0;
+        int m1 = 0;
+        for (int b1 = 0; b1 < n2; b1 += 64, m1++) {
+            const int c = min(64, n2 - b1);
+            const double s = wave_tree(lane < c ? leaf(b2 + b1 + lane) : 0.0, c);
+            if (lane == m1) l1 = s;
+        }
+        const double s2 = wave_tree(l1, m1);
+        if (lane == m2) l2 = s2;
+    }
+    return wave_tree(l2, m2);
+}
+
+// matmul_f32_acc (kernels.rs:87-101): one wave per output element, products
+// a*b exact in f64, pairwise sum over k, acc + sum in f64, rounded once.
+__global__ __launch_bounds__(OPS_TPB) void matmul_acc_kernel(float *__restrict__ acc, const float *__restrict__ a,
+                                                             const float *__restrict__ b, int m, int k, int n) {
+    const size_t o = (size_t)blockIdx.x * (OPS_TPB / 64) + (threadIdx.x >> 6);
+    if (o >= (size_t)m * n) return;  // whole waves
+    const int i = (int)(o / n), j = (int)(o % n);
+    const float *ar = a + (size_t)i * k;
+    const double s = wave_pairwise_n([&](int l) { return (double)ar[l] * (double)b[(size_t)l * n + j]; }, k);
+    if ((threadIdx.x & 63) == 0) acc[o] = (float)((double)acc[o] + s);
 }
 
 // ---- decode attention (qwen35_forward.rs:639-671) ----
@@ -452,6 +507,17 @@ hipError_t launch_attn_decode(float *out, float *soft, const float *q, const flo
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(attn_pv_kernel, dim3(hd / 64, n_head_kv), dim3(kPvWaves * 64), 0, s, out, soft, vc, n_ctx,
                        n_head_kv, hd, group);
+    return hipGetLastError();
+}
+
+int matmul_max_k() { return kWaveTreeMax; }
+
+hipError_t launch_matmul_acc(float *acc, const float *a, const float *b, int m, int k, int n, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    if (k > kWaveTreeMax) return hipErrorInvalidValue;
+    const size_t waves = (size_t)m * n, blocks = (waves + OPS_TPB / 64 - 1) / (OPS_TPB / 64);
+    if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(matmul_acc_kernel, dim3((unsigned)blocks), dim3(OPS_TPB), 0, s, acc, a, b, m, k, n);
     return hipGetLastError();
 }
 

@@ -357,3 +357,82 @@ uq_status uq_attn_decode_d(float *d_out, float *d_soft, const float *d_q, const 
                                          (int)head_dim, (int)(n_head / n_head_kv), kq_scale, (hipStream_t)stream),
                   "attn_decode_d");
 }
+
+uq_status uq_gelu_tanh(float *out, size_t out_len, const float *x, size_t x_len) {
+    return unary_host(3, "gelu_tanh", out, out_len, x, x_len);
+}
+uq_status uq_gelu_tanh_d(float *d_out, const float *d_x, size_t n, void *stream) {
+    return unary_dev(3, "gelu_tanh_d", d_out, d_x, n, stream);
+}
+
+namespace {
+uq_status matmul_shape(const char *fn, size_t m, size_t k, size_t n) {
+    if (k > (size_t)uq::matmul_max_k()) return set_error(UQ_ERR_ARG, "%s: k %zu above %d", fn, k, uq::matmul_max_k());
+    if (m > INT_MAX || n > INT_MAX || (n && m > (size_t)INT_MAX * 4 / n)) return too_big(fn, m > n ? m : n);
+    return UQ_OK;
+}
+}  // namespace
+
+uq_status uq_matmul_f32_acc(float *acc, size_t acc_len, const float *a, size_t a_len, const float *b, size_t b_len,
+                            size_t m, size_t k, size_t n) {
+    if (a_len != m * k) return set_error(UQ_ERR_LEN, "matmul: len(a) %zu != m*k %zu", a_len, m * k);
+    if (b_len != k * n) return set_error(UQ_ERR_LEN, "matmul: len(b) %zu != k*n %zu", b_len, k * n);
+    if (acc_len != m * n) return set_error(UQ_ERR_LEN, "matmul: len(acc) %zu != m*n %zu", acc_len, m * n);
+    if (bad(acc, acc_len) || bad(a, a_len) || bad(b, b_len)) return set_error(UQ_ERR_ARG, "matmul: null pointer");
+    if (acc_len == 0) return UQ_OK;
+    if (uq_status st = matmul_shape("matmul", m, k, n)) return st;
+    HostCall h("matmul");
+    float *dc = h.in(acc, acc_len), *da = h.in(a, a_len), *db = h.in(b, b_len);
+    if (h.status()) return h.status();
+    h.launched(uq::launch_matmul_acc(dc, da, db, (int)m, (int)k, (int)n, h.stream()));
+    h.back(acc, dc, acc_len);
+    return h.finish();
+}
+
+uq_status uq_matmul_f32_acc_d(float *d_acc, const float *d_a, const float *d_b, size_t m, size_t k, size_t n,
+                              void *stream) {
+    if (m == 0 || n == 0) return UQ_OK;
+    if (!d_acc || (k && (!d_a || !d_b))) return set_error(UQ_ERR_ARG, "matmul_d: null device pointer");
+    if (uq_status st = matmul_shape("matmul_d", m, k, n)) return st;
+    return hip_st(uq::launch_matmul_acc(d_acc, d_a, d_b, (int)m, (int)k, (int)n, (hipStream_t)stream), "matmul_d");
+}
+
+namespace {
+uq_status lookup_check(const char *fn, size_t out_len, size_t table_len, const uint32_t *ids, size_t n_ids,
+                       size_t dim) {
+    if (dim == 0 || table_len % dim)
+        return set_error(UQ_ERR_LEN, "%s: len(table) %zu is not a multiple of dim %zu", fn, table_len, dim);
+    if (out_len != n_ids * dim)
+        return set_error(UQ_ERR_LEN, "%s: len(out) %zu != len(ids) * dim %zu", fn, out_len, n_ids * dim);
+    if (bad(ids, n_ids)) return set_error(UQ_ERR_ARG, "%s: null ids", fn);
+    for (size_t r = 0; r < n_ids; r++)
+        if ((size_t)ids[r] >= table_len / dim)
+            return set_error(UQ_ERR_TOKEN, "%s: id %u outside the table (vocab %zu)", fn, ids[r], table_len / dim);
+    if (dim > INT_MAX / 4) return too_big(fn, dim);
+    return UQ_OK;
+}
+}  // namespace
+
+uq_status uq_embedding_lookup(float *out, size_t out_len, const float *table, size_t table_len, const uint32_t *ids,
+                              size_t n_ids, size_t dim) {
+    if (uq_status st = lookup_check("embedding_lookup", out_len, table_len, ids, n_ids, dim)) return st;
+    if (bad(out, out_len) || bad(table, table_len)) return set_error(UQ_ERR_ARG, "embedding_lookup: null pointer");
+    if (n_ids == 0) return UQ_OK;
+    HostCall h("embedding_lookup");
+    float *dt = h.in(table, table_len), *dy = h.out(out_len);
+    if (h.status()) return h.status();
+    h.launched(uq::launch_embed(UQ_F32, (const uint8_t *)dt, dim * 4, (int)dim, ids, n_ids, dy, h.stream()));
+    h.back(out, dy, out_len);
+    return h.finish();
+}
+
+uq_status uq_embedding_lookup_d(float *d_out, const float *d_table, size_t table_len, const uint32_t *ids,
+                                size_t n_ids, size_t dim, void *stream) {
+    if (uq_status st = lookup_check("embedding_lookup_d", n_ids * dim, table_len, ids, n_ids, dim)) return st;
+    if (n_ids == 0) return UQ_OK;
+    if (!d_out || !d_table) return set_error(UQ_ERR_ARG, "embedding_lookup_d: null device pointer");
+    return hip_st(uq::launch_embed(UQ_F32, (const uint8_t *)d_table, dim * 4, (int)dim, ids, n_ids, d_out,
+                                   (hipStream_t)stream),
+                  "embedding_lookup_d");
+}
+

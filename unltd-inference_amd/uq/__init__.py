@@ -124,6 +124,12 @@ SIGNATURES = {
     "uq_rope_neox_d": ([_P, _S, _S, _P, _S, _P], _I),
     "uq_rope_imrope": ([_P, _S, _S, C.c_double, _S], _I),
     "uq_rope_imrope_d": ([_P, _S, _S, _S, C.c_double, _S, _P], _I),
+    "uq_gelu_tanh": ([_P, _S, _P, _S], _I),
+    "uq_gelu_tanh_d": ([_P, _P, _S, _P], _I),
+    "uq_matmul_f32_acc": ([_P, _S, _P, _S, _P, _S, _S, _S, _S], _I),
+    "uq_matmul_f32_acc_d": ([_P, _P, _P, _S, _S, _S, _P], _I),
+    "uq_embedding_lookup": ([_P, _S, _P, _S, _P, _S, _S], _I),
+    "uq_embedding_lookup_d": ([_P, _P, _S, _P, _S, _S, _P], _I),
     "uq_attn_decode": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _S, C.c_float], _I),
     "uq_attn_decode_d": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, C.c_float, _P], _I),
 }

@@ -65,8 +65,13 @@ def softplus(x) -> np.ndarray:
     return _unary("uq_softplus", x)
 
 
+def gelu_tanh(x) -> np.ndarray:
+    """kernels.rs:185-194"""
+    return _unary("uq_gelu_tanh", x)
+
+
 def unary_d(name: str, d_out: DeviceArray, d_x: DeviceArray, n: int, stream=None):
-    """name: sigmoid, silu or softplus"""
+    """name: sigmoid, silu, softplus or gelu_tanh"""
     _check(getattr(lib(), f"uq_{name}_d")(d_out.ptr, d_x.ptr, n, stream))
 
 
@@ -146,4 +151,29 @@ def attn_decode_d(d_out: DeviceArray, d_soft: DeviceArray, d_q: DeviceArray, d_k
                   stream=None):
     _check(lib().uq_attn_decode_d(d_out.ptr, d_soft.ptr, d_q.ptr, d_k_cache.ptr, d_v_cache.ptr, n_ctx, n_head,
                                   n_head_kv, head_dim, kq_scale, stream))
+
+
+def matmul_f32_acc(acc, a, b, m: int, k: int, n: int) -> np.ndarray:
+    """kernels.rs:87-101; returns the updated copy of acc"""
+    out, a, b = _f32(acc).copy(), _f32(a), _f32(b)
+    _check(lib().uq_matmul_f32_acc(_ptr(out), len(out), _ptr(a), len(a), _ptr(b), len(b), m, k, n))
+    return out
+
+
+def matmul_f32_acc_d(d_acc: DeviceArray, d_a: DeviceArray, d_b: DeviceArray, m: int, k: int, n: int, stream=None):
+    _check(lib().uq_matmul_f32_acc_d(d_acc.ptr, d_a.ptr, d_b.ptr, m, k, n, stream))
+
+
+def embedding_lookup(table, ids, dim: int) -> np.ndarray:
+    """kernels.rs:402-422"""
+    t = _f32(table)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.zeros(len(ids) * dim, np.float32)
+    _check(lib().uq_embedding_lookup(_ptr(out), len(out), _ptr(t), len(t), _ptr(ids), len(ids), dim))
+    return out
+
+
+def embedding_lookup_d(d_out: DeviceArray, d_table: DeviceArray, table_len: int, ids, dim: int, stream=None):
+    ids = np.ascontiguousarray(ids, np.uint32)
+    _check(lib().uq_embedding_lookup_d(d_out.ptr, d_table.ptr, table_len, _ptr(ids), len(ids), dim, stream))
 
