@@ -36,6 +36,7 @@
 //
 // Other formats, N not a multiple of 256, and M < 16 run as M decode-GEMV
 // launches.
+#include <algorithm>
 #include <map>
 #include <mutex>
 
@@ -51,8 +52,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 
-constexpr int GM = 128, GN = 256;  // workgroup tile
-constexpr int GTPB = 512;          // 8 waves, two per SIMD
+constexpr int GN = 192;            // workgroup tile columns (rows: 64 or 128)
+constexpr int GTPB = 256;          // 4 waves, one per SIMD
 constexpr int SUBK = 64;           // k per staging sub-step (one group pair)
 constexpr int kMinM = 16;          // below this M the GEMV path is used
 
@@ -175,21 +176,24 @@ __device__ __forceinline__ void sc_m(uint32_t S0, uint32_t S1, uint32_t S2, int 
     }
 }
 
-// LDS of one workgroup (dynamic shared memory, 156 KB): a ring of NSTAGE
-// sub-steps of 64 k, each filled entirely by direct-to-LDS loads:
+// LDS of one workgroup: a ring of NSTAGE sub-steps of 64 k, each filled
+// entirely by direct-to-LDS loads:
 //  * A: the activation planes, rows of 64 halves (128 B) unpadded; the
 //    16-byte part p of row r sits at part p ^ ((r >> 1) & 7), which spreads
 //    16 consecutive rows of one MFMA operand read over all banks;
 //  * Bq: the weight bytes, chunk-major: chunk 0 = block header (d, dmin,
 //    scales), chunks 1, 2 = the 32 qs bytes of the sub-step's group pair,
-//    chunk 3 = the header again (keeps every wave at two loads);
-//  * G: the block's group sums (filled on the block's first sub-step).
+//    chunk 3 = the header again (keeps every wave at three loads);
+//  * G: the block's group sums, [hi/lo][row][8 groups] (filled on the
+//    block's first sub-step; 4 KB so that every wave makes one load, the
+//    part past 2*TM*16 bytes is never read).
 // Each wave dequantizes its own B operands from Bq (sc*q in f16).
 constexpr int NSTAGE = 3;
+template <int TM>
 struct GemmLds {
-    _Float16 A[NSTAGE][2][GM][SUBK];  // [stage][hi/lo][row][k]   96 KB
-    u4 Bq[NSTAGE][4][GN];             // [stage][chunk][row]       48 KB
-    _Float16 G[NSTAGE][2][GM][8];     // [stage][hi/lo][row][g]    12 KB
+    _Float16 A[NSTAGE][2][TM][SUBK];  // [stage][hi/lo][row][k]
+    u4 Bq[NSTAGE][4][GN];             // [stage][chunk][row]
+    uint8_t G[NSTAGE][4096];          // [stage][hi/lo][row][g] halves
 };
 __device__ __forceinline__ int swz_part(int r, int p) { return p ^ ((r >> 1) & 7); }
 __device__ __forceinline__ int swz(int r, int p) { return 8 * swz_part(r, p); }
@@ -222,206 +226,356 @@ __device__ __forceinline__ h8 dq8(uint32_t d0, uint32_t d1, int sh, h2 sc2, h2 o
 }
 
 // Wait until at most N of this wave's vector-memory operations are
-// outstanding (they complete in issue order), then barrier. Written as one
-// asm block so no fence-implied full wait is added: every stage is written
-// by direct-to-LDS loads only, whose completion is what vmcnt tracks, and
-// the LDS reads of earlier stages have all been consumed by then.
+// outstanding (they complete in issue order) and its LDS reads have
+// returned, then barrier. One asm block, so no fence-implied full wait is
+// added: every stage is written by direct-to-LDS loads only, whose
+// completion is what vmcnt tracks.
 template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
-    static_assert(N >= 0 && N <= 15, "vmcnt immediate");
-    __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__restrict__ W,
-                                                                           size_t row_bytes, int K, int N, int M,
-                                                                           GemmWs ws, int ntn,
-                                                                           float *__restrict__ Y) {
+// One 16-byte direct-to-LDS load per lane (lane i writes dst + 16 i); a
+// non-template helper, so the builtin is never instantiated inside a
+// lambda of a kernel template.
+__device__ __forceinline__ void dma16(const void *g, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
+
+// The B-side constants of one sub-step for one 32-column tile: the four qs
+// dwords of this lane's k range and the f16 scale operands of the pair's
+// two groups.
+struct BConst {
+    uint32_t q[4];
+    h2 sc2[2], off2[2];
+};
+
+// Scheduling hints for one 16-k step: MFMAs alternate with the step's other
+// work (LDS reads, VALU, direct-to-LDS loads), so the matrix core is fed
+// while the wave issues the rest. Masks: 0x008 MFMA, 0x100 LDS read,
+// 0x002 VALU, 0x020 VMEM read.
+template <int NM>
+__device__ __forceinline__ void sched_step() {
+#pragma unroll
+    for (int k = 0; k < NM; k++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (k < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (k >= 4 && k < 7) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+}
+
+// A workgroup of four waves (one per SIMD) computes a TM x 192 tile; wave
+// (wm, wn) owns rows 32*WMT*wm + 32i (i < WMT) and columns 96*wn + 32j
+// (j < 3). One loop iteration is one 256-k block: 4 sub-steps of 64 k,
+// each 4 k-steps of 16, all unrolled, with no branch inside:
+//  * the operands of k-step t+1 (LDS reads, B dequantization) are formed
+//    while the MFMAs of step t run;
+//  * at k-step 2 of sub-step u the wave reads the operands of (u, 3), then
+//    waits for stage u+1 and meets the others at the barrier; stage u+3
+//    then goes into stage u's slot (every wave has read it), its loads
+//    spread over the next four k-steps;
+//  * past the last sub-step the loads re-read the last one into a free
+//    slot and the reads of it are discarded, so counts stay static.
+template <int WMT>
+__global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__restrict__ W, size_t row_bytes, int K,
+                                                           int N, int M, GemmWs ws, int ntn, float *__restrict__ Y) {
+    constexpr int TM = 64 * WMT;
+    constexpr int NA = TM / 16;  // A loads per wave per stage (1 KB each)
+    constexpr int NAP = NA / 4;  // ... per k-step
     extern __shared__ __align__(16) uint8_t lds_raw[];
-    GemmLds &S = *(GemmLds *)lds_raw;
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    GemmLds<TM> &S = *(GemmLds<TM> *)lds_raw;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     // Tile order: workgroups are dealt round-robin to the 8 XCDs (id % 8).
     // XCD x takes a contiguous run of the M-major tile list, i.e. mostly one
     // M tile, so that tile's activation planes stay in the XCD's L2 while
     // its N tiles stream the weights.
-    const int ntm = (M + GM - 1) / GM, T = ntm * ntn, per = (T + 7) / 8;
+    const int ntm = (M + TM - 1) / TM, T = ntm * ntn, per = (T + 7) / 8;
     const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if ((blockIdx.x >> 3) >= per || L >= T) return;  // padding of the last round
     const int mt = L / ntn, nt = L % ntn;
-    const int m0 = mt * GM, n0 = nt * GN;
-    const int wm = wv >> 2, wn = wv & 3;  // 2 x 4 waves of 64 x 64
+    const int m0 = mt * TM, n0 = nt * GN;
+    const int wm = wv >> 1, wn = wv & 1;
     const int lr = lane & 31, lh = lane >> 5;
     const int nblk = K / 256, KG = K / 32, nsub = 4 * nblk;
 
-    // Stage u (block u/4, group pair u%4): per wave 4 A loads + 2 Bq loads,
-    // + 1 G load on waves 0-3 when u % 4 == 0. Lane i of a 1 KB load fills
-    // bytes 1024 J + 16 i of its region.
-    // Per-lane source offsets of the loads (bytes from the plane / weight
-    // base); only the uniform stage term changes per sub-step.
-    uint32_t aoff[4], boff[2], goff;
-    const _Float16 *abase[4];
-    bool bq[2];
-    for (int c = 0; c < 4; c++) {
-        const int J = 4 * wv + c, lin = 1024 * J + 16 * lane;
-        const int hl = lin >> 14, row = (lin >> 7) & 127, pp = (lin >> 4) & 7;
+    // Per-lane source offsets of the loads; only the uniform stage term
+    // changes per sub-step. Lane i of a 1 KB load fills bytes 1024 J + 16 i
+    // of its region. Rows past M or N read the last valid row (never
+    // stored). A offsets are from ws.ahi (the lo plane follows it in the
+    // workspace); the host keeps the workspace below 4 GiB.
+    const uint32_t lo_off = (uint32_t)((const uint8_t *)ws.alo - (const uint8_t *)ws.ahi);
+    uint32_t aoff[NA], boff[3];
+    bool bq[3];
+#pragma unroll
+    for (int c = 0; c < NA; c++) {
+        const int lin = 1024 * (NA * wv + c) + 16 * lane;
+        const int hl = lin / (TM * 128), row = (lin >> 7) % TM, pp = (lin >> 4) & 7;
         const int p = swz_part(row, pp);  // the swizzle is an involution
-        const int mr = m0 + row < M ? m0 + row : M - 1;  // rows past M are never stored
-        abase[c] = hl ? ws.alo : ws.ahi;
-        aoff[c] = (uint32_t)(((size_t)mr * K + 8 * p) * 2);
+        const int mr = min(m0 + row, M - 1);
+        aoff[c] = (hl ? lo_off : 0u) + (uint32_t)(((size_t)mr * K + 8 * p) * 2);
     }
-    for (int c = 0; c < 2; c++) {
-        const int J = 2 * wv + c, lin = 1024 * J + 16 * lane;
-        const int ch = lin >> 12, row = (lin >> 4) & 255;
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        const int lin = 1024 * (3 * wv + c) + 16 * lane;
+        const int ch = lin / (GN * 16), row = (lin % (GN * 16)) >> 4;
+        const int nr = min(n0 + row, N - 1);
         bq[c] = ch == 1 || ch == 2;
-        boff[c] = (uint32_t)((size_t)row * row_bytes + (ch == 1 ? 16 : ch == 2 ? 32 : 0));
+        boff[c] = (uint32_t)((size_t)nr * row_bytes + (ch == 1 ? 16 : ch == 2 ? 32 : 0));
     }
     const _Float16 *gbase;
+    uint32_t goff;
     {
-        const int c = 64 * (wv & 3) + lane, hl = c >> 7, row = c & 127;
-        const int mr = m0 + row < M ? m0 + row : M - 1;
+        const int lin = 1024 * wv + 16 * lane, hl = (lin / (TM * 16)) & 1, row = (lin >> 4) % TM;
         gbase = hl ? ws.glo : ws.ghi;
-        goff = (uint32_t)((size_t)mr * KG * 2);
+        goff = (uint32_t)((size_t)min(m0 + row, M - 1) * KG * 2);
     }
-    const uint8_t *wtile = W + (size_t)n0 * row_bytes;
-    auto issue = [&](int u) {
-        const int st = u % NSTAGE, kb = u >> 2, ss = u & 3;
-        for (int c = 0; c < 4; c++)
-            __builtin_amdgcn_global_load_lds((const uint8_t *)abase[c] + (size_t)u * (SUBK * 2) + aoff[c],
-                                             (__attribute__((address_space(3))) void *)((uint8_t *)&S.A[st][0][0][0] + 1024 * (4 * wv + c)),
-                                             16, 0, 0);
-        for (int c = 0; c < 2; c++)
-            __builtin_amdgcn_global_load_lds(wtile + (size_t)kb * BQ4K + boff[c] + (bq[c] ? 32 * ss : 0),
-                                             (__attribute__((address_space(3))) void *)((uint8_t *)&S.Bq[st][0][0] + 1024 * (2 * wv + c)),
-                                             16, 0, 0);
-        if (ss == 0 && wv < 4)
-            __builtin_amdgcn_global_load_lds((const uint8_t *)gbase + (size_t)kb * 16 + goff,
-                                             (__attribute__((address_space(3))) void *)((uint8_t *)&S.G[st][0][0][0] + 1024 * wv),
-                                             16, 0, 0);
+    const uint8_t *abase = (const uint8_t *)ws.ahi;
+    // Part p (0..3) of stage v's loads: A loads [p*NAP, (p+1)*NAP), then B
+    // load p (p < 3) or the G load (p == 3, when the stage starts a block:
+    // G_STAGE). Stages past the end re-read the last sub-step.
+    auto issue_part = [&](int v, int p, bool g_stage) {
+        const int vs = min(v, nsub - 1), st = v % NSTAGE, kb = vs >> 2, ss = vs & 3;
+#pragma unroll
+        for (int c = p * NAP; c < (p + 1) * NAP; c++)
+            dma16(abase + (size_t)vs * (SUBK * 2) + aoff[c], (uint8_t *)&S.A[st][0][0][0] + 1024 * (NA * wv + c));
+        if (p < 3)
+            dma16(W + (size_t)kb * BQ4K + boff[p] + (bq[p] ? 32 * ss : 0), (uint8_t *)&S.Bq[st][0][0] + 1024 * (3 * wv + p));
+        else if (g_stage)
+            dma16((const uint8_t *)gbase + (size_t)kb * 16 + goff, &S.G[st][0] + 1024 * wv);
     };
-    // this wave's loads per stage (the wait counts below)
-    const bool gw = wv < 4;
     const uint32_t kmask = 0x000F000Fu, kmagic = 0x64006400u;
 
-    f16x P[2][2], C[2][2];
-    for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 2; j++)
-            for (int r = 0; r < 16; r++) C[i][j][r] = 0.0f;
-
-    issue(0);
-    if (nsub > 1) issue(1);
-    for (int u = 0; u < nsub; u++) {
-        const int st = u % NSTAGE, ss = u & 3;
-        // stage u has landed once only stage u+1's loads may be outstanding
-        if (u + 1 < nsub) {
-            const bool g1 = gw && ((u + 1) & 3) == 0;
-            if (g1)
-                wait_vm_barrier<7>();
-            else
-                wait_vm_barrier<6>();
-        } else {
-            wait_vm_barrier<0>();
-        }
-        if (u + 2 < nsub) issue(u + 2);  // into the stage read two iterations ago
-        // B operand inputs of this wave's two column tiles
-        uint32_t q[2][4];
-        h2 sc2[2][2], off2[2][2];  // [j][low/high nibble group]
-        u4 hdr[2];
-        for (int j = 0; j < 2; j++) {
-            const int col = 64 * wn + 32 * j + lr;
-            hdr[j] = S.Bq[st][0][col];
-            const u4 a = S.Bq[st][1][col], b = S.Bq[st][2][col];
-            // qs bytes [8 lh, +8) and [16 + 8 lh, +8) of the pair
-            q[j][0] = lh ? a.z : a.x;
-            q[j][1] = lh ? a.w : a.y;
-            q[j][2] = lh ? b.z : b.x;
-            q[j][3] = lh ? b.w : b.y;
+    // B-side constants of one sub-step (group pair ss of the block): per
+    // column tile the four qs dwords of this lane's k range (bytes
+    // [8 lh, +8) and [16 + 8 lh, +8) of the pair) and the f16 scale
+    // operands of the pair's two groups.
+    BConst bc[3];
+    auto load_consts = [&](int u, int ss) {
+        const uint8_t *st = (const uint8_t *)&S.Bq[u % NSTAGE][0][0];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int col = 96 * wn + 32 * j + lr;
+            const u4 h = *(const u4 *)(st + 16 * col);
+            const uint2 a = *(const uint2 *)(st + GN * 16 + 16 * col + 8 * lh);
+            const uint2 b = *(const uint2 *)(st + 2 * GN * 16 + 16 * col + 8 * lh);
+            bc[j].q[0] = a.x;
+            bc[j].q[1] = a.y;
+            bc[j].q[2] = b.x;
+            bc[j].q[3] = b.y;
+#pragma unroll
             for (int sh2 = 0; sh2 < 2; sh2++) {
                 uint32_t sc, mm;
-                sc_m(hdr[j].y, hdr[j].z, hdr[j].w, 2 * ss + sh2, sc, mm);
+                sc_m(h.y, h.z, h.w, 2 * ss + sh2, sc, mm);
                 const _Float16 scf = (_Float16)(float)sc, off = (_Float16)(-1024.0f * (float)sc);
-                sc2[j][sh2] = h2{scf, scf};
-                off2[j][sh2] = h2{off, off};
+                bc[j].sc2[sh2] = h2{scf, scf};
+                bc[j].off2[sh2] = h2{off, off};
             }
         }
-        // MFMA: k-steps s = 0..3 (slots 16s..16s+15): s 0, 1 low nibbles of
-        // group 2ss (qs bytes 0-15 / 16-31), s 2, 3 high nibbles (group 2ss+1)
-        for (int s = 0; s < 4; s++) {
-            const int p = 2 * s + lh, sh2 = s >> 1, half = s & 1;
-            h8 ah[2], al[2], b[2];
-            for (int i = 0; i < 2; i++) {
-                const int row = 64 * wm + 32 * i + lr;
-                ah[i] = *(const h8 *)&S.A[st][0][row][swz(row, p)];
-                al[i] = *(const h8 *)&S.A[st][1][row][swz(row, p)];
+    };
+    // block epilogue inputs, formed when the block's last sub-step has
+    // landed: B = -dmin*m_g (hi, lo) and d per column tile, A = this lane's
+    // group sums (hi for lh 0, lo for lh 1) per row tile
+    h8 ebh[3], ebl[3], eg[WMT];
+    float ed[3];
+    auto load_epilogue = [&](int u) {
+        const int st = u % NSTAGE, gst = (u - 3) % NSTAGE;  // G arrived with the block's first sub-step
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const u4 h = S.Bq[st][0][96 * wn + 32 * j + lr];
+            const float dmin = f16_hi(h.x);
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                uint32_t sc, mm;
+                sc_m(h.y, h.z, h.w, g, sc, mm);
+                const float bm = -(dmin * (float)mm);  // exact in f32
+                ebh[j][g] = (_Float16)bm;
+                ebl[j][g] = (_Float16)(bm - (float)ebh[j][g]);
             }
-            for (int j = 0; j < 2; j++)
-                b[j] = dq8(q[j][2 * half], q[j][2 * half + 1], 4 * sh2, sc2[j][sh2], off2[j][sh2], kmask, kmagic);
-            const bool first = ss == 0 && s == 0;
-            for (int i = 0; i < 2; i++)
-                for (int j = 0; j < 2; j++) {
-                    f16x acc = P[i][j];
-                    if (first)
-                        for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-                    acc = mfma(ah[i], b[j], acc);
-                    P[i][j] = mfma(al[i], b[j], acc);
-                }
+            ed[j] = f16_lo(h.x);
         }
-        if (ss == 3) {
-            // end of the block: min term into C, then C += d * P. Operand slots
-            // (lh, g): A = group sum hi (lh 0) / lo (lh 1) of group g, B =
-            // -dmin*m_g hi, then lo. G was loaded with the block's first stage.
-            const int gst = (u - 3) % NSTAGE;
-            for (int j = 0; j < 2; j++) {
-                h8 bh, bl;
-                const float dmin = f16_hi(hdr[j].x);
-                for (int g = 0; g < 8; g++) {
-                    uint32_t sc, mm;
-                    sc_m(hdr[j].y, hdr[j].z, hdr[j].w, g, sc, mm);
-                    const float bm = -(dmin * (float)mm);  // exact in f32
-                    bh[g] = (_Float16)bm;
-                    bl[g] = (_Float16)(bm - (float)bh[g]);
+#pragma unroll
+        for (int i = 0; i < WMT; i++)
+            eg[i] = *(const h8 *)&S.G[gst][(lh * TM + 32 * WMT * wm + 32 * i + lr) * 16];
+    };
+    struct Ops {
+        h8 ah[WMT], al[WMT], b[3];
+    };
+    // operands of k-step s (16 k) of sub-step u: s 0, 1 are the low nibbles
+    // of group 2ss (qs bytes 0-15 / 16-31), s 2, 3 the high nibbles (group
+    // 2ss+1)
+    auto load_ops = [&](Ops &o, int u, int s) {
+        const int st = u % NSTAGE, p = 2 * s + lh, sh2 = s >> 1, half = s & 1;
+#pragma unroll
+        for (int i = 0; i < WMT; i++) {
+            const int row = 32 * WMT * wm + 32 * i + lr;
+            o.ah[i] = *(const h8 *)&S.A[st][0][row][swz(row, p)];
+            o.al[i] = *(const h8 *)&S.A[st][1][row][swz(row, p)];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++)
+            o.b[j] = dq8(bc[j].q[2 * half], bc[j].q[2 * half + 1], 4 * sh2, bc[j].sc2[sh2], bc[j].off2[sh2], kmask,
+                         kmagic);
+    };
+
+    f16x P[WMT][3], C[WMT][3];
+    const f16x zero = {};
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) C[i][j] = zero;
+
+    // prologue: stages 0, 1 and half of 2 in flight, stage 0 landed
+#pragma unroll
+    for (int p = 0; p < 4; p++) issue_part(0, p, true);
+#pragma unroll
+    for (int p = 0; p < 4; p++) issue_part(1, p, false);
+    wait_vm_barrier<NA + 3>();
+    issue_part(2, 0, false);  // parts 2, 3 of stage 2 follow in k-steps 0, 1
+    issue_part(2, 1, false);
+    load_consts(0, 0);
+    Ops cur, nxt;
+    load_ops(cur, 0, 0);
+    for (int kb = 0; kb < nblk; kb++) {
+#pragma unroll
+        for (int ss = 0; ss < 4; ss++) {
+            const int u = 4 * kb + ss;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                if (s == 2) {
+                    load_ops(nxt, u, 3);
+                    // stage u+1 landed: only stage u+2's loads may be outstanding
+                    if (((ss + 2) & 3) == 0)
+                        wait_vm_barrier<NA + 4>();
+                    else
+                        wait_vm_barrier<NA + 3>();
+                    load_consts(u + 1, (ss + 1) & 3);
+                    if (ss == 2) load_epilogue(u + 1);
+                } else if (s == 3) {
+                    load_ops(nxt, u + 1, 0);
+                } else {
+                    load_ops(nxt, u, s + 1);
                 }
-                const float dj = f16_lo(hdr[j].x);
-                for (int i = 0; i < 2; i++) {
-                    const h8 ae = *(const h8 *)&S.G[gst][lh][64 * wm + 32 * i + lr][0];
-                    f16x acc = mfma(ae, bh, C[i][j]);
-                    acc = mfma(ae, bl, acc);
-                    for (int r = 0; r < 16; r++) acc[r] = fmaf(dj, P[i][j][r], acc[r]);
-                    C[i][j] = acc;
-                }
+                // part of stage u+3 (issued from k-step 2 of u to k-step 1 of u+1)
+                if (s >= 2)
+                    issue_part(u + 3, s - 2, ((ss + 3) & 3) == 0);
+                else
+                    issue_part(u + 2, s + 2, ((ss + 2) & 3) == 0);
+#pragma unroll
+                for (int i = 0; i < WMT; i++)
+#pragma unroll
+                    for (int j = 0; j < 3; j++) P[i][j] = mfma(cur.ah[i], cur.b[j], ss == 0 && s == 0 ? zero : P[i][j]);
+#pragma unroll
+                for (int i = 0; i < WMT; i++)
+#pragma unroll
+                    for (int j = 0; j < 3; j++) P[i][j] = mfma(cur.al[i], cur.b[j], P[i][j]);
+                sched_step<6 * WMT>();
+                cur = nxt;
             }
         }
+        // end of the block: min term into C, then C += d * P
+#pragma unroll
+        for (int i = 0; i < WMT; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                f16x acc = mfma(eg[i], ebh[j], C[i][j]);
+                acc = mfma(eg[i], ebl[j], acc);
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[r] = fmaf(ed[j], P[i][j][r], acc[r]);
+                C[i][j] = acc;
+            }
     }
-    // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4
-    for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + 64 * wn + 32 * j + lr;
+    wait_vm_barrier<0>();  // the loads past the end land before the workgroup leaves
+    // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4.
+    // The row scales are loaded first, unconditionally (clamped rows), so
+    // the loads are issued together rather than one per guarded store.
+    float rs[WMT][16];
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + 32 * WMT * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+            rs[i][r] = ws.scale[min(m, M - 1)];
+        }
+    // scale every output before the first store: stores count in vmcnt too,
+    // so a scale consumed after a store would wait for that store
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++)
+#pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m < M) Y[(size_t)m * N + n] = ws.scale[m] * C[i][j][r];
+                float v = C[i][j][r] * rs[i][r];
+                __asm__ volatile("" : "+v"(v));  // formed here, not sunk next to its store
+                C[i][j][r] = v;
+            }
+    if (m0 + TM <= M && n0 + GN <= N) {  // whole tile in range: stores without guards
+#pragma unroll
+        for (int i = 0; i < WMT; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                float *y = Y + (size_t)(m0 + 32 * WMT * wm + 32 * i + 4 * lh) * N + n0 + 96 * wn + 32 * j + lr;
+#pragma unroll
+                for (int r = 0; r < 16; r++) y[(size_t)(8 * (r >> 2) + (r & 3)) * N] = C[i][j][r];
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int n = n0 + 96 * wn + 32 * j + lr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + 32 * WMT * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m < M && n < N) Y[(size_t)m * N + n] = C[i][j][r];
             }
         }
 }
 
+template <int WMT>
+hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out, TM = 64 * WMT;
+    const int ntm = (M + TM - 1) / TM, ntn = (N + GN - 1) / GN;
+    const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
+    const void *k = (const void *)gemm_q4k_kernel<WMT>;
+    hipError_t e = allow_lds(k, sizeof(GemmLds<64 * WMT>));
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gemm_q4k_kernel<WMT>, dim3(grid), dim3(GTPB), sizeof(GemmLds<64 * WMT>), s, w.bytes,
+                       w.row_bytes, K, N, M, ws, ntn, Y);
+    return hipGetLastError();
+}
+
 hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out;
+    const int K = w.dim_in;
+    // the kernel addresses the workspace with 32-bit offsets: run M in
+    // chunks whose workspace stays below 4 GiB
+    const int mmax = (int)std::min<size_t>((size_t)M, ((size_t)1 << 31) / ((size_t)K * 4 + 64));
+    if (mmax < M) {
+        for (int m = 0; m < M; m += mmax) {
+            const int mc = std::min(mmax, M - m);
+            hipError_t e = gemm_mfma_q4k(w, mc, X + (size_t)m * K, Y + (size_t)m * w.dim_out, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     uint8_t *base = nullptr;
     hipError_t e = ws_get(ws_bytes(M, K), s, &base);
     if (e != hipSuccess) return e;
     const GemmWs ws = ws_carve(base, M, K);
     hipLaunchKernelGGL(gemm_prep_kernel, dim3(M), dim3(256), 0, s, X, K, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const int ntm = (M + GM - 1) / GM, ntn = N / GN;
-    const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
-    if ((e = allow_lds((const void *)gemm_q4k_kernel, sizeof(GemmLds))) != hipSuccess) return e;
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(grid), dim3(GTPB), sizeof(GemmLds), s, w.bytes, w.row_bytes, K, N, M,
-                       ws, ntn, Y);
-    return hipGetLastError();
+    // 128-row tiles once there are enough of them to cover the CUs
+    return M >= 384 ? gemm_launch<2>(w, M, ws, Y, s) : gemm_launch<1>(w, M, ws, Y, s);
 }
 
 }  // namespace
 
 hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
     if (M == 0 || w.dim_out == 0) return hipSuccess;
-    if (w.dtype == UQ_Q4_K && M >= kMinM && w.dim_out % GN == 0) return gemm_mfma_q4k(w, M, X, Y, s);
+    if (w.dtype == UQ_Q4_K && M >= kMinM) return gemm_mfma_q4k(w, M, X, Y, s);
     for (int m = 0; m < M; m++) {
         hipError_t e = launch_gemv(w, X + (size_t)m * w.dim_in, Y + (size_t)m * w.dim_out, s);
         if (e != hipSuccess) return e;
