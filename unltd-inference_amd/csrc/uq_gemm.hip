@@ -471,21 +471,24 @@ __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__rest
                 for (int i = 0; i < WMT; i++)
 #pragma unroll
                     for (int j = 0; j < 3; j++) P[i][j] = mfma(cur.al[i], cur.b[j], P[i][j]);
+                // the block's min term into C (its inputs arrived at k-step 10):
+                // the hi MFMAs at k-step 12, the lo ones at 13, off the block's end
+                if (ss == 3 && s < 2)
+#pragma unroll
+                    for (int i = 0; i < WMT; i++)
+#pragma unroll
+                        for (int j = 0; j < 3; j++) C[i][j] = mfma(eg[i], s == 0 ? ebh[j] : ebl[j], C[i][j]);
                 sched_step<6 * WMT>();
                 cur = nxt;
             }
         }
-        // end of the block: min term into C, then C += d * P
+        // end of the block: C += d * P
 #pragma unroll
         for (int i = 0; i < WMT; i++)
 #pragma unroll
-            for (int j = 0; j < 3; j++) {
-                f16x acc = mfma(eg[i], ebh[j], C[i][j]);
-                acc = mfma(eg[i], ebl[j], acc);
+            for (int j = 0; j < 3; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) acc[r] = fmaf(ed[j], P[i][j][r], acc[r]);
-                C[i][j] = acc;
-            }
+                for (int r = 0; r < 16; r++) C[i][j][r] = fmaf(ed[j], P[i][j][r], C[i][j][r]);
     }
     wait_vm_barrier<0>();  // the loads past the end land before the workgroup leaves
     // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4.
