@@ -30,6 +30,16 @@ UQ_HD int sdot4(uint32_t a, uint32_t b, int c) {
 #endif
 }
 
+// v_mul_i32_i24: a * b for operands within 24 bits (full rate; the 32-bit
+// v_mul_lo_u32 is quarter rate). Callers guarantee the ranges.
+UQ_HD int mul24(int a, int b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __mul24(a, b);
+#else
+    return a * b;
+#endif
+}
+
 // v_perm_b32: byte i of the result is byte sel.i of {s0:s1} (s1 = bytes 0-3)
 UQ_HD uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
 #if defined(__HIP_DEVICE_COMPILE__)

@@ -919,6 +919,154 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
     }
 }
 
+// Streaming variant of gemv_q8k_kernel (bit-exact, same arithmetic) for one
+// Q4_K / Q6_K tensor or a batch, K <= 4096: rows arrive through the per-wave
+// LDS ring of gemv_stream_kernel (coalesced nontemporal direct-to-LDS loads,
+// one row in flight per wave, issued before the wave computes the previous
+// one), instead of per-lane loads into VGPRs. The x records, the lane-quad
+// sums, the per-wave row records and the reference-order epilogue are those
+// of gemv_q8k_kernel.
+template <class F> struct Q8Base;
+template <> struct Q8Base<Q6KQ8> { using T = Q6K; };
+template <> struct Q8Base<Q4KQ8> { using T = Q4K; };
+
+struct Q8SLayout {
+    size_t xq, d8, region, ring, total;  // byte offsets
+    int R;                               // rows per epilogue batch (<= 8)
+};
+template <class F>
+__host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni) {
+    const int nblk = K >> 8, ntask = 4 * nblk;
+    Q8SLayout L;
+    L.xq = 0;
+    L.d8 = (size_t)ntask * F::kDw * 4;
+    L.region = (L.d8 + (size_t)nblk * 4 + 15) & ~(size_t)15;
+    int R = (int)(65536 / ((size_t)nw * nblk * 40));
+    L.R = R < 1 ? 1 : (R > 8 ? 8 : R);
+    const size_t prep = (size_t)K + (size_t)(K / 16) * 4;
+    const size_t recs = (size_t)nw * L.R * nblk * 40;
+    L.ring = (L.region + (prep > recs ? prep : recs) + 15) & ~(size_t)15;
+    L.total = L.ring + (size_t)nw * ni * 1024;
+    return L;
+}
+
+template <class F, int NI, int NW, bool MULTI>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
+gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
+    using St = Stage<typename Q8Base<F>::T>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
+    const int nblk = K >> 8, ntask = 4 * nblk, R = L.R;
+    uint32_t *xq = (uint32_t *)(lds + L.xq);
+    float *d8 = (float *)(lds + L.d8);
+    uint32_t *qtmp = (uint32_t *)(lds + L.region);
+    int *bst = (int *)(lds + L.region + K);
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = blockIdx.x * NW + wv, nwave = gridDim.x * NW;
+    const int N = Sg.start[Sg.n];
+    const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
+    const int nchunk = nblk * St::BC;
+    uint8_t *ring = lds + L.ring + (size_t)wv * NI * 1024;
+
+    uint32_t goff[NI];
+    bool gval[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) {
+        const int k = lane + 64 * m, b = k / St::BC;
+        gval[m] = k < nchunk;
+        goff[m] = (uint32_t)(b * St::BB + 16 * (k - b * St::BC));
+    }
+    auto issue = [&](int i) {
+        if (i < nrows) {  // wave-uniform
+            const int Rw = wave + i * nwave, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(Sg, Rw)) : 0;
+            const uint8_t *row = Sg.w[sg] + (size_t)(Rw - Sg.start[sg]) * row_bytes;
+#pragma unroll
+            for (int m = 0; m < NI; m++)
+                if (gval[m]) lds_dma16(row + goff[m], ring + m * 1024);
+        }
+    };
+    issue(0);
+
+    for (int b = wv; b < nblk; b += NW) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    __syncthreads();
+    for (int t = threadIdx.x; t < ntask; t += 64 * NW)
+        F::build_task(xq + (size_t)t * F::kDw, qtmp + 64 * (t >> 2), bst + 16 * (t >> 2), t & 3);
+    __syncthreads();  // the prep region becomes the per-wave record area
+    if (nrows == 0) return;
+
+    uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)wv * R * nblk * 10;
+    const typename F::LC c = F::lane_consts(lane);
+    typename F::XS xs0;
+    if (lane < ntask) F::load_x(xs0, xq, lane);
+    const uint8_t *myblk = ring + (lane >> 2) * St::BP;
+
+    int slot = 0;
+    bool stored = false;  // an epilogue store was issued after the current row's loads
+    for (int i = 0; i < nrows; i++) {
+        const int row = wave + i * nwave;
+        if (stored)
+            wait_vm<1>();
+        else
+            wait_vm<0>();
+        typename F::Frag f{};
+        if (lane < ntask) f = St::frag(myblk, c);
+        // the slot's LDS reads have returned before the next row lands in it
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + 1);
+        stored = false;
+        int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
+        uint32_t h = 0;
+        if (lane < ntask) {
+            F::dot(f, xs0, c, Ssum, M);
+            h = F::hdr(f);
+        }
+        // the four tasks of a block are one lane quad: sum them
+#pragma unroll
+        for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
+        if (F::kMin) M = group4_sum_i(M);
+        if (lane < ntask) {
+            const int q = lane & 3;
+            uint32_t *r = rec + ((size_t)slot * nblk + (lane >> 2)) * 10;
+            r[2 * q] = (uint32_t)Ssum[2 * q];
+            r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
+            if (q == 0) {
+                r[8] = (uint32_t)M;
+                r[9] = h;
+            }
+        }
+        slot++;
+        if (slot == R || i + 1 == nrows) {
+            // epilogue (quants.rs:343-358 / :402-411), as gemv_q8k_kernel
+            __builtin_amdgcn_wave_barrier();
+            const int r = lane >> 3, k = lane & 7;
+            float sums = 0.0f, sumf = 0.0f;
+            if (r < slot) {
+                for (int kb = 0; kb < nblk; kb++) {
+                    const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
+                    const uint32_t hw = rr[9];
+                    const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                    sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
+                    if (F::kMin && k == 0) {
+                        const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                        sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
+                    }
+                }
+            }
+            float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
+            if (k == 0 && r < slot) {  // lane 0 always stores: one store instruction per batch
+                const int Rr = row - (slot - 1 - r) * nwave, so = MULTI ? seg_of(Sg, Rr) : 0;
+                Sg.y[so][Rr - Sg.start[so]] = sv;
+            }
+            __builtin_amdgcn_wave_barrier();
+            stored = true;
+            slot = 0;
+        }
+    }
+}
+
 // Any K (multiple of 256) the fast kernel cannot hold: one thread per row
 // running the reference loop verbatim on the workgroup's Q8_K blocks.
 __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, const uint8_t *__restrict__ W,
@@ -984,10 +1132,34 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
     }
 }
 
+#ifndef UQ_Q8K_STREAM
+#define UQ_Q8K_STREAM 1
+#endif
+template <class F, int NI, bool MULTI>
+hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+    constexpr int NW = StreamShape<typename Q8Base<F>::T>::NW;
+    const int N = S.start[S.n];
+    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
+    const void *k = (const void *)gemv_q8k_stream_kernel<F, NI, NW, MULTI>;
+    const hipError_t e = allow_lds(k, L.total);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, NI, NW, MULTI>), dim3(resident_grid(k, L.total, N, NW)),
+                       dim3(64 * NW), L.total, s, S, row_bytes, K, x);
+    return hipGetLastError();
+}
+
 template <class F, bool MULTI>
 hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const Q8KLayout L = q8k_layout<F>(K);
+    if (F::ntasks(K) <= 64 && UQ_Q8K_STREAM) {
+        using B = typename Q8Base<F>::T;
+        const int ni = ((K >> 8) * Stage<B>::BC + 63) / 64;
+        if (ni == 4) return launch_q8k_stream<F, 4, MULTI>(S, row_bytes, K, x, s);
+        if (ni == 3) return launch_q8k_stream<F, 3, MULTI>(S, row_bytes, K, x, s);
+        if (ni == 2) return launch_q8k_stream<F, 2, MULTI>(S, row_bytes, K, x, s);
+        return launch_q8k_stream<F, 1, MULTI>(S, row_bytes, K, x, s);
+    }
     if (F::ntasks(K) <= 64) {
         const void *k = (const void *)gemv_q8k_kernel<F, true, MULTI>;
         hipLaunchKernelGGL((gemv_q8k_kernel<F, true, MULTI>), dim3(resident_grid(k, L.total, N)), dim3(TPB), L.total,

@@ -435,9 +435,11 @@ struct Q4KQ8 {
         for (int k = 0; k < 8; k++) {
             const int dl = sdot4(T[k] & 0x0F0F0F0Fu, s.lo[k], 0);
             const int dh = sdot4((T[k] >> 4) & 0x0F0F0F0Fu, s.hi[k], 0);
-            S[k] = (int)sc0 * dl + (int)sc1 * dh;
+            // 24-bit multiplies (full rate; v_mul_lo_u32 is quarter rate): sc <= 63,
+            // |dl|, |dh| <= 4 * 15 * 127; m <= 63, |bslo|, |bshi| <= 2 * 16 * 127
+            S[k] = mul24((int)sc0, dl) + mul24((int)sc1, dh);
         }
-        M = (int)m0 * s.bslo + (int)m1 * s.bshi;
+        M = mul24((int)m0, s.bslo) + mul24((int)m1, s.bshi);
     }
     // Build the (block, p) record from the block's 256 Q8_K bytes (64 dwords)
     // and bsums.
@@ -497,9 +499,10 @@ struct Q6KQ8 {
             uint32_t T[4];
             transpose4(q0, q2, q1, q3, T);  // T[b] = {l=b, l=8+b, l=4+b, l=12+b}
             const int sc = q6k_scale(f, j);
+            // 24-bit multiplies: |sc| <= 128, |dot| <= 2 * 128 * 127
             for (int b = 0; b < 4; b++) {
-                S[b] += sc * sdot4(T[b], s.X[8 * j + 2 * b], 0);
-                S[4 + b] += sc * sdot4(T[b], s.X[8 * j + 2 * b + 1], 0);
+                S[b] += mul24(sc, sdot4(T[b], s.X[8 * j + 2 * b], 0));
+                S[4 + b] += mul24(sc, sdot4(T[b], s.X[8 * j + 2 * b + 1], 0));
             }
         }
         for (int k = 0; k < 8; k++) S[k] >>= 2;  // products carried 4*(raw-32): exact
