@@ -110,15 +110,31 @@ hipError_t ws_get(size_t need, hipStream_t s, uint8_t **out) {
 // ------------------------------------------------------------ prep kernel
 // One workgroup per row: s_m from max|x|, the x' hi/lo planes in the
 // (0,2,1,3) k order, and the group sums (f64 sum of the 32 x', exact to
-// rounding, then hi/lo).
+// rounding, then hi/lo). NV > 0: the thread's K/1024 float4 of x are loaded
+// once, all before the first is used (K <= 1024 * NV); NV == 0: two passes
+// over x (any K).
+template <int NV>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const float *__restrict__ X, int K, GemmWs ws) {
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const float *x = X + (size_t)m * K;
+    const int nit = (K + 1023) >> 10;  // iterations of 1024 elements (the last may be partial)
+    float4 v[NV > 0 ? NV : 1];
     float mx = 0.0f;
-    for (int k = 4 * t; k < K; k += 1024) {
-        const float4 v = *(const float4 *)(x + k);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            v[i] = i < nit && k < K ? *(const float4 *)(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    } else {
+        for (int k = 4 * t; k < K; k += 1024) {
+            const float4 w = *(const float4 *)(x + k);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x), fabsf(w.y)), fmaxf(fabsf(w.z), fabsf(w.w))));
+        }
     }
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if (lane == 0) red[t >> 6] = mx;
@@ -129,13 +145,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float *__restrict_
     const float inv = ldexpf(1.0f, 10 - ex);  // x' = x * 2^(10-ex), max|x'| in [512, 1024)
     if (t == 0) ws.scale[m] = ldexpf(1.0f, ex - 10);
     _Float16 *ahi = ws.ahi + (size_t)m * K, *alo = ws.alo + (size_t)m * K;
-    // K/4 float4 per row, 8 per group: the loop keeps every group in one
-    // aligned set of 8 lanes (K is a multiple of 1024 or the tail is whole
-    // groups of the last iteration).
-    for (int k = 4 * t; k < ((K + 1023) & ~1023); k += 1024) {
+    // K/4 float4 per row, 8 per group: each iteration keeps every group in
+    // one aligned set of 8 lanes (K is a multiple of 1024 or the tail is
+    // whole groups of the last iteration).
+    auto convert = [&](int k, float4 w) {
         const bool in = k < K;
-        float4 v = in ? *(const float4 *)(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float xs[4] = {v.x * inv, v.z * inv, v.y * inv, v.w * inv};  // slots (0,2,1,3)
+        const float xs[4] = {w.x * inv, w.z * inv, w.y * inv, w.w * inv};  // slots (0,2,1,3)
         h4 hi, lo;
         double gs = 0.0;
         for (int i = 0; i < 4; i++) {
@@ -156,6 +171,14 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float *__restrict_
                 ws.glo[gi] = (_Float16)(gs - (double)gh);
             }
         }
+    };
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (i < nit) convert(4 * t + 1024 * i, v[i]);
+    } else {
+        for (int k = 4 * t; k < nit * 1024; k += 1024)
+            convert(k, k < K ? *(const float4 *)(x + k) : make_float4(0.f, 0.f, 0.f, 0.f));
     }
 }
 
@@ -568,7 +591,12 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
     hipError_t e = ws_get(ws_bytes(M, K), s, &base);
     if (e != hipSuccess) return e;
     const GemmWs ws = ws_carve(base, M, K);
-    hipLaunchKernelGGL(gemm_prep_kernel, dim3(M), dim3(256), 0, s, X, K, ws);
+    if (K <= 4096)
+        hipLaunchKernelGGL(gemm_prep_kernel<4>, dim3(M), dim3(256), 0, s, X, K, ws);
+    else if (K <= 16384)
+        hipLaunchKernelGGL(gemm_prep_kernel<16>, dim3(M), dim3(256), 0, s, X, K, ws);
+    else
+        hipLaunchKernelGGL(gemm_prep_kernel<0>, dim3(M), dim3(256), 0, s, X, K, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // 128-row tiles once there are enough of them to cover the CUs
     return M >= 384 ? gemm_launch<2>(w, M, ws, Y, s) : gemm_launch<1>(w, M, ws, Y, s);

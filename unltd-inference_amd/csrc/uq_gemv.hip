@@ -653,6 +653,9 @@ template <> struct Shape<Q6K> { static constexpr int NW = UQ_Q6K_NW, D = UQ_Q6K_
 #ifndef UQ_STREAM_PAIR_NW
 #define UQ_STREAM_PAIR_NW 12
 #endif
+#ifndef UQ_STREAM_PAIR_S
+#define UQ_STREAM_PAIR_S 1
+#endif
 #ifndef UQ_STREAM_ON
 #define UQ_STREAM_ON 1
 #endif
@@ -661,7 +664,7 @@ template <> struct StreamShape<Q6K> { static constexpr int NW = UQ_STREAM_Q6K_NW
 
 template <class F, int NI, bool PAIR, bool MULTI>
 hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
-    constexpr int SNW = PAIR ? UQ_STREAM_PAIR_NW : StreamShape<F>::NW, SS = PAIR ? 1 : StreamShape<F>::S;
+    constexpr int SNW = PAIR ? UQ_STREAM_PAIR_NW : StreamShape<F>::NW, SS = PAIR ? UQ_STREAM_PAIR_S : StreamShape<F>::S;
     const int N = S.start[S.n];
     const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * (PAIR ? 2 : 1) * NI * 1024;
     const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>;
