@@ -20,22 +20,23 @@
 // A small prep kernel converts X once per call into a library-owned device
 // workspace (hi/lo planes, group sums, row scales).
 //
-// Tiling: a workgroup of 8 waves (two per SIMD, one workgroup per CU)
-// computes a 128 (M) x 256 (N) tile; wave w owns rows 64*(w/4).. and columns
-// 64*(w%4).. (2x2 MFMA tiles of 32x32). K runs in 64-k sub-steps through a
-// ring of three LDS stages, each filled only by direct-to-LDS loads
-// (global_load_lds_dwordx4): the activation planes, the raw weight bytes
-// (header + 32 nibble bytes per row) and, once per block, the group sums.
-// A sub-step waits for its own stage with an explicit vmcnt and a plain
-// s_barrier, so the loads of the next stage stay in flight; each wave
-// dequantizes its B operands (sc*q) from the raw bytes in registers.
-// Within each aligned group of four k, both operands use the k order
-// (0, 2, 1, 3): the weight unpack then needs no byte shuffle. Workgroups
-// are ordered so that each XCD takes mostly one M tile (its activation
-// planes stay in that XCD's L2).
+// Tiling: a workgroup of four waves (one per SIMD, one workgroup per CU)
+// computes a TM (M) x 192 (N) tile, TM = 128 from M = 384 and 64 below; wave
+// (wm, wn) owns 2 (or 1) x 3 MFMA tiles of 32x32. Rows past M or N read a
+// clamped row and are not stored, so any N works. K runs in 64-k sub-steps
+// through a ring of three LDS stages, each filled only by direct-to-LDS
+// loads (global_load_lds_dwordx4) spread over the k-steps before it is
+// needed: the activation planes, the raw weight bytes (header + 32 nibble
+// bytes per row) and, once per block, the group sums. A sub-step waits for
+// its stage with an explicit vmcnt and a plain s_barrier, so the loads of
+// later stages stay in flight; each wave dequantizes its B operands (sc*q)
+// from the raw bytes in registers. Within each aligned group of four k,
+// both operands use the k order (0, 2, 1, 3): the weight unpack then needs
+// no byte shuffle. Workgroups are ordered so that each XCD takes mostly one
+// M tile (its activation planes stay in that XCD's L2).
 //
-// Other formats, N not a multiple of 256, and M < 16 run as M decode-GEMV
-// launches.
+// Other formats, M < 16, and tensors of 4 GiB or more (32-bit row offsets)
+// run as M decode-GEMV launches.
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -606,7 +607,9 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
 
 hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
     if (M == 0 || w.dim_out == 0) return hipSuccess;
-    if (w.dtype == UQ_Q4_K && M >= kMinM) return gemm_mfma_q4k(w, M, X, Y, s);
+    // the MFMA kernel addresses weight rows with 32-bit offsets from the tensor base
+    const bool fits = (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32);
+    if (w.dtype == UQ_Q4_K && M >= kMinM && fits) return gemm_mfma_q4k(w, M, X, Y, s);
     for (int m = 0; m < M; m++) {
         hipError_t e = launch_gemv(w, X + (size_t)m * w.dim_in, Y + (size_t)m * w.dim_out, s);
         if (e != hipSuccess) return e;
