@@ -286,16 +286,37 @@ def bench_decode(hip, steps, warmup, head_w=None, head_h=None):
             uq.ffn_swiglu(g, u, d, bufs["o"], bufs["h"], x, s)
         uq.gemv(head, x, bufs["logits"], s)
 
+    g2, u2 = uq.DeviceArray(4 * nff), uq.DeviceArray(4 * nff)
+
+    def chain_q8k():
+        # the reference forward's semantics: every projection is gemv_quant_q8k
+        for attn, P in built:
+            if attn:
+                q, k, v, o, g, u, d = P
+                uq.gemv_q8k_batch([q, k, v], x, [bufs["a"], bufs["c"], bufs["d"]], s)
+                uq.gemv_q8k(o, bufs["a"], bufs["o"], s)
+            else:
+                qkv, z, beta, alpha, out, g, u, d = P
+                uq.gemv_q8k_batch([qkv, z, beta, alpha], x, [bufs["a"], bufs["b"], bufs["e"], bufs["f"]], s)
+                uq.gemv_q8k(out, bufs["b"], bufs["o"], s)
+            uq.ffn_swiglu_q8k(g, u, d, bufs["o"], g2, u2, bufs["h"], x, s)
+        uq.gemv_q8k(head, x, bufs["logits"], s)
+
     graph = hip.capture(s, chain)
     wall, ev = timed(hip, lambda: hip.launch_graph(graph, s), steps, warmup, s)
     t = ev * 1e-3 / steps
+    graph8 = hip.capture(s, chain_q8k)
+    _, ev8 = timed(hip, lambda: hip.launch_graph(graph8, s), steps, warmup, s)
+    t8 = ev8 * 1e-3 / steps
     launches = sum(2 + 2 for a, _ in built) + 1
     res = {"config": "decode step, synthetic hybrid 9B (32 layers, 24 GDN + 8 attention, FFN 12288, "
                      "Q6_K head 152064), all quantized linear layers in one HIP graph; projections of one input "
                      "batched (uq_gemv_batch)",
            "weight_bytes_per_token": total, "launches": launches, "ms_per_token": t * 1e3,
            "tok_s": 1.0 / t, "gbs": total / t / 1e9, "frac_hbm_peak": total / t / 1e9 / HBM_PEAK_GBS,
-           "tok_s_wall": steps / wall}
+           "tok_s_wall": steps / wall,
+           "q8k": {"semantics": "gemv_quant_q8k for every projection (bit-exact with the reference forward)",
+                   "ms_per_token": t8 * 1e3, "tok_s": 1.0 / t8, "gbs": total / t8 / 1e9}}
     for _, P in built:
         for W in P:
             W.free()

@@ -923,19 +923,23 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
 }
 
 // Streaming variant of gemv_q8k_kernel (bit-exact, same arithmetic) for one
-// Q4_K / Q6_K tensor or a batch, K <= 4096: rows arrive through the per-wave
-// LDS ring of gemv_stream_kernel (coalesced nontemporal direct-to-LDS loads,
-// one row in flight per wave, issued before the wave computes the previous
-// one), instead of per-lane loads into VGPRs. The x records, the lane-quad
-// sums, the per-wave row records and the reference-order epilogue are those
-// of gemv_q8k_kernel.
+// Q4_K / Q6_K tensor or a batch, K <= 12288: rows arrive through the
+// per-wave LDS ring of gemv_stream_kernel (coalesced nontemporal
+// direct-to-LDS loads, one row in flight per wave, issued before the wave
+// computes the previous one), instead of per-lane loads into VGPRs. A lane
+// owns T tasks of a row (t = lane + 64 tt); with T = 1 its x record stays in
+// VGPRs, otherwise each task's record is read from LDS. The lane-quad sums,
+// the per-wave row records and the reference-order epilogue are those of
+// gemv_q8k_kernel.
 template <class F> struct Q8Base;
 template <> struct Q8Base<Q6KQ8> { using T = Q6K; };
 template <> struct Q8Base<Q4KQ8> { using T = Q4K; };
 
+constexpr size_t kQ8SLds = 160 * 1024;  // LDS of one workgroup (one per CU)
+
 struct Q8SLayout {
     size_t xq, d8, region, ring, total;  // byte offsets
-    int R;                               // rows per epilogue batch (<= 8)
+    int R;                               // rows per epilogue batch (<= 8; 0: does not fit)
 };
 template <class F>
 __host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni) {
@@ -944,19 +948,21 @@ __host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni) {
     L.xq = 0;
     L.d8 = (size_t)ntask * F::kDw * 4;
     L.region = (L.d8 + (size_t)nblk * 4 + 15) & ~(size_t)15;
-    int R = (int)(65536 / ((size_t)nw * nblk * 40));
-    L.R = R < 1 ? 1 : (R > 8 ? 8 : R);
-    const size_t prep = (size_t)K + (size_t)(K / 16) * 4;
-    const size_t recs = (size_t)nw * L.R * nblk * 40;
+    const size_t ring = (size_t)nw * ni * 1024, prep = (size_t)K + (size_t)(K / 16) * 4;
+    const size_t left = kQ8SLds > L.region + ring ? kQ8SLds - L.region - ring : 0;
+    int R = (int)(left / ((size_t)nw * nblk * 40 + 16));
+    L.R = R > 8 ? 8 : R;
+    const size_t recs = (size_t)nw * (L.R > 0 ? L.R : 1) * nblk * 40;
     L.ring = (L.region + (prep > recs ? prep : recs) + 15) & ~(size_t)15;
-    L.total = L.ring + (size_t)nw * ni * 1024;
+    L.total = L.ring + ring;
     return L;
 }
 
-template <class F, int NI, int NW, bool MULTI>
+template <class F, int T, int NW, bool MULTI>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
 gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
     using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NI = (16 * T * St::BC + 63) / 64;  // 1 KB loads per row (K <= 4096 T)
     extern __shared__ __align__(16) uint8_t lds[];
     const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
     const int nblk = K >> 8, ntask = 4 * nblk, R = L.R;
@@ -1001,8 +1007,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)wv * R * nblk * 10;
     const typename F::LC c = F::lane_consts(lane);
     typename F::XS xs0;
-    if (lane < ntask) F::load_x(xs0, xq, lane);
-    const uint8_t *myblk = ring + (lane >> 2) * St::BP;
+    if (T == 1 && lane < ntask) F::load_x(xs0, xq, lane);
 
     int slot = 0;
     bool stored = false;  // an epilogue store was issued after the current row's loads
@@ -1012,30 +1017,45 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
             wait_vm<1>();
         else
             wait_vm<0>();
-        typename F::Frag f{};
-        if (lane < ntask) f = St::frag(myblk, c);
+        typename F::Frag f[T];
+#pragma unroll
+        for (int tt = 0; tt < T; tt++) {
+            const int t = lane + 64 * tt;
+            f[tt] = typename F::Frag{};
+            if (t < ntask) f[tt] = St::frag(ring + (t >> 2) * St::BP, c);
+        }
         // the slot's LDS reads have returned before the next row lands in it
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         issue(i + 1);
         stored = false;
-        int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
-        uint32_t h = 0;
-        if (lane < ntask) {
-            F::dot(f, xs0, c, Ssum, M);
-            h = F::hdr(f);
-        }
-        // the four tasks of a block are one lane quad: sum them
 #pragma unroll
-        for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
-        if (F::kMin) M = group4_sum_i(M);
-        if (lane < ntask) {
-            const int q = lane & 3;
-            uint32_t *r = rec + ((size_t)slot * nblk + (lane >> 2)) * 10;
-            r[2 * q] = (uint32_t)Ssum[2 * q];
-            r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
-            if (q == 0) {
-                r[8] = (uint32_t)M;
-                r[9] = h;
+        for (int tt = 0; tt < T; tt++) {
+            const int t = lane + 64 * tt;
+            int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
+            uint32_t h = 0;
+            if (t < ntask) {
+                if (T == 1) {
+                    F::dot(f[tt], xs0, c, Ssum, M);
+                } else {
+                    typename F::XS xs;
+                    F::load_x(xs, xq, t);
+                    F::dot(f[tt], xs, c, Ssum, M);
+                }
+                h = F::hdr(f[tt]);
+            }
+            // the four tasks of a block are one lane quad: sum them
+#pragma unroll
+            for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
+            if (F::kMin) M = group4_sum_i(M);
+            if (t < ntask) {
+                const int q = t & 3;
+                uint32_t *r = rec + ((size_t)slot * nblk + (t >> 2)) * 10;
+                r[2 * q] = (uint32_t)Ssum[2 * q];
+                r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
+                if (q == 0) {
+                    r[8] = (uint32_t)M;
+                    r[9] = h;
+                }
             }
         }
         slot++;
@@ -1138,15 +1158,32 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
 #ifndef UQ_Q8K_STREAM
 #define UQ_Q8K_STREAM 1
 #endif
-template <class F, int NI, bool MULTI>
+// waves per workgroup of the streaming q8k kernel: the head's shapes for
+// K <= 4096; fewer waves for the longer rows of K <= 12288 (LDS ring)
+template <class F, int T> struct Q8SShape { static constexpr int NW = StreamShape<typename Q8Base<F>::T>::NW; };
+template <> struct Q8SShape<Q6KQ8, 2> { static constexpr int NW = 8; };
+template <> struct Q8SShape<Q6KQ8, 3> { static constexpr int NW = 8; };
+template <> struct Q8SShape<Q4KQ8, 2> { static constexpr int NW = 12; };
+template <> struct Q8SShape<Q4KQ8, 3> { static constexpr int NW = 12; };
+
+template <class F, int T, bool MULTI>
+bool q8k_stream_fits(int K) {
+    using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NW = Q8SShape<F, T>::NW, NI = (16 * T * St::BC + 63) / 64;
+    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
+    return L.R > 0 && L.total <= kQ8SLds;
+}
+
+template <class F, int T, bool MULTI>
 hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
-    constexpr int NW = StreamShape<typename Q8Base<F>::T>::NW;
+    using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NW = Q8SShape<F, T>::NW, NI = (16 * T * St::BC + 63) / 64;
     const int N = S.start[S.n];
     const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
-    const void *k = (const void *)gemv_q8k_stream_kernel<F, NI, NW, MULTI>;
+    const void *k = (const void *)gemv_q8k_stream_kernel<F, T, NW, MULTI>;
     const hipError_t e = allow_lds(k, L.total);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, NI, NW, MULTI>), dim3(resident_grid(k, L.total, N, NW)),
+    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, MULTI>), dim3(resident_grid(k, L.total, N, NW)),
                        dim3(64 * NW), L.total, s, S, row_bytes, K, x);
     return hipGetLastError();
 }
@@ -1155,13 +1192,11 @@ template <class F, bool MULTI>
 hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const Q8KLayout L = q8k_layout<F>(K);
-    if (F::ntasks(K) <= 64 && UQ_Q8K_STREAM) {
-        using B = typename Q8Base<F>::T;
-        const int ni = ((K >> 8) * Stage<B>::BC + 63) / 64;
-        if (ni == 4) return launch_q8k_stream<F, 4, MULTI>(S, row_bytes, K, x, s);
-        if (ni == 3) return launch_q8k_stream<F, 3, MULTI>(S, row_bytes, K, x, s);
-        if (ni == 2) return launch_q8k_stream<F, 2, MULTI>(S, row_bytes, K, x, s);
-        return launch_q8k_stream<F, 1, MULTI>(S, row_bytes, K, x, s);
+    if (UQ_Q8K_STREAM) {
+        const int T = (F::ntasks(K) + 63) / 64;  // tasks per lane
+        if (T == 1 && q8k_stream_fits<F, 1, MULTI>(K)) return launch_q8k_stream<F, 1, MULTI>(S, row_bytes, K, x, s);
+        if (T == 2 && q8k_stream_fits<F, 2, MULTI>(K)) return launch_q8k_stream<F, 2, MULTI>(S, row_bytes, K, x, s);
+        if (T == 3 && q8k_stream_fits<F, 3, MULTI>(K)) return launch_q8k_stream<F, 3, MULTI>(S, row_bytes, K, x, s);
     }
     if (F::ntasks(K) <= 64) {
         const void *k = (const void *)gemv_q8k_kernel<F, true, MULTI>;
