@@ -515,9 +515,13 @@ uq_status uq_ffn_swiglu_q8k(uq_weights gh, uq_weights uh, uq_weights dh, const f
     if (!d_x || !d_g || !d_u || !d_h || !d_y) return fail(UQ_ERR_ARG, "ffn_swiglu_q8k: null device pointer");
     const hipStream_t s = (hipStream_t)stream;
     const uq::WeightsView gu[2] = {uq::view(*g), uq::view(*u)};
-    float *const gy[2] = {d_g, d_u};
-    UQ_HIP(uq::launch_gemv_q8k_batch(gu, 2, d_x, gy, s), "ffn_q8k gate/up launch");
-    UQ_HIP(uq::launch_swiglu(d_g, d_u, g->dim_out, d_h, s), "ffn_q8k swiglu launch");
+    bool fused = false;
+    UQ_HIP(uq::launch_q8k_gate_up(gu[0], gu[1], d_x, d_g, d_u, d_h, s, &fused), "ffn_q8k gate/up/swiglu launch");
+    if (!fused) {
+        float *const gy[2] = {d_g, d_u};
+        UQ_HIP(uq::launch_gemv_q8k_batch(gu, 2, d_x, gy, s), "ffn_q8k gate/up launch");
+        UQ_HIP(uq::launch_swiglu(d_g, d_u, g->dim_out, d_h, s), "ffn_q8k swiglu launch");
+    }
     UQ_HIP(uq::launch_gemv_q8k(uq::view(*dn), d_h, d_y, s), "ffn_q8k down launch");
     return UQ_OK;
 }

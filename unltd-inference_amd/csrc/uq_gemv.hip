@@ -333,7 +333,8 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
             } else {
                 wait_vm<0>();
             }
-            typename F::Frag f{}, f2{};
+            // read only by lanes with a task: no zero fill (it cost a move per dword per row)
+            typename F::Frag f, f2;
             const uint8_t *b0 = myblk + (r % S) * UNIT * 1024;
             if (lane < ntask) {
                 f = St::frag(b0, c);
@@ -941,30 +942,36 @@ struct Q8SLayout {
     size_t xq, d8, region, ring, total;  // byte offsets
     int R;                               // rows per epilogue batch (<= 8; 0: does not fit)
 };
+// NT = 2: gate/up pairs (two rows per ring unit, two record sets per wave)
 template <class F>
-__host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni) {
+__host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni, int nt = 1) {
     const int nblk = K >> 8, ntask = 4 * nblk;
     Q8SLayout L;
     L.xq = 0;
     L.d8 = (size_t)ntask * F::kDw * 4;
     L.region = (L.d8 + (size_t)nblk * 4 + 15) & ~(size_t)15;
-    const size_t ring = (size_t)nw * ni * 1024, prep = (size_t)K + (size_t)(K / 16) * 4;
+    const size_t ring = (size_t)nw * nt * ni * 1024, prep = (size_t)K + (size_t)(K / 16) * 4;
     const size_t left = kQ8SLds > L.region + ring ? kQ8SLds - L.region - ring : 0;
-    int R = (int)(left / ((size_t)nw * nblk * 40 + 16));
+    int R = (int)(left / ((size_t)nw * nt * nblk * 40 + 16));
     L.R = R > 8 ? 8 : R;
-    const size_t recs = (size_t)nw * (L.R > 0 ? L.R : 1) * nblk * 40;
+    const size_t recs = (size_t)nw * nt * (L.R > 0 ? L.R : 1) * nblk * 40;
     L.ring = (L.region + (prep > recs ? prep : recs) + 15) & ~(size_t)15;
     L.total = L.ring + ring;
     return L;
 }
 
-template <class F, int T, int NW, bool MULTI>
+// PAIR (T = 1, one segment): a ring unit is gate row r (Sg.w) and up row r
+// (Sg.w2); the wave keeps a record set for each and stores g (Sg.y[0]), u
+// (Sg.y[1]) and h = swiglu(g, u) (Sg.y[2]).
+template <class F, int T, int NW, bool MULTI, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
 gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
+    static_assert(!PAIR || (T == 1 && !MULTI), "pairs: one segment, K <= 4096");
     using St = Stage<typename Q8Base<F>::T>;
     constexpr int NI = (16 * T * St::BC + 63) / 64;  // 1 KB loads per row (K <= 4096 T)
+    constexpr int NT = PAIR ? 2 : 1;                 // rows per ring unit
     extern __shared__ __align__(16) uint8_t lds[];
-    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI);
+    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI, NT);
     const int nblk = K >> 8, ntask = 4 * nblk, R = L.R;
     uint32_t *xq = (uint32_t *)(lds + L.xq);
     float *d8 = (float *)(lds + L.d8);
@@ -976,7 +983,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     const int N = Sg.start[Sg.n];
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
     const int nchunk = nblk * St::BC;
-    uint8_t *ring = lds + L.ring + (size_t)wv * NI * 1024;
+    uint8_t *ring = lds + L.ring + (size_t)wv * NT * NI * 1024;
 
     uint32_t goff[NI];
     bool gval[NI];
@@ -989,10 +996,13 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     auto issue = [&](int i) {
         if (i < nrows) {  // wave-uniform
             const int Rw = wave + i * nwave, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(Sg, Rw)) : 0;
-            const uint8_t *row = Sg.w[sg] + (size_t)(Rw - Sg.start[sg]) * row_bytes;
 #pragma unroll
-            for (int m = 0; m < NI; m++)
-                if (gval[m]) lds_dma16(row + goff[m], ring + m * 1024);
+            for (int u = 0; u < NT; u++) {
+                const uint8_t *row = (u == 0 ? Sg.w[sg] : Sg.w2[sg]) + (size_t)(Rw - Sg.start[sg]) * row_bytes;
+#pragma unroll
+                for (int m = 0; m < NI; m++)
+                    if (gval[m]) lds_dma16(row + goff[m], ring + (u * NI + m) * 1024);
+            }
         }
     };
     issue(0);
@@ -1004,84 +1014,103 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     __syncthreads();  // the prep region becomes the per-wave record area
     if (nrows == 0) return;
 
-    uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)wv * R * nblk * 10;
+    // record sets: [pair half][slot][block] x 10 dwords
+    uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)wv * NT * R * nblk * 10;
     const typename F::LC c = F::lane_consts(lane);
     typename F::XS xs0;
     if (T == 1 && lane < ntask) F::load_x(xs0, xq, lane);
 
     int slot = 0;
-    bool stored = false;  // an epilogue store was issued after the current row's loads
+    bool stored = false;  // the epilogue stores were issued after the current row's loads
     for (int i = 0; i < nrows; i++) {
         const int row = wave + i * nwave;
         if (stored)
-            wait_vm<1>();
+            wait_vm<NT == 2 ? 3 : 1>();
         else
             wait_vm<0>();
-        typename F::Frag f[T];
+        // read only by lanes with a task: no zero fill
+        typename F::Frag f[NT][T];
 #pragma unroll
-        for (int tt = 0; tt < T; tt++) {
-            const int t = lane + 64 * tt;
-            f[tt] = typename F::Frag{};
-            if (t < ntask) f[tt] = St::frag(ring + (t >> 2) * St::BP, c);
-        }
+        for (int u = 0; u < NT; u++)
+#pragma unroll
+            for (int tt = 0; tt < T; tt++) {
+                const int t = lane + 64 * tt;
+                if (t < ntask) f[u][tt] = St::frag(ring + u * NI * 1024 + (t >> 2) * St::BP, c);
+            }
         // the slot's LDS reads have returned before the next row lands in it
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         issue(i + 1);
         stored = false;
 #pragma unroll
-        for (int tt = 0; tt < T; tt++) {
-            const int t = lane + 64 * tt;
-            int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
-            uint32_t h = 0;
-            if (t < ntask) {
-                if (T == 1) {
-                    F::dot(f[tt], xs0, c, Ssum, M);
-                } else {
-                    typename F::XS xs;
-                    F::load_x(xs, xq, t);
-                    F::dot(f[tt], xs, c, Ssum, M);
-                }
-                h = F::hdr(f[tt]);
-            }
-            // the four tasks of a block are one lane quad: sum them
+        for (int u = 0; u < NT; u++)
 #pragma unroll
-            for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
-            if (F::kMin) M = group4_sum_i(M);
-            if (t < ntask) {
-                const int q = t & 3;
-                uint32_t *r = rec + ((size_t)slot * nblk + (t >> 2)) * 10;
-                r[2 * q] = (uint32_t)Ssum[2 * q];
-                r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
-                if (q == 0) {
-                    r[8] = (uint32_t)M;
-                    r[9] = h;
+            for (int tt = 0; tt < T; tt++) {
+                const int t = lane + 64 * tt;
+                int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
+                uint32_t h = 0;
+                if (t < ntask) {
+                    if (T == 1) {
+                        F::dot(f[u][tt], xs0, c, Ssum, M);
+                    } else {
+                        typename F::XS xs;
+                        F::load_x(xs, xq, t);
+                        F::dot(f[u][tt], xs, c, Ssum, M);
+                    }
+                    h = F::hdr(f[u][tt]);
                 }
-            }
-        }
-        slot++;
-        if (slot == R || i + 1 == nrows) {
-            // epilogue (quants.rs:343-358 / :402-411), as gemv_q8k_kernel
-            __builtin_amdgcn_wave_barrier();
-            const int r = lane >> 3, k = lane & 7;
-            float sums = 0.0f, sumf = 0.0f;
-            if (r < slot) {
-                for (int kb = 0; kb < nblk; kb++) {
-                    const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
-                    const uint32_t hw = rr[9];
-                    const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
-                    sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
-                    if (F::kMin && k == 0) {
-                        const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
-                        sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
+                // the four tasks of a block are one lane quad: sum them
+#pragma unroll
+                for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
+                if (F::kMin) M = group4_sum_i(M);
+                if (t < ntask) {
+                    const int q = t & 3;
+                    uint32_t *r = rec + (((size_t)u * R + slot) * nblk + (t >> 2)) * 10;
+                    r[2 * q] = (uint32_t)Ssum[2 * q];
+                    r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
+                    if (q == 0) {
+                        r[8] = (uint32_t)M;
+                        r[9] = h;
                     }
                 }
             }
-            float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
+        slot++;
+        if (slot == R || i + 1 == nrows) {
+            // epilogue (quants.rs:343-358 / :402-411), as gemv_q8k_kernel:
+            // lane (r, k) replays sums[k] += d*sumi[k] over the blocks in
+            // order (k = 0 also sumf -= dmin*minsum), then
+            // s = sumf + sums[0] + ... + sums[7]
+            __builtin_amdgcn_wave_barrier();
+            const int r = lane >> 3, k = lane & 7;
+            float out[NT];
 #pragma unroll
-            for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
-            if (k == 0 && r < slot) {  // lane 0 always stores: one store instruction per batch
+            for (int u = 0; u < NT; u++) {
+                float sums = 0.0f, sumf = 0.0f;
+                if (r < slot) {
+                    for (int kb = 0; kb < nblk; kb++) {
+                        const uint32_t *rr = rec + (((size_t)u * R + r) * nblk + kb) * 10;
+                        const uint32_t hw = rr[9];
+                        const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                        sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
+                        if (F::kMin && k == 0) {
+                            const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                            sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
+                        }
+                    }
+                }
+                float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
+                out[u] = sv;
+            }
+            if (k == 0 && r < slot) {  // lane 0 always stores: NT == 1: one store, else three
                 const int Rr = row - (slot - 1 - r) * nwave, so = MULTI ? seg_of(Sg, Rr) : 0;
-                Sg.y[so][Rr - Sg.start[so]] = sv;
+                if (PAIR) {
+                    Sg.y[0][Rr] = out[0];
+                    Sg.y[1][Rr] = out[NT - 1];
+                    Sg.y[2][Rr] = swiglu1(out[0], out[NT - 1]);
+                } else {
+                    Sg.y[so][Rr - Sg.start[so]] = out[0];
+                }
             }
             __builtin_amdgcn_wave_barrier();
             stored = true;
@@ -1188,6 +1217,23 @@ hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float
     return hipGetLastError();
 }
 
+template <class F>
+hipError_t launch_q8k_pair(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done) {
+    using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NW = UQ_STREAM_PAIR_NW, NI = (16 * St::BC + 63) / 64;
+    *done = false;
+    const Q8SLayout L = q8k_stream_layout<F>(K, NW, NI, 2);
+    if (!UQ_Q8K_STREAM || F::ntasks(K) > 64 || L.R == 0 || L.total > kQ8SLds) return hipSuccess;
+    const int N = S.start[S.n];
+    const void *k = (const void *)gemv_q8k_stream_kernel<F, 1, NW, false, true>;
+    const hipError_t e = allow_lds(k, L.total);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, 1, NW, false, true>), dim3(resident_grid(k, L.total, N, NW)),
+                       dim3(64 * NW), L.total, s, S, row_bytes, K, x);
+    *done = true;
+    return hipGetLastError();
+}
+
 template <class F, bool MULTI>
 hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
@@ -1266,6 +1312,30 @@ hipError_t launch_gemv_q8k_batch(const WeightsView *w, int n, const float *x, fl
 hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u, const float *x, float *h,
                                  hipStream_t s) {
     return launch_segs(g.dtype, g.dim_in, g.row_bytes, one_seg(g, u.bytes, h), true, x, s);
+}
+
+// g = gemv_quant_q8k(gate, x), u = gemv_quant_q8k(up, x) and h = swiglu(g, u)
+// in one launch; *done is false when the shapes do not take the streaming
+// kernel (the caller then runs the three steps).
+hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const float *x, float *yg, float *yu,
+                              float *h, hipStream_t s, bool *done) {
+    *done = false;
+    if (g.dim_out == 0) {
+        *done = true;
+        return hipSuccess;
+    }
+    Segs S{};
+    S.n = 1;
+    S.start[0] = 0;
+    S.start[1] = g.dim_out;
+    S.w[0] = g.bytes;
+    S.w2[0] = u.bytes;
+    S.y[0] = yg;
+    S.y[1] = yu;
+    S.y[2] = h;
+    if (g.dtype == UQ_Q4_K) return launch_q8k_pair<Q4KQ8>(S, g.row_bytes, g.dim_in, x, s, done);
+    if (g.dtype == UQ_Q6_K) return launch_q8k_pair<Q6KQ8>(S, g.row_bytes, g.dim_in, x, s, done);
+    return hipSuccess;
 }
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {

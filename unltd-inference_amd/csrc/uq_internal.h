@@ -103,6 +103,9 @@ hipError_t launch_gemv_q8k_batch(const WeightsView *w, int n, const float *x, fl
 hipError_t launch_gate_up_swiglu(const WeightsView &g, const WeightsView &u,
                                  const float *x, float *h, hipStream_t s);
 // y = gemv_quant_q8k(W, x), bit-exact.
+// gate/up q8k GEMVs and swiglu in one launch when the shapes allow (*done)
+hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const float *x, float *yg, float *yu,
+                              float *h, hipStream_t s, bool *done);
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y,
                            hipStream_t s);
 // Y[m] = W X[m] for m < M.
