@@ -1119,6 +1119,137 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     }
 }
 
+// K-split variant for 4096 < K <= 16384 (one tensor, bit-exact): the
+// workgroup's waves are KS slices x NG row groups. A wave streams its slice
+// (16 blocks) of its group's rows through its own ring slot and keeps its
+// lane's x record in VGPRs; the slice's block records go to the group's
+// shared record area. Every R rows all waves meet at a barrier, the slice-0
+// wave of each group runs the reference-order epilogue over the 48 (K/256)
+// blocks, and a second barrier frees the records. Every wave runs the
+// workgroup's largest row count, so all reach the same barriers.
+template <class F, int KS, int NG>
+__global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg, size_t row_bytes, int K,
+                                                                  const float *__restrict__ x) {
+    using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NW = KS * NG;
+    constexpr int NI = (16 * St::BC + 63) / 64;  // 1 KB loads per slice
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int nblk = K >> 8, ntask = 4 * nblk;
+    const Q8SLayout L = q8k_stream_layout<F>(K, NG, NI * KS);  // records per group, ring per wave
+    const int R = L.R;
+    uint32_t *xq = (uint32_t *)(lds + L.xq);
+    float *d8 = (float *)(lds + L.d8);
+    uint32_t *qtmp = (uint32_t *)(lds + L.region);
+    int *bst = (int *)(lds + L.region + K);
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sl = wv % KS, gi = wv / KS;
+    const int t = 64 * sl + lane;  // this lane's task
+    const bool act = t < ntask;
+    const int G = blockIdx.x * NG + gi, nG = gridDim.x * NG;
+    const int N = Sg.start[Sg.n];
+    const int nrows = G < N ? (N - 1 - G) / nG + 1 : 0;
+    const int G0 = blockIdx.x * NG;
+    const int nmax = G0 < N ? (N - 1 - G0) / nG + 1 : 0;  // rows of the workgroup's first group
+    const int nch = (min(nblk, 16 * sl + 16) - 16 * sl) * St::BC;  // chunks of this slice
+    uint8_t *ring = lds + L.ring + (size_t)wv * NI * 1024;
+
+    uint32_t goff[NI];
+    bool gval[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) {
+        const int k = lane + 64 * m, b = k / St::BC;
+        gval[m] = k < nch;
+        goff[m] = (uint32_t)((16 * sl + b) * St::BB + 16 * (k - b * St::BC));
+    }
+    auto issue = [&](int i) {
+        if (i < nrows) {  // wave-uniform
+            const uint8_t *row = Sg.w[0] + (size_t)(G + i * nG) * row_bytes;
+#pragma unroll
+            for (int m = 0; m < NI; m++)
+                if (gval[m]) lds_dma16(row + goff[m], ring + m * 1024);
+        }
+    };
+    issue(0);
+
+    for (int b = wv; b < nblk; b += NW) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    __syncthreads();
+    for (int q = threadIdx.x; q < ntask; q += 64 * NW)
+        F::build_task(xq + (size_t)q * F::kDw, qtmp + 64 * (q >> 2), bst + 16 * (q >> 2), q & 3);
+    __syncthreads();  // the prep region becomes the record area
+    if (nmax == 0) return;  // the whole workgroup: no rows
+
+    uint32_t *rec = (uint32_t *)(lds + L.region) + (size_t)gi * R * nblk * 10;  // [slot][block] x 10
+    const typename F::LC c = F::lane_consts(lane);
+    typename F::XS xs0;
+    if (act) F::load_x(xs0, xq, t);
+
+    int slot = 0;
+    bool stored = false;  // this wave's epilogue store came after its current row's loads
+    for (int i = 0; i < nmax; i++) {
+        if (i < nrows) {  // wave-uniform
+            if (stored)
+                wait_vm<1>();
+            else
+                wait_vm<0>();
+            typename F::Frag f;
+            if (act) f = St::frag(ring + (lane >> 2) * St::BP, c);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(i + 1);
+            stored = false;
+            int Ssum[8] = {0, 0, 0, 0, 0, 0, 0, 0}, M = 0;
+            uint32_t h = 0;
+            if (act) {
+                F::dot(f, xs0, c, Ssum, M);
+                h = F::hdr(f);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) Ssum[k] = group4_sum_i(Ssum[k]);
+            if (F::kMin) M = group4_sum_i(M);
+            if (act) {
+                const int q = t & 3;
+                uint32_t *r = rec + ((size_t)slot * nblk + (t >> 2)) * 10;
+                r[2 * q] = (uint32_t)Ssum[2 * q];
+                r[2 * q + 1] = (uint32_t)Ssum[2 * q + 1];
+                if (q == 0) {
+                    r[8] = (uint32_t)M;
+                    r[9] = h;
+                }
+            }
+        }
+        slot++;
+        if (slot == R || i + 1 == nmax) {
+            __syncthreads();  // every slice's records of these rows are written
+            const int nr = min(slot, nrows - (i + 1 - slot));  // rows of this group in the batch
+            if (sl == 0 && nr > 0) {
+                // epilogue (quants.rs:343-358 / :402-411), as gemv_q8k_kernel
+                const int r = lane >> 3, k = lane & 7;
+                float sums = 0.0f, sumf = 0.0f;
+                if (r < nr) {
+                    for (int kb = 0; kb < nblk; kb++) {
+                        const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
+                        const uint32_t hw = rr[9];
+                        const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                        sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
+                        if (F::kMin && k == 0) {
+                            const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                            sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
+                        }
+                    }
+                }
+                float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
+                if (k == 0 && r < nr)  // lane 0 always stores: one store instruction
+                    Sg.y[0][G + (i + 1 - slot + r) * nG] = sv;
+                stored = true;
+            }
+            __syncthreads();  // the records are free again
+            slot = 0;
+        }
+    }
+}
+
 // Any K (multiple of 256) the fast kernel cannot hold: one thread per row
 // running the reference loop verbatim on the workgroup's Q8_K blocks.
 __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, const uint8_t *__restrict__ W,
@@ -1234,10 +1365,40 @@ hipError_t launch_q8k_pair(const Segs &S, size_t row_bytes, int K, const float *
     return hipGetLastError();
 }
 
+template <class F>
+hipError_t launch_q8k_ks(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done) {
+    using St = Stage<typename Q8Base<F>::T>;
+    constexpr int NI = (16 * St::BC + 63) / 64;
+    const int ks = (F::ntasks(K) + 63) / 64;
+    *done = false;
+    auto go = [&](auto kern, int KSv, int NGv) -> hipError_t {
+        const Q8SLayout L = q8k_stream_layout<F>(K, NGv, NI * KSv);
+        if (L.R == 0 || L.total > kQ8SLds) return hipSuccess;
+        const int N = S.start[S.n];
+        const void *k = (const void *)kern;
+        hipError_t e = allow_lds(k, L.total);
+        if (e != hipSuccess) return e;
+        // one workgroup per CU, NG row groups each, rows dealt round-robin to the groups
+        const int rpg = (N + num_cus() * NGv - 1) / (num_cus() * NGv);  // rows per group
+        const int grid = (N + rpg * NGv - 1) / (rpg * NGv);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * KSv * NGv), L.total, s, S, row_bytes, K, x);
+        *done = true;
+        return hipGetLastError();
+    };
+    if (ks == 2) return go(gemv_q8k_ks_kernel<F, 2, 6>, 2, 6);
+    if (ks == 3) return go(gemv_q8k_ks_kernel<F, 3, 4>, 3, 4);
+    return hipSuccess;
+}
+
 template <class F, bool MULTI>
 hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const Q8KLayout L = q8k_layout<F>(K);
+    if (UQ_Q8K_STREAM && !MULTI && F::ntasks(K) > 64 && F::ntasks(K) <= 192) {
+        bool done = false;
+        const hipError_t e = launch_q8k_ks<F>(S, row_bytes, K, x, s, &done);
+        if (e != hipSuccess || done) return e;
+    }
     if (UQ_Q8K_STREAM) {
         const int T = (F::ntasks(K) + 63) / 64;  // tasks per lane
         if (T == 1 && q8k_stream_fits<F, 1, MULTI>(K)) return launch_q8k_stream<F, 1, MULTI>(S, row_bytes, K, x, s);
