@@ -1119,7 +1119,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     }
 }
 
-// K-split variant for 4096 < K <= 16384 (one tensor, bit-exact): the
+// K-split variant for 4096 < K <= 12288 (one tensor, bit-exact): the
 // workgroup's waves are KS slices x NG row groups. A wave streams its slice
 // (16 blocks) of its group's rows through its own ring slot and keeps its
 // lane's x record in VGPRs; the slice's block records go to the group's
