@@ -168,10 +168,13 @@ uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count
 /* Batched prefill: d_y[m][dim_out] = W . d_x[m][dim_in] for m < m_rows, with
  * gemv_quant semantics per row (the reference feeds prefill tokens one at a
  * time, greedy.rs:55-65; each row equals gemv_quant of that token).
- * Q4_K with m_rows >= 16 and dim_out % 256 == 0 runs on the f16 MFMA and
+ * Q4_K with m_rows >= 8 (and a tensor below 4 GiB) runs on the f16 MFMA and
  * uses a library-owned device workspace of about 4*m_rows*dim_in bytes per
  * (device, stream), allocated on first use and grown when a call needs more
- * (growing synchronizes the stream). Other shapes run as m_rows GEMVs. */
+ * (growing synchronizes the stream). When the output tiles do not cover the
+ * CUs (small m_rows), K is split and the workspace also holds the partial
+ * results: at most CUs x 64 x 192 floats (12.6 MB on 256 CUs). Other shapes
+ * run as m_rows GEMVs. */
 uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                   void *stream);
 

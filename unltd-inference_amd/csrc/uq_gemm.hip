@@ -35,7 +35,12 @@
 // no byte shuffle. Workgroups are ordered so that each XCD takes mostly one
 // M tile (its activation planes stay in that XCD's L2).
 //
-// Other formats, M < 16, and tensors of 4 GiB or more (32-bit row offsets)
+// Small M (fewer tiles than CUs) splits K: each tile's 256-k blocks are cut
+// into ks ranges, one workgroup per (tile, range), each writing its partial
+// tile to the workspace; gemm_splitk_reduce then sums the ks partials in
+// range order into Y.
+//
+// Other formats, M < 8, and tensors of 4 GiB or more (32-bit row offsets)
 // run as M decode-GEMV launches.
 #include <algorithm>
 #include <map>
@@ -56,7 +61,7 @@ typedef float f16x __attribute__((ext_vector_type(16)));
 constexpr int GN = 192;            // workgroup tile columns (rows: 64 or 128)
 constexpr int GTPB = 256;          // 4 waves, one per SIMD
 constexpr int SUBK = 64;           // k per staging sub-step (one group pair)
-constexpr int kMinM = 16;          // below this M the GEMV path is used
+constexpr int kMinM = 8;           // below this M the GEMV path is used
 
 // ------------------------------------------------------------ workspace
 struct GemmWs {
@@ -304,7 +309,9 @@ __device__ __forceinline__ void sched_step() {
 //    slot and the reads of it are discarded, so counts stay static.
 template <int WMT>
 __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__restrict__ W, size_t row_bytes, int K,
-                                                           int N, int M, GemmWs ws, int ntn, float *__restrict__ Y) {
+                                                           int N, int M, GemmWs ws, int ntn, int ks,
+                                                           float *__restrict__ Y, float *__restrict__ Ypart,
+                                                           size_t part_stride) {
     constexpr int TM = 64 * WMT;
     constexpr int NA = TM / 16;  // A loads per wave per stage (1 KB each)
     constexpr int NAP = NA / 4;  // ... per k-step
@@ -316,14 +323,20 @@ __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__rest
     // XCD x takes a contiguous run of the M-major tile list, i.e. mostly one
     // M tile, so that tile's activation planes stay in the XCD's L2 while
     // its N tiles stream the weights.
-    const int ntm = (M + TM - 1) / TM, T = ntm * ntn, per = (T + 7) / 8;
+    // With ks > 1 the K blocks are split into ks ranges: the list is
+    // (M tile, K range, N tile), and each workgroup writes its range's
+    // partial tile to Ypart[kidx] for gemm_splitk_reduce.
+    const int ntm = (M + TM - 1) / TM, T = ntm * ntn * ks, per = (T + 7) / 8;
     const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if ((blockIdx.x >> 3) >= per || L >= T) return;  // padding of the last round
-    const int mt = L / ntn, nt = L % ntn;
+    const int nt = L % ntn, mk = L / ntn, mt = mk / ks, kidx = mk % ks;
     const int m0 = mt * TM, n0 = nt * GN;
     const int wm = wv >> 1, wn = wv & 1;
     const int lr = lane & 31, lh = lane >> 5;
-    const int nblk = K / 256, KG = K / 32, nsub = 4 * nblk;
+    const int nbt = K / 256, kb0 = kidx * nbt / ks;
+    const int nblk = (kidx + 1) * nbt / ks - kb0, KG = K / 32, nsub = 4 * nblk;
+    W += (size_t)kb0 * BQ4K;  // the range's first block: the row strides stay those of K
+    float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
 
     // Per-lane source offsets of the loads; only the uniform stage term
     // changes per sub-step. Lane i of a 1 KB load fills bytes 1024 J + 16 i
@@ -353,10 +366,10 @@ __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__rest
     uint32_t goff;
     {
         const int lin = 1024 * wv + 16 * lane, hl = (lin / (TM * 16)) & 1, row = (lin >> 4) % TM;
-        gbase = hl ? ws.glo : ws.ghi;
+        gbase = (hl ? ws.glo : ws.ghi) + 8 * kb0;
         goff = (uint32_t)((size_t)min(m0 + row, M - 1) * KG * 2);
     }
-    const uint8_t *abase = (const uint8_t *)ws.ahi;
+    const uint8_t *abase = (const uint8_t *)ws.ahi + (size_t)kb0 * 512;
     // Part p (0..3) of stage v's loads: A loads [p*NAP, (p+1)*NAP), then B
     // load p (p < 3) or the G load (p == 3, when the stage starts a block:
     // G_STAGE). Stages past the end re-read the last sub-step.
@@ -543,7 +556,7 @@ __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__rest
         for (int i = 0; i < WMT; i++)
 #pragma unroll
             for (int j = 0; j < 3; j++) {
-                float *y = Y + (size_t)(m0 + 32 * WMT * wm + 32 * i + 4 * lh) * N + n0 + 96 * wn + 32 * j + lr;
+                float *y = Yo + (size_t)(m0 + 32 * WMT * wm + 32 * i + 4 * lh) * N + n0 + 96 * wn + 32 * j + lr;
 #pragma unroll
                 for (int r = 0; r < 16; r++) y[(size_t)(8 * (r >> 2) + (r & 3)) * N] = C[i][j][r];
             }
@@ -557,21 +570,57 @@ __global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__rest
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + 32 * WMT * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m < M && n < N) Y[(size_t)m * N + n] = C[i][j][r];
+                if (m < M && n < N) Yo[(size_t)m * N + n] = C[i][j][r];
             }
         }
 }
 
+// Sum of the ks partial results of a split-K launch, in range order.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ P, int ks, size_t stride,
+                                                          size_t MN, float *__restrict__ Y) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+        float v = P[i];
+        for (int k = 1; k < ks; k++) v += P[(size_t)k * stride + i];
+        Y[i] = v;
+    }
+}
+
+int gemm_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        n = hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                ? v
+                : 256;
+    }
+    return n;
+}
+
+// K ranges per tile: enough workgroups to cover the CUs when the tiles alone
+// do not (small M), at most one 256-k block per range.
+int gemm_ksplit(int M, int N, int K, int TM) {
+    const int tiles = ((M + TM - 1) / TM) * ((N + GN - 1) / GN);
+    return std::max(1, std::min(K / 256, gemm_cus() / std::max(tiles, 1)));
+}
+
+size_t part_stride(int M, int N) { return ((size_t)M * N + 63) & ~(size_t)63; }
+
 template <int WMT>
-hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, hipStream_t s) {
+hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out, TM = 64 * WMT;
     const int ntm = (M + TM - 1) / TM, ntn = (N + GN - 1) / GN;
-    const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
+    const int grid = 8 * ((ntm * ntn * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
+    const size_t ps = part_stride(M, N);
     const void *k = (const void *)gemm_q4k_kernel<WMT>;
     hipError_t e = allow_lds(k, sizeof(GemmLds<64 * WMT>));
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gemm_q4k_kernel<WMT>, dim3(grid), dim3(GTPB), sizeof(GemmLds<64 * WMT>), s, w.bytes,
-                       w.row_bytes, K, N, M, ws, ntn, Y);
+                       w.row_bytes, K, N, M, ws, ntn, ks, Y, part, ps);
+    if ((e = hipGetLastError()) != hipSuccess || ks == 1) return e;
+    const size_t MN = (size_t)M * N;
+    const int rgrid = (int)std::min<size_t>((MN + 255) / 256, 4096);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const float *)part, ks, ps, MN, Y);
     return hipGetLastError();
 }
 
@@ -588,10 +637,15 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
         }
         return hipSuccess;
     }
+    // 128-row tiles once there are enough of them to cover the CUs
+    const bool big = M >= 384;
+    const int N = w.dim_out, ks = gemm_ksplit(M, N, K, big ? 128 : 64);
+    const size_t wsb = ws_bytes(M, K), pb = ks > 1 ? (size_t)ks * part_stride(M, N) * 4 : 0;
     uint8_t *base = nullptr;
-    hipError_t e = ws_get(ws_bytes(M, K), s, &base);
+    hipError_t e = ws_get(wsb + pb, s, &base);
     if (e != hipSuccess) return e;
     const GemmWs ws = ws_carve(base, M, K);
+    float *part = ks > 1 ? (float *)(base + wsb) : nullptr;
     if (K <= 4096)
         hipLaunchKernelGGL(gemm_prep_kernel<4>, dim3(M), dim3(256), 0, s, X, K, ws);
     else if (K <= 16384)
@@ -599,8 +653,7 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
     else
         hipLaunchKernelGGL(gemm_prep_kernel<0>, dim3(M), dim3(256), 0, s, X, K, ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    // 128-row tiles once there are enough of them to cover the CUs
-    return M >= 384 ? gemm_launch<2>(w, M, ws, Y, s) : gemm_launch<1>(w, M, ws, Y, s);
+    return big ? gemm_launch<2>(w, M, ws, Y, part, ks, s) : gemm_launch<1>(w, M, ws, Y, part, ks, s);
 }
 
 }  // namespace
