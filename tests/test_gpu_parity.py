@@ -316,8 +316,8 @@ def _gemm_check(K, N, M, X, seed, what):
                                    (12288, 256, 20), (5120, 200, 17), (16640, 192, 16),
                                    (4096, 12288, 8), (1280, 1000, 11), (4096, 3072, 96)])
 def test_gemm_mfma_q4k_rows_equal_gemv_quant(K, N, M):
-    """The MFMA prefill path (Q4_K, M >= 8): 64-row tiles below M = 384 and
-    128-row tiles from there, masked M and N tails (N not a multiple of the
+    """The MFMA prefill path (Q4_K, M >= 8): 64-row tiles up to M = 64 and
+    128-row tiles beyond, masked M and N tails (N not a multiple of the
     192-column tile, nor of 32), K not a multiple of 1024, several N tiles,
     and the activation prep's three K regimes (<= 4096, <= 16384, beyond).
     Shapes with fewer tiles than CUs split K into 2 to 65 ranges (uneven

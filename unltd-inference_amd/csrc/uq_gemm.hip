@@ -21,7 +21,7 @@
 // workspace (hi/lo planes, group sums, row scales).
 //
 // Tiling: a workgroup of four waves (one per SIMD, one workgroup per CU)
-// computes a TM (M) x 192 (N) tile, TM = 128 from M = 384 and 64 below; wave
+// computes a TM (M) x 192 (N) tile, TM = 128 from M = 65 and 64 below; wave
 // (wm, wn) owns 2 (or 1) x 3 MFMA tiles of 32x32. Rows past M or N read a
 // clamped row and are not stored, so any N works. K runs in 64-k sub-steps
 // through a ring of three LDS stages, each filled only by direct-to-LDS
@@ -637,8 +637,9 @@ hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, 
         }
         return hipSuccess;
     }
-    // 128-row tiles once there are enough of them to cover the CUs
-    const bool big = M >= 384;
+    // 128-row tiles (more MFMA work per operand load) from M > 64; split K
+    // fills the CUs when their count falls short
+    const bool big = M > 64;
     const int N = w.dim_out, ks = gemm_ksplit(M, N, K, big ? 128 : 64);
     const size_t wsb = ws_bytes(M, K), pb = ks > 1 ? (size_t)ks * part_stride(M, N) * 4 : 0;
     uint8_t *base = nullptr;
