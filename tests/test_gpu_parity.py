@@ -343,6 +343,25 @@ def test_gemm_mfma_q4k_dynamic_range():
     _gemm_check(K, N, M, X, seed=99, what="gemm dynamic range")
 
 
+def test_gemm_split_k_is_deterministic():
+    """Small M splits K over workgroups; the partial tiles are summed in range
+    order, so two calls on the same input give the same bits."""
+    K, N, M = 2048, 1000, 24
+    w = S.weights(S.Q4_K, N, K, seed=7)
+    X = S.activations(K, seed=7, rows=M).reshape(M, K)
+    W = uq.Weights(w, S.Q4_K, K, N)
+    dx = uq.DeviceArray.from_numpy(X)
+    outs = []
+    for _ in range(2):
+        dy = uq.DeviceArray(4 * M * N)
+        uq.gemm(W, M, dx, dy)
+        outs.append(dy.download(np.float32, M * N))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = np.zeros(N, np.float32)
+    O.gemv_quant(ref, X[M - 1], w, K, N, S.Q4_K, nthreads=NT)
+    assert_close(outs[0].reshape(M, N)[M - 1], ref, what="split-K gemm last row")
+
+
 def test_gemm_mfma_workspace_regrows_between_calls():
     """Two calls on one stream, the second with a larger M (the workspace
     grows), then a smaller one again."""
