@@ -147,6 +147,11 @@ def test_swiglu_close():
 GEMV_CASES = [
     (S.Q4_K, 256, 7), (S.Q4_K, 4096, 4096), (S.Q4_K, 4096, 33), (S.Q4_K, 12288, 512),
     (S.Q4_K, 1024, 300),
+    # K split over waves, slices streamed through LDS: two and three full
+    # slices, a last slice of one or two blocks, uneven rows per group; 16384
+    # (four slices) runs the register-fed split
+    (S.Q4_K, 8192, 1000), (S.Q4_K, 4352, 77), (S.Q6_K, 4608, 513), (S.Q6_K, 8192, 2000),
+    (S.Q4_K, 16384, 64),
     (S.Q6_K, 256, 5), (S.Q6_K, 4096, 4096), (S.Q6_K, 12288, 512), (S.Q6_K, 2048, 301),
     (S.Q8_0, 4096, 4096), (S.Q8_0, 64, 9), (S.Q8_0, 4064, 33),  # K % 64 == 32: generic kernel
     (S.F32, 4096, 64),
@@ -163,8 +168,20 @@ def test_gemv_quant_parity(dtype, K, N):
     got = np.zeros(N, np.float32)
     uq.gemv_quant(got, x, w, K, N, dtype)
     assert_close(got, ref, what=f"gemv dtype {dtype} K {K} N {N}")
-    if dtype != S.F32 and not (dtype == S.Q8_0 and K % 64):
+    if not _gemv_runs_generic(dtype, K):
         assert_bitwise(got, uq.emu_gemv(x[:K], w, K, N, dtype), "device vs emulation")
+
+
+def _gemv_runs_generic(dtype, K):
+    """True when gemv_quant runs the generic kernel (exact f64 products, not
+    the digit-plane path the emulation models): F32 rows, Q8_0 with
+    K % 64 != 0, and activation layouts beyond 64 KB of LDS (64-task padded
+    planes of 256 bytes per task, Q6_K's 32-byte aux, run scales, group sums)."""
+    if dtype == S.F32 or (dtype == S.Q8_0 and K % 64):
+        return True
+    nt = -(-(K // 64) // 64) * 64  # tasks of 64 activations, rounded to whole waves
+    lds = nt * 256 + (nt * 32 if dtype == S.Q6_K else 0) + (K // 128 + 1) * 4 + (K // 32) * 8
+    return lds > 64 * 1024
 
 
 @pytest.mark.parametrize("dtype,K,N", [(S.Q4_K, 256, 7), (S.Q4_K, 4096, 4096), (S.Q4_K, 12288, 512),

@@ -524,6 +524,115 @@ __global__ __launch_bounds__(64 * KS_NW) __attribute__((amdgpu_waves_per_eu(3)))
     }
 }
 
+// gemv_ks_kernel's split with the weights streamed into LDS (Q4_K / Q6_K,
+// 4096 < K <= 12288): wave w owns slice s = w % KS (blocks [16 s, 16 s + 16))
+// of row group gi = w / KS. Each wave moves its slice of a row into its own
+// ring slot with coalesced direct-to-LDS nontemporal loads (NI per row, D
+// rows in flight), as gemv_stream_kernel does for whole rows, and reads its
+// lane's task from there. Slice sums of a 4-row batch meet in LDS and the
+// slice-0 wave adds them in slice order, as in gemv_ks_kernel.
+template <class F, int NI, int KS, int NG, int D, bool MULTI>
+__global__ __launch_bounds__(64 * KS * NG) void gemv_stream_ks_kernel(const Segs Sg, size_t row_bytes, int K,
+                                                                     const float *__restrict__ x) {
+    static_assert(D == 1 || D == 2 || D == 4, "ring depth divides the 4-row batch");
+    using St = Stage<F>;
+    constexpr int NW = KS * NG;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sl = wv % KS, gi = wv / KS;
+    const int ntask = F::ntasks(K);
+    const int t = 64 * sl + lane;
+    const bool act = t < ntask;
+    const typename F::LC c = F::lane_consts(lane);
+    const int G = blockIdx.x * NG + gi, nG = gridDim.x * NG;  // row group: rows G, G + nG, ...
+    const int N = Sg.start[Sg.n];
+    const int nrows = G < N ? (N - 1 - G) / nG + 1 : 0;
+    const int G0 = blockIdx.x * NG;
+    const int nb = G0 < N ? ((N - 1 - G0) / nG + 1 + 3) >> 2 : 0;  // batches of the workgroup's first group
+    const int nblk = K >> 8;
+    const int nch = (min(nblk, 16 * sl + 16) - 16 * sl) * St::BC;  // 16-byte chunks of this slice
+    // every one of the NI loads of a row has an active lane, so each is issued
+    // and counted; a short last slice instead waits for all its loads
+    const bool full = nch > 64 * (NI - 1);
+    const size_t part_off = (x_lds_bytes<F>(K) + 15) & ~(size_t)15;
+    double *part = (double *)(lds + part_off);  // [2][NG][KS][4]
+    uint8_t *ring = lds + part_off + (size_t)2 * NG * KS * 4 * 8 + (size_t)wv * D * NI * 1024;
+
+    uint32_t goff[NI];
+    bool gval[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) {
+        const int k = lane + 64 * m, b = k / St::BC;
+        gval[m] = k < nch;
+        goff[m] = (uint32_t)((16 * sl + b) * St::BB + 16 * (k - b * St::BC));
+    }
+    auto issue = [&](int i, int slot) {
+        if (i < nrows) {  // wave-uniform
+            const int R = G + i * nG, sg = MULTI ? __builtin_amdgcn_readfirstlane(seg_of(Sg, R)) : 0;
+            const uint8_t *row = Sg.w[sg] + (size_t)(R - Sg.start[sg]) * row_bytes;
+#pragma unroll
+            for (int m = 0; m < NI; m++)
+                if (gval[m]) lds_dma16(row + goff[m], ring + (slot * NI + m) * 1024);
+        }
+    };
+
+    const float4 x_first = prep_x_first(x, K);
+#pragma unroll
+    for (int d = 0; d < D; d++) issue(d, d);
+    const XLayout L = x_layout_at<F>(lds, K);
+    prep_x<F, 64 * NW>(x, K, L, x_first);
+    __syncthreads();
+    if (nb == 0) return;  // the whole workgroup: no rows
+    const XView PV{L.xq, L.aux, L.scale, L.gsum, L.NT};
+    typename F::XS xr;
+    if (act) F::load_x(xr, PV, t, c);
+    const uint8_t *myblk = ring + (lane >> 2) * St::BP;
+
+    for (int b = 0; b < nb; b++) {
+        double g[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            g[r] = 0.0;
+            const int i = 4 * b + r;
+            if (i < nrows) {  // wave-uniform
+                // ops issued after row i's loads: the later rows' loads and,
+                // for the slice-0 wave, the y store of the previous batch
+                const bool store_between = sl == 0 && b > 0 && (D == 4 || (D == 2 ? r <= 1 : r == 0));
+                if (full && i + D - 1 < nrows) {
+                    if (store_between)
+                        wait_vm<(D - 1) * NI + 1>();
+                    else
+                        wait_vm<(D - 1) * NI>();
+                } else {
+                    wait_vm<0>();
+                }
+                typename F::Frag f;
+                if (act) f = St::frag(myblk + (r % D) * NI * 1024, c);
+                // the slot's LDS reads have returned before its next loads land in it
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(i + D, r % D);
+                if (act) g[r] = F::dot(f, xr, c);
+            }
+        }
+        const double P = reduce4_rows(g);
+        double *pb = part + (size_t)(b & 1) * NG * KS * 4;
+        if ((lane & 15) == 0) pb[(gi * KS + sl) * 4 + (lane >> 4)] = P;
+        __syncthreads();
+        if (sl == 0) {
+            double v = 0.0;
+            if (lane < 4) {
+                v = pb[(gi * KS) * 4 + lane];
+                for (int q = 1; q < KS; q++) v += pb[(gi * KS + q) * 4 + lane];
+            }
+            // lane 16r stores row r: move lane r's sum there
+            v = __hiloint2double(__builtin_amdgcn_ds_bpermute(4 * (lane >> 4), __double2hiint(v)),
+                                 __builtin_amdgcn_ds_bpermute(4 * (lane >> 4), __double2loint(v)));
+            store4<MULTI>(Sg, lane, G + 4 * b * nG, nG, nrows - 4 * b, (float)v);
+        }
+    }
+}
+
 // Generic fallback (F32 rows, Q8_0 with K % 64 != 0, K beyond the LDS
 // budget): one wave per row, f32 dequantization (exact: one rounding for
 // Q4_K, none for Q6_K/Q8_0/F32, quants.rs:129-131, :170) and f64
@@ -676,6 +785,39 @@ hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x,
     return hipGetLastError();
 }
 
+#ifndef UQ_STREAM_KS
+#define UQ_STREAM_KS 1
+#endif
+constexpr int kSksNG = 4, kSksD = 2;  // row groups per workgroup, rows in flight per wave
+constexpr size_t kSksLds = 160 * 1024;  // LDS of one workgroup (one per CU)
+
+// gemv_stream_ks_kernel for 4096 < K <= 12288 when its LDS fits; *done
+// reports whether it was launched.
+template <class F, bool MULTI>
+hipError_t launch_stream_ks(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done) {
+    constexpr int NI = (16 * Stage<F>::BC + 63) / 64;
+    const int ks = (F::ntasks(K) + 63) / 64;
+    *done = false;
+    auto go = [&](auto kern, int KSv) -> hipError_t {
+        const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)2 * kSksNG * KSv * 4 * 8 +
+                         (size_t)KSv * kSksNG * kSksD * NI * 1024;
+        if (l > kSksLds) return hipSuccess;
+        const void *k = (const void *)kern;
+        hipError_t e = allow_lds(k, l);
+        if (e != hipSuccess) return e;
+        const int N = S.start[S.n];
+        // one workgroup per CU, kSksNG row groups each, rows dealt round-robin to the groups
+        const int rpg = (N + num_cus() * kSksNG - 1) / (num_cus() * kSksNG);
+        const int grid = (N + rpg * kSksNG - 1) / (rpg * kSksNG);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * KSv * kSksNG), l, s, S, row_bytes, K, x);
+        *done = true;
+        return hipGetLastError();
+    };
+    if (ks == 2) return go(gemv_stream_ks_kernel<F, NI, 2, kSksNG, kSksD, MULTI>, 2);
+    if (ks == 3) return go(gemv_stream_ks_kernel<F, NI, 3, kSksNG, kSksD, MULTI>, 3);
+    return hipSuccess;
+}
+
 template <class F, bool PAIR, bool MULTI>
 hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
@@ -696,6 +838,13 @@ hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x,
         hipLaunchKernelGGL((gemv_kernel<F, PAIR, true, D, NW, MULTI>), dim3(resident_grid(k, lds, N, NW)),
                            dim3(64 * NW), lds, s, S, row_bytes, K, x);
     } else if constexpr (!PAIR) {
+        if constexpr (std::is_same<F, Q6K>::value || std::is_same<F, Q4K>::value) {
+            if (UQ_STREAM_KS && F::ntasks(K) <= 192) {
+                bool done = false;
+                const hipError_t e = launch_stream_ks<F, MULTI>(S, row_bytes, K, x, s, &done);
+                if (e != hipSuccess || done) return e;
+            }
+        }
         const int ks = kslices<F>(K);
         const size_t lds_ks = ks_lds_bytes<F>(K);
         if (ks) {
