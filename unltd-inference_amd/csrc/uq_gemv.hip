@@ -788,7 +788,13 @@ hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x,
 #ifndef UQ_STREAM_KS
 #define UQ_STREAM_KS 1
 #endif
-constexpr int kSksNG = 4, kSksD = 2;  // row groups per workgroup, rows in flight per wave
+#ifndef UQ_SKS_NG
+#define UQ_SKS_NG 4
+#endif
+#ifndef UQ_SKS_D
+#define UQ_SKS_D 2
+#endif
+constexpr int kSksNG = UQ_SKS_NG, kSksD = UQ_SKS_D;  // row groups per workgroup, rows in flight per wave
 constexpr size_t kSksLds = 160 * 1024;  // LDS of one workgroup (one per CU)
 
 // gemv_stream_ks_kernel for 4096 < K <= 12288 when its LDS fits; *done
