@@ -13,6 +13,15 @@
 // activation data is read from LDS once and stays in VGPRs while the next
 // row's weights are prefetched with 128-bit loads. Row sums are reduced
 // across the wave with DPP.
+//
+// Q4_K / Q6_K rows mostly run the streaming forms, in which each wave moves
+// its rows into its own LDS ring with coalesced direct-to-LDS nontemporal
+// loads and its lanes read their tasks from there:
+//   gemv_stream_kernel      K <= 4096 (and the fused gate/up pair)
+//   gemv_stream_ks_kernel   4096 < K <= 12288, rows split into 16-block
+//                           slices over the waves of a workgroup
+//   gemv_q8k_stream_kernel  gemv_quant_q8k, K <= 12288
+//   gemv_q8k_ks_kernel      gemv_quant_q8k, one tensor, 4096 < K <= 12288
 #include <map>
 #include <type_traits>
 #include <mutex>
