@@ -269,9 +269,27 @@ __device__ __forceinline__ void wait_vm() {
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Wave priority for long row loops (PRIO): a SIMD's issue arbiter favours
+// its oldest wave, and on the 152064-row head (three waves per SIMD, ~50
+// rows each) the first wave of each SIMD finished at 77 us, the third at
+// 85 us. A PRIO wave sets its priority to (age + row) mod (waves per SIMD)
+// for each row, so every wave holds the top priority for an equal share of
+// rows. Only launches with many rows per wave use it: the short launches
+// keep the plain instantiation.
+__device__ __forceinline__ void set_prio(int p) {  // p wave-uniform
+    if (p <= 0)
+        __builtin_amdgcn_s_setprio(0);
+    else if (p == 1)
+        __builtin_amdgcn_s_setprio(1);
+    else if (p == 2)
+        __builtin_amdgcn_s_setprio(2);
+    else
+        __builtin_amdgcn_s_setprio(3);
+}
+
 // PAIR: each row unit is a gate row and an up row (2*NI loads, two slots'
 // worth of LDS); MULTI: the row's tensor is looked up in the segment table.
-template <class F, int NI, int NW, int S, bool PAIR, bool MULTI>
+template <class F, int NI, int NW, int S, bool PAIR, bool MULTI, bool PRIO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
 gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
     static_assert(S == 1 || S == 2 || S == 4, "ring depth divides the 4-row batch");
@@ -331,6 +349,7 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
             u[r] = 0.0;
             const int i = rb + r;
             if (i >= nrows) continue;  // wave-uniform
+            if constexpr (PRIO) set_prio(((int)wv / 4 + i) % (NW / 4));
             // ops issued after row i's loads: the later rows' loads, and the
             // one y store of the batch that ended among steps i-S .. i-1
             const bool store_between = i >= S && (S == 4 || (S == 2 ? r <= 1 : r == 0));
@@ -781,6 +800,8 @@ template <> struct Shape<Q6K> { static constexpr int NW = UQ_Q6K_NW, D = UQ_Q6K_
 template <class F> struct StreamShape { static constexpr int NW = UQ_STREAM_Q4K_NW, S = UQ_STREAM_Q4K_S; };
 template <> struct StreamShape<Q6K> { static constexpr int NW = UQ_STREAM_Q6K_NW, S = UQ_STREAM_Q6K_S; };
 
+constexpr int kPrioRows = 16;  // rows per wave from which the PRIO instantiation runs
+
 template <class F, int NI, bool PAIR, bool MULTI>
 hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     constexpr int SNW = PAIR ? UQ_STREAM_PAIR_NW : StreamShape<F>::NW, SS = PAIR ? UQ_STREAM_PAIR_S : StreamShape<F>::S;
@@ -789,8 +810,19 @@ hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x,
     const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>;
     const hipError_t e = allow_lds(k, l);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>), dim3(resident_grid(k, l, N, SNW)),
-                       dim3(64 * SNW), l, s, S, row_bytes, K, x);
+    const int grid = resident_grid(k, l, N, SNW);
+    if constexpr (!PAIR && !MULTI) {
+        if ((N + grid * SNW - 1) / (grid * SNW) >= kPrioRows) {  // rows per wave
+            const void *kp = (const void *)gemv_stream_kernel<F, NI, SNW, SS, false, false, true>;
+            const hipError_t ep = allow_lds(kp, l);
+            if (ep != hipSuccess) return ep;
+            hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS, false, false, true>), dim3(grid), dim3(64 * SNW),
+                               l, s, S, row_bytes, K, x);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>), dim3(grid), dim3(64 * SNW), l, s, S,
+                       row_bytes, K, x);
     return hipGetLastError();
 }
 
