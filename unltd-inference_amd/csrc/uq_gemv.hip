@@ -1159,7 +1159,7 @@ __host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni, in
 // PAIR (T = 1, one segment): a ring unit is gate row r (Sg.w) and up row r
 // (Sg.w2); the wave keeps a record set for each and stores g (Sg.y[0]), u
 // (Sg.y[1]) and h = swiglu(g, u) (Sg.y[2]).
-template <class F, int T, int NW, bool MULTI, bool PAIR = false>
+template <class F, int T, int NW, bool MULTI, bool PAIR = false, bool PRIO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
 gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
     static_assert(!PAIR || (T == 1 && !MULTI), "pairs: one segment, K <= 4096");
@@ -1220,6 +1220,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     bool stored = false;  // the epilogue stores were issued after the current row's loads
     for (int i = 0; i < nrows; i++) {
         const int row = wave + i * nwave;
+        if constexpr (PRIO) set_prio((wv / 4 + i) % (NW / 4));  // as gemv_stream_kernel's PRIO
         if (stored)
             wait_vm<NT == 2 ? 3 : 1>();
         else
@@ -1539,8 +1540,19 @@ hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float
     const void *k = (const void *)gemv_q8k_stream_kernel<F, T, NW, MULTI>;
     const hipError_t e = allow_lds(k, L.total);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, MULTI>), dim3(resident_grid(k, L.total, N, NW)),
-                       dim3(64 * NW), L.total, s, S, row_bytes, K, x);
+    const int grid = resident_grid(k, L.total, N, NW);
+    if constexpr (!MULTI) {
+        if ((N + grid * NW - 1) / (grid * NW) >= kPrioRows) {  // rows per wave
+            const void *kp = (const void *)gemv_q8k_stream_kernel<F, T, NW, false, false, true>;
+            const hipError_t ep = allow_lds(kp, L.total);
+            if (ep != hipSuccess) return ep;
+            hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, false, false, true>), dim3(grid), dim3(64 * NW),
+                               L.total, s, S, row_bytes, K, x);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, MULTI>), dim3(grid), dim3(64 * NW), L.total, s, S,
+                       row_bytes, K, x);
     return hipGetLastError();
 }
 
