@@ -151,7 +151,10 @@ GEMV_CASES = [
     # slices, a last slice of one or two blocks, uneven rows per group; 16384
     # (four slices) runs the register-fed split
     (S.Q4_K, 8192, 1000), (S.Q4_K, 4352, 77), (S.Q6_K, 4608, 513), (S.Q6_K, 8192, 2000),
-    (S.Q4_K, 16384, 64),
+    # four and five slices (K up to 20480, beyond the 64 KB layout budget),
+    # a last slice of 4 blocks (13312)
+    (S.Q4_K, 16384, 64), (S.Q6_K, 16384, 300), (S.Q4_K, 13312, 129), (S.Q4_K, 20480, 200),
+    (S.Q6_K, 20480, 97),
     (S.Q6_K, 256, 5), (S.Q6_K, 4096, 4096), (S.Q6_K, 12288, 512), (S.Q6_K, 2048, 301),
     (S.Q8_0, 4096, 4096), (S.Q8_0, 64, 9), (S.Q8_0, 4064, 33),  # K % 64 == 32: generic kernel
     (S.F32, 4096, 64),
@@ -181,7 +184,16 @@ def _gemv_runs_generic(dtype, K):
         return True
     nt = -(-(K // 64) // 64) * 64  # tasks of 64 activations, rounded to whole waves
     lds = nt * 256 + (nt * 32 if dtype == S.Q6_K else 0) + (K // 128 + 1) * 4 + (K // 32) * 8
-    return lds > 64 * 1024
+    if lds <= 64 * 1024:
+        return False
+    # the streaming split (Q4_K / Q6_K, 2..5 slices) runs within the CU's 160 KB
+    loads = {S.Q4_K: 3, S.Q6_K: 4}.get(dtype, 0)
+    ks = -(-(K // 64) // 64)
+    if not loads or not 2 <= ks <= 5:
+        return True
+    ng, d = (4, 2) if ks <= 3 else (3, 1)
+    sks = (lds + 15) // 16 * 16 + 2 * ng * ks * 4 * 8 + ks * ng * d * loads * 1024
+    return sks > 160 * 1024
 
 
 @pytest.mark.parametrize("dtype,K,N", [(S.Q4_K, 256, 7), (S.Q4_K, 4096, 4096), (S.Q4_K, 12288, 512),
@@ -498,7 +510,8 @@ def test_device_api_errors():
 
 
 @pytest.mark.parametrize("dtype,K,ns", [(S.Q4_K, 4096, (8192, 4096, 32, 32)), (S.Q6_K, 4096, (8192, 1024, 1024)),
-                                        (S.Q4_K, 12288, (4096, 7)), (S.Q8_0, 4096, (100, 4096))])
+                                        (S.Q4_K, 12288, (4096, 7)), (S.Q8_0, 4096, (100, 4096)),
+                                        (S.Q6_K, 16384, (1000, 33))])
 def test_gemv_batch_equals_separate_gemvs(dtype, K, ns):
     """uq_gemv_batch: one launch over several weight tensors sharing x writes
     exactly what separate uq_gemv calls write (same per-row arithmetic), and

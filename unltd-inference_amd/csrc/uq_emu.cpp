@@ -113,14 +113,14 @@ double row_sum64(const double *v) {
 
 // A row is reduced as the kernel that runs it does: lane sums over the
 // lane's tasks, then row_sum64 (gemv_kernel, gemv_kt_kernel); or, when the
-// row runs K-split (kslices), row_sum64 per slice of 64 tasks and the slice
+// row runs K-split (gemv_slices), row_sum64 per slice of 64 tasks and the slice
 // sums added in slice order (gemv_ks_kernel).
 template <class F>
 void emu_gemv(float *y, const float *x, const uint8_t *W, size_t row_bytes, int K, int N) {
     const HostLayout<F> L = prep_layout<F>(x, K);
     const XView PV = L.view();
     const int ntask = F::ntasks(K);
-    const int ks = kslices<F>(K);
+    const int ks = gemv_slices<F>(K);
     for (int row = 0; row < N; row++) {
         const uint8_t *R = W + (size_t)row * row_bytes;
         double part[64];

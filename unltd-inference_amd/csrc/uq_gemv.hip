@@ -18,7 +18,7 @@
 // its rows into its own LDS ring with coalesced direct-to-LDS nontemporal
 // loads and its lanes read their tasks from there:
 //   gemv_stream_kernel      K <= 4096 (and the fused gate/up pair)
-//   gemv_stream_ks_kernel   4096 < K <= 12288, rows split into 16-block
+//   gemv_stream_ks_kernel   4096 < K <= 20480, rows split into 16-block
 //                           slices over the waves of a workgroup
 //   gemv_q8k_stream_kernel  gemv_quant_q8k, K <= 12288
 //   gemv_q8k_ks_kernel      gemv_quant_q8k, one tensor, 4096 < K <= 12288
@@ -553,7 +553,8 @@ __global__ __launch_bounds__(64 * KS_NW) __attribute__((amdgpu_waves_per_eu(3)))
 }
 
 // gemv_ks_kernel's split with the weights streamed into LDS (Q4_K / Q6_K,
-// 4096 < K <= 12288): wave w owns slice s = w % KS (blocks [16 s, 16 s + 16))
+// 4096 < K <= 20480, sks_slices): wave w owns slice s = w % KS (blocks
+// [16 s, 16 s + 16))
 // of row group gi = w / KS. Each wave moves its slice of a row into its own
 // ring slot with coalesced direct-to-LDS nontemporal loads (NI per row, D
 // rows in flight), as gemv_stream_kernel does for whole rows, and reads its
@@ -829,40 +830,36 @@ hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x,
 #ifndef UQ_STREAM_KS
 #define UQ_STREAM_KS 1
 #endif
-#ifndef UQ_SKS_NG
-#define UQ_SKS_NG 4
-#endif
-#ifndef UQ_SKS_D
-#define UQ_SKS_D 2
-#endif
-constexpr int kSksNG = UQ_SKS_NG, kSksD = UQ_SKS_D;  // row groups per workgroup, rows in flight per wave
-constexpr size_t kSksLds = 160 * 1024;  // LDS of one workgroup (one per CU)
-
-// gemv_stream_ks_kernel for 4096 < K <= 12288 when its LDS fits; *done
+// gemv_stream_ks_kernel for the rows that sks_slices splits (K <= 20480):
+// 2-3 slices run 4 row groups with 2 rows in flight, 4-5 slices 3 groups
+// with 1 (sks_shape; the template arguments below follow it). *done
 // reports whether it was launched.
 template <class F, bool MULTI>
 hipError_t launch_stream_ks(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done) {
     constexpr int NI = (16 * Stage<F>::BC + 63) / 64;
-    const int ks = (F::ntasks(K) + 63) / 64;
+    static_assert(NI == F::kSksLoads, "1 KB loads per row slice");
+    const int ks = sks_slices<F>(K);
     *done = false;
-    auto go = [&](auto kern, int KSv) -> hipError_t {
-        const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)2 * kSksNG * KSv * 4 * 8 +
-                         (size_t)KSv * kSksNG * kSksD * NI * 1024;
-        if (l > kSksLds) return hipSuccess;
+    if (!ks) return hipSuccess;
+    int ng, d;
+    sks_shape(ks, ng, d);
+    const size_t l = sks_lds<F>(K, ks);
+    auto go = [&](auto kern) -> hipError_t {
         const void *k = (const void *)kern;
         hipError_t e = allow_lds(k, l);
         if (e != hipSuccess) return e;
         const int N = S.start[S.n];
-        // one workgroup per CU, kSksNG row groups each, rows dealt round-robin to the groups
-        const int rpg = (N + num_cus() * kSksNG - 1) / (num_cus() * kSksNG);
-        const int grid = (N + rpg * kSksNG - 1) / (rpg * kSksNG);
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * KSv * kSksNG), l, s, S, row_bytes, K, x);
+        // one workgroup per CU, ng row groups each, rows dealt round-robin to the groups
+        const int rpg = (N + num_cus() * ng - 1) / (num_cus() * ng);
+        const int grid = (N + rpg * ng - 1) / (rpg * ng);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * ks * ng), l, s, S, row_bytes, K, x);
         *done = true;
         return hipGetLastError();
     };
-    if (ks == 2) return go(gemv_stream_ks_kernel<F, NI, 2, kSksNG, kSksD, MULTI>, 2);
-    if (ks == 3) return go(gemv_stream_ks_kernel<F, NI, 3, kSksNG, kSksD, MULTI>, 3);
-    return hipSuccess;
+    if (ks == 2) return go(gemv_stream_ks_kernel<F, NI, 2, 4, 2, MULTI>);
+    if (ks == 3) return go(gemv_stream_ks_kernel<F, NI, 3, 4, 2, MULTI>);
+    if (ks == 4) return go(gemv_stream_ks_kernel<F, NI, 4, 3, 1, MULTI>);
+    return go(gemv_stream_ks_kernel<F, NI, 5, 3, 1, MULTI>);
 }
 
 template <class F, bool PAIR, bool MULTI>
@@ -886,7 +883,7 @@ hipError_t launch_fast_m(const Segs &S, size_t row_bytes, int K, const float *x,
                            dim3(64 * NW), lds, s, S, row_bytes, K, x);
     } else if constexpr (!PAIR) {
         if constexpr (std::is_same<F, Q6K>::value || std::is_same<F, Q4K>::value) {
-            if (UQ_STREAM_KS && F::ntasks(K) <= 192) {
+            if (UQ_STREAM_KS && sks_slices<F>(K)) {
                 bool done = false;
                 const hipError_t e = launch_stream_ks<F, MULTI>(S, row_bytes, K, x, s, &done);
                 if (e != hipSuccess || done) return e;
@@ -932,9 +929,11 @@ hipError_t launch_fast(const Segs &S, size_t row_bytes, int K, const float *x, h
 hipError_t launch_segs(uq_dtype dt, int K, size_t row_bytes, const Segs &S, bool pair, const float *x,
                        hipStream_t s) {
     if (S.start[S.n] == 0) return hipSuccess;
-    if (dt == UQ_Q4_K && x_lds_bytes<Q4K>(K) <= kLdsCap)
+    // Q4_K / Q6_K rows beyond the 64 KB layout budget still take the fast
+    // path when the streaming split holds them (K <= 20480)
+    if (dt == UQ_Q4_K && (x_lds_bytes<Q4K>(K) <= kLdsCap || (!pair && UQ_STREAM_KS && sks_slices<Q4K>(K))))
         return pair ? launch_fast<Q4K, true>(S, row_bytes, K, x, s) : launch_fast<Q4K, false>(S, row_bytes, K, x, s);
-    if (dt == UQ_Q6_K && x_lds_bytes<Q6K>(K) <= kLdsCap)
+    if (dt == UQ_Q6_K && (x_lds_bytes<Q6K>(K) <= kLdsCap || (!pair && UQ_STREAM_KS && sks_slices<Q6K>(K))))
         return pair ? launch_fast<Q6K, true>(S, row_bytes, K, x, s) : launch_fast<Q6K, false>(S, row_bytes, K, x, s);
     if (dt == UQ_Q8_0 && K % 64 == 0 && x_lds_bytes<Q80>(K) <= kLdsCap)
         return pair ? launch_fast<Q80, true>(S, row_bytes, K, x, s) : launch_fast<Q80, false>(S, row_bytes, K, x, s);

@@ -139,6 +139,7 @@ struct Q4K {
         uint32_t shA0, shA1, shC0, shC1, shB0, shB1, wA, wB;
     };
     static constexpr bool kAux = false;
+    static constexpr int kSksLoads = 3;  // 1 KB loads per 16-block row slice (0: no streaming split)
     UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
     // element-dword w -> (task, dword within task)
     UQ_HD static void xmap(int w, int &t, int &i) {
@@ -270,6 +271,7 @@ struct Q6K {
         int h, u;
     };
     static constexpr bool kAux = true;
+    static constexpr int kSksLoads = 4;  // 1 KB loads per 16-block row slice (0: no streaming split)
     UQ_HD static int ntasks(int K) { return (K >> 8) * 4; }
     UQ_HD static void xmap(int w, int &t, int &i) {
         const int kb = w >> 6, r = w & 63;
@@ -337,6 +339,7 @@ struct Q80 {
         int unused;
     };
     static constexpr bool kAux = false;
+    static constexpr int kSksLoads = 0;  // 1 KB loads per 16-block row slice (0: no streaming split)
     UQ_HD static int ntasks(int K) { return K >> 6; }
     UQ_HD static void xmap(int w, int &t, int &i) {
         t = w >> 4;
@@ -400,6 +403,35 @@ struct Q80 {
 // the four tasks of a block is the reference's sumi[k] exactly.
 constexpr int kQ4Q8Dw = 20;  // dwords per (block, p)
 constexpr int kQ6Q8Dw = 32;  // dwords per (block, task)
+
+// gemv_stream_ks_kernel (Q4_K / Q6_K): rows of 2..5 slices of 64 tasks (16
+// blocks), NG row groups per workgroup, D rows in flight per wave, each row
+// slice streamed as kSksLoads 1 KB loads. Its LDS is the activation layout,
+// two batches of NG*KS*4 doubles and the rings, within the CU's 160 KB.
+// gemv_slices is the slice count a gemv_quant row of this K is split into,
+// by that kernel or by gemv_ks_kernel (0: not split), for the emulation.
+constexpr size_t kLdsCU = 160 * 1024;
+UQ_HD void sks_shape(int ks, int &ng, int &d) {
+    ng = ks <= 3 ? 4 : 3;
+    d = ks <= 3 ? 2 : 1;
+}
+template <class F>
+UQ_HD size_t sks_lds(int K, int ks) {
+    int ng, d;
+    sks_shape(ks, ng, d);
+    return ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)2 * ng * ks * 4 * sizeof(double) +
+           (size_t)ks * ng * d * F::kSksLoads * 1024;
+}
+template <class F>
+UQ_HD int sks_slices(int K) {
+    const int ks = (F::ntasks(K) + 63) / 64;
+    return F::kSksLoads && ks >= 2 && ks <= 5 && sks_lds<F>(K, ks) <= kLdsCU ? ks : 0;
+}
+template <class F>
+UQ_HD int gemv_slices(int K) {
+    const int s = sks_slices<F>(K);
+    return s ? s : kslices<F>(K);
+}
 
 struct Q4KQ8 {
     struct XS {
