@@ -199,11 +199,13 @@ def _gemv_runs_generic(dtype, K):
 @pytest.mark.parametrize("dtype,K,N", [(S.Q4_K, 256, 7), (S.Q4_K, 4096, 4096), (S.Q4_K, 12288, 512),
                                        (S.Q6_K, 256, 5), (S.Q6_K, 4096, 4096), (S.Q6_K, 12288, 512),
                                        (S.Q4_K, 1024, 301), (S.Q6_K, 2048, 33),
-                                       (S.Q4_K, 8192, 1000), (S.Q6_K, 12288, 5000), (S.Q6_K, 4352, 77)])
+                                       (S.Q4_K, 8192, 1000), (S.Q6_K, 12288, 5000), (S.Q6_K, 4352, 77),
+                                       (S.Q4_K, 16384, 300), (S.Q6_K, 16384, 77), (S.Q4_K, 13312, 100),
+                                       (S.Q6_K, 20480, 50)])
 def test_gemv_quant_q8k_bit_exact(dtype, K, N):
     """Every kernel of the path: rows streamed with one or three tasks per
-    lane, the K-split kernel (two or three slices; a last slice of one block;
-    row groups with uneven or no rows in the last workgroups)."""
+    lane, the K-split kernel (two to five slices; a last slice of one or four
+    blocks; row groups with uneven or no rows in the last workgroups)."""
     log(f"gemv_quant_q8k dtype={dtype} K={K} N={N}")
     w = S.weights(dtype, N, K, seed=K * 17 + N + dtype)
     x = S.activations(K, seed=N * 3 + dtype)

@@ -21,7 +21,7 @@
 //   gemv_stream_ks_kernel   4096 < K <= 20480, rows split into 16-block
 //                           slices over the waves of a workgroup
 //   gemv_q8k_stream_kernel  gemv_quant_q8k, K <= 12288
-//   gemv_q8k_ks_kernel      gemv_quant_q8k, one tensor, 4096 < K <= 12288
+//   gemv_q8k_ks_kernel      gemv_quant_q8k, one tensor, 4096 < K <= 20480
 #include <map>
 #include <type_traits>
 #include <mutex>
@@ -1315,7 +1315,8 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     }
 }
 
-// K-split variant for 4096 < K <= 12288 (one tensor, bit-exact): the
+// K-split variant for 4096 < K <= 20480 (one tensor, bit-exact; 2-5 slices
+// when the layout fits the CU's LDS): the
 // workgroup's waves are KS slices x NG row groups. A wave streams its slice
 // (16 blocks) of its group's rows through its own ring slot and keeps its
 // lane's x record in VGPRs; the slice's block records go to the group's
@@ -1594,6 +1595,8 @@ hipError_t launch_q8k_ks(const Segs &S, size_t row_bytes, int K, const float *x,
     };
     if (ks == 2) return go(gemv_q8k_ks_kernel<F, 2, 6>, 2, 6);
     if (ks == 3) return go(gemv_q8k_ks_kernel<F, 3, 4>, 3, 4);
+    if (ks == 4) return go(gemv_q8k_ks_kernel<F, 4, 3>, 4, 3);
+    if (ks == 5) return go(gemv_q8k_ks_kernel<F, 5, 3>, 5, 3);
     return hipSuccess;
 }
 
@@ -1601,7 +1604,7 @@ template <class F, bool MULTI>
 hipError_t launch_q8k_fast_m(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     const int N = S.start[S.n];
     const Q8KLayout L = q8k_layout<F>(K);
-    if (UQ_Q8K_STREAM && !MULTI && F::ntasks(K) > 64 && F::ntasks(K) <= 192) {
+    if (UQ_Q8K_STREAM && !MULTI && F::ntasks(K) > 64 && F::ntasks(K) <= 320) {
         bool done = false;
         const hipError_t e = launch_q8k_ks<F>(S, row_bytes, K, x, s, &done);
         if (e != hipSuccess || done) return e;
