@@ -1,7 +1,8 @@
 /*
  * oracle.c -- CPU restatement of unltd-inference's quantized linear-layer path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product): see oracle.h.
+ * TEST INFRASTRUCTURE ONLY (the oracle the GPU results are compared with,
+ * never the product): see oracle.h.
  * Each function cites the reference function it restates. Arithmetic follows
  * the reference operation by operation; the build disables FP contraction so
  * that every a*b+c stays two roundings, as in the reference (kernels.rs:9,

@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of unltd-inference's quantized linear-layer path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker the GPU kernels are
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle the GPU kernels are
  * compared against. Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it; the product library (libuq) never links,
  * loads or calls it.

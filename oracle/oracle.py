@@ -1,6 +1,6 @@
 """ctypes wrapper of the CPU oracle (liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: the checker the GPU kernels are compared against.
+TEST INFRASTRUCTURE ONLY: the oracle the GPU kernels are compared against.
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this module. Function names mirror the reference's
 (crates/unltd-tensor/src/quants.rs, kernels.rs); reference panics surface as

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker.
+"""Pins the CPU oracle before the GPU results are compared with it.
 
 Three kinds of evidence, per function:
   * the reference's own known-answer tests, restated with their values
