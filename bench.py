@@ -243,83 +243,97 @@ def decode_layers():
     return layers
 
 
-def bench_decode(hip, steps, warmup, head_w=None, head_h=None):
-    n, nff = 4096, 12288
-    layers = decode_layers()
-    cache = {}
+class DecodeStep:
+    """All quantized linear layers of one decode step of the synthetic hybrid
+    9B, weights device-resident. Every layer reads the token's layer input x
+    (N(0,1), f32); within a layer the projections chain as in the forward:
+    the projections of x (batched), the output projection of the block (its
+    input stands in for the GDN / attention result: the z gate output of a
+    GDN layer, the first 4096 of q for attention), then gate/up with SwiGLU
+    on that output and down on h. Each launch writes its own buffer, so one
+    step leaves every launch's input and output in HBM for checking.
+    Tensors of one shape share their host bytes (seeded once per shape)."""
 
-    def host_bytes(dt, K, N):
+    def __init__(self, head_h=None):
+        n, nff = 4096, 12288
+        self.n, self.nff = n, nff
+        self.host = {}
+        self.layers = []
+        self.total = 0
+        for attn, proj, ffn in decode_layers():
+            L = {"attn": attn, "w": [], "shape": []}
+            for name, dt, K, N in proj + ffn:
+                L["w"].append(uq.Weights(self.bytes_of(dt, K, N), dt, K, N))
+                L["shape"].append((name, dt, K, N))
+                self.total += S.row_bytes(dt, K) * N
+            sizes = ({"a": 8192, "c": 1024, "d": 1024} if attn else {"a": 8192, "b": n, "e": 32, "f": 32})
+            sizes.update({"o": n, "g": nff, "u": nff, "h": nff, "y": n})
+            L["buf"] = {k: uq.DeviceArray(4 * v) for k, v in sizes.items()}
+            L["size"] = sizes
+            self.layers.append(L)
+        # the head's bytes are those of the head workload (seed of config 1)
+        self.head_host = None if head_h is not None else S.weights(S.Q6_K, 152064, n, seed=S.seed_for(1))
+        self.head = head_h if head_h is not None else uq.Weights(self.head_host, uq.DType.Q6K, n, 152064)
+        self.total += S.row_bytes(S.Q6_K, n) * 152064
+        self.x_host = S.activations(n, seed=S.seed_for(4))
+        self.x = uq.DeviceArray.from_numpy(self.x_host)
+        self.logits = uq.DeviceArray(4 * 152064)
+
+    def bytes_of(self, dt, K, N):
         key = (dt, K, N)
-        if key not in cache:
-            cache[key] = S.weights(dt, N, K, seed=S.seed_for(4, len(cache) + 1))
-        return cache[key]
+        if key not in self.host:
+            self.host[key] = S.weights(dt, N, K, seed=S.seed_for(4, len(self.host) + 1))
+        return self.host[key]
 
-    total = 0
-    built = []
-    for attn, proj, ffn in layers:
-        P = []
-        for name, dt, K, N in proj + ffn:
-            b = host_bytes(dt, K, N)
-            P.append(uq.Weights(b, dt, K, N))
-            total += b.size
-        built.append((attn, P))
-    head = head_h if head_h is not None else uq.Weights(S.weights(S.Q6_K, 152064, n, seed=S.seed_for(1)),
-                                                         uq.DType.Q6K, n, 152064)
-    total += S.row_bytes(S.Q6_K, n) * 152064
-    x = uq.DeviceArray.from_numpy(S.activations(n, seed=S.seed_for(4)))
-    bufs = {k: uq.DeviceArray(4 * v) for k, v in
-            (("a", 8192), ("b", 4096), ("c", 1024), ("d", 1024), ("e", 32), ("f", 32), ("o", 4096),
-             ("h", nff), ("logits", 152064))}
+    def chain(self, s, q8k=False):
+        """Issue the step's launches on stream s (gemv_quant semantics, or
+        the reference forward's gemv_quant_q8k for every projection)."""
+        batch, one = (uq.gemv_q8k_batch, uq.gemv_q8k) if q8k else (uq.gemv_batch, uq.gemv)
+        for L in self.layers:
+            B, Wt = L["buf"], L["w"]
+            if L["attn"]:
+                q, k, v, o, g, u, d = Wt
+                batch([q, k, v], self.x, [B["a"], B["c"], B["d"]], s)
+                one(o, B["a"], B["o"], s)
+            else:
+                qkv, z, beta, alpha, o, g, u, d = Wt
+                batch([qkv, z, beta, alpha], self.x, [B["a"], B["b"], B["e"], B["f"]], s)
+                one(o, B["b"], B["o"], s)
+            if q8k:
+                uq.ffn_swiglu_q8k(g, u, d, B["o"], B["g"], B["u"], B["h"], B["y"], s)
+            else:
+                uq.ffn_swiglu(g, u, d, B["o"], B["h"], B["y"], s)
+        one(self.head, self.x, self.logits, s)
+
+    def launches(self):
+        return sum(4 for _ in self.layers) + 1
+
+    def free(self):
+        for L in self.layers:
+            for W in L["w"]:
+                W.free()
+
+
+def bench_decode(hip, steps, warmup, head_h=None):
+    st = DecodeStep(head_h)
     s = hip.stream()
-
-    def chain():
-        # projections that read the same input run as one batched launch
-        for attn, P in built:
-            if attn:
-                q, k, v, o, g, u, d = P
-                uq.gemv_batch([q, k, v], x, [bufs["a"], bufs["c"], bufs["d"]], s)
-                uq.gemv(o, bufs["a"], bufs["o"], s)  # first 4096 of q stand in for the attention output
-            else:
-                qkv, z, beta, alpha, out, g, u, d = P
-                uq.gemv_batch([qkv, z, beta, alpha], x, [bufs["a"], bufs["b"], bufs["e"], bufs["f"]], s)
-                uq.gemv(out, bufs["b"], bufs["o"], s)
-            uq.ffn_swiglu(g, u, d, bufs["o"], bufs["h"], x, s)
-        uq.gemv(head, x, bufs["logits"], s)
-
-    g2, u2 = uq.DeviceArray(4 * nff), uq.DeviceArray(4 * nff)
-
-    def chain_q8k():
-        # the reference forward's semantics: every projection is gemv_quant_q8k
-        for attn, P in built:
-            if attn:
-                q, k, v, o, g, u, d = P
-                uq.gemv_q8k_batch([q, k, v], x, [bufs["a"], bufs["c"], bufs["d"]], s)
-                uq.gemv_q8k(o, bufs["a"], bufs["o"], s)
-            else:
-                qkv, z, beta, alpha, out, g, u, d = P
-                uq.gemv_q8k_batch([qkv, z, beta, alpha], x, [bufs["a"], bufs["b"], bufs["e"], bufs["f"]], s)
-                uq.gemv_q8k(out, bufs["b"], bufs["o"], s)
-            uq.ffn_swiglu_q8k(g, u, d, bufs["o"], g2, u2, bufs["h"], x, s)
-        uq.gemv_q8k(head, x, bufs["logits"], s)
-
-    graph = hip.capture(s, chain)
+    graph = hip.capture(s, lambda: st.chain(s))
     wall, ev = timed(hip, lambda: hip.launch_graph(graph, s), steps, warmup, s)
     t = ev * 1e-3 / steps
-    graph8 = hip.capture(s, chain_q8k)
+    graph8 = hip.capture(s, lambda: st.chain(s, q8k=True))
     _, ev8 = timed(hip, lambda: hip.launch_graph(graph8, s), steps, warmup, s)
     t8 = ev8 * 1e-3 / steps
-    launches = sum(2 + 2 for a, _ in built) + 1
+    total = st.total
     res = {"config": "decode step, synthetic hybrid 9B (32 layers, 24 GDN + 8 attention, FFN 12288, "
                      "Q6_K head 152064), all quantized linear layers in one HIP graph; projections of one input "
-                     "batched (uq_gemv_batch)",
-           "weight_bytes_per_token": total, "launches": launches, "ms_per_token": t * 1e3,
+                     "batched (uq_gemv_batch); every layer reads the N(0,1) layer input",
+           "weight_bytes_per_token": total, "launches": st.launches(), "ms_per_token": t * 1e3,
            "tok_s": 1.0 / t, "gbs": total / t / 1e9, "frac_hbm_peak": total / t / 1e9 / HBM_PEAK_GBS,
            "tok_s_wall": steps / wall,
-           "q8k": {"semantics": "gemv_quant_q8k for every projection (bit-exact with the reference forward)",
+           "q8k": {"semantics": "gemv_quant_q8k for every projection, the reference forward's numerics: every "
+                                "projection bit-exact given its input; h = swiglu within 2 ulp (expf)",
                    "ms_per_token": t8 * 1e3, "tok_s": 1.0 / t8, "gbs": total / t8 / 1e9}}
-    for _, P in built:
-        for W in P:
-            W.free()
+    st.free()
     return res
 
 

@@ -85,3 +85,20 @@ def test_emulated_reference_pins():
         for x, key in ((xp, "dot_x_pattern"), (xa, "dot_x_alt")):
             y = uq.emu_gemv(x, blk, 256, 1, dt)
             assert abs(float(y[0]) - case[key]) < fx["tolerance"], (case["block"], key)
+
+
+@pytest.mark.parametrize("dtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_emulated_gemv_non_finite_activation_gives_nan(dtype, bad):
+    """A NaN or infinite activation makes its run's scale NaN, so every row
+    is NaN; gemv_quant gives NaN (NaN input) or +-inf / NaN (infinite input)
+    for such rows: non-finite either way, never a finite number."""
+    K, N = 1024, 9
+    w = S.weights(dtype, N, K, seed=79)
+    x = S.activations(K, seed=10)
+    x[517] = bad
+    ref = np.zeros(N, np.float32)
+    O.gemv_quant(ref, x, w, K, N, dtype)
+    assert not np.any(np.isfinite(ref))
+    y = uq.emu_gemv(x, w, K, N, dtype)
+    assert np.all(np.isnan(y)), y

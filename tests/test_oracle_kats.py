@@ -619,3 +619,30 @@ def test_swiglu_close_to_f64_formula():
     u = (rng.standard_normal(4096) * 30).astype(np.float32)
     ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
     np.testing.assert_allclose(O.swiglu(g, u), ref, rtol=3e-7, atol=1e-30)
+
+
+@pytest.mark.parametrize("dtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+def test_exact_f64_weights_reproduce_gemv_quant(dtype):
+    """tests/helpers.exact_weights_f64 (used as the reference of the GEMM
+    tests at full size) against the oracle's gemv_quant: the f64 product
+    X @ W.T equals gemv_quant row for row after rounding to f32, except where
+    the two f64 summation orders straddle an f32 rounding boundary (at most
+    1 ulp, and rarely). Also across an adversarial x with huge and tiny
+    entries, and with Q6_K scales over the full int8 range."""
+    from helpers import exact_weights_f64
+    K, N = 1024, 96
+    rng = np.random.default_rng(dtype)
+    bb, be = O.BLOCK_BYTES[dtype], O.BLOCK_ELEMS[dtype]
+    b = rng.integers(0, 256, size=(N * K // be, bb), dtype=np.uint8)  # scales over the full int8 range
+    dpos = {O.Q4_K: (0, 2), O.Q6_K: (208,), O.Q8_0: (0,)}[dtype]
+    for p in dpos:  # finite f16 scales
+        b[:, p:p + 2] = np.abs(rng.normal(0, 2e-3, b.shape[0])).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    w = b.reshape(-1)
+    W = exact_weights_f64(dtype, w, N, K)
+    for x in (rng.standard_normal(K).astype(np.float32),
+              (rng.standard_normal(K) * 10.0 ** rng.uniform(-6, 6, K)).astype(np.float32)):
+        ref = np.zeros(N, np.float32)
+        O.gemv_quant(ref, x, w, K, N, dtype)
+        y = (W @ x.astype(np.float64)).astype(np.float32)
+        ulp = np.abs(y.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+        assert int(ulp.max()) <= 1 and int((ulp > 0).sum()) <= 2, (int(ulp.max()), int((ulp > 0).sum()))

@@ -78,7 +78,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // act as xor 4 and xor 8 once quads and halves are uniform), then
 // v_permlane16_swap pairs rows 0-1 and 2-3. No LDS round trip.
 // Operates on the bit patterns of non-negative floats, which order like
-// unsigned integers (NaN is outside the callers' contract).
+// unsigned integers; NaN patterns (sign cleared) order above infinity.
 __device__ __forceinline__ uint32_t group32_max_bits(uint32_t v) {
     v = max(v, dpp_u<0xB1>(v));
     v = max(v, dpp_u<0x4E>(v));
@@ -170,8 +170,11 @@ __device__ __forceinline__ double reduce4_rows(const double (&v)[4]) {
 // Activation prep into the layout of uq_policies.h (XView): one thread per
 // element-dword w (4 activations); a run of 128 activations is one aligned
 // group of 32 lanes. Error per activation <= s/2 <= max|x_run| * 2^-30.
-// Non-finite activations are outside this path's contract (outputs
-// unspecified).
+// A run holding a NaN or an infinity gets the scale s = NaN (its digits are
+// those of zeros), so every row sum that reads the run is NaN: a non-finite
+// activation is never turned into a finite output. (gemv_quant's f64 sum
+// gives NaN for a NaN activation and, for an infinite one, +-inf or NaN
+// depending on the row's weights; here such rows are NaN.)
 // ---------------------------------------------------------------------------
 struct XLayout {
     uint32_t *xq;
@@ -200,7 +203,11 @@ __device__ __forceinline__ void prep_dword(int w, int nw, float4 f, XLayout L) {
     const bool in = w < nw;
     const uint32_t ab = max(max(__float_as_uint(f.x) & 0x7FFFFFFFu, __float_as_uint(f.y) & 0x7FFFFFFFu),
                             max(__float_as_uint(f.z) & 0x7FFFFFFFu, __float_as_uint(f.w) & 0x7FFFFFFFu));
-    const float am = __uint_as_float(group32_max_bits(ab));
+    const uint32_t amb = group32_max_bits(ab);
+    // a NaN or infinite activation in the run: digits of zeros, scale NaN
+    const bool finite = amb < 0x7F800000u;
+    if (!finite) f = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float am = finite ? __uint_as_float(amb) : 0.0f;
     const int ex = am > 0.0f ? __builtin_amdgcn_frexp_expf(am) : 0;  // am = m * 2^ex, m in [0.5, 1)
     const int X0 = (int)rintf(ldexpf(f.x, 30 - ex)), X1 = (int)rintf(ldexpf(f.y, 30 - ex));
     const int X2 = (int)rintf(ldexpf(f.z, 30 - ex)), X3 = (int)rintf(ldexpf(f.w, 30 - ex));
@@ -212,7 +219,7 @@ __device__ __forceinline__ void prep_dword(int w, int nw, float4 f, XLayout L) {
                             __builtin_amdgcn_perm(b_lo, a_lo, 0x07060302u) ^ 0x80808080u,
                             __builtin_amdgcn_perm(b_hi, a_hi, 0x05040100u) ^ 0x80808080u,
                             __builtin_amdgcn_perm(b_hi, a_hi, 0x07060302u) ^ 0x80808080u};
-    const float s = am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
+    const float s = !finite ? __uint_as_float(0x7FC00000u) : am > 0.0f ? ldexpf(1.0f, ex - 30) : 0.0f;
     int t, i;
     F::xmap(w, t, i);
     if (in) {

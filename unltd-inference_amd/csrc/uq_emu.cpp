@@ -7,6 +7,7 @@
 // arithmetic of the kernels are checked before they run on a GPU; GPU tests
 // then compare the device results with this emulation.
 #include <cmath>
+#include <limits>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -39,11 +40,16 @@ HostLayout<F> prep_layout(const float *x, int K) {
     L.gsum.assign(K / 32, 0.0);
     for (int run = 0; run < nruns; run++) {
         float am = 0.0f;
+        bool finite = true;  // a NaN or infinity in the run: digits of zeros, scale NaN
         for (int w = 32 * run; w < 32 * run + 32 && w < nw; w++)
-            for (int i = 0; i < 4; i++) am = std::fmax(am, std::fabs(x[4 * w + i]));
+            for (int i = 0; i < 4; i++) {
+                finite = finite && std::isfinite(x[4 * w + i]);
+                am = std::fmax(am, std::fabs(x[4 * w + i]));
+            }
+        if (!finite) am = 0.0f;
         int ex = 0;
         if (am > 0.0f) (void)std::frexp(am, &ex);
-        const float s = am > 0.0f ? std::ldexp(1.0f, ex - 30) : 0.0f;
+        const float s = !finite ? std::numeric_limits<float>::quiet_NaN() : am > 0.0f ? std::ldexp(1.0f, ex - 30) : 0.0f;
         L.scale[run] = s;
         double part[32];
         int P[32][kPlanes];

@@ -1,50 +1,51 @@
 // Batched prefill GEMM: Y[m] = W X[m] for m < M, gemv_quant semantics per row
 // (the reference has no batched path; prefill feeds tokens one at a time,
-// greedy.rs:55-65, so each row of Y is judged against gemv_quant of X[m]).
+// greedy.rs:55-65, so each row of Y is judged against gemv_quant of X[m],
+// quants.rs:422-466).
 //
-// Q4_K weights run on the f16 MFMA (v_mfma_f32_32x32x16_f16). The reference
-// weight is w = (d*sc)*q - dmin*m (quants.rs:151); the kernel computes
-//     Y[m][n] = s_m * sum_b ( d_b * P_b[m][n] - sum_{g in b} dmin_b*m_g * Xg[m][g] )
-//     P_b     = sum_{k in block b} (sc_g*q_k) * x'[m][k]            (MFMA, f32)
-// with
-//  * x' = x / s_m, s_m a power of two per row (max|x'| in [512, 1024)),
-//    split into f16 x'_hi + x'_lo (22 significant bits; the products with
-//    the exact integers below are exact in f32);
-//  * sc*q <= 945: an exact f16 integer, built from the nibble with one
-//    packed fma on the 1024+q magic;
-//  * Xg = sum of x' over each 32-element group, f16 hi + lo, and
-//    dmin*m (17 bits) f16 hi + lo, so the min term is two more MFMAs per
-//    block;
-//  * P_b restarts every 256-block and is scaled by d_b into an f32
-//    accumulator; s_m is applied at the store.
-// A small prep kernel converts X once per call into a library-owned device
-// workspace (hi/lo planes, group sums, row scales).
+// Every format runs on the f16 MFMA (v_mfma_f32_32x32x16_f16) with f32
+// accumulation, on operands whose products are exact:
+//  * A (activations): x' = x / s_m, s_m a power of two per row (max|x'| in
+//    [512, 1024)), split into f16 hi + lo (22 significant bits). A small
+//    prep kernel writes both planes once per call, in MFMA fragment order.
+//  * B (weights), dequantized once per workgroup into LDS as f16 integers or
+//    an exact f16 pair:
+//      Q4_K  B = sc*q (<= 945, exact). P_b = sum over block b of x'*B is
+//            scaled by d_b into the accumulator C; the min term
+//            -dmin*m_g*sum_g(x') is two more MFMAs per block (group sums of
+//            x' hi/lo times -dmin*m hi/lo). Two passes per k-step.
+//      Q6_K  B1 = (sc & ~1)*q, B2 = (sc & 1)*q with q = raw-32: both exact
+//            in f16 for every int8 scale (|B1| <= 4096 and even, |B2| <= 32);
+//            P_b scaled by d_b. Four passes per k-step.
+//      Q8_0  B_hi = f16(d*q), B_lo = d*q - B_hi (exact residual): C
+//            accumulates x'_hi*B_hi + x'_lo*B_hi + x'_hi*B_lo over all of K
+//            (the dropped x'_lo*B_lo is below 2^-21 of each product). Three
+//            passes per k-step.
+//    The row scale s_m is applied at the store.
 //
-// Tiling: a workgroup of four waves (one per SIMD, one workgroup per CU)
-// computes a TM (M) x 192 (N) tile, TM = 128 from M = 65 and 64 below; wave
-// (wm, wn) owns 2 (or 1) x 3 MFMA tiles of 32x32. Rows past M or N read a
-// clamped row and are not stored, so any N works. K runs in 64-k sub-steps
-// through a ring of three LDS stages, each filled only by direct-to-LDS
-// loads (global_load_lds_dwordx4) spread over the k-steps before it is
-// needed: the activation planes, the raw weight bytes (header + 32 nibble
-// bytes per row) and, once per block, the group sums. A sub-step waits for
-// its stage with an explicit vmcnt and a plain s_barrier, so the loads of
-// later stages stay in flight; each wave dequantizes its B operands (sc*q)
-// from the raw bytes in registers. Within each aligned group of four k,
-// both operands use the k order (0, 2, 1, 3): the weight unpack then needs
-// no byte shuffle. Workgroups are ordered so that each XCD takes mostly one
-// M tile (its activation planes stay in that XCD's L2).
-//
-// Small M (fewer tiles than CUs) splits K: each tile's 256-k blocks are cut
-// into ks ranges, one workgroup per (tile, range), each writing its partial
-// tile to the workspace; gemm_splitk_reduce then sums the ks partials in
-// range order into Y.
-//
-// Other formats, M < 8, and tensors of 4 GiB or more (32-bit row offsets)
-// run as M decode-GEMV launches.
+// Tiling: a workgroup of eight waves (two per SIMD, one workgroup per CU)
+// computes a TM x TN tile; wave (wm, wn) owns 32 rows and NT 32-column MFMA
+// tiles. K runs in 256-k blocks of four 64-k sub-steps of four 16-k steps.
+//  * Raw weight bytes of each block stream into a two-slot LDS ring with
+//    direct-to-LDS loads (global_load_lds_dwordx4), issued a block ahead.
+//  * During sub-step u the eight waves dequantize sub-step u+1 into the
+//    other slot of a two-slot B ring (one 16-byte MFMA operand per lane and
+//    k-octet): wave w takes quarter w%4 of each column's 64 k, lane l the
+//    columns l + 64(w/4) + 128i.
+//  * Activation fragments come from global memory straight into VGPRs,
+//    four k-steps ahead; the prep wrote them so that each fragment load is
+//    two contiguous 512-byte runs.
+//  * One barrier per sub-step, after the B reads of its third k-step: the
+//    next sub-step's B tile is complete and this one's slot is free.
+// Workgroups are ordered so that each XCD takes mostly one M tile (its
+// activation planes stay in that XCD's L2). When the tiles do not cover the
+// CUs (small M), K is split into ranges, one workgroup per (tile, range),
+// each writing a partial tile; gemm_splitk_reduce sums them in range order.
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <type_traits>
+#include <vector>
 
 #include "uq_internal.h"
 #include "uq_policies.h"
@@ -54,525 +55,640 @@ namespace uq {
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 
-constexpr int GN = 192;            // workgroup tile columns (rows: 64 or 128)
-constexpr int GTPB = 256;          // 4 waves, one per SIMD
-constexpr int SUBK = 64;           // k per staging sub-step (one group pair)
-constexpr int kMinM = 8;           // below this M the GEMV path is used
+constexpr int GTPB = 512;  // eight waves, two per SIMD
 
 // ------------------------------------------------------------ workspace
+// Activation planes in fragment order: the 16 bytes of row m and k-octet o
+// (eight x' values, f16, slots in k order 0,2,1,3,4,6,5,7) sit at
+// (o*M + m)*16, so the 32 rows of one MFMA operand and one octet are 512
+// contiguous bytes. g: per 256-k block and row, the eight group sums of x'
+// as f16 hi (16 bytes) then lo (16 bytes).
 struct GemmWs {
-    _Float16 *ahi, *alo;  // [M][K] x' planes, k order (0,2,1,3) per aligned 4
-    _Float16 *ghi, *glo;  // [M][K/32] group sums of x'
-    float *scale;         // [M] s_m
+    uint8_t *ahi, *alo;
+    uint8_t *g;
+    float *scale;  // [M] s_m
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-size_t ws_bytes(int M, int K) {
-    const size_t a = align256((size_t)M * K * 2), g = align256((size_t)M * (K / 32) * 2);
-    return 2 * a + 2 * g + align256((size_t)M * 4);
-}
+size_t plane_bytes(int M, int K) { return align256((size_t)M * K * 2); }
+size_t gsum_bytes(int M, int K) { return align256((size_t)M * (K / 256) * 32); }
+size_t prep_bytes(int M, int K) { return 2 * plane_bytes(M, K) + gsum_bytes(M, K) + align256((size_t)M * 4); }
+size_t part_stride(int M, int N) { return ((size_t)M * N + 63) & ~(size_t)63; }
 
 GemmWs ws_carve(uint8_t *base, int M, int K) {
-    const size_t a = align256((size_t)M * K * 2), g = align256((size_t)M * (K / 32) * 2);
     GemmWs w;
-    w.ahi = (_Float16 *)base;
-    w.alo = (_Float16 *)(base + a);
-    w.ghi = (_Float16 *)(base + 2 * a);
-    w.glo = (_Float16 *)(base + 2 * a + g);
-    w.scale = (float *)(base + 2 * a + 2 * g);
+    const size_t a = plane_bytes(M, K);
+    w.ahi = base;
+    w.alo = base + a;
+    w.g = base + 2 * a;
+    w.scale = (float *)(base + 2 * a + gsum_bytes(M, K));
     return w;
 }
 
-// One grow-only buffer per (device, stream): calls on one stream are ordered,
-// so they can share it; calls on different streams get different buffers.
-hipError_t ws_get(size_t need, hipStream_t s, uint8_t **out) {
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<uint8_t *, size_t>> cache;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> g(mu);
-    auto &slot = cache[{dev, s}];
-    if (slot.second < need) {
-        if (slot.first) {
-            // the old buffer may still be read by work queued on this stream
-            if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
-            if ((e = hipFree(slot.first)) != hipSuccess) return e;
-            slot = {nullptr, 0};
-        }
-        void *p = nullptr;
-        if ((e = hipMalloc(&p, need)) != hipSuccess) return e;
-        slot = {(uint8_t *)p, need};
-    }
-    *out = slot.first;
-    return hipSuccess;
-}
-
 // ------------------------------------------------------------ prep kernel
-// One workgroup per row: s_m from max|x|, the x' hi/lo planes in the
-// (0,2,1,3) k order, and the group sums (f64 sum of the 32 x', exact to
-// rounding, then hi/lo). NV > 0: the thread's K/1024 float4 of x are loaded
-// once, all before the first is used (K <= 1024 * NV); NV == 0: two passes
-// over x (any K).
+// Four waves per row, four rows per workgroup (1024 threads). Pass 1: max
+// |x| over the row (per wave, then across the row's four waves in LDS); a
+// NaN or an infinity makes the row's scale NaN and its planes zero, so the
+// row's outputs are NaN. Pass 2: x' hi/lo per octet in fragment order and
+// the group sums (f64 over the 32 x' of a group, then hi/lo). Thread i of a
+// row takes octets i, i+256, ...; NV > 0 keeps its NV/2 octets in registers
+// (K <= 1024*NV), NV == 0 reads x again for pass 2.
+constexpr int PREP_TPB = 1024, PREP_ROWS = 4, PREP_TPR = PREP_TPB / PREP_ROWS;
 template <int NV>
-__global__ __launch_bounds__(256) void gemm_prep_kernel(const float *__restrict__ X, int K, GemmWs ws) {
-    __shared__ float red[4];
-    const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
-    const float *x = X + (size_t)m * K;
-    const int nit = (K + 1023) >> 10;  // iterations of 1024 elements (the last may be partial)
+__global__ __launch_bounds__(PREP_TPB) void gemm_prep_kernel(const float *__restrict__ X, int K, int M, GemmWs ws) {
+    __shared__ uint32_t red[PREP_TPB / 64];
+    const int i = threadIdx.x % PREP_TPR, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rl = threadIdx.x / PREP_TPR, m = blockIdx.x * PREP_ROWS + rl;
+    const bool live = m < M;  // uniform per wave (a row's waves are whole waves)
+    const float *x = X + (size_t)min(m, M - 1) * K;
+    const int nocts = K >> 3, nit = (nocts + PREP_TPR - 1) / PREP_TPR;
     float4 v[NV > 0 ? NV : 1];
-    float mx = 0.0f;
+    uint32_t mb = 0;
+    auto absmax = [&](float4 a) {
+        mb = max(mb, max(max(__float_as_uint(a.x) & 0x7FFFFFFFu, __float_as_uint(a.y) & 0x7FFFFFFFu),
+                         max(__float_as_uint(a.z) & 0x7FFFFFFFu, __float_as_uint(a.w) & 0x7FFFFFFFu)));
+    };
     if constexpr (NV > 0) {
 #pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int k = 4 * t + 1024 * i;
-            v[i] = i < nit && k < K ? *(const float4 *)(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < NV / 2; j++) {
+            const int o = i + PREP_TPR * j;
+            const bool in = j < nit && o < nocts;
+            v[2 * j] = in ? *(const float4 *)(x + 8 * o) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[2 * j + 1] = in ? *(const float4 *)(x + 8 * o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int i = 0; i < NV; i++)
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        for (int j = 0; j < NV; j++) absmax(v[j]);
     } else {
-        for (int k = 4 * t; k < K; k += 1024) {
-            const float4 w = *(const float4 *)(x + k);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x), fabsf(w.y)), fmaxf(fabsf(w.z), fabsf(w.w))));
+        for (int o = i; o < nocts; o += PREP_TPR) {
+            absmax(*(const float4 *)(x + 8 * o));
+            absmax(*(const float4 *)(x + 8 * o + 4));
         }
     }
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[t >> 6] = mx;
+    for (int off = 32; off >= 1; off >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
+    if (lane == 0) red[wv] = mb;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    constexpr int WPR = PREP_TPR / 64;  // waves per row
+#pragma unroll
+    for (int q = 0; q < WPR; q++) mb = max(mb, red[rl * WPR + q]);
+    const bool finite = mb < 0x7F800000u;
     int ex = 0;
-    if (mx > 0.0f) (void)frexpf(mx, &ex);
-    const float inv = ldexpf(1.0f, 10 - ex);  // x' = x * 2^(10-ex), max|x'| in [512, 1024)
-    if (t == 0) ws.scale[m] = ldexpf(1.0f, ex - 10);
-    _Float16 *ahi = ws.ahi + (size_t)m * K, *alo = ws.alo + (size_t)m * K;
-    // K/4 float4 per row, 8 per group: each iteration keeps every group in
-    // one aligned set of 8 lanes (K is a multiple of 1024 or the tail is
-    // whole groups of the last iteration).
-    auto convert = [&](int k, float4 w) {
-        const bool in = k < K;
-        const float xs[4] = {w.x * inv, w.z * inv, w.y * inv, w.w * inv};  // slots (0,2,1,3)
-        h4 hi, lo;
+    if (finite && mb) (void)frexpf(__uint_as_float(mb), &ex);
+    const float inv = finite ? ldexpf(1.0f, 10 - ex) : 0.0f;  // x' = x * 2^(10-ex), max|x'| in [512, 1024)
+    if (live && i == 0) ws.scale[m] = finite ? ldexpf(1.0f, ex - 10) : __uint_as_float(0x7FC00000u);
+    auto convert = [&](int o, float4 a, float4 b) {
+        const bool in = live && o < nocts;
+        // slots (0,2,1,3,4,6,5,7): the order in which the weight side unpacks
+        float xs[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
+        h8 hi, lo;
         double gs = 0.0;
-        for (int i = 0; i < 4; i++) {
-            hi[i] = (_Float16)xs[i];
-            lo[i] = (_Float16)(xs[i] - (float)hi[i]);
-            gs += (double)xs[i];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float xv = finite ? xs[e] * inv : 0.0f;
+            hi[e] = (_Float16)xv;
+            lo[e] = (_Float16)(xv - (float)hi[e]);
+            gs += (double)xv;
         }
-        gs += __shfl_xor(gs, 1);
+        gs += __shfl_xor(gs, 1);  // the four octets of a 32-k group are threads 4q..4q+3
         gs += __shfl_xor(gs, 2);
-        gs += __shfl_xor(gs, 4);
         if (in) {
-            *(h4 *)(ahi + k) = hi;
-            *(h4 *)(alo + k) = lo;
-            if ((t & 7) == 0) {
-                const size_t gi = (size_t)m * (K / 32) + k / 32;
+            const size_t at = ((size_t)o * M + m) * 16;
+            *(h8 *)(ws.ahi + at) = hi;
+            *(h8 *)(ws.alo + at) = lo;
+            if ((i & 3) == 0) {
+                const int g = o >> 2, b = g >> 3, gi = g & 7;
+                _Float16 *dst = (_Float16 *)(ws.g + ((size_t)b * M + m) * 32);
                 const _Float16 gh = (_Float16)gs;
-                ws.ghi[gi] = gh;
-                ws.glo[gi] = (_Float16)(gs - (double)gh);
+                dst[gi] = gh;
+                dst[8 + gi] = (_Float16)(gs - (double)gh);
             }
         }
     };
     if constexpr (NV > 0) {
 #pragma unroll
-        for (int i = 0; i < NV; i++)
-            if (i < nit) convert(4 * t + 1024 * i, v[i]);
+        for (int j = 0; j < NV / 2; j++)
+            if (j < nit) convert(i + PREP_TPR * j, v[2 * j], v[2 * j + 1]);
     } else {
-        for (int k = 4 * t; k < nit * 1024; k += 1024)
-            convert(k, k < K ? *(const float4 *)(x + k) : make_float4(0.f, 0.f, 0.f, 0.f));
+        for (int j = 0; j < nit; j++) {
+            const int o = i + PREP_TPR * j;
+            const bool in = o < nocts;
+            const float4 a = in ? *(const float4 *)(x + 8 * o) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 b = in ? *(const float4 *)(x + 8 * o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            convert(o, a, b);
+        }
     }
 }
 
-// ------------------------------------------------------------ GEMM kernel
+// ------------------------------------------------------------ device helpers
 __device__ __forceinline__ f16x mfma(h8 a, h8 b, f16x c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// scale_min_k4 (quants.rs:92-102) of group g from the three scale dwords
-__device__ __forceinline__ void sc_m(uint32_t S0, uint32_t S1, uint32_t S2, int g, uint32_t &sc, uint32_t &m) {
-    if (g < 4) {
-        sc = (S0 >> (8 * g)) & 63;
-        m = (S1 >> (8 * g)) & 63;
-    } else {
-        const int h = 8 * (g - 4);
-        sc = ((S2 >> h) & 0xF) | (((S0 >> (h + 6)) & 3) << 4);
-        m = ((S2 >> (h + 4)) & 0xF) | (((S1 >> (h + 6)) & 3) << 4);
-    }
-}
-
-// LDS of one workgroup: a ring of NSTAGE sub-steps of 64 k, each filled
-// entirely by direct-to-LDS loads:
-//  * A: the activation planes, rows of 64 halves (128 B) unpadded; the
-//    16-byte part p of row r sits at part p ^ ((r >> 1) & 7), which spreads
-//    16 consecutive rows of one MFMA operand read over all banks;
-//  * Bq: the weight bytes, chunk-major: chunk 0 = block header (d, dmin,
-//    scales), chunks 1, 2 = the 32 qs bytes of the sub-step's group pair,
-//    chunk 3 = the header again (keeps every wave at three loads);
-//  * G: the block's group sums, [hi/lo][row][8 groups] (filled on the
-//    block's first sub-step; 4 KB so that every wave makes one load, the
-//    part past 2*TM*16 bytes is never read).
-// Each wave dequantizes its own B operands from Bq (sc*q in f16).
-constexpr int NSTAGE = 3;
-template <int TM>
-struct GemmLds {
-    _Float16 A[NSTAGE][2][TM][SUBK];  // [stage][hi/lo][row][k]
-    u4 Bq[NSTAGE][4][GN];             // [stage][chunk][row]
-    uint8_t G[NSTAGE][4096];          // [stage][hi/lo][row][g] halves
-};
-__device__ __forceinline__ int swz_part(int r, int p) { return p ^ ((r >> 1) & 7); }
-__device__ __forceinline__ int swz(int r, int p) { return 8 * swz_part(r, p); }
-
-// 8 f16 MFMA operand values (sc * nibble) from two qs dwords, slot order
-// (0,2,1,3) per aligned 4: one packed fma on the 1024+q magic per pair.
-// v_bfi_b32: (x & mask) | (y & ~mask) in one instruction, both constants in
-// VGPRs (gfx9 VOP3 takes no literals and one SGPR).
+// v_bfi_b32: (x & mask) | (y & ~mask), constants in VGPRs (a VOP3 takes no
+// literal here)
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
     uint32_t r;
     __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(x), "v"(y));
     return r;
 }
-__device__ __forceinline__ h8 dq8(uint32_t d0, uint32_t d1, int sh, h2 sc2, h2 off2, uint32_t kmask,
-                                  uint32_t kmagic) {
-    h8 o;
-    const uint32_t D[2] = {d0, d1};
-    for (int e = 0; e < 2; e++) {
-        const uint32_t v0 = bfi(kmask, D[e] >> sh, kmagic);        // 1024 + q of k 4e, 4e+2
-        const uint32_t v1 = bfi(kmask, D[e] >> (sh + 8), kmagic);  // k 4e+1, 4e+3
-        // (1024 + q) * sc - 1024 * sc = sc*q, one rounding of an exact f16 integer
-        const h2 r0 = __builtin_elementwise_fma(__builtin_bit_cast(h2, v0), sc2, off2);
-        const h2 r1 = __builtin_elementwise_fma(__builtin_bit_cast(h2, v1), sc2, off2);
-        o[4 * e] = r0[0];
-        o[4 * e + 1] = r0[1];
-        o[4 * e + 2] = r1[0];
-        o[4 * e + 3] = r1[1];
-    }
-    return o;
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 hh(float v) {
+    const _Float16 f = (_Float16)v;
+    return h2{f, f};
 }
 
 // Wait until at most N of this wave's vector-memory operations are
-// outstanding (they complete in issue order) and its LDS reads have
-// returned, then barrier. One asm block, so no fence-implied full wait is
-// added: every stage is written by direct-to-LDS loads only, whose
-// completion is what vmcnt tracks.
+// outstanding (they retire in issue order) and its LDS operations are done,
+// then meet the workgroup. One asm block, so the compiler adds no full wait.
 template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
     static_assert(N >= 0 && N <= 63, "vmcnt immediate");
     __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// No memory operation moves across this point (the vmcnt counts above rely
+// on the issue order of the loads around it).
+__device__ __forceinline__ void fence() { __asm__ volatile("" ::: "memory"); }
 
-// One 16-byte direct-to-LDS load per lane (lane i writes dst + 16 i); a
-// non-template helper, so the builtin is never instantiated inside a
-// lambda of a kernel template.
-__device__ __forceinline__ void dma16(const void *g, uint8_t *dst) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+// Raw buffer resource over nbytes at p (gfx9 descriptor word 3: 0x00020000)
+// and a 16-byte load at voffset (per lane) + soffset (wave-uniform).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ h8 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    const i4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return __builtin_bit_cast(h8, v);
 }
 
-// The B-side constants of one sub-step for one 32-column tile: the four qs
-// dwords of this lane's k range and the f16 scale operands of the pair's
-// two groups.
-struct BConst {
-    uint32_t q[4];
-    h2 sc2[2], off2[2];
+// One 16-byte direct-to-LDS load per lane: lane i writes dst + 16 i (dst
+// wave-uniform, through M0). Written as asm so that the compiler does not
+// treat every later LDS read as waiting on it (it cannot tell the ring
+// slots apart and would wait for all outstanding loads); the kernel orders
+// these loads with its own vmcnt counts and barriers instead.
+// Nothing else in these kernels uses M0 (checked in the generated code), so
+// clobbering it here is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *g, uint8_t *dst) {
+    const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// B operand slot of (k-step t, B tile b, column col, lane half h) in one
+// sub-step's B ring slot: fragment (b, t, col/32) is 1 KB, lane = col%32 + 32h.
+template <int NTILE>
+__device__ __forceinline__ uint8_t *bslot(uint8_t *bt, int b, int t, int col, int h) {
+    return bt + ((((b * 4 + t) * NTILE + (col >> 5)) * 64) + 32 * h + (col & 31)) * 16;
+}
+
+// ------------------------------------------------------------ weight formats
+// Each format: RB raw bytes per row and 256-k block, CPR 16-byte chunks per
+// row and block in the LDS ring (the chunks past RB are never read), NBT B
+// tiles per k-step, the MFMA passes (A plane, B tile), whether P restarts
+// per block and is scaled by d, and the min term.
+//
+// dequant(rc, s, c, bt, col): quarter c (0..3) of column col's sub-step s,
+// from the column's raw bytes rc, into the sub-step's B slot bt.
+
+// Q4_K (quants.rs:116-156): element e of a block is the low (group g even)
+// or high nibble of qs[32*(g/2) + e%32], g = e/32; w = (d*sc_g)*q - dmin*m_g.
+// Sub-step s covers groups 2s (low nibbles) and 2s+1 (high nibbles) of the
+// 32 qs bytes at 16 + 32s; quarter c is bytes 8c..8c+7: its low nibbles are
+// k-octet c of the sub-step, its high nibbles k-octet 4 + c.
+struct GQ4K {
+    static constexpr int RB = 144, CPR = 9, NBT = 1, NPASS = 2;
+    static constexpr bool kBlockScale = true, kMin = true;
+    __device__ static constexpr int pa(int p) { return p; }
+    __device__ static constexpr int pb(int) { return 0; }
+    // scale_min_k4 (quants.rs:92-102): 6-bit sc and m of group g from the
+    // scale dwords S0 = s[0..3], S1 = s[4..7], S2 = s[8..11]
+    __device__ static uint32_t sc_of(uint32_t S0, uint32_t S2, int g) {
+        return g < 4 ? (S0 >> (8 * g)) & 63 : ((S2 >> (8 * (g - 4))) & 0xF) | (((S0 >> (8 * (g - 4) + 6)) & 3) << 4);
+    }
+    __device__ static uint32_t m_of(uint32_t S1, uint32_t S2, int g) {
+        return g < 4 ? (S1 >> (8 * g)) & 63
+                     : ((S2 >> (8 * (g - 4) + 4)) & 0xF) | (((S1 >> (8 * (g - 4) + 6)) & 3) << 4);
+    }
+    template <int NTILE>
+    __device__ static void dequant(const uint8_t *rc, int s, int c, uint8_t *bt, int col) {
+        const u4 h = *(const u4 *)rc;
+        const uint2 q = *(const uint2 *)(rc + 16 + 32 * s + 8 * c);
+        const float sa = (float)sc_of(h.y, h.w, 2 * s), sb = (float)sc_of(h.y, h.w, 2 * s + 1);
+        // a nibble n in bits 0-3 of an f16 with the bits of 1024 reads 1024+n,
+        // in bits 4-7 it reads 1024+16n: sc*n = fma(1024+n, sc, -1024 sc) =
+        // fma(1024+16n, sc/16, -64 sc), every operand and the result exact
+        // f16, one rounding of an exact value
+        const h2 lsc = hh(sa), loff = hh(-1024.0f * sa), hsc = hh(sb * 0.0625f), hoff = hh(-64.0f * sb);
+        const uint32_t lm = 0x000F000Fu, hm = 0x00F000F0u, lmag = 0x64006400u, hmag = 0x64006400u;
+        const uint32_t D[2] = {q.x, q.y};
+        u4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const uint32_t d8 = D[e] >> 8;
+            // bytes (0, 2) then (1, 3): element slots (0,2,1,3) of each 4
+            (&lo.x)[2 * e] = as_u(__builtin_elementwise_fma(as_h2(bfi(lm, D[e], lmag)), lsc, loff));
+            (&lo.x)[2 * e + 1] = as_u(__builtin_elementwise_fma(as_h2(bfi(lm, d8, lmag)), lsc, loff));
+            (&hi.x)[2 * e] = as_u(__builtin_elementwise_fma(as_h2(bfi(hm, D[e], hmag)), hsc, hoff));
+            (&hi.x)[2 * e + 1] = as_u(__builtin_elementwise_fma(as_h2(bfi(hm, d8, hmag)), hsc, hoff));
+        }
+        *(u4 *)bslot<NTILE>(bt, 0, c >> 1, col, c & 1) = lo;
+        *(u4 *)bslot<NTILE>(bt, 0, 2 + (c >> 1), col, c & 1) = hi;
+    }
+    // the block's d (f32) and -dmin*m_g split f16 hi (bm[0..7]) and lo (bm[8..15]);
+    // -dmin*m is exact in f32 (11 + 6 significant bits)
+    __device__ static void block_consts(const uint8_t *rc, uint8_t *bm, float *dv) {
+        const u4 h = *(const u4 *)rc;
+        const float dmin = f16_hi(h.x);
+        h8 bh, bl;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const float v = -(dmin * (float)m_of(h.z, h.w, g));
+            bh[g] = (_Float16)v;
+            bl[g] = (_Float16)(v - (float)bh[g]);
+        }
+        *(h8 *)bm = bh;
+        *(h8 *)(bm + 16) = bl;
+        *dv = f16_lo(h.x);
+    }
 };
 
-// Scheduling hints for one 16-k step: MFMAs alternate with the step's other
-// work (LDS reads, VALU, direct-to-LDS loads), so the matrix core is fed
-// while the wave issues the rest. Masks: 0x008 MFMA, 0x100 LDS read,
-// 0x002 VALU, 0x020 VMEM read.
-template <int NM>
-__device__ __forceinline__ void sched_step() {
+// Q6_K (quants.rs:171-200): element e has ql byte 64*(e/128) + e%64 (high
+// nibble if (e/64)%2), hi2 = bits 2*((e%128)/32) of qh[32*(e/128) + e%32],
+// q = (nibble | hi2 << 4) - 32, int8 scale sc[e/16]; w = d*(sc*q). Sub-step
+// s is elements 64s..64s+63; quarter c (16 elements, one scale) is k-step c.
+// Raw rows are 224 bytes per block in LDS (14 chunks; the last 14 bytes
+// belong to the next block or to the tensor padding and are not read).
+struct GQ6K {
+    static constexpr int RB = 210, CPR = 14, NBT = 2, NPASS = 4;
+    static constexpr bool kBlockScale = true, kMin = false;
+    __device__ static constexpr int pa(int p) { return p & 1; }
+    __device__ static constexpr int pb(int p) { return p >> 1; }
+    template <int NTILE>
+    __device__ static void dequant(const uint8_t *rc, int s, int c, uint8_t *bt, int col) {
+        const int hb = s >> 1, j = s & 1, shift = 2 * (2 * j + (c >> 1));
+        const u4 ql = *(const u4 *)(rc + 64 * hb + 16 * c);
+        const u4 qh = *(const u4 *)(rc + 128 + 32 * hb + 16 * (c & 1));
+        const int sc = (int)*(const int8_t *)(rc + 192 + 4 * s + c);
+        const h2 se = hh((float)(sc & ~1)), so = hh((float)(sc & 1)), off = hh(-1056.0f);
+        const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+        u4 b1[2], b2[2];  // [lane half]
 #pragma unroll
-    for (int k = 0; k < NM; k++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (k < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        if (k >= 4 && k < 7) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t A = (&ql.x)[i], C = (&qh.x)[i];
+            const uint32_t raw = (j ? (A >> 4) & 0x0F0F0F0Fu : A & 0x0F0F0F0Fu) | (((C >> shift) & 0x03030303u) << 4);
+            // 1024 + raw, exact; q = raw - 32 exact; q * (sc & ~1) even and
+            // |.| <= 4096, q * (sc & 1) in [-32, 31]: both exact f16
+            const h2 q0 = as_h2(bfi(bm, raw, mag)) + off, q1 = as_h2(bfi(bm, raw >> 8, mag)) + off;
+            (&b1[i >> 1].x)[2 * (i & 1)] = as_u(q0 * se);
+            (&b1[i >> 1].x)[2 * (i & 1) + 1] = as_u(q1 * se);
+            (&b2[i >> 1].x)[2 * (i & 1)] = as_u(q0 * so);
+            (&b2[i >> 1].x)[2 * (i & 1) + 1] = as_u(q1 * so);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *(u4 *)bslot<NTILE>(bt, 0, c, col, h) = b1[h];
+            *(u4 *)bslot<NTILE>(bt, 1, c, col, h) = b2[h];
+        }
     }
-}
+    __device__ static void block_consts(const uint8_t *rc, uint8_t *, float *dv) {
+        *dv = f16_lo(*(const uint16_t *)(rc + 208));
+    }
+};
 
-// A workgroup of four waves (one per SIMD) computes a TM x 192 tile; wave
-// (wm, wn) owns rows 32*WMT*wm + 32i (i < WMT) and columns 96*wn + 32j
-// (j < 3). One loop iteration is one 256-k block: 4 sub-steps of 64 k,
-// each 4 k-steps of 16, all unrolled, with no branch inside:
-//  * the operands of k-step t+1 (LDS reads, B dequantization) are formed
-//    while the MFMAs of step t run;
-//  * at k-step 2 of sub-step u the wave reads the operands of (u, 3), then
-//    waits for stage u+1 and meets the others at the barrier; stage u+3
-//    then goes into stage u's slot (every wave has read it), its loads
-//    spread over the next four k-steps;
-//  * past the last sub-step the loads re-read the last one into a free
-//    slot and the reads of it are discarded, so counts stay static.
-template <int WMT>
-__global__ __launch_bounds__(GTPB, 1) void gemm_q4k_kernel(const uint8_t *__restrict__ W, size_t row_bytes, int K,
-                                                           int N, int M, GemmWs ws, int ntn, int ks,
-                                                           float *__restrict__ Y, float *__restrict__ Ypart,
-                                                           size_t part_stride) {
-    constexpr int TM = 64 * WMT;
-    constexpr int NA = TM / 16;  // A loads per wave per stage (1 KB each)
-    constexpr int NAP = NA / 4;  // ... per k-step
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    GemmLds<TM> &S = *(GemmLds<TM> *)lds_raw;
+// Q8_0 (GGUF block_q8_0: f16 d, int8 q[32]; w = d*q). A 256-k block is
+// eight Q8_0 blocks (272 bytes per row, 17 chunks). Sub-step s is blocks
+// 2s, 2s+1; quarter c is block 2s + c/2, elements 16(c%2)..+15 (k-step c).
+// The q bytes sit at 2 (mod 4) for even blocks: they are read as aligned
+// dwords and realigned with v_alignbyte.
+struct GQ80 {
+    static constexpr int RB = 272, CPR = 17, NBT = 2, NPASS = 3;
+    static constexpr bool kBlockScale = false, kMin = false;  // P added to C unscaled
+    __device__ static constexpr int pa(int p) { return p == 1 ? 1 : 0; }
+    __device__ static constexpr int pb(int p) { return p == 2 ? 1 : 0; }
+    template <int NTILE>
+    __device__ static void dequant(const uint8_t *rc, int s, int c, uint8_t *bt, int col) {
+        const int bi = 2 * s + (c >> 1);
+        const uint8_t *blk = rc + 34 * bi;
+        const _Float16 df = __builtin_bit_cast(_Float16, *(const uint16_t *)blk);
+        const h2 d2 = h2{df, df}, off = hh(-1152.0f);
+        uint32_t w[4];
+        const uint8_t *q = blk + 2 + 16 * (c & 1);
+        if (c & 2) {  // odd block: q at 0 (mod 4); wave-uniform (c is the wave)
+            const uint32_t *p = (const uint32_t *)q;
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = p[i];
+        } else {
+            const uint32_t *p = (const uint32_t *)(q - 2);
+            uint32_t r[5];
+#pragma unroll
+            for (int i = 0; i < 5; i++) r[i] = p[i];
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);
+        }
+        const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+        u4 bh[2], bl[2];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t u = w[i] ^ 0x80808080u;  // bytes q + 128
+            const h2 q0 = as_h2(bfi(bm, u, mag)) + off, q1 = as_h2(bfi(bm, u >> 8, mag)) + off;  // exact q
+            const h2 h0 = q0 * d2, h1 = q1 * d2;  // f16(d*q)
+            // d*q - f16(d*q): at most 8 significant bits, exact in f16
+            const h2 l0 = __builtin_elementwise_fma(q0, d2, -h0), l1 = __builtin_elementwise_fma(q1, d2, -h1);
+            (&bh[i >> 1].x)[2 * (i & 1)] = as_u(h0);
+            (&bh[i >> 1].x)[2 * (i & 1) + 1] = as_u(h1);
+            (&bl[i >> 1].x)[2 * (i & 1)] = as_u(l0);
+            (&bl[i >> 1].x)[2 * (i & 1) + 1] = as_u(l1);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *(u4 *)bslot<NTILE>(bt, 0, c, col, h) = bh[h];
+            *(u4 *)bslot<NTILE>(bt, 1, c, col, h) = bl[h];
+        }
+    }
+    __device__ static void block_consts(const uint8_t *, uint8_t *, float *) {}
+};
+
+template <class BP, int NTILE>
+struct GemmLayout {
+    static constexpr int TN = 32 * NTILE;
+    static constexpr int CHUNKS = TN * BP::CPR;                    // 16-byte chunks per block
+    static constexpr int RAWR = (CHUNKS + GTPB - 1) / GTPB;        // direct-to-LDS rounds per block
+    static constexpr int RAWSLOT = CHUNKS * 16;
+    static constexpr int BTSLOT = BP::NBT * 4 * NTILE * 1024;
+    static constexpr int BMSLOT = BP::kMin ? TN * 32 : 0;
+    static constexpr int DVSLOT = BP::kBlockScale ? TN * 4 : 0;
+    static constexpr int RAW = 0, BT = 2 * RAWSLOT, BM = BT + 2 * BTSLOT, DV = BM + 2 * BMSLOT;
+    static constexpr int BYTES = DV + 2 * DVSLOT;
+    // dequant tasks per wave and sub-step: columns lane + 64(w/4) + 128 i
+    static constexpr int NDQ = (TN + 127) / 128;
+};
+
+// The k-step of a block at which raw-load round r (of RAWR) of the block two
+// ahead is issued: rounds spread over k-steps 11..15 (the ring slot they
+// fill is free from the barrier of k-step 10 on).
+__device__ constexpr int raw_step(int r, int R) { return 11 + (r * 5) / R; }
+
+// ------------------------------------------------------------ GEMM kernel
+template <class BP, int WM, int WN, int NT, bool C64, int D>
+__global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(
+    const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ntn, int ks,
+    float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
+    static_assert(WM * WN == GTPB / 64, "one wave per (wm, wn)");
+    constexpr int TM = 32 * WM, NTILE = NT * WN;
+    using Lay = GemmLayout<BP, NTILE>;
+    constexpr int TN = Lay::TN, RAWR = Lay::RAWR, NDQ = Lay::NDQ;
+    static_assert(16 % D == 0, "D: activation fragments in flight, in k-steps, divides 16");
+    extern __shared__ __align__(16) uint8_t lds[];
     const int t = threadIdx.x, lane = t & 63;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+
     // Tile order: workgroups are dealt round-robin to the 8 XCDs (id % 8).
-    // XCD x takes a contiguous run of the M-major tile list, i.e. mostly one
-    // M tile, so that tile's activation planes stay in the XCD's L2 while
-    // its N tiles stream the weights.
-    // With ks > 1 the K blocks are split into ks ranges: the list is
-    // (M tile, K range, N tile), and each workgroup writes its range's
-    // partial tile to Ypart[kidx] for gemm_splitk_reduce.
+    // XCD x takes a contiguous run of the (M tile, K range, N tile) list, so
+    // mostly one M tile's activation planes per XCD L2.
     const int ntm = (M + TM - 1) / TM, T = ntm * ntn * ks, per = (T + 7) / 8;
     const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if ((blockIdx.x >> 3) >= per || L >= T) return;  // padding of the last round
     const int nt = L % ntn, mk = L / ntn, mt = mk / ks, kidx = mk % ks;
-    const int m0 = mt * TM, n0 = nt * GN;
-    const int wm = wv >> 1, wn = wv & 1;
-    const int lr = lane & 31, lh = lane >> 5;
-    const int nbt = K / 256, kb0 = kidx * nbt / ks;
-    const int nblk = (kidx + 1) * nbt / ks - kb0, KG = K / 32, nsub = 4 * nblk;
-    W += (size_t)kb0 * BQ4K;  // the range's first block: the row strides stay those of K
+    const int m0 = mt * TM, n0 = nt * TN;
+    const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
     float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
 
-    // Per-lane source offsets of the loads; only the uniform stage term
-    // changes per sub-step. Lane i of a 1 KB load fills bytes 1024 J + 16 i
-    // of its region. Rows past M or N read the last valid row (never
-    // stored). A offsets are from ws.ahi (the lo plane follows it in the
-    // workspace); the host keeps the workspace below 4 GiB.
-    const uint32_t lo_off = (uint32_t)((const uint8_t *)ws.alo - (const uint8_t *)ws.ahi);
-    uint32_t aoff[NA], boff[3];
-    bool bq[3];
-#pragma unroll
-    for (int c = 0; c < NA; c++) {
-        const int lin = 1024 * (NA * wv + c) + 16 * lane;
-        const int hl = lin / (TM * 128), row = (lin >> 7) % TM, pp = (lin >> 4) & 7;
-        const int p = swz_part(row, pp);  // the swizzle is an involution
-        const int mr = min(m0 + row, M - 1);
-        aoff[c] = (hl ? lo_off : 0u) + (uint32_t)(((size_t)mr * K + 8 * p) * 2);
-    }
-#pragma unroll
-    for (int c = 0; c < 3; c++) {
-        const int lin = 1024 * (3 * wv + c) + 16 * lane;
-        const int ch = lin / (GN * 16), row = (lin % (GN * 16)) >> 4;
-        const int nr = min(n0 + row, N - 1);
-        bq[c] = ch == 1 || ch == 2;
-        boff[c] = (uint32_t)((size_t)nr * row_bytes + (ch == 1 ? 16 : ch == 2 ? 32 : 0));
-    }
-    const _Float16 *gbase;
-    uint32_t goff;
-    {
-        const int lin = 1024 * wv + 16 * lane, hl = (lin / (TM * 16)) & 1, row = (lin >> 4) % TM;
-        gbase = (hl ? ws.glo : ws.ghi) + 8 * kb0;
-        goff = (uint32_t)((size_t)min(m0 + row, M - 1) * KG * 2);
-    }
-    const uint8_t *abase = (const uint8_t *)ws.ahi + (size_t)kb0 * 512;
-    // Part p (0..3) of stage v's loads: A loads [p*NAP, (p+1)*NAP), then B
-    // load p (p < 3) or the G load (p == 3, when the stage starts a block:
-    // G_STAGE). Stages past the end re-read the last sub-step.
-    auto issue_part = [&](int v, int p, bool g_stage) {
-        const int vs = min(v, nsub - 1), st = v % NSTAGE, kb = vs >> 2, ss = vs & 3;
-#pragma unroll
-        for (int c = p * NAP; c < (p + 1) * NAP; c++)
-            dma16(abase + (size_t)vs * (SUBK * 2) + aoff[c], (uint8_t *)&S.A[st][0][0][0] + 1024 * (NA * wv + c));
-        if (p < 3)
-            dma16(W + (size_t)kb * BQ4K + boff[p] + (bq[p] ? 32 * ss : 0), (uint8_t *)&S.Bq[st][0][0] + 1024 * (3 * wv + p));
-        else if (g_stage)
-            dma16((const uint8_t *)gbase + (size_t)kb * 16 + goff, &S.G[st][0] + 1024 * wv);
-    };
-    const uint32_t kmask = 0x000F000Fu, kmagic = 0x64006400u;
+    const int wm = wv / WN, wn = wv % WN, lr = lane & 31, lh = lane >> 5;
 
-    // B-side constants of one sub-step (group pair ss of the block): per
-    // column tile the four qs dwords of this lane's k range (bytes
-    // [8 lh, +8) and [16 + 8 lh, +8) of the pair) and the f16 scale
-    // operands of the pair's two groups.
-    BConst bc[3];
-    auto load_consts = [&](int u, int ss) {
-        const uint8_t *st = (const uint8_t *)&S.Bq[u % NSTAGE][0][0];
+    // raw-weight loads: chunk GTPB*r + t of a block's ring slot is 16 bytes
+    // of column (chunk / CPR); lanes past the last chunk load nothing
+    uint32_t roff[RAWR];
 #pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const int col = 96 * wn + 32 * j + lr;
-            const u4 h = *(const u4 *)(st + 16 * col);
-            const uint2 a = *(const uint2 *)(st + GN * 16 + 16 * col + 8 * lh);
-            const uint2 b = *(const uint2 *)(st + 2 * GN * 16 + 16 * col + 8 * lh);
-            bc[j].q[0] = a.x;
-            bc[j].q[1] = a.y;
-            bc[j].q[2] = b.x;
-            bc[j].q[3] = b.y;
-#pragma unroll
-            for (int sh2 = 0; sh2 < 2; sh2++) {
-                uint32_t sc, mm;
-                sc_m(h.y, h.z, h.w, 2 * ss + sh2, sc, mm);
-                const _Float16 scf = (_Float16)(float)sc, off = (_Float16)(-1024.0f * (float)sc);
-                bc[j].sc2[sh2] = h2{scf, scf};
-                bc[j].off2[sh2] = h2{off, off};
+    for (int r = 0; r < RAWR; r++) {
+        const int c = GTPB * r + t, col = min(c / BP::CPR, TN - 1), part = c % BP::CPR;
+        roff[r] = (uint32_t)min(n0 + col, N - 1) * row_bytes + 16u * (uint32_t)part;
+    }
+    const uint8_t *wbase = W + (size_t)kb0 * BP::RB;
+    auto raw_load = [&](int b, int r) {  // round r of block b (clamped to the range)
+        const int bb = min(b, nblk - 1);
+        if (GTPB * r + t < Lay::CHUNKS)
+            dma16(wbase + (size_t)bb * BP::RB + roff[r],
+                  lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + GTPB * 16 * r + 1024 * wv);
+    };
+
+    // activation fragments: row m of this wave's tile, octet 2 kk + lh.
+    // Buffer loads: the lane part of the offset in a VGPR, the k-step part
+    // wave-uniform in an SGPR (the planes are below 2 GiB).
+    const int am = min(m0 + 32 * wm + lr, M - 1);
+    const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
+    const uint32_t pbytes = (uint32_t)((size_t)M * K * 2);
+    const auto rah = buf_rsrc(ws.ahi, pbytes), ral = buf_rsrc(ws.alo, pbytes);
+    const int nks = 16 * nblk;
+    const uint32_t kstep = (uint32_t)M * 32u, abase = (uint32_t)kb0 * 16u * kstep;
+    auto a_load = [&](h8 &hi, h8 &lo, int kk) {
+        const uint32_t so = abase + (uint32_t)min(kk, nks - 1) * kstep;
+        hi = buf_load16(rah, aoff, so);
+        lo = buf_load16(ral, aoff, so);
+    };
+    const auto rg = buf_rsrc(ws.g, (uint32_t)((size_t)M * (K / 256) * 32));  // group sums (Q4_K)
+    const uint32_t goff = (uint32_t)am * 32u + 16u * lh;
+    auto g_load = [&](int b) { return buf_load16(rg, goff, (uint32_t)(kb0 + min(b, nblk - 1)) * (uint32_t)M * 32u); };
+
+    // dequant role: quarter wv%4 of columns lane + 64(wv/4) + 128 i
+    const int dq_c = wv & 3, dq_col0 = lane + 64 * (wv >> 2);
+    auto dequant = [&](int v, int i) {  // task i of sub-step v
+        const int col = dq_col0 + 128 * i;
+        if (col < TN) {
+            const uint8_t *rc = lds + Lay::RAW + ((v >> 2) & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
+            BP::template dequant<NTILE>(rc, v & 3, dq_c, lds + Lay::BT + (v & 1) * Lay::BTSLOT, col);
+        }
+    };
+    auto block_pass = [&](int b) {  // per-column constants of block b, one column per thread
+        if constexpr (BP::kBlockScale || BP::kMin) {
+            if (t < TN) {
+                const uint8_t *rc = lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + t * (16 * BP::CPR);
+                BP::block_consts(rc, lds + Lay::BM + (b & 1) * Lay::BMSLOT + t * 32,
+                                 (float *)(lds + Lay::DV + (b & 1) * Lay::DVSLOT) + t);
             }
         }
     };
-    // block epilogue inputs, formed when the block's last sub-step has
-    // landed: B = -dmin*m_g (hi, lo) and d per column tile, A = this lane's
-    // group sums (hi for lh 0, lo for lh 1) per row tile
-    h8 ebh[3], ebl[3], eg[WMT];
-    float ed[3];
-    auto load_epilogue = [&](int u) {
-        const int st = u % NSTAGE, gst = (u - 3) % NSTAGE;  // G arrived with the block's first sub-step
-#pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const u4 h = S.Bq[st][0][96 * wn + 32 * j + lr];
-            const float dmin = f16_hi(h.x);
-#pragma unroll
-            for (int g = 0; g < 8; g++) {
-                uint32_t sc, mm;
-                sc_m(h.y, h.z, h.w, g, sc, mm);
-                const float bm = -(dmin * (float)mm);  // exact in f32
-                ebh[j][g] = (_Float16)bm;
-                ebl[j][g] = (_Float16)(bm - (float)ebh[j][g]);
-            }
-            ed[j] = f16_lo(h.x);
-        }
-#pragma unroll
-        for (int i = 0; i < WMT; i++)
-            eg[i] = *(const h8 *)&S.G[gst][(lh * TM + 32 * WMT * wm + 32 * i + lr) * 16];
-    };
-    struct Ops {
-        h8 ah[WMT], al[WMT], b[3];
-    };
-    // operands of k-step s (16 k) of sub-step u: s 0, 1 are the low nibbles
-    // of group 2ss (qs bytes 0-15 / 16-31), s 2, 3 the high nibbles (group
-    // 2ss+1)
-    auto load_ops = [&](Ops &o, int u, int s) {
-        const int st = u % NSTAGE, p = 2 * s + lh, sh2 = s >> 1, half = s & 1;
-#pragma unroll
-        for (int i = 0; i < WMT; i++) {
-            const int row = 32 * WMT * wm + 32 * i + lr;
-            o.ah[i] = *(const h8 *)&S.A[st][0][row][swz(row, p)];
-            o.al[i] = *(const h8 *)&S.A[st][1][row][swz(row, p)];
-        }
-#pragma unroll
-        for (int j = 0; j < 3; j++)
-            o.b[j] = dq8(bc[j].q[2 * half], bc[j].q[2 * half + 1], 4 * sh2, bc[j].sc2[sh2], bc[j].off2[sh2], kmask,
-                         kmagic);
-    };
 
-    f16x P[WMT][3], C[WMT][3];
+    // P: this block's MFMA accumulator (f32), at most 16 k-steps long (the
+    // matrix cores' f32 accumulation is coarser than sequential f32
+    // rounding, so long sums are split). C: the sum over blocks, in f64
+    // (C64) or, where registers are short (128 x 192 Q4_K tiles), f32.
+    // Cm: the Q4_K min term on the MFMA (C itself when C is f32).
+    using CT = typename std::conditional<C64, double, float>::type;
+    f16x P[NT], Cm[NT];
+    CT C[NT][16];
     const f16x zero = {};
 #pragma unroll
-    for (int i = 0; i < WMT; i++)
+    for (int j = 0; j < NT; j++) {
+        Cm[j] = zero;
 #pragma unroll
-        for (int j = 0; j < 3; j++) C[i][j] = zero;
+        for (int r = 0; r < 16; r++) C[j][r] = 0;
+    }
+    h8 ah[D], al[D];
+    h8 gmin;  // this lane's group sums of the current block (Q4_K)
+    h8 bcur[BP::NBT][NT], bnxt[BP::NBT][NT];
+    auto b_read = [&](h8 (&dst)[BP::NBT][NT], int v, int tt) {
+        const uint8_t *bt = lds + Lay::BT + (v & 1) * Lay::BTSLOT;
+#pragma unroll
+        for (int b = 0; b < BP::NBT; b++)
+#pragma unroll
+            for (int j = 0; j < NT; j++)
+                dst[b][j] = *(const h8 *)(bt + ((((b * 4 + tt) * NTILE + wn * NT + j) * 64) + lane) * 16);
+    };
 
-    // prologue: stages 0, 1 and half of 2 in flight, stage 0 landed
+    // prologue: raw blocks 0 and 1, the first D activation k-steps and the
+    // first block's group sums; then block 0's constants and sub-step 0
 #pragma unroll
-    for (int p = 0; p < 4; p++) issue_part(0, p, true);
+    for (int r = 0; r < RAWR; r++) raw_load(0, r);
 #pragma unroll
-    for (int p = 0; p < 4; p++) issue_part(1, p, false);
-    wait_vm_barrier<NA + 3>();
-    issue_part(2, 0, false);  // parts 2, 3 of stage 2 follow in k-steps 0, 1
-    issue_part(2, 1, false);
-    load_consts(0, 0);
-    Ops cur, nxt;
-    load_ops(cur, 0, 0);
+    for (int r = 0; r < RAWR; r++) raw_load(1, r);
+    fence();
+#pragma unroll
+    for (int d = 0; d < D; d++) a_load(ah[d], al[d], d);
+    if constexpr (BP::kMin) gmin = g_load(0);
+    fence();
+    // raw block 0 landed: after its last load every wave issued at least
+    // RAWR-1 loads of block 1 (a partial last round is skipped by the waves
+    // it does not reach) and the 2D activation loads (and the group sums)
+    wait_vm_barrier<RAWR - 1 + 2 * D + (BP::kMin ? 1 : 0)>();
+    block_pass(0);
+#pragma unroll
+    for (int i = 0; i < NDQ; i++) dequant(0, i);
+    lds_barrier();
+    b_read(bcur, 0, 0);
+
     for (int kb = 0; kb < nblk; kb++) {
 #pragma unroll
-        for (int ss = 0; ss < 4; ss++) {
-            const int u = 4 * kb + ss;
+        for (int t16 = 0; t16 < 16; t16++) {
+            const int s = t16 >> 2, tt = t16 & 3, u = 4 * kb + s, kk = 16 * kb + t16;
+            // B operands of the next k-step (the next sub-step's after the barrier)
+            if (tt < 3) b_read(bnxt, u, tt + 1);
+            else b_read(bnxt, u + 1, 0);
+            // MFMAs of this k-step
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                if (s == 2) {
-                    load_ops(nxt, u, 3);
-                    // stage u+1 landed: only stage u+2's loads may be outstanding
-                    if (((ss + 2) & 3) == 0)
-                        wait_vm_barrier<NA + 4>();
-                    else
-                        wait_vm_barrier<NA + 3>();
-                    load_consts(u + 1, (ss + 1) & 3);
-                    if (ss == 2) load_epilogue(u + 1);
-                } else if (s == 3) {
-                    load_ops(nxt, u + 1, 0);
-                } else {
-                    load_ops(nxt, u, s + 1);
+            for (int p = 0; p < BP::NPASS; p++)
+#pragma unroll
+                for (int j = 0; j < NT; j++) {
+                    const h8 a = BP::pa(p) ? al[t16 % D] : ah[t16 % D];
+                    P[j] = mfma(a, bcur[BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
                 }
-                // part of stage u+3 (issued from k-step 2 of u to k-step 1 of u+1)
-                if (s >= 2)
-                    issue_part(u + 3, s - 2, ((ss + 3) & 3) == 0);
-                else
-                    issue_part(u + 2, s + 2, ((ss + 2) & 3) == 0);
+            if constexpr (BP::kMin) {
+                // the block's min term into C: -sum_g dmin*m_g * sum_g(x')
+                if (t16 == 13) {
+                    const uint8_t *bm = lds + Lay::BM + (kb & 1) * Lay::BMSLOT;
 #pragma unroll
-                for (int i = 0; i < WMT; i++)
+                    for (int j = 0; j < NT; j++) {
+                        const int col = 32 * (wn * NT + j) + lr;
+                        const h8 bh = *(const h8 *)(bm + col * 32), bl = *(const h8 *)(bm + col * 32 + 16);
+                        if constexpr (C64) {
+                            Cm[j] = mfma(gmin, bh, Cm[j]);
+                            Cm[j] = mfma(gmin, bl, Cm[j]);
+                        } else {
+                            f16x c;
 #pragma unroll
-                    for (int j = 0; j < 3; j++) P[i][j] = mfma(cur.ah[i], cur.b[j], ss == 0 && s == 0 ? zero : P[i][j]);
+                            for (int r = 0; r < 16; r++) c[r] = C[j][r];
+                            c = mfma(gmin, bh, c);
+                            c = mfma(gmin, bl, c);
 #pragma unroll
-                for (int i = 0; i < WMT; i++)
-#pragma unroll
-                    for (int j = 0; j < 3; j++) P[i][j] = mfma(cur.al[i], cur.b[j], P[i][j]);
-                // the block's min term into C (its inputs arrived at k-step 10):
-                // the hi MFMAs at k-step 12, the lo ones at 13, off the block's end
-                if (ss == 3 && s < 2)
-#pragma unroll
-                    for (int i = 0; i < WMT; i++)
-#pragma unroll
-                        for (int j = 0; j < 3; j++) C[i][j] = mfma(eg[i], s == 0 ? ebh[j] : ebl[j], C[i][j]);
-                sched_step<6 * WMT>();
-                cur = nxt;
+                            for (int r = 0; r < 16; r++) C[j][r] = c[r];
+                        }
+                    }
+                }
             }
+            // loads: raw rounds of block kb+2, then activations D k-steps ahead
+            // (and the next block's group sums)
+#pragma unroll
+            for (int r = 0; r < RAWR; r++)
+                if (raw_step(r, RAWR) == t16) raw_load(kb + 2, r);
+            a_load(ah[t16 % D], al[t16 % D], kk + D);
+            if constexpr (BP::kMin)
+                if (t16 == 14) gmin = g_load(kb + 1);
+            fence();
+            // dequant of sub-step u+1 in k-steps 0..NDQ-1; block constants of
+            // the next block in k-step 3 of sub-step 3
+#pragma unroll
+            for (int i = 0; i < NDQ; i++)
+                if (i == tt) dequant(u + 1, i);
+            if (tt == 2) {
+                // this sub-step's B reads are done and the next sub-step's B
+                // tile is complete; at sub-step 2 the next block's raw bytes
+                // (issued at k-steps 11-15 of the previous block) have landed:
+                // after them this wave issued at least the 22 activation loads
+                // of k-steps 0-10
+                if (s == 2)
+                    wait_vm_barrier<2 * 11>();
+                else
+                    lds_barrier();
+            }
+            if (s == 3 && tt == 3) block_pass(kb + 1);
+#pragma unroll
+            for (int b = 0; b < BP::NBT; b++)
+#pragma unroll
+                for (int j = 0; j < NT; j++) bcur[b][j] = bnxt[b][j];
         }
-        // end of the block: C += d * P
+        // end of the block: C += d * P (d*P is exact in f64)
+        if constexpr (BP::kBlockScale) {
+            const float *dv = (const float *)(lds + Lay::DV + (kb & 1) * Lay::DVSLOT);
 #pragma unroll
-        for (int i = 0; i < WMT; i++)
+            for (int j = 0; j < NT; j++) {
+                const float d = dv[32 * (wn * NT + j) + lr];
 #pragma unroll
-            for (int j = 0; j < 3; j++)
+                for (int r = 0; r < 16; r++) {
+                    if constexpr (C64)
+                        C[j][r] = fma((double)d, (double)P[j][r], C[j][r]);
+                    else
+                        C[j][r] = fmaf(d, P[j][r], C[j][r]);
+                }
+            }
+        } else {
 #pragma unroll
-                for (int r = 0; r < 16; r++) C[i][j][r] = fmaf(ed[j], P[i][j][r], C[i][j][r]);
+            for (int j = 0; j < NT; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) C[j][r] += (CT)P[j][r];
+        }
     }
-    wait_vm_barrier<0>();  // the loads past the end land before the workgroup leaves
-    // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4.
-    // The row scales are loaded first, unconditionally (clamped rows), so
-    // the loads are issued together rather than one per guarded store.
-    float rs[WMT][16];
+    wait_vm_barrier<0>();  // loads past the end land before the workgroup leaves
+
+    // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4
+    float rs[16];
 #pragma unroll
-    for (int i = 0; i < WMT; i++)
+    for (int r = 0; r < 16; r++) rs[r] = ws.scale[min(m0 + 32 * wm + 8 * (r >> 2) + 4 * lh + (r & 3), M - 1)];
+    f16x Yv[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int m = m0 + 32 * WMT * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-            rs[i][r] = ws.scale[min(m, M - 1)];
+            // y = s * (C + min term), one rounding to f32 (s is a power of two)
+            float v;
+            if constexpr (C64)
+                v = (float)((C[j][r] + (double)Cm[j][r]) * (double)rs[r]);
+            else
+                v = C[j][r] * rs[r];
+            __asm__ volatile("" : "+v"(v));  // formed before the stores
+            Yv[j][r] = v;
         }
-    // scale every output before the first store: stores count in vmcnt too,
-    // so a scale consumed after a store would wait for that store
+    if (m0 + TM <= M && n0 + TN <= N) {
 #pragma unroll
-    for (int i = 0; i < WMT; i++)
+        for (int j = 0; j < NT; j++) {
+            float *y = Yo + (size_t)(m0 + 32 * wm + 4 * lh) * N + n0 + 32 * (wn * NT + j) + lr;
 #pragma unroll
-        for (int j = 0; j < 3; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v = C[i][j][r] * rs[i][r];
-                __asm__ volatile("" : "+v"(v));  // formed here, not sunk next to its store
-                C[i][j][r] = v;
-            }
-    if (m0 + TM <= M && n0 + GN <= N) {  // whole tile in range: stores without guards
-#pragma unroll
-        for (int i = 0; i < WMT; i++)
-#pragma unroll
-            for (int j = 0; j < 3; j++) {
-                float *y = Yo + (size_t)(m0 + 32 * WMT * wm + 32 * i + 4 * lh) * N + n0 + 96 * wn + 32 * j + lr;
-#pragma unroll
-                for (int r = 0; r < 16; r++) y[(size_t)(8 * (r >> 2) + (r & 3)) * N] = C[i][j][r];
-            }
+            for (int r = 0; r < 16; r++) y[(size_t)(8 * (r >> 2) + (r & 3)) * N] = Yv[j][r];
+        }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < WMT; i++)
+    for (int j = 0; j < NT; j++) {
+        const int n = n0 + 32 * (wn * NT + j) + lr;
 #pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const int n = n0 + 96 * wn + 32 * j + lr;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + 32 * WMT * wm + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m < M && n < N) Yo[(size_t)m * N + n] = C[i][j][r];
-            }
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + 32 * wm + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (m < M && n < N) Yo[(size_t)m * N + n] = Yv[j][r];
         }
+    }
 }
 
 // Sum of the ks partial results of a split-K launch, in range order.
@@ -583,6 +699,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restric
         for (int k = 1; k < ks; k++) v += P[(size_t)k * stride + i];
         Y[i] = v;
     }
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ Y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) Y[i] = 0.0f;
 }
 
 int gemm_cus() {
@@ -597,26 +717,39 @@ int gemm_cus() {
     return n;
 }
 
-// K ranges per tile: enough workgroups to cover the CUs when the tiles alone
-// do not (small M), at most one 256-k block per range.
-int gemm_ksplit(int M, int N, int K, int TM) {
-    const int tiles = ((M + TM - 1) / TM) * ((N + GN - 1) / GN);
-    return std::max(1, std::min(K / 256, gemm_cus() / std::max(tiles, 1)));
+// Launch plan of one call: the kernel shape (rows per tile from M, columns
+// per tile from the format) and the K split.
+struct Plan {
+    int wm, tm, tn, ks;
+};
+
+Plan plan_for(uq_dtype dt, int M, int N, int K) {
+    Plan p;
+    // rows per tile: 128 beyond M = 64, else 64, else (Q4_K) 32; columns:
+    // Q4_K 192 (128-row tiles) or 256, Q6_K / Q8_0 128
+    const bool q4 = dt == UQ_Q4_K;
+    p.wm = M > 64 ? 4 : (M > 32 || !q4) ? 2 : 1;
+    p.tm = 32 * p.wm;
+    p.tn = q4 ? (p.wm == 4 ? 192 : 256) : 128;
+    const int tiles = ((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
+    p.ks = std::max(1, std::min(K / 256, gemm_cus() / std::max(tiles, 1)));
+    return p;
 }
 
-size_t part_stride(int M, int N) { return ((size_t)M * N + 63) & ~(size_t)63; }
-
-template <int WMT>
+template <class BP, int WM, int WN, int NT, bool C64, int D>
 hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
-    const int K = w.dim_in, N = w.dim_out, TM = 64 * WMT;
-    const int ntm = (M + TM - 1) / TM, ntn = (N + GN - 1) / GN;
+    constexpr int TM = 32 * WM, TN = 32 * NT * WN;
+    const int K = w.dim_in, N = w.dim_out;
+    const int ntm = (M + TM - 1) / TM, ntn = (N + TN - 1) / TN;
     const int grid = 8 * ((ntm * ntn * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
-    const void *k = (const void *)gemm_q4k_kernel<WMT>;
-    hipError_t e = allow_lds(k, sizeof(GemmLds<64 * WMT>));
+    const void *k = (const void *)gemm_kernel<BP, WM, WN, NT, C64, D>;
+    constexpr int lds = GemmLayout<BP, NT * WN>::BYTES;
+    static_assert(lds <= 160 * 1024, "LDS");
+    hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gemm_q4k_kernel<WMT>, dim3(grid), dim3(GTPB), sizeof(GemmLds<64 * WMT>), s, w.bytes,
-                       w.row_bytes, K, N, M, ws, ntn, ks, Y, part, ps);
+    hipLaunchKernelGGL((gemm_kernel<BP, WM, WN, NT, C64, D>), dim3(grid), dim3(GTPB), lds, s, w.bytes, (uint32_t)w.row_bytes, K,
+                       N, M, ws, ntn, ks, Y, part, ps);
     if ((e = hipGetLastError()) != hipSuccess || ks == 1) return e;
     const size_t MN = (size_t)M * N;
     const int rgrid = (int)std::min<size_t>((MN + 255) / 256, 4096);
@@ -624,51 +757,105 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
     return hipGetLastError();
 }
 
-hipError_t gemm_mfma_q4k(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
-    const int K = w.dim_in;
-    // the kernel addresses the workspace with 32-bit offsets: run M in
-    // chunks whose workspace stays below 4 GiB
-    const int mmax = (int)std::min<size_t>((size_t)M, ((size_t)1 << 31) / ((size_t)K * 4 + 64));
-    if (mmax < M) {
-        for (int m = 0; m < M; m += mmax) {
-            const int mc = std::min(mmax, M - m);
-            hipError_t e = gemm_mfma_q4k(w, mc, X + (size_t)m * K, Y + (size_t)m * w.dim_out, s);
-            if (e != hipSuccess) return e;
-        }
-        return hipSuccess;
+// Activation fragments run D k-steps ahead: a whole block (16) for the
+// small tiles, whose k-steps are short, 8 for the others (what the
+// registers allow).
+template <class BP>
+hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &ws, float *Y, float *part,
+                      hipStream_t s) {
+    if constexpr (std::is_same<BP, GQ4K>::value) {
+        if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 8>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
+        if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
+        return gemm_launch<BP, 1, 8, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 32 x 256
+    } else {
+        if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
+        return gemm_launch<BP, 2, 4, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 64 x 128
     }
-    // 128-row tiles (more MFMA work per operand load) from M > 64; split K
-    // fills the CUs when their count falls short
-    const bool big = M > 64;
-    const int N = w.dim_out, ks = gemm_ksplit(M, N, K, big ? 128 : 64);
-    const size_t wsb = ws_bytes(M, K), pb = ks > 1 ? (size_t)ks * part_stride(M, N) * 4 : 0;
-    uint8_t *base = nullptr;
-    hipError_t e = ws_get(wsb + pb, s, &base);
-    if (e != hipSuccess) return e;
-    const GemmWs ws = ws_carve(base, M, K);
-    float *part = ks > 1 ? (float *)(base + wsb) : nullptr;
-    if (K <= 4096)
-        hipLaunchKernelGGL(gemm_prep_kernel<4>, dim3(M), dim3(256), 0, s, X, K, ws);
-    else if (K <= 16384)
-        hipLaunchKernelGGL(gemm_prep_kernel<16>, dim3(M), dim3(256), 0, s, X, K, ws);
-    else
-        hipLaunchKernelGGL(gemm_prep_kernel<0>, dim3(M), dim3(256), 0, s, X, K, ws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    return big ? gemm_launch<2>(w, M, ws, Y, part, ks, s) : gemm_launch<1>(w, M, ws, Y, part, ks, s);
 }
 
 }  // namespace
 
-hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
+// Workspace bytes of one uq_gemm call (0: the call needs none).
+size_t gemm_ws_bytes(const WeightsView &w, int M) {
+    if (M == 0 || w.dim_out == 0 || w.dim_in == 0) return 0;
+    const Plan p = plan_for(w.dtype, M, w.dim_out, w.dim_in);
+    return prep_bytes(M, w.dim_in) + (p.ks > 1 ? (size_t)p.ks * part_stride(M, w.dim_out) * 4 : 0);
+}
+
+// Formats and sizes the MFMA path takes: Q4_K, Q6_K, Q8_0 with K a multiple
+// of 256, the tensor below 4 GiB and the activation planes below 2 GiB (the
+// kernel forms 32-bit row offsets).
+bool gemm_mfma_ok(const WeightsView &w, int M) {
+    const bool fmt = w.dtype == UQ_Q4_K || w.dtype == UQ_Q6_K || w.dtype == UQ_Q8_0;
+    return fmt && w.dim_in % 256 == 0 && (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32) &&
+           (size_t)M * w.dim_in * 2 < ((size_t)1 << 31);
+}
+
+hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y, void *wsp, size_t wsb, hipStream_t s) {
     if (M == 0 || w.dim_out == 0) return hipSuccess;
-    // the MFMA kernel addresses weight rows with 32-bit offsets from the tensor base
-    const bool fits = (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32);
-    if (w.dtype == UQ_Q4_K && M >= kMinM && fits) return gemm_mfma_q4k(w, M, X, Y, s);
-    for (int m = 0; m < M; m++) {
-        hipError_t e = launch_gemv(w, X + (size_t)m * w.dim_in, Y + (size_t)m * w.dim_out, s);
-        if (e != hipSuccess) return e;
+    const size_t MN = (size_t)M * w.dim_out;
+    if (w.dim_in == 0) {  // empty dots: every output is 0 (a fill kernel, no memset, so it can be captured)
+        const int grid = (int)std::min<size_t>((MN + 255) / 256, 4096);
+        hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, s, Y, MN);
+        return hipGetLastError();
     }
-    return hipSuccess;
+    if (!gemm_mfma_ok(w, M)) {
+        for (int m = 0; m < M; m++) {
+            hipError_t e = launch_gemv(w, X + (size_t)m * w.dim_in, Y + (size_t)m * w.dim_out, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const int K = w.dim_in, N = w.dim_out;
+    const Plan p = plan_for(w.dtype, M, N, K);
+    if (wsb < gemm_ws_bytes(w, M) || !wsp) return hipErrorInvalidValue;
+    const GemmWs ws = ws_carve((uint8_t *)wsp, M, K);
+    float *part = p.ks > 1 ? (float *)((uint8_t *)wsp + prep_bytes(M, K)) : nullptr;
+    const int pgrid = (M + PREP_ROWS - 1) / PREP_ROWS;
+    if (K <= 4096)
+        hipLaunchKernelGGL(gemm_prep_kernel<4>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
+    else if (K <= 12288)
+        hipLaunchKernelGGL(gemm_prep_kernel<12>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
+    else
+        hipLaunchKernelGGL(gemm_prep_kernel<0>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (w.dtype) {
+        case UQ_Q4_K: return gemm_shape<GQ4K>(w, p, M, ws, Y, part, s);
+        case UQ_Q6_K: return gemm_shape<GQ6K>(w, p, M, ws, Y, part, s);
+        default: return gemm_shape<GQ80>(w, p, M, ws, Y, part, s);
+    }
+}
+
+// uq_gemm's workspace: one buffer per (device, stream), grown on demand.
+// A grown-out buffer is never freed (a graph captured earlier, or work
+// still queued on the stream, may refer to it); growth at least doubles,
+// so what is kept stays below twice the largest need.
+hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
+    const size_t need = gemm_ws_bytes(w, M);
+    if (need == 0) return launch_gemm_ws(w, M, X, Y, nullptr, 0, s);
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<uint8_t *, size_t>> cache;
+    static std::vector<void *> retired;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    uint8_t *buf;
+    size_t have;
+    {
+        std::lock_guard<std::mutex> g(mu);
+        auto &slot = cache[{dev, s}];
+        if (slot.second < need) {
+            const size_t sz = std::max(need, 2 * slot.second);
+            void *p = nullptr;
+            if ((e = hipMalloc(&p, sz)) != hipSuccess) return e;
+            if (slot.first) retired.push_back(slot.first);
+            slot = {(uint8_t *)p, sz};
+        }
+        buf = slot.first;
+        have = slot.second;
+    }
+    return launch_gemm_ws(w, M, X, Y, buf, have, s);
 }
 
 }  // namespace uq

@@ -256,9 +256,7 @@ template <> struct Stage<Q4K> {
 // The loads carry the nontemporal hint (cache policy NT = 2): every weight
 // byte is read once, and these full-line coalesced loads then stream at a
 // markedly higher rate (measured: Q6_K head 101 -> 89 us).
-#ifndef UQ_STREAM_CPOL
-#define UQ_STREAM_CPOL 2
-#endif
+constexpr int UQ_STREAM_CPOL = 2;
 __device__ __forceinline__ void lds_dma16(const uint8_t *g, uint8_t *dst) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)dst, 16, 0, UQ_STREAM_CPOL);
 }
@@ -392,15 +390,9 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
 // soon as it is consumed, and the first KT_DEPTH units are issued before the
 // prep. Summation per lane is over tasks in order, then reduce4_rows, as in
 // gemv_kernel.
-#ifndef UQ_KT_NW
-#define UQ_KT_NW 8
-#endif
-#ifndef UQ_KT_DEPTH
-#define UQ_KT_DEPTH 1
-#endif
-#ifndef UQ_KT_WPE
-#define UQ_KT_WPE 2
-#endif
+constexpr int UQ_KT_NW = 8;
+constexpr int UQ_KT_DEPTH = 1;
+constexpr int UQ_KT_WPE = 2;
 constexpr int KT_NW = UQ_KT_NW;        // waves per workgroup, one workgroup per CU
 constexpr int KT_DEPTH = UQ_KT_DEPTH;  // units in flight per wave
 template <class F, bool MULTI>
@@ -476,12 +468,8 @@ __global__ __launch_bounds__(64 * KT_NW) __attribute__((amdgpu_waves_per_eu(UQ_K
 //     y = ((p_0 + p_1) + p_2) + p_3,  p_s = reduce4_rows over slice s.
 // Every wave of the workgroup runs the same number of batches (those of its
 // first group, which has the most rows), so the per-batch barrier is uniform.
-#ifndef UQ_KS_D
-#define UQ_KS_D 4  // rows in flight per wave (Q4_K, Q8_0)
-#endif
-#ifndef UQ_KS_D6
-#define UQ_KS_D6 2  // Q6_K (larger fragments; 4 would spill at 3 waves per SIMD)
-#endif
+constexpr int UQ_KS_D = 4;  // rows in flight per wave (Q4_K, Q8_0)
+constexpr int UQ_KS_D6 = 2;  // Q6_K (larger fragments; 4 would spill at 3 waves per SIMD)
 
 template <class F, int KS, bool MULTI>
 __global__ __launch_bounds__(64 * KS_NW) __attribute__((amdgpu_waves_per_eu(3))) void gemv_ks_kernel(
@@ -739,9 +727,6 @@ int blocks_per_cu(const void *kernel, size_t lds, int tpb) {
 
 int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
     int per_cu = blocks_per_cu(kernel, lds, 64 * nw);
-#ifdef UQ_WG_PER_CU
-    per_cu = UQ_WG_PER_CU;
-#endif
     const int max_waves = num_cus() * per_cu * nw;
     const int rows_per_wave = (N + max_waves - 1) / max_waves;
     const int waves = (N + rows_per_wave - 1) / rows_per_wave;
@@ -753,51 +738,25 @@ int resident_grid(const void *kernel, size_t lds, int N, int nw = WAVES) {
 // per wave. Q6_K: 12 waves (3 per SIMD, <= 168 VGPRs) with two units in
 // flight; Q4_K and Q8_0: 16 waves (4 per SIMD, <= 128 VGPRs), one unit; the
 // gate/up pair: 12 waves, one unit (two fragments).
-#ifndef UQ_Q4K_NW
-#define UQ_Q4K_NW 16
-#endif
-#ifndef UQ_Q4K_D
-#define UQ_Q4K_D 1
-#endif
-#ifndef UQ_PAIR_NW
-#define UQ_PAIR_NW 12
-#endif
-#ifndef UQ_PAIR_D
-#define UQ_PAIR_D 1
-#endif
+constexpr int UQ_Q4K_NW = 16;
+constexpr int UQ_Q4K_D = 1;
+constexpr int UQ_PAIR_NW = 12;
+constexpr int UQ_PAIR_D = 1;
 template <class F> struct Shape { static constexpr int NW = UQ_Q4K_NW, D = UQ_Q4K_D; };
-#ifndef UQ_Q6K_NW
-#define UQ_Q6K_NW 12
-#endif
-#ifndef UQ_Q6K_D
-#define UQ_Q6K_D 2
-#endif
+constexpr int UQ_Q6K_NW = 12;
+constexpr int UQ_Q6K_D = 2;
 template <> struct Shape<Q6K> { static constexpr int NW = UQ_Q6K_NW, D = UQ_Q6K_D; };
 
 // Launch shape of the streaming kernel (one workgroup per CU, SNW waves,
 // SS rows per wave in flight), measured on the 152064 x 4096 Q6_K head and
 // the 4096 / 12288 x 4096 Q4_K projections.
-#ifndef UQ_STREAM_Q6K_NW
-#define UQ_STREAM_Q6K_NW 12
-#endif
-#ifndef UQ_STREAM_Q6K_S
-#define UQ_STREAM_Q6K_S 1
-#endif
-#ifndef UQ_STREAM_Q4K_NW
-#define UQ_STREAM_Q4K_NW 16
-#endif
-#ifndef UQ_STREAM_Q4K_S
-#define UQ_STREAM_Q4K_S 1
-#endif
-#ifndef UQ_STREAM_PAIR_NW
-#define UQ_STREAM_PAIR_NW 12
-#endif
-#ifndef UQ_STREAM_PAIR_S
-#define UQ_STREAM_PAIR_S 1
-#endif
-#ifndef UQ_STREAM_ON
-#define UQ_STREAM_ON 1
-#endif
+constexpr int UQ_STREAM_Q6K_NW = 12;
+constexpr int UQ_STREAM_Q6K_S = 1;
+constexpr int UQ_STREAM_Q4K_NW = 16;
+constexpr int UQ_STREAM_Q4K_S = 1;
+constexpr int UQ_STREAM_PAIR_NW = 12;
+constexpr int UQ_STREAM_PAIR_S = 1;
+constexpr int UQ_STREAM_ON = 1;
 template <class F> struct StreamShape { static constexpr int NW = UQ_STREAM_Q4K_NW, S = UQ_STREAM_Q4K_S; };
 template <> struct StreamShape<Q6K> { static constexpr int NW = UQ_STREAM_Q6K_NW, S = UQ_STREAM_Q6K_S; };
 
@@ -827,9 +786,7 @@ hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x,
     return hipGetLastError();
 }
 
-#ifndef UQ_STREAM_KS
-#define UQ_STREAM_KS 1
-#endif
+constexpr int UQ_STREAM_KS = 1;
 // gemv_stream_ks_kernel for the rows that sks_slices splits (K <= 20480):
 // 2-3 slices run 4 row groups with 2 rows in flight, 4-5 slices 3 groups
 // with 1 (sks_shape; the template arguments below follow it). *done
@@ -1512,9 +1469,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
     }
 }
 
-#ifndef UQ_Q8K_STREAM
-#define UQ_Q8K_STREAM 1
-#endif
+constexpr int UQ_Q8K_STREAM = 1;
 // waves per workgroup of the streaming q8k kernel: the head's shapes for
 // K <= 4096; fewer waves for the longer rows of K <= 12288 (LDS ring)
 template <class F, int T> struct Q8SShape { static constexpr int NW = StreamShape<typename Q8Base<F>::T>::NW; };

@@ -108,8 +108,14 @@ hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const 
                               float *h, hipStream_t s, bool *done);
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y,
                            hipStream_t s);
-// Y[m] = W X[m] for m < M.
+// Y[m] = W X[m] for m < M, with a library-owned workspace per (device,
+// stream), grown on demand.
 hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y,
                        hipStream_t s);
+// The same with a caller-provided workspace of wsb bytes (at least
+// gemm_ws_bytes(w, M); nullptr allowed when that is 0). Allocates nothing.
+size_t gemm_ws_bytes(const WeightsView &w, int M);
+hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
+                          hipStream_t s);
 
 }  // namespace uq

@@ -16,8 +16,7 @@ import os
 import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-# UQ_LIB_PATH selects another build of the library (e.g. a tuning variant).
-LIB_PATH = os.environ.get("UQ_LIB_PATH") or os.path.join(_PKG, "libuq.so")
+LIB_PATH = os.path.join(_PKG, "libuq.so")
 EMU_PATH = os.path.join(_PKG, "libuq_emu.so")
 
 
