@@ -178,6 +178,20 @@ uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count
 uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                   void *stream);
 
+/* uq_gemm that allocates nothing: no reference counterpart. For callers that
+ * cannot allocate device memory inside the call (HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels
+ * and results as uq_gemm, bit for bit; the workspace is a fixed device array
+ * of UQ_GEMM_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends. A call whose workspace would not fit (roughly
+ * 4*m_rows*dim_in bytes, plus the split-K partial tiles for small m_rows)
+ * fails with UQ_ERR_ARG and launches nothing. Calls on one GPU share the
+ * array: calls that may overlap on a GPU (other streams, other threads)
+ * race and must be ordered by the caller. */
+#define UQ_GEMM_SCRATCH_BYTES (32u << 20)
+uq_status uq_gemm_static(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
+                         void *stream);
+
 /* Gated FFN of one token (qwen35_forward.rs:713-768): d_h = swiglu(gate.x, up.x)
  * (kernels.rs:174-182) computed in the GEMV epilogue, then d_y = down.d_h.
  * gate/up: [n_ff][n]; down: [n][n_ff]. d_h holds n_ff floats. */

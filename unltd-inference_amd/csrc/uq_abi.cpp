@@ -547,6 +547,21 @@ uq_status uq_gemm(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, vo
     return UQ_OK;
 }
 
+uq_status uq_gemm_static(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, void *stream) {
+    uq_weights_s *w = handle(wh);
+    if (!w) return fail(UQ_ERR_ARG, "gemm_static: invalid handle");
+    if (m_rows == 0 || w->dim_out == 0) return UQ_OK;
+    if (m_rows > (size_t)INT_MAX) return fail(UQ_ERR_ARG, "gemm_static: m_rows above INT_MAX");
+    if (!d_y || !d_x) return fail(UQ_ERR_ARG, "gemm_static: null device pointer");
+    const uq::WeightsView v = uq::view(*w);
+    const size_t need = uq::gemm_ws_bytes(v, (int)m_rows);
+    if (need > UQ_GEMM_SCRATCH_BYTES)
+        return fail(UQ_ERR_ARG, "gemm_static: workspace of %zu bytes for m_rows %zu exceeds the fixed %u bytes",
+                    need, m_rows, (unsigned)UQ_GEMM_SCRATCH_BYTES);
+    UQ_HIP(uq::launch_gemm_static(v, (int)m_rows, d_x, d_y, (hipStream_t)stream), "gemm_static launch");
+    return UQ_OK;
+}
+
 uq_status uq_ffn_swiglu(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_h, float *d_y,
                         void *stream) {
     uq_weights_s *g = handle(gh), *u = handle(uh), *dn = handle(dh);

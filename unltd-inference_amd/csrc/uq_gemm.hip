@@ -827,6 +827,41 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
     }
 }
 
+// Fixed workspace of uq_gemm_static: a file-scope device array, one copy per
+// GPU the library runs on, held until the process ends. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// for the symbol): its device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and that address is what
+// the kernels receive. Every call on one GPU uses the same array, so calls
+// that overlap on a GPU race; nothing in it needs to start at zero (the
+// prep and the partial tiles overwrite everything the GEMM reads).
+static __device__ __align__(256) uint8_t scratch[UQ_GEMM_SCRATCH_BYTES];
+
+hipError_t scratch_ptr(void **out) {
+    constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static void *ptr[kMaxDev] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        ptr[dev] = p;
+    }
+    *out = ptr[dev];
+    return hipSuccess;
+}
+
+hipError_t launch_gemm_static(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
+    void *p = nullptr;
+    const hipError_t e = scratch_ptr(&p);
+    if (e != hipSuccess) return e;
+    return launch_gemm_ws(w, M, X, Y, p, UQ_GEMM_SCRATCH_BYTES, s);
+}
+
 // uq_gemm's workspace: one buffer per (device, stream), grown on demand.
 // A grown-out buffer is never freed (a graph captured earlier, or work
 // still queued on the stream, may refer to it); growth at least doubles,

@@ -117,5 +117,8 @@ hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y,
 size_t gemm_ws_bytes(const WeightsView &w, int M);
 hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
                           hipStream_t s);
+// The same on the library's fixed device workspace (UQ_GEMM_SCRATCH_BYTES
+// per GPU); the caller checks gemm_ws_bytes(w, M) <= UQ_GEMM_SCRATCH_BYTES.
+hipError_t launch_gemm_static(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s);
 
 }  // namespace uq

@@ -73,6 +73,7 @@ SIGNATURES = {
     "uq_swiglu_d": ([_P, _P, _P, _S, _P], _I),
     "uq_gemv_q8k": ([_P, _P, _P, _P], _I),
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
+    "uq_gemm_static": ([_P, _S, _P, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
     "uq_dequantize": ([_P, _P, _P], _I),
     "uq_embed": ([_P, _P, _S, _P, _P], _I),
@@ -368,6 +369,14 @@ def gemv_q8k(w: Weights, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> Non
 
 def gemm(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
     _check(lib().uq_gemm(w.h, m, d_x.ptr, d_y.ptr, stream))
+
+
+def gemm_static(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
+    """uq_gemm on the library's fixed workspace (allocates nothing)."""
+    _check(lib().uq_gemm_static(w.h, m, d_x.ptr, d_y.ptr, stream))
+
+
+GEMM_SCRATCH_BYTES = 32 << 20
 
 
 def ffn_swiglu(gate: Weights, up: Weights, down: Weights, d_x: DeviceArray, d_h: DeviceArray,
