@@ -6,8 +6,9 @@
 // Every format runs on the f16 MFMA (v_mfma_f32_32x32x16_f16) with f32
 // accumulation, on operands whose products are exact:
 //  * A (activations): x' = x / s_m, s_m a power of two per row (max|x'| in
-//    [512, 1024)), split into f16 hi + lo (22 significant bits). A small
-//    prep kernel writes both planes once per call, in MFMA fragment order.
+//    [512, 1024)), split into f16 hi + lo (22 significant bits). Two small
+//    kernels (row scales, then the conversion) write both planes once per
+//    call, in MFMA fragment order.
 //  * B (weights), dequantized once per workgroup into LDS as f16 integers or
 //    an exact f16 pair:
 //      Q4_K  B = sc*q (<= 945, exact). P_b = sum over block b of x'*B is
@@ -88,96 +89,73 @@ GemmWs ws_carve(uint8_t *base, int M, int K) {
     return w;
 }
 
-// ------------------------------------------------------------ prep kernel
-// Four waves per row, four rows per workgroup (1024 threads). Pass 1: max
-// |x| over the row (per wave, then across the row's four waves in LDS); a
-// NaN or an infinity makes the row's scale NaN and its planes zero, so the
-// row's outputs are NaN. Pass 2: x' hi/lo per octet in fragment order and
-// the group sums (f64 over the 32 x' of a group, then hi/lo). Thread i of a
-// row takes octets i, i+256, ...; NV > 0 keeps its NV/2 octets in registers
-// (K <= 1024*NV), NV == 0 reads x again for pass 2.
-constexpr int PREP_TPB = 1024, PREP_ROWS = 4, PREP_TPR = PREP_TPB / PREP_ROWS;
-template <int NV>
-__global__ __launch_bounds__(PREP_TPB) void gemm_prep_kernel(const float *__restrict__ X, int K, int M, GemmWs ws) {
-    __shared__ uint32_t red[PREP_TPB / 64];
-    const int i = threadIdx.x % PREP_TPR, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int rl = threadIdx.x / PREP_TPR, m = blockIdx.x * PREP_ROWS + rl;
-    const bool live = m < M;  // uniform per wave (a row's waves are whole waves)
-    const float *x = X + (size_t)min(m, M - 1) * K;
-    const int nocts = K >> 3, nit = (nocts + PREP_TPR - 1) / PREP_TPR;
-    float4 v[NV > 0 ? NV : 1];
+// ------------------------------------------------------------ prep kernels
+// gemm_scale_kernel: one wave per row finds max |x| and writes the row
+// scale s_m = 2^(e-10) with max|x| in [2^(e-1), 2^e), so that x' = x / s_m
+// has max|x'| in [512, 1024). The exponent is kept at or above -115 (s_m
+// and 1/s_m stay normal floats; rows that small only lose precision they
+// cannot show). A NaN or an infinity makes s_m NaN: the convert kernel then
+// writes zero planes and the GEMM's NaN scale makes the row's outputs NaN.
+constexpr int SCALE_ROWS = 4;  // rows (waves) per workgroup
+__global__ __launch_bounds__(64 * SCALE_ROWS) void gemm_scale_kernel(const float *__restrict__ X, int K, int M,
+                                                                     float *__restrict__ scale) {
+    const int lane = threadIdx.x & 63, m = blockIdx.x * SCALE_ROWS + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float4 *x = (const float4 *)(X + (size_t)m * K);
+    const int n4 = K >> 2;
     uint32_t mb = 0;
-    auto absmax = [&](float4 a) {
+#pragma unroll 8
+    for (int i = lane; i < n4; i += 64) {
+        const float4 a = x[i];
         mb = max(mb, max(max(__float_as_uint(a.x) & 0x7FFFFFFFu, __float_as_uint(a.y) & 0x7FFFFFFFu),
                          max(__float_as_uint(a.z) & 0x7FFFFFFFu, __float_as_uint(a.w) & 0x7FFFFFFFu)));
-    };
-    if constexpr (NV > 0) {
-#pragma unroll
-        for (int j = 0; j < NV / 2; j++) {
-            const int o = i + PREP_TPR * j;
-            const bool in = j < nit && o < nocts;
-            v[2 * j] = in ? *(const float4 *)(x + 8 * o) : make_float4(0.f, 0.f, 0.f, 0.f);
-            v[2 * j + 1] = in ? *(const float4 *)(x + 8 * o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < NV; j++) absmax(v[j]);
-    } else {
-        for (int o = i; o < nocts; o += PREP_TPR) {
-            absmax(*(const float4 *)(x + 8 * o));
-            absmax(*(const float4 *)(x + 8 * o + 4));
-        }
     }
-    for (int off = 32; off >= 1; off >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
-    if (lane == 0) red[wv] = mb;
-    __syncthreads();
-    constexpr int WPR = PREP_TPR / 64;  // waves per row
+    for (int off = 1; off < 64; off <<= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
+    if (lane == 0) {
+        int ex = 0;
+        if (mb) (void)frexpf(__uint_as_float(mb), &ex);
+        scale[m] = mb < 0x7F800000u ? ldexpf(1.0f, max(ex, -115) - 10) : __uint_as_float(0x7FC00000u);
+    }
+}
+
+// gemm_convert_kernel: workgroup (g, b) converts 256-k block b of rows
+// 8g..8g+7. Lane l of wave w takes row 8g + l%8 and octet 32b + 8w + l/8,
+// so for one octet the eight rows' 16-byte slots form one 128-byte line and
+// the stores write whole lines. Per octet: x' hi/lo in the slot order the
+// weight side unpacks (0,2,1,3,4,6,5,7); per 32-k group (four octets, lanes
+// 8 apart): the sum of x' in f64, stored as an f16 hi/lo pair.
+__global__ __launch_bounds__(256) void gemm_convert_kernel(const float *__restrict__ X, int K, int M, GemmWs ws) {
+    const int lane = threadIdx.x & 63, r = lane & 7, q = lane >> 3;
+    const int m = blockIdx.x * 8 + r, o = blockIdx.y * 32 + (threadIdx.x >> 6) * 8 + q;
+    const bool live = m < M;
+    const int mm = live ? m : M - 1;
+    const float s = ws.scale[mm];
+    const bool finite = s == s;
+    const float inv = finite ? 1.0f / s : 0.0f;  // a power of two: exact
+    const float4 *x = (const float4 *)(X + (size_t)mm * K + 8 * o);
+    const float4 a = x[0], b = x[1];
+    const float xs[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
+    h8 hi, lo;
+    double gs = 0.0;
 #pragma unroll
-    for (int q = 0; q < WPR; q++) mb = max(mb, red[rl * WPR + q]);
-    const bool finite = mb < 0x7F800000u;
-    int ex = 0;
-    if (finite && mb) (void)frexpf(__uint_as_float(mb), &ex);
-    const float inv = finite ? ldexpf(1.0f, 10 - ex) : 0.0f;  // x' = x * 2^(10-ex), max|x'| in [512, 1024)
-    if (live && i == 0) ws.scale[m] = finite ? ldexpf(1.0f, ex - 10) : __uint_as_float(0x7FC00000u);
-    auto convert = [&](int o, float4 a, float4 b) {
-        const bool in = live && o < nocts;
-        // slots (0,2,1,3,4,6,5,7): the order in which the weight side unpacks
-        float xs[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
-        h8 hi, lo;
-        double gs = 0.0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float xv = finite ? xs[e] * inv : 0.0f;
-            hi[e] = (_Float16)xv;
-            lo[e] = (_Float16)(xv - (float)hi[e]);
-            gs += (double)xv;
-        }
-        gs += __shfl_xor(gs, 1);  // the four octets of a 32-k group are threads 4q..4q+3
-        gs += __shfl_xor(gs, 2);
-        if (in) {
-            const size_t at = ((size_t)o * M + m) * 16;
-            *(h8 *)(ws.ahi + at) = hi;
-            *(h8 *)(ws.alo + at) = lo;
-            if ((i & 3) == 0) {
-                const int g = o >> 2, b = g >> 3, gi = g & 7;
-                _Float16 *dst = (_Float16 *)(ws.g + ((size_t)b * M + m) * 32);
-                const _Float16 gh = (_Float16)gs;
-                dst[gi] = gh;
-                dst[8 + gi] = (_Float16)(gs - (double)gh);
-            }
-        }
-    };
-    if constexpr (NV > 0) {
-#pragma unroll
-        for (int j = 0; j < NV / 2; j++)
-            if (j < nit) convert(i + PREP_TPR * j, v[2 * j], v[2 * j + 1]);
-    } else {
-        for (int j = 0; j < nit; j++) {
-            const int o = i + PREP_TPR * j;
-            const bool in = o < nocts;
-            const float4 a = in ? *(const float4 *)(x + 8 * o) : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 b = in ? *(const float4 *)(x + 8 * o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            convert(o, a, b);
-        }
+    for (int e = 0; e < 8; e++) {
+        const float xc = finite ? xs[e] * inv : 0.0f;
+        hi[e] = (_Float16)xc;
+        lo[e] = (_Float16)(xc - (float)hi[e]);
+        gs += (double)xc;
+    }
+    gs += __shfl_xor(gs, 8);
+    gs += __shfl_xor(gs, 16);
+    if (!live) return;
+    const size_t at = ((size_t)o * M + m) * 16;
+    *(h8 *)(ws.ahi + at) = hi;
+    *(h8 *)(ws.alo + at) = lo;
+    if ((q & 3) == 0) {
+        _Float16 *dst = (_Float16 *)(ws.g + ((size_t)blockIdx.y * M + m) * 32);
+        const int gi = ((threadIdx.x >> 6) * 8 + q) >> 2;
+        const _Float16 gh = (_Float16)(float)gs;
+        dst[gi] = gh;
+        dst[8 + gi] = (_Float16)(float)(gs - (double)gh);
     }
 }
 
@@ -496,12 +474,16 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
 
     // dequant role: quarter wv%4 of columns lane + 64(wv/4) + 128 i
     const int dq_c = wv & 3, dq_col0 = lane + 64 * (wv >> 2);
-    auto dequant = [&](int v, int i) {  // task i of sub-step v
-        const int col = dq_col0 + 128 * i;
-        if (col < TN) {
-            const uint8_t *rc = lds + Lay::RAW + ((v >> 2) & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
-            BP::template dequant<NTILE>(rc, v & 3, dq_c, lds + Lay::BT + (v & 1) * Lay::BTSLOT, col);
-        }
+    // Task i of sub-step v. Every wave runs NDQ tasks, with no branch, so
+    // that the dequantization interleaves with the MFMAs: where TN is not a
+    // multiple of 128 (192), the waves of the upper half redo the task of
+    // their lower-half partner for columns past the tile (same column, same
+    // quarter: the same bytes written to the same LDS slots).
+    auto dequant = [&](int v, int i) {
+        int col = dq_col0 + 128 * i;
+        if constexpr (TN % 128 != 0) col = col < TN ? col : col - 64;
+        const uint8_t *rc = lds + Lay::RAW + ((v >> 2) & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
+        BP::template dequant<NTILE>(rc, v & 3, dq_c, lds + Lay::BT + (v & 1) * Lay::BTSLOT, col);
     };
     auto block_pass = [&](int b) {  // per-column constants of block b, one column per thread
         if constexpr (BP::kBlockScale || BP::kMin) {
@@ -548,13 +530,13 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int r = 0; r < RAWR; r++) raw_load(1, r);
     fence();
 #pragma unroll
-    for (int d = 0; d < D; d++) a_load(ah[d], al[d], d);
+    for (int d = 0; d < D - 1; d++) a_load(ah[d], al[d], d);
     if constexpr (BP::kMin) gmin = g_load(0);
     fence();
     // raw block 0 landed: after its last load every wave issued at least
     // RAWR-1 loads of block 1 (a partial last round is skipped by the waves
-    // it does not reach) and the 2D activation loads (and the group sums)
-    wait_vm_barrier<RAWR - 1 + 2 * D + (BP::kMin ? 1 : 0)>();
+    // it does not reach) and the 2(D-1) activation loads (and the group sums)
+    wait_vm_barrier<RAWR - 1 + 2 * (D - 1) + (BP::kMin ? 1 : 0)>();
     block_pass(0);
 #pragma unroll
     for (int i = 0; i < NDQ; i++) dequant(0, i);
@@ -565,10 +547,25 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int t16 = 0; t16 < 16; t16++) {
             const int s = t16 >> 2, tt = t16 & 3, u = 4 * kb + s, kk = 16 * kb + t16;
-            // B operands of the next k-step (the next sub-step's after the barrier)
+            // global loads first (the raw rounds are asm that orders memory
+            // operations): raw rounds of block kb+2, the activations of
+            // k-step kk+D-1 into the slot the previous k-step consumed, the
+            // next block's group sums
+#pragma unroll
+            for (int r = 0; r < RAWR; r++)
+                if (raw_step(r, RAWR) == t16) raw_load(kb + 2, r);
+            a_load(ah[(t16 + D - 1) % D], al[(t16 + D - 1) % D], kk + D - 1);
+            if constexpr (BP::kMin)
+                if (t16 == 14) gmin = g_load(kb + 1);
+            // then one region the scheduler can interleave: B operands of the
+            // next k-step (the next sub-step's after the barrier), the
+            // dequantization of sub-step u+1 (tasks in k-steps 0..NDQ-1), the
+            // MFMAs of this k-step
             if (tt < 3) b_read(bnxt, u, tt + 1);
             else b_read(bnxt, u + 1, 0);
-            // MFMAs of this k-step
+#pragma unroll
+            for (int i = 0; i < NDQ; i++)
+                if (i == tt) dequant(u + 1, i);
 #pragma unroll
             for (int p = 0; p < BP::NPASS; p++)
 #pragma unroll
@@ -577,7 +574,7 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
                     P[j] = mfma(a, bcur[BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
                 }
             if constexpr (BP::kMin) {
-                // the block's min term into C: -sum_g dmin*m_g * sum_g(x')
+                // the block's min term: -sum_g dmin*m_g * sum_g(x')
                 if (t16 == 13) {
                     const uint8_t *bm = lds + Lay::BM + (kb & 1) * Lay::BMSLOT;
 #pragma unroll
@@ -599,20 +596,14 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
                     }
                 }
             }
-            // loads: raw rounds of block kb+2, then activations D k-steps ahead
-            // (and the next block's group sums)
+            // interleave: the LDS reads, then each MFMA followed by a few VALU
+            // (the dequantization), the LDS writes last
+            __builtin_amdgcn_sched_group_barrier(0x100, BP::NBT * NT + 2, 0);
 #pragma unroll
-            for (int r = 0; r < RAWR; r++)
-                if (raw_step(r, RAWR) == t16) raw_load(kb + 2, r);
-            a_load(ah[t16 % D], al[t16 % D], kk + D);
-            if constexpr (BP::kMin)
-                if (t16 == 14) gmin = g_load(kb + 1);
-            fence();
-            // dequant of sub-step u+1 in k-steps 0..NDQ-1; block constants of
-            // the next block in k-step 3 of sub-step 3
-#pragma unroll
-            for (int i = 0; i < NDQ; i++)
-                if (i == tt) dequant(u + 1, i);
+            for (int q = 0; q < BP::NPASS * NT; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
             if (tt == 2) {
                 // this sub-step's B reads are done and the next sub-step's B
                 // tile is complete; at sub-step 2 the next block's raw bytes
@@ -783,11 +774,12 @@ size_t gemm_ws_bytes(const WeightsView &w, int M) {
 }
 
 // Formats and sizes the MFMA path takes: Q4_K, Q6_K, Q8_0 with K a multiple
-// of 256, the tensor below 4 GiB and the activation planes below 2 GiB (the
-// kernel forms 32-bit row offsets).
+// of 256 and at most 65535 blocks of 256 (the convert kernel's grid), the
+// tensor below 4 GiB and the activation planes below 2 GiB (the kernel forms
+// 32-bit row offsets).
 bool gemm_mfma_ok(const WeightsView &w, int M) {
     const bool fmt = w.dtype == UQ_Q4_K || w.dtype == UQ_Q6_K || w.dtype == UQ_Q8_0;
-    return fmt && w.dim_in % 256 == 0 && (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32) &&
+    return fmt && w.dim_in % 256 == 0 && w.dim_in / 256 <= 65535 && (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32) &&
            (size_t)M * w.dim_in * 2 < ((size_t)1 << 31);
 }
 
@@ -799,7 +791,7 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
         hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, s, Y, MN);
         return hipGetLastError();
     }
-    if (!gemm_mfma_ok(w, M)) {
+    if (M == 1 || !gemm_mfma_ok(w, M)) {  // one row is a GEMV (the decode kernels stream it faster)
         for (int m = 0; m < M; m++) {
             hipError_t e = launch_gemv(w, X + (size_t)m * w.dim_in, Y + (size_t)m * w.dim_out, s);
             if (e != hipSuccess) return e;
@@ -811,13 +803,9 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
     if (wsb < gemm_ws_bytes(w, M) || !wsp) return hipErrorInvalidValue;
     const GemmWs ws = ws_carve((uint8_t *)wsp, M, K);
     float *part = p.ks > 1 ? (float *)((uint8_t *)wsp + prep_bytes(M, K)) : nullptr;
-    const int pgrid = (M + PREP_ROWS - 1) / PREP_ROWS;
-    if (K <= 4096)
-        hipLaunchKernelGGL(gemm_prep_kernel<4>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
-    else if (K <= 12288)
-        hipLaunchKernelGGL(gemm_prep_kernel<12>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
-    else
-        hipLaunchKernelGGL(gemm_prep_kernel<0>, dim3(pgrid), dim3(PREP_TPB), 0, s, X, K, M, ws);
+    hipLaunchKernelGGL(gemm_scale_kernel, dim3((M + SCALE_ROWS - 1) / SCALE_ROWS), dim3(64 * SCALE_ROWS), 0, s, X, K, M,
+                       ws.scale);
+    hipLaunchKernelGGL(gemm_convert_kernel, dim3((M + 7) / 8, K / 256), dim3(256), 0, s, X, K, M, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (w.dtype) {
