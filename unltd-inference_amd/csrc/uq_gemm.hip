@@ -34,10 +34,12 @@
 //    k-octet): wave w takes quarter w%4 of each column's 64 k, lane l the
 //    columns l + 64(w/4) + 128i.
 //  * Activation fragments come from global memory straight into VGPRs,
-//    four k-steps ahead; the prep wrote them so that each fragment load is
+//    D k-steps ahead; the prep wrote them so that each fragment load is
 //    two contiguous 512-byte runs.
-//  * One barrier per sub-step, after the B reads of its third k-step: the
-//    next sub-step's B tile is complete and this one's slot is free.
+//  * B fragments are read from LDS two k-steps ahead into a four-slot
+//    register ring. One barrier per sub-step, after its second k-step: the
+//    next sub-step's B tile is complete and this one's slot is no longer
+//    read (its last fragments were read in k-step 1).
 // Workgroups are ordered so that each XCD takes mostly one M tile (its
 // activation planes stay in that XCD's L2). When the tiles do not cover the
 // CUs (small M), K is split into ranges, one workgroup per (tile, range),
@@ -240,7 +242,7 @@ __device__ __forceinline__ uint8_t *bslot(uint8_t *bt, int b, int t, int col, in
 // k-octet c of the sub-step, its high nibbles k-octet 4 + c.
 struct GQ4K {
     static constexpr int RB = 144, CPR = 9, NBT = 1, NPASS = 2;
-    static constexpr bool kBlockScale = true, kMin = true;
+    static constexpr bool kBlockScale = true, kMin = true, kSub = true;
     __device__ static constexpr int pa(int p) { return p; }
     __device__ static constexpr int pb(int) { return 0; }
     // scale_min_k4 (quants.rs:92-102): 6-bit sc and m of group g from the
@@ -252,16 +254,21 @@ struct GQ4K {
         return g < 4 ? (S1 >> (8 * g)) & 63
                      : ((S2 >> (8 * (g - 4) + 4)) & 0xF) | (((S1 >> (8 * (g - 4) + 6)) & 3) << 4);
     }
+    // Sub-step s's dequantization constants {sc_a, -1024 sc_a, sc_b/16,
+    // -64 sc_b} (groups a = 2s, b = 2s+1) as f16 pairs: a nibble n in bits
+    // 0-3 of an f16 with the bits of 1024 reads 1024+n, in bits 4-7 it reads
+    // 1024+16n, so sc*n = fma(1024+n, sc, -1024 sc) = fma(1024+16n, sc/16,
+    // -64 sc), every operand and the result exact f16.
+    __device__ static u4 sub_consts(const uint8_t *rc, int s) {
+        const uint32_t S0 = *(const uint32_t *)(rc + 4), S2 = *(const uint32_t *)(rc + 12);
+        const float sa = (float)sc_of(S0, S2, 2 * s), sb = (float)sc_of(S0, S2, 2 * s + 1);
+        return u4{as_u(hh(sa)), as_u(hh(-1024.0f * sa)), as_u(hh(sb * 0.0625f)), as_u(hh(-64.0f * sb))};
+    }
+    // quarter c of sub-step s with the sub-step's constants k (sub_consts)
     template <int NTILE>
-    __device__ static void dequant(const uint8_t *rc, int s, int c, uint8_t *bt, int col) {
-        const u4 h = *(const u4 *)rc;
+    __device__ static void dequant(const uint8_t *rc, int s, int c, uint8_t *bt, int col, u4 k) {
         const uint2 q = *(const uint2 *)(rc + 16 + 32 * s + 8 * c);
-        const float sa = (float)sc_of(h.y, h.w, 2 * s), sb = (float)sc_of(h.y, h.w, 2 * s + 1);
-        // a nibble n in bits 0-3 of an f16 with the bits of 1024 reads 1024+n,
-        // in bits 4-7 it reads 1024+16n: sc*n = fma(1024+n, sc, -1024 sc) =
-        // fma(1024+16n, sc/16, -64 sc), every operand and the result exact
-        // f16, one rounding of an exact value
-        const h2 lsc = hh(sa), loff = hh(-1024.0f * sa), hsc = hh(sb * 0.0625f), hoff = hh(-64.0f * sb);
+        const h2 lsc = as_h2(k.x), loff = as_h2(k.y), hsc = as_h2(k.z), hoff = as_h2(k.w);
         const uint32_t lm = 0x000F000Fu, hm = 0x00F000F0u, lmag = 0x64006400u, hmag = 0x64006400u;
         const uint32_t D[2] = {q.x, q.y};
         u4 lo, hi;
@@ -303,7 +310,7 @@ struct GQ4K {
 // belong to the next block or to the tensor padding and are not read).
 struct GQ6K {
     static constexpr int RB = 210, CPR = 14, NBT = 2, NPASS = 4;
-    static constexpr bool kBlockScale = true, kMin = false;
+    static constexpr bool kBlockScale = true, kMin = false, kSub = false;
     __device__ static constexpr int pa(int p) { return p & 1; }
     __device__ static constexpr int pb(int p) { return p >> 1; }
     template <int NTILE>
@@ -345,7 +352,7 @@ struct GQ6K {
 // dwords and realigned with v_alignbyte.
 struct GQ80 {
     static constexpr int RB = 272, CPR = 17, NBT = 2, NPASS = 3;
-    static constexpr bool kBlockScale = false, kMin = false;  // P added to C unscaled
+    static constexpr bool kBlockScale = false, kMin = false, kSub = false;  // P added to C unscaled
     __device__ static constexpr int pa(int p) { return p == 1 ? 1 : 0; }
     __device__ static constexpr int pb(int p) { return p == 2 ? 1 : 0; }
     template <int NTILE>
@@ -401,7 +408,11 @@ struct GemmLayout {
     static constexpr int BMSLOT = BP::kMin ? TN * 32 : 0;
     static constexpr int DVSLOT = BP::kBlockScale ? TN * 4 : 0;
     static constexpr int RAW = 0, BT = 2 * RAWSLOT, BM = BT + 2 * BTSLOT, DV = BM + 2 * BMSLOT;
-    static constexpr int BYTES = DV + 2 * DVSLOT;
+    static constexpr int SC = DV + 2 * DVSLOT;
+    // sub_consts of sub-steps 1..3 of one block (one slot: written at k-step
+    // 11 of the block before, read up to k-step 9), where the LDS has room
+    static constexpr bool SUB = BP::kSub && SC + 3 * TN * 16 <= 160 * 1024;
+    static constexpr int BYTES = SC + (SUB ? 3 * TN * 16 : 0);
     // dequant tasks per wave and sub-step: columns lane + 64(w/4) + 128 i
     static constexpr int NDQ = (TN + 127) / 128;
 };
@@ -474,23 +485,41 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
 
     // dequant role: quarter wv%4 of columns lane + 64(wv/4) + 128 i
     const int dq_c = wv & 3, dq_col0 = lane + 64 * (wv >> 2);
-    // Task i of sub-step v. Every wave runs NDQ tasks, with no branch, so
-    // that the dequantization interleaves with the MFMAs: where TN is not a
-    // multiple of 128 (192), the waves of the upper half redo the task of
-    // their lower-half partner for columns past the tile (same column, same
-    // quarter: the same bytes written to the same LDS slots).
-    auto dequant = [&](int v, int i) {
-        int col = dq_col0 + 128 * i;
-        if constexpr (TN % 128 != 0) col = col < TN ? col : col - 64;
-        const uint8_t *rc = lds + Lay::RAW + ((v >> 2) & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
-        BP::template dequant<NTILE>(rc, v & 3, dq_c, lds + Lay::BT + (v & 1) * Lay::BTSLOT, col);
+    // Task i (k-step i of the sub-step before) of sub-step sv (0..3, known
+    // at compile time) of block blk.
+    auto dequant = [&](int blk, int sv, int i) {
+        // where TN is not a multiple of 128 (192), the upper-half waves have
+        // no second task (a wave-uniform branch)
+        if constexpr (TN % 128 != 0)
+            if (64 * (wv >> 2) + 128 * i >= TN) return;
+        const int col = dq_col0 + 128 * i;
+        const uint8_t *rc = lds + Lay::RAW + (blk & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
+        uint8_t *bt = lds + Lay::BT + (sv & 1) * Lay::BTSLOT;
+        if constexpr (Lay::SUB) {
+            // sub-step 0 is dequantized before its block's constants exist
+            const u4 k = sv == 0 ? BP::sub_consts(rc, 0) : *(const u4 *)(lds + Lay::SC + ((sv - 1) * TN + col) * 16);
+            BP::template dequant<NTILE>(rc, sv, dq_c, bt, col, k);
+        } else if constexpr (BP::kSub) {
+            BP::template dequant<NTILE>(rc, sv, dq_c, bt, col, BP::sub_consts(rc, sv));
+        } else {
+            BP::template dequant<NTILE>(rc, sv, dq_c, bt, col);
+        }
     };
-    auto block_pass = [&](int b) {  // per-column constants of block b, one column per thread
+    // Per-column constants of block b: one column per thread, and the
+    // dequantization constants of its sub-steps 1..3.
+    auto block_pass = [&](int b) {
         if constexpr (BP::kBlockScale || BP::kMin) {
             if (t < TN) {
                 const uint8_t *rc = lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + t * (16 * BP::CPR);
                 BP::block_consts(rc, lds + Lay::BM + (b & 1) * Lay::BMSLOT + t * 32,
                                  (float *)(lds + Lay::DV + (b & 1) * Lay::DVSLOT) + t);
+            }
+        }
+        if constexpr (Lay::SUB) {
+            for (int p = t; p < 3 * TN; p += GTPB) {
+                const int sv = 1 + p / TN, col = p - (sv - 1) * TN;
+                const uint8_t *rc = lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
+                *(u4 *)(lds + Lay::SC + p * 16) = BP::sub_consts(rc, sv);
             }
         }
     };
@@ -512,7 +541,8 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     h8 ah[D], al[D];
     h8 gmin;  // this lane's group sums of the current block (Q4_K)
-    h8 bcur[BP::NBT][NT], bnxt[BP::NBT][NT];
+    // B operands of k-step t in ring slot t % 4, read two k-steps ahead
+    h8 bring[4][BP::NBT][NT];
     auto b_read = [&](h8 (&dst)[BP::NBT][NT], int v, int tt) {
         const uint8_t *bt = lds + Lay::BT + (v & 1) * Lay::BTSLOT;
 #pragma unroll
@@ -539,9 +569,10 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     wait_vm_barrier<RAWR - 1 + 2 * (D - 1) + (BP::kMin ? 1 : 0)>();
     block_pass(0);
 #pragma unroll
-    for (int i = 0; i < NDQ; i++) dequant(0, i);
+    for (int i = 0; i < NDQ; i++) dequant(0, 0, i);
     lds_barrier();
-    b_read(bcur, 0, 0);
+    b_read(bring[0], 0, 0);
+    b_read(bring[1], 0, 1);
 
     for (int kb = 0; kb < nblk; kb++) {
 #pragma unroll
@@ -557,21 +588,21 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
             a_load(ah[(t16 + D - 1) % D], al[(t16 + D - 1) % D], kk + D - 1);
             if constexpr (BP::kMin)
                 if (t16 == 14) gmin = g_load(kb + 1);
-            // then one region the scheduler can interleave: B operands of the
-            // next k-step (the next sub-step's after the barrier), the
+            // then one region the scheduler can interleave: B operands of
+            // k-step t16+2 (the next sub-step's after the barrier), the
             // dequantization of sub-step u+1 (tasks in k-steps 0..NDQ-1), the
             // MFMAs of this k-step
-            if (tt < 3) b_read(bnxt, u, tt + 1);
-            else b_read(bnxt, u + 1, 0);
+            if (tt < 2) b_read(bring[tt + 2], u, tt + 2);
+            else b_read(bring[tt - 2], u + 1, tt - 2);
 #pragma unroll
             for (int i = 0; i < NDQ; i++)
-                if (i == tt) dequant(u + 1, i);
+                if (i == tt) dequant(s < 3 ? kb : kb + 1, (s + 1) & 3, i);
 #pragma unroll
             for (int p = 0; p < BP::NPASS; p++)
 #pragma unroll
                 for (int j = 0; j < NT; j++) {
                     const h8 a = BP::pa(p) ? al[t16 % D] : ah[t16 % D];
-                    P[j] = mfma(a, bcur[BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
+                    P[j] = mfma(a, bring[tt][BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
                 }
             if constexpr (BP::kMin) {
                 // the block's min term: -sum_g dmin*m_g * sum_g(x')
@@ -604,22 +635,22 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
             }
-            if (tt == 2) {
-                // this sub-step's B reads are done and the next sub-step's B
-                // tile is complete; at sub-step 2 the next block's raw bytes
-                // (issued at k-steps 11-15 of the previous block) have landed:
-                // after them this wave issued at least the 22 activation loads
-                // of k-steps 0-10
+            if (tt == 1) {
+                // this sub-step's B reads are done (k-step 1 read k-step 3's)
+                // and the next sub-step's B tile is complete (its
+                // dequantization ran in k-steps 0 and 1); at sub-step 2 the
+                // next block's raw bytes (issued at k-steps 11-15 of the
+                // previous block) have landed: after them this wave issued at
+                // least the 20 activation loads of k-steps 0-9
                 if (s == 2)
-                    wait_vm_barrier<2 * 11>();
+                    wait_vm_barrier<2 * 10>();
                 else
                     lds_barrier();
             }
-            if (s == 3 && tt == 3) block_pass(kb + 1);
-#pragma unroll
-            for (int b = 0; b < BP::NBT; b++)
-#pragma unroll
-                for (int j = 0; j < NT; j++) bcur[b][j] = bnxt[b][j];
+            // the next block's raw bytes landed at the barrier above; its
+            // constants are read from the next barrier on (sub-step 3's
+            // dequantization of its sub-step 0 decodes its own)
+            if (s == 2 && tt == 3) block_pass(kb + 1);
         }
         // end of the block: C += d * P (d*P is exact in f64)
         if constexpr (BP::kBlockScale) {
@@ -749,14 +780,14 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
 }
 
 // Activation fragments run D k-steps ahead: a whole block (16) for the
-// small tiles, whose k-steps are short, 8 for the others (what the
-// registers allow).
+// small tiles, whose k-steps are short, 8 or 4 for the others (what the
+// registers allow; the 128 x 192 tile measured the same at 2, 4 and 8).
 template <class BP>
 hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &ws, float *Y, float *part,
                       hipStream_t s) {
     if constexpr (std::is_same<BP, GQ4K>::value) {
-        if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 8>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
-        if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
+        if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
+        if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 4>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
         return gemm_launch<BP, 1, 8, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 32 x 256
     } else {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
