@@ -205,21 +205,30 @@ def bench_ffn(hip, steps, warmup):
 
 
 def bench_gemm(hip, steps, warmup):
-    K, N = 4096, 12288
-    w = S.weights(S.Q4_K, N, K, seed=S.seed_for(3))
-    W = uq.Weights(w, uq.DType.Q4K, K, N)
-    X = S.activations(K, seed=S.seed_for(3), rows=512)
-    dx, dy = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * 512 * N)
+    """Prefill GEMM M sweeps: Q4_K N=12288 K=4096 (the prefill workload), and
+    the same sweep for Q6_K (N=4096, K=12288, an FFN down shape) and Q8_0
+    (N=12288, K=4096). Timed with HIP events on the launch stream."""
+    s = hip.stream()
     out = {}
-    for M in (1, 8, 32, 128, 512):
-        st = max(2, steps // (1 if M < 128 else 4))
-        wall, ev = timed(hip, lambda: uq.gemm(W, M, dx, dy), st, max(1, warmup // 2))
-        t = ev * 1e-3 / st
-        out[str(M)] = {"us": t * 1e6, "tflops": 2 * M * N * K / t / 1e12,
-                       "frac_bf16_peak": 2 * M * N * K / t / 1e12 / BF16_PEAK_TFLOPS,
-                       "weight_gbs": w.size / t / 1e9}
-    W.free()
-    return {"config": "Q4_K prefill GEMM N=12288 K=4096, M sweep", "by_m": out}
+    for dt, name, K, N in ((S.Q4_K, "q4k", 4096, 12288), (S.Q6_K, "q6k", 12288, 4096), (S.Q8_0, "q80", 4096, 12288)):
+        w = S.weights(dt, N, K, seed=S.seed_for(3))
+        W = uq.Weights(w, dt, K, N)
+        X = S.activations(K, seed=S.seed_for(3), rows=512)
+        dx, dy = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * 512 * N)
+        by_m = {}
+        for M in (1, 8, 32, 128, 512):
+            st = max(2, steps // (1 if M < 128 else 4))
+            wall, ev = timed(hip, lambda: uq.gemm(W, M, dx, dy, s), st, max(1, warmup // 2), s)
+            t = ev * 1e-3 / st
+            by_m[str(M)] = {"us": t * 1e6, "tflops": 2 * M * N * K / t / 1e12,
+                            "frac_bf16_peak": 2 * M * N * K / t / 1e12 / BF16_PEAK_TFLOPS,
+                            "weight_gbs": w.size / t / 1e9}
+        out[name] = {"N": N, "K": K, "by_m": by_m}
+        W.free()
+        dx.free()
+        dy.free()
+    return {"config": "prefill GEMM M sweeps (uq_gemm); q4k is the prefill workload N=12288 K=4096",
+            "by_m": out["q4k"]["by_m"], "q6k": out["q6k"], "q80": out["q80"]}
 
 
 def decode_layers():

@@ -168,20 +168,25 @@ uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count
 /* Batched prefill: d_y[m][dim_out] = W . d_x[m][dim_in] for m < m_rows, with
  * gemv_quant semantics per row (the reference feeds prefill tokens one at a
  * time, greedy.rs:55-65; each row equals gemv_quant of that token).
- * Q4_K with m_rows >= 8 (and a tensor below 4 GiB) runs on the f16 MFMA and
- * uses a library-owned device workspace of about 4*m_rows*dim_in bytes per
- * (device, stream), allocated on first use and grown when a call needs more
- * (growing synchronizes the stream). When the output tiles do not cover the
- * CUs (small m_rows), K is split and the workspace also holds the partial
- * results: at most CUs x 64 x 192 floats (12.6 MB on 256 CUs). Other shapes
- * run as m_rows GEMVs. */
+ * Q4_K, Q6_K and Q8_0 with m_rows >= 2 and dim_in a multiple of 256 (tensor
+ * below 4 GiB, activation planes below 2 GiB) run on the f16 MFMA, one weight
+ * pass per 32-128-row tile; the row results are within the gemv_quant
+ * tolerance plus 2^-22 * sum_e |x_e w_e| (the matrix cores' f32
+ * accumulation). m_rows == 1 and other shapes run as m_rows GEMVs. A NaN or
+ * infinity in a row of d_x makes that row of d_y NaN. The MFMA path uses a
+ * library-owned device workspace per (device, stream) of about
+ * 4*m_rows*dim_in bytes (plus the split-K partial tiles when the output
+ * tiles do not cover the CUs), allocated on first use and grown when a call
+ * needs more; a grown-out buffer is kept, never freed, so work queued on the
+ * stream or a graph captured earlier stays valid. A call can be captured in
+ * a HIP graph once a call of that size or larger has run on the stream. */
 uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                   void *stream);
 
 /* uq_gemm that allocates nothing: no reference counterpart. For callers that
  * cannot allocate device memory inside the call (HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels
- * and results as uq_gemm, bit for bit; the workspace is a fixed device array
+ * and results as uq_gemm (the same bits); the workspace is a fixed device array
  * of UQ_GEMM_SCRATCH_BYTES inside the library, one per GPU, held until the
  * process ends. A call whose workspace would not fit (roughly
  * 4*m_rows*dim_in bytes, plus the split-K partial tiles for small m_rows)
@@ -198,11 +203,13 @@ uq_status uq_gemm_static(uq_weights w, size_t m_rows, const float *d_x, float *d
 uq_status uq_ffn_swiglu(uq_weights gate, uq_weights up, uq_weights down,
                         const float *d_x, float *d_h, float *d_y, void *stream);
 
-/* The reference FFN (qwen35_forward.rs:735-765) bit for bit on the device:
- * d_g = gemv_quant_q8k(gate, d_x), d_u = gemv_quant_q8k(up, d_x) (one
- * launch), d_h = swiglu(d_g, d_u) (kernels.rs:174-182), d_y =
- * gemv_quant_q8k(down, d_h). gate/up: [n_ff][n]; down: [n][n_ff]; Q4_K or
- * Q6_K. d_g, d_u, d_h hold n_ff floats (the reference's g, u, sw). */
+/* The reference FFN (qwen35_forward.rs:735-765) on the device: d_g =
+ * gemv_quant_q8k(gate, d_x), d_u = gemv_quant_q8k(up, d_x) (one launch),
+ * d_h = swiglu(d_g, d_u) (kernels.rs:174-182), d_y = gemv_quant_q8k(down,
+ * d_h). d_g, d_u and d_y (given d_h) are bit-exact; d_h is within 2 ulp of
+ * the reference's swiglu, whose expf is the platform libm's (here expf is
+ * evaluated in f64 and rounded once). gate/up: [n_ff][n]; down: [n][n_ff];
+ * Q4_K or Q6_K. d_g, d_u, d_h hold n_ff floats (the reference's g, u, sw). */
 uq_status uq_ffn_swiglu_q8k(uq_weights gate, uq_weights up, uq_weights down,
                             const float *d_x, float *d_g, float *d_u, float *d_h,
                             float *d_y, void *stream);

@@ -117,7 +117,8 @@ def test_gemm_q6k_full_int8_scales():
 @pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0])
 def test_gemm_dynamic_range(dtype):
     """Rows of very different magnitude (1e-4 .. 1e4), rows spanning many
-    binades, a zero row and a row with one large entry: the per-row
+    binades, a zero row, a row with one large entry and rows of tiny or
+    subnormal values: the per-row
     power-of-two scale and the f16 hi/lo split keep the operands exact to
     22 bits. The matrix cores accumulate in f32, so an output whose terms
     cancel deeply sits within the gemv_quant tolerance plus the accumulation
@@ -131,6 +132,10 @@ def test_gemm_dynamic_range(dtype):
     X[5] = 0.0
     X[7, :] = 0.0
     X[7, 100] = 3.0e4
+    # rows near the bottom of the f32 range (max|x| ~ 2^-124, and subnormals):
+    # the row exponent is clamped so that 1/s stays finite
+    X[9] = (rng.standard_normal(K) * 1e-38).astype(np.float32)
+    X[11] = (rng.standard_normal(K) * 1e-41).astype(np.float32)
     w = S.weights(dtype, N, K, seed=99)
     Y = run_gemm(dtype, w, K, N, X)
     Wx = exact_weights_f64(dtype, w, N, K)
