@@ -216,6 +216,39 @@ def test_gemv_quant_q8k_bit_exact(dtype, K, N):
     assert_bitwise(got, ref, f"q8k dtype {dtype} K {K}")
 
 
+@pytest.mark.parametrize("dtype,K,N", [(S.Q4_K, 4096, 64), (S.Q6_K, 4096, 64), (S.Q6_K, 12288, 64),
+                                       (S.Q4_K, 12288, 64)])
+def test_gemv_quant_q8k_special_block_scales(dtype, K, N):
+    """Blocks whose f16 d (and Q4_K dmin) is subnormal, the largest finite,
+    zero, negative, infinite or NaN: the epilogue's f16 decode matches the
+    reference's f16_to_f32 (quants.rs:44-72). Finite outputs are compared
+    bit for bit; the rows a NaN or infinite scale reaches are NaN in both."""
+    w = S.weights(dtype, N, K, seed=K + N + dtype).reshape(N, -1)
+    bb = 144 if dtype == S.Q4_K else 210
+    doff = 0 if dtype == S.Q4_K else 208
+    specials = [0x0001, 0x03FF, 0x0200, 0x7BFF, 0x0000, 0x8000, 0x83FF, 0xFBFF, 0x7C00, 0xFC00, 0x7E00, 0x7D01]
+    rng = np.random.default_rng(dtype + K)
+    for r in range(N):
+        blk = int(rng.integers(0, K // 256))
+        v = specials[r % len(specials)]
+        w[r, blk * bb + doff] = v & 0xFF
+        w[r, blk * bb + doff + 1] = v >> 8
+        if dtype == S.Q4_K and r % 3 == 0:  # dmin too
+            v2 = specials[(r // 3) % len(specials)]
+            w[r, blk * bb + 2] = v2 & 0xFF
+            w[r, blk * bb + 3] = v2 >> 8
+    w = w.reshape(-1)
+    x = S.activations(K, seed=N + 5)
+    ref = np.zeros(N, np.float32)
+    O.gemv_quant_q8k(ref, x, w, K, N, dtype, nthreads=NT)
+    got = np.zeros(N, np.float32)
+    uq.gemv_quant_q8k(got, x, w, K, N, dtype)
+    nan_r, nan_g = np.isnan(ref), np.isnan(got)
+    assert np.array_equal(nan_r, nan_g), f"NaN rows differ: ref {np.nonzero(nan_r)[0][:8]} got {np.nonzero(nan_g)[0][:8]}"
+    assert nan_r.any(), "the test plants infinite and NaN scales"
+    assert_bitwise(got[~nan_r], ref[~nan_r], f"q8k special scales dtype {dtype} K {K}")
+
+
 def _edge_activations(K):
     """The edge-case vector of test_cpu_emulation (zero run, tiny run, one
     huge outlier, subnormals, a sign-flipped scaled block), tiled over K."""

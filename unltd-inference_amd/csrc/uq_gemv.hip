@@ -1054,10 +1054,10 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
                 for (int kb = 0; kb < nblk; kb++) {
                     const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
                     const uint32_t hw = rr[9];
-                    const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                    const float d = __fmul_rn(d8[kb], f16_canon(hw));
                     sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
                     if (F::kMin && k == 0) {
-                        const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                        const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
                         sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
                     }
                 }
@@ -1242,10 +1242,10 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
                     for (int kb = 0; kb < nblk; kb++) {
                         const uint32_t *rr = rec + (((size_t)u * R + r) * nblk + kb) * 10;
                         const uint32_t hw = rr[9];
-                        const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                        const float d = __fmul_rn(d8[kb], f16_canon(hw));
                         sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
                         if (F::kMin && k == 0) {
-                            const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                            const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
                             sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
                         }
                     }
@@ -1383,10 +1383,10 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
                     for (int kb = 0; kb < nblk; kb++) {
                         const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
                         const uint32_t hw = rr[9];
-                        const float d = __fmul_rn(d8[kb], f16_bits_exact(hw & 0xFFFFu));
+                        const float d = __fmul_rn(d8[kb], f16_canon(hw));
                         sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
                         if (F::kMin && k == 0) {
-                            const float dmin = __fmul_rn(f16_bits_exact(hw >> 16), d8[kb]);
+                            const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
                             sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
                         }
                     }
