@@ -39,8 +39,46 @@ __device__ __forceinline__ float f16_bits_exact(uint32_t h) {
 // reference's canonical quiet NaN with the input's sign: four instructions
 // instead of the bit decode.
 __device__ __forceinline__ float f16_canon(uint32_t h) {
-    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
-    return v == v ? v : __uint_as_float((((h >> 15) & 1u) << 31) | 0x7FC00000u);
+    const uint32_t v = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu)));
+    const uint32_t nan = ((h & 0x8000u) << 16) | 0x7FC00000u;
+    return __uint_as_float((h & 0x7FFFu) > 0x7C00u ? nan : v);  // a select, no branch
+}
+
+// The reference's per-row epilogue of the Q8_K dots (quants.rs:343-358 /
+// :402-411) for lane k of one row: over the row's blocks in order,
+// sums += (d8*d) * sumi[k] and (Q4_K) sumf -= (dmin*d8) * minsum, each an
+// f32 multiply and add. rr points at the row's block records (10 dwords:
+// the 8 lane sums, minsum, the f16 d | dmin header). Four blocks' records
+// are read before their products enter the sequential sums; sumf is formed
+// on every lane and used from lane 0.
+template <bool MIN>
+__device__ __forceinline__ void q8k_replay(const uint32_t *rr, const float *d8, int nblk, int k, float &sums,
+                                           float &sumf) {
+    int kb = 0;
+    for (; kb + 4 <= nblk; kb += 4) {
+        uint32_t hw[4];
+        int q[4], mq[4];
+        float dd[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t *b = rr + (kb + u) * 10;
+            hw[u] = b[9];
+            q[u] = (int)b[k];
+            mq[u] = MIN ? (int)b[8] : 0;
+            dd[u] = d8[kb + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            sums = __fadd_rn(sums, __fmul_rn(__fmul_rn(dd[u], f16_canon(hw[u])), (float)q[u]));
+            if (MIN) sumf = __fsub_rn(sumf, __fmul_rn(__fmul_rn(f16_canon(hw[u] >> 16), dd[u]), (float)mq[u]));
+        }
+    }
+    for (; kb < nblk; kb++) {
+        const uint32_t *b = rr + kb * 10;
+        const uint32_t hw = b[9];
+        sums = __fadd_rn(sums, __fmul_rn(__fmul_rn(d8[kb], f16_canon(hw)), (float)(int)b[k]));
+        if (MIN) sumf = __fsub_rn(sumf, __fmul_rn(__fmul_rn(f16_canon(hw >> 16), d8[kb]), (float)(int)b[8]));
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -1051,16 +1051,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
             const int r = lane >> 3, k = lane & 7;
             float sums = 0.0f, sumf = 0.0f;
             if (r < slot) {
-                for (int kb = 0; kb < nblk; kb++) {
-                    const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
-                    const uint32_t hw = rr[9];
-                    const float d = __fmul_rn(d8[kb], f16_canon(hw));
-                    sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
-                    if (F::kMin && k == 0) {
-                        const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
-                        sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
-                    }
-                }
+                q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, d8, nblk, k, sums, sumf);
             }
             float s = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
@@ -1239,16 +1230,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
             for (int u = 0; u < NT; u++) {
                 float sums = 0.0f, sumf = 0.0f;
                 if (r < slot) {
-                    for (int kb = 0; kb < nblk; kb++) {
-                        const uint32_t *rr = rec + (((size_t)u * R + r) * nblk + kb) * 10;
-                        const uint32_t hw = rr[9];
-                        const float d = __fmul_rn(d8[kb], f16_canon(hw));
-                        sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
-                        if (F::kMin && k == 0) {
-                            const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
-                            sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
-                        }
-                    }
+                    q8k_replay<F::kMin>(rec + ((size_t)(u * R + r)) * nblk * 10, d8, nblk, k, sums, sumf);
                 }
                 float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
@@ -1380,16 +1362,7 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
                 const int r = lane >> 3, k = lane & 7;
                 float sums = 0.0f, sumf = 0.0f;
                 if (r < nr) {
-                    for (int kb = 0; kb < nblk; kb++) {
-                        const uint32_t *rr = rec + ((size_t)r * nblk + kb) * 10;
-                        const uint32_t hw = rr[9];
-                        const float d = __fmul_rn(d8[kb], f16_canon(hw));
-                        sums = __fadd_rn(sums, __fmul_rn(d, (float)(int)rr[k]));
-                        if (F::kMin && k == 0) {
-                            const float dmin = __fmul_rn(f16_canon(hw >> 16), d8[kb]);
-                            sumf = __fsub_rn(sumf, __fmul_rn(dmin, (float)(int)rr[8]));
-                        }
-                    }
+                    q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, d8, nblk, k, sums, sumf);
                 }
                 float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
