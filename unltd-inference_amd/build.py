@@ -25,6 +25,10 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # v_dot4_i32_i8 (VOP3P) takes an inline zero accumulator; without this the
+    # compiler prefers v_dot4c_i32_i8, whose tied accumulator costs a v_mov per
+    # chain start
+    "-Xclang", "-target-feature", "-Xclang", "-dot6-insts",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 
@@ -34,7 +38,7 @@ def _run(cmd, verbose):
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
-                    if "packed-fp32-ops" not in l)  # host pass ignores the device feature
+                    if "packed-fp32-ops" not in l and "dot6-insts" not in l)  # host pass ignores the device feature
     if r.returncode != 0:
         raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
     if verbose and out.strip():
