@@ -45,39 +45,42 @@ __device__ __forceinline__ float f16_canon(uint32_t h) {
 }
 
 // The reference's per-row epilogue of the Q8_K dots (quants.rs:343-358 /
-// :402-411) for lane k of one row: over the row's blocks in order,
-// sums += (d8*d) * sumi[k] and (Q4_K) sumf -= (dmin*d8) * minsum, each an
-// f32 multiply and add. rr points at the row's block records (10 dwords:
-// the 8 lane sums, minsum, the f16 d | dmin header). Four blocks' records
-// are read before their products enter the sequential sums; sumf is formed
-// on every lane and used from lane 0.
+// :402-411), in two steps over a wave's block records (10 dwords: the 8
+// lane sums sumi[k], minsum, the f16 d | dmin header).
+//
+// q8k_fold: the per-block factors do not depend on k, so lanes take
+// (row, block) pairs and write, in place, d = d8*d (one f32 multiply,
+// quants.rs:343) over the header and (Q4_K) the whole term
+// (dmin*d8) * minsum (:352-353) over minsum. Rows are `stride` dwords
+// apart; blocks [b0, b1) are folded. The f32 reciprocal gives the exact
+// quotient r = idx / nb: (idx + 0.5) / nb lies at least 0.5/nb from an
+// integer, and two roundings move it by less than (idx + 0.5) 2^-23 / nb,
+// which is smaller for idx < 2^22.
 template <bool MIN>
-__device__ __forceinline__ void q8k_replay(const uint32_t *rr, const float *d8, int nblk, int k, float &sums,
-                                           float &sumf) {
-    int kb = 0;
-    for (; kb + 4 <= nblk; kb += 4) {
-        uint32_t hw[4];
-        int q[4], mq[4];
-        float dd[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t *b = rr + (kb + u) * 10;
-            hw[u] = b[9];
-            q[u] = (int)b[k];
-            mq[u] = MIN ? (int)b[8] : 0;
-            dd[u] = d8[kb + u];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            sums = __fadd_rn(sums, __fmul_rn(__fmul_rn(dd[u], f16_canon(hw[u])), (float)q[u]));
-            if (MIN) sumf = __fsub_rn(sumf, __fmul_rn(__fmul_rn(f16_canon(hw[u] >> 16), dd[u]), (float)mq[u]));
-        }
+__device__ __forceinline__ void q8k_fold(uint32_t *rec, int stride, const float *d8, int nrows, int b0, int b1,
+                                         int lane) {
+    const int nb = b1 - b0, n = nrows * nb;
+    const float rnb = 1.0f / (float)nb;
+    for (int idx = lane; idx < n; idx += 64) {
+        const int r = (int)(((float)idx + 0.5f) * rnb), b = b0 + idx - r * nb;
+        uint32_t *p = rec + (size_t)r * stride + b * 10;
+        const uint32_t h = p[9];
+        const float dd = d8[b];
+        p[9] = __float_as_uint(__fmul_rn(dd, f16_canon(h)));
+        if (MIN) p[8] = __float_as_uint(__fmul_rn(__fmul_rn(f16_canon(h >> 16), dd), (float)(int)p[8]));
     }
-    for (; kb < nblk; kb++) {
+}
+
+// q8k_replay, lane k of one folded row: over the blocks in order,
+// sums += d * sumi[k] (f32 multiply, then add) and (Q4_K) sumf -= the
+// folded min term; sumf is formed on every lane and used from lane 0.
+template <bool MIN>
+__device__ __forceinline__ void q8k_replay(const uint32_t *rr, int nblk, int k, float &sums, float &sumf) {
+#pragma unroll 4
+    for (int kb = 0; kb < nblk; kb++) {
         const uint32_t *b = rr + kb * 10;
-        const uint32_t hw = b[9];
-        sums = __fadd_rn(sums, __fmul_rn(__fmul_rn(d8[kb], f16_canon(hw)), (float)(int)b[k]));
-        if (MIN) sumf = __fsub_rn(sumf, __fmul_rn(__fmul_rn(f16_canon(hw >> 16), d8[kb]), (float)(int)b[8]));
+        sums = __fadd_rn(sums, __fmul_rn(__uint_as_float(b[9]), (float)(int)b[k]));
+        if (MIN) sumf = __fsub_rn(sumf, __uint_as_float(b[8]));
     }
 }
 

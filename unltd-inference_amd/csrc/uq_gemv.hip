@@ -1048,11 +1048,11 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
             // sums[k] += d*sumi[k] over the blocks in order; k = 0 also
             // replays sumf -= dmin*minsum; then s = sumf + sums[0] + ... + sums[7].
             __builtin_amdgcn_wave_barrier();
+            q8k_fold<F::kMin>(rec, nblk * 10, d8, slot, 0, nblk, lane);
+            __builtin_amdgcn_wave_barrier();
             const int r = lane >> 3, k = lane & 7;
             float sums = 0.0f, sumf = 0.0f;
-            if (r < slot) {
-                q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, d8, nblk, k, sums, sumf);
-            }
+            if (r < slot) q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, nblk, k, sums, sumf);
             float s = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) s = __fadd_rn(s, __shfl(sums, (lane & ~7) + kk));
@@ -1224,14 +1224,16 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
             // order (k = 0 also sumf -= dmin*minsum), then
             // s = sumf + sums[0] + ... + sums[7]
             __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < NT; u++)
+                q8k_fold<F::kMin>(rec + (size_t)u * R * nblk * 10, nblk * 10, d8, slot, 0, nblk, lane);
+            __builtin_amdgcn_wave_barrier();
             const int r = lane >> 3, k = lane & 7;
             float out[NT];
 #pragma unroll
             for (int u = 0; u < NT; u++) {
                 float sums = 0.0f, sumf = 0.0f;
-                if (r < slot) {
-                    q8k_replay<F::kMin>(rec + ((size_t)(u * R + r)) * nblk * 10, d8, nblk, k, sums, sumf);
-                }
+                if (r < slot) q8k_replay<F::kMin>(rec + ((size_t)(u * R + r)) * nblk * 10, nblk, k, sums, sumf);
                 float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
                 for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
@@ -1355,15 +1357,16 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
         }
         slot++;
         if (slot == R || i + 1 == nmax) {
-            __syncthreads();  // every slice's records of these rows are written
             const int nr = min(slot, nrows - (i + 1 - slot));  // rows of this group in the batch
+            // each slice folds the block factors into its own records
+            __builtin_amdgcn_wave_barrier();
+            if (nr > 0) q8k_fold<F::kMin>(rec, nblk * 10, d8, nr, 16 * sl, min(nblk, 16 * sl + 16), lane);
+            __syncthreads();  // every slice's records of these rows are written
             if (sl == 0 && nr > 0) {
                 // epilogue (quants.rs:343-358 / :402-411), as gemv_q8k_kernel
                 const int r = lane >> 3, k = lane & 7;
                 float sums = 0.0f, sumf = 0.0f;
-                if (r < nr) {
-                    q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, d8, nblk, k, sums, sumf);
-                }
+                if (r < nr) q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, nblk, k, sums, sumf);
                 float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
                 for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
