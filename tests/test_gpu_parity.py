@@ -201,11 +201,14 @@ def _gemv_runs_generic(dtype, K):
                                        (S.Q4_K, 1024, 301), (S.Q6_K, 2048, 33),
                                        (S.Q4_K, 8192, 1000), (S.Q6_K, 12288, 5000), (S.Q6_K, 4352, 77),
                                        (S.Q4_K, 16384, 300), (S.Q6_K, 16384, 77), (S.Q4_K, 13312, 100),
-                                       (S.Q6_K, 20480, 50)])
+                                       (S.Q6_K, 20480, 50),
+                                       (S.Q4_K, 4096, 65636), (S.Q6_K, 3584, 50001), (S.Q6_K, 2048, 50000)])
 def test_gemv_quant_q8k_bit_exact(dtype, K, N):
     """Every kernel of the path: rows streamed with one or three tasks per
     lane, the K-split kernel (two to five slices; a last slice of one or four
-    blocks; row groups with uneven or no rows in the last workgroups)."""
+    blocks; row groups with uneven or no rows in the last workgroups), and
+    long launches (16 or more rows per wave, the rotating wave priority)
+    beside the full head."""
     log(f"gemv_quant_q8k dtype={dtype} K={K} N={N}")
     w = S.weights(dtype, N, K, seed=K * 17 + N + dtype)
     x = S.activations(K, seed=N * 3 + dtype)
