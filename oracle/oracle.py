@@ -393,3 +393,105 @@ def rope_imrope(x, n_rot: int, theta_scale: float, pos: int) -> np.ndarray:
     y = _f32(x).copy()
     _ok(_fn("or_rope_imrope", [_P, _S, _S, C.c_double, _S])(_p(y), len(y), n_rot, theta_scale, pos), "rope_imrope")
     return y
+
+
+# ------------------------------------------------ one decode layer
+# Qwen35Forward::recr_layer, attn_layer and ffn
+# (crates/unltd-generation/src/qwen35_forward.rs:333-768), step for step,
+# composed from the functions above. cfg carries the uq_qwen35_dims field
+# names; w maps a projection name to (bytes, dtype) and a vector name to an
+# f32 array. The f32 element-wise additions and products are numpy float32
+# operations (each one IEEE rounding, as the reference's).
+
+def _q8k(w, x, dim_in: int, dim_out: int, nthreads: int) -> np.ndarray:
+    out = np.zeros(dim_out, np.float32)
+    gemv_quant_q8k(out, x, w[0], dim_in, dim_out, w[1], nthreads=nthreads)
+    return out
+
+
+def layer_ffn(cfg, w, residual, nodes: dict, nthreads: int = 1) -> np.ndarray:
+    """ffn (qwen35_forward.rs:713-768): f = ffn_down . swiglu(ffn_gate . p, ffn_up . p),
+    p = rmsnorm(residual, post_attention_norm)."""
+    n, nff = cfg.n_embd, cfg.n_ff
+    p = rmsnorm(residual, w["post_attention_norm"], cfg.rms_eps)
+    g = _q8k(w["ffn_gate"], p, n, nff, nthreads)
+    u = _q8k(w["ffn_up"], p, n, nff, nthreads)
+    sw = swiglu(g, u)
+    f = _q8k(w["ffn_down"], sw, nff, n, nthreads)
+    nodes.update(post_norm=p, ffn_gate=g, ffn_up=u, ffn_swiglu=sw, ffn_out=f)
+    return f
+
+
+def recr_layer(cfg, w, ring: np.ndarray, state: np.ndarray, x_in, nthreads: int = 1):
+    """recr_layer (qwen35_forward.rs:333-543) for one token. ring
+    [conv_kernel - 1][channels] and state [n_v][hd][hd] are updated in place,
+    as the session's conv ring and GDN state. Returns (l_out, nodes)."""
+    n, eps = cfg.n_embd, cfg.rms_eps
+    nqk, nv, hd, ck = cfg.n_qk_heads, cfg.n_v_heads, cfg.head_dim_linear, cfg.conv_kernel
+    ch = 2 * nqk * hd + nv * hd
+    x_in = _f32(x_in)
+    nodes = {}
+    x = rmsnorm(x_in, w["attn_norm"], eps)                                 # :352-360
+    qkv = _q8k(w["attn_qkv"], x, n, ch, nthreads)                          # :363-372
+    z = _q8k(w["attn_gate"], x, n, nv * hd, nthreads)                      # :373-381
+    beta_raw = _q8k(w["ssm_beta"], x, n, nv, nthreads)                     # :386-394
+    alpha = _q8k(w["ssm_alpha"], x, n, nv, nthreads)                       # :395-403
+    beta = sigmoid(beta_raw)                                               # :405
+    sp = softplus(alpha + w["ssm_dt_bias"])                                # :413-416
+    gate = sp * w["ssm_a"]                                                 # :417-419
+    win = np.concatenate([ring.reshape(-1), qkv])                          # :427-431
+    kernel = np.ascontiguousarray(_f32(w["ssm_conv1d"]).reshape(ch, ck).T).reshape(-1)  # :441-446
+    conv = ssm_conv(win, kernel, ck, ch)                                   # :447
+    ring[:-1] = ring[1:].copy()                                            # :449-450
+    ring[-1] = qkv
+    mix = silu(conv)                                                       # :454
+    qc = l2_norm_rows(mix[:nqk * hd], hd, eps)                             # :463
+    kc = l2_norm_rows(mix[nqk * hd:2 * nqk * hd], hd, eps)                 # :464
+    vc = mix[2 * nqk * hd:]
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))                      # :472
+    out = np.zeros(nv * hd, np.float32)
+    for h in range(nv):                                                    # :474-491
+        qk = h % nqk
+        st, o = gdn_fused_step(state[h].reshape(-1), qc[qk * hd:(qk + 1) * hd], kc[qk * hd:(qk + 1) * hd],
+                               vc[h * hd:(h + 1) * hd], float(gate[h]), float(beta[h]), float(scale))
+        state[h] = st.reshape(hd, hd)
+        out[h * hd:(h + 1) * hd] = o
+    y = np.concatenate([rmsnorm(out[h * hd:(h + 1) * hd], w["ssm_norm"], eps) for h in range(nv)])  # :495-505
+    y = y * silu(z)                                                        # :507-511
+    attn_out = _q8k(w["ssm_out"], y, nv * hd, n, nthreads)                 # :514-521
+    residual = x_in + attn_out                                             # :524-527
+    nodes.update(attn_norm=x, qkv=qkv, z=z, beta_raw=beta_raw, alpha=alpha, beta=beta, a_softplus=sp, gate=gate,
+                 conv_raw=conv, conv_silu=np.concatenate([qc, kc, vc]), gdn_out=out, final=y, attn_out=attn_out,
+                 residual=residual)
+    f = layer_ffn(cfg, w, residual, nodes, nthreads)                      # :530
+    return residual + f, nodes                                             # :533-536
+
+
+def attn_layer(cfg, w, k_cache: np.ndarray, v_cache: np.ndarray, pos: int, x_in, nthreads: int = 1):
+    """attn_layer (qwen35_forward.rs:546-710) for one token at pos. The
+    caches [n_ctx][n_head_kv * head_dim] get row pos. Returns (l_out, nodes)."""
+    n, eps = cfg.n_embd, cfg.rms_eps
+    nh, nkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+    x_in = _f32(x_in)
+    nodes = {}
+    x = rmsnorm(x_in, w["attn_norm"], eps)                                 # :563-571
+    qfull = _q8k(w["attn_q"], x, n, 2 * nh * hd, nthreads)                 # :573-582
+    q = np.concatenate([rmsnorm(qfull[2 * h * hd:2 * h * hd + hd], w["attn_q_norm"], eps) for h in range(nh)])
+    gate = np.concatenate([qfull[2 * h * hd + hd:2 * (h + 1) * hd] for h in range(nh)])  # :583-600
+    k = _q8k(w["attn_k"], x, n, nkv * hd, nthreads)                        # :603-610
+    kn = np.concatenate([rmsnorm(k[i * hd:(i + 1) * hd], w["attn_k_norm"], eps) for i in range(nkv)])  # :611-623
+    v = _q8k(w["attn_v"], x, n, nkv * hd, nthreads)                        # :625-632
+    q = np.concatenate([rope_imrope(q[h * hd:(h + 1) * hd], cfg.n_rot, cfg.theta_scale, pos)
+                        for h in range(nh)])                               # :634-639
+    kn = np.concatenate([rope_imrope(kn[i * hd:(i + 1) * hd], cfg.n_rot, cfg.theta_scale, pos)
+                         for i in range(nkv)])                             # :640-642
+    k_cache[pos] = kn                                                      # :643-645
+    v_cache[pos] = v
+    attn, soft = attn_decode(q, k_cache[:pos + 1], v_cache[:pos + 1], pos + 1, nh, nkv, hd, cfg.kq_scale)  # :647-675
+    gated = attn * sigmoid(gate)                                           # :677-684
+    attn_out = _q8k(w["attn_output"], gated, nh * hd, n, nthreads)         # :686-693
+    residual = x_in + attn_out                                             # :696-699
+    nodes.update(attn_norm=x, qfull=qfull, k_raw=k, q=q, k_row=kn, v_row=v, attn=attn, soft=soft, gated=gated,
+                 attn_out=attn_out, residual=residual)
+    f = layer_ffn(cfg, w, residual, nodes, nthreads)                      # :700
+    return residual + f, nodes                                             # :701-704

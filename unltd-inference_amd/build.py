@@ -2,7 +2,7 @@
 
     python unltd-inference_amd/build.py
 
-libuq.so: every csrc/*.hip plus uq_abi.cpp, uq_gguf.cpp and uq_ops_abi.cpp, compiled by hipcc for gfx950
+libuq.so: every csrc/*.hip plus uq_abi.cpp, uq_gguf.cpp, uq_ops_abi.cpp and uq_layer.cpp, compiled by hipcc for gfx950
   only, -O3, FP contraction off (FMAs are written explicitly), f32
   denormals kept, packed-FP32 instructions disabled.
 libuq_emu.so: csrc/uq_emu.cpp with g++: the kernels' per-lane code run on
@@ -47,7 +47,7 @@ def _run(cmd, verbose):
 
 def build_lib(verbose: bool = False) -> str:
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + [os.path.join(CSRC, f)
-                                                              for f in ("uq_abi.cpp", "uq_gguf.cpp", "uq_ops_abi.cpp")]
+                                                              for f in ("uq_abi.cpp", "uq_gguf.cpp", "uq_ops_abi.cpp", "uq_layer.cpp")]
     tmp = LIB + ".tmp"
     _run(["hipcc", *HIPCC_FLAGS, "-x", "hip", *srcs, "-o", tmp], verbose)
     os.replace(tmp, LIB)

@@ -226,8 +226,11 @@ __global__ __launch_bounds__(64 * NW) UQ_GEMV_OCC void gemv_kernel(const Segs S,
 // loads of the S-1 later rows (NI instructions each) and the y stores made
 // in between; at the tail, where fewer rows follow, it waits for all.
 template <class F> struct Stage;
+// RP: LDS bytes of one row of up to 16 blocks (a ring slot of the K <= 4096
+// streaming kernel); a row's 1 KB loads land at 1024 m within it.
 template <> struct Stage<Q6K> {
     static constexpr int BC = 14, BP = 224, BB = kBQ6K;  // chunks per block, LDS pitch, block bytes
+    static constexpr int RP = 16 * BP;
     __device__ static Q6KFrag frag(const uint8_t *blk, const Q6K::LC &c) {
         Q6KFrag f;
         f.a = *(const u4 *)(blk + 64 * c.h + 16 * c.u);
@@ -242,6 +245,7 @@ template <> struct Stage<Q6K> {
 };
 template <> struct Stage<Q4K> {
     static constexpr int BC = 9, BP = 144, BB = kBQ4K;
+    static constexpr int RP = 16 * BP;
     __device__ static Q4K::Frag frag(const uint8_t *blk, const Q4K::LC &c) {
         Q4K::Frag f;
         f.h = *(const u4 *)blk;
@@ -303,7 +307,8 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
     const typename F::LC c = F::lane_consts(lane);
     const int N = Sg.start[Sg.n];
     const int nrows = wave < N ? (N - 1 - wave) / nwave + 1 : 0;
-    uint8_t *ring = lds + ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)wv * S * UNIT * 1024;
+    constexpr int UP = NT * St::RP;    // LDS bytes per row unit
+    uint8_t *ring = lds + ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)wv * S * UP;
 
     uint32_t goff[NI];
     bool gval[NI];
@@ -322,7 +327,7 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
                 const uint8_t *row = (t == 0 ? Sg.w[sg] : Sg.w2[sg]) + off;
 #pragma unroll
                 for (int m = 0; m < NI; m++)
-                    if (gval[m]) lds_dma16(row + goff[m], ring + (slot * UNIT + t * NI + m) * 1024);
+                    if (gval[m]) lds_dma16(row + goff[m], ring + slot * UP + t * St::RP + m * 1024);
             }
         }
     };
@@ -361,10 +366,10 @@ gemv_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restri
             }
             // read only by lanes with a task: no zero fill (it cost a move per dword per row)
             typename F::Frag f, f2;
-            const uint8_t *b0 = myblk + (r % S) * UNIT * 1024;
+            const uint8_t *b0 = myblk + (r % S) * UP;
             if (lane < ntask) {
                 f = St::frag(b0, c);
-                if (PAIR) f2 = St::frag(b0 + NI * 1024, c);
+                if (PAIR) f2 = St::frag(b0 + St::RP, c);
             }
             // the slot's LDS reads have returned before its next loads land in it
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -766,7 +771,7 @@ template <class F, int NI, bool PAIR, bool MULTI>
 hipError_t launch_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
     constexpr int SNW = PAIR ? UQ_STREAM_PAIR_NW : StreamShape<F>::NW, SS = PAIR ? UQ_STREAM_PAIR_S : StreamShape<F>::S;
     const int N = S.start[S.n];
-    const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * (PAIR ? 2 : 1) * NI * 1024;
+    const size_t l = ((x_lds_bytes<F>(K) + 15) & ~(size_t)15) + (size_t)SNW * SS * (PAIR ? 2 : 1) * Stage<F>::RP;
     const void *k = (const void *)gemv_stream_kernel<F, NI, SNW, SS, PAIR, MULTI>;
     const hipError_t e = allow_lds(k, l);
     if (e != hipSuccess) return e;

@@ -1,0 +1,289 @@
+// Device-resident Qwen3.5 layers (include/uq_layer.h): the per-token steps
+// of Qwen35Forward::recr_layer and attn_layer with their FFN
+// (crates/unltd-generation/src/qwen35_forward.rs:333-768), issued as a
+// sequence of this library's launches on the caller's stream. The
+// projections run as gemv_quant_q8k (the projections of one input share a
+// batched launch per format, bit-identical to separate ones); the glue is
+// uq_ops.hip. No allocation, no host copy, so a step can be captured in a
+// HIP graph.
+#include <cmath>
+#include <climits>
+
+#include "../../include/uq_layer.h"
+#include "../../include/uq_ops.h"
+#include "uq_internal.h"
+
+using uq::set_error;
+
+namespace {
+
+struct Dims {
+    size_t n, nff, nqk, nv, hd, ck, ch, nh, nkv, ahd;
+};
+
+// Node sizes in floats, in uq_layer_node order; the workspace holds them
+// one after another, each at a 64-float (256-byte) boundary.
+size_t node_count(const Dims &D, size_t n_ctx_max, int node) {
+    switch (node) {
+        case UQ_NODE_ATTN_NORM: return D.n;
+        case UQ_NODE_Z: return D.nv * D.hd;
+        case UQ_NODE_BETA_RAW:
+        case UQ_NODE_ALPHA:
+        case UQ_NODE_BETA:
+        case UQ_NODE_A_SOFTPLUS:
+        case UQ_NODE_GATE: return D.nv;
+        case UQ_NODE_CONV_RAW:
+        case UQ_NODE_CONV_SILU: return D.ch;
+        case UQ_NODE_GDN_OUT:
+        case UQ_NODE_FINAL: return D.nv * D.hd;
+        case UQ_NODE_QFULL: return 2 * D.nh * D.ahd;
+        case UQ_NODE_K_RAW: return D.nkv * D.ahd;
+        case UQ_NODE_Q:
+        case UQ_NODE_ATTN:
+        case UQ_NODE_GATED: return D.nh * D.ahd;
+        case UQ_NODE_SOFT: return D.nh * n_ctx_max;
+        case UQ_NODE_ATTN_OUT:
+        case UQ_NODE_RESIDUAL:
+        case UQ_NODE_POST_NORM: return D.n;
+        case UQ_NODE_FFN_GATE:
+        case UQ_NODE_FFN_UP:
+        case UQ_NODE_FFN_SWIGLU: return D.nff;
+        case UQ_NODE_FFN_OUT: return D.n;
+        default: return 0;
+    }
+}
+
+size_t node_offset(const Dims &D, size_t n_ctx_max, int node) {
+    size_t off = 0;
+    for (int i = 0; i < node; i++) off += (node_count(D, n_ctx_max, i) + 63) & ~(size_t)63;
+    return off;
+}
+
+// The dims' own consistency (UQ_ERR_ARG), as Qwen35Config::validate and the
+// forward's shape assumptions require.
+uq_status check_dims(const char *fn, const uq_qwen35_dims *d, Dims *D) {
+    if (!d) return set_error(UQ_ERR_ARG, "%s: null dims", fn);
+    Dims r;
+    r.n = d->n_embd;
+    r.nff = d->n_ff;
+    r.nqk = d->n_qk_heads;
+    r.nv = d->n_v_heads;
+    r.hd = d->head_dim_linear;
+    r.ck = d->conv_kernel;
+    r.ch = 2 * r.nqk * r.hd + r.nv * r.hd;
+    r.nh = d->n_head;
+    r.nkv = d->n_head_kv;
+    r.ahd = d->head_dim;
+    const size_t big = (size_t)1 << 26;
+    if (!r.n || !r.nff || !r.nqk || !r.nv || !r.hd || !r.nh || !r.nkv || !r.ahd || r.n > big || r.nff > big ||
+        r.ch > big)
+        return set_error(UQ_ERR_ARG, "%s: a dimension is zero or above 2^26", fn);
+    if (r.ck < 2 || r.ck > 9) return set_error(UQ_ERR_ARG, "%s: conv_kernel %zu outside 2..9", fn, r.ck);
+    if (r.nv % r.nqk || r.nv * r.hd != r.n)
+        return set_error(UQ_ERR_ARG, "%s: n_v_heads %zu * head_dim_linear %zu != n_embd %zu or not a multiple of "
+                                     "n_qk_heads %zu", fn, r.nv, r.hd, r.n, r.nqk);
+    if (r.nh % r.nkv || r.nh * r.ahd != r.n || !uq::attn_shape_ok((int)r.ahd, (int)(r.nh / r.nkv)))
+        return set_error(UQ_ERR_ARG, "%s: attention heads %zu / %zu of dim %zu do not fit n_embd %zu", fn, r.nh,
+                         r.nkv, r.ahd, r.n);
+    if (d->n_rot % 2 || d->n_rot > r.ahd)
+        return set_error(UQ_ERR_ARG, "%s: n_rot %zu not even or above head_dim", fn, d->n_rot);
+    if (D) *D = r;
+    return UQ_OK;
+}
+
+uq_weights_s *wh(uq_weights w) { return (w && w->magic == UQ_WEIGHTS_MAGIC) ? w : nullptr; }
+
+// A projection of the forward: a q8k-capable handle of the stated shape.
+uq_status check_proj(const char *fn, const char *name, uq_weights w, size_t dim_in, size_t dim_out) {
+    uq_weights_s *p = wh(w);
+    if (!p) return set_error(UQ_ERR_ARG, "%s: invalid handle for %s", fn, name);
+    if (p->dtype != UQ_Q4_K && p->dtype != UQ_Q6_K)
+        return set_error(UQ_ERR_DTYPE, "%s: %s is not Q4_K or Q6_K", fn, name);
+    if (p->dim_in != dim_in || p->dim_out != dim_out)
+        return set_error(UQ_ERR_LEN, "%s: %s is %zu x %zu, expected %zu x %zu", fn, name, p->dim_out, p->dim_in,
+                         dim_out, dim_in);
+    return UQ_OK;
+}
+
+uq_status hip_st(hipError_t e, const char *what) { return e == hipSuccess ? UQ_OK : uq::hip_error(e, what); }
+
+#define UQ_TRY(expr)                      \
+    do {                                  \
+        const uq_status st_ = (expr);     \
+        if (st_ != UQ_OK) return st_;     \
+    } while (0)
+
+// q8k projections of one input: one batched launch per dtype (a batch
+// takes tensors of one format; the outputs are the same either way).
+uq_status project_q8k(const uq_weights *w, float *const *y, int n, const float *x, void *stream) {
+    const uq_dtype first = wh(w[0])->dtype;
+    uq_weights a[8], b[8];
+    float *ya[8], *yb[8];
+    int na = 0, nb = 0;
+    for (int i = 0; i < n; i++) {
+        if (wh(w[i])->dtype == first) {
+            a[na] = w[i];
+            ya[na++] = y[i];
+        } else {
+            b[nb] = w[i];
+            yb[nb++] = y[i];
+        }
+    }
+    UQ_TRY(uq_gemv_q8k_batch(a, ya, na, x, stream));
+    return nb ? uq_gemv_q8k_batch(b, yb, nb, x, stream) : UQ_OK;
+}
+
+// post_attention_norm + FFN + l_out (ffn, :713-768, and :534-536 / :702-704)
+uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, uq_weights g, uq_weights u, uq_weights dn,
+                   const float *post_norm, float *ws, size_t nctx, float *l_out, hipStream_t s) {
+    auto at = [&](int node) { return ws + node_offset(D, nctx, node); };
+    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_POST_NORM), at(UQ_NODE_RESIDUAL), post_norm, (int)D.n, 1, d->rms_eps,
+                                     s), fn));
+    UQ_TRY(uq_ffn_swiglu_q8k(g, u, dn, at(UQ_NODE_POST_NORM), at(UQ_NODE_FFN_GATE), at(UQ_NODE_FFN_UP),
+                             at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT), s));
+    return hip_st(uq::launch_add(l_out, at(UQ_NODE_RESIDUAL), at(UQ_NODE_FFN_OUT), D.n, s), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t uq_layer_ws_floats(const uq_qwen35_dims *d, size_t n_ctx_max) {
+    Dims D;
+    if (check_dims("layer_ws_floats", d, &D) != UQ_OK) return 0;
+    return node_offset(D, n_ctx_max, UQ_NODE_COUNT);
+}
+
+uq_status uq_layer_node_at(const uq_qwen35_dims *d, size_t n_ctx_max, int node, size_t *offset, size_t *count) {
+    Dims D;
+    UQ_TRY(check_dims("layer_node_at", d, &D));
+    if (node < 0 || node >= UQ_NODE_COUNT || !offset || !count)
+        return set_error(UQ_ERR_ARG, "layer_node_at: node %d out of range or null output", node);
+    *offset = node_offset(D, n_ctx_max, node);
+    *count = node_count(D, n_ctx_max, node);
+    return UQ_OK;
+}
+
+uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, float *d_conv_win, float *d_state,
+                              const float *d_x_in, float *d_l_out, float *d_ws, size_t ws_floats, void *stream) {
+    const char *fn = "gdn_layer_step_d";
+    Dims D;
+    UQ_TRY(check_dims(fn, d, &D));
+    if (!w || !d_conv_win || !d_state || !d_x_in || !d_l_out || !d_ws || !w->attn_norm || !w->ssm_dt_bias ||
+        !w->ssm_a || !w->ssm_conv1d || !w->ssm_norm || !w->post_attention_norm)
+        return set_error(UQ_ERR_ARG, "%s: null pointer", fn);
+    if (ws_floats < node_offset(D, 0, UQ_NODE_COUNT))
+        return set_error(UQ_ERR_ARG, "%s: workspace of %zu floats below %zu", fn, ws_floats,
+                         node_offset(D, 0, UQ_NODE_COUNT));
+    UQ_TRY(check_proj(fn, "attn_qkv", w->attn_qkv, D.n, D.ch));
+    UQ_TRY(check_proj(fn, "attn_gate", w->attn_gate, D.n, D.nv * D.hd));
+    UQ_TRY(check_proj(fn, "ssm_beta", w->ssm_beta, D.n, D.nv));
+    UQ_TRY(check_proj(fn, "ssm_alpha", w->ssm_alpha, D.n, D.nv));
+    UQ_TRY(check_proj(fn, "ssm_out", w->ssm_out, D.nv * D.hd, D.n));
+    UQ_TRY(check_proj(fn, "ffn_gate", w->ffn_gate, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_up", w->ffn_up, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_down", w->ffn_down, D.nff, D.n));
+    const hipStream_t s = (hipStream_t)stream;
+    auto at = [&](int node) { return d_ws + node_offset(D, 0, node); };
+    const int hd = (int)D.hd, nv = (int)D.nv, nqk = (int)D.nqk, ch = (int)D.ch;
+    float *qkv = d_conv_win + (D.ck - 1) * D.ch;  // the window's last row
+
+    // 1) attn_norm (:352-360)
+    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_ATTN_NORM), d_x_in, w->attn_norm, (int)D.n, 1, d->rms_eps, s), fn));
+    // 2-3) qkv, z, beta, alpha: four q8k projections of x, one launch per format (:363-403)
+    {
+        const uq_weights ws4[4] = {w->attn_qkv, w->attn_gate, w->ssm_beta, w->ssm_alpha};
+        float *const ys[4] = {qkv, at(UQ_NODE_Z), at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA)};
+        UQ_TRY(project_q8k(ws4, ys, 4, at(UQ_NODE_ATTN_NORM), stream));
+    }
+    // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419)
+    UQ_TRY(hip_st(uq::launch_gdn_gates(at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), w->ssm_dt_bias, w->ssm_a,
+                                       at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s), fn));
+    // 4) depthwise conv over [ring; qkv], the ring's shift, silu (:427-454)
+    UQ_TRY(hip_st(uq::launch_ssm_conv(at(UQ_NODE_CONV_RAW), d_conv_win, w->ssm_conv1d, (int)D.ck, ch, 1, s, true),
+                  fn));
+    UQ_TRY(hip_st(uq::launch_conv_shift(d_conv_win, (int)D.ck, ch, s), fn));
+    UQ_TRY(hip_st(uq::launch_unary(1, at(UQ_NODE_CONV_RAW), D.ch, at(UQ_NODE_CONV_SILU), s), fn));
+    // q and k parts l2-normalised per head (:463-464)
+    float *qc = at(UQ_NODE_CONV_SILU), *kc = qc + D.nqk * D.hd, *vc = kc + D.nqk * D.hd;
+    UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
+    // 5) gdn_fused_step per v head, q/k head h % n_qk, scale on the output (:470-492)
+    const float scale = 1.0f / sqrtf((float)D.hd);
+    UQ_TRY(hip_st(uq::launch_gdn_step(d_state, at(UQ_NODE_GDN_OUT), qc, kc, vc, at(UQ_NODE_GATE), at(UQ_NODE_BETA), hd,
+                                      nv, scale, s, nqk),
+                  fn));
+    // 6) rmsnorm per head with ssm_norm, times silu(z) (:495-511)
+    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_FINAL), at(UQ_NODE_GDN_OUT), w->ssm_norm, hd, nv, d->rms_eps, s), fn));
+    UQ_TRY(hip_st(uq::launch_mul_act(1, at(UQ_NODE_FINAL), at(UQ_NODE_FINAL), at(UQ_NODE_Z), (int)(D.nv * D.hd), 0,
+                                     D.nv * D.hd, s),
+                  fn));
+    // 7) ssm_out + residual (:514-527)
+    UQ_TRY(uq_gemv_q8k(w->ssm_out, at(UQ_NODE_FINAL), at(UQ_NODE_ATTN_OUT), stream));
+    UQ_TRY(hip_st(uq::launch_add(at(UQ_NODE_RESIDUAL), d_x_in, at(UQ_NODE_ATTN_OUT), D.n, s), fn));
+    // 8) FFN and l_out (:530-536)
+    return ffn_tail(fn, D, d, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, 0, d_l_out, s);
+}
+
+uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w, float *d_k_cache,
+                               float *d_v_cache, size_t n_ctx_max, size_t pos, const float *d_x_in, float *d_l_out,
+                               float *d_ws, size_t ws_floats, void *stream) {
+    const char *fn = "attn_layer_step_d";
+    Dims D;
+    UQ_TRY(check_dims(fn, d, &D));
+    if (!w || !d_k_cache || !d_v_cache || !d_x_in || !d_l_out || !d_ws || !w->attn_norm || !w->attn_q_norm ||
+        !w->attn_k_norm || !w->post_attention_norm)
+        return set_error(UQ_ERR_ARG, "%s: null pointer", fn);
+    if (pos >= n_ctx_max)
+        return set_error(UQ_ERR_ARG, "%s: context full: position %zu, n_ctx_max %zu", fn, pos, n_ctx_max);
+    if (n_ctx_max > (size_t)uq::softmax_max_len() || n_ctx_max * D.nh > ((size_t)1 << 31))
+        return set_error(UQ_ERR_ARG, "%s: n_ctx_max %zu above the attention's limit", fn, n_ctx_max);
+    if (ws_floats < node_offset(D, n_ctx_max, UQ_NODE_COUNT))
+        return set_error(UQ_ERR_ARG, "%s: workspace of %zu floats below %zu", fn, ws_floats,
+                         node_offset(D, n_ctx_max, UQ_NODE_COUNT));
+    const size_t kv_len = D.nkv * D.ahd;
+    UQ_TRY(check_proj(fn, "attn_q", w->attn_q, D.n, 2 * D.nh * D.ahd));
+    UQ_TRY(check_proj(fn, "attn_k", w->attn_k, D.n, kv_len));
+    UQ_TRY(check_proj(fn, "attn_v", w->attn_v, D.n, kv_len));
+    UQ_TRY(check_proj(fn, "attn_output", w->attn_output, D.nh * D.ahd, D.n));
+    UQ_TRY(check_proj(fn, "ffn_gate", w->ffn_gate, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_up", w->ffn_up, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_down", w->ffn_down, D.nff, D.n));
+    const hipStream_t s = (hipStream_t)stream;
+    auto at = [&](int node) { return d_ws + node_offset(D, n_ctx_max, node); };
+    const int ahd = (int)D.ahd, nh = (int)D.nh, nkv = (int)D.nkv;
+    float *krow = d_k_cache + pos * kv_len, *vrow = d_v_cache + pos * kv_len;
+
+    // 1) attn_norm (:563-571)
+    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_ATTN_NORM), d_x_in, w->attn_norm, (int)D.n, 1, d->rms_eps, s), fn));
+    // 2-3) q|gate, k and v: three q8k projections of x, one launch per format; v lands
+    // in its cache row (it has no norm, :625-632)
+    {
+        const uq_weights ws3[3] = {w->attn_q, w->attn_k, w->attn_v};
+        float *const ys[3] = {at(UQ_NODE_QFULL), at(UQ_NODE_K_RAW), vrow};
+        UQ_TRY(project_q8k(ws3, ys, 3, at(UQ_NODE_ATTN_NORM), stream));
+    }
+    // q: rmsnorm of each head's first half (:585-599); k: rmsnorm per kv
+    // head, into the cache row (:611-623)
+    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_Q), ahd, at(UQ_NODE_QFULL), 2 * ahd, w->attn_q_norm, ahd, nh,
+                                          d->rms_eps, s),
+                  fn));
+    UQ_TRY(hip_st(uq::launch_rmsnorm(krow, at(UQ_NODE_K_RAW), w->attn_k_norm, ahd, nkv, d->rms_eps, s), fn));
+    // 4) IMROPE on q and on the new k row (:634-642)
+    UQ_TRY(hip_st(uq::launch_rope_imrope(at(UQ_NODE_Q), nh, ahd, (int)d->n_rot, d->theta_scale, pos, s), fn));
+    UQ_TRY(hip_st(uq::launch_rope_imrope(krow, nkv, ahd, (int)d->n_rot, d->theta_scale, pos, s), fn));
+    // 5) causal attention over rows 0..pos (:647-675)
+    UQ_TRY(hip_st(uq::launch_attn_decode(at(UQ_NODE_ATTN), at(UQ_NODE_SOFT), at(UQ_NODE_Q), d_k_cache, d_v_cache,
+                                         (int)pos + 1, nkv, ahd, nh / nkv, d->kq_scale, s),
+                  fn));
+    // 6) attn * sigmoid(gate), gate the second half of each head's q row (:677-684)
+    UQ_TRY(hip_st(uq::launch_mul_act(0, at(UQ_NODE_GATED), at(UQ_NODE_ATTN), at(UQ_NODE_QFULL) + ahd, ahd, 2 * ahd,
+                                     D.nh * D.ahd, s),
+                  fn));
+    // 7) attn_output + residual (:686-699), FFN and l_out (:700-704)
+    UQ_TRY(uq_gemv_q8k(w->attn_output, at(UQ_NODE_GATED), at(UQ_NODE_ATTN_OUT), stream));
+    UQ_TRY(hip_st(uq::launch_add(at(UQ_NODE_RESIDUAL), d_x_in, at(UQ_NODE_ATTN_OUT), D.n, s), fn));
+    return ffn_tail(fn, D, d, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, n_ctx_max, d_l_out,
+                    s);
+}
+
+}  // extern "C"

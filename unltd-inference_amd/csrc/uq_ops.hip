@@ -75,13 +75,15 @@ __device__ float seq_sum_f32(const float *__restrict__ sq_src, int n, double S, 
     return r;
 }
 
-// rmsnorm (kernels.rs:61-78), one workgroup per row of n.
+// rmsnorm (kernels.rs:61-78), one workgroup per row of n; rows xs (input)
+// and ys (output) floats apart.
 __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
-                                                          const float *__restrict__ w, int n, float eps) {
+                                                          const float *__restrict__ w, int n, float eps, int xs,
+                                                          int ys) {
     __shared__ double red[OPS_TPB / 64];
     __shared__ float bc;
-    const float *xr = x + (size_t)blockIdx.x * n;
-    float *yr = out + (size_t)blockIdx.x * n;
+    const float *xr = x + (size_t)blockIdx.x * xs;
+    float *yr = out + (size_t)blockIdx.x * ys;
     double s = 0.0;
     for (int i = threadIdx.x; i < n; i += OPS_TPB) s += (double)__fmul_rn(xr[i], xr[i]);
     const double S = block_sum_d<OPS_TPB>(s, red);
@@ -161,17 +163,22 @@ __global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const floa
     for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
 }
 
-// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228), gelu_tanh (:185-194)
+// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
+__device__ __forceinline__ float sigmoid1(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v))); }
+__device__ __forceinline__ float silu1(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v))); }
+__device__ __forceinline__ float softplus1(float v) { return v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v))); }
+
+// sigmoid, silu, softplus, gelu_tanh (kernels.rs:185-194)
 __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
         const float v = x[t];
         float r;
         if (op == 0)
-            r = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v)));
+            r = sigmoid1(v);
         else if (op == 1)
-            r = __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v)));
+            r = silu1(v);
         else if (op == 2)
-            r = v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v)));
+            r = softplus1(v);
         else {  // gelu_tanh (kernels.rs:185-194), f64 left to right
             const double d = (double)v;
             const double inner = 0.7978845608028654 * (d + 0.044715 * d * d * d);
@@ -182,14 +189,19 @@ __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, floa
 }
 
 // ssm_conv (kernels.rs:265-305): out[t*channels + c], sequential f32 sum.
+// The kernel is kern[tau*channels + c] (ssm_conv's layout), or with
+// GGUF_K kern[c*d_conv + tau], the GGUF tensor ssm_conv1d.weight as stored
+// (the forward transposes it into the first layout, qwen35_forward.rs:441-446).
 __global__ void ssm_conv_kernel(float *__restrict__ out, const float *__restrict__ x, const float *__restrict__ kern,
-                                int d_conv, int channels, int n_t) {
+                                int d_conv, int channels, int n_t, int gguf_k) {
     const size_t total = (size_t)n_t * channels;
     for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total; o += (size_t)gridDim.x * blockDim.x) {
         const int t = (int)(o / channels), c = (int)(o % channels);
         float s = 0.0f;
-        for (int tau = 0; tau < d_conv; tau++)
-            s = __fadd_rn(s, __fmul_rn(x[(size_t)(t + tau) * channels + c], kern[(size_t)tau * channels + c]));
+        for (int tau = 0; tau < d_conv; tau++) {
+            const float kv = gguf_k ? kern[(size_t)c * d_conv + tau] : kern[(size_t)tau * channels + c];
+            s = __fadd_rn(s, __fmul_rn(x[(size_t)(t + tau) * channels + c], kv));
+        }
         out[o] = s;
     }
 }
@@ -201,10 +213,10 @@ __global__ void ssm_conv_kernel(float *__restrict__ out, const float *__restrict
 __global__ void gdn_step_kernel(float *__restrict__ state, float *__restrict__ out, const float *__restrict__ q,
                                 const float *__restrict__ k, const float *__restrict__ v,
                                 const float *__restrict__ gate, const float *__restrict__ beta, int dim,
-                                float scale) {
-    const int h = blockIdx.x;
+                                float scale, int n_qk) {
+    const int h = blockIdx.x, hq = h % n_qk;  // q/k head of v head h (qwen35_forward.rs:475)
     float *S = state + (size_t)h * dim * dim;
-    const float *qh = q + (size_t)h * dim, *kh = k + (size_t)h * dim, *vh = v + (size_t)h * dim;
+    const float *qh = q + (size_t)hq * dim, *kh = k + (size_t)hq * dim, *vh = v + (size_t)h * dim;
     const float g_exp = expf_cr(gate[h]), bt = beta[h];
     for (int j = threadIdx.x; j < dim; j += blockDim.x) {
         double sum = 0.0;
@@ -421,6 +433,48 @@ __global__ __launch_bounds__(kPvWaves * 64) void attn_pv_kernel(float *__restric
     }
 }
 
+// ---- glue of the layer forward (qwen35_forward.rs:333-710) ----------------
+// GatedDeltaNet gates (:405-419): beta = sigmoid(beta_raw), sp =
+// softplus(alpha + dt_bias), gate = sp * a, per v head.
+__global__ void gdn_gates_kernel(const float *__restrict__ beta_raw, const float *__restrict__ alpha,
+                                 const float *__restrict__ dt_bias, const float *__restrict__ a,
+                                 float *__restrict__ beta, float *__restrict__ sp, float *__restrict__ gate, int n) {
+    for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < n; h += gridDim.x * blockDim.x) {
+        beta[h] = sigmoid1(beta_raw[h]);
+        const float p = softplus1(__fadd_rn(alpha[h], dt_bias[h]));
+        sp[h] = p;
+        gate[h] = __fmul_rn(p, a[h]);
+    }
+}
+
+// The conv window's shift (:449-450): rows 1..rows-1 move to 0..rows-2,
+// column by column (each thread reads its column's rows before writing).
+__global__ void conv_shift_kernel(float *__restrict__ win, int rows, int channels) {
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < channels; c += gridDim.x * blockDim.x) {
+        float v[8];
+        for (int r = 1; r < rows; r++) v[r - 1] = win[(size_t)r * channels + c];
+        for (int r = 1; r < rows; r++) win[(size_t)(r - 1) * channels + c] = v[r - 1];
+    }
+}
+
+// out[i] = y[i] * act(z[(i / n) * zs + i % n]), act 0 sigmoid (:679-683),
+// 1 silu (:507-511): the activation is rounded to f32 first, as the
+// reference's separate buffer.
+__global__ void mul_act_kernel(int op, float *out, const float *y, const float *__restrict__ z, int n, int zs,
+                               size_t total) {  // out may be y
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const float zv = z[(i / n) * zs + i % n];
+        out[i] = __fmul_rn(y[i], op == 0 ? sigmoid1(zv) : silu1(zv));
+    }
+}
+
+// out = a + b (the residual additions, :525-527, :534-536)
+__global__ void add_kernel(float *__restrict__ out, const float *__restrict__ a, const float *__restrict__ b,
+                           size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = __fadd_rn(a[i], b[i]);
+}
+
 inline unsigned ops_grid(size_t n) {
     const size_t g = (n + OPS_TPB - 1) / OPS_TPB;
     return (unsigned)(g < 65535u * 32u ? (g ? g : 1) : 65535u * 32u);
@@ -429,8 +483,13 @@ inline unsigned ops_grid(size_t n) {
 }  // namespace
 
 hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s) {
+    return launch_rmsnorm_rows(out, n, x, n, w, n, rows, eps, s);
+}
+
+hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const float *w, int n, int rows, float eps,
+                               hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys);
     return hipGetLastError();
 }
 
@@ -456,18 +515,19 @@ hipError_t launch_unary(int op, const float *x, size_t n, float *out, hipStream_
 }
 
 hipError_t launch_ssm_conv(float *out, const float *x, const float *kern, int d_conv, int channels, int n_t,
-                           hipStream_t s) {
+                           hipStream_t s, bool gguf_kernel) {
     if (n_t == 0 || channels == 0) return hipSuccess;
     hipLaunchKernelGGL(ssm_conv_kernel, dim3(ops_grid((size_t)n_t * channels)), dim3(OPS_TPB), 0, s, out, x, kern,
-                       d_conv, channels, n_t);
+                       d_conv, channels, n_t, gguf_kernel ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t launch_gdn_step(float *state, float *out, const float *q, const float *k, const float *v, const float *gate,
-                           const float *beta, int dim, int heads, float scale, hipStream_t s) {
+                           const float *beta, int dim, int heads, float scale, hipStream_t s, int n_qk) {
     if (heads == 0 || dim == 0) return hipSuccess;
     const int tpb = dim >= 256 ? 256 : ((dim + 63) / 64) * 64;
-    hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale);
+    hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale,
+                       n_qk > 0 ? n_qk : heads);
     return hipGetLastError();
 }
 
@@ -507,6 +567,33 @@ hipError_t launch_attn_decode(float *out, float *soft, const float *q, const flo
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(attn_pv_kernel, dim3(hd / 64, n_head_kv), dim3(kPvWaves * 64), 0, s, out, soft, vc, n_ctx,
                        n_head_kv, hd, group);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_gates(const float *beta_raw, const float *alpha, const float *dt_bias, const float *a,
+                            float *beta, float *sp, float *gate, int n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(gdn_gates_kernel, dim3(ops_grid(n)), dim3(OPS_TPB), 0, s, beta_raw, alpha, dt_bias, a, beta, sp,
+                       gate, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_shift(float *win, int rows, int channels, hipStream_t s) {
+    if (rows < 2 || rows > 9 || channels == 0) return rows > 9 ? hipErrorInvalidValue : hipSuccess;
+    hipLaunchKernelGGL(conv_shift_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, rows, channels);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_act(int op, float *out, const float *y, const float *z, int n, int zs, size_t total,
+                          hipStream_t s) {
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(mul_act_kernel, dim3(ops_grid(total)), dim3(OPS_TPB), 0, s, op, out, y, z, n, zs, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(float *out, const float *a, const float *b, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(add_kernel, dim3(ops_grid(n)), dim3(OPS_TPB), 0, s, out, a, b, n);
     return hipGetLastError();
 }
 

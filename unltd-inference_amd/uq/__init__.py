@@ -132,6 +132,11 @@ SIGNATURES = {
     "uq_embedding_lookup_d": ([_P, _P, _S, _P, _S, _S, _P], _I),
     "uq_attn_decode": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _S, C.c_float], _I),
     "uq_attn_decode_d": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, C.c_float, _P], _I),
+    # include/uq_layer.h (struct arguments by address; uq.layer builds them)
+    "uq_layer_ws_floats": ([_P, _S], _S),
+    "uq_layer_node_at": ([_P, _S, C.c_int, _P, _P], _I),
+    "uq_gdn_layer_step_d": ([_P, _P, _P, _P, _P, _P, _P, _S, _P], _I),
+    "uq_attn_layer_step_d": ([_P, _P, _P, _P, _S, _S, _P, _P, _P, _S, _P], _I),
 }
 
 
