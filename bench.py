@@ -344,8 +344,87 @@ def bench_decode(hip, steps, warmup, head_h=None):
            "q8k": {"semantics": "gemv_quant_q8k for every projection, the reference forward's numerics: every "
                                 "projection bit-exact given its input; h = swiglu within 2 ulp (expf)",
                    "ms_per_token": t8 * 1e3, "tok_s": 1.0 / t8, "gbs": total / t8 / 1e9}}
+    res["forward"] = bench_forward(hip, steps, warmup, st)
     st.free()
     return res
+
+
+QWEN35_9B = dict(n_embd=4096, n_ff=12288, n_qk_heads=16, n_v_heads=32, head_dim_linear=128, conv_kernel=4,
+                 n_head=16, n_head_kv=4, head_dim=256, n_rot=64)
+
+
+def bench_forward(hip, steps, warmup, st, ctx=512):
+    """The whole decode forward of one token on device: 24 GatedDeltaNet and
+    8 attention layers (uq_gdn_layer_step_d / uq_attn_layer_step_d, the
+    reference's recr_layer / attn_layer with gemv_quant_q8k projections),
+    each layer's input the previous layer's output, then result_norm and the
+    head; one HIP graph, attention at position ctx - 1 over a filled cache.
+    Uses the decode step's weights; norms, conv kernels and gates are
+    synthetic vectors shared by the layers of one kind."""
+    from uq import layer as L
+    from uq import ops as UO
+
+    sh = QWEN35_9B
+    theta = float(np.float32(1.0e7) ** np.float32(-2.0 / sh["n_rot"]))
+    kq = float(np.float32(1.0) / np.sqrt(np.float32(sh["head_dim"])))
+    d = L.Dims(**sh, theta_scale=theta, kq_scale=kq, rms_eps=1e-6)
+    n, nv, hd, kv = sh["n_embd"], sh["n_v_heads"], sh["head_dim_linear"], sh["n_head_kv"] * sh["head_dim"]
+    rng = np.random.default_rng(5)
+    keep = []
+
+    def dv(a):
+        arr = uq.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
+        keep.append(arr)
+        return arr
+
+    def norm(m):
+        return dv(1.0 + 0.1 * rng.standard_normal(m))
+
+    gvec = dict(attn_norm=norm(n), ssm_dt_bias=dv(rng.standard_normal(nv)),
+                ssm_a=dv(-np.exp(0.5 * rng.standard_normal(nv))),
+                ssm_conv1d=dv(0.3 * rng.standard_normal(d.channels * sh["conv_kernel"])), ssm_norm=norm(hd),
+                post_attention_norm=norm(n))
+    avec = dict(attn_norm=norm(n), attn_q_norm=norm(sh["head_dim"]), attn_k_norm=norm(sh["head_dim"]),
+                post_attention_norm=norm(n))
+    layers = []
+    for Lr in st.layers:
+        Wt = Lr["w"]
+        if Lr["attn"]:
+            q, k, v, o, g, u, dn = Wt
+            w = L.AttnWeights(attn_q=q, attn_k=k, attn_v=v, attn_output=o, ffn_gate=g, ffn_up=u, ffn_down=dn, **avec)
+            layers.append(("attn", w, dv(rng.standard_normal(ctx * kv) / 16), dv(rng.standard_normal(ctx * kv))))
+        else:
+            qkv, z, beta, alpha, o, g, u, dn = Wt
+            w = L.GdnWeights(attn_qkv=qkv, attn_gate=z, ssm_beta=beta, ssm_alpha=alpha, ssm_out=o, ffn_gate=g,
+                             ffn_up=u, ffn_down=dn, **gvec)
+            layers.append(("gdn", w, dv(np.zeros(sh["conv_kernel"] * d.channels)), dv(np.zeros(nv * hd * hd))))
+    ws = uq.DeviceArray(4 * L.ws_floats(d, ctx))
+    xa, xb, xn = uq.DeviceArray(4 * n), uq.DeviceArray(4 * n), uq.DeviceArray(4 * n)
+    out_norm = norm(n)
+    s = hip.stream()
+
+    def chain():
+        x = st.x
+        for i, (kind, w, a, b) in enumerate(layers):
+            y = xa if i % 2 == 0 else xb
+            if kind == "gdn":
+                L.gdn_step(d, w, a, b, x, y, ws, s)
+            else:
+                L.attn_step(d, w, a, b, ctx, ctx - 1, x, y, ws, s)
+            x = y
+        UO.rmsnorm_d(xn, x, out_norm, n, 1, 1e-6, s)  # result_norm (min_forward.rs:187-205)
+        uq.gemv_q8k(st.head, xn, st.logits, s)        # output_logits (min_forward.rs:207-266)
+
+    graph = hip.capture(s, chain)
+    wall, ev = timed(hip, lambda: hip.launch_graph(graph, s), steps, warmup, s)
+    t = ev * 1e-3 / steps
+    for a in keep + [ws, xa, xb, xn]:
+        a.free()
+    return {"config": f"one decode token through the device-resident forward: 24 GatedDeltaNet + 8 attention "
+                      f"layers of the synthetic hybrid 9B with their FFNs, result_norm and the Q6_K head, "
+                      f"gemv_quant_q8k projections, attention at position {ctx - 1}; one HIP graph",
+            "ms_per_token": t * 1e3, "tok_s": 1.0 / t, "weight_bytes_per_token": st.total,
+            "gbs": st.total / t / 1e9}
 
 
 def cpu_baseline(w, x):

@@ -311,3 +311,57 @@ def test_layer_step_refuses_context_full():
             a.free()
     finally:
         m.free()
+
+
+def test_layer_steps_replay_in_a_graph():
+    """Both steps captured in one HIP graph (they allocate nothing and hold
+    no memset): every replay from the same saved state gives the eager run's
+    bits, with eager work and synchronisations between the replays."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(__file__))))
+    import bench
+    m = Model(SMALL, seed=51, q6=True)
+    hip = bench.Hip()
+    s = hip.stream()
+    try:
+        d, c = m.d, m.cfg
+        n, ch, ctx = c.n_embd, d.channels, 8
+        win0 = (0.5 * np.random.default_rng(1).standard_normal(c.conv_kernel * ch)).astype(np.float32)
+        st0 = np.zeros(c.n_v_heads * c.head_dim_linear ** 2, np.float32)
+        kv = c.n_head_kv * c.head_dim
+        k0 = np.random.default_rng(2).standard_normal(ctx * kv).astype(np.float32) / 16
+        v0 = np.random.default_rng(3).standard_normal(ctx * kv).astype(np.float32)
+        win, state = uq.DeviceArray.from_numpy(win0), uq.DeviceArray.from_numpy(st0)
+        kc, vc = uq.DeviceArray.from_numpy(k0), uq.DeviceArray.from_numpy(v0)
+        ws = uq.DeviceArray(4 * L.ws_floats(d, ctx))
+        dx = uq.DeviceArray.from_numpy(S.activations(n, seed=7))
+        y1, y2 = uq.DeviceArray(4 * n), uq.DeviceArray(4 * n)
+
+        def reset():
+            win.upload(win0)
+            state.upload(st0)
+            kc.upload(k0)
+            vc.upload(v0)
+            hip.sync()
+
+        def steps():
+            L.gdn_step(d, m.gw, win, state, dx, y1, ws, s)
+            L.attn_step(d, m.aw, kc, vc, ctx, 5, y1, y2, ws, s)
+
+        reset()
+        steps()
+        hip.sync()
+        ref = (y2.download(np.float32, n), state.download(np.float32, st0.size), kc.download(np.float32, k0.size))
+        reset()
+        g = hip.capture(s, steps)
+        for r in range(3):
+            reset()
+            y2.upload(np.zeros(n, np.float32))
+            hip.launch_graph(g, s)
+            hip.sync()
+            got = (y2.download(np.float32, n), state.download(np.float32, st0.size), kc.download(np.float32, k0.size))
+            for a, b, what in zip(got, ref, ("l_out", "gdn state", "k cache")):
+                assert_bitwise(a, b, f"replay {r} {what}")
+        for a in (win, state, kc, vc, ws, dx, y1, y2):
+            a.free()
+    finally:
+        m.free()

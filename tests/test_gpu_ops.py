@@ -41,7 +41,7 @@ def dev(a):
     return uq.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
 
 
-@pytest.mark.parametrize("n", [1, 7, 4096, 12288])
+@pytest.mark.parametrize("n", [1, 7, 300, 4096, 5000, 12288])
 def test_rmsnorm_bit_exact(n):
     rng = np.random.default_rng(n)
     x = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 40.0], n)).astype(np.float32)
@@ -167,9 +167,12 @@ def test_ssm_conv_bit_exact(d_conv, channels, n_t):
     assert_bitwise(dy.download(np.float32, len(ref)), ref, "ssm_conv device")
 
 
-def test_gdn_fused_step_heads():
-    rng = np.random.default_rng(10)
-    dim, heads = 128, 8
+@pytest.mark.parametrize("dim", [128, 64, 100, 200])
+def test_gdn_fused_step_heads(dim):
+    """dim <= 128: the column-in-registers kernel (one or two elements of
+    q and k per lane, a partial last wave at 100); 200: the general one."""
+    rng = np.random.default_rng(10 + dim)
+    heads = 8
     S = (rng.standard_normal((heads, dim, dim)) * 0.1).astype(np.float32)
     q, k, v = (rng.standard_normal((heads, dim)).astype(np.float32) for _ in range(3))
     k /= np.linalg.norm(k, axis=1, keepdims=True)
@@ -195,6 +198,32 @@ def test_gdn_fused_step_heads():
     hs, ho = ops.gdn_fused_step(S[0].reshape(-1), q[0], k[0], v[0], 0.0, float(beta[0]), 0.5)
     assert_bitwise(hs, rs, "gdn host state")
     assert_bitwise(ho, ro, "gdn host out")
+
+
+def test_gdn_fused_step_midpoint_dots_take_the_ordered_sum():
+    """Columns whose k- and q-dots are exact f32 midpoints (1 + 2^-24): the
+    parallel partial sums cannot decide the rounding, so the kernel sums in
+    the reference's order; the results stay bit-exact."""
+    dim, heads = 128, 2
+    S = np.zeros((heads, dim, dim), np.float32)
+    S[:, 0, :] = 1.0
+    S[:, 1, :] = 2.0 ** -24
+    q = np.zeros((heads, dim), np.float32)
+    k = np.zeros((heads, dim), np.float32)
+    q[:, :2] = 1.0
+    k[:, :2] = 1.0
+    v = np.full((heads, dim), 3.0, np.float32)
+    gate, beta = np.zeros(heads, np.float32), np.array([0.5, 0.25], np.float32)
+    ds, dq, dk, dv, dg, db = dev(S), dev(q), dev(k), dev(v), dev(gate), dev(beta)
+    dout = uq.DeviceArray(4 * heads * dim)
+    ops.gdn_fused_step_d(ds, dout, dq, dk, dv, dg, db, dim, heads, 1.0)
+    uq.synchronize()
+    gs = ds.download(np.float32, heads * dim * dim).reshape(heads, dim * dim)
+    go = dout.download(np.float32, heads * dim).reshape(heads, dim)
+    for h in range(heads):
+        rs, ro = O.gdn_fused_step(S[h].reshape(-1), q[h], k[h], v[h], 0.0, float(beta[h]), 1.0)
+        assert_bitwise(gs[h], rs, f"midpoint state head {h}")
+        assert_bitwise(go[h], ro, f"midpoint out head {h}")
 
 
 @pytest.mark.parametrize("kind", ["llama", "neox"])
@@ -257,7 +286,7 @@ def check_attn(q, kc, vc, n_ctx, nh, nhkv, hd, scale, what, bit_exact_soft=False
 
 @pytest.mark.parametrize("n_ctx,nh,nhkv,hd", [(1, 16, 4, 256), (7, 16, 4, 256), (300, 16, 4, 256),
                                               (2049, 16, 4, 256), (33, 8, 8, 64), (100, 16, 2, 128),
-                                              (65, 8, 1, 512)])
+                                              (65, 8, 1, 512), (50, 6, 2, 64), (40, 4, 2, 128), (70, 10, 2, 64)])
 def test_attn_decode_matches_the_reference_loop(n_ctx, nh, nhkv, hd):
     q, kc, vc = attn_case(n_ctx * 7 + hd, n_ctx, nh, nhkv, hd, spare=3)  # caches longer than n_ctx, as in a session
     check_attn(q, kc, vc, n_ctx, nh, nhkv, hd, 1.0 / np.sqrt(hd), f"attn n_ctx={n_ctx} hd={hd}")

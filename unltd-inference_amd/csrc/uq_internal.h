@@ -37,24 +37,28 @@ hipError_t allow_lds(const void *kernel, size_t lds);
 
 // Per-layer non-linear ops (uq_ops.hip).
 hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s);
-// rows of n, xs / ys floats apart in x / out
+// rows of n, xs / ys floats apart in x / out; xb: normalise x + xb, written
+// to xsum when given; z: multiply the output by silu(z) (z laid out as out)
 hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const float *w, int n, int rows, float eps,
-                               hipStream_t s);
+                               hipStream_t s, const float *xb = nullptr, float *xsum = nullptr,
+                               const float *z = nullptr);
 hipError_t launch_l2norm(float *data, int dim, int rows, float eps, hipStream_t s);
 int softmax_max_len();
 hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s);
 hipError_t launch_unary(int op, const float *x, size_t n, float *out, hipStream_t s);  // 0 sigmoid, 1 silu, 2 softplus
-// gguf_kernel: kern is [channels][d_conv] (the GGUF tensor) instead of [d_conv][channels]
 hipError_t launch_ssm_conv(float *out, const float *x, const float *kern, int d_conv, int channels, int n_t,
-                           hipStream_t s, bool gguf_kernel = false);
+                           hipStream_t s);
 // v head h takes q/k head h % n_qk (n_qk 0: heads, one q/k head per v head)
 hipError_t launch_gdn_step(float *state, float *out, const float *q, const float *k, const float *v, const float *gate,
                            const float *beta, int dim, int heads, float scale, hipStream_t s, int n_qk = 0);
-// layer glue: GatedDeltaNet gates, the conv window shift (rows <= 9),
-// out = y * act(z) (op 0 sigmoid, 1 silu; z index (i / n) * zs + i % n), out = a + b
+// layer glue: GatedDeltaNet gates, out = y * act(z) (op 0 sigmoid, 1 silu;
+// z index (i / n) * zs + i % n), out = a + b
 hipError_t launch_gdn_gates(const float *beta_raw, const float *alpha, const float *dt_bias, const float *a,
                             float *beta, float *sp, float *gate, int n, hipStream_t s);
-hipError_t launch_conv_shift(float *win, int rows, int channels, hipStream_t s);
+// one token of the GatedDeltaNet conv: conv over the window with the GGUF
+// kernel [channels][d_conv] into raw, silu into act, the window shifted up
+hipError_t launch_conv_step(float *win, const float *kern_gguf, float *raw, float *act, int d_conv, int channels,
+                            hipStream_t s);
 hipError_t launch_mul_act(int op, float *out, const float *y, const float *z, int n, int zs, size_t total,
                           hipStream_t s);
 hipError_t launch_add(float *out, const float *a, const float *b, size_t n, hipStream_t s);

@@ -133,12 +133,15 @@ uq_status project_q8k(const uq_weights *w, float *const *y, int n, const float *
     return nb ? uq_gemv_q8k_batch(b, yb, nb, x, stream) : UQ_OK;
 }
 
-// post_attention_norm + FFN + l_out (ffn, :713-768, and :534-536 / :702-704)
-uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, uq_weights g, uq_weights u, uq_weights dn,
-                   const float *post_norm, float *ws, size_t nctx, float *l_out, hipStream_t s) {
+// residual = x_in + attn_out and post_attention_norm of it (one launch), FFN,
+// l_out (:524-536 / :696-704, ffn :713-768)
+uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const float *x_in, uq_weights g,
+                   uq_weights u, uq_weights dn, const float *post_norm, float *ws, size_t nctx, float *l_out,
+                   hipStream_t s) {
     auto at = [&](int node) { return ws + node_offset(D, nctx, node); };
-    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_POST_NORM), at(UQ_NODE_RESIDUAL), post_norm, (int)D.n, 1, d->rms_eps,
-                                     s), fn));
+    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_POST_NORM), (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, 1,
+                                          d->rms_eps, s, at(UQ_NODE_ATTN_OUT), at(UQ_NODE_RESIDUAL)),
+                  fn));
     UQ_TRY(uq_ffn_swiglu_q8k(g, u, dn, at(UQ_NODE_POST_NORM), at(UQ_NODE_FFN_GATE), at(UQ_NODE_FFN_UP),
                              at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT), s));
     return hip_st(uq::launch_add(l_out, at(UQ_NODE_RESIDUAL), at(UQ_NODE_FFN_OUT), D.n, s), fn);
@@ -199,11 +202,10 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
     // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419)
     UQ_TRY(hip_st(uq::launch_gdn_gates(at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), w->ssm_dt_bias, w->ssm_a,
                                        at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s), fn));
-    // 4) depthwise conv over [ring; qkv], the ring's shift, silu (:427-454)
-    UQ_TRY(hip_st(uq::launch_ssm_conv(at(UQ_NODE_CONV_RAW), d_conv_win, w->ssm_conv1d, (int)D.ck, ch, 1, s, true),
+    // 4) depthwise conv over [ring; qkv], silu, the ring's shift: one launch (:427-454)
+    UQ_TRY(hip_st(uq::launch_conv_step(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), at(UQ_NODE_CONV_SILU),
+                                       (int)D.ck, ch, s),
                   fn));
-    UQ_TRY(hip_st(uq::launch_conv_shift(d_conv_win, (int)D.ck, ch, s), fn));
-    UQ_TRY(hip_st(uq::launch_unary(1, at(UQ_NODE_CONV_RAW), D.ch, at(UQ_NODE_CONV_SILU), s), fn));
     // q and k parts l2-normalised per head (:463-464)
     float *qc = at(UQ_NODE_CONV_SILU), *kc = qc + D.nqk * D.hd, *vc = kc + D.nqk * D.hd;
     UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
@@ -212,16 +214,15 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
     UQ_TRY(hip_st(uq::launch_gdn_step(d_state, at(UQ_NODE_GDN_OUT), qc, kc, vc, at(UQ_NODE_GATE), at(UQ_NODE_BETA), hd,
                                       nv, scale, s, nqk),
                   fn));
-    // 6) rmsnorm per head with ssm_norm, times silu(z) (:495-511)
-    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_FINAL), at(UQ_NODE_GDN_OUT), w->ssm_norm, hd, nv, d->rms_eps, s), fn));
-    UQ_TRY(hip_st(uq::launch_mul_act(1, at(UQ_NODE_FINAL), at(UQ_NODE_FINAL), at(UQ_NODE_Z), (int)(D.nv * D.hd), 0,
-                                     D.nv * D.hd, s),
+    // 6) rmsnorm per head with ssm_norm, times silu(z): one launch (:495-511)
+    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_FINAL), hd, at(UQ_NODE_GDN_OUT), hd, w->ssm_norm, hd, nv,
+                                          d->rms_eps, s, nullptr, nullptr, at(UQ_NODE_Z)),
                   fn));
-    // 7) ssm_out + residual (:514-527)
+    // 7) ssm_out (:514-521); the residual is formed with the next norm
     UQ_TRY(uq_gemv_q8k(w->ssm_out, at(UQ_NODE_FINAL), at(UQ_NODE_ATTN_OUT), stream));
-    UQ_TRY(hip_st(uq::launch_add(at(UQ_NODE_RESIDUAL), d_x_in, at(UQ_NODE_ATTN_OUT), D.n, s), fn));
-    // 8) FFN and l_out (:530-536)
-    return ffn_tail(fn, D, d, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, 0, d_l_out, s);
+    // 8) residual, FFN and l_out (:524-536)
+    return ffn_tail(fn, D, d, d_x_in, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, 0, d_l_out,
+                    s);
 }
 
 uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w, float *d_k_cache,
@@ -279,11 +280,10 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
     UQ_TRY(hip_st(uq::launch_mul_act(0, at(UQ_NODE_GATED), at(UQ_NODE_ATTN), at(UQ_NODE_QFULL) + ahd, ahd, 2 * ahd,
                                      D.nh * D.ahd, s),
                   fn));
-    // 7) attn_output + residual (:686-699), FFN and l_out (:700-704)
+    // 7) attn_output (:686-693), residual, FFN and l_out (:696-704)
     UQ_TRY(uq_gemv_q8k(w->attn_output, at(UQ_NODE_GATED), at(UQ_NODE_ATTN_OUT), stream));
-    UQ_TRY(hip_st(uq::launch_add(at(UQ_NODE_RESIDUAL), d_x_in, at(UQ_NODE_ATTN_OUT), D.n, s), fn));
-    return ffn_tail(fn, D, d, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, n_ctx_max, d_l_out,
-                    s);
+    return ffn_tail(fn, D, d, d_x_in, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, n_ctx_max,
+                    d_l_out, s);
 }
 
 }  // extern "C"

@@ -59,14 +59,17 @@ __device__ float block_max_f(float v, float *red) {
 // sq[i] (f32 squares), mapped through finish(): finish(lo) == finish(hi)
 // proves the result; otherwise thread 0 replays the loop. Every thread
 // returns the same value.
-template <int TPB, class Finish>
-__device__ float seq_sum_f32(const float *__restrict__ sq_src, int n, double S, Finish finish, float *bcast) {
+template <int TPB, class Val, class Finish>
+__device__ float seq_sum_f32(Val val, int n, double S, Finish finish, float *bcast) {
     const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
     const float a = finish(S - e), b = finish(S + e);
     if (__float_as_uint(a) == __float_as_uint(b)) return a;  // -0 and +0 differ: replay
     if (threadIdx.x == 0) {
         double s = 0.0;
-        for (int i = 0; i < n; i++) s += (double)__fmul_rn(sq_src[i], sq_src[i]);
+        for (int i = 0; i < n; i++) {
+            const float v = val(i);
+            s += (double)__fmul_rn(v, v);
+        }
         *bcast = finish(s);
     }
     __syncthreads();
@@ -75,22 +78,71 @@ __device__ float seq_sum_f32(const float *__restrict__ sq_src, int n, double S, 
     return r;
 }
 
+// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
+__device__ __forceinline__ float sigmoid1(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v))); }
+__device__ __forceinline__ float silu1(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v))); }
+__device__ __forceinline__ float softplus1(float v) { return v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v))); }
+
 // rmsnorm (kernels.rs:61-78), one workgroup per row of n; rows xs (input)
-// and ys (output) floats apart.
+// and ys (output) floats apart. Two fusions of the layer forward: with xb
+// the row normalised is x + xb (an f32 add), also written to xsum (the
+// residual and the norm after it, qwen35_forward.rs:525-530); with z the
+// output is multiplied by silu(z) (the gated norm, :495-511; z in the
+// output's layout). PT > 0 (n <= PT * OPS_TPB): a thread's elements are
+// loaded once, all before the sum, and kept in registers.
+template <int PT>
 __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
                                                           const float *__restrict__ w, int n, float eps, int xs,
-                                                          int ys) {
+                                                          int ys, const float *__restrict__ xb,
+                                                          float *__restrict__ xsum, const float *__restrict__ z) {
     __shared__ double red[OPS_TPB / 64];
     __shared__ float bc;
     const float *xr = x + (size_t)blockIdx.x * xs;
+    const float *xbr = xb ? xb + (size_t)blockIdx.x * xs : nullptr;
     float *yr = out + (size_t)blockIdx.x * ys;
+    auto val = [&](int i) { return xbr ? __fadd_rn(xr[i], xbr[i]) : xr[i]; };
+    constexpr int R = PT > 0 ? PT : 1;
+    float v[R];
     double s = 0.0;
-    for (int i = threadIdx.x; i < n; i += OPS_TPB) s += (double)__fmul_rn(xr[i], xr[i]);
+    if constexpr (PT > 0) {
+#pragma unroll
+        for (int k = 0; k < PT; k++) {
+            const int i = threadIdx.x + k * OPS_TPB;
+            v[k] = i < n ? val(i) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < PT; k++) {
+            const int i = threadIdx.x + k * OPS_TPB;
+            if (i < n) {
+                if (xsum) xsum[(size_t)blockIdx.x * xs + i] = v[k];
+                s += (double)__fmul_rn(v[k], v[k]);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += OPS_TPB) {
+            const float t = val(i);
+            if (xsum) xsum[(size_t)blockIdx.x * xs + i] = t;
+            s += (double)__fmul_rn(t, t);
+        }
+    }
     const double S = block_sum_d<OPS_TPB>(s, red);
     const double dn = (double)n;
-    const float mean = seq_sum_f32<OPS_TPB>(xr, n, S, [dn](double v) { return (float)(v / dn); }, &bc);
+    const float mean = seq_sum_f32<OPS_TPB>(val, n, S, [dn](double u) { return (float)(u / dn); }, &bc);
     const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
-    for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+    auto emit = [&](int i, float t) {
+        float y = __fmul_rn(__fmul_rn(t, scale), w[i]);
+        if (z) y = __fmul_rn(y, silu1(z[(size_t)blockIdx.x * ys + i]));
+        yr[i] = y;
+    };
+    if constexpr (PT > 0) {
+#pragma unroll
+        for (int k = 0; k < PT; k++) {
+            const int i = threadIdx.x + k * OPS_TPB;
+            if (i < n) emit(i, v[k]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += OPS_TPB) emit(i, val(i));
+    }
 }
 
 // l2_norm_rows (kernels.rs:236-256), in place, one workgroup per row.
@@ -101,7 +153,7 @@ __global__ __launch_bounds__(OPS_TPB) void l2norm_kernel(float *__restrict__ dat
     double s = 0.0;
     for (int i = threadIdx.x; i < dim; i += OPS_TPB) s += (double)__fmul_rn(r[i], r[i]);
     const double S = block_sum_d<OPS_TPB>(s, red);
-    const float sum32 = seq_sum_f32<OPS_TPB>(r, dim, S, [](double v) { return (float)v; }, &bc);
+    const float sum32 = seq_sum_f32<OPS_TPB>([r](int i) { return r[i]; }, dim, S, [](double v) { return (float)v; }, &bc);
     const float scale = __fdiv_rn(1.0f, fmaxf(sqrtf_cr(sum32), eps));
     for (int i = threadIdx.x; i < dim; i += OPS_TPB) r[i] = __fmul_rn(r[i], scale);
 }
@@ -163,11 +215,6 @@ __global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const floa
     for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
 }
 
-// sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
-__device__ __forceinline__ float sigmoid1(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_cr(-v))); }
-__device__ __forceinline__ float silu1(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf_cr(-v))); }
-__device__ __forceinline__ float softplus1(float v) { return v > 20.0f ? v : logf_cr(__fadd_rn(1.0f, expf_cr(v))); }
-
 // sigmoid, silu, softplus, gelu_tanh (kernels.rs:185-194)
 __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
@@ -189,20 +236,33 @@ __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, floa
 }
 
 // ssm_conv (kernels.rs:265-305): out[t*channels + c], sequential f32 sum.
-// The kernel is kern[tau*channels + c] (ssm_conv's layout), or with
-// GGUF_K kern[c*d_conv + tau], the GGUF tensor ssm_conv1d.weight as stored
-// (the forward transposes it into the first layout, qwen35_forward.rs:441-446).
 __global__ void ssm_conv_kernel(float *__restrict__ out, const float *__restrict__ x, const float *__restrict__ kern,
-                                int d_conv, int channels, int n_t, int gguf_k) {
+                                int d_conv, int channels, int n_t) {
     const size_t total = (size_t)n_t * channels;
     for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total; o += (size_t)gridDim.x * blockDim.x) {
         const int t = (int)(o / channels), c = (int)(o % channels);
         float s = 0.0f;
-        for (int tau = 0; tau < d_conv; tau++) {
-            const float kv = gguf_k ? kern[(size_t)c * d_conv + tau] : kern[(size_t)tau * channels + c];
-            s = __fadd_rn(s, __fmul_rn(x[(size_t)(t + tau) * channels + c], kv));
-        }
+        for (int tau = 0; tau < d_conv; tau++)
+            s = __fadd_rn(s, __fmul_rn(x[(size_t)(t + tau) * channels + c], kern[(size_t)tau * channels + c]));
         out[o] = s;
+    }
+}
+
+// One token of the GatedDeltaNet conv (qwen35_forward.rs:427-454), one
+// thread per channel c: ssm_conv's sequential sum over the window's rows,
+// with the kernel indexed as the GGUF tensor ssm_conv1d.weight is stored,
+// [c][tau] (the forward transposes it first, :441-446), then silu of it,
+// and the window's shift up by a row (:449-450).
+__global__ void conv_step_kernel(float *__restrict__ win, const float *__restrict__ kern, float *__restrict__ raw,
+                                 float *__restrict__ act, int d_conv, int channels) {
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < channels; c += gridDim.x * blockDim.x) {
+        float x[9];
+        for (int r = 0; r < d_conv; r++) x[r] = win[(size_t)r * channels + c];
+        float s = 0.0f;
+        for (int tau = 0; tau < d_conv; tau++) s = __fadd_rn(s, __fmul_rn(x[tau], kern[(size_t)c * d_conv + tau]));
+        raw[c] = s;
+        act[c] = silu1(s);
+        for (int r = 1; r < d_conv; r++) win[(size_t)(r - 1) * channels + c] = x[r];
     }
 }
 
@@ -234,6 +294,83 @@ __global__ void gdn_step_kernel(float *__restrict__ state, float *__restrict__ o
         }
         out[(size_t)h * dim + j] = __fmul_rn((float)o, scale);
     }
+}
+
+// The same step for dim <= 128 with the column in VGPRs: a workgroup of
+// four waves per 64 columns of a head, grid (dim / 64, heads); wave w holds
+// rows [32w, 32w + 32) of the 64 columns, loaded once and stored once.
+// Each f64 dot is the four waves' partial sums (each in row order) added in
+// LDS, plus a bound: any order of summing n terms lies within
+// (n - 1) 2^-53 sum|t| of the exact sum, as does the reference's
+// sequential loop, so when both ends of [S - e, S + e] round to one f32
+// that is the reference's (float)sum. Otherwise (rarely; the decision is
+// the same for every wave) the column goes through LDS and the loop runs in
+// the reference's order.
+constexpr int kGdnRows = 32;  // rows per wave
+__global__ __launch_bounds__(256) void gdn_step_wg_kernel(float *__restrict__ state, float *__restrict__ out,
+                                                         const float *__restrict__ q, const float *__restrict__ k,
+                                                         const float *__restrict__ v, const float *__restrict__ gate,
+                                                         const float *__restrict__ beta, int dim, float scale,
+                                                         int n_qk) {
+    __shared__ double ps[4][64], pa[4][64];
+    __shared__ float col[128][64];  // the column, for the ordered replay
+    __shared__ float kq[2][128];
+    const int h = blockIdx.y, hq = h % n_qk, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    if (threadIdx.x < dim) {
+        kq[0][threadIdx.x] = k[(size_t)hq * dim + threadIdx.x];
+        kq[1][threadIdx.x] = q[(size_t)hq * dim + threadIdx.x];
+    }
+    __syncthreads();
+    const bool live = j < dim;
+    const int i0 = kGdnRows * wv;
+    float *S = state + (size_t)h * dim * dim + (live ? j : 0);
+    const float g_exp = expf_cr(gate[h]), bt = beta[h];
+    float c[kGdnRows];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r++) c[r] = (i0 + r < dim && live) ? S[(size_t)(i0 + r) * dim] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r++) c[r] = __fmul_rn(c[r], g_exp);
+    // (float) of the sequential f64 sum over i < dim of c_i * kq[sel][i]
+    auto dot = [&](int sel) {
+        double s = 0.0, a = 0.0;
+#pragma unroll
+        for (int r = 0; r < kGdnRows; r++)
+            if (i0 + r < dim) {
+                const double t = (double)__fmul_rn(c[r], kq[sel][i0 + r]);
+                s += t;
+                a += fabs(t);
+            }
+        ps[wv][lane] = s;
+        pa[wv][lane] = a;
+        __syncthreads();
+        const double S4 = (ps[0][lane] + ps[1][lane]) + (ps[2][lane] + ps[3][lane]);
+        const double A4 = (pa[0][lane] + pa[1][lane]) + (pa[2][lane] + pa[3][lane]);
+        __syncthreads();  // ps / pa are free for the next dot
+        const double e = (double)(dim + 66) * 0x1p-52 * A4;
+        const float lo = (float)(S4 - e), hi = (float)(S4 + e);
+        // one decision for the workgroup: any lane of any wave undecided
+        const int undecided = __syncthreads_or(__float_as_uint(lo) != __float_as_uint(hi));
+        if (!undecided) return lo;
+#pragma unroll
+        for (int r = 0; r < kGdnRows; r++)
+            if (i0 + r < dim) col[i0 + r][lane] = c[r];
+        __syncthreads();
+        double qq = 0.0;
+        for (int i = 0; i < dim; i++) qq += (double)__fmul_rn(col[i][lane], kq[sel][i]);
+        __syncthreads();
+        return (float)qq;
+    };
+    const float sum = dot(0);
+    const float d = __fmul_rn(__fsub_rn(live ? v[(size_t)h * dim + j] : 0.0f, sum), bt);
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r++)
+        if (i0 + r < dim) {
+            c[r] = __fadd_rn(c[r], __fmul_rn(kq[0][i0 + r], d));
+            if (live) S[(size_t)(i0 + r) * dim] = c[r];
+        }
+    const float o = dot(1);
+    if (live && wv == 0) out[(size_t)h * dim + j] = __fmul_rn(o, scale);
 }
 
 // The rope rotation (kernels.rs:121-123): f64 sin/cos, fma, rounded to f32.
@@ -362,17 +499,26 @@ __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict_
     for (int t = threadIdx.x; t < group * HD; t += OPS_TPB) qs[t] = q[(size_t)kv * group * HD + t];
     __syncthreads();
     const size_t kv_len = (size_t)n_head_kv * HD;
-    const int p1 = min(n_ctx, (int)(blockIdx.x + 1) * kScoresPPB);
-    for (int p = blockIdx.x * kScoresPPB + w; p < p1; p += OPS_TPB / 64) {
+    // the wave's positions p0 + 4t: every K row is loaded before the dots
+    constexpr int PW = kScoresPPB / (OPS_TPB / 64);
+    const int p0 = blockIdx.x * kScoresPPB + w;
+    float kx[PW][E];
+#pragma unroll
+    for (int t = 0; t < PW; t++) {
+        const int p = min(p0 + t * (OPS_TPB / 64), n_ctx - 1);
         const float *kr = kc + (size_t)p * kv_len + (size_t)kv * HD + lane * E;
-        float kx[E];
 #pragma unroll
-        for (int e = 0; e < E; e++) kx[e] = kr[e];
+        for (int e = 0; e < E; e++) kx[t][e] = kr[e];
+    }
+#pragma unroll
+    for (int t = 0; t < PW; t++) {
+        const int p = p0 + t * (OPS_TPB / 64);
+        if (p >= n_ctx) break;  // wave-uniform
         for (int g = 0; g < group; g++) {
-            double t[E];
+            double d[E];
 #pragma unroll
-            for (int e = 0; e < E; e++) t[e] = (double)qs[g * HD + lane * E + e] * (double)kx[e];
-            const double sc = wave_pairwise<E>(t);
+            for (int e = 0; e < E; e++) d[e] = (double)qs[g * HD + lane * E + e] * (double)kx[t][e];
+            const double sc = wave_pairwise<E>(d);
             if (lane == 0) scores[(size_t)(kv * group + g) * n_ctx + p] = (float)sc;
         }
     }
@@ -385,31 +531,49 @@ __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict_
 // lies in [S - e, S + e], e = (n + 66) 2^-52 A (with room for the rounding
 // of e and S +- e); when both ends round to the same f32 (same bits) that
 // is the reference's value, else the lane replays the sequential loop.
-constexpr int kPvWaves = 8;
-__global__ __launch_bounds__(kPvWaves * 64) void attn_pv_kernel(float *__restrict__ out, const float *__restrict__ soft,
-                                                                const float *__restrict__ vc, int n_ctx, int n_head_kv,
-                                                                int hd, int group) {
-    __shared__ double part[2][kPvWaves][kAttnMaxGroup][64];
+constexpr int kPvBatch = 16;  // positions whose V loads a wave issues before summing
+template <int G>
+constexpr int pv_waves() { return G <= 4 ? 16 : 8; }  // the LDS partials stay within 64 KB
+// G: q heads per kv head, compile-time so that a batch's loads issue back to back
+template <int G>
+__global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__restrict__ out,
+                                                                    const float *__restrict__ soft,
+                                                                    const float *__restrict__ vc, int n_ctx,
+                                                                    int n_head_kv, int hd) {
+    constexpr int group = G, kPvWaves = pv_waves<G>();
+    __shared__ double part[2][kPvWaves][G][64];
     const int kv = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int i = blockIdx.x * 64 + lane;
     const size_t kv_len = (size_t)n_head_kv * hd;
     const float *vcol = vc + (size_t)kv * hd + i;
     const float *sr = soft + (size_t)kv * group * n_ctx;
-    double S[kAttnMaxGroup], A[kAttnMaxGroup];
+    double S[G], A[G];
 #pragma unroll
-    for (int g = 0; g < kAttnMaxGroup; g++) S[g] = A[g] = 0.0;
-    for (int p = w; p < n_ctx; p += kPvWaves) {
-        const double v = (double)vcol[(size_t)p * kv_len];
+    for (int g = 0; g < G; g++) S[g] = A[g] = 0.0;
+    // positions in batches of kPvBatch per wave, loads first (the sums only
+    // need some order: the bound below covers any)
+    for (int p0 = w; p0 < n_ctx; p0 += kPvWaves * kPvBatch) {
+        float vb[kPvBatch], sb[kPvBatch][G];
 #pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; g++)
-            if (g < group) {
-                const double t = (double)sr[(size_t)g * n_ctx + p] * v;
+        for (int u = 0; u < kPvBatch; u++) {
+            const int p = min(p0 + u * kPvWaves, n_ctx - 1);
+            vb[u] = vcol[(size_t)p * kv_len];
+#pragma unroll
+            for (int g = 0; g < G; g++) sb[u][g] = sr[(size_t)g * n_ctx + p];
+        }
+#pragma unroll
+        for (int u = 0; u < kPvBatch; u++) {
+            const bool in = p0 + u * kPvWaves < n_ctx;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const double t = in ? (double)sb[u][g] * (double)vb[u] : 0.0;
                 S[g] += t;
                 A[g] += fabs(t);
             }
+        }
     }
 #pragma unroll
-    for (int g = 0; g < kAttnMaxGroup; g++) {
+    for (int g = 0; g < G; g++) {
         part[0][w][g][lane] = S[g];
         part[1][w][g][lane] = A[g];
     }
@@ -425,8 +589,22 @@ __global__ __launch_bounds__(kPvWaves * 64) void attn_pv_kernel(float *__restric
         const float lo = (float)(st - e), hi = (float)(st + e);
         float r = lo;
         if (__float_as_uint(lo) != __float_as_uint(hi)) {
+            // the reference's sequential sum (about 1e-4 of the outputs come
+            // here): loads in batches, the adds in order
+            constexpr int RB = 32;
             double q = 0.0;
-            for (int p = 0; p < n_ctx; p++) q += (double)sr[(size_t)g * n_ctx + p] * (double)vcol[(size_t)p * kv_len];
+            for (int p0 = 0; p0 < n_ctx; p0 += RB) {
+                float vb[RB], sb[RB];
+#pragma unroll
+                for (int u = 0; u < RB; u++) {
+                    const int p = min(p0 + u, n_ctx - 1);
+                    vb[u] = vcol[(size_t)p * kv_len];
+                    sb[u] = sr[(size_t)g * n_ctx + p];
+                }
+#pragma unroll
+                for (int u = 0; u < RB; u++)
+                    if (p0 + u < n_ctx) q += (double)sb[u] * (double)vb[u];
+            }
             r = (float)q;
         }
         out[(size_t)(kv * group + g) * hd + i] = r;
@@ -444,16 +622,6 @@ __global__ void gdn_gates_kernel(const float *__restrict__ beta_raw, const float
         const float p = softplus1(__fadd_rn(alpha[h], dt_bias[h]));
         sp[h] = p;
         gate[h] = __fmul_rn(p, a[h]);
-    }
-}
-
-// The conv window's shift (:449-450): rows 1..rows-1 move to 0..rows-2,
-// column by column (each thread reads its column's rows before writing).
-__global__ void conv_shift_kernel(float *__restrict__ win, int rows, int channels) {
-    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < channels; c += gridDim.x * blockDim.x) {
-        float v[8];
-        for (int r = 1; r < rows; r++) v[r - 1] = win[(size_t)r * channels + c];
-        for (int r = 1; r < rows; r++) win[(size_t)(r - 1) * channels + c] = v[r - 1];
     }
 }
 
@@ -487,9 +655,14 @@ hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int
 }
 
 hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const float *w, int n, int rows, float eps,
-                               hipStream_t s) {
+                               hipStream_t s, const float *xb, float *xsum, const float *z) {
     if (rows == 0 || n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys);
+    if (n <= OPS_TPB)
+        hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
+    else if (n <= 16 * OPS_TPB)
+        hipLaunchKernelGGL(rmsnorm_kernel<16>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
     return hipGetLastError();
 }
 
@@ -515,19 +688,24 @@ hipError_t launch_unary(int op, const float *x, size_t n, float *out, hipStream_
 }
 
 hipError_t launch_ssm_conv(float *out, const float *x, const float *kern, int d_conv, int channels, int n_t,
-                           hipStream_t s, bool gguf_kernel) {
+                           hipStream_t s) {
     if (n_t == 0 || channels == 0) return hipSuccess;
     hipLaunchKernelGGL(ssm_conv_kernel, dim3(ops_grid((size_t)n_t * channels)), dim3(OPS_TPB), 0, s, out, x, kern,
-                       d_conv, channels, n_t, gguf_kernel ? 1 : 0);
+                       d_conv, channels, n_t);
     return hipGetLastError();
 }
 
 hipError_t launch_gdn_step(float *state, float *out, const float *q, const float *k, const float *v, const float *gate,
                            const float *beta, int dim, int heads, float scale, hipStream_t s, int n_qk) {
     if (heads == 0 || dim == 0) return hipSuccess;
+    const int nq = n_qk > 0 ? n_qk : heads;
+    if (dim <= 4 * kGdnRows) {
+        hipLaunchKernelGGL(gdn_step_wg_kernel, dim3((dim + 63) / 64, heads), dim3(256), 0, s, state, out, q, k, v, gate,
+                           beta, dim, scale, nq);
+        return hipGetLastError();
+    }
     const int tpb = dim >= 256 ? 256 : ((dim + 63) / 64) * 64;
-    hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale,
-                       n_qk > 0 ? n_qk : heads);
+    hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale, nq);
     return hipGetLastError();
 }
 
@@ -565,8 +743,20 @@ hipError_t launch_attn_decode(float *out, float *soft, const float *q, const flo
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_pv_kernel, dim3(hd / 64, n_head_kv), dim3(kPvWaves * 64), 0, s, out, soft, vc, n_ctx,
-                       n_head_kv, hd, group);
+    const dim3 gp(hd / 64, n_head_kv);
+#define UQ_PV(G) hipLaunchKernelGGL(attn_pv_kernel<G>, gp, dim3(pv_waves<G>() * 64), 0, s, out, soft, vc, n_ctx, \
+                                    n_head_kv, hd)
+    switch (group) {
+        case 1: UQ_PV(1); break;
+        case 2: UQ_PV(2); break;
+        case 3: UQ_PV(3); break;
+        case 4: UQ_PV(4); break;
+        case 5: UQ_PV(5); break;
+        case 6: UQ_PV(6); break;
+        case 7: UQ_PV(7); break;
+        default: UQ_PV(8); break;
+    }
+#undef UQ_PV
     return hipGetLastError();
 }
 
@@ -578,9 +768,12 @@ hipError_t launch_gdn_gates(const float *beta_raw, const float *alpha, const flo
     return hipGetLastError();
 }
 
-hipError_t launch_conv_shift(float *win, int rows, int channels, hipStream_t s) {
-    if (rows < 2 || rows > 9 || channels == 0) return rows > 9 ? hipErrorInvalidValue : hipSuccess;
-    hipLaunchKernelGGL(conv_shift_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, rows, channels);
+hipError_t launch_conv_step(float *win, const float *kern_gguf, float *raw, float *act, int d_conv, int channels,
+                            hipStream_t s) {
+    if (d_conv < 1 || d_conv > 9) return hipErrorInvalidValue;
+    if (channels == 0) return hipSuccess;
+    hipLaunchKernelGGL(conv_step_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, kern_gguf, raw, act,
+                       d_conv, channels);
     return hipGetLastError();
 }
 
