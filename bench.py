@@ -175,6 +175,23 @@ def bench_q4k_small(hip, steps, warmup):
             "gbs_wall": nbytes * n / wall / 1e9}
 
 
+def bench_q4k_large(hip, steps, warmup):
+    """The Q4_K streaming kernel at the head's shape (152064 x 4096, 350 MB):
+    one launch long enough that its fixed cost is amortised."""
+    K, N = 4096, 152064
+    w = S.weights(S.Q4_K, N, K, seed=S.seed_for(0, 7))
+    x = S.activations(K, seed=S.seed_for(0, 7))
+    W = uq.Weights(w, uq.DType.Q4K, K, N)
+    dx, dy = uq.DeviceArray.from_numpy(x), uq.DeviceArray(4 * N)
+    s = hip.stream()
+    wall, ev = timed(hip, lambda: uq.gemv(W, dx, dy, s), steps, warmup, s)
+    nbytes = gemv_bytes(S.Q4_K, K, N)
+    W.free()
+    gbs = nbytes * steps / (ev * 1e-3) / 1e9
+    return {"config": "Q4_K GEMV 152064x4096 (350 MB)", "bytes": nbytes, "us_per_call": ev * 1e3 / steps,
+            "gbs_event": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS, "gbs_wall": nbytes * steps / wall / 1e9}
+
+
 def bench_ffn(hip, steps, warmup):
     n, nff, copies = 4096, 12288, 6
     g = S.weights(S.Q4_K, nff, n, seed=S.seed_for(2, 1))
@@ -499,7 +516,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of: head,q4k,ffn,gemm,decode")
+    ap.add_argument("--only", default="", help="comma list of: head,q4k,q4k_large,ffn,gemm,decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run two 1 GiB device copies (reference dispatches for counter runs)")
     a = ap.parse_args()
@@ -515,7 +532,8 @@ def main():
     head, w, x, W = bench_head(hip, a.steps, a.warmup)
     extra = {"head_q8k_bit_exact": head["q8k"]}
     if not a.quick:
-        for name, fn in (("q4k", bench_q4k_small), ("ffn", bench_ffn), ("gemm", bench_gemm)):
+        for name, fn in (("q4k", bench_q4k_small), ("q4k_large", bench_q4k_large), ("ffn", bench_ffn),
+                         ("gemm", bench_gemm)):
             if not only or name in only:
                 log("bench:", name)
                 extra[name] = fn(hip, a.steps, a.warmup)
