@@ -316,6 +316,26 @@ def test_attn_decode_order_adversaries_take_the_replay():
     assert got.tolist() == [0.5] * hd
 
 
+@pytest.mark.parametrize("cols", [(0,), (5, 9, 63), (1, 2, 3, 4, 5, 6, 7)])
+def test_attn_decode_replays_a_few_columns_over_a_long_context(cols):
+    """Equal weights over 300 positions; the listed value columns hold
+    [2^62, 1, -2^62, 1, 0, ...], whose sum is the weight only in sequential
+    order, the others N(0,1). Up to four such columns per wave are replayed
+    by the whole wave one at a time, more by their own lanes: both must give
+    the reference's sequential sum."""
+    hd, n_ctx = 64, 300
+    rng = np.random.default_rng(len(cols))
+    q = np.ones(hd, np.float32)
+    kc = np.ones(n_ctx * hd, np.float32)
+    vc = rng.standard_normal((n_ctx, hd)).astype(np.float32)
+    for c in cols:
+        vc[:, c] = 0.0
+        vc[:4, c] = [2.0 ** 62, 1.0, -(2.0 ** 62), 1.0]
+    got = check_attn(q, kc, vc.reshape(-1), n_ctx, 1, 1, hd, 1.0, f"replay {cols}", bit_exact_soft=True)
+    w = np.float32(got[cols[0]])
+    assert all(got[c] == w for c in cols) and w > 0
+
+
 def test_gelu_tanh_within_1_ulp():
     rng = np.random.default_rng(23)
     x = np.concatenate([rng.uniform(-8, 8, 100000), [0.0, -0.0, 1.0, -1.0, 30.0, -30.0]]).astype(np.float32)

@@ -503,6 +503,16 @@ uq_status uq_swiglu_d(float *d_out, const float *d_gate, const float *d_up, size
 
 uq_status uq_ffn_swiglu_q8k(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_g, float *d_u,
                             float *d_h, float *d_y, void *stream) {
+    return uq::ffn_swiglu_q8k_sum(gh, uh, dh, d_x, d_g, d_u, d_h, d_y, nullptr, nullptr, stream);
+}
+
+}  // extern "C"
+
+// uq_ffn_swiglu_q8k; with d_ysum set, the down projection also writes
+// d_ysum = d_add + d_y (the layer's residual sum, in the same launch).
+uq_status uq::ffn_swiglu_q8k_sum(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_g,
+                                 float *d_u, float *d_h, float *d_y, const float *d_add, float *d_ysum,
+                                 void *stream) {
     uq_weights_s *g = handle(gh), *u = handle(uh), *dn = handle(dh);
     if (!g || !u || !dn) return fail(UQ_ERR_ARG, "ffn_swiglu_q8k: invalid handle");
     for (uq_weights_s *w : {g, u, dn})
@@ -522,9 +532,14 @@ uq_status uq_ffn_swiglu_q8k(uq_weights gh, uq_weights uh, uq_weights dh, const f
         UQ_HIP(uq::launch_gemv_q8k_batch(gu, 2, d_x, gy, s), "ffn_q8k gate/up launch");
         UQ_HIP(uq::launch_swiglu(d_g, d_u, g->dim_out, d_h, s), "ffn_q8k swiglu launch");
     }
-    UQ_HIP(uq::launch_gemv_q8k(uq::view(*dn), d_h, d_y, s), "ffn_q8k down launch");
+    if (d_ysum)
+        UQ_HIP(uq::launch_gemv_q8k_sum(uq::view(*dn), d_h, d_y, d_add, d_ysum, s), "ffn_q8k down launch");
+    else
+        UQ_HIP(uq::launch_gemv_q8k(uq::view(*dn), d_h, d_y, s), "ffn_q8k down launch");
     return UQ_OK;
 }
+
+extern "C" {
 
 uq_status uq_gemv_q8k(uq_weights wh, const float *d_x, float *d_y, void *stream) {
     uq_weights_s *w = handle(wh);

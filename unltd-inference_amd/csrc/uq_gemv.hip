@@ -84,6 +84,10 @@ struct Segs {
     const uint8_t *w[kMaxSegs];
     const uint8_t *w2[kMaxSegs];
     float *y[kMaxSegs];
+    // one-segment q8k launches: also ysum[r] = add[r] + y[r] (one f32 add,
+    // the layer's residual sum) when ysum is set
+    const float *add;
+    float *ysum;
 };
 __device__ __forceinline__ int seg_of(const Segs &S, int R) {
     int s = 0;
@@ -1064,6 +1068,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
             if (k == 0 && r < slot) {
                 const int Rr = row - (slot - 1 - r) * nwave, so = MULTI ? seg_of(S, Rr) : 0;
                 S.y[so][Rr - S.start[so]] = s;
+                if (!MULTI && S.ysum) S.ysum[Rr] = __fadd_rn(S.add[Rr], s);
             }
             __builtin_amdgcn_wave_barrier();
             slot = 0;
@@ -1252,6 +1257,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
                     Sg.y[2][Rr] = swiglu1(out[0], out[NT - 1]);
                 } else {
                     Sg.y[so][Rr - Sg.start[so]] = out[0];
+                    if (!MULTI && Sg.ysum) Sg.ysum[Rr] = __fadd_rn(Sg.add[Rr], out[0]);
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -1375,8 +1381,11 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
                 float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
 #pragma unroll
                 for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
-                if (k == 0 && r < nr)  // lane 0 always stores: one store instruction
-                    Sg.y[0][G + (i + 1 - slot + r) * nG] = sv;
+                if (k == 0 && r < nr) {  // lane 0 always stores: one store instruction
+                    const int Rr = G + (i + 1 - slot + r) * nG;
+                    Sg.y[0][Rr] = sv;
+                    if (Sg.ysum) Sg.ysum[Rr] = __fadd_rn(Sg.add[Rr], sv);
+                }
                 stored = true;
             }
             __syncthreads();  // the records are free again
@@ -1390,7 +1399,9 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
 __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, const uint8_t *__restrict__ W,
                                                                size_t row_bytes, int K, int N,
                                                                const float *__restrict__ x,
-                                                               float *__restrict__ y) {
+                                                               float *__restrict__ y,
+                                                               const float *__restrict__ add,
+                                                               float *__restrict__ ysum) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nblk = K >> 8;
     uint32_t *q = (uint32_t *)lds;
@@ -1447,6 +1458,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
         float s = sumf;
         for (int k = 0; k < 8; k++) s = __fadd_rn(s, sums[k]);
         y[row] = s;
+        if (ysum) ysum[row] = __fadd_rn(add[row], s);
     }
 }
 
@@ -1581,7 +1593,7 @@ hipError_t launch_q8k_segs(uq_dtype dt, int K, size_t row_bytes, const Segs &S, 
         int grid = (N + TPB - 1) / TPB;
         if (grid > num_cus() * 4) grid = num_cus() * 4;
         hipLaunchKernelGGL(gemv_q8k_generic_kernel, dim3(grid), dim3(TPB), lds, s, dt, S.w[i], row_bytes, K, N, x,
-                           S.y[i]);
+                           S.y[i], S.n == 1 ? S.add : nullptr, S.n == 1 ? S.ysum : nullptr);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -1647,6 +1659,14 @@ hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const 
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {
     return launch_q8k_segs(w.dtype, w.dim_in, w.row_bytes, one_seg(w, nullptr, y), x, s);
+}
+
+hipError_t launch_gemv_q8k_sum(const WeightsView &w, const float *x, float *y, const float *add, float *ysum,
+                               hipStream_t s) {
+    Segs S = one_seg(w, nullptr, y);
+    S.add = add;
+    S.ysum = ysum;
+    return launch_q8k_segs(w.dtype, w.dim_in, w.row_bytes, S, x, s);
 }
 
 // Dynamic LDS above 64 KB must be allowed per kernel and device, once.

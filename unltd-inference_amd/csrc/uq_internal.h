@@ -69,8 +69,21 @@ int matmul_max_k();
 hipError_t launch_matmul_acc(float *acc, const float *a, const float *b, int m, int k, int n, hipStream_t s);
 // decode attention: hd in {64, 128, 256, 512}, 1 <= group <= 8
 bool attn_shape_ok(int hd, int group);
+// gz/gzs/gated (optional): also gated[h][i] = out[h][i] * sigmoid(gz[h * gzs + i])
 hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
-                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s);
+                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s,
+                              const float *gz = nullptr, int gzs = 0, float *gated = nullptr);
+// The GatedDeltaNet conv step, the l2 norms of the q / k heads and the gates
+// in one launch (hd <= 1024, conv_norm_ok)
+hipError_t launch_gdn_conv_norm(float *win, const float *kern_gguf, float *raw, float *act, int d_conv, int channels,
+                                int hd, int n_qk, float eps, const float *beta_raw, const float *alpha,
+                                const float *dt_bias, const float *a, float *beta, float *sp, float *gate, int n_v,
+                                hipStream_t s);
+bool conv_norm_ok(int hd);
+// q and k rmsnorm + IMROPE of the attention layer in one launch (hd <= 512)
+hipError_t launch_attn_qk_prep(const float *qfull, float *q_out, const float *k_raw, float *k_out, const float *wq,
+                               const float *wk, int hd, int n_head, int n_head_kv, int n_rot, double theta_scale,
+                               size_t pos, float eps, hipStream_t s);
 
 // For host-pointer entry points: checks for a gfx950 device and returns the
 // calling thread's stream (uq_abi.cpp).
@@ -125,6 +138,13 @@ hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const 
                               float *h, hipStream_t s, bool *done);
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y,
                            hipStream_t s);
+// uq_ffn_swiglu_q8k whose down projection also writes d_ysum = d_add + d_y
+// when d_ysum is set (the layer's residual sum)
+uq_status ffn_swiglu_q8k_sum(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_g, float *d_u,
+                             float *d_h, float *d_y, const float *d_add, float *d_ysum, void *stream);
+// gemv_quant_q8k that also writes ysum = add + y (the residual sum of a layer)
+hipError_t launch_gemv_q8k_sum(const WeightsView &w, const float *x, float *y, const float *add, float *ysum,
+                               hipStream_t s);
 // Y[m] = W X[m] for m < M, with a library-owned workspace per (device,
 // stream), grown on demand.
 hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y,

@@ -134,7 +134,8 @@ uq_status project_q8k(const uq_weights *w, float *const *y, int n, const float *
 }
 
 // residual = x_in + attn_out and post_attention_norm of it (one launch), FFN,
-// l_out (:524-536 / :696-704, ffn :713-768)
+// l_out = residual + ffn_out with the down projection (:524-536 / :696-704,
+// ffn :713-768)
 uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const float *x_in, uq_weights g,
                    uq_weights u, uq_weights dn, const float *post_norm, float *ws, size_t nctx, float *l_out,
                    hipStream_t s) {
@@ -142,9 +143,9 @@ uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const
     UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_POST_NORM), (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, 1,
                                           d->rms_eps, s, at(UQ_NODE_ATTN_OUT), at(UQ_NODE_RESIDUAL)),
                   fn));
-    UQ_TRY(uq_ffn_swiglu_q8k(g, u, dn, at(UQ_NODE_POST_NORM), at(UQ_NODE_FFN_GATE), at(UQ_NODE_FFN_UP),
-                             at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT), s));
-    return hip_st(uq::launch_add(l_out, at(UQ_NODE_RESIDUAL), at(UQ_NODE_FFN_OUT), D.n, s), fn);
+    // the down projection also forms l_out = residual + ffn_out
+    return uq::ffn_swiglu_q8k_sum(g, u, dn, at(UQ_NODE_POST_NORM), at(UQ_NODE_FFN_GATE), at(UQ_NODE_FFN_UP),
+                                  at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT), at(UQ_NODE_RESIDUAL), l_out, s);
 }
 
 }  // namespace
@@ -199,16 +200,24 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
         float *const ys[4] = {qkv, at(UQ_NODE_Z), at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA)};
         UQ_TRY(project_q8k(ws4, ys, 4, at(UQ_NODE_ATTN_NORM), stream));
     }
-    // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419)
-    UQ_TRY(hip_st(uq::launch_gdn_gates(at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), w->ssm_dt_bias, w->ssm_a,
-                                       at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s), fn));
-    // 4) depthwise conv over [ring; qkv], silu, the ring's shift: one launch (:427-454)
-    UQ_TRY(hip_st(uq::launch_conv_step(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), at(UQ_NODE_CONV_SILU),
-                                       (int)D.ck, ch, s),
-                  fn));
-    // q and k parts l2-normalised per head (:463-464)
+    // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419);
+    // 4) depthwise conv over [ring; qkv], silu, the ring's shift (:427-454);
+    // the q and k parts l2-normalised per head (:463-464)
     float *qc = at(UQ_NODE_CONV_SILU), *kc = qc + D.nqk * D.hd, *vc = kc + D.nqk * D.hd;
-    UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
+    if (uq::conv_norm_ok(hd)) {  // one launch
+        UQ_TRY(hip_st(uq::launch_gdn_conv_norm(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, hd,
+                                               nqk, d->rms_eps, at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA),
+                                               w->ssm_dt_bias, w->ssm_a, at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS),
+                                               at(UQ_NODE_GATE), nv, s),
+                      fn));
+    } else {
+        UQ_TRY(hip_st(uq::launch_gdn_gates(at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), w->ssm_dt_bias, w->ssm_a,
+                                           at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s),
+                      fn));
+        UQ_TRY(hip_st(uq::launch_conv_step(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, s),
+                      fn));
+        UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
+    }
     // 5) gdn_fused_step per v head, q/k head h % n_qk, scale on the output (:470-492)
     const float scale = 1.0f / sqrtf((float)D.hd);
     UQ_TRY(hip_st(uq::launch_gdn_step(d_state, at(UQ_NODE_GDN_OUT), qc, kc, vc, at(UQ_NODE_GATE), at(UQ_NODE_BETA), hd,
@@ -264,21 +273,17 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
         UQ_TRY(project_q8k(ws3, ys, 3, at(UQ_NODE_ATTN_NORM), stream));
     }
     // q: rmsnorm of each head's first half (:585-599); k: rmsnorm per kv
-    // head, into the cache row (:611-623)
-    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_Q), ahd, at(UQ_NODE_QFULL), 2 * ahd, w->attn_q_norm, ahd, nh,
+    // head, into the cache row (:611-623); 4) IMROPE on both (:634-642): one launch
+    UQ_TRY(hip_st(uq::launch_attn_qk_prep(at(UQ_NODE_QFULL), at(UQ_NODE_Q), at(UQ_NODE_K_RAW), krow, w->attn_q_norm,
+                                          w->attn_k_norm, ahd, nh, nkv, (int)d->n_rot, d->theta_scale, pos,
                                           d->rms_eps, s),
                   fn));
-    UQ_TRY(hip_st(uq::launch_rmsnorm(krow, at(UQ_NODE_K_RAW), w->attn_k_norm, ahd, nkv, d->rms_eps, s), fn));
-    // 4) IMROPE on q and on the new k row (:634-642)
-    UQ_TRY(hip_st(uq::launch_rope_imrope(at(UQ_NODE_Q), nh, ahd, (int)d->n_rot, d->theta_scale, pos, s), fn));
-    UQ_TRY(hip_st(uq::launch_rope_imrope(krow, nkv, ahd, (int)d->n_rot, d->theta_scale, pos, s), fn));
-    // 5) causal attention over rows 0..pos (:647-675)
+    // 5) causal attention over rows 0..pos (:647-675); 6) attn * sigmoid(gate),
+    // the gate the second half of each head's q row (:677-684), formed by the
+    // attention's last kernel
     UQ_TRY(hip_st(uq::launch_attn_decode(at(UQ_NODE_ATTN), at(UQ_NODE_SOFT), at(UQ_NODE_Q), d_k_cache, d_v_cache,
-                                         (int)pos + 1, nkv, ahd, nh / nkv, d->kq_scale, s),
-                  fn));
-    // 6) attn * sigmoid(gate), gate the second half of each head's q row (:677-684)
-    UQ_TRY(hip_st(uq::launch_mul_act(0, at(UQ_NODE_GATED), at(UQ_NODE_ATTN), at(UQ_NODE_QFULL) + ahd, ahd, 2 * ahd,
-                                     D.nh * D.ahd, s),
+                                         (int)pos + 1, nkv, ahd, nh / nkv, d->kq_scale, s, at(UQ_NODE_QFULL) + ahd,
+                                         2 * ahd, at(UQ_NODE_GATED)),
                   fn));
     // 7) attn_output (:686-693), residual, FFN and l_out (:696-704)
     UQ_TRY(uq_gemv_q8k(w->attn_output, at(UQ_NODE_GATED), at(UQ_NODE_ATTN_OUT), stream));

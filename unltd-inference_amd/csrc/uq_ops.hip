@@ -485,7 +485,7 @@ __device__ double wave_pairwise(double (&t)[E]) {
 }
 
 constexpr int kAttnMaxGroup = 8;
-constexpr int kScoresPPB = 32;  // positions per workgroup (8 per wave)
+constexpr int kScoresPPB = 8;  // positions per workgroup (2 per wave)
 
 // scores[h][p] = (f32) dot_f32(q_h, K[p][kv]) for the group's heads; one
 // wave per position, E = hd / 64 values per lane.
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict_
                                                               int group) {
     constexpr int HD = 64 * E;
     __shared__ float qs[kAttnMaxGroup * HD];
-    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int t = threadIdx.x; t < group * HD; t += OPS_TPB) qs[t] = q[(size_t)kv * group * HD + t];
     __syncthreads();
     const size_t kv_len = (size_t)n_head_kv * HD;
@@ -532,6 +532,8 @@ __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict_
 // of e and S +- e); when both ends round to the same f32 (same bits) that
 // is the reference's value, else the lane replays the sequential loop.
 constexpr int kPvBatch = 16;  // positions whose V loads a wave issues before summing
+constexpr int kPvCoop = 4;    // at most this many replays per wave run one column at a time
+constexpr int kPvChunk = 8;   // positions per lane loaded at once in such a replay
 template <int G>
 constexpr int pv_waves() { return G <= 4 ? 16 : 8; }  // the LDS partials stay within 64 KB
 // G: q heads per kv head, compile-time so that a batch's loads issue back to back
@@ -539,10 +541,12 @@ template <int G>
 __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__restrict__ out,
                                                                     const float *__restrict__ soft,
                                                                     const float *__restrict__ vc, int n_ctx,
-                                                                    int n_head_kv, int hd) {
+                                                                    int n_head_kv, int hd,
+                                                                    const float *__restrict__ gz, int gzs,
+                                                                    float *__restrict__ gated) {
     constexpr int group = G, kPvWaves = pv_waves<G>();
     __shared__ double part[2][kPvWaves][G][64];
-    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = blockIdx.x * 64 + lane;
     const size_t kv_len = (size_t)n_head_kv * hd;
     const float *vcol = vc + (size_t)kv * hd + i;
@@ -588,26 +592,62 @@ __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__re
         const double e = (double)(n_ctx + 66) * 0x1p-52 * at;
         const float lo = (float)(st - e), hi = (float)(st + e);
         float r = lo;
-        if (__float_as_uint(lo) != __float_as_uint(hi)) {
-            // the reference's sequential sum (about 1e-4 of the outputs come
-            // here): loads in batches, the adds in order
-            constexpr int RB = 32;
-            double q = 0.0;
-            for (int p0 = 0; p0 < n_ctx; p0 += RB) {
-                float vb[RB], sb[RB];
+        // the reference's sequential sum where the bound cannot decide
+        // (about 1e-4 of the outputs)
+        const bool need = __float_as_uint(lo) != __float_as_uint(hi);
+        unsigned long long mask = __ballot(need);
+        if (__popcll(mask) > kPvCoop) {
+            // many columns: each lane replays its own, loads in batches, the adds in order
+            if (need) {
+                constexpr int RB = 32;
+                double q = 0.0;
+                for (int p0 = 0; p0 < n_ctx; p0 += RB) {
+                    float vb[RB], sb[RB];
 #pragma unroll
-                for (int u = 0; u < RB; u++) {
-                    const int p = min(p0 + u, n_ctx - 1);
-                    vb[u] = vcol[(size_t)p * kv_len];
-                    sb[u] = sr[(size_t)g * n_ctx + p];
+                    for (int u = 0; u < RB; u++) {
+                        const int p = min(p0 + u, n_ctx - 1);
+                        vb[u] = vcol[(size_t)p * kv_len];
+                        sb[u] = sr[(size_t)g * n_ctx + p];
+                    }
+#pragma unroll
+                    for (int u = 0; u < RB; u++)
+                        if (p0 + u < n_ctx) q += (double)sb[u] * (double)vb[u];
                 }
-#pragma unroll
-                for (int u = 0; u < RB; u++)
-                    if (p0 + u < n_ctx) q += (double)sb[u] * (double)vb[u];
+                r = (float)q;
             }
-            r = (float)q;
+        } else {
+            // a few columns: the wave replays them one at a time, every lane
+            // forming the products of its positions (loads in parallel) and
+            // all lanes adding them in position order (the same sum in each)
+            while (mask) {
+                const int l = __ffsll(mask) - 1;
+                mask &= mask - 1;
+                const float *vl = vc + (size_t)kv * hd + blockIdx.x * 64 + l;
+                double q = 0.0;
+                for (int p0 = 0; p0 < n_ctx; p0 += 64 * kPvChunk) {
+                    double t[kPvChunk];
+#pragma unroll
+                    for (int k = 0; k < kPvChunk; k++) {
+                        const int p = min(p0 + 64 * k + lane, n_ctx - 1);
+                        t[k] = (double)sr[(size_t)g * n_ctx + p] * (double)vl[(size_t)p * kv_len];
+                    }
+#pragma unroll
+                    for (int k = 0; k < kPvChunk; k++) {
+                        const int pk = p0 + 64 * k;
+                        if (pk >= n_ctx) break;  // wave-uniform
+                        const int lo32 = __double2loint(t[k]), hi32 = __double2hiint(t[k]);
+                        const int m = min(64, n_ctx - pk);
+                        for (int j = 0; j < m; j++)
+                            q += __hiloint2double(__builtin_amdgcn_readlane(hi32, j),
+                                                  __builtin_amdgcn_readlane(lo32, j));
+                    }
+                }
+                if (lane == l) r = (float)q;
+            }
         }
         out[(size_t)(kv * group + g) * hd + i] = r;
+        // the gated output (qwen35_forward.rs:677-684, as mul_act_kernel)
+        if (gated) gated[(size_t)(kv * group + g) * hd + i] = __fmul_rn(r, sigmoid1(gz[(size_t)(kv * group + g) * gzs + i]));
     }
 }
 
@@ -641,6 +681,102 @@ __global__ void add_kernel(float *__restrict__ out, const float *__restrict__ a,
                            size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = __fadd_rn(a[i], b[i]);
+}
+
+// One launch for the GatedDeltaNet steps between the projections and the
+// delta rule (qwen35_forward.rs:405-464): workgroup b < n_chunks runs the
+// conv step (as conv_step_kernel) over channels [b*hd, (b+1)*hd), and for
+// the q and k chunks (b < 2*n_qk) the l2 norm of the chunk (as l2norm_kernel,
+// the chunk's values kept in LDS); the last workgroup forms the gates (as
+// gdn_gates_kernel). Same operations in the same order as the three
+// kernels, so the same bits.
+constexpr int kConvNormMaxHd = 1024;
+__global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_kernel(
+    float *__restrict__ win, const float *__restrict__ kern, float *__restrict__ raw, float *__restrict__ act,
+    int d_conv, int channels, int hd, int n_qk, float eps, const float *__restrict__ beta_raw,
+    const float *__restrict__ alpha, const float *__restrict__ dt_bias, const float *__restrict__ a,
+    float *__restrict__ beta, float *__restrict__ sp, float *__restrict__ gate, int n_v) {
+    __shared__ float vals[kConvNormMaxHd];
+    __shared__ double red[OPS_TPB / 64];
+    __shared__ float bc;
+    const int b = blockIdx.x, n_chunks = channels / hd;
+    if (b == n_chunks) {
+        for (int h = threadIdx.x; h < n_v; h += OPS_TPB) {
+            beta[h] = sigmoid1(beta_raw[h]);
+            const float p = softplus1(__fadd_rn(alpha[h], dt_bias[h]));
+            sp[h] = p;
+            gate[h] = __fmul_rn(p, a[h]);
+        }
+        return;
+    }
+    const bool norm = b < 2 * n_qk;  // workgroup-uniform
+    double s = 0.0;
+    for (int j = threadIdx.x; j < hd; j += OPS_TPB) {
+        const int c = b * hd + j;
+        float x[9];
+        for (int r = 0; r < d_conv; r++) x[r] = win[(size_t)r * channels + c];
+        float t = 0.0f;
+        for (int tau = 0; tau < d_conv; tau++) t = __fadd_rn(t, __fmul_rn(x[tau], kern[(size_t)c * d_conv + tau]));
+        raw[c] = t;
+        const float v = silu1(t);
+        for (int r = 1; r < d_conv; r++) win[(size_t)(r - 1) * channels + c] = x[r];
+        if (norm) {
+            vals[j] = v;
+            s += (double)__fmul_rn(v, v);
+        } else {
+            act[c] = v;
+        }
+    }
+    if (!norm) return;
+    const double S = block_sum_d<OPS_TPB>(s, red);  // its barrier also publishes vals
+    const float sum32 = seq_sum_f32<OPS_TPB>([](int i) { return vals[i]; }, hd, S, [](double v) { return (float)v; },
+                                             &bc);
+    const float scale = __fdiv_rn(1.0f, fmaxf(sqrtf_cr(sum32), eps));
+    for (int j = threadIdx.x; j < hd; j += OPS_TPB) act[b * hd + j] = __fmul_rn(vals[j], scale);
+}
+
+// One launch for the attention layer's q and k preparation
+// (qwen35_forward.rs:585-642): workgroup h < n_head normalises the first
+// half of q head h (rmsnorm with attn_q_norm, as rmsnorm_kernel) into q_out
+// row h, workgroup n_head + j the raw k row of kv head j (attn_k_norm) into
+// k_out row j; then IMROPE rotates the row (as rope_imrope_kernel) before
+// it is stored.
+constexpr int kQkMaxHd = 512;
+__global__ __launch_bounds__(OPS_TPB) void attn_qk_prep_kernel(const float *__restrict__ qfull, float *__restrict__ q_out,
+                                                             const float *__restrict__ k_raw, float *__restrict__ k_out,
+                                                             const float *__restrict__ wq, const float *__restrict__ wk,
+                                                             int hd, int n_head, int n_rot, double theta_scale,
+                                                             double pos, float eps) {
+    __shared__ float rowv[kQkMaxHd];
+    __shared__ double red[OPS_TPB / 64];
+    __shared__ float bc;
+    const int b = blockIdx.x;
+    const bool isq = b < n_head;
+    const float *xr = isq ? qfull + (size_t)b * 2 * hd : k_raw + (size_t)(b - n_head) * hd;
+    const float *w = isq ? wq : wk;
+    float *yr = isq ? q_out + (size_t)b * hd : k_out + (size_t)(b - n_head) * hd;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < hd; i += OPS_TPB) {
+        const float v = xr[i];
+        rowv[i] = v;
+        s += (double)__fmul_rn(v, v);
+    }
+    const double S = block_sum_d<OPS_TPB>(s, red);  // its barrier also publishes rowv
+    const double dn = (double)hd;
+    const float mean = seq_sum_f32<OPS_TPB>([](int i) { return rowv[i]; }, hd, S,
+                                            [dn](double u) { return (float)(u / dn); }, &bc);
+    const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
+    for (int i = threadIdx.x; i < hd; i += OPS_TPB) rowv[i] = __fmul_rn(__fmul_rn(rowv[i], scale), w[i]);
+    __syncthreads();
+    const int half = n_rot / 2, nrot3 = (half + 2) / 3;
+    for (int t = threadIdx.x; t < nrot3; t += OPS_TPB) {
+        const int ic = 3 * t;
+        double angle = pos;
+        for (int i = 0; i < ic; i++) angle *= theta_scale;
+        rotate_pair(&rowv[ic], &rowv[ic + half], angle);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < hd; i += OPS_TPB) yr[i] = rowv[i];
 }
 
 inline unsigned ops_grid(size_t n) {
@@ -729,7 +865,8 @@ bool attn_shape_ok(int hd, int group) {
 }
 
 hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
-                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s) {
+                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s, const float *gz,
+                              int gzs, float *gated) {
     if (n_ctx <= 0 || n_head_kv <= 0) return hipSuccess;
     if (!attn_shape_ok(hd, group) || n_ctx > softmax_max_len()) return hipErrorInvalidValue;
     const dim3 gs((n_ctx + kScoresPPB - 1) / kScoresPPB, n_head_kv);
@@ -745,7 +882,7 @@ hipError_t launch_attn_decode(float *out, float *soft, const float *q, const flo
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const dim3 gp(hd / 64, n_head_kv);
 #define UQ_PV(G) hipLaunchKernelGGL(attn_pv_kernel<G>, gp, dim3(pv_waves<G>() * 64), 0, s, out, soft, vc, n_ctx, \
-                                    n_head_kv, hd)
+                                    n_head_kv, hd, gz, gzs, gated)
     switch (group) {
         case 1: UQ_PV(1); break;
         case 2: UQ_PV(2); break;
@@ -781,6 +918,29 @@ hipError_t launch_mul_act(int op, float *out, const float *y, const float *z, in
                           hipStream_t s) {
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(mul_act_kernel, dim3(ops_grid(total)), dim3(OPS_TPB), 0, s, op, out, y, z, n, zs, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_conv_norm(float *win, const float *kern_gguf, float *raw, float *act, int d_conv, int channels,
+                                int hd, int n_qk, float eps, const float *beta_raw, const float *alpha,
+                                const float *dt_bias, const float *a, float *beta, float *sp, float *gate, int n_v,
+                                hipStream_t s) {
+    if (d_conv < 1 || d_conv > 9 || hd < 1 || hd > kConvNormMaxHd || channels % hd || 2 * n_qk > channels / hd)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_conv_norm_kernel, dim3(channels / hd + 1), dim3(OPS_TPB), 0, s, win, kern_gguf, raw, act,
+                       d_conv, channels, hd, n_qk, eps, beta_raw, alpha, dt_bias, a, beta, sp, gate, n_v);
+    return hipGetLastError();
+}
+
+bool conv_norm_ok(int hd) { return hd >= 1 && hd <= kConvNormMaxHd; }
+
+hipError_t launch_attn_qk_prep(const float *qfull, float *q_out, const float *k_raw, float *k_out, const float *wq,
+                               const float *wk, int hd, int n_head, int n_head_kv, int n_rot, double theta_scale,
+                               size_t pos, float eps, hipStream_t s) {
+    if (hd < 1 || hd > kQkMaxHd || n_rot > hd || n_rot % 2) return hipErrorInvalidValue;
+    if (n_head + n_head_kv == 0) return hipSuccess;
+    hipLaunchKernelGGL(attn_qk_prep_kernel, dim3(n_head + n_head_kv), dim3(OPS_TPB), 0, s, qfull, q_out, k_raw, k_out,
+                       wq, wk, hd, n_head, n_rot, theta_scale, (double)pos, eps);
     return hipGetLastError();
 }
 
