@@ -102,13 +102,16 @@ __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ ou
     float *yr = out + (size_t)blockIdx.x * ys;
     auto val = [&](int i) { return xbr ? __fadd_rn(xr[i], xbr[i]) : xr[i]; };
     constexpr int R = PT > 0 ? PT : 1;
-    float v[R];
+    float v[R], wv[R], zv[R];
     double s = 0.0;
     if constexpr (PT > 0) {
+        // the weights and z are loaded with x, before the sum
 #pragma unroll
         for (int k = 0; k < PT; k++) {
             const int i = threadIdx.x + k * OPS_TPB;
             v[k] = i < n ? val(i) : 0.0f;
+            wv[k] = i < n ? w[i] : 0.0f;
+            zv[k] = (z && i < n) ? z[(size_t)blockIdx.x * ys + i] : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < PT; k++) {
@@ -129,19 +132,20 @@ __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ ou
     const double dn = (double)n;
     const float mean = seq_sum_f32<OPS_TPB>(val, n, S, [dn](double u) { return (float)(u / dn); }, &bc);
     const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
-    auto emit = [&](int i, float t) {
-        float y = __fmul_rn(__fmul_rn(t, scale), w[i]);
-        if (z) y = __fmul_rn(y, silu1(z[(size_t)blockIdx.x * ys + i]));
+    auto emit = [&](int i, float t, float wi, float zi) {
+        float y = __fmul_rn(__fmul_rn(t, scale), wi);
+        if (z) y = __fmul_rn(y, silu1(zi));
         yr[i] = y;
     };
     if constexpr (PT > 0) {
 #pragma unroll
         for (int k = 0; k < PT; k++) {
             const int i = threadIdx.x + k * OPS_TPB;
-            if (i < n) emit(i, v[k]);
+            if (i < n) emit(i, v[k], wv[k], zv[k]);
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += OPS_TPB) emit(i, val(i));
+        for (int i = threadIdx.x; i < n; i += OPS_TPB)
+            emit(i, val(i), w[i], z ? z[(size_t)blockIdx.x * ys + i] : 0.0f);
     }
 }
 
@@ -317,18 +321,20 @@ __global__ __launch_bounds__(256) void gdn_step_wg_kernel(float *__restrict__ st
     __shared__ float kq[2][128];
     const int h = blockIdx.y, hq = h % n_qk, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int j = blockIdx.x * 64 + lane;
+    const bool live = j < dim;
+    const int i0 = kGdnRows * wv;
+    float *S = state + (size_t)h * dim * dim + (live ? j : 0);
+    // every global load first (state rows, v, gate, beta, k, q), one round trip
+    float c[kGdnRows];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r++) c[r] = (i0 + r < dim && live) ? S[(size_t)(i0 + r) * dim] : 0.0f;
+    const float vj = live ? v[(size_t)h * dim + j] : 0.0f, gh = gate[h], bt = beta[h];
     if (threadIdx.x < dim) {
         kq[0][threadIdx.x] = k[(size_t)hq * dim + threadIdx.x];
         kq[1][threadIdx.x] = q[(size_t)hq * dim + threadIdx.x];
     }
     __syncthreads();
-    const bool live = j < dim;
-    const int i0 = kGdnRows * wv;
-    float *S = state + (size_t)h * dim * dim + (live ? j : 0);
-    const float g_exp = expf_cr(gate[h]), bt = beta[h];
-    float c[kGdnRows];
-#pragma unroll
-    for (int r = 0; r < kGdnRows; r++) c[r] = (i0 + r < dim && live) ? S[(size_t)(i0 + r) * dim] : 0.0f;
+    const float g_exp = expf_cr(gh);
 #pragma unroll
     for (int r = 0; r < kGdnRows; r++) c[r] = __fmul_rn(c[r], g_exp);
     // (float) of the sequential f64 sum over i < dim of c_i * kq[sel][i]
@@ -362,7 +368,7 @@ __global__ __launch_bounds__(256) void gdn_step_wg_kernel(float *__restrict__ st
         return (float)qq;
     };
     const float sum = dot(0);
-    const float d = __fmul_rn(__fsub_rn(live ? v[(size_t)h * dim + j] : 0.0f, sum), bt);
+    const float d = __fmul_rn(__fsub_rn(vj, sum), bt);
 #pragma unroll
     for (int r = 0; r < kGdnRows; r++)
         if (i0 + r < dim) {
@@ -582,13 +588,15 @@ __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__re
         part[1][w][g][lane] = A[g];
     }
     __syncthreads();
+    double st = 0.0, at = 0.0;
+    if (w < group)
+        for (int u = 0; u < kPvWaves; u++) {
+            st += part[0][u][w][lane];
+            at += part[1][u][w][lane];
+        }
+    __syncthreads();  // part is free: a replay below uses it as its wave's scratch
     if (w < group) {
         const int g = w;
-        double st = 0.0, at = 0.0;
-        for (int u = 0; u < kPvWaves; u++) {
-            st += part[0][u][g][lane];
-            at += part[1][u][g][lane];
-        }
         const double e = (double)(n_ctx + 66) * 0x1p-52 * at;
         const float lo = (float)(st - e), hi = (float)(st + e);
         float r = lo;
@@ -617,30 +625,47 @@ __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__re
             }
         } else {
             // a few columns: the wave replays them one at a time, every lane
-            // forming the products of its positions (loads in parallel) and
-            // all lanes adding them in position order (the same sum in each)
+            // forming the products of its positions (loads in parallel) into
+            // the wave's LDS scratch, then all lanes adding them in position
+            // order (broadcast reads; the same sum in each lane)
+            double *buf = &part[0][0][0][0] + (size_t)w * 64 * kPvChunk;  // within part: kPvWaves >= 4
             while (mask) {
                 const int l = __ffsll(mask) - 1;
                 mask &= mask - 1;
                 const float *vl = vc + (size_t)kv * hd + blockIdx.x * 64 + l;
                 double q = 0.0;
                 for (int p0 = 0; p0 < n_ctx; p0 += 64 * kPvChunk) {
-                    double t[kPvChunk];
 #pragma unroll
                     for (int k = 0; k < kPvChunk; k++) {
                         const int p = min(p0 + 64 * k + lane, n_ctx - 1);
-                        t[k] = (double)sr[(size_t)g * n_ctx + p] * (double)vl[(size_t)p * kv_len];
+                        buf[64 * k + lane] = (double)sr[(size_t)g * n_ctx + p] * (double)vl[(size_t)p * kv_len];
                     }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    const int m = min(64 * kPvChunk, n_ctx - p0);
+                    // the reads of the next 8 values issue before the adds of these 8
+                    int p = 0;
+                    double b[8];
+                    if (m >= 8) {
 #pragma unroll
-                    for (int k = 0; k < kPvChunk; k++) {
-                        const int pk = p0 + 64 * k;
-                        if (pk >= n_ctx) break;  // wave-uniform
-                        const int lo32 = __double2loint(t[k]), hi32 = __double2hiint(t[k]);
-                        const int m = min(64, n_ctx - pk);
-                        for (int j = 0; j < m; j++)
-                            q += __hiloint2double(__builtin_amdgcn_readlane(hi32, j),
-                                                  __builtin_amdgcn_readlane(lo32, j));
+                        for (int u = 0; u < 8; u++) b[u] = buf[u];
                     }
+                    for (; p + 8 <= m; p += 8) {
+                        double nb[8];
+                        const int pn = p + 16 <= m ? p + 8 : p;  // the last batch rereads itself
+#pragma unroll
+                        for (int u = 0; u < 8; u++) nb[u] = buf[pn + u];
+#pragma unroll
+                        for (int u = 0; u < 8; u++) q += b[u];
+#pragma unroll
+                        for (int u = 0; u < 8; u++) b[u] = nb[u];
+                    }
+                    for (; p < m; p++) q += buf[p];
+                    // every lane's reads are done before the next chunk's writes
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 }
                 if (lane == l) r = (float)q;
             }
@@ -756,6 +781,12 @@ __global__ __launch_bounds__(OPS_TPB) void attn_qk_prep_kernel(const float *__re
     const float *w = isq ? wq : wk;
     float *yr = isq ? q_out + (size_t)b * hd : k_out + (size_t)(b - n_head) * hd;
     double s = 0.0;
+    float wr[kQkMaxHd / OPS_TPB];  // the weights, loaded with x
+#pragma unroll
+    for (int k = 0; k < kQkMaxHd / OPS_TPB; k++) {
+        const int i = threadIdx.x + k * OPS_TPB;
+        wr[k] = i < hd ? w[i] : 0.0f;
+    }
     for (int i = threadIdx.x; i < hd; i += OPS_TPB) {
         const float v = xr[i];
         rowv[i] = v;
@@ -766,7 +797,11 @@ __global__ __launch_bounds__(OPS_TPB) void attn_qk_prep_kernel(const float *__re
     const float mean = seq_sum_f32<OPS_TPB>([](int i) { return rowv[i]; }, hd, S,
                                             [dn](double u) { return (float)(u / dn); }, &bc);
     const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
-    for (int i = threadIdx.x; i < hd; i += OPS_TPB) rowv[i] = __fmul_rn(__fmul_rn(rowv[i], scale), w[i]);
+#pragma unroll
+    for (int k = 0; k < kQkMaxHd / OPS_TPB; k++) {
+        const int i = threadIdx.x + k * OPS_TPB;
+        if (i < hd) rowv[i] = __fmul_rn(__fmul_rn(rowv[i], scale), wr[k]);
+    }
     __syncthreads();
     const int half = n_rot / 2, nrot3 = (half + 2) / 3;
     for (int t = threadIdx.x; t < nrot3; t += OPS_TPB) {
