@@ -88,14 +88,17 @@ __device__ __forceinline__ float softplus1(float v) { return v > 20.0f ? v : log
 // the row normalised is x + xb (an f32 add), also written to xsum (the
 // residual and the norm after it, qwen35_forward.rs:525-530); with z the
 // output is multiplied by silu(z) (the gated norm, :495-511; z in the
-// output's layout). PT > 0 (n <= PT * OPS_TPB): a thread's elements are
-// loaded once, all before the sum, and kept in registers.
-template <int PT>
-__global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
-                                                          const float *__restrict__ w, int n, float eps, int xs,
-                                                          int ys, const float *__restrict__ xb,
-                                                          float *__restrict__ xsum, const float *__restrict__ z) {
-    __shared__ double red[OPS_TPB / 64];
+// output's layout). PT > 0 (n <= PT * TPB): a thread's elements are
+// loaded once, all before the sum, and kept in registers. Rows up to 4096
+// run on 1024 threads (four elements each: the per-thread chains of loads
+// and f64 adds are a quarter as long; 3.2 us per 4096-row in a graph against
+// 5.0 us on 256 threads).
+template <int PT, int TPB = OPS_TPB>
+__global__ __launch_bounds__(TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
+                                                      const float *__restrict__ w, int n, float eps, int xs,
+                                                      int ys, const float *__restrict__ xb,
+                                                      float *__restrict__ xsum, const float *__restrict__ z) {
+    __shared__ double red[TPB / 64];
     __shared__ float bc;
     const float *xr = x + (size_t)blockIdx.x * xs;
     const float *xbr = xb ? xb + (size_t)blockIdx.x * xs : nullptr;
@@ -108,29 +111,29 @@ __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ ou
         // the weights and z are loaded with x, before the sum
 #pragma unroll
         for (int k = 0; k < PT; k++) {
-            const int i = threadIdx.x + k * OPS_TPB;
+            const int i = threadIdx.x + k * TPB;
             v[k] = i < n ? val(i) : 0.0f;
             wv[k] = i < n ? w[i] : 0.0f;
             zv[k] = (z && i < n) ? z[(size_t)blockIdx.x * ys + i] : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < PT; k++) {
-            const int i = threadIdx.x + k * OPS_TPB;
+            const int i = threadIdx.x + k * TPB;
             if (i < n) {
                 if (xsum) xsum[(size_t)blockIdx.x * xs + i] = v[k];
                 s += (double)__fmul_rn(v[k], v[k]);
             }
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += OPS_TPB) {
+        for (int i = threadIdx.x; i < n; i += TPB) {
             const float t = val(i);
             if (xsum) xsum[(size_t)blockIdx.x * xs + i] = t;
             s += (double)__fmul_rn(t, t);
         }
     }
-    const double S = block_sum_d<OPS_TPB>(s, red);
+    const double S = block_sum_d<TPB>(s, red);
     const double dn = (double)n;
-    const float mean = seq_sum_f32<OPS_TPB>(val, n, S, [dn](double u) { return (float)(u / dn); }, &bc);
+    const float mean = seq_sum_f32<TPB>(val, n, S, [dn](double u) { return (float)(u / dn); }, &bc);
     const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
     auto emit = [&](int i, float t, float wi, float zi) {
         float y = __fmul_rn(__fmul_rn(t, scale), wi);
@@ -140,11 +143,11 @@ __global__ __launch_bounds__(OPS_TPB) void rmsnorm_kernel(float *__restrict__ ou
     if constexpr (PT > 0) {
 #pragma unroll
         for (int k = 0; k < PT; k++) {
-            const int i = threadIdx.x + k * OPS_TPB;
+            const int i = threadIdx.x + k * TPB;
             if (i < n) emit(i, v[k], wv[k], zv[k]);
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += OPS_TPB)
+        for (int i = threadIdx.x; i < n; i += TPB)
             emit(i, val(i), w[i], z ? z[(size_t)blockIdx.x * ys + i] : 0.0f);
     }
 }
@@ -830,6 +833,9 @@ hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const
     if (rows == 0 || n == 0) return hipSuccess;
     if (n <= OPS_TPB)
         hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
+    else if (n <= 4 * 1024)  // wider rows: 1024 threads, four elements each
+        hipLaunchKernelGGL((rmsnorm_kernel<4, 1024>), dim3(rows), dim3(1024), 0, s, out, x, w, n, eps, xs, ys, xb, xsum,
+                           z);
     else if (n <= 16 * OPS_TPB)
         hipLaunchKernelGGL(rmsnorm_kernel<16>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
     else
