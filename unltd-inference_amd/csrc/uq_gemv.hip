@@ -930,12 +930,11 @@ Segs one_seg(const WeightsView &w, const uint8_t *w2, float *y) {
 // ---------------------------- gemv_quant_q8k -------------------------------
 // quantize_q8_k (quants.rs:250-290) of one 256-block by one wave into LDS:
 // q = 64 dwords of qs, bs = 16 bsums, *d = block scale.
-__device__ void quantize_block_lds(const float *__restrict__ c, int lane, uint32_t *q, int *bs, float *dq) {
-    float v[4];
+// v: the lane's four values of the block (elements 4 lane .. 4 lane + 3).
+__device__ __forceinline__ void quantize_vals_lds(const float (&v)[4], int lane, uint32_t *q, int *bs, float *dq) {
     float am = 0.0f, mx = 0.0f;
     int idx = 0x7FFFFFFF;
     for (int i = 0; i < 4; i++) {
-        v[i] = c[lane * 4 + i];
         const float a = fabsf(v[i]);
         if (a > am) {
             am = a;
@@ -974,6 +973,28 @@ __device__ void quantize_block_lds(const float *__restrict__ c, int lane, uint32
     if ((lane & 3) == 0) bs[lane >> 2] = s;
 }
 
+// Blocks first, first + step, ... < nblk of x by one wave, as
+// quantize_vals_lds; the loads of four blocks issue before any of them is
+// processed, so their latencies overlap.
+__device__ __forceinline__ void quantize_blocks_lds(const float *__restrict__ x, int first, int step, int nblk,
+                                                    int lane, uint32_t *q, int *bs, float *d8) {
+    for (int b0 = first; b0 < nblk; b0 += 4 * step) {
+        float v[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int b = b0 + j * step;
+            if (b < nblk)  // wave-uniform
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[j][i] = x[256 * b + lane * 4 + i];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int b = b0 + j * step;
+            if (b < nblk) quantize_vals_lds(v[j], lane, q + 64 * b, bs + 16 * b, d8 + b);
+        }
+    }
+}
+
 struct Q8KLayout {
     size_t xq, d8, region, total;  // byte offsets
     int R;                         // rows per epilogue batch
@@ -1007,7 +1028,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
     int *bst = (int *)(lds + L.region + K);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 
-    for (int b = wid; b < nblk; b += WAVES) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    quantize_blocks_lds(x, wid, WAVES, nblk, lane, qtmp, bst, d8);
     __syncthreads();
     for (int t = threadIdx.x; t < ntask; t += TPB)
         F::build_task(xq + (size_t)t * F::kDw, qtmp + 64 * (t >> 2), bst + 16 * (t >> 2), t & 3);
@@ -1160,7 +1181,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     };
     issue(0);
 
-    for (int b = wv; b < nblk; b += NW) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    quantize_blocks_lds(x, wv, NW, nblk, lane, qtmp, bst, d8);
     __syncthreads();
     for (int t = threadIdx.x; t < ntask; t += 64 * NW)
         F::build_task(xq + (size_t)t * F::kDw, qtmp + 64 * (t >> 2), bst + 16 * (t >> 2), t & 3);
@@ -1321,7 +1342,7 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
     };
     issue(0);
 
-    for (int b = wv; b < nblk; b += NW) quantize_block_lds(x + 256 * b, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+    quantize_blocks_lds(x, wv, NW, nblk, lane, qtmp, bst, d8);
     __syncthreads();
     for (int q = threadIdx.x; q < ntask; q += 64 * NW)
         F::build_task(xq + (size_t)q * F::kDw, qtmp + 64 * (q >> 2), bst + 16 * (q >> 2), q & 3);
@@ -1408,7 +1429,7 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_generic_kernel(uq_dtype dt, cons
     int *bs = (int *)(lds + K);
     float *d8 = (float *)(lds + K + (K / 16) * 4);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    for (int b = wid; b < nblk; b += WAVES) quantize_block_lds(x + 256 * b, lane, q + 64 * b, bs + 16 * b, d8 + b);
+    quantize_blocks_lds(x, wid, WAVES, nblk, lane, q, bs, d8);
     __syncthreads();
     const int8_t *qs = (const int8_t *)q;
     for (int row = blockIdx.x * TPB + threadIdx.x; row < N; row += gridDim.x * TPB) {
