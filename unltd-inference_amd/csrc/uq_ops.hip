@@ -304,22 +304,22 @@ __global__ void gdn_step_kernel(float *__restrict__ state, float *__restrict__ o
 }
 
 // The same step for dim <= 128 with the column in VGPRs: a workgroup of
-// four waves per 64 columns of a head, grid (dim / 64, heads); wave w holds
-// rows [32w, 32w + 32) of the 64 columns, loaded once and stored once.
-// Each f64 dot is the four waves' partial sums (each in row order) added in
+// eight waves per 64 columns of a head, grid (dim / 64, heads); wave w holds
+// rows [16w, 16w + 16) of the 64 columns, loaded once and stored once.
+// Each f64 dot is the eight waves' partial sums (each in row order) added in
 // LDS, plus a bound: any order of summing n terms lies within
 // (n - 1) 2^-53 sum|t| of the exact sum, as does the reference's
 // sequential loop, so when both ends of [S - e, S + e] round to one f32
 // that is the reference's (float)sum. Otherwise (rarely; the decision is
 // the same for every wave) the column goes through LDS and the loop runs in
 // the reference's order.
-constexpr int kGdnRows = 32;  // rows per wave
-__global__ __launch_bounds__(256) void gdn_step_wg_kernel(float *__restrict__ state, float *__restrict__ out,
+constexpr int kGdnWaves = 8, kGdnRows = 16;  // waves per workgroup, rows per wave
+__global__ __launch_bounds__(64 * kGdnWaves) void gdn_step_wg_kernel(float *__restrict__ state, float *__restrict__ out,
                                                          const float *__restrict__ q, const float *__restrict__ k,
                                                          const float *__restrict__ v, const float *__restrict__ gate,
                                                          const float *__restrict__ beta, int dim, float scale,
                                                          int n_qk) {
-    __shared__ double ps[4][64], pa[4][64];
+    __shared__ double ps[kGdnWaves][64], pa[kGdnWaves][64];
     __shared__ float col[128][64];  // the column, for the ordered replay
     __shared__ float kq[2][128];
     const int h = blockIdx.y, hq = h % n_qk, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -353,8 +353,12 @@ __global__ __launch_bounds__(256) void gdn_step_wg_kernel(float *__restrict__ st
         ps[wv][lane] = s;
         pa[wv][lane] = a;
         __syncthreads();
-        const double S4 = (ps[0][lane] + ps[1][lane]) + (ps[2][lane] + ps[3][lane]);
-        const double A4 = (pa[0][lane] + pa[1][lane]) + (pa[2][lane] + pa[3][lane]);
+        double S4 = 0.0, A4 = 0.0;
+#pragma unroll
+        for (int u = 0; u < kGdnWaves; u++) {
+            S4 += ps[u][lane];
+            A4 += pa[u][lane];
+        }
         __syncthreads();  // ps / pa are free for the next dot
         const double e = (double)(dim + 66) * 0x1p-52 * A4;
         const float lo = (float)(S4 - e), hi = (float)(S4 + e);
@@ -876,9 +880,9 @@ hipError_t launch_gdn_step(float *state, float *out, const float *q, const float
                            const float *beta, int dim, int heads, float scale, hipStream_t s, int n_qk) {
     if (heads == 0 || dim == 0) return hipSuccess;
     const int nq = n_qk > 0 ? n_qk : heads;
-    if (dim <= 4 * kGdnRows) {
-        hipLaunchKernelGGL(gdn_step_wg_kernel, dim3((dim + 63) / 64, heads), dim3(256), 0, s, state, out, q, k, v, gate,
-                           beta, dim, scale, nq);
+    if (dim <= kGdnWaves * kGdnRows) {
+        hipLaunchKernelGGL(gdn_step_wg_kernel, dim3((dim + 63) / 64, heads), dim3(64 * kGdnWaves), 0, s, state, out, q,
+                           k, v, gate, beta, dim, scale, nq);
         return hipGetLastError();
     }
     const int tpb = dim >= 256 ? 256 : ((dim + 63) / 64) * 64;
