@@ -157,6 +157,8 @@ GEMV_CASES = [
     (S.Q6_K, 20480, 97),
     (S.Q6_K, 256, 5), (S.Q6_K, 4096, 4096), (S.Q6_K, 12288, 512), (S.Q6_K, 2048, 301),
     (S.Q8_0, 4096, 4096), (S.Q8_0, 64, 9), (S.Q8_0, 4064, 33),  # K % 64 == 32: generic kernel
+    # Q8_0 rows of 256 to 4096 weights (the register-fed kernel)
+    (S.Q8_0, 256, 5), (S.Q8_0, 1024, 77), (S.Q8_0, 2048, 301), (S.Q8_0, 3072, 100), (S.Q8_0, 512, 3000),
     (S.F32, 4096, 64),
 ]
 
