@@ -36,10 +36,10 @@
 //  * Activation fragments come from global memory straight into VGPRs,
 //    D k-steps ahead; the prep wrote them so that each fragment load is
 //    two contiguous 512-byte runs.
-//  * B fragments are read from LDS two k-steps ahead into a four-slot
-//    register ring. One barrier per sub-step, after its second k-step: the
+//  * B fragments are read from LDS one k-step ahead into a two-slot
+//    register ring. One barrier per sub-step, after its third k-step: the
 //    next sub-step's B tile is complete and this one's slot is no longer
-//    read (its last fragments were read in k-step 1).
+//    read (its last fragments were read in k-step 2).
 // Workgroups are ordered so that each XCD takes mostly one M tile (its
 // activation planes stay in that XCD's L2). When the tiles do not cover the
 // CUs (small M), K is split into ranges, one workgroup per (tile, range),
@@ -398,11 +398,11 @@ struct GQ80 {
     __device__ static void block_consts(const uint8_t *, uint8_t *, float *) {}
 };
 
-template <class BP, int NTILE>
+template <class BP, int NTILE, int TPB = GTPB>
 struct GemmLayout {
     static constexpr int TN = 32 * NTILE;
     static constexpr int CHUNKS = TN * BP::CPR;                    // 16-byte chunks per block
-    static constexpr int RAWR = (CHUNKS + GTPB - 1) / GTPB;        // direct-to-LDS rounds per block
+    static constexpr int RAWR = (CHUNKS + TPB - 1) / TPB;          // direct-to-LDS rounds per block
     static constexpr int RAWSLOT = CHUNKS * 16;
     static constexpr int BTSLOT = BP::NBT * 4 * NTILE * 1024;
     static constexpr int BMSLOT = BP::kMin ? TN * 32 : 0;
@@ -413,8 +413,10 @@ struct GemmLayout {
     // 11 of the block before, read up to k-step 9), where the LDS has room
     static constexpr bool SUB = BP::kSub && SC + 3 * TN * 16 <= 160 * 1024;
     static constexpr int BYTES = SC + (SUB ? 3 * TN * 16 : 0);
-    // dequant tasks per wave and sub-step: columns lane + 64(w/4) + 128 i
-    static constexpr int NDQ = (TN + 127) / 128;
+    // dequant tasks per wave and sub-step: columns lane + 64(w/4) + 64 QW i,
+    // QW waves per quarter of the k-octets
+    static constexpr int QW = TPB / 256;
+    static constexpr int NDQ = (TN + 64 * QW - 1) / (64 * QW);
 };
 
 // The k-step of a block at which raw-load round r (of RAWR) of the block two
@@ -424,12 +426,13 @@ __device__ constexpr int raw_step(int r, int R) { return 11 + (r * 5) / R; }
 
 // ------------------------------------------------------------ GEMM kernel
 template <class BP, int WM, int WN, int NT, bool C64, int D>
-__global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(
+__global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu(WM * WN / 4))) void gemm_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ntn, int ks,
     float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
-    static_assert(WM * WN == GTPB / 64, "one wave per (wm, wn)");
+    static_assert(WM * WN == 8 || WM * WN == 4, "one wave per (wm, wn): two or one per SIMD");
+    constexpr int TPB = 64 * WM * WN;
     constexpr int TM = 32 * WM, NTILE = NT * WN;
-    using Lay = GemmLayout<BP, NTILE>;
+    using Lay = GemmLayout<BP, NTILE, TPB>;
     constexpr int TN = Lay::TN, RAWR = Lay::RAWR, NDQ = Lay::NDQ;
     static_assert(16 % D == 0, "D: activation fragments in flight, in k-steps, divides 16");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -449,20 +452,20 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
 
     const int wm = wv / WN, wn = wv % WN, lr = lane & 31, lh = lane >> 5;
 
-    // raw-weight loads: chunk GTPB*r + t of a block's ring slot is 16 bytes
+    // raw-weight loads: chunk TPB*r + t of a block's ring slot is 16 bytes
     // of column (chunk / CPR); lanes past the last chunk load nothing
     uint32_t roff[RAWR];
 #pragma unroll
     for (int r = 0; r < RAWR; r++) {
-        const int c = GTPB * r + t, col = min(c / BP::CPR, TN - 1), part = c % BP::CPR;
+        const int c = TPB * r + t, col = min(c / BP::CPR, TN - 1), part = c % BP::CPR;
         roff[r] = (uint32_t)min(n0 + col, N - 1) * row_bytes + 16u * (uint32_t)part;
     }
     const uint8_t *wbase = W + (size_t)kb0 * BP::RB;
     auto raw_load = [&](int b, int r) {  // round r of block b (clamped to the range)
         const int bb = min(b, nblk - 1);
-        if (GTPB * r + t < Lay::CHUNKS)
+        if (TPB * r + t < Lay::CHUNKS)
             dma16(wbase + (size_t)bb * BP::RB + roff[r],
-                  lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + GTPB * 16 * r + 1024 * wv);
+                  lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + TPB * 16 * r + 1024 * wv);
     };
 
     // activation fragments: row m of this wave's tile, octet 2 kk + lh.
@@ -483,16 +486,17 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     const uint32_t goff = (uint32_t)am * 32u + 16u * lh;
     auto g_load = [&](int b) { return buf_load16(rg, goff, (uint32_t)(kb0 + min(b, nblk - 1)) * (uint32_t)M * 32u); };
 
-    // dequant role: quarter wv%4 of columns lane + 64(wv/4) + 128 i
+    // dequant role: quarter wv%4 of columns lane + 64(wv/4) + 64 QW i
+    constexpr int QW = Lay::QW;  // waves per quarter: column stride 64 QW between a wave's tasks
     const int dq_c = wv & 3, dq_col0 = lane + 64 * (wv >> 2);
     // Task i (k-step i of the sub-step before) of sub-step sv (0..3, known
     // at compile time) of block blk.
     auto dequant = [&](int blk, int sv, int i) {
-        // where TN is not a multiple of 128 (192), the upper-half waves have
-        // no second task (a wave-uniform branch)
-        if constexpr (TN % 128 != 0)
-            if (64 * (wv >> 2) + 128 * i >= TN) return;
-        const int col = dq_col0 + 128 * i;
+        // where TN is not a multiple of 64 QW (192 on eight waves), the
+        // upper-half waves have no last task (a wave-uniform branch)
+        if constexpr (TN % (64 * QW) != 0)
+            if (64 * (wv >> 2) + 64 * QW * i >= TN) return;
+        const int col = dq_col0 + 64 * QW * i;
         const uint8_t *rc = lds + Lay::RAW + (blk & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
         uint8_t *bt = lds + Lay::BT + (sv & 1) * Lay::BTSLOT;
         if constexpr (Lay::SUB) {
@@ -516,7 +520,7 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
             }
         }
         if constexpr (Lay::SUB) {
-            for (int p = t; p < 3 * TN; p += GTPB) {
+            for (int p = t; p < 3 * TN; p += TPB) {
                 const int sv = 1 + p / TN, col = p - (sv - 1) * TN;
                 const uint8_t *rc = lds + Lay::RAW + (b & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
                 *(u4 *)(lds + Lay::SC + p * 16) = BP::sub_consts(rc, sv);
@@ -541,8 +545,9 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     h8 ah[D], al[D];
     h8 gmin;  // this lane's group sums of the current block (Q4_K)
-    // B operands of k-step t in ring slot t % 4, read two k-steps ahead
-    h8 bring[4][BP::NBT][NT];
+    // B operands of k-step t in ring slot t % 2, read one k-step ahead
+    static_assert(NDQ <= 3, "the dequantization tasks run in k-steps 0-2, before the sub-step's barrier");
+    h8 bring[2][BP::NBT][NT];
     auto b_read = [&](h8 (&dst)[BP::NBT][NT], int v, int tt) {
         const uint8_t *bt = lds + Lay::BT + (v & 1) * Lay::BTSLOT;
 #pragma unroll
@@ -572,7 +577,6 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int i = 0; i < NDQ; i++) dequant(0, 0, i);
     lds_barrier();
     b_read(bring[0], 0, 0);
-    b_read(bring[1], 0, 1);
 
     for (int kb = 0; kb < nblk; kb++) {
 #pragma unroll
@@ -589,11 +593,11 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
             if constexpr (BP::kMin)
                 if (t16 == 14) gmin = g_load(kb + 1);
             // then one region the scheduler can interleave: B operands of
-            // k-step t16+2 (the next sub-step's after the barrier), the
+            // k-step t16+1 (the next sub-step's after the barrier), the
             // dequantization of sub-step u+1 (tasks in k-steps 0..NDQ-1), the
             // MFMAs of this k-step
-            if (tt < 2) b_read(bring[tt + 2], u, tt + 2);
-            else b_read(bring[tt - 2], u + 1, tt - 2);
+            if (tt < 3) b_read(bring[(tt + 1) & 1], u, tt + 1);
+            else b_read(bring[0], u + 1, 0);
 #pragma unroll
             for (int i = 0; i < NDQ; i++)
                 if (i == tt) dequant(s < 3 ? kb : kb + 1, (s + 1) & 3, i);
@@ -602,7 +606,7 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
                 for (int j = 0; j < NT; j++) {
                     const h8 a = BP::pa(p) ? al[t16 % D] : ah[t16 % D];
-                    P[j] = mfma(a, bring[tt][BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
+                    P[j] = mfma(a, bring[tt & 1][BP::pb(p)][j], (t16 == 0 && p == 0) ? zero : P[j]);
                 }
             if constexpr (BP::kMin) {
                 // the block's min term: -sum_g dmin*m_g * sum_g(x')
@@ -635,15 +639,15 @@ __global__ __launch_bounds__(GTPB, 1) __attribute__((amdgpu_waves_per_eu(2))) vo
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
             }
-            if (tt == 1) {
-                // this sub-step's B reads are done (k-step 1 read k-step 3's)
+            if (tt == 2) {
+                // this sub-step's B reads are done (k-step 2 read k-step 3's)
                 // and the next sub-step's B tile is complete (its
-                // dequantization ran in k-steps 0 and 1); at sub-step 2 the
-                // next block's raw bytes (issued at k-steps 11-15 of the
-                // previous block) have landed: after them this wave issued at
-                // least the 20 activation loads of k-steps 0-9
+                // dequantization ran in k-steps 0-2); at sub-step 2 the next
+                // block's raw bytes (issued at k-steps 11-15 of the previous
+                // block) have landed: after them this wave issued at least
+                // the 22 activation loads of k-steps 0-10
                 if (s == 2)
-                    wait_vm_barrier<2 * 10>();
+                    wait_vm_barrier<2 * 11>();
                 else
                     lds_barrier();
             }
@@ -766,11 +770,11 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
     const int grid = 8 * ((ntm * ntn * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
     const void *k = (const void *)gemm_kernel<BP, WM, WN, NT, C64, D>;
-    constexpr int lds = GemmLayout<BP, NT * WN>::BYTES;
+    constexpr int lds = GemmLayout<BP, NT * WN, 64 * WM * WN>::BYTES;
     static_assert(lds <= 160 * 1024, "LDS");
     hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemm_kernel<BP, WM, WN, NT, C64, D>), dim3(grid), dim3(GTPB), lds, s, w.bytes, (uint32_t)w.row_bytes, K,
+    hipLaunchKernelGGL((gemm_kernel<BP, WM, WN, NT, C64, D>), dim3(grid), dim3(64 * WM * WN), lds, s, w.bytes, (uint32_t)w.row_bytes, K,
                        N, M, ws, ntn, ks, Y, part, ps);
     if ((e = hipGetLastError()) != hipSuccess || ks == 1) return e;
     const size_t MN = (size_t)M * N;
