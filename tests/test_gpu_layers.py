@@ -287,6 +287,20 @@ def test_attn_layer_small(q6):
         m.free()
 
 
+def test_gdn_layer_wide_heads():
+    """GatedDeltaNet heads of 2048 (one q/k head, two v heads): above the
+    1024 of the one-launch conv / l2-norm / gates kernel and the 128 of the
+    register-resident delta rule, so the step runs the separate glue launches
+    and the workgroup-per-head delta rule; the same bar as every layer."""
+    wide = dict(SMALL, n_embd=4096, n_qk_heads=1, n_v_heads=2, head_dim_linear=2048, n_head=16, n_head_kv=4,
+                head_dim=256, n_rot=64)
+    m = Model(wide, seed=61)
+    try:
+        run_gdn(m, ntok=2, seed=600)
+    finally:
+        m.free()
+
+
 def test_layers_9b_shapes():
     """The decode benchmark's layer shapes (Q6_K on the attention layer's
     v and down projections, as its every-4th-layer mix)."""
