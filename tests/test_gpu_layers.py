@@ -301,6 +301,20 @@ def test_gdn_layer_wide_heads():
         m.free()
 
 
+def test_layers_wide_embedding():
+    """n_embd 5120: the projections of a norm take the two-task streaming
+    kernel, which does not form the norm in its prologue, so the steps run
+    the norm launches (attn_norm; residual + post_attention_norm) before them."""
+    wide = dict(SMALL, n_embd=5120, n_qk_heads=10, n_v_heads=40, head_dim_linear=128, n_head=20, n_head_kv=5,
+                head_dim=256, n_rot=64)
+    m = Model(wide, seed=71)
+    try:
+        run_gdn(m, ntok=1, seed=700)
+        run_attn(m, ntok=2, n_ctx_max=4, seed=800)
+    finally:
+        m.free()
+
+
 def test_layers_9b_shapes():
     """The decode benchmark's layer shapes (Q6_K on the attention layer's
     v and down projections, as its every-4th-layer mix)."""

@@ -320,4 +320,53 @@ __device__ __forceinline__ void prep_x(const float *__restrict__ x, int K, XLayo
     }
 }
 
+// ---------------------------------------------------------------------------
+// Sequential f64 sums of f32 squares (rmsnorm, l2_norm_rows) as a tree sum S
+// plus a rigorous bound: for n non-negative terms the sequential sum and S
+// both lie within (n + log2 n + 2) * 2^-53 * S of the exact sum, so when both
+// ends of [S - e, S + e] round to the same f32 result (rounding is
+// monotonic), that is the reference's result; otherwise one thread replays
+// the sequential loop.
+// ---------------------------------------------------------------------------
+// Correctly rounded f32 square root: the f64 root (correctly rounded) rounded
+// to f32 is the correctly rounded f32 root, since 53 >= 2 * 24 + 2. The f32
+// hardware root alone (v_sqrt_f32) is accurate to 1 ulp only.
+__device__ __forceinline__ float sqrtf_cr(float v) { return (float)__dsqrt_rn((double)v); }
+
+// Sum over the workgroup (f64, fixed tree), returned to every thread.
+template <int TPB>
+__device__ double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < TPB / 64; i++) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// The f32 result of a sequential f64 sum of the n non-negative values
+// sq[i] (f32 squares), mapped through finish(): finish(lo) == finish(hi)
+// proves the result; otherwise thread 0 replays the loop. Every thread
+// returns the same value.
+template <int TPB, class Val, class Finish>
+__device__ float seq_sum_f32(Val val, int n, double S, Finish finish, float *bcast) {
+    const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
+    const float a = finish(S - e), b = finish(S + e);
+    if (__float_as_uint(a) == __float_as_uint(b)) return a;  // -0 and +0 differ: replay
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int i = 0; i < n; i++) {
+            const float v = val(i);
+            s += (double)__fmul_rn(v, v);
+        }
+        *bcast = finish(s);
+    }
+    __syncthreads();
+    const float r = *bcast;
+    __syncthreads();
+    return r;
+}
+
 }  // namespace uq

@@ -995,6 +995,66 @@ __device__ __forceinline__ void quantize_blocks_lds(const float *__restrict__ x,
     }
 }
 
+// The q8k input of a launch: x itself, or its row norm (nrm.w set): the
+// elements rmsnorm_kernel forms (kernels.rs:61-78), (t * scale) * w with t =
+// x (+ xb) and scale = 1 / sqrt(mean + eps), mean the sequential f64 sum of
+// t*t over K (the bound-or-replay sum of seq_sum_f32). A wave loads the t
+// and w of the blocks it quantizes (b = wv, wv + nw, ..., at most four: K <=
+// 4096 with four or more waves) once, before the workgroup's sum; workgroup 0
+// also writes the normalised row and x + xb where asked. qtmp is the prep
+// area (at least 256 bytes, free until the quantization writes it).
+template <int TPB>
+__device__ __forceinline__ void q8k_input(const float *__restrict__ x, const RowNorm &nrm, int K, int wv, int nw,
+                                          int lane, uint32_t *qtmp, int *bst, float *d8) {
+    const int nblk = K >> 8;
+    if (!nrm.w) {
+        quantize_blocks_lds(x, wv, nw, nblk, lane, qtmp, bst, d8);
+        return;
+    }
+    const float *xb = nrm.xb, *w = nrm.w;
+    float t[4][4], wt[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int b = wv + j * nw;
+        if (b < nblk)  // wave-uniform
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = 256 * b + lane * 4 + i;
+                t[j][i] = xb ? __fadd_rn(x[e], xb[e]) : x[e];
+                wt[j][i] = w[e];
+            }
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        if (wv + j * nw < nblk)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s += (double)__fmul_rn(t[j][i], t[j][i]);
+    const double S = block_sum_d<TPB>(s, (double *)qtmp);
+    const double dn = (double)K;
+    auto val = [&](int e) { return xb ? __fadd_rn(x[e], xb[e]) : x[e]; };
+    const float mean = seq_sum_f32<TPB>(val, K, S, [dn](double u) { return (float)(u / dn); }, (float *)qtmp + 64);
+    const float scale = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, nrm.eps)));
+    const bool out = blockIdx.x == 0 && nrm.xn_out;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int b = wv + j * nw;
+        if (b < nblk) {
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[i] = __fmul_rn(__fmul_rn(t[j][i], scale), wt[j][i]);
+            quantize_vals_lds(y, lane, qtmp + 64 * b, bst + 16 * b, d8 + b);
+            if (out)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int e = 256 * b + lane * 4 + i;
+                    nrm.xn_out[e] = y[i];
+                    if (nrm.xsum_out) nrm.xsum_out[e] = t[j][i];
+                }
+        }
+    }
+}
+
 struct Q8KLayout {
     size_t xq, d8, region, total;  // byte offsets
     int R;                         // rows per epilogue batch
@@ -1139,7 +1199,7 @@ __host__ __device__ inline Q8SLayout q8k_stream_layout(int K, int nw, int ni, in
 // (Sg.y[1]) and h = swiglu(g, u) (Sg.y[2]).
 template <class F, int T, int NW, bool MULTI, bool PAIR = false, bool PRIO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4 > 0 ? NW / 4 : 1))) void
-gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x) {
+gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__restrict__ x, const RowNorm nrm) {
     static_assert(!PAIR || (T == 1 && !MULTI), "pairs: one segment, K <= 4096");
     using St = Stage<typename Q8Base<F>::T>;
     constexpr int NI = (16 * T * St::BC + 63) / 64;  // 1 KB loads per row (K <= 4096 T)
@@ -1181,7 +1241,7 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
     };
     issue(0);
 
-    quantize_blocks_lds(x, wv, NW, nblk, lane, qtmp, bst, d8);
+    q8k_input<64 * NW>(x, nrm, K, wv, NW, lane, qtmp, bst, d8);
     __syncthreads();
     for (int t = threadIdx.x; t < ntask; t += 64 * NW)
         F::build_task(xq + (size_t)t * F::kDw, qtmp + 64 * (t >> 2), bst + 16 * (t >> 2), t & 3);
@@ -1501,7 +1561,8 @@ bool q8k_stream_fits(int K) {
 }
 
 template <class F, int T, bool MULTI>
-hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s) {
+hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s,
+                             const RowNorm &nrm = RowNorm()) {
     using St = Stage<typename Q8Base<F>::T>;
     constexpr int NW = Q8SShape<F, T>::NW, NI = (16 * T * St::BC + 63) / 64;
     const int N = S.start[S.n];
@@ -1516,17 +1577,18 @@ hipError_t launch_q8k_stream(const Segs &S, size_t row_bytes, int K, const float
             const hipError_t ep = allow_lds(kp, L.total);
             if (ep != hipSuccess) return ep;
             hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, false, false, true>), dim3(grid), dim3(64 * NW),
-                               L.total, s, S, row_bytes, K, x);
+                               L.total, s, S, row_bytes, K, x, nrm);
             return hipGetLastError();
         }
     }
     hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, T, NW, MULTI>), dim3(grid), dim3(64 * NW), L.total, s, S,
-                       row_bytes, K, x);
+                       row_bytes, K, x, nrm);
     return hipGetLastError();
 }
 
 template <class F>
-hipError_t launch_q8k_pair(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done) {
+hipError_t launch_q8k_pair(const Segs &S, size_t row_bytes, int K, const float *x, hipStream_t s, bool *done,
+                           const RowNorm &nrm = RowNorm()) {
     using St = Stage<typename Q8Base<F>::T>;
     constexpr int NW = UQ_STREAM_PAIR_NW, NI = (16 * St::BC + 63) / 64;
     *done = false;
@@ -1537,7 +1599,7 @@ hipError_t launch_q8k_pair(const Segs &S, size_t row_bytes, int K, const float *
     const hipError_t e = allow_lds(k, L.total);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_q8k_stream_kernel<F, 1, NW, false, true>), dim3(resident_grid(k, L.total, N, NW)),
-                       dim3(64 * NW), L.total, s, S, row_bytes, K, x);
+                       dim3(64 * NW), L.total, s, S, row_bytes, K, x, nrm);
     *done = true;
     return hipGetLastError();
 }
@@ -1680,6 +1742,53 @@ hipError_t launch_q8k_gate_up(const WeightsView &g, const WeightsView &u, const 
 
 hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y, hipStream_t s) {
     return launch_q8k_segs(w.dtype, w.dim_in, w.row_bytes, one_seg(w, nullptr, y), x, s);
+}
+
+namespace {
+// The streaming kernel with one task per lane (K <= 4096), the one launch
+// shape that forms a row norm in its prologue.
+template <class F, bool MULTI>
+hipError_t q8k_norm_stream(const Segs &S, size_t row_bytes, int K, const float *x, const RowNorm &nrm,
+                           hipStream_t s, bool *done) {
+    *done = false;
+    if (!UQ_Q8K_STREAM || F::ntasks(K) > 64 || !q8k_stream_fits<F, 1, MULTI>(K)) return hipSuccess;
+    *done = true;
+    return launch_q8k_stream<F, 1, MULTI>(S, row_bytes, K, x, s, nrm);
+}
+}  // namespace
+
+hipError_t launch_gemv_q8k_batch_norm(const WeightsView *w, int n, const float *x, float *const *y, const RowNorm &nrm,
+                                      hipStream_t s, bool *done) {
+    *done = false;
+    const Segs S = batch_segs(w, n, y);
+    if (S.start[S.n] == 0 || w[0].dim_in == 0) return hipSuccess;
+    const int K = w[0].dim_in;
+    const size_t rb = w[0].row_bytes;
+    if (w[0].dtype == UQ_Q4_K)
+        return n > 1 ? q8k_norm_stream<Q4KQ8, true>(S, rb, K, x, nrm, s, done)
+                     : q8k_norm_stream<Q4KQ8, false>(S, rb, K, x, nrm, s, done);
+    if (w[0].dtype == UQ_Q6_K)
+        return n > 1 ? q8k_norm_stream<Q6KQ8, true>(S, rb, K, x, nrm, s, done)
+                     : q8k_norm_stream<Q6KQ8, false>(S, rb, K, x, nrm, s, done);
+    return hipSuccess;
+}
+
+hipError_t launch_q8k_gate_up_norm(const WeightsView &g, const WeightsView &u, const float *x, float *yg, float *yu,
+                                   float *h, const RowNorm &nrm, hipStream_t s, bool *done) {
+    *done = false;
+    if (g.dim_out == 0 || g.dim_in == 0) return hipSuccess;
+    Segs S{};
+    S.n = 1;
+    S.start[0] = 0;
+    S.start[1] = g.dim_out;
+    S.w[0] = g.bytes;
+    S.w2[0] = u.bytes;
+    S.y[0] = yg;
+    S.y[1] = yu;
+    S.y[2] = h;
+    if (g.dtype == UQ_Q4_K) return launch_q8k_pair<Q4KQ8>(S, g.row_bytes, g.dim_in, x, s, done, nrm);
+    if (g.dtype == UQ_Q6_K) return launch_q8k_pair<Q6KQ8>(S, g.row_bytes, g.dim_in, x, s, done, nrm);
+    return hipSuccess;
 }
 
 hipError_t launch_gemv_q8k_sum(const WeightsView &w, const float *x, float *y, const float *add, float *ysum,

@@ -93,6 +93,16 @@ uq_status hip_error(hipError_t e, const char *what);
 // Records the calling thread's error message (uq_last_error) and returns s.
 uq_status set_error(uq_status s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// The input of a q8k launch formed in its prologue as rmsnorm(x (+ xb)) * w
+// (kernels.rs:61-78): the layer norms in front of the projections.
+struct RowNorm {
+    const float *w = nullptr;   // the norm weights; nullptr: the input is x itself
+    const float *xb = nullptr;  // optional addend: the row normalised is x + xb
+    float *xn_out = nullptr;    // the normalised row, written by workgroup 0 (optional)
+    float *xsum_out = nullptr;  // x + xb, written by workgroup 0 (optional, with xb)
+    float eps = 0.0f;
+};
+
 struct WeightsView {
     const uint8_t *bytes;
     uq_dtype dtype;
@@ -142,6 +152,13 @@ hipError_t launch_gemv_q8k(const WeightsView &w, const float *x, float *y,
 // when d_ysum is set (the layer's residual sum)
 uq_status ffn_swiglu_q8k_sum(uq_weights gh, uq_weights uh, uq_weights dh, const float *d_x, float *d_g, float *d_u,
                              float *d_h, float *d_y, const float *d_add, float *d_ysum, void *stream);
+// gemv_quant_q8k batch / gate-up pair whose input is the row norm nrm of x,
+// formed by the launch itself; *done is false (nothing launched) where the
+// shapes do not take the streaming kernel (K > 4096)
+hipError_t launch_gemv_q8k_batch_norm(const WeightsView *w, int n, const float *x, float *const *y, const RowNorm &nrm,
+                                      hipStream_t s, bool *done);
+hipError_t launch_q8k_gate_up_norm(const WeightsView &g, const WeightsView &u, const float *x, float *yg, float *yu,
+                                   float *h, const RowNorm &nrm, hipStream_t s, bool *done);
 // gemv_quant_q8k that also writes ysum = add + y (the residual sum of a layer)
 hipError_t launch_gemv_q8k_sum(const WeightsView &w, const float *x, float *y, const float *add, float *ysum,
                                hipStream_t s);

@@ -133,6 +133,40 @@ uq_status project_q8k(const uq_weights *w, float *const *y, int n, const float *
     return nb ? uq_gemv_q8k_batch(b, yb, nb, x, stream) : UQ_OK;
 }
 
+// The norm in front of a layer's projections, attn_norm (:352-360 / :563-571),
+// and its q8k projections: where the streaming kernel takes the shape, each
+// projection launch forms the norm of x_in in its prologue (the first one
+// also writes the node); otherwise a norm launch, then the projections.
+uq_status norm_project_q8k(const char *fn, const Dims &D, const float *norm_w, float eps, const float *x_in,
+                           float *xn, const uq_weights *w, float *const *y, int n, hipStream_t s) {
+    uq::WeightsView va[8], vb[8];
+    float *ya[8], *yb[8];
+    int na = 0, nb = 0;
+    const uq_dtype first = wh(w[0])->dtype;
+    for (int i = 0; i < n; i++) {
+        if (wh(w[i])->dtype == first) {
+            va[na] = uq::view(*wh(w[i]));
+            ya[na++] = y[i];
+        } else {
+            vb[nb] = uq::view(*wh(w[i]));
+            yb[nb++] = y[i];
+        }
+    }
+    uq::RowNorm nrm;
+    nrm.w = norm_w;
+    nrm.xn_out = xn;
+    nrm.eps = eps;
+    bool done = false;
+    UQ_TRY(hip_st(uq::launch_gemv_q8k_batch_norm(va, na, x_in, ya, nrm, s, &done), fn));
+    if (!done) {
+        UQ_TRY(hip_st(uq::launch_rmsnorm(xn, x_in, norm_w, (int)D.n, 1, eps, s), fn));
+        return project_q8k(w, y, n, xn, s);
+    }
+    if (nb == 0) return UQ_OK;
+    // the other format's batch reads the node the first launch wrote
+    return hip_st(uq::launch_gemv_q8k_batch(vb, nb, xn, yb, s), fn);
+}
+
 // residual = x_in + attn_out and post_attention_norm of it (one launch), FFN,
 // l_out = residual + ffn_out with the down projection (:524-536 / :696-704,
 // ffn :713-768)
@@ -140,6 +174,25 @@ uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const
                    uq_weights u, uq_weights dn, const float *post_norm, float *ws, size_t nctx, float *l_out,
                    hipStream_t s) {
     auto at = [&](int node) { return ws + node_offset(D, nctx, node); };
+    // where the streaming pair kernel takes the shape it forms the residual and
+    // its norm in its prologue (one launch fewer)
+    uq_weights_s *G = wh(g), *U = wh(u), *DN = wh(dn);
+    if (G->dtype == U->dtype) {
+        uq::RowNorm nrm;
+        nrm.w = post_norm;
+        nrm.xb = at(UQ_NODE_ATTN_OUT);
+        nrm.xn_out = at(UQ_NODE_POST_NORM);
+        nrm.xsum_out = at(UQ_NODE_RESIDUAL);
+        nrm.eps = d->rms_eps;
+        bool done = false;
+        UQ_TRY(hip_st(uq::launch_q8k_gate_up_norm(uq::view(*G), uq::view(*U), x_in, at(UQ_NODE_FFN_GATE),
+                                                  at(UQ_NODE_FFN_UP), at(UQ_NODE_FFN_SWIGLU), nrm, s, &done),
+                      fn));
+        if (done)
+            return hip_st(uq::launch_gemv_q8k_sum(uq::view(*DN), at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT),
+                                                  at(UQ_NODE_RESIDUAL), l_out, s),
+                          fn);
+    }
     UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_POST_NORM), (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, 1,
                                           d->rms_eps, s, at(UQ_NODE_ATTN_OUT), at(UQ_NODE_RESIDUAL)),
                   fn));
@@ -192,13 +245,12 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
     const int hd = (int)D.hd, nv = (int)D.nv, nqk = (int)D.nqk, ch = (int)D.ch;
     float *qkv = d_conv_win + (D.ck - 1) * D.ch;  // the window's last row
 
-    // 1) attn_norm (:352-360)
-    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_ATTN_NORM), d_x_in, w->attn_norm, (int)D.n, 1, d->rms_eps, s), fn));
-    // 2-3) qkv, z, beta, alpha: four q8k projections of x, one launch per format (:363-403)
+    // 1-3) attn_norm (:352-360); qkv, z, beta, alpha: four q8k projections of
+    // it, one launch per format (:363-403)
     {
         const uq_weights ws4[4] = {w->attn_qkv, w->attn_gate, w->ssm_beta, w->ssm_alpha};
         float *const ys[4] = {qkv, at(UQ_NODE_Z), at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA)};
-        UQ_TRY(project_q8k(ws4, ys, 4, at(UQ_NODE_ATTN_NORM), stream));
+        UQ_TRY(norm_project_q8k(fn, D, w->attn_norm, d->rms_eps, d_x_in, at(UQ_NODE_ATTN_NORM), ws4, ys, 4, s));
     }
     // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419);
     // 4) depthwise conv over [ring; qkv], silu, the ring's shift (:427-454);
@@ -263,14 +315,12 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
     const int ahd = (int)D.ahd, nh = (int)D.nh, nkv = (int)D.nkv;
     float *krow = d_k_cache + pos * kv_len, *vrow = d_v_cache + pos * kv_len;
 
-    // 1) attn_norm (:563-571)
-    UQ_TRY(hip_st(uq::launch_rmsnorm(at(UQ_NODE_ATTN_NORM), d_x_in, w->attn_norm, (int)D.n, 1, d->rms_eps, s), fn));
-    // 2-3) q|gate, k and v: three q8k projections of x, one launch per format; v lands
-    // in its cache row (it has no norm, :625-632)
+    // 1-3) attn_norm (:563-571); q|gate, k and v: three q8k projections of it,
+    // one launch per format; v lands in its cache row (it has no norm, :625-632)
     {
         const uq_weights ws3[3] = {w->attn_q, w->attn_k, w->attn_v};
         float *const ys[3] = {at(UQ_NODE_QFULL), at(UQ_NODE_K_RAW), vrow};
-        UQ_TRY(project_q8k(ws3, ys, 3, at(UQ_NODE_ATTN_NORM), stream));
+        UQ_TRY(norm_project_q8k(fn, D, w->attn_norm, d->rms_eps, d_x_in, at(UQ_NODE_ATTN_NORM), ws3, ys, 3, s));
     }
     // q: rmsnorm of each head's first half (:585-599); k: rmsnorm per kv
     // head, into the cache row (:611-623); 4) IMROPE on both (:634-642): one launch

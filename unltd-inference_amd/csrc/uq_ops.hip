@@ -26,24 +26,6 @@ constexpr int OPS_TPB = 256;
 
 __device__ __forceinline__ float logf_cr(float v) { return (float)log((double)v); }
 
-// Correctly rounded f32 square root: the f64 root (correctly rounded) rounded
-// to f32 is the correctly rounded f32 root, since 53 >= 2 * 24 + 2. The f32
-// hardware root alone (v_sqrt_f32) is accurate to 1 ulp only.
-__device__ __forceinline__ float sqrtf_cr(float v) { return (float)__dsqrt_rn((double)v); }
-
-// Sum over the workgroup (f64, fixed tree), returned to every thread.
-template <int TPB>
-__device__ double block_sum_d(double v, double *red) {
-    v = wave_sum_d(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int i = 0; i < TPB / 64; i++) t += red[i];
-    __syncthreads();
-    return t;
-}
-
 __device__ float block_max_f(float v, float *red) {
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     const int w = threadIdx.x >> 6;
@@ -53,29 +35,6 @@ __device__ float block_max_f(float v, float *red) {
     for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, red[i]);
     __syncthreads();
     return t;
-}
-
-// The f32 result of a sequential f64 sum of the n non-negative values
-// sq[i] (f32 squares), mapped through finish(): finish(lo) == finish(hi)
-// proves the result; otherwise thread 0 replays the loop. Every thread
-// returns the same value.
-template <int TPB, class Val, class Finish>
-__device__ float seq_sum_f32(Val val, int n, double S, Finish finish, float *bcast) {
-    const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
-    const float a = finish(S - e), b = finish(S + e);
-    if (__float_as_uint(a) == __float_as_uint(b)) return a;  // -0 and +0 differ: replay
-    if (threadIdx.x == 0) {
-        double s = 0.0;
-        for (int i = 0; i < n; i++) {
-            const float v = val(i);
-            s += (double)__fmul_rn(v, v);
-        }
-        *bcast = finish(s);
-    }
-    __syncthreads();
-    const float r = *bcast;
-    __syncthreads();
-    return r;
 }
 
 // sigmoid (kernels.rs:198-203), silu (:207-212), softplus (:217-228)
