@@ -237,8 +237,10 @@ def bench_gemm(hip, steps, warmup):
         dx, dy = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * 512 * N)
         by_m = {}
         for M in (1, 8, 32, 128, 512):
-            st = max(2, steps // (1 if M < 128 else 4))
-            wall, ev = timed(hip, lambda: uq.gemm(W, M, dx, dy, s), st, max(1, warmup // 2), s)
+            # the MFMA-heavy kernels run slower for their first few ms (the clock settles):
+            # 50 warmup calls, then at least 10 timed ones
+            st = max(10, steps // (1 if M < 128 else 2))
+            wall, ev = timed(hip, lambda: uq.gemm(W, M, dx, dy, s), st, max(warmup, 50), s)
             t = ev * 1e-3 / st
             by_m[str(M)] = {"us": t * 1e6, "tflops": 2 * M * N * K / t / 1e12,
                             "frac_bf16_peak": 2 * M * N * K / t / 1e12 / BF16_PEAK_TFLOPS,
