@@ -9,7 +9,8 @@ oracle's gemv_quant in tests/test_oracle_kats.py); a few rows of every case
 are also compared with the oracle's gemv_quant itself.
 
 The shapes cover each kernel shape the launcher picks (128 x 192, 64 x 256
-and 32 x 256 tiles for Q4_K; 128 x 128 and 64 x 128 for Q6_K and Q8_0),
+and, for M <= 32, the loader-wave kernel over 256 columns for Q4_K; 128 x 128
+and 64 x 128 for Q6_K and Q8_0),
 several 256-k blocks per workgroup (the LDS rings' steady state and the
 per-block scaling), K split across workgroups (even and uneven ranges),
 masked M and N tails, and the activation prep's three K regimes.
@@ -69,7 +70,7 @@ def test_gemm_q4k_prefill_config(K, N, M):
 
 
 Q4K_SHAPES = [
-    # 32 x 256 tiles (M <= 32), split K; one to seven rows
+    # M <= 32 (the loader-wave kernel, 256 columns per workgroup), split K; one to seven rows
     (4096, 1024, 1), (4096, 1024, 2), (4096, 1024, 3), (4096, 768, 5), (4096, 1000, 7), (4096, 12288, 8),
     (12288, 600, 16), (768, 512, 32),
     # 64 x 256 tiles (32 < M <= 64)

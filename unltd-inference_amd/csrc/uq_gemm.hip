@@ -24,8 +24,9 @@
 //            passes per k-step.
 //    The row scale s_m is applied at the store.
 //
-// Tiling: a workgroup of eight waves (two per SIMD, one workgroup per CU)
-// computes a TM x TN tile; wave (wm, wn) owns 32 rows and NT 32-column MFMA
+// Tiling (Q4_K with M <= 32 runs gemm_q4k_skinny_kernel, described there):
+// a workgroup of eight waves (two per SIMD, one workgroup per CU) computes a
+// TM x TN tile; wave (wm, wn) owns 32 rows and NT 32-column MFMA
 // tiles. K runs in 256-k blocks of four 64-k sub-steps of four 16-k steps.
 //  * Raw weight bytes of each block stream into a two-slot LDS ring with
 //    direct-to-LDS loads (global_load_lds_dwordx4), issued a block ahead.
@@ -731,6 +732,189 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ Y, s
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) Y[i] = 0.0f;
 }
 
+// ------------------------------------------------------------ Q4_K GEMM, M <= 32
+// With one 32-row tile every B column feeds a single MFMA tile, so nothing
+// is gained by sharing dequantized B through LDS: each compute wave owns 32
+// columns and dequantizes them straight into its B operands. A workgroup is
+// SK_CW compute waves (adjacent 32-column tiles over one K range; their
+// activation loads are the same addresses, which the CU's L1 serves once)
+// and one loader wave that streams the raw blocks of all SK_CW tiles into an
+// SK_RING-slot LDS ring with direct-to-LDS loads. The split keeps the HBM
+// loads out of the compute waves' in-order vmcnt queue, which then holds
+// only activation loads (L2): with the weight loads in the same queue, each
+// activation wait also waited for the next block's HBM loads. One barrier
+// per block: at barrier b, block b has landed (the loader waited for it)
+// and every wave is done with block b-1, whose slot the loader refills with
+// block b + SK_RING - 1. Per block the arithmetic is gemm_kernel's (results
+// bit-identical): P over the block's 16 k-steps on the f16 MFMA (hi plane,
+// then lo plane), C += d*P in f64, the min term on the MFMA; a split K is
+// summed by gemm_splitk_reduce. Eight compute waves measured faster than
+// two or four, a four-slot ring and eight activation k-steps in flight no
+// faster.
+constexpr int SK_CW = 8, SK_D = 4, SK_RING = 3;
+constexpr int SK_COLS = 32 * SK_CW;
+constexpr int SK_CHUNKS = SK_COLS * GQ4K::CPR;          // 16-byte chunks per block
+constexpr int SK_ROUNDS = (SK_CHUNKS + 63) / 64;        // loader loads per block
+constexpr int SK_SLOT = SK_CHUNKS * 16;
+static_assert(SK_CHUNKS % 64 == 0, "every loader round is a full wave");
+static_assert((SK_RING - 2) * SK_ROUNDS <= 63, "vmcnt immediate");
+
+// Quarter q of a sub-step (the Q4_K layout of gemm_kernel) into the lane's
+// B operands: low nibbles -> lo8, high nibbles -> hi8, slots 0,2,1,3 per four.
+__device__ __forceinline__ void sk_dequant(uint2 q, h2 lsc, h2 loff, h2 hsc, h2 hoff, h8 &lo8, h8 &hi8) {
+    const uint32_t lm = 0x000F000Fu, hm = 0x00F000F0u, mag = 0x64006400u;
+    const uint32_t D[2] = {q.x, q.y};
+    u4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const uint32_t d8 = D[e] >> 8;
+        (&lo.x)[2 * e] = as_u(__builtin_elementwise_fma(as_h2(bfi(lm, D[e], mag)), lsc, loff));
+        (&lo.x)[2 * e + 1] = as_u(__builtin_elementwise_fma(as_h2(bfi(lm, d8, mag)), lsc, loff));
+        (&hi.x)[2 * e] = as_u(__builtin_elementwise_fma(as_h2(bfi(hm, D[e], mag)), hsc, hoff));
+        (&hi.x)[2 * e + 1] = as_u(__builtin_elementwise_fma(as_h2(bfi(hm, d8, mag)), hsc, hoff));
+    }
+    lo8 = __builtin_bit_cast(h8, lo);
+    hi8 = __builtin_bit_cast(h8, hi);
+}
+
+__global__ __launch_bounds__(64 * (SK_CW + 1)) __attribute__((amdgpu_waves_per_eu(3))) void gemm_q4k_skinny_kernel(
+    const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
+    float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
+    __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
+    const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // (column group, K range) list dealt to the XCDs in contiguous runs, as gemm_kernel
+    const int T = ncg * ks, per = (T + 7) / 8;
+    const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if ((blockIdx.x >> 3) >= per || L >= T) return;  // the whole workgroup
+    const int cg = L % ncg, kidx = L / ncg;
+    const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
+
+    if (wv == SK_CW) {
+        // loader: chunk 64 r + lane of a block is 16 bytes of column
+        // (chunk / 9) of the group; rows past N repeat the last one
+        uint32_t goff[SK_ROUNDS];
+#pragma unroll
+        for (int r = 0; r < SK_ROUNDS; r++) {
+            const int c = min(64 * r + lane, SK_CHUNKS - 1), col = c / GQ4K::CPR, part = c - col * GQ4K::CPR;
+            goff[r] = (uint32_t)min(cg * SK_COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
+        }
+        const uint8_t *wb = W + (size_t)kb0 * GQ4K::RB;
+        auto issue = [&](int b) {  // block b into slot b % SK_RING
+            const uint8_t *g = wb + (size_t)b * GQ4K::RB;
+            uint8_t *dst = ring + (b % SK_RING) * SK_SLOT;
+#pragma unroll
+            for (int r = 0; r < SK_ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
+        };
+        // barrier 0: block 0 landed (blocks 1..SK_RING-2 may be in flight)
+        for (int j = 0; j < SK_RING - 1; j++)
+            if (j < nblk) issue(j);
+        if (nblk >= SK_RING - 1)
+            wait_vm_barrier<(SK_RING - 2) * SK_ROUNDS>();
+        else
+            wait_vm_barrier<0>();
+        for (int b = 0; b < nblk; b++) {
+            // barrier b+1: block b+1 landed. Block b-1's slot is free since
+            // barrier b: refill it with block b+SK_RING-1 first, whose loads
+            // (and those of the blocks between) may stay outstanding; near
+            // the end, wait for everything.
+            if (b + SK_RING - 1 < nblk) {
+                issue(b + SK_RING - 1);
+                wait_vm_barrier<(SK_RING - 2) * SK_ROUNDS>();
+            } else {
+                wait_vm_barrier<0>();
+            }
+        }
+        return;
+    }
+
+    // compute wave wv: columns n0..n0+31 (a tile past N computes on the
+    // repeated last row and stores nothing; it still meets every barrier)
+    const int n0 = (cg * SK_CW + wv) * 32;
+    float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
+    const int am = min(lr, M - 1);
+    const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
+    const uint32_t pbytes = (uint32_t)((size_t)M * K * 2);
+    const auto rah = buf_rsrc(ws.ahi, pbytes), ral = buf_rsrc(ws.alo, pbytes);
+    const int nks = 16 * nblk;
+    const uint32_t kstep = (uint32_t)M * 32u, abase = (uint32_t)kb0 * 16u * kstep;
+    auto a_load = [&](h8 &hi, h8 &lo, int kk) {
+        const uint32_t so = abase + (uint32_t)min(kk, nks - 1) * kstep;
+        hi = buf_load16(rah, aoff, so);
+        lo = buf_load16(ral, aoff, so);
+    };
+    const auto rg = buf_rsrc(ws.g, (uint32_t)((size_t)M * (K / 256) * 32));
+    const uint32_t goff = (uint32_t)am * 32u + 16u * lh;
+    auto g_load = [&](int b) { return buf_load16(rg, goff, (uint32_t)(kb0 + min(b, nblk - 1)) * (uint32_t)M * 32u); };
+
+    const f16x zero = {};
+    f16x Cm = zero;
+    double C[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) C[r] = 0.0;
+    h8 ah[SK_D], al[SK_D];
+#pragma unroll
+    for (int d = 0; d < SK_D - 1; d++) a_load(ah[d], al[d], d);
+    h8 gm = g_load(0);
+    const uint8_t *mycol = ring + (wv * 32 + lr) * (16 * GQ4K::CPR);
+    lds_barrier();  // barrier 0
+
+    for (int b = 0; b < nblk; b++) {
+        const uint8_t *rc = mycol + (b % SK_RING) * SK_SLOT;
+        const u4 h = *(const u4 *)rc;
+        uint2 q[8];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            q[2 * s] = *(const uint2 *)(rc + 16 + 32 * s + 8 * lh);
+            q[2 * s + 1] = *(const uint2 *)(rc + 32 + 32 * s + 8 * lh);
+        }
+        const h8 gcur = gm;
+        gm = g_load(b + 1);
+        const uint32_t S0 = h.y, S1 = h.z, S2 = h.w;
+        f16x P = zero;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            // sub-step s: groups 2s (low nibbles, k-steps 0, 1) and 2s+1 (high, 2, 3)
+            const float sa = (float)GQ4K::sc_of(S0, S2, 2 * s), sb = (float)GQ4K::sc_of(S0, S2, 2 * s + 1);
+            h8 B[4];
+            sk_dequant(q[2 * s], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[0], B[2]);
+            sk_dequant(q[2 * s + 1], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[1], B[3]);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int i = 4 * s + t;  // k-step of the block; 16 b is a multiple of SK_D
+                a_load(ah[(i + SK_D - 1) % SK_D], al[(i + SK_D - 1) % SK_D], 16 * b + i + SK_D - 1);
+                P = mfma(ah[i % SK_D], B[t], P);
+                P = mfma(al[i % SK_D], B[t], P);
+            }
+        }
+        // the block's min term and C += d * P (d*P is exact in f64)
+        const float dmin = f16_hi(h.x), d = f16_lo(h.x);
+        h8 bh, bl;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const float v = -(dmin * (float)GQ4K::m_of(S1, S2, g));
+            bh[g] = (_Float16)v;
+            bl[g] = (_Float16)(v - (float)bh[g]);
+        }
+        Cm = mfma(gcur, bh, Cm);
+        Cm = mfma(gcur, bl, Cm);
+#pragma unroll
+        for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+        lds_barrier();  // barrier b+1: this wave is done with the slot of block b
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the end land before the wave leaves
+
+    // lane holds column n0 + lr, rows 8*(r/4) + 4*lh + r%4
+    const int n = n0 + lr;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float rs = ws.scale[min(m, M - 1)];
+        const float v = (float)((C[r] + (double)Cm[r]) * (double)rs);
+        if (m < M && n < N) Yo[(size_t)m * N + n] = v;
+    }
+}
+
 int gemm_cus() {
     static int n = 0;
     if (!n) {
@@ -786,13 +970,28 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
 // Activation fragments run D k-steps ahead: a whole block (16) for the
 // small tiles, whose k-steps are short, 8 or 4 for the others (what the
 // registers allow; the 128 x 192 tile measured the same at 2, 4 and 8).
+hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
+    const int K = w.dim_in, N = w.dim_out;
+    const int ncg = (N + SK_COLS - 1) / SK_COLS;
+    const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
+    const size_t ps = part_stride(M, N);
+    hipLaunchKernelGGL(gemm_q4k_skinny_kernel, dim3(grid), dim3(64 * (SK_CW + 1)), 0, s, w.bytes, (uint32_t)w.row_bytes,
+                       K, N, M, ws, ncg, ks, Y, part, ps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return e;
+    const size_t MN = (size_t)M * N;
+    const int rgrid = (int)std::min<size_t>((MN + 255) / 256, 4096);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const float *)part, ks, ps, MN, Y);
+    return hipGetLastError();
+}
+
 template <class BP>
 hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &ws, float *Y, float *part,
                       hipStream_t s) {
     if constexpr (std::is_same<BP, GQ4K>::value) {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
         if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 4>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
-        return gemm_launch<BP, 1, 8, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 32 x 256
+        return skinny_launch(w, M, ws, Y, part, p.ks, s);                                       // 32 x 128
     } else {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
         return gemm_launch<BP, 2, 4, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 64 x 128
