@@ -8,9 +8,9 @@ weights of the oracle's integer unpack times X in f64, pinned against the
 oracle's gemv_quant in tests/test_oracle_kats.py); a few rows of every case
 are also compared with the oracle's gemv_quant itself.
 
-The shapes cover each kernel shape the launcher picks (128 x 192, 64 x 256
-and, for M <= 32, the loader-wave kernel over 256 columns for Q4_K; 128 x 128
-and 64 x 128 for Q6_K and Q8_0),
+The shapes cover each kernel shape the launcher picks (128 x 192 and 64 x 256
+for Q4_K, 128 x 128 and 64 x 128 for Q6_K and Q8_0, and for M <= 32 the
+loader-wave kernel of each format),
 several 256-k blocks per workgroup (the LDS rings' steady state and the
 per-block scaling), K split across workgroups (even and uneven ranges),
 masked M and N tails, and the activation prep's three K regimes.
@@ -91,10 +91,12 @@ def test_gemm_q4k_shapes(K, N, M):
 
 @pytest.mark.parametrize("dtype", [S.Q6_K, S.Q8_0])
 @pytest.mark.parametrize("K,N,M", [(12288, 4096, 300), (12288, 4096, 100), (12288, 4096, 8), (4096, 1000, 70),
-                                   (256, 200, 3), (1024, 130, 65), (4352, 384, 33)])
+                                   (256, 200, 3), (1024, 130, 65), (4352, 384, 33), (12288, 1000, 29)])
 def test_gemm_q6k_q8_0(dtype, K, N, M):
     """Q6_K and Q8_0 on the MFMA: the down-projection shape (K = 12288) at
-    M = 300, 100 and 8, and small / ragged shapes."""
+    M = 300, 100 and 8, and small / ragged shapes (M <= 32 runs the
+    loader-wave kernel: 128-column workgroups, tiles past N, K split into
+    ranges of one or two blocks at 12288 x 1000)."""
     log(f"gemm dtype={dtype} K={K} N={N} M={M}")
     w = S.weights(dtype, N, K, seed=K + N + M + dtype)
     X = S.activations(K, seed=M + dtype, rows=M).reshape(M, K)

@@ -24,7 +24,7 @@
 //            passes per k-step.
 //    The row scale s_m is applied at the store.
 //
-// Tiling (Q4_K with M <= 32 runs gemm_q4k_skinny_kernel, described there):
+// Tiling (M <= 32 runs gemm_skinny_kernel, described there):
 // a workgroup of eight waves (two per SIMD, one workgroup per CU) computes a
 // TM x TN tile; wave (wm, wn) owns 32 rows and NT 32-column MFMA
 // tiles. K runs in 256-k blocks of four 64-k sub-steps of four 16-k steps.
@@ -732,32 +732,37 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ Y, s
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) Y[i] = 0.0f;
 }
 
-// ------------------------------------------------------------ Q4_K GEMM, M <= 32
+// ------------------------------------------------------------ GEMM, M <= 32
 // With one 32-row tile every B column feeds a single MFMA tile, so nothing
 // is gained by sharing dequantized B through LDS: each compute wave owns 32
 // columns and dequantizes them straight into its B operands. A workgroup is
-// SK_CW compute waves (adjacent 32-column tiles over one K range; their
+// CW compute waves (adjacent 32-column tiles over one K range; their
 // activation loads are the same addresses, which the CU's L1 serves once)
-// and one loader wave that streams the raw blocks of all SK_CW tiles into an
+// and one loader wave that streams the raw blocks of all CW tiles into an
 // SK_RING-slot LDS ring with direct-to-LDS loads. The split keeps the HBM
 // loads out of the compute waves' in-order vmcnt queue, which then holds
 // only activation loads (L2): with the weight loads in the same queue, each
 // activation wait also waited for the next block's HBM loads. One barrier
 // per block: at barrier b, block b has landed (the loader waited for it)
 // and every wave is done with block b-1, whose slot the loader refills with
-// block b + SK_RING - 1. Per block the arithmetic is gemm_kernel's (results
-// bit-identical): P over the block's 16 k-steps on the f16 MFMA (hi plane,
-// then lo plane), C += d*P in f64, the min term on the MFMA; a split K is
-// summed by gemm_splitk_reduce. Eight compute waves measured faster than
-// two or four, a four-slot ring and eight activation k-steps in flight no
-// faster.
-constexpr int SK_CW = 8, SK_D = 4, SK_RING = 3;
-constexpr int SK_COLS = 32 * SK_CW;
-constexpr int SK_CHUNKS = SK_COLS * GQ4K::CPR;          // 16-byte chunks per block
-constexpr int SK_ROUNDS = (SK_CHUNKS + 63) / 64;        // loader loads per block
-constexpr int SK_SLOT = SK_CHUNKS * 16;
-static_assert(SK_CHUNKS % 64 == 0, "every loader round is a full wave");
-static_assert((SK_RING - 2) * SK_ROUNDS <= 63, "vmcnt immediate");
+// block b + SK_RING - 1. Per block the arithmetic is gemm_kernel's with the
+// same passes, so the results are bit-identical to its 64-row (Q6_K, Q8_0)
+// and 32-row (Q4_K) tiles: P over the block's 16 k-steps on the f16 MFMA,
+// then C += d*P (Q4_K, Q6_K) or C += P (Q8_0) in f64, and the Q4_K min
+// term on the MFMA; a split K is summed by gemm_splitk_reduce. For Q4_K,
+// eight compute waves measured faster than two or four; a four-slot ring and
+// eight activation k-steps in flight measured no faster.
+constexpr int SK_D = 4, SK_RING = 3;
+template <class BP, int CW>
+struct SkShape {
+    static constexpr int COLS = 32 * CW;
+    static constexpr int CHUNKS = COLS * BP::CPR;  // 16-byte chunks per block
+    static constexpr int ROUNDS = CHUNKS / 64;     // loader loads per block
+    static constexpr int SLOT = CHUNKS * 16;
+    static_assert(CHUNKS % 64 == 0, "every loader round is a full wave");
+    static_assert((SK_RING - 2) * ROUNDS <= 63, "vmcnt immediate");
+    static_assert(SK_RING * SLOT <= 160 * 1024, "LDS");
+};
 
 // Quarter q of a sub-step (the Q4_K layout of gemm_kernel) into the lane's
 // B operands: low nibbles -> lo8, high nibbles -> hi8, slots 0,2,1,3 per four.
@@ -777,9 +782,12 @@ __device__ __forceinline__ void sk_dequant(uint2 q, h2 lsc, h2 loff, h2 hsc, h2 
     hi8 = __builtin_bit_cast(h8, hi);
 }
 
-__global__ __launch_bounds__(64 * (SK_CW + 1)) __attribute__((amdgpu_waves_per_eu(3))) void gemm_q4k_skinny_kernel(
+template <class BP, int CW>
+__global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((CW + 4) / 4))) void gemm_skinny_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
     float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
+    using Sh = SkShape<BP, CW>;
+    constexpr int SK_CW = CW, SK_COLS = Sh::COLS, SK_CHUNKS = Sh::CHUNKS, SK_ROUNDS = Sh::ROUNDS, SK_SLOT = Sh::SLOT;
     __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
     const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -796,12 +804,12 @@ __global__ __launch_bounds__(64 * (SK_CW + 1)) __attribute__((amdgpu_waves_per_e
         uint32_t goff[SK_ROUNDS];
 #pragma unroll
         for (int r = 0; r < SK_ROUNDS; r++) {
-            const int c = min(64 * r + lane, SK_CHUNKS - 1), col = c / GQ4K::CPR, part = c - col * GQ4K::CPR;
+            const int c = 64 * r + lane, col = c / BP::CPR, part = c - col * BP::CPR;
             goff[r] = (uint32_t)min(cg * SK_COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
         }
-        const uint8_t *wb = W + (size_t)kb0 * GQ4K::RB;
+        const uint8_t *wb = W + (size_t)kb0 * BP::RB;
         auto issue = [&](int b) {  // block b into slot b % SK_RING
-            const uint8_t *g = wb + (size_t)b * GQ4K::RB;
+            const uint8_t *g = wb + (size_t)b * BP::RB;
             uint8_t *dst = ring + (b % SK_RING) * SK_SLOT;
 #pragma unroll
             for (int r = 0; r < SK_ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
@@ -855,51 +863,143 @@ __global__ __launch_bounds__(64 * (SK_CW + 1)) __attribute__((amdgpu_waves_per_e
     h8 ah[SK_D], al[SK_D];
 #pragma unroll
     for (int d = 0; d < SK_D - 1; d++) a_load(ah[d], al[d], d);
-    h8 gm = g_load(0);
-    const uint8_t *mycol = ring + (wv * 32 + lr) * (16 * GQ4K::CPR);
+    h8 gm = {};
+    if constexpr (BP::kMin) gm = g_load(0);
+    const uint8_t *mycol = ring + (wv * 32 + lr) * (16 * BP::CPR);
     lds_barrier();  // barrier 0
 
     for (int b = 0; b < nblk; b++) {
         const uint8_t *rc = mycol + (b % SK_RING) * SK_SLOT;
-        const u4 h = *(const u4 *)rc;
-        uint2 q[8];
+        // k-step i (0..15) of the block: the activation fragments of k-step
+        // i + SK_D - 1 are requested, then the passes of k-step i run on B
+        // (16 b is a multiple of SK_D, so the ring slots are compile-time)
+        auto kstep = [&](int i, const h8 &B0, const h8 &B1, f16x &P) {
+            a_load(ah[(i + SK_D - 1) % SK_D], al[(i + SK_D - 1) % SK_D], 16 * b + i + SK_D - 1);
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            q[2 * s] = *(const uint2 *)(rc + 16 + 32 * s + 8 * lh);
-            q[2 * s + 1] = *(const uint2 *)(rc + 32 + 32 * s + 8 * lh);
-        }
-        const h8 gcur = gm;
-        gm = g_load(b + 1);
-        const uint32_t S0 = h.y, S1 = h.z, S2 = h.w;
-        f16x P = zero;
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            // sub-step s: groups 2s (low nibbles, k-steps 0, 1) and 2s+1 (high, 2, 3)
-            const float sa = (float)GQ4K::sc_of(S0, S2, 2 * s), sb = (float)GQ4K::sc_of(S0, S2, 2 * s + 1);
-            h8 B[4];
-            sk_dequant(q[2 * s], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[0], B[2]);
-            sk_dequant(q[2 * s + 1], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[1], B[3]);
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int i = 4 * s + t;  // k-step of the block; 16 b is a multiple of SK_D
-                a_load(ah[(i + SK_D - 1) % SK_D], al[(i + SK_D - 1) % SK_D], 16 * b + i + SK_D - 1);
-                P = mfma(ah[i % SK_D], B[t], P);
-                P = mfma(al[i % SK_D], B[t], P);
+            for (int p = 0; p < BP::NPASS; p++) {
+                const h8 a = BP::pa(p) ? al[i % SK_D] : ah[i % SK_D];
+                P = mfma(a, BP::pb(p) ? B1 : B0, (i == 0 && p == 0) ? zero : P);
             }
-        }
-        // the block's min term and C += d * P (d*P is exact in f64)
-        const float dmin = f16_hi(h.x), d = f16_lo(h.x);
-        h8 bh, bl;
+        };
+        f16x P = zero;
+        if constexpr (std::is_same<BP, GQ4K>::value) {
+            const u4 h = *(const u4 *)rc;
+            uint2 q[8];
 #pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const float v = -(dmin * (float)GQ4K::m_of(S1, S2, g));
-            bh[g] = (_Float16)v;
-            bl[g] = (_Float16)(v - (float)bh[g]);
-        }
-        Cm = mfma(gcur, bh, Cm);
-        Cm = mfma(gcur, bl, Cm);
+            for (int s = 0; s < 4; s++) {
+                q[2 * s] = *(const uint2 *)(rc + 16 + 32 * s + 8 * lh);
+                q[2 * s + 1] = *(const uint2 *)(rc + 32 + 32 * s + 8 * lh);
+            }
+            const h8 gcur = gm;
+            gm = g_load(b + 1);
+            const uint32_t S0 = h.y, S1 = h.z, S2 = h.w;
 #pragma unroll
-        for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+            for (int s = 0; s < 4; s++) {
+                // sub-step s: groups 2s (low nibbles, k-steps 0, 1) and 2s+1 (high, 2, 3)
+                const float sa = (float)GQ4K::sc_of(S0, S2, 2 * s), sb = (float)GQ4K::sc_of(S0, S2, 2 * s + 1);
+                h8 B[4];
+                sk_dequant(q[2 * s], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[0], B[2]);
+                sk_dequant(q[2 * s + 1], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), B[1], B[3]);
+#pragma unroll
+                for (int t = 0; t < 4; t++) kstep(4 * s + t, B[t], B[t], P);
+            }
+            // the block's min term and C += d * P (d*P is exact in f64)
+            const float dmin = f16_hi(h.x), d = f16_lo(h.x);
+            h8 bh, bl;
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const float v = -(dmin * (float)GQ4K::m_of(S1, S2, g));
+                bh[g] = (_Float16)v;
+                bl[g] = (_Float16)(v - (float)bh[g]);
+            }
+            Cm = mfma(gcur, bh, Cm);
+            Cm = mfma(gcur, bl, Cm);
+#pragma unroll
+            for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+        } else if constexpr (std::is_same<BP, GQ6K>::value) {
+            // the lane's half (8 of 16 elements) of each k-step: ql bytes
+            // 64 hb + 16 c + 8 lh, qh bytes 128 + 32 hb + 16 (c & 1) + 8 lh
+            // (hb = sub-step / 2), the int8 scale of the k-step
+            uint2 ql[8], qh[4];
+#pragma unroll
+            for (int hb = 0; hb < 2; hb++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) ql[4 * hb + c] = *(const uint2 *)(rc + 64 * hb + 16 * c + 8 * lh);
+#pragma unroll
+                for (int c = 0; c < 2; c++) qh[2 * hb + c] = *(const uint2 *)(rc + 128 + 32 * hb + 16 * c + 8 * lh);
+            }
+            const u4 scv = *(const u4 *)(rc + 192);
+            const float d = f16_lo(*(const uint16_t *)(rc + 208));
+            const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+            const h2 off = hh(-1056.0f);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int hb = s >> 1, j = s & 1;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int i = 4 * s + c, shift = 2 * (2 * j + (c >> 1));
+                    const int sc = (int)(int8_t)(((&scv.x)[i >> 2] >> (8 * (i & 3))) & 0xFF);
+                    const h2 se = hh((float)(sc & ~1)), so = hh((float)(sc & 1));
+                    const uint2 A = ql[4 * hb + c], Cq = qh[2 * hb + (c & 1)];
+                    u4 b1, b2;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t Ad = e ? A.y : A.x, Cd = e ? Cq.y : Cq.x;
+                        const uint32_t raw = (j ? (Ad >> 4) & 0x0F0F0F0Fu : Ad & 0x0F0F0F0Fu) | (((Cd >> shift) & 0x03030303u) << 4);
+                        // 1024 + raw, exact; q = raw - 32 exact; q * (sc & ~1) even and
+                        // |.| <= 4096, q * (sc & 1) in [-32, 31]: both exact f16
+                        const h2 q0 = as_h2(bfi(bm, raw, mag)) + off, q1 = as_h2(bfi(bm, raw >> 8, mag)) + off;
+                        (&b1.x)[2 * e] = as_u(q0 * se);
+                        (&b1.x)[2 * e + 1] = as_u(q1 * se);
+                        (&b2.x)[2 * e] = as_u(q0 * so);
+                        (&b2.x)[2 * e + 1] = as_u(q1 * so);
+                    }
+                    kstep(i, __builtin_bit_cast(h8, b1), __builtin_bit_cast(h8, b2), P);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+        } else {
+            // Q8_0: k-step i = 4 s + c is elements 16 (c & 1).. of Q8_0 block
+            // bi = 2 s + c / 2 (34 bytes at 34 bi); the lane's 8 q bytes sit
+            // at 2 (mod 4) for even bi and are realigned from dwords
+            const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+            const h2 off = hh(-1152.0f);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int bi = i >> 1;
+                const uint8_t *blk = rc + 34 * bi;
+                const _Float16 df = __builtin_bit_cast(_Float16, *(const uint16_t *)blk);
+                const h2 d2 = h2{df, df};
+                const uint8_t *qp = blk + 2 + 16 * (i & 1) + 8 * lh;
+                uint32_t w[2];
+                if (bi & 1) {  // q at 0 (mod 4)
+                    w[0] = ((const uint32_t *)qp)[0];
+                    w[1] = ((const uint32_t *)qp)[1];
+                } else {
+                    const uint32_t *pp = (const uint32_t *)(qp - 2);
+                    const uint32_t r0 = pp[0], r1 = pp[1], r2 = pp[2];
+                    w[0] = __builtin_amdgcn_alignbyte(r1, r0, 2);
+                    w[1] = __builtin_amdgcn_alignbyte(r2, r1, 2);
+                }
+                u4 bh, bl;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t u = w[e] ^ 0x80808080u;  // bytes q + 128
+                    const h2 q0 = as_h2(bfi(bm, u, mag)) + off, q1 = as_h2(bfi(bm, u >> 8, mag)) + off;  // exact q
+                    const h2 h0 = q0 * d2, h1 = q1 * d2;  // f16(d*q)
+                    // d*q - f16(d*q): at most 8 significant bits, exact in f16
+                    const h2 l0 = __builtin_elementwise_fma(q0, d2, -h0), l1 = __builtin_elementwise_fma(q1, d2, -h1);
+                    (&bh.x)[2 * e] = as_u(h0);
+                    (&bh.x)[2 * e + 1] = as_u(h1);
+                    (&bl.x)[2 * e] = as_u(l0);
+                    (&bl.x)[2 * e + 1] = as_u(l1);
+                }
+                kstep(i, __builtin_bit_cast(h8, bh), __builtin_bit_cast(h8, bl), P);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) C[r] += (double)P[r];
+        }
         lds_barrier();  // barrier b+1: this wave is done with the slot of block b
     }
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the end land before the wave leaves
@@ -970,13 +1070,14 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
 // Activation fragments run D k-steps ahead: a whole block (16) for the
 // small tiles, whose k-steps are short, 8 or 4 for the others (what the
 // registers allow; the 128 x 192 tile measured the same at 2, 4 and 8).
+template <class BP, int CW>
 hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
-    const int ncg = (N + SK_COLS - 1) / SK_COLS;
+    const int ncg = (N + SkShape<BP, CW>::COLS - 1) / SkShape<BP, CW>::COLS;
     const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
-    hipLaunchKernelGGL(gemm_q4k_skinny_kernel, dim3(grid), dim3(64 * (SK_CW + 1)), 0, s, w.bytes, (uint32_t)w.row_bytes,
-                       K, N, M, ws, ncg, ks, Y, part, ps);
+    hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
+                       (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ks == 1) return e;
     const size_t MN = (size_t)M * N;
@@ -991,9 +1092,10 @@ hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &
     if constexpr (std::is_same<BP, GQ4K>::value) {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
         if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 4>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
-        return skinny_launch(w, M, ws, Y, part, p.ks, s);                                       // 32 x 128
+        return skinny_launch<BP, 8>(w, M, ws, Y, part, p.ks, s);                                // M <= 32
     } else {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
+        if (M <= 32) return skinny_launch<BP, 4>(w, M, ws, Y, part, p.ks, s);                 // M <= 32
         return gemm_launch<BP, 2, 4, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 64 x 128
     }
 }
