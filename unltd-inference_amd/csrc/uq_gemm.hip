@@ -1036,7 +1036,9 @@ struct Plan {
 Plan plan_for(uq_dtype dt, int M, int N, int K) {
     Plan p;
     // rows per tile: 128 beyond M = 64, else 64, else (Q4_K) 32; columns:
-    // Q4_K 192 (128-row tiles) or 256, Q6_K / Q8_0 128
+    // Q4_K 192 (128-row tiles) or 256, Q6_K / Q8_0 128. M <= 32 runs the
+    // loader-wave kernel over the same column groups (256 for Q4_K, 128
+    // otherwise), so the K split below holds for it too.
     const bool q4 = dt == UQ_Q4_K;
     p.wm = M > 64 ? 4 : (M > 32 || !q4) ? 2 : 1;
     p.tm = 32 * p.wm;
