@@ -70,9 +70,10 @@ def test_gemm_q4k_prefill_config(K, N, M):
 
 
 Q4K_SHAPES = [
-    # M <= 32 (the loader-wave kernel, 256 columns per workgroup), split K; one to seven rows
+    # M <= 32 (the loader-wave kernel, 256 columns per workgroup), split K (ranges of one to four
+    # blocks; two at 2560 x 12288); one to seven rows
     (4096, 1024, 1), (4096, 1024, 2), (4096, 1024, 3), (4096, 768, 5), (4096, 1000, 7), (4096, 12288, 8),
-    (12288, 600, 16), (768, 512, 32),
+    (12288, 600, 16), (768, 512, 32), (2560, 12288, 4),
     # 64 x 256 tiles (32 < M <= 64)
     (4096, 256, 33), (5120, 200, 40), (1280, 1000, 64),
     # 128 x 192 tiles (M > 64): one block, a few blocks, many; tails in M and N
