@@ -782,12 +782,54 @@ __device__ __forceinline__ void sk_dequant(uint2 q, h2 lsc, h2 loff, h2 hsc, h2 
     hi8 = __builtin_bit_cast(h8, hi);
 }
 
+// The loader wave of the M <= 32 kernels: chunk 64 r + lane of a block is
+// 16 bytes of column chunk / CPR of column group cg (rows past N repeat the
+// last one), block b goes to ring slot b % SK_RING. It meets barrier 0
+// once block 0 has landed and barrier b+1 once block b+1 has.
+template <class BP, int CW>
+__device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_t row_bytes, int N, int cg, int kb0,
+                                          int nblk, int lane, uint8_t *ring) {
+    using Sh = SkShape<BP, CW>;
+    uint32_t goff[Sh::ROUNDS];
+#pragma unroll
+    for (int r = 0; r < Sh::ROUNDS; r++) {
+        const int c = 64 * r + lane, col = c / BP::CPR, part = c - col * BP::CPR;
+        goff[r] = (uint32_t)min(cg * Sh::COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
+    }
+    const uint8_t *wb = W + (size_t)kb0 * BP::RB;
+    auto issue = [&](int b) {
+        const uint8_t *g = wb + (size_t)b * BP::RB;
+        uint8_t *dst = ring + (b % SK_RING) * Sh::SLOT;
+#pragma unroll
+        for (int r = 0; r < Sh::ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
+    };
+    // barrier 0: block 0 landed (blocks 1..SK_RING-2 may be in flight)
+    for (int j = 0; j < SK_RING - 1; j++)
+        if (j < nblk) issue(j);
+    if (nblk >= SK_RING - 1)
+        wait_vm_barrier<(SK_RING - 2) * Sh::ROUNDS>();
+    else
+        wait_vm_barrier<0>();
+    for (int b = 0; b < nblk; b++) {
+        // barrier b+1: block b+1 landed. Block b-1's slot is free since
+        // barrier b: refill it with block b+SK_RING-1 first, whose loads (and
+        // those of the blocks between) may stay outstanding; near the end,
+        // wait for everything.
+        if (b + SK_RING - 1 < nblk) {
+            issue(b + SK_RING - 1);
+            wait_vm_barrier<(SK_RING - 2) * Sh::ROUNDS>();
+        } else {
+            wait_vm_barrier<0>();
+        }
+    }
+}
+
 template <class BP, int CW>
 __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((CW + 4) / 4))) void gemm_skinny_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
     float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
     using Sh = SkShape<BP, CW>;
-    constexpr int SK_CW = CW, SK_COLS = Sh::COLS, SK_CHUNKS = Sh::CHUNKS, SK_ROUNDS = Sh::ROUNDS, SK_SLOT = Sh::SLOT;
+    constexpr int SK_CW = CW, SK_SLOT = Sh::SLOT;
     __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
     const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -799,40 +841,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
     const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
 
     if (wv == SK_CW) {
-        // loader: chunk 64 r + lane of a block is 16 bytes of column
-        // (chunk / 9) of the group; rows past N repeat the last one
-        uint32_t goff[SK_ROUNDS];
-#pragma unroll
-        for (int r = 0; r < SK_ROUNDS; r++) {
-            const int c = 64 * r + lane, col = c / BP::CPR, part = c - col * BP::CPR;
-            goff[r] = (uint32_t)min(cg * SK_COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
-        }
-        const uint8_t *wb = W + (size_t)kb0 * BP::RB;
-        auto issue = [&](int b) {  // block b into slot b % SK_RING
-            const uint8_t *g = wb + (size_t)b * BP::RB;
-            uint8_t *dst = ring + (b % SK_RING) * SK_SLOT;
-#pragma unroll
-            for (int r = 0; r < SK_ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
-        };
-        // barrier 0: block 0 landed (blocks 1..SK_RING-2 may be in flight)
-        for (int j = 0; j < SK_RING - 1; j++)
-            if (j < nblk) issue(j);
-        if (nblk >= SK_RING - 1)
-            wait_vm_barrier<(SK_RING - 2) * SK_ROUNDS>();
-        else
-            wait_vm_barrier<0>();
-        for (int b = 0; b < nblk; b++) {
-            // barrier b+1: block b+1 landed. Block b-1's slot is free since
-            // barrier b: refill it with block b+SK_RING-1 first, whose loads
-            // (and those of the blocks between) may stay outstanding; near
-            // the end, wait for everything.
-            if (b + SK_RING - 1 < nblk) {
-                issue(b + SK_RING - 1);
-                wait_vm_barrier<(SK_RING - 2) * SK_ROUNDS>();
-            } else {
-                wait_vm_barrier<0>();
-            }
-        }
+        sk_loader<BP, CW>(W, row_bytes, N, cg, kb0, nblk, lane, ring);
         return;
     }
 
