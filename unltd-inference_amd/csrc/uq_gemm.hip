@@ -93,28 +93,33 @@ GemmWs ws_carve(uint8_t *base, int M, int K) {
 }
 
 // ------------------------------------------------------------ prep kernels
-// gemm_scale_kernel: one wave per row finds max |x| and writes the row
-// scale s_m = 2^(e-10) with max|x| in [2^(e-1), 2^e), so that x' = x / s_m
-// has max|x'| in [512, 1024). The exponent is kept at or above -115 (s_m
-// and 1/s_m stay normal floats; rows that small only lose precision they
-// cannot show). A NaN or an infinity makes s_m NaN: the convert kernel then
-// writes zero planes and the GEMM's NaN scale makes the row's outputs NaN.
-constexpr int SCALE_ROWS = 4;  // rows (waves) per workgroup
-__global__ __launch_bounds__(64 * SCALE_ROWS) void gemm_scale_kernel(const float *__restrict__ X, int K, int M,
-                                                                     float *__restrict__ scale) {
-    const int lane = threadIdx.x & 63, m = blockIdx.x * SCALE_ROWS + (threadIdx.x >> 6);
-    if (m >= M) return;
+// gemm_scale_kernel: one workgroup of SCALE_WAVES waves per row finds max
+// |x| and writes the row scale s_m = 2^(e-10) with max|x| in [2^(e-1), 2^e),
+// so that x' = x / s_m has max|x'| in [512, 1024). The exponent is kept at
+// or above -115 (s_m and 1/s_m stay normal floats; rows that small only lose
+// precision they cannot show). A NaN or an infinity makes s_m NaN: the
+// convert kernel then writes zero planes and the GEMM's NaN scale makes the
+// row's outputs NaN. (One wave per row took two to six rounds of dependent
+// loads at K = 4096-12288.)
+constexpr int SCALE_WAVES = 4;
+__global__ __launch_bounds__(64 * SCALE_WAVES) void gemm_scale_kernel(const float *__restrict__ X, int K, int M,
+                                                                      float *__restrict__ scale) {
+    __shared__ uint32_t red[SCALE_WAVES];
+    const int t = threadIdx.x, lane = t & 63, m = blockIdx.x;
     const float4 *x = (const float4 *)(X + (size_t)m * K);
     const int n4 = K >> 2;
     uint32_t mb = 0;
-#pragma unroll 8
-    for (int i = lane; i < n4; i += 64) {
+#pragma unroll 4
+    for (int i = t; i < n4; i += 64 * SCALE_WAVES) {
         const float4 a = x[i];
         mb = max(mb, max(max(__float_as_uint(a.x) & 0x7FFFFFFFu, __float_as_uint(a.y) & 0x7FFFFFFFu),
                          max(__float_as_uint(a.z) & 0x7FFFFFFFu, __float_as_uint(a.w) & 0x7FFFFFFFu)));
     }
     for (int off = 1; off < 64; off <<= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
-    if (lane == 0) {
+    if (lane == 0) red[t >> 6] = mb;
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < SCALE_WAVES; w++) mb = max(mb, red[w]);
         int ex = 0;
         if (mb) (void)frexpf(__uint_as_float(mb), &ex);
         scale[m] = mb < 0x7F800000u ? ldexpf(1.0f, max(ex, -115) - 10) : __uint_as_float(0x7FC00000u);
@@ -1150,8 +1155,7 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
     if (wsb < gemm_ws_bytes(w, M) || !wsp) return hipErrorInvalidValue;
     const GemmWs ws = ws_carve((uint8_t *)wsp, M, K);
     float *part = p.ks > 1 ? (float *)((uint8_t *)wsp + prep_bytes(M, K)) : nullptr;
-    hipLaunchKernelGGL(gemm_scale_kernel, dim3((M + SCALE_ROWS - 1) / SCALE_ROWS), dim3(64 * SCALE_ROWS), 0, s, X, K, M,
-                       ws.scale);
+    hipLaunchKernelGGL(gemm_scale_kernel, dim3(M), dim3(64 * SCALE_WAVES), 0, s, X, K, M, ws.scale);
     hipLaunchKernelGGL(gemm_convert_kernel, dim3((M + 7) / 8, K / 256), dim3(256), 0, s, X, K, M, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
