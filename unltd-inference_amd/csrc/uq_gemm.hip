@@ -723,12 +723,23 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     }
 }
 
-// Sum of the ks partial results of a split-K launch, in range order.
+// Sum of the ks partial results of a split-K launch, in range order
+// (v = P_0, v += P_1, ...). The partials of eight ranges are loaded before
+// any is added, so a thread waits for one round of loads per eight ranges
+// instead of one per range.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ P, int ks, size_t stride,
                                                           size_t MN, float *__restrict__ Y) {
+    constexpr int G = 8;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-        float v = P[i];
-        for (int k = 1; k < ks; k++) v += P[(size_t)k * stride + i];
+        float v = 0.0f;
+        for (int k0 = 0; k0 < ks; k0 += G) {
+            float p[G];
+#pragma unroll
+            for (int j = 0; j < G; j++) p[j] = k0 + j < ks ? P[(size_t)(k0 + j) * stride + i] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < G; j++)
+                if (k0 + j < ks) v = (k0 + j == 0) ? p[j] : v + p[j];
+        }
         Y[i] = v;
     }
 }
