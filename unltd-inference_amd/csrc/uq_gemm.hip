@@ -866,6 +866,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
     const int n0 = (cg * SK_CW + wv) * 32;
     float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
     const int am = min(lr, M - 1);
+    const float rs_lane = ws.scale[am];  // row lr's scale, read long before the epilogue
     const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
     const uint32_t pbytes = (uint32_t)((size_t)M * K * 2);
     const auto rah = buf_rsrc(ws.ahi, pbytes), ral = buf_rsrc(ws.alo, pbytes);
@@ -1034,7 +1035,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int m = 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float rs = ws.scale[min(m, M - 1)];
+        const float rs = __shfl(rs_lane, min(m, M - 1));  // lane m holds row m's scale (m < 32)
         const float v = (float)((C[r] + (double)Cm[r]) * (double)rs);
         if (m < M && n < N) Yo[(size_t)m * N + n] = v;
     }
