@@ -478,6 +478,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     // Buffer loads: the lane part of the offset in a VGPR, the k-step part
     // wave-uniform in an SGPR (the planes are below 2 GiB).
     const int am = min(m0 + 32 * wm + lr, M - 1);
+    const float rs_lane = ws.scale[am];  // row 32 wm + lr's scale, read long before the epilogue
     const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
     const uint32_t pbytes = (uint32_t)((size_t)M * K * 2);
     const auto rah = buf_rsrc(ws.ahi, pbytes), ral = buf_rsrc(ws.alo, pbytes);
@@ -688,7 +689,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     // store: lane holds column lr of each tile, rows 8*(r/4) + 4*lh + r%4
     float rs[16];
 #pragma unroll
-    for (int r = 0; r < 16; r++) rs[r] = ws.scale[min(m0 + 32 * wm + 8 * (r >> 2) + 4 * lh + (r & 3), M - 1)];
+    for (int r = 0; r < 16; r++) rs[r] = __shfl(rs_lane, 8 * (r >> 2) + 4 * lh + (r & 3));  // lane x: row 32 wm + x
     f16x Yv[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++)
