@@ -471,19 +471,35 @@ def cpu_baseline(w, x):
     q8k_1 = rate(O.gemv_quant_q8k, 1, 3)
     exact_1 = rate(O.gemv_quant, 1, 3)
     q8k_all = rate(O.gemv_quant_q8k, ncpu, 3)
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": q8k_1, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"gemv_quant_q8k (the reference forward's path) over rows 0..{rows} of the same "
                       f"Q6_K head, C restatement of quants.rs built -O2 -ffp-contract=off, median of 3",
             "gemv_quant_exact_1core_gbs": exact_1, "q8k_all_cores_gbs": q8k_all, "all_cores": ncpu,
-            "cpu_model": cpu, "nproc": os.cpu_count()}
+            **host_cpu(), "nproc": os.cpu_count()}
+
+
+def host_cpu():
+    """The host CPU as /proc/cpuinfo reports it: the full model string of the
+    first processor, its family / model / stepping numbers, clock, cache and
+    vector extensions, and the count of logical processors listed."""
+    first, n = {}, 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("processor"):
+                    n += 1
+                if n == 1 and ":" in line:
+                    k, v = line.split(":", 1)
+                    first.setdefault(k.strip(), v.strip())
+    except OSError:
+        pass
+    flags = set(first.get("flags", "").split())
+    return {"cpu_model": first.get("model name", "unknown"),
+            "cpu_vendor": first.get("vendor_id"), "cpu_family": first.get("cpu family"),
+            "cpu_model_number": first.get("model"), "cpu_stepping": first.get("stepping"),
+            "cpu_mhz": first.get("cpu MHz"), "cpu_cache": first.get("cache size"),
+            "cpu_vector_ext": sorted(flags & {"avx2", "avx512f", "avx512bw", "avx512_vnni", "avx512_bf16", "fma"}),
+            "cpuinfo_processors": n}
 
 
 def load_traffic():

@@ -80,6 +80,15 @@ uq_status uq_gdn_fused_step_d(float *d_state, float *d_out, const float *d_q, co
                               const float *d_gate, const float *d_beta, size_t dim, size_t heads, float scale,
                               void *stream);
 
+/* ---- Off the Qwen3.5 forward's path --------------------------------------
+ * The forward imports dot_f32, gdn_fused_step, gemv_quant_q8k, l2_norm_rows,
+ * rmsnorm, rope_apply_imrope, sigmoid, silu, softmax, softplus, ssm_conv and
+ * swiglu from unltd-tensor (qwen35_forward.rs:38-41). rope_apply_llama,
+ * rope_apply_neox, gelu_tanh and matmul_f32_acc below are the rest of
+ * kernels.rs's public surface: exported for callers of that surface, not
+ * used by any layer of this library (uq_layer.h) and not tuned.
+ * ------------------------------------------------------------------------ */
+
 /* rope_apply_llama (kernels.rs:109-125) and rope_apply_neox (:131-148), in
  * place. Panics: len(x) odd, len(freqs) < len(x)/2. */
 uq_status uq_rope_llama(float *x, size_t x_len, const float *freqs, size_t freqs_len, size_t pos);

@@ -135,6 +135,69 @@ def test_quantize_q8_k_bit_exact():
     assert np.array_equal(got["bsums"], ref["bsums"])
 
 
+def _non_finite_x(K, with_inf):
+    """N(0,1) activations with a quiet NaN (block 0), a NaN with the sign bit
+    set (block 1) and, with_inf, +inf (block 2), -inf (block 3) and a NaN
+    beside an infinity (block 4); later blocks are finite."""
+    x = S.activations(K, seed=21)
+    x[5] = np.float32(np.nan)
+    x[256 + 9] = np.uint32(0xFFC00000).view(np.float32)
+    if with_inf:
+        x[512 + 77] = np.inf
+        x[768 + 3] = -np.inf
+        x[1024 + 1], x[1024 + 200] = np.nan, np.inf
+    return x
+
+
+def assert_bitwise_or_both_nan(got, ref, what):
+    """Bit-exact wherever the reference is a number; NaN exactly where it is
+    NaN (the NaN an invalid operation makes is positive on the GPU and
+    negative on x86, so NaN bits are not compared)."""
+    got, ref = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan), f"{what}: NaN positions differ"
+    assert_bitwise(got[~nan], ref[~nan], what)
+
+
+@pytest.mark.parametrize("with_inf", [False, True])
+def test_quantize_q8_k_non_finite_bit_exact(with_inf):
+    """quantize_q8_k (quants.rs:250-290) on NaN and infinite activations: the
+    strict argmax skips NaN, nearest_int's magic-number add maps a quiet NaN
+    product to 0, and a block whose maximum is +-inf gets iscale = -+0 and
+    d = -+inf with every quant 0."""
+    x = _non_finite_x(4096, with_inf)
+    got, ref = uq.quantize_q8_k(x), O.quantize_q8_k(x)
+    assert_bitwise(got["d"], ref["d"], "q8k d")
+    assert np.array_equal(got["qs"], ref["qs"])
+    assert np.array_equal(got["bsums"], ref["bsums"])
+    if with_inf:
+        assert np.isinf(ref["d"][2]) and np.isinf(ref["d"][3])
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+@pytest.mark.parametrize("with_inf", [False, True])
+def test_gemv_quant_q8k_non_finite_activations(dtype, with_inf):
+    """gemv_quant_q8k (quants.rs:474-515) with NaN / infinite activations,
+    host mirror and batched device launch: NaNs quantize to 0, so such x
+    gives the reference's finite outputs bit for bit; an infinity makes the
+    block's d infinite and every row NaN, as in the reference."""
+    K, N = 4096, 300
+    w = S.weights(dtype, N, K, seed=K + N + dtype)
+    x = _non_finite_x(K, with_inf)
+    ref = np.zeros(N, np.float32)
+    O.gemv_quant_q8k(ref, x, w, K, N, dtype)
+    assert np.all(np.isnan(ref)) if with_inf else np.all(np.isfinite(ref))
+    got = np.zeros(N, np.float32)
+    uq.gemv_quant_q8k(got, x, w, K, N, dtype)
+    assert_bitwise_or_both_nan(got, ref, f"gemv_quant_q8k dtype {dtype} inf {with_inf}")
+    W = uq.Weights(w, dtype, K, N)
+    dx, dys = uq.DeviceArray.from_numpy(x), [uq.DeviceArray(4 * N) for _ in range(2)]
+    uq.gemv_q8k_batch([W, W], dx, dys)
+    for i, dy in enumerate(dys):
+        assert_bitwise_or_both_nan(dy.download(np.float32, N), ref, f"q8k batch {i} dtype {dtype} inf {with_inf}")
+    W.free()
+
+
 def test_swiglu_close():
     rng = np.random.default_rng(1)
     g = (rng.standard_normal(1 << 16) * 20).astype(np.float32)

@@ -7,6 +7,11 @@ row, the second smaller, check that the array's leftover contents from the
 first call do not leak into the second; a call whose workspace exceeds the
 array is refused with UQ_ERR_ARG before anything is launched.
 """
+import json
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -53,3 +58,29 @@ def test_gemm_static_refuses_a_workspace_beyond_the_array():
     uq.synchronize()
     assert np.all(dy.download(np.float32, M * N) == 7.0), "nothing written after the refusal"
     W.free()
+
+
+@pytest.mark.parametrize("dtype,K,N,M", [(S.F32, 4096, 64, 2048), (S.Q4_K, 4096, 300, 1)])
+def test_gemm_static_needs_no_workspace_for_gemv_calls(dtype, K, N, M):
+    """Calls that run as GEMVs (F32 weights, one row) need no workspace:
+    uq_gemm_static takes them even where the activation planes of an MFMA
+    call (4*M*K bytes, 32 MiB here for F32) would exceed the fixed array,
+    with uq_gemm's bits."""
+    W = uq.Weights(S.weights(dtype, N, K, seed=3), dtype, K, N)
+    X = S.activations(K, seed=4, rows=M).reshape(M, K)
+    got = _run(uq.gemm_static, W, X, N)
+    ref = _run(uq.gemm, W, X, N)
+    assert_bitwise(got, ref, f"gemm_static vs gemm dtype {dtype} M={M}")
+    W.free()
+
+
+def test_gemm_static_first_call_captured_in_a_graph():
+    """The first uq_gemm_static call of a fresh process (its one-time set-up
+    inside the capture), replayed twice from a HIP graph: every replay equals
+    an eager uq_gemm bit for bit (tests/capture_child.py, a child process)."""
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "capture_child.py")
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=300)
+    print(r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, f"child exit {r.returncode}: {r.stdout[-2000:]} {r.stderr[-2000:]}"
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["ok"], out

@@ -126,17 +126,7 @@ UQ_HD uint32_t ld1(const uint8_t *p) {
 }
 // The same loads from a 2-byte-aligned address (Q6_K blocks are 210 bytes).
 // gfx950 global loads run in unaligned mode, so this is still one
-// global_load_dwordx4 / global_load_dword. On the device these weight-stream
-// loads carry the nontemporal hint (each weight byte is read once).
-#if defined(__HIP_DEVICE_COMPILE__) && defined(UQ_NT_LOADS)
-typedef uint32_t v4u_a2 __attribute__((ext_vector_type(4), aligned(2)));
-typedef uint32_t u32_a2 __attribute__((aligned(2)));
-UQ_HD u4 ldu4(const uint8_t *p) {
-    const auto v = __builtin_nontemporal_load((const v4u_a2 *)p);
-    return u4{v.x, v.y, v.z, v.w};
-}
-UQ_HD uint32_t ldu1(const uint8_t *p) { return __builtin_nontemporal_load((const u32_a2 *)p); }
-#else
+// global_load_dwordx4 / global_load_dword.
 UQ_HD u4 ldu4(const uint8_t *p) {
     u4 v;
     __builtin_memcpy(&v, p, 16);
@@ -147,7 +137,6 @@ UQ_HD uint32_t ldu1(const uint8_t *p) {
     __builtin_memcpy(&v, p, 4);
     return v;
 }
-#endif
 
 // 4x4 byte transpose: t[i] = {a.i, b.i, c.i, d.i}
 UQ_HD void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&t)[4]) {

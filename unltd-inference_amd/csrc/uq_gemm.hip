@@ -1131,13 +1131,6 @@ hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &
 
 }  // namespace
 
-// Workspace bytes of one uq_gemm call (0: the call needs none).
-size_t gemm_ws_bytes(const WeightsView &w, int M) {
-    if (M == 0 || w.dim_out == 0 || w.dim_in == 0) return 0;
-    const Plan p = plan_for(w.dtype, M, w.dim_out, w.dim_in);
-    return prep_bytes(M, w.dim_in) + (p.ks > 1 ? (size_t)p.ks * part_stride(M, w.dim_out) * 4 : 0);
-}
-
 // Formats and sizes the MFMA path takes: Q4_K, Q6_K, Q8_0 with K a multiple
 // of 256 and at most 65535 blocks of 256 (the convert kernel's grid), the
 // tensor below 4 GiB and the activation planes below 2 GiB (the kernel forms
@@ -1146,6 +1139,14 @@ bool gemm_mfma_ok(const WeightsView &w, int M) {
     const bool fmt = w.dtype == UQ_Q4_K || w.dtype == UQ_Q6_K || w.dtype == UQ_Q8_0;
     return fmt && w.dim_in % 256 == 0 && w.dim_in / 256 <= 65535 && (size_t)w.dim_out * w.row_bytes < ((size_t)1 << 32) &&
            (size_t)M * w.dim_in * 2 < ((size_t)1 << 31);
+}
+
+// Workspace bytes of one uq_gemm call (0: the call needs none: no rows, an
+// empty dot, or a call that runs as GEMVs).
+size_t gemm_ws_bytes(const WeightsView &w, int M) {
+    if (M == 0 || w.dim_out == 0 || w.dim_in == 0 || M == 1 || !gemm_mfma_ok(w, M)) return 0;
+    const Plan p = plan_for(w.dtype, M, w.dim_out, w.dim_in);
+    return prep_bytes(M, w.dim_in) + (p.ks > 1 ? (size_t)p.ks * part_stride(M, w.dim_out) * 4 : 0);
 }
 
 hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y, void *wsp, size_t wsb, hipStream_t s) {
@@ -1200,6 +1201,7 @@ hipError_t scratch_ptr(void **out) {
     std::lock_guard<std::mutex> g(mu);
     if (!ptr[dev]) {
         void *p = nullptr;
+        RelaxedCapture relax;
         if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
         ptr[dev] = p;
     }

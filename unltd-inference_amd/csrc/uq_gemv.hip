@@ -1810,6 +1810,7 @@ hipError_t allow_lds(const void *kernel, size_t lds) {
     std::lock_guard<std::mutex> g(mu);
     size_t &have = done[{kernel, dev}];
     if (have >= lds) return hipSuccess;
+    RelaxedCapture relax;
     e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e == hipSuccess) have = lds;
     return e;

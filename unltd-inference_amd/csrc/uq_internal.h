@@ -35,6 +35,18 @@ constexpr int BQ8_0 = 34;
 // on the current device; a no-op after the first call per kernel and device.
 hipError_t allow_lds(const void *kernel, size_t lds);
 
+// Relaxes the calling thread's stream-capture mode for the guard's lifetime,
+// so that one-time set-up calls (function attributes, symbol addresses) made
+// by the first call of an entry point stay legal when that call is being
+// captured into a HIP graph; the previous mode is restored after.
+struct RelaxedCapture {
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    RelaxedCapture() { (void)hipThreadExchangeStreamCaptureMode(&mode); }
+    ~RelaxedCapture() { (void)hipThreadExchangeStreamCaptureMode(&mode); }
+    RelaxedCapture(const RelaxedCapture &) = delete;
+    RelaxedCapture &operator=(const RelaxedCapture &) = delete;
+};
+
 // Per-layer non-linear ops (uq_ops.hip).
 hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s);
 // rows of n, xs / ys floats apart in x / out; xb: normalise x + xb, written
