@@ -253,6 +253,34 @@ def bench_gemm(hip, steps, warmup):
             "by_m": out["q4k"]["by_m"], "q6k": out["q6k"], "q80": out["q80"]}
 
 
+def bench_gemm_q8k(hip, steps, warmup):
+    """Bit-exact batched prefill (uq_gemm_q8k: every row gemv_quant_q8k, the
+    reference forward's numerics) over M: Q4_K N=12288 K=4096 (the prefill
+    workload) and Q6_K N=4096 K=12288; per_row_gemv_us is one uq_gemv_q8k
+    call (M of them is what the reference's token-serial prefill issues)."""
+    s = hip.stream()
+    out = {}
+    for dt, name, K, N in ((S.Q4_K, "q4k", 4096, 12288), (S.Q6_K, "q6k", 12288, 4096)):
+        w = S.weights(dt, N, K, seed=S.seed_for(3))
+        W = uq.Weights(w, dt, K, N)
+        X = S.activations(K, seed=S.seed_for(3), rows=512)
+        dx, dy = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * 512 * N)
+        by_m = {}
+        for M in (1, 8, 32, 128, 512):
+            st = max(10, steps // (1 if M < 128 else 2))
+            wall, ev = timed(hip, lambda: uq.gemm_q8k(W, M, dx, dy, s), st, max(warmup, 20), s)
+            t = ev * 1e-3 / st
+            by_m[str(M)] = {"us": t * 1e6, "tflops": 2 * M * N * K / t / 1e12,
+                            "frac_bf16_peak": 2 * M * N * K / t / 1e12 / BF16_PEAK_TFLOPS,
+                            "weight_gbs": w.size / t / 1e9}
+        out[name] = {"N": N, "K": K, "by_m": by_m, "per_row_gemv_us": by_m["1"]["us"]}
+        W.free()
+        dx.free()
+        dy.free()
+    return {"config": "bit-exact prefill GEMM (uq_gemm_q8k, gemv_quant_q8k per row) M sweeps; q4k is the prefill "
+                      "workload N=12288 K=4096", **out}
+
+
 def decode_layers():
     """Synthetic Qwen3.5-style hybrid 9B: 32 layers, hidden 4096; layer il is
     full attention when (il+1) % 4 == 0 (qwen35.rs:289-291), else GatedDeltaNet.
@@ -534,7 +562,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of: head,q4k,q4k_large,ffn,gemm,decode")
+    ap.add_argument("--only", default="", help="comma list of: head,q4k,q4k_large,ffn,gemm,gemm_q8k,decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run two 1 GiB device copies (reference dispatches for counter runs)")
     a = ap.parse_args()
@@ -551,7 +579,7 @@ def main():
     extra = {"head_q8k_bit_exact": head["q8k"]}
     if not a.quick:
         for name, fn in (("q4k", bench_q4k_small), ("q4k_large", bench_q4k_large), ("ffn", bench_ffn),
-                         ("gemm", bench_gemm)):
+                         ("gemm", bench_gemm), ("gemm_q8k", bench_gemm_q8k)):
             if not only or name in only:
                 log("bench:", name)
                 extra[name] = fn(hip, a.steps, a.warmup)

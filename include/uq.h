@@ -18,13 +18,13 @@
  *    calling thread).
  *  - Device entry points take device pointers and a hipStream_t (void*; NULL
  *    = the null stream). They are asynchronous on that stream and allocate
- *    no device memory, except uq_gemm (see there). Weights live behind a
+ *    no device memory, except uq_gemm and uq_gemm_q8k (see there). Weights live behind a
  *    uq_weights handle whose bytes are copied to HBM unchanged.
  *  - Numerics: uq_gemv_quant / uq_gemv / uq_gemm / uq_ffn_swiglu follow
  *    gemv_quant's semantics (f32 result of the exact dequantized weights times
  *    f32 x; matched within |y-r| <= 1e-4 + 1e-3*|r|). uq_gemv_quant_q8k /
- *    uq_gemv_q8k, uq_quantize_q8_k, the dequantize and unpack exports are
- *    bit-exact with the reference.
+ *    uq_gemv_q8k / uq_gemm_q8k, uq_quantize_q8_k, the dequantize and unpack
+ *    exports are bit-exact with the reference.
  */
 #ifndef UQ_H
 #define UQ_H
@@ -182,6 +182,22 @@ uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count
  * a HIP graph once a call of that size or larger has run on the stream. */
 uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                   void *stream);
+
+/* Batched prefill in the reference forward's numerics: d_y[m][dim_out] =
+ * gemv_quant_q8k(W, d_x[m][dim_in]) (quants.rs:474-515) for m < m_rows, bit
+ * for bit per row. The reference prefills one token at a time through
+ * gemv_quant_q8k (greedy.rs:55-65; qwen35_forward.rs:365-401); this is
+ * those m_rows calls in one weight pass: each row quantized to Q8_K as
+ * quantize_q8_k does, the eight integer lane sums per block formed exactly
+ * on the f16 MFMA, the f32 epilogue of dot_q4_k_q8_k / dot_q6_k_q8_k
+ * replayed per output in the reference's order. Q4_K and Q6_K only
+ * (UQ_ERR_DTYPE otherwise, as the reference panics, quants.rs:497-499);
+ * m_rows == 1 runs uq_gemv_q8k. Workspace (about 2*m_rows*dim_in bytes) as
+ * uq_gemm's: library-owned per (device, stream), grown on demand, never
+ * freed; a call can be captured in a HIP graph once one of that size or
+ * larger has run on the stream. */
+uq_status uq_gemm_q8k(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
+                      void *stream);
 
 /* uq_gemm that allocates nothing: no reference counterpart. For callers that
  * cannot allocate device memory inside the call (HIP graph capture, tight

@@ -1,0 +1,198 @@
+"""GPU parity of uq_gemm_q8k through the C ABI: Y[m] = gemv_quant_q8k(W, X[m])
+(quants.rs:474-515) for every row, bit for bit against the oracle.
+
+The reference forward prefills token by token through gemv_quant_q8k
+(greedy.rs:55-65; qwen35_forward.rs:365-401), so every row of the batched
+call must carry exactly the bits of that token's call. The shapes cover the
+prefill workload itself (Q4_K 12288 x 4096 at M = 512), the Q6_K FFN-down
+shape (4096 x 12288), each workgroup width the launcher picks (8, 4, 2 and
+1 waves: large M, M around 128, small M), ragged M (padding rows) and N
+(columns past the end), one block, many blocks, and the edge cases of the
+quantizer and of the block scales.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import uq
+import uq.synth as S
+from helpers import assert_bitwise
+
+pytestmark = pytest.mark.gpu
+NT = min(16, os.cpu_count() or 1)
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run(dtype, w, K, N, X):
+    M = X.shape[0]
+    W = uq.Weights(w, dtype, K, N)
+    dx, dy = uq.DeviceArray.from_numpy(np.ascontiguousarray(X, np.float32)), uq.DeviceArray(4 * M * N)
+    dy.upload(np.full(M * N, np.nan, np.float32))
+    uq.gemm_q8k(W, M, dx, dy)
+    Y = dy.download(np.float32, M * N).reshape(M, N)
+    W.free()
+    return Y
+
+
+def oracle_rows(dtype, w, K, N, X, rows=None):
+    rows = range(X.shape[0]) if rows is None else rows
+    out = {}
+    for m in rows:
+        r = np.zeros(N, np.float32)
+        O.gemv_quant_q8k(r, X[m], w, K, N, dtype, nthreads=NT)
+        out[m] = r
+    return out
+
+
+def assert_rows(Y, R, what):
+    for m, r in R.items():
+        nan = np.isnan(r)
+        assert np.array_equal(np.isnan(Y[m]), nan), f"{what} row {m}: NaN positions differ"
+        assert_bitwise(Y[m][~nan], r[~nan], f"{what} row {m}")
+
+
+def test_gemm_q8k_prefill_config_every_row():
+    """The prefill workload: Q4_K N = 12288, K = 4096, M = 512 (eight-wave
+    workgroups, 16 blocks each), every row against the oracle."""
+    K, N, M = 4096, 12288, 512
+    log(f"gemm_q8k q4k K={K} N={N} M={M}")
+    w = S.weights(S.Q4_K, N, K, seed=S.seed_for(3))
+    X = S.activations(K, seed=S.seed_for(3) + M, rows=M).reshape(M, K)
+    Y = run(S.Q4_K, w, K, N, X)
+    assert_rows(Y, oracle_rows(S.Q4_K, w, K, N, X), "q4k prefill")
+
+
+def test_gemm_q8k_q6k_down_shape_every_row():
+    """Q6_K N = 4096, K = 12288 (an FFN down projection), M = 300: 48 blocks
+    per row, ragged M (the last tile's padding rows), every row."""
+    K, N, M = 12288, 4096, 300
+    log(f"gemm_q8k q6k K={K} N={N} M={M}")
+    w = S.weights(S.Q6_K, N, K, seed=S.seed_for(2))
+    X = S.activations(K, seed=M + 1, rows=M).reshape(M, K)
+    Y = run(S.Q6_K, w, K, N, X)
+    assert_rows(Y, oracle_rows(S.Q6_K, w, K, N, X), "q6k down")
+
+
+SHAPES = [
+    # (K, N, M): waves per workgroup from the tile count (8 at many tiles, then 4, 2, 1)
+    (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
+    (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
+]
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+@pytest.mark.parametrize("K,N,M", SHAPES)
+def test_gemm_q8k_shapes(dtype, K, N, M):
+    log(f"gemm_q8k dtype={dtype} K={K} N={N} M={M}")
+    w = S.weights(dtype, N, K, seed=K + N + M + dtype)
+    X = S.activations(K, seed=M * 7 + dtype, rows=M).reshape(M, K)
+    Y = run(dtype, w, K, N, X)
+    rows = sorted({0, 1, M // 2, M - 1} | set(range(0, M, max(1, M // 12))))
+    assert_rows(Y, oracle_rows(dtype, w, K, N, X, rows), f"dtype {dtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+def test_gemm_q8k_equals_per_row_gemv_q8k(dtype):
+    """Every row equals the device's own gemv_quant_q8k of that row (the
+    decode kernel, checked against the oracle elsewhere), at a shape with
+    several tiles in both directions."""
+    K, N, M = 2048, 1536, 70
+    w = S.weights(dtype, N, K, seed=21 + dtype)
+    X = S.activations(K, seed=22, rows=M).reshape(M, K)
+    Y = run(dtype, w, K, N, X)
+    W = uq.Weights(w, dtype, K, N)
+    for m in range(M):
+        dx, dy = uq.DeviceArray.from_numpy(X[m]), uq.DeviceArray(4 * N)
+        uq.gemv_q8k(W, dx, dy)
+        assert_bitwise(Y[m], dy.download(np.float32, N), f"row {m} vs gemv_q8k")
+    W.free()
+
+
+def test_gemm_q8k_q6k_full_int8_scales():
+    """Q6_K scales over the whole int8 range (real files reach -128): the
+    exact (sc & ~1)*q + (sc & 1)*q operand pair."""
+    K, N, M = 2048, 512, 80
+    w = S.weights(S.Q6_K, N, K, seed=5).reshape(-1, 210)
+    rng = np.random.default_rng(6)
+    w[:, 192:208] = rng.integers(-128, 128, size=(w.shape[0], 16)).astype(np.int8).view(np.uint8)
+    w[::7, 192:208] = np.uint8(0x80)
+    w = w.reshape(-1)
+    X = S.activations(K, seed=7, rows=M).reshape(M, K)
+    Y = run(S.Q6_K, w, K, N, X)
+    assert_rows(Y, oracle_rows(S.Q6_K, w, K, N, X), "q6k int8 scales")
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+def test_gemm_q8k_special_block_scales(dtype):
+    """Blocks whose f16 d (and Q4_K dmin) is subnormal, the largest finite,
+    zero, negative, infinite or NaN (f16_to_f32, quants.rs:44-72): numbers
+    bit for bit, NaN where the reference is NaN."""
+    K, N, M = 1024, 96, 40
+    w = S.weights(dtype, N, K, seed=K + N + dtype).reshape(N, -1)
+    bb = 144 if dtype == S.Q4_K else 210
+    doff = 0 if dtype == S.Q4_K else 208
+    specials = [0x0001, 0x03FF, 0x0200, 0x7BFF, 0x0000, 0x8000, 0x83FF, 0xFBFF, 0x7C00, 0xFC00, 0x7E00, 0x7D01]
+    rng = np.random.default_rng(dtype + K)
+    for r in range(N):
+        blk = int(rng.integers(0, K // 256))
+        v = specials[r % len(specials)]
+        w[r, blk * bb + doff] = v & 0xFF
+        w[r, blk * bb + doff + 1] = v >> 8
+        if dtype == S.Q4_K and r % 3 == 0:
+            v2 = specials[(r // 3) % len(specials)]
+            w[r, blk * bb + 2] = v2 & 0xFF
+            w[r, blk * bb + 3] = v2 >> 8
+    w = w.reshape(-1)
+    X = S.activations(K, seed=N + 5, rows=M).reshape(M, K)
+    Y = run(dtype, w, K, N, X)
+    R = oracle_rows(dtype, w, K, N, X)
+    assert any(np.isnan(r).any() for r in R.values()), "the test plants infinite and NaN scales"
+    assert_rows(Y, R, f"special scales dtype {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+def test_gemm_q8k_edge_activations(dtype):
+    """Rows of the quantizer's edge cases: zero rows and blocks, a negative
+    maximum, ties in |x|, subnormals, rows of very different magnitude, a
+    NaN (quantized to 0: the row stays finite) and an infinity (d = -inf:
+    the row is NaN in the reference and here)."""
+    K, N, M = 1024, 200, 36
+    rng = np.random.default_rng(dtype)
+    X = S.activations(K, seed=9, rows=M).reshape(M, K).copy()
+    X *= (10.0 ** rng.uniform(-6, 6, size=(M, 1))).astype(np.float32)
+    X[0] = 0.0
+    X[1, 256:512] = 0.0
+    X[2, 700] = -1e5
+    X[3, 5], X[3, 6] = 3.0e3, -3.0e3
+    X[4] = (rng.standard_normal(K) * 1e-41).astype(np.float32)
+    X[5, 17] = np.nan
+    X[6, 600] = np.inf
+    X[7, 1] = -np.inf
+    w = S.weights(dtype, N, K, seed=31 + dtype)
+    Y = run(dtype, w, K, N, X)
+    R = oracle_rows(dtype, w, K, N, X)
+    assert np.all(np.isfinite(R[5])) and np.all(np.isnan(R[6]))
+    assert_rows(Y, R, f"edge activations dtype {dtype}")
+
+
+def test_gemm_q8k_one_row_is_gemv_q8k_and_errors():
+    """m_rows == 1 runs the decode kernel (the same bits); Q8_0 and F32
+    weights are refused as gemv_quant_q8k panics (quants.rs:497-499)."""
+    K, N = 4096, 500
+    w = S.weights(S.Q4_K, N, K, seed=3)
+    X = S.activations(K, seed=4, rows=1).reshape(1, K)
+    Y = run(S.Q4_K, w, K, N, X)
+    assert_rows(Y, oracle_rows(S.Q4_K, w, K, N, X), "one row")
+    W = uq.Weights(S.weights(S.Q8_0, 64, 256, seed=1), S.Q8_0, 256, 64)
+    dx, dy = uq.DeviceArray(4 * 2 * 256), uq.DeviceArray(4 * 2 * 64)
+    with pytest.raises(uq.UqError) as e:
+        uq.gemm_q8k(W, 2, dx, dy)
+    assert e.value.kind == "DTYPE"
+    W.free()

@@ -562,6 +562,19 @@ uq_status uq_gemm(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, vo
     return UQ_OK;
 }
 
+uq_status uq_gemm_q8k(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, void *stream) {
+    uq_weights_s *w = handle(wh);
+    if (!w) return fail(UQ_ERR_ARG, "gemm_q8k: invalid handle");
+    if (w->dtype != UQ_Q4_K && w->dtype != UQ_Q6_K)
+        return fail(UQ_ERR_DTYPE, "gemm_q8k: dtype %s does not use the Q8_K dot", dtype_name(w->dtype));
+    if (m_rows == 0 || w->dim_out == 0) return UQ_OK;
+    if (m_rows > (size_t)INT_MAX / 2) return fail(UQ_ERR_ARG, "gemm_q8k: m_rows above INT_MAX / 2");
+    if (!d_y || (!d_x && w->dim_in)) return fail(UQ_ERR_ARG, "gemm_q8k: null device pointer");
+    if (w->dim_in / 256 > 65535) return fail(UQ_ERR_ARG, "gemm_q8k: dim_in above 65535 blocks of 256");
+    UQ_HIP(uq::launch_gemm_q8k(uq::view(*w), (int)m_rows, d_x, d_y, (hipStream_t)stream), "gemm_q8k launch");
+    return UQ_OK;
+}
+
 uq_status uq_gemm_static(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, void *stream) {
     uq_weights_s *w = handle(wh);
     if (!w) return fail(UQ_ERR_ARG, "gemm_static: invalid handle");

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "uq_policies.h"
+#include "uq_q8k_tiles.h"
 
 using namespace uq;
 
@@ -233,6 +234,117 @@ void emu_gemv_q8k(float *y, const float *x, const uint8_t *W, size_t row_bytes, 
     }
 }
 
+// uq_gemm_q8k (uq_gemm_q8k.hip) per (row, column, block) as the kernel forms
+// it: the activation octets filled through q8k_slot_elem (the prep
+// kernel), the weight octets decoded from the block's bytes through the
+// same gathers and bit-field inserts as the kernel, each lane sum the sum of
+// its octets' slot products (exact integers, as on the MFMA), the Q4_K min
+// sum from the block sums, and the reference's f32 epilogue.
+uint32_t dw_at(const uint8_t *p) {
+    uint32_t v;
+    std::memcpy(&v, p, 4);
+    return v;
+}
+
+template <bool Q6>
+void emu_gemm_q8k(float *Y, const float *X, int M, const uint8_t *W, size_t row_bytes, int K, int N) {
+    const int nblk = K >> 8, RB = Q6 ? 210 : 144;
+    // activation octets [m][b][l][h][o][s], block sums and d per (m, b)
+    std::vector<int8_t> A((size_t)M * nblk * 256);
+    std::vector<int> bsum((size_t)M * nblk * 16);
+    std::vector<float> d8((size_t)M * nblk);
+    for (int m = 0; m < M; m++)
+        for (int b = 0; b < nblk; b++) {
+            uint32_t q[64];
+            const size_t mb = (size_t)m * nblk + b;
+            quantize_block(X + (size_t)m * K + 256 * b, q, &bsum[mb * 16], &d8[mb]);
+            const int8_t *qs = (const int8_t *)q;
+            for (int l = 0; l < 8; l++)
+                for (int h = 0; h < 2; h++)
+                    for (int o = 0; o < 2; o++)
+                        for (int sl = 0; sl < 8; sl++)
+                            A[mb * 256 + (((l * 2 + h) * 2 + o) * 8) + sl] = qs[q8k_slot_elem<Q6>(l, h, o, sl)];
+        }
+    for (int n = 0; n < N; n++)
+        for (int m = 0; m < M; m++) {
+            float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sumf = 0.0f;
+            for (int b = 0; b < nblk; b++) {
+                const uint8_t *blk = W + (size_t)n * row_bytes + (size_t)b * RB;
+                const size_t mb = (size_t)m * nblk + b;
+                const int8_t *a = &A[mb * 256];
+                long long sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for (int h = 0; h < 2; h++)
+                    for (int o = 0; o < 2; o++) {
+                        int Bv[8][8];  // [l][slot]
+                        if (!Q6) {
+                            const int c = 2 * h + o;
+                            uint32_t w[8];
+                            for (int i = 0; i < 8; i++) w[i] = dw_at(blk + 16 + 32 * c + 4 * i);
+                            const uint32_t S0 = dw_at(blk + 4), S2 = dw_at(blk + 12);
+                            const int sa = (int)q4k_sc(S0, S2, 2 * c), sb = (int)q4k_sc(S0, S2, 2 * c + 1);
+                            for (int lg = 0; lg < 2; lg++) {
+                                uint32_t T[4];
+                                q8k_gather(w, lg, T);
+                                for (int li = 0; li < 4; li++) {
+                                    uint32_t pr[4];
+                                    q4k_pairs(T[li], pr);
+                                    for (int k = 0; k < 4; k++)
+                                        for (int half = 0; half < 2; half++) {
+                                            const float v = f16_lo(pr[k] >> (16 * half));  // 1024 + n, 1024 + 16 n
+                                            const float bv = k < 2 ? v * (float)sa - 1024.0f * (float)sa
+                                                                   : v * ((float)sb / 16.0f) - 64.0f * (float)sb;
+                                            Bv[4 * lg + li][2 * k + half] = (int)bv;
+                                        }
+                                }
+                            }
+                        } else {
+                            uint32_t wl[8], wh[8];
+                            for (int i = 0; i < 8; i++) {
+                                wl[i] = dw_at(blk + 64 * h + 32 * o + 4 * i);
+                                wh[i] = dw_at(blk + 128 + 32 * h + 4 * i);
+                            }
+                            const int8_t *sc = (const int8_t *)(blk + 192);
+                            for (int lg = 0; lg < 2; lg++) {
+                                uint32_t QL[4], QH[4];
+                                q8k_gather(wl, lg, QL);
+                                q8k_gather(wh, lg, QH);
+                                for (int li = 0; li < 4; li++) {
+                                    uint32_t ra, rb, pr[4];
+                                    q6k_raw(QL[li], QH[li], o, ra, rb);
+                                    q6k_pairs(ra, pr);
+                                    q6k_pairs(rb, pr + 2);
+                                    for (int k = 0; k < 4; k++)
+                                        for (int half = 0; half < 2; half++) {
+                                            // slots (0,1), (2,3): elements i = (0,2), (1,3) of the low
+                                            // nibbles, scales 8h + 2o + half; (4,5), (6,7): high, + 4
+                                            const int sci = 8 * h + 2 * o + half + (k >= 2 ? 4 : 0);
+                                            const int qv = (int)(f16_lo(pr[k] >> (16 * half)) - 1056.0f);
+                                            Bv[4 * lg + li][2 * k + half] = (int)sc[sci] * qv;
+                                        }
+                                }
+                            }
+                        }
+                        for (int l = 0; l < 8; l++)
+                            for (int sl = 0; sl < 8; sl++)
+                                sumi[l] += (long long)a[((l * 2 + h) * 2 + o) * 8 + sl] * Bv[l][sl];
+                    }
+                const float dw = f16_lo(blk[Q6 ? 208 : 0] | (uint32_t)blk[Q6 ? 209 : 1] << 8);
+                const float d = d8[mb] * dw;
+                for (int k = 0; k < 8; k++) sums[k] += d * (float)sumi[k];
+                if (!Q6) {
+                    const uint32_t S1 = dw_at(blk + 8), S2 = dw_at(blk + 12);
+                    int minsum = 0;
+                    for (int g = 0; g < 16; g++) minsum += bsum[mb * 16 + g] * (int)q4k_m(S1, S2, g / 2);
+                    const float dmin = f16_lo(blk[2] | (uint32_t)blk[3] << 8) * d8[mb];
+                    sumf -= dmin * (float)minsum;
+                }
+            }
+            float s = sumf;
+            for (int k = 0; k < 8; k++) s += sums[k];
+            Y[(size_t)m * N + n] = s;
+        }
+}
+
 // Weights copied into a padded, 256-byte aligned buffer as on the device.
 struct Padded {
     uint8_t *p = nullptr;
@@ -284,6 +396,20 @@ int uq_emu_gemv_q8k(float *y, const float *x, const uint8_t *w, size_t dim_in, s
         return 0;
     }
     return -1;
+}
+
+// uq_gemm_q8k's arithmetic: Y[m] = gemv_quant_q8k(W, X[m]) for m < M.
+int uq_emu_gemm_q8k(float *y, const float *x, size_t m_rows, const uint8_t *w, size_t dim_in, size_t dim_out,
+                    int dtype) {
+    const int K = (int)dim_in, N = (int)dim_out, M = (int)m_rows;
+    if (K % 256 || (dtype != 12 && dtype != 14)) return -1;
+    const size_t rb = dtype == 12 ? (size_t)K / 256 * 144 : (size_t)K / 256 * 210;
+    const Padded W(w, rb * dim_out);
+    if (dtype == 12)
+        emu_gemm_q8k<false>(y, x, M, W.p, rb, K, N);
+    else
+        emu_gemm_q8k<true>(y, x, M, W.p, rb, K, N);
+    return 0;
 }
 
 }  // extern "C"

@@ -52,15 +52,12 @@
 #include <vector>
 
 #include "uq_internal.h"
+#include "uq_mfma.h"
 #include "uq_policies.h"
 
 namespace uq {
 
 namespace {
-
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f16x __attribute__((ext_vector_type(16)));
 
 constexpr int GTPB = 512;  // eight waves, two per SIMD
 
@@ -166,64 +163,6 @@ __global__ __launch_bounds__(256) void gemm_convert_kernel(const float *__restri
         dst[8 + gi] = (_Float16)(float)(gs - (double)gh);
     }
 }
-
-// ------------------------------------------------------------ device helpers
-__device__ __forceinline__ f16x mfma(h8 a, h8 b, f16x c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// v_bfi_b32: (x & mask) | (y & ~mask), constants in VGPRs (a VOP3 takes no
-// literal here)
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
-    uint32_t r;
-    __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(x), "v"(y));
-    return r;
-}
-__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
-__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ __forceinline__ h2 hh(float v) {
-    const _Float16 f = (_Float16)v;
-    return h2{f, f};
-}
-
-// Wait until at most N of this wave's vector-memory operations are
-// outstanding (they retire in issue order) and its LDS operations are done,
-// then meet the workgroup. One asm block, so the compiler adds no full wait.
-template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-    static_assert(N >= 0 && N <= 63, "vmcnt immediate");
-    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// No memory operation moves across this point (the vmcnt counts above rely
-// on the issue order of the loads around it).
-__device__ __forceinline__ void fence() { __asm__ volatile("" ::: "memory"); }
-
-// Raw buffer resource over nbytes at p (gfx9 descriptor word 3: 0x00020000)
-// and a 16-byte load at voffset (per lane) + soffset (wave-uniform).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)nbytes, 0x00020000);
-}
-__device__ __forceinline__ h8 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    typedef int i4 __attribute__((ext_vector_type(4)));
-    const i4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    return __builtin_bit_cast(h8, v);
-}
-
-// One 16-byte direct-to-LDS load per lane: lane i writes dst + 16 i (dst
-// wave-uniform, through M0). Written as asm so that the compiler does not
-// treat every later LDS read as waiting on it (it cannot tell the ring
-// slots apart and would wait for all outstanding loads); the kernel orders
-// these loads with its own vmcnt counts and barriers instead.
-// Nothing else in these kernels uses M0 (checked in the generated code), so
-// clobbering it here is safe.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void *g, uint8_t *dst) {
-    const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
-    __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // B operand slot of (k-step t, B tile b, column col, lane half h) in one
 // sub-step's B ring slot: fragment (b, t, col/32) is 1 KB, lane = col%32 + 32h.
@@ -1216,34 +1155,38 @@ hipError_t launch_gemm_static(const WeightsView &w, int M, const float *X, float
     return launch_gemm_ws(w, M, X, Y, p, UQ_GEMM_SCRATCH_BYTES, s);
 }
 
-// uq_gemm's workspace: one buffer per (device, stream), grown on demand.
+// The GEMMs' workspace: one buffer per (device, stream), grown on demand.
 // A grown-out buffer is never freed (a graph captured earlier, or work
 // still queued on the stream, may refer to it); growth at least doubles,
 // so what is kept stays below twice the largest need.
-hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
-    const size_t need = gemm_ws_bytes(w, M);
-    if (need == 0) return launch_gemm_ws(w, M, X, Y, nullptr, 0, s);
+hipError_t gemm_workspace(size_t need, hipStream_t s, uint8_t **buf, size_t *have) {
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, std::pair<uint8_t *, size_t>> cache;
     static std::vector<void *> retired;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    uint8_t *buf;
-    size_t have;
-    {
-        std::lock_guard<std::mutex> g(mu);
-        auto &slot = cache[{dev, s}];
-        if (slot.second < need) {
-            const size_t sz = std::max(need, 2 * slot.second);
-            void *p = nullptr;
-            if ((e = hipMalloc(&p, sz)) != hipSuccess) return e;
-            if (slot.first) retired.push_back(slot.first);
-            slot = {(uint8_t *)p, sz};
-        }
-        buf = slot.first;
-        have = slot.second;
+    std::lock_guard<std::mutex> g(mu);
+    auto &slot = cache[{dev, s}];
+    if (slot.second < need) {
+        const size_t sz = std::max(need, 2 * slot.second);
+        void *p = nullptr;
+        if ((e = hipMalloc(&p, sz)) != hipSuccess) return e;
+        if (slot.first) retired.push_back(slot.first);
+        slot = {(uint8_t *)p, sz};
     }
+    *buf = slot.first;
+    *have = slot.second;
+    return hipSuccess;
+}
+
+hipError_t launch_gemm(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s) {
+    const size_t need = gemm_ws_bytes(w, M);
+    if (need == 0) return launch_gemm_ws(w, M, X, Y, nullptr, 0, s);
+    uint8_t *buf = nullptr;
+    size_t have = 0;
+    const hipError_t e = gemm_workspace(need, s, &buf, &have);
+    if (e != hipSuccess) return e;
     return launch_gemm_ws(w, M, X, Y, buf, have, s);
 }
 

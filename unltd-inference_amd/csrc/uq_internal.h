@@ -186,5 +186,15 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
 // The same on the library's fixed device workspace (UQ_GEMM_SCRATCH_BYTES
 // per GPU); the caller checks gemm_ws_bytes(w, M) <= UQ_GEMM_SCRATCH_BYTES.
 hipError_t launch_gemm_static(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s);
+// The library-owned workspace of the GEMMs on stream s: at least need
+// bytes, one buffer per (device, stream), grown on demand and never freed.
+hipError_t gemm_workspace(size_t need, hipStream_t s, uint8_t **buf, size_t *have);
+// Y[m] = gemv_quant_q8k(W, X[m]) for m < M, bit-exact (Q4_K / Q6_K, K a
+// multiple of 256), on the library-owned workspace; _ws: on a caller
+// workspace of wsb >= gemm_q8k_ws_bytes(w, M) bytes.
+hipError_t launch_gemm_q8k(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s);
+size_t gemm_q8k_ws_bytes(const WeightsView &w, int M);
+hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
+                              hipStream_t s);
 
 }  // namespace uq

@@ -74,6 +74,7 @@ SIGNATURES = {
     "uq_gemv_q8k": ([_P, _P, _P, _P], _I),
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
     "uq_gemm_static": ([_P, _S, _P, _P, _P], _I),
+    "uq_gemm_q8k": ([_P, _S, _P, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
     "uq_dequantize": ([_P, _P, _P], _I),
     "uq_embed": ([_P, _P, _S, _P, _P], _I),
@@ -376,6 +377,11 @@ def gemm(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) ->
     _check(lib().uq_gemm(w.h, m, d_x.ptr, d_y.ptr, stream))
 
 
+def gemm_q8k(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
+    """d_y[r] = gemv_quant_q8k(w, d_x[r]) for r < m, bit-exact (uq_gemm_q8k)."""
+    _check(lib().uq_gemm_q8k(w.h, m, d_x.ptr, d_y.ptr, stream))
+
+
 def gemm_static(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
     """uq_gemm on the library's fixed workspace (allocates nothing)."""
     _check(lib().uq_gemm_static(w.h, m, d_x.ptr, d_y.ptr, stream))
@@ -428,6 +434,8 @@ def emu():
         for n in ("uq_emu_gemv", "uq_emu_gemv_q8k"):
             getattr(E, n).argtypes = [_P, _P, _P, _S, _S, _I]
             getattr(E, n).restype = _I
+        E.uq_emu_gemm_q8k.argtypes = [_P, _P, _S, _P, _S, _S, _I]
+        E.uq_emu_gemm_q8k.restype = _I
         _emu = E
     return _emu
 
@@ -440,3 +448,15 @@ def emu_gemv(x, w, dim_in: int, dim_out: int, dtype: int, q8k: bool = False) -> 
     if rc != 0:
         raise ValueError(f"shape not taken by the fast kernels: dtype {dtype}, K {dim_in}")
     return y
+
+
+def emu_gemm_q8k(X, w, dim_in: int, dim_out: int, dtype: int) -> np.ndarray:
+    """uq_gemm_q8k's operand maps and epilogue run on the CPU: Y[m] =
+    gemv_quant_q8k(W, X[m])."""
+    X, w = _f32(X), _u8(w)
+    M = X.size // dim_in
+    Y = np.zeros(M * dim_out, np.float32)
+    rc = emu().uq_emu_gemm_q8k(_ptr(Y), _ptr(X), M, _ptr(w), dim_in, dim_out, int(dtype))
+    if rc != 0:
+        raise ValueError(f"uq_gemm_q8k takes Q4_K / Q6_K with K a multiple of 256: dtype {dtype}, K {dim_in}")
+    return Y.reshape(M, dim_out)
