@@ -21,15 +21,17 @@
 // fragment order, plus per (block, row) the f32 d and the f16 bsums.
 // Rows are padded to a multiple of 32 with zero blocks.
 //
-// Main kernel: a workgroup of NW waves owns 32 rows x 32 NW columns, one
-// 32 x 32 output tile per wave, and walks the blocks in order (the f32
-// epilogue is sequential over blocks, so K is never split). Per block, the
-// activation octets of its 32 rows (16 KB), the raw weight blocks of its
-// columns and the rows' d / bsums stream into a two-slot LDS ring with
-// direct-to-LDS loads, issued one block ahead; one barrier per block. Each
-// wave decodes its own 32 columns' weights into B operands in registers:
-// a lane holds column lane % 32 and octet lane / 32 of every operand.
+// Main kernel: a workgroup owns 32 rows x 32 NC columns, two waves per
+// 32 x 32 output tile, and walks the blocks in order (the f32 epilogue is
+// sequential over blocks, so K is never split). Per block, the activation
+// octets of its 32 rows (16 KB), the raw weight blocks of its columns and
+// the rows' d / bsums stream into a two-slot LDS ring with direct-to-LDS
+// loads, issued one block ahead; one barrier per block. Each wave decodes
+// its own column tile's weights for its four lane sums into B operands in
+// registers: a lane holds column lane % 32 and octet lane / 32 of every
+// operand.
 #include <algorithm>
+#include <type_traits>
 
 #include "uq_internal.h"
 #include "uq_mfma.h"
@@ -149,9 +151,10 @@ struct Q8Fmt {
     static constexpr int CPR = Q6 ? 14 : 9;    // 16-byte chunks per column and block in LDS
 };
 
-template <bool Q6, int NW>
+// A workgroup: NC column tiles of 32, two waves per tile (2 NC waves).
+template <bool Q6, int NC>
 struct Q8Lay {
-    static constexpr int TN = 32 * NW;
+    static constexpr int NW = 2 * NC, TN = 32 * NC;
     static constexpr int A = 0, ASZ = 16 * 1024;                       // 16 fragments of 64 lanes x 16 bytes
     static constexpr int B = ASZ, BSZ = TN * Q8Fmt<Q6>::CPR * 16;      // raw blocks, column-major
     static constexpr int BS = B + BSZ, D8 = BS + 32 * 32;              // bsums [32 rows][32 B], d8 [32 rows]
@@ -159,20 +162,39 @@ struct Q8Lay {
     static constexpr int BYTES = 2 * SLOT;
     static constexpr int BROUNDS = (TN * Q8Fmt<Q6>::CPR + 64 * NW - 1) / (64 * NW);
     static_assert(BYTES <= 160 * 1024, "LDS");
+    static_assert(NC * 2 * 64 * 16 * 4 <= BYTES, "the end-of-tile exchange fits the ring");
 };
 
 __device__ __forceinline__ h2 h2_of(float a, float b) { return h2{(_Float16)a, (_Float16)b}; }
 
-template <bool Q6, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q8k_kernel(
+// Scale of Q4_K group 2c + hi (hi = 0, 1) of qs chunk c = 2h + cc, h known
+// at compile time (scale_min_k4, quants.rs:92-102).
+template <int H>
+__device__ __forceinline__ float q4k_chunk_sc(uint32_t S0, uint32_t S2, int cc, int hi) {
+    const int g4 = 2 * cc + hi;  // group - 4 H
+    if constexpr (H == 0) return (float)((S0 >> (8 * g4)) & 63);
+    return (float)(((S2 >> (8 * g4)) & 0xF) | (((S0 >> (8 * g4 + 6)) & 3) << 4));
+}
+
+// Wave (c, half) of a workgroup owns the 32 x 32 output tile of column tile
+// c and the lane sums l = 4 half .. 4 half + 3 of it (the reference's
+// sums[l] accumulators), so a wave holds 64 accumulator registers and
+// dequantizes only the weights of its four lanes. Per lane: the two MFMAs
+// of the next lane are issued before this lane's epilogue. The block's
+// d = q8.d * f16(d) products are formed by both waves; the Q4_K min term by
+// half 0 for rows r < 8 of the lane's 16 and by half 1 for the rest. At the
+// end half 1 hands its sumf to half 0, half 0 forms sumf + sums[0..3] and
+// hands it back, and half 1 adds sums[4..7] in order and stores.
+template <bool Q6, int NC>
+__global__ __launch_bounds__(128 * NC) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q8k_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, Q8Ws ws, int ntm, int ntn,
     float *__restrict__ Y) {
     using F = Q8Fmt<Q6>;
-    using Lay = Q8Lay<Q6, NW>;
-    constexpr int TN = Lay::TN, CPR = F::CPR;
+    using Lay = Q8Lay<Q6, NC>;
+    constexpr int NW = Lay::NW, TN = Lay::TN, CPR = F::CPR;
     extern __shared__ __align__(16) uint8_t lds[];
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
-    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), ct = wv >> 1, half = wv & 1;
 
     // tiles (M fastest) dealt to the 8 XCDs in contiguous runs
     const int T = ntm * ntn, per = (T + 7) / 8;
@@ -206,75 +228,70 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
     };
 
-    float sums[8][16];
-    float sumf[16];
+    // the wave's half of the lane sums is a compile-time constant of the
+    // loop below (its gathers and accumulators are indexed by it)
+    auto run = [&](auto half_c) {
+        constexpr int HALF = decltype(half_c)::value;
+        float sums[4][16];
+        float sumf[8];  // rows 8 half .. 8 half + 7 of the lane's 16 (Q4_K)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        sumf[r] = 0.0f;
+        for (int r = 0; r < 16; r++)
 #pragma unroll
-        for (int k = 0; k < 8; k++) sums[k][r] = 0.0f;
-    }
-    const f16x zero = {};
+            for (int k = 0; k < 4; k++) sums[k][r] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 8; r++) sumf[r] = 0.0f;
+        const f16x zero = {};
 
-    issue(0);
-    wait_vm_barrier<0>();
-    for (int b = 0; b < nblk; b++) {
-        if (b + 1 < nblk) issue(b + 1);
-        fence();
-        const uint8_t *sl = lds + (b & 1) * Lay::SLOT;
-        const uint8_t *rc = sl + Lay::B + (32 * wv + lr) * (CPR * 16);  // this lane's column
-        // the lane's rows 8 (r / 4) + 4 lh + r % 4: their q8.d
-        float d8v[16];
+        issue(0);
+        wait_vm_barrier<0>();
+        for (int b = 0; b < nblk; b++) {
+            if (b + 1 < nblk) issue(b + 1);
+            fence();
+            const uint8_t *sl = lds + (b & 1) * Lay::SLOT;
+            const uint8_t *rc = sl + Lay::B + (32 * ct + lr) * (CPR * 16);  // this lane's column
+            const uint8_t *ab = sl + Lay::A + 16 * lane;
+            // the lane's rows 8 (r / 4) + 4 lh + r % 4: their q8.d
+            float d8v[16];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 v = *(const float4 *)(sl + Lay::D8 + (8 * q + 4 * lh) * 4);
-            d8v[4 * q] = v.x, d8v[4 * q + 1] = v.y, d8v[4 * q + 2] = v.z, d8v[4 * q + 3] = v.w;
-        }
-        float dd[16];
-        if constexpr (!Q6) {
-            const u4 hd = *(const u4 *)rc;
-            const float dw = f16_lo(hd.x), dmw = f16_hi(hd.x);
-            const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
-            // min sum on the MFMA: bsums g = 8 lh .. 8 lh + 7 of the lane's row times m[g / 2]
-            const h8 bsA = *(const h8 *)(sl + Lay::BS + lr * 32 + 16 * lh);
-            h8 mB;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const _Float16 mv = (_Float16)(float)q4k_m(S1, S2, 4 * lh + k);
-                mB[2 * k] = mv;
-                mB[2 * k + 1] = mv;
+            for (int q = 0; q < 4; q++) {
+                const float4 v = *(const float4 *)(sl + Lay::D8 + (8 * q + 4 * lh) * 4);
+                d8v[4 * q] = v.x, d8v[4 * q + 1] = v.y, d8v[4 * q + 2] = v.z, d8v[4 * q + 3] = v.w;
             }
-            const f16x mt = mfma(bsA, mB, zero);
-            // chunk c = 2 h + lh of qs, and its groups' scale constants
-            uint32_t w[2][8];
-            h2 lsc[2], loff[2], hsc[2], hoff[2];
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int c = 2 * h + lh;
-                const u4 a = *(const u4 *)(rc + 16 + 32 * c), bq = *(const u4 *)(rc + 32 + 32 * c);
-                w[h][0] = a.x, w[h][1] = a.y, w[h][2] = a.z, w[h][3] = a.w;
-                w[h][4] = bq.x, w[h][5] = bq.y, w[h][6] = bq.z, w[h][7] = bq.w;
-                const float sa = (float)q4k_sc(S0, S2, 2 * c), sb = (float)q4k_sc(S0, S2, 2 * c + 1);
-                lsc[h] = h2_of(sa, sa);
-                loff[h] = h2_of(-1024.0f * sa, -1024.0f * sa);
-                hsc[h] = h2_of(sb * 0.0625f, sb * 0.0625f);
-                hoff[h] = h2_of(-64.0f * sb, -64.0f * sb);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                dd[r] = __fmul_rn(d8v[r], dw);
-                sumf[r] = __fsub_rn(sumf[r], __fmul_rn(__fmul_rn(dmw, d8v[r]), mt[r]));
-            }
-#pragma unroll
-            for (int lg = 0; lg < 2; lg++) {
+            float dd[16];
+            f16x S[2];
+            if constexpr (!Q6) {
+                const u4 hd = *(const u4 *)rc;
+                const float dw = f16_lo(hd.x), dmw = f16_hi(hd.x);
+                const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
+                // qs chunks c = 2 h + lh: the dwords HALF + 2i (bytes 8i + l of
+                // the wave's lanes l), and the chunk's groups' scale constants
                 uint32_t T0[4], T1[4];
-                q8k_gather(w[0], lg, T0);
-                q8k_gather(w[1], lg, T1);
+                h2 lsc[2], loff[2], hsc[2], hoff[2];
 #pragma unroll
-                for (int li = 0; li < 4; li++) {
-                    const int l = 4 * lg + li;
-                    const h8 A0 = *(const h8 *)(sl + Lay::A + (2 * l) * 1024 + 16 * lane);
-                    const h8 A1 = *(const h8 *)(sl + Lay::A + (2 * l + 1) * 1024 + 16 * lane);
+                for (int h = 0; h < 2; h++) {
+                    const int c = 2 * h + lh;
+                    const uint32_t *q = (const uint32_t *)(rc + 16 + 32 * c) + HALF;
+                    transpose4(q[0], q[2], q[4], q[6], h ? T1 : T0);
+                    const float sa = h ? q4k_chunk_sc<1>(S0, S2, lh, 0) : q4k_chunk_sc<0>(S0, S2, lh, 0);
+                    const float sb = h ? q4k_chunk_sc<1>(S0, S2, lh, 1) : q4k_chunk_sc<0>(S0, S2, lh, 1);
+                    lsc[h] = h2_of(sa, sa);
+                    loff[h] = h2_of(-1024.0f * sa, -1024.0f * sa);
+                    hsc[h] = h2_of(sb * 0.0625f, sb * 0.0625f);
+                    hoff[h] = h2_of(-64.0f * sb, -64.0f * sb);
+                }
+                // min sum on the MFMA: bsums g = 8 lh .. 8 lh + 7 of the lane's row times m[g / 2]
+                const h8 bsA = *(const h8 *)(sl + Lay::BS + lr * 32 + 16 * lh);
+                h8 mB;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const _Float16 mv = (_Float16)(float)q4k_m(S1, S2, 4 * lh + k);
+                    mB[2 * k] = mv;
+                    mB[2 * k + 1] = mv;
+                }
+                const f16x mt = mfma(bsA, mB, zero);
+                auto lane_mfma = [&](int li, f16x &acc) {
+                    const int l = 4 * HALF + li;
+                    const h8 A0 = *(const h8 *)(ab + (2 * l) * 1024), A1 = *(const h8 *)(ab + (2 * l + 1) * 1024);
                     uint32_t p0[4], p1[4];
                     q4k_pairs(T0[li], p0);
                     q4k_pairs(T1[li], p1);
@@ -288,55 +305,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                         B0[2 * k] = u0.x, B0[2 * k + 1] = u0.y, B0[4 + 2 * k] = u1.x, B0[4 + 2 * k + 1] = u1.y;
                         B1[2 * k] = v0.x, B1[2 * k + 1] = v0.y, B1[4 + 2 * k] = v1.x, B1[4 + 2 * k + 1] = v1.y;
                     }
-                    f16x S = mfma(A0, B0, zero);
-                    S = mfma(A1, B1, S);
+                    acc = mfma(A0, B0, zero);
+                    acc = mfma(A1, B1, acc);
+                };
+                lane_mfma(0, S[0]);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) sums[l][r] = __fadd_rn(sums[l][r], __fmul_rn(dd[r], S[r]));
-                }
-            }
-        } else {
-            const float dw = f16_lo(*(const uint16_t *)(rc + 208));
-            // ql run 64 h + 32 lh and qh run 32 h (both 32 bytes) of each half h,
-            // and the pair scales: low-nibble slots sc[8h + 2lh + (0, 1)], high +4,
-            // split into (sc & ~1) and (sc & 1)
-            uint32_t wl[2][8], wq[2][8];
-            h2 se[2][2], so[2][2];  // [h][low / high]
+                for (int r = 0; r < 16; r++) dd[r] = __fmul_rn(d8v[r], dw);
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const u4 a = *(const u4 *)(rc + 64 * h + 32 * lh), bq = *(const u4 *)(rc + 64 * h + 32 * lh + 16);
-                const u4 c = *(const u4 *)(rc + 128 + 32 * h), e = *(const u4 *)(rc + 128 + 32 * h + 16);
-                wl[h][0] = a.x, wl[h][1] = a.y, wl[h][2] = a.z, wl[h][3] = a.w;
-                wl[h][4] = bq.x, wl[h][5] = bq.y, wl[h][6] = bq.z, wl[h][7] = bq.w;
-                wq[h][0] = c.x, wq[h][1] = c.y, wq[h][2] = c.z, wq[h][3] = c.w;
-                wq[h][4] = e.x, wq[h][5] = e.y, wq[h][6] = e.z, wq[h][7] = e.w;
-                const uint2 scw = *(const uint2 *)(rc + 192 + 8 * h);
-                const uint32_t lo = scw.x >> (16 * lh), hi = scw.y >> (16 * lh);
-#pragma unroll
-                for (int part = 0; part < 2; part++) {
-                    const uint32_t v = part ? hi : lo;
-                    const int s0 = (int)(int8_t)(v & 0xFF), s1 = (int)(int8_t)((v >> 8) & 0xFF);
-                    se[h][part] = h2_of((float)(s0 & ~1), (float)(s1 & ~1));
-                    so[h][part] = h2_of((float)(s0 & 1), (float)(s1 & 1));
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) dd[r] = __fmul_rn(d8v[r], dw);
-            const h2 off = h2_of(-1056.0f, -1056.0f);
-#pragma unroll
-            for (int lg = 0; lg < 2; lg++) {
-                uint32_t QL[2][4], QH[2][4];
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    q8k_gather(wl[h], lg, QL[h]);
-                    q8k_gather(wq[h], lg, QH[h]);
+                for (int r = 0; r < 8; r++) {
+                    const int rr = 8 * HALF + r;
+                    sumf[r] = __fsub_rn(sumf[r], __fmul_rn(__fmul_rn(dmw, d8v[rr]), mt[rr]));
                 }
 #pragma unroll
                 for (int li = 0; li < 4; li++) {
-                    const int l = 4 * lg + li;
-                    f16x S = zero;
+                    if (li < 3) lane_mfma(li + 1, S[(li + 1) & 1]);
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        sums[li][r] = __fadd_rn(sums[li][r], __fmul_rn(dd[r], S[li & 1][r]));
+                }
+            } else {
+                const float dw = f16_lo(*(const uint16_t *)(rc + 208));
+                // ql run 64 h + 32 lh and qh run 32 h (both 32 bytes) of each half h,
+                // and the pair scales: low-nibble slots sc[8h + 2lh + (0, 1)], high +4,
+                // split into (sc & ~1) and (sc & 1)
+                uint32_t QL[2][4], QH[2][4];
+                h2 se[2][2], so[2][2];  // [h][low / high]
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t *ql = (const uint32_t *)(rc + 64 * h + 32 * lh) + HALF;
+                    const uint32_t *qh = (const uint32_t *)(rc + 128 + 32 * h) + HALF;
+                    transpose4(ql[0], ql[2], ql[4], ql[6], QL[h]);
+                    transpose4(qh[0], qh[2], qh[4], qh[6], QH[h]);
+                    const uint2 scw = *(const uint2 *)(rc + 192 + 8 * h);
+                    const uint32_t lo = scw.x >> (16 * lh), hi = scw.y >> (16 * lh);
+#pragma unroll
+                    for (int part = 0; part < 2; part++) {
+                        const uint32_t v = part ? hi : lo;
+                        const int s0 = (int)(int8_t)(v & 0xFF), s1 = (int)(int8_t)((v >> 8) & 0xFF);
+                        se[h][part] = h2_of((float)(s0 & ~1), (float)(s1 & ~1));
+                        so[h][part] = h2_of((float)(s0 & 1), (float)(s1 & 1));
+                    }
+                }
+                const h2 off = h2_of(-1056.0f, -1056.0f);
+                auto lane_mfma = [&](int li, f16x &acc) {
+                    const int l = 4 * HALF + li;
+                    acc = zero;
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
-                        const h8 A = *(const h8 *)(sl + Lay::A + (2 * l + h) * 1024 + 16 * lane);
+                        const h8 A = *(const h8 *)(ab + (2 * l + h) * 1024);
                         uint32_t ra, rb, p[4];
                         q6k_raw(QL[h][li], QH[h][li], lh, ra, rb);
                         q6k_pairs(ra, p);
@@ -349,54 +365,86 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                             B1[2 * k] = e1.x, B1[2 * k + 1] = e1.y;
                             B2[2 * k] = e2.x, B2[2 * k + 1] = e2.y;
                         }
-                        S = mfma(A, B1, S);
-                        S = mfma(A, B2, S);
+                        acc = mfma(A, B1, acc);
+                        acc = mfma(A, B2, acc);
                     }
+                };
+                lane_mfma(0, S[0]);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) sums[l][r] = __fadd_rn(sums[l][r], __fmul_rn(dd[r], S[r]));
+                for (int r = 0; r < 16; r++) dd[r] = __fmul_rn(d8v[r], dw);
+#pragma unroll
+                for (int li = 0; li < 4; li++) {
+                    if (li < 3) lane_mfma(li + 1, S[(li + 1) & 1]);
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        sums[li][r] = __fadd_rn(sums[li][r], __fmul_rn(dd[r], S[li & 1][r]));
                 }
             }
+            // this wave's own loads of block b + 1 landed, then every wave's; the
+            // slot of block b is free for block b + 2
+            wait_vm_barrier<0>();
         }
-        // this wave's own loads of block b + 1 landed, then every wave's; the
-        // slot of block b is free for block b + 2
-        wait_vm_barrier<0>();
-    }
 
-    // s = sumf + sums[0] + ... + sums[7] (Q6_K: sumf is 0), column n0 + 32 wv + lr
-    const int n = n0 + 32 * wv + lr;
+        // s = sumf + sums[0] + ... + sums[7] (Q6_K: sumf is 0), in that order,
+        // exchanged through the (now idle) ring: X[c][w][r][lane], w = 0 the
+        // sumf rows of half 1, w = 1 the partial sum of half 0
+        float *X = (float *)lds;
+        auto xat = [&](int w, int r) { return X + (((ct * 2 + w) * 16 + r) * 64 + lane); };
+        if constexpr (HALF == 1)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        float s = sumf[r];
+            for (int r = 0; r < 8; r++) *xat(0, 8 + r) = sumf[r];
+        lds_barrier();
+        if constexpr (HALF == 0) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) s = __fadd_rn(s, sums[k][r]);
-        const int m = m0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (m < M && n < N) Y[(size_t)m * N + n] = s;
-    }
+            for (int r = 0; r < 16; r++) {
+                float s = r < 8 ? sumf[r] : *xat(0, r);
+#pragma unroll
+                for (int k = 0; k < 4; k++) s = __fadd_rn(s, sums[k][r]);
+                *xat(1, r) = s;
+            }
+        }
+        lds_barrier();
+        if constexpr (HALF == 1) {
+            const int n = n0 + 32 * ct + lr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float s = *xat(1, r);
+#pragma unroll
+                for (int k = 0; k < 4; k++) s = __fadd_rn(s, sums[k][r]);
+                const int m = m0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m < M && n < N) Y[(size_t)m * N + n] = s;
+            }
+        }
+
+    };
+    if (half)
+        run(std::integral_constant<int, 1>{});
+    else
+        run(std::integral_constant<int, 0>{});
 }
 
-template <bool Q6, int NW>
+template <bool Q6, int NC>
 hipError_t q8k_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
-    const int ntm = ws.Mp / 32, ntn = (N + 32 * NW - 1) / (32 * NW);
+    const int ntm = ws.Mp / 32, ntn = (N + 32 * NC - 1) / (32 * NC);
     const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
-    const void *k = (const void *)gemm_q8k_kernel<Q6, NW>;
-    constexpr int lds = Q8Lay<Q6, NW>::BYTES;
+    const void *k = (const void *)gemm_q8k_kernel<Q6, NC>;
+    constexpr int lds = Q8Lay<Q6, NC>::BYTES;
     hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemm_q8k_kernel<Q6, NW>), dim3(grid), dim3(64 * NW), lds, s, w.bytes, (uint32_t)w.row_bytes, K,
-                       N, M, ws, ntm, ntn, Y);
+    hipLaunchKernelGGL((gemm_q8k_kernel<Q6, NC>), dim3(grid), dim3(128 * NC), lds, s, w.bytes, (uint32_t)w.row_bytes,
+                       K, N, M, ws, ntm, ntn, Y);
     return hipGetLastError();
 }
 
-// Waves per workgroup: the widest tile (eight 32-column waves) whose tiles
-// still number at least one per CU.
+// Column tiles per workgroup: four (eight waves) where the workgroups still
+// number at least one per CU, else fewer.
 template <bool Q6>
 hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int ntm = ws.Mp / 32, N = w.dim_out, cus = 256;
-    auto tiles = [&](int nw) { return ntm * ((N + 32 * nw - 1) / (32 * nw)); };
-    if (tiles(8) >= cus) return q8k_launch<Q6, 8>(w, M, ws, Y, s);
-    if (tiles(4) >= cus) return q8k_launch<Q6, 4>(w, M, ws, Y, s);
-    if (tiles(2) >= cus) return q8k_launch<Q6, 2>(w, M, ws, Y, s);
+    auto groups = [&](int nc) { return ntm * ((N + 32 * nc - 1) / (32 * nc)); };
+    if (groups(4) >= cus) return q8k_launch<Q6, 4>(w, M, ws, Y, s);
+    if (groups(2) >= cus) return q8k_launch<Q6, 2>(w, M, ws, Y, s);
     return q8k_launch<Q6, 1>(w, M, ws, Y, s);
 }
 

@@ -58,20 +58,11 @@ UQ_HD uint32_t bfi32(uint32_t mask, uint32_t x, uint32_t y) {
 #endif
 }
 
-// 4x4 byte transpose: t[j] = {a.j, b.j, c.j, d.j} (byte j of each row).
-UQ_HD void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t t[4]) {
-    const uint32_t ab_lo = perm(b, a, 0x05010400u), ab_hi = perm(b, a, 0x07030602u);
-    const uint32_t cd_lo = perm(d, c, 0x05010400u), cd_hi = perm(d, c, 0x07030602u);
-    t[0] = perm(cd_lo, ab_lo, 0x05040100u);
-    t[1] = perm(cd_lo, ab_lo, 0x07060302u);
-    t[2] = perm(cd_hi, ab_hi, 0x05040100u);
-    t[3] = perm(cd_hi, ab_hi, 0x07060302u);
-}
-
 // The four dwords of byte lane l (0..7) of a 32-byte run w[0..7] of raw
 // bytes at stride 8: run bytes l, 8 + l, 16 + l, 24 + l are the transposes
-// of w[l/4 + 2i], i = 0..3 (t[l % 4] of q8k_gather).
-UQ_HD void q8k_gather(const uint32_t w[8], int lg, uint32_t t[4]) {
+// of w[l/4 + 2i], i = 0..3 (t[l % 4] of q8k_gather; transpose4 is the
+// 4x4 byte transpose of uq_bits.h).
+UQ_HD void q8k_gather(const uint32_t w[8], int lg, uint32_t (&t)[4]) {
     transpose4(w[lg], w[lg + 2], w[lg + 4], w[lg + 6], t);
 }
 
