@@ -172,11 +172,14 @@ uq_status uq_gemv_q8k_batch(const uq_weights *w, float *const *d_y, size_t count
  * below 4 GiB, activation planes below 2 GiB) run on the f16 MFMA, one weight
  * pass per 32-128-row tile; the row results are within the gemv_quant
  * tolerance plus 2^-22 * sum_e |x_e w_e| (the matrix cores' f32
- * accumulation). m_rows == 1 and other shapes run as m_rows GEMVs. A NaN or
+ * accumulation within each 256-k block; when K is split across workgroups
+ * the partial tiles stay f64 and are summed in range order, adding no
+ * term). m_rows == 1 and other shapes run as m_rows GEMVs. A NaN or
  * infinity in a row of d_x makes that row of d_y NaN. The MFMA path uses a
  * library-owned device workspace per (device, stream) of about
- * 4*m_rows*dim_in bytes (plus the split-K partial tiles when the output
- * tiles do not cover the CUs), allocated on first use and grown when a call
+ * 4*m_rows*dim_in bytes (plus f64 split-K partial tiles, 8 bytes per output
+ * and K range, when the output tiles do not cover the CUs), allocated on
+ * first use and grown when a call
  * needs more; a grown-out buffer is kept, never freed, so work queued on the
  * stream or a graph captured earlier stays valid. A call can be captured in
  * a HIP graph once a call of that size or larger has run on the stream. */
@@ -205,11 +208,12 @@ uq_status uq_gemm_q8k(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
  * and results as uq_gemm (the same bits); the workspace is a fixed device array
  * of UQ_GEMM_SCRATCH_BYTES inside the library, one per GPU, held until the
  * process ends. A call whose workspace would not fit (roughly
- * 4*m_rows*dim_in bytes, plus the split-K partial tiles for small m_rows)
+ * 4*m_rows*dim_in bytes, plus 8 bytes per output and K range when K is
+ * split)
  * fails with UQ_ERR_ARG and launches nothing. Calls on one GPU share the
  * array: calls that may overlap on a GPU (other streams, other threads)
  * race and must be ordered by the caller. */
-#define UQ_GEMM_SCRATCH_BYTES (32u << 20)
+#define UQ_GEMM_SCRATCH_BYTES (64u << 20)
 uq_status uq_gemm_static(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                          void *stream);
 

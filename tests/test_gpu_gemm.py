@@ -155,6 +155,37 @@ def test_gemm_dynamic_range(dtype):
 
 
 @pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0])
+def test_gemm_split_k_cancellation_bound(dtype):
+    """Small M at K = 12288 on a narrow N, so K is split across 24-48
+    workgroups per column group, with rows built to cancel: row m is a random
+    vector with its projection on weight rows 7m .. 7m + 6 removed, so those
+    outputs are tiny against sum_e |x_e w_e|. The partial tiles stay f64 and
+    are summed in range order, so the split adds nothing to the stated bound
+    1e-4 + 1e-3 |r| + 2^-22 sum_e |x_e w_e|."""
+    K, N, M = 12288, 1000, 8
+    w = S.weights(dtype, N, K, seed=77 + dtype)
+    Wx = exact_weights_f64(dtype, w, N, K)
+    rng = np.random.default_rng(78)
+    X = np.empty((M, K), np.float32)
+    for m in range(M):
+        z = rng.standard_normal(K) * 100.0
+        Q, _ = np.linalg.qr(Wx[7 * m:7 * m + 7].T)
+        X[m] = (z - Q @ (Q.T @ z)).astype(np.float32)
+    Y = run_gemm(dtype, w, K, N, X)
+    R = X.astype(np.float64) @ Wx.T
+    A = np.abs(X.astype(np.float64)) @ np.abs(Wx).T
+    err = np.abs(Y.astype(np.float64) - R)
+    bad = np.argwhere(~(err <= 1e-4 + 1e-3 * np.abs(R) + 2.0 ** -22 * A))
+    assert bad.size == 0, f"{len(bad)} outside the bound, first {bad[:3].tolist()}"
+    planted = np.array([[m, 7 * m + j] for m in range(M) for j in range(7)])
+    ratio = np.abs(R[planted[:, 0], planted[:, 1]]) / A[planted[:, 0], planted[:, 1]]
+    assert np.all(ratio < 1e-6), "the planted outputs cancel"
+    strict = np.argwhere(~(err <= 1e-4 + 1e-3 * np.abs(R)))
+    log(f"dtype {dtype}: {len(strict)} of {err.size} outputs need the accumulation term; "
+        f"worst err / sum|xw| = {float(np.max(err / A)):.3g}")
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0])
 def test_gemm_non_finite_rows_are_nan(dtype):
     """A row holding a NaN or an infinity gives NaN outputs (gemv_quant's f64
     sum is NaN, or +-inf by the row's weights, for such a row: non-finite

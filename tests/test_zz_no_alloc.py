@@ -48,7 +48,7 @@ def test_gemm_static_equals_gemm_on_two_calls_the_second_smaller(dtype, K, N, Ms
 
 
 def test_gemm_static_refuses_a_workspace_beyond_the_array():
-    K, N, M = 4096, 256, 2048  # activation planes alone: 2 * 2048 * 4096 * 2 bytes > 32 MiB
+    K, N, M = 4096, 256, 4096  # activation planes alone: 2 * 4096 * 4096 * 2 bytes > 64 MiB
     W = uq.Weights(S.weights(S.Q4_K, N, K, seed=1), S.Q4_K, K, N)
     dx, dy = uq.DeviceArray(4 * M * K), uq.DeviceArray(4 * M * N)
     dy.upload(np.full(M * N, 7.0, np.float32))
@@ -60,11 +60,11 @@ def test_gemm_static_refuses_a_workspace_beyond_the_array():
     W.free()
 
 
-@pytest.mark.parametrize("dtype,K,N,M", [(S.F32, 4096, 64, 2048), (S.Q4_K, 4096, 300, 1)])
+@pytest.mark.parametrize("dtype,K,N,M", [(S.F32, 4096, 64, 4096), (S.Q4_K, 4096, 300, 1)])
 def test_gemm_static_needs_no_workspace_for_gemv_calls(dtype, K, N, M):
     """Calls that run as GEMVs (F32 weights, one row) need no workspace:
     uq_gemm_static takes them even where the activation planes of an MFMA
-    call (4*M*K bytes, 32 MiB here for F32) would exceed the fixed array,
+    call (4*M*K bytes, 32 MiB here for F32; 64 MiB at M = 4096) would exceed the fixed array,
     with uq_gemm's bits."""
     W = uq.Weights(S.weights(dtype, N, K, seed=3), dtype, K, N)
     X = S.activations(K, seed=4, rows=M).reshape(M, K)

@@ -66,18 +66,23 @@ constexpr int GTPB = 512;  // eight waves, two per SIMD
 // (eight x' values, f16, slots in k order 0,2,1,3,4,6,5,7) sit at
 // (o*M + m)*16, so the 32 rows of one MFMA operand and one octet are 512
 // contiguous bytes. g: per 256-k block and row, the eight group sums of x'
-// as f16 hi (16 bytes) then lo (16 bytes).
+// as f16 hi (16 bytes) then lo (16 bytes). scale: the power-of-two scale
+// of each row (M > 32: [M], s_m) or of each (256-k block, row) (M <= 32:
+// [K/256][M], s_bm), padded by 64 bytes (a loader reads 16 per block).
 struct GemmWs {
     uint8_t *ahi, *alo;
     uint8_t *g;
-    float *scale;  // [M] s_m
+    float *scale;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 size_t plane_bytes(int M, int K) { return align256((size_t)M * K * 2); }
 size_t gsum_bytes(int M, int K) { return align256((size_t)M * (K / 256) * 32); }
-size_t prep_bytes(int M, int K) { return 2 * plane_bytes(M, K) + gsum_bytes(M, K) + align256((size_t)M * 4); }
-size_t part_stride(int M, int N) { return ((size_t)M * N + 63) & ~(size_t)63; }
+size_t prep_bytes(int M, int K) {
+    return 2 * plane_bytes(M, K) + gsum_bytes(M, K) + align256((size_t)M * (K / 256) * 4 + 64);
+}
+// split-K partial tiles: f64, one M x N tile per K range
+size_t part_stride(int M, int N) { return ((size_t)M * N + 31) & ~(size_t)31; }
 
 GemmWs ws_carve(uint8_t *base, int M, int K) {
     GemmWs w;
@@ -158,6 +163,59 @@ __global__ __launch_bounds__(256) void gemm_convert_kernel(const float *__restri
     if ((q & 3) == 0) {
         _Float16 *dst = (_Float16 *)(ws.g + ((size_t)blockIdx.y * M + m) * 32);
         const int gi = ((threadIdx.x >> 6) * 8 + q) >> 2;
+        const _Float16 gh = (_Float16)(float)gs;
+        dst[gi] = gh;
+        dst[8 + gi] = (_Float16)(float)(gs - (double)gh);
+    }
+}
+
+// gemm_block_prep_kernel (M <= 32): as gemm_convert_kernel, with a power-of-
+// two scale per (256-k block, row) instead of per row, formed by the
+// workgroup from its own block: s_bm = 2^(e-10) with max|x| over the
+// block's 256 values in [2^(e-1), 2^e) (exponent kept at or above -115; a
+// NaN or infinity makes s_bm NaN and the block's planes zero). No pass over
+// the whole row, so one launch; the GEMM applies s_bm per block.
+__global__ __launch_bounds__(256) void gemm_block_prep_kernel(const float *__restrict__ X, int K, int M, GemmWs ws) {
+    __shared__ uint32_t red[4][8];
+    const int lane = threadIdx.x & 63, r = lane & 7, q = lane >> 3, wv = threadIdx.x >> 6;
+    const int m = blockIdx.x * 8 + r, o = blockIdx.y * 32 + wv * 8 + q;
+    const bool live = m < M;
+    const int mm = live ? m : M - 1;
+    const float4 *x = (const float4 *)(X + (size_t)mm * K + 8 * o);
+    const float4 a = x[0], b = x[1];
+    const float xs[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
+    uint32_t mb = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) mb = max(mb, __float_as_uint(xs[e]) & 0x7FFFFFFFu);
+    // the row's eight lanes of this wave (lane bits 3-5), then the four waves
+    for (int off = 8; off < 64; off <<= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
+    if (q == 0) red[wv][r] = mb;
+    __syncthreads();
+    mb = max(max(red[0][r], red[1][r]), max(red[2][r], red[3][r]));
+    int ex = 0;
+    if (mb) (void)frexpf(__uint_as_float(mb), &ex);
+    const float s = mb < 0x7F800000u ? ldexpf(1.0f, max(ex, -115) - 10) : __uint_as_float(0x7FC00000u);
+    const bool finite = s == s;
+    const float inv = finite ? 1.0f / s : 0.0f;  // a power of two: exact
+    h8 hi, lo;
+    double gs = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float xc = finite ? xs[e] * inv : 0.0f;
+        hi[e] = (_Float16)xc;
+        lo[e] = (_Float16)(xc - (float)hi[e]);
+        gs += (double)xc;
+    }
+    gs += __shfl_xor(gs, 8);
+    gs += __shfl_xor(gs, 16);
+    if (!live) return;
+    const size_t at = ((size_t)o * M + m) * 16;
+    *(h8 *)(ws.ahi + at) = hi;
+    *(h8 *)(ws.alo + at) = lo;
+    if (wv == 0 && q == 0) ws.scale[(size_t)blockIdx.y * M + m] = s;
+    if ((q & 3) == 0) {
+        _Float16 *dst = (_Float16 *)(ws.g + ((size_t)blockIdx.y * M + m) * 32);
+        const int gi = (wv * 8 + q) >> 2;
         const _Float16 gh = (_Float16)(float)gs;
         dst[gi] = gh;
         dst[8 + gi] = (_Float16)(float)(gs - (double)gh);
@@ -373,7 +431,7 @@ __device__ constexpr int raw_step(int r, int R) { return 11 + (r * 5) / R; }
 template <class BP, int WM, int WN, int NT, bool C64, int D>
 __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu(WM * WN / 4))) void gemm_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ntn, int ks,
-    float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
+    float *__restrict__ Y, double *__restrict__ Ypart, size_t part_stride) {
     static_assert(WM * WN == 8 || WM * WN == 4, "one wave per (wm, wn): two or one per SIMD");
     constexpr int TPB = 64 * WM * WN;
     constexpr int TM = 32 * WM, NTILE = NT * WN;
@@ -393,7 +451,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     const int nt = L % ntn, mk = L / ntn, mt = mk / ks, kidx = mk % ks;
     const int m0 = mt * TM, n0 = nt * TN;
     const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
-    float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
+    double *const Yp = ks > 1 ? Ypart + (size_t)kidx * part_stride : nullptr;
 
     const int wm = wv / WN, wn = wv % WN, lr = lane & 31, lh = lane >> 5;
 
@@ -629,6 +687,24 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     float rs[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) rs[r] = __shfl(rs_lane, 8 * (r >> 2) + 4 * lh + (r & 3));  // lane x: row 32 wm + x
+    if (Yp) {
+        // a K range's partial tile, in f64 (summed in range order by gemm_splitk_reduce)
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int n = n0 + 32 * (wn * NT + j) + lr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + 32 * wm + 8 * (r >> 2) + 4 * lh + (r & 3);
+                double v;
+                if constexpr (C64)
+                    v = (C[j][r] + (double)Cm[j][r]) * (double)rs[r];
+                else
+                    v = (double)C[j][r] * (double)rs[r];
+                if (m < M && n < N) Yp[(size_t)m * N + n] = v;
+            }
+        }
+        return;
+    }
     f16x Yv[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++)
@@ -646,7 +722,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     if (m0 + TM <= M && n0 + TN <= N) {
 #pragma unroll
         for (int j = 0; j < NT; j++) {
-            float *y = Yo + (size_t)(m0 + 32 * wm + 4 * lh) * N + n0 + 32 * (wn * NT + j) + lr;
+            float *y = Y + (size_t)(m0 + 32 * wm + 4 * lh) * N + n0 + 32 * (wn * NT + j) + lr;
 #pragma unroll
             for (int r = 0; r < 16; r++) y[(size_t)(8 * (r >> 2) + (r & 3)) * N] = Yv[j][r];
         }
@@ -658,29 +734,29 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int m = m0 + 32 * wm + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (m < M && n < N) Yo[(size_t)m * N + n] = Yv[j][r];
+            if (m < M && n < N) Y[(size_t)m * N + n] = Yv[j][r];
         }
     }
 }
 
-// Sum of the ks partial results of a split-K launch, in range order
-// (v = P_0, v += P_1, ...). The partials of eight ranges are loaded before
-// any is added, so a thread waits for one round of loads per eight ranges
-// instead of one per range.
-__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ P, int ks, size_t stride,
+// Sum of the ks f64 partial results of a split-K launch, in range order
+// (v = P_0, v += P_1, ...), rounded to f32 once. The partials of eight
+// ranges are loaded before any is added, so a thread waits for one round of
+// loads per eight ranges instead of one per range.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const double *__restrict__ P, int ks, size_t stride,
                                                           size_t MN, float *__restrict__ Y) {
     constexpr int G = 8;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-        float v = 0.0f;
+        double v = 0.0;
         for (int k0 = 0; k0 < ks; k0 += G) {
-            float p[G];
+            double p[G];
 #pragma unroll
-            for (int j = 0; j < G; j++) p[j] = k0 + j < ks ? P[(size_t)(k0 + j) * stride + i] : 0.0f;
+            for (int j = 0; j < G; j++) p[j] = k0 + j < ks ? P[(size_t)(k0 + j) * stride + i] : 0.0;
 #pragma unroll
             for (int j = 0; j < G; j++)
                 if (k0 + j < ks) v = (k0 + j == 0) ? p[j] : v + p[j];
         }
-        Y[i] = v;
+        Y[i] = (float)v;
     }
 }
 
@@ -692,31 +768,36 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ Y, s
 // With one 32-row tile every B column feeds a single MFMA tile, so nothing
 // is gained by sharing dequantized B through LDS: each compute wave owns 32
 // columns and dequantizes them straight into its B operands. A workgroup is
-// CW compute waves (adjacent 32-column tiles over one K range; their
-// activation loads are the same addresses, which the CU's L1 serves once)
-// and one loader wave that streams the raw blocks of all CW tiles into an
-// SK_RING-slot LDS ring with direct-to-LDS loads. The split keeps the HBM
-// loads out of the compute waves' in-order vmcnt queue, which then holds
-// only activation loads (L2): with the weight loads in the same queue, each
-// activation wait also waited for the next block's HBM loads. One barrier
-// per block: at barrier b, block b has landed (the loader waited for it)
-// and every wave is done with block b-1, whose slot the loader refills with
-// block b + SK_RING - 1. Per block the arithmetic is gemm_kernel's with the
-// same passes, so the results are bit-identical to its 64-row (Q6_K, Q8_0)
-// and 32-row (Q4_K) tiles: P over the block's 16 k-steps on the f16 MFMA,
-// then C += d*P (Q4_K, Q6_K) or C += P (Q8_0) in f64, and the Q4_K min
-// term on the MFMA; a split K is summed by gemm_splitk_reduce. For Q4_K,
-// eight compute waves measured faster than two or four; a four-slot ring and
-// eight activation k-steps in flight measured no faster.
-constexpr int SK_D = 4, SK_RING = 3;
-template <class BP, int CW>
+// CW compute waves (adjacent 32-column tiles over one K range) and one
+// loader wave that streams the raw blocks of all CW tiles into an
+// SK_RING-slot LDS ring with direct-to-LDS loads; with LA (M <= 16) the same
+// loads bring each block's activation fragments (hi and lo planes, 512 M
+// bytes each, contiguous in the prep's layout) and its row scales, so a
+// k-step's operands come from LDS, not from L2 (with four k-steps of L2
+// loads in flight, a block took about four L2 round trips). Without LA
+// (17 <= M <= 32) the compute waves load the activation fragments
+// themselves, SK_D k-steps ahead; the loader keeps the HBM loads out of
+// their in-order vmcnt queue. One barrier per block: at barrier b, block b
+// has landed (the loader waited for it) and every wave is done with block
+// b-1, whose slot the loader refills with block b + SK_RING - 1.
+// Per block: P over the block's 16 k-steps on the f16 MFMA (the passes of
+// gemm_kernel), then C += (d s_bm) * P (Q4_K, Q6_K) or s_bm * P (Q8_0) in
+// f64, s_bm the block's row scale (gemm_block_prep_kernel), and the Q4_K
+// min term as two MFMAs per block added as s_bm * (min term). A split K
+// writes f64 partial tiles that gemm_splitk_reduce sums in range order.
+constexpr int SK_D = 4, SK_RING = 3, SK_MA = 16;  // LA: rows staged in LDS (M <= SK_MA)
+template <class BP, int CW, bool LA>
 struct SkShape {
     static constexpr int COLS = 32 * CW;
-    static constexpr int CHUNKS = COLS * BP::CPR;  // 16-byte chunks per block
-    static constexpr int ROUNDS = CHUNKS / 64;     // loader loads per block
-    static constexpr int SLOT = CHUNKS * 16;
+    static constexpr int CHUNKS = COLS * BP::CPR;                     // 16-byte chunks of raw weights per block
+    static constexpr int ROUNDS = CHUNKS / 64;                        // loader loads of raw weights per block
+    static constexpr int RAW = CHUNKS * 16;
+    static constexpr int AHI = RAW, ALO = RAW + 512 * SK_MA, SC = RAW + 1024 * SK_MA;  // LA
+    static constexpr int SLOT = LA ? SC + 128 : RAW;
+    static constexpr int NA = LA ? 1024 * SK_MA / 1024 : 0;          // activation loads per block (16 KB)
+    static constexpr int LOADS = ROUNDS + (LA ? NA + 1 : 0);          // loader loads per block
     static_assert(CHUNKS % 64 == 0, "every loader round is a full wave");
-    static_assert((SK_RING - 2) * ROUNDS <= 63, "vmcnt immediate");
+    static_assert((SK_RING - 2) * LOADS <= 63, "vmcnt immediate");
     static_assert(SK_RING * SLOT <= 160 * 1024, "LDS");
 };
 
@@ -740,12 +821,15 @@ __device__ __forceinline__ void sk_dequant(uint2 q, h2 lsc, h2 loff, h2 hsc, h2 
 
 // The loader wave of the M <= 32 kernels: chunk 64 r + lane of a block is
 // 16 bytes of column chunk / CPR of column group cg (rows past N repeat the
-// last one), block b goes to ring slot b % SK_RING. It meets barrier 0
-// once block 0 has landed and barrier b+1 once block b+1 has.
-template <class BP, int CW>
-__device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_t row_bytes, int N, int cg, int kb0,
-                                          int nblk, int lane, uint8_t *ring) {
-    using Sh = SkShape<BP, CW>;
+// last one), block b goes to ring slot b % SK_RING; with LA also the
+// block's 512 M activation bytes of each plane (loads past them repeat the
+// last 16 bytes) and its M row scales (64 bytes; the workspace is padded).
+// It meets barrier 0 once block 0 has landed and barrier b+1 once block b+1
+// has.
+template <class BP, int CW, bool LA>
+__device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_t row_bytes, int N, int M,
+                                          const GemmWs &ws, int cg, int kb0, int nblk, int lane, uint8_t *ring) {
+    using Sh = SkShape<BP, CW, LA>;
     uint32_t goff[Sh::ROUNDS];
 #pragma unroll
     for (int r = 0; r < Sh::ROUNDS; r++) {
@@ -753,17 +837,28 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
         goff[r] = (uint32_t)min(cg * Sh::COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
     }
     const uint8_t *wb = W + (size_t)kb0 * BP::RB;
+    const uint32_t abytes = 512u * (uint32_t)M;  // one plane of one block
     auto issue = [&](int b) {
         const uint8_t *g = wb + (size_t)b * BP::RB;
         uint8_t *dst = ring + (b % SK_RING) * Sh::SLOT;
 #pragma unroll
         for (int r = 0; r < Sh::ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
+        if constexpr (LA) {
+            const size_t ab = (size_t)(kb0 + b) * abytes;
+#pragma unroll
+            for (int j = 0; j < Sh::NA / 2; j++) {
+                const uint32_t o = min((uint32_t)(1024 * j + 16 * lane), abytes - 16u);
+                dma16(ws.ahi + ab + o, dst + Sh::AHI + 1024 * j);
+                dma16(ws.alo + ab + o, dst + Sh::ALO + 1024 * j);
+            }
+            if (lane < 4) dma16(ws.scale + (size_t)(kb0 + b) * M + 4 * lane, dst + Sh::SC);
+        }
     };
     // barrier 0: block 0 landed (blocks 1..SK_RING-2 may be in flight)
     for (int j = 0; j < SK_RING - 1; j++)
         if (j < nblk) issue(j);
     if (nblk >= SK_RING - 1)
-        wait_vm_barrier<(SK_RING - 2) * Sh::ROUNDS>();
+        wait_vm_barrier<(SK_RING - 2) * Sh::LOADS>();
     else
         wait_vm_barrier<0>();
     for (int b = 0; b < nblk; b++) {
@@ -773,18 +868,18 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
         // wait for everything.
         if (b + SK_RING - 1 < nblk) {
             issue(b + SK_RING - 1);
-            wait_vm_barrier<(SK_RING - 2) * Sh::ROUNDS>();
+            wait_vm_barrier<(SK_RING - 2) * Sh::LOADS>();
         } else {
             wait_vm_barrier<0>();
         }
     }
 }
 
-template <class BP, int CW>
+template <class BP, int CW, bool LA>
 __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((CW + 4) / 4))) void gemm_skinny_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
-    float *__restrict__ Y, float *__restrict__ Ypart, size_t part_stride) {
-    using Sh = SkShape<BP, CW>;
+    float *__restrict__ Y, double *__restrict__ Ypart, size_t part_stride) {
+    using Sh = SkShape<BP, CW, LA>;
     constexpr int SK_CW = CW, SK_SLOT = Sh::SLOT;
     __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
     const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
@@ -797,21 +892,19 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
     const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
 
     if (wv == SK_CW) {
-        sk_loader<BP, CW>(W, row_bytes, N, cg, kb0, nblk, lane, ring);
+        sk_loader<BP, CW, LA>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
         return;
     }
 
     // compute wave wv: columns n0..n0+31 (a tile past N computes on the
     // repeated last row and stores nothing; it still meets every barrier)
     const int n0 = (cg * SK_CW + wv) * 32;
-    float *const Yo = ks > 1 ? Ypart + (size_t)kidx * part_stride : Y;
     const int am = min(lr, M - 1);
-    const float rs_lane = ws.scale[am];  // row lr's scale, read long before the epilogue
-    const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
     const uint32_t pbytes = (uint32_t)((size_t)M * K * 2);
     const auto rah = buf_rsrc(ws.ahi, pbytes), ral = buf_rsrc(ws.alo, pbytes);
     const int nks = 16 * nblk;
     const uint32_t kstep = (uint32_t)M * 32u, abase = (uint32_t)kb0 * 16u * kstep;
+    const uint32_t aoff = (uint32_t)(lh * M + am) * 16u;
     auto a_load = [&](h8 &hi, h8 &lo, int kk) {
         const uint32_t so = abase + (uint32_t)min(kk, nks - 1) * kstep;
         hi = buf_load16(rah, aoff, so);
@@ -820,30 +913,58 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
     const auto rg = buf_rsrc(ws.g, (uint32_t)((size_t)M * (K / 256) * 32));
     const uint32_t goff = (uint32_t)am * 32u + 16u * lh;
     auto g_load = [&](int b) { return buf_load16(rg, goff, (uint32_t)(kb0 + min(b, nblk - 1)) * (uint32_t)M * 32u); };
+    // the lane's rows 8 (r / 4) + 4 lh + r % 4: their block scales (rows
+    // past M read a neighbour's value; those outputs are not stored)
+    auto s_load = [&](int b, float (&sv)[16]) {
+        const float *sp = ws.scale + (size_t)(kb0 + b) * M;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sv[r] = sp[8 * (r >> 2) + 4 * lh + (r & 3)];
+    };
 
     const f16x zero = {};
-    f16x Cm = zero;
     double C[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) C[r] = 0.0;
     h8 ah[SK_D], al[SK_D];
+    if constexpr (!LA) {
 #pragma unroll
-    for (int d = 0; d < SK_D - 1; d++) a_load(ah[d], al[d], d);
+        for (int d = 0; d < SK_D - 1; d++) a_load(ah[d], al[d], d);
+    }
     h8 gm = {};
     if constexpr (BP::kMin) gm = g_load(0);
     const uint8_t *mycol = ring + (wv * 32 + lr) * (16 * BP::CPR);
     lds_barrier();  // barrier 0
 
     for (int b = 0; b < nblk; b++) {
+        const uint8_t *slot = ring + (b % SK_RING) * SK_SLOT;
         const uint8_t *rc = mycol + (b % SK_RING) * SK_SLOT;
-        // k-step i (0..15) of the block: the activation fragments of k-step
-        // i + SK_D - 1 are requested, then the passes of k-step i run on B
-        // (16 b is a multiple of SK_D, so the ring slots are compile-time)
+        float sv[16];
+        if constexpr (LA) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 v = *(const float4 *)(slot + Sh::SC + (8 * q + 4 * lh) * 4);
+                sv[4 * q] = v.x, sv[4 * q + 1] = v.y, sv[4 * q + 2] = v.z, sv[4 * q + 3] = v.w;
+            }
+        } else {
+            s_load(b, sv);  // first used after the block's k-steps
+        }
+        // k-step i (0..15) of the block: the passes of k-step i on B; the
+        // activation fragments from the ring (LA) or, SK_D k-steps ahead,
+        // from L2 (16 b is a multiple of SK_D, so the ring slots are compile-time)
         auto kstep = [&](int i, const h8 &B0, const h8 &B1, f16x &P) {
-            a_load(ah[(i + SK_D - 1) % SK_D], al[(i + SK_D - 1) % SK_D], 16 * b + i + SK_D - 1);
+            h8 xa, xl;
+            if constexpr (LA) {
+                const uint32_t o = (uint32_t)((2 * i + lh) * M + am) * 16u;
+                xa = *(const h8 *)(slot + Sh::AHI + o);
+                xl = *(const h8 *)(slot + Sh::ALO + o);
+            } else {
+                a_load(ah[(i + SK_D - 1) % SK_D], al[(i + SK_D - 1) % SK_D], 16 * b + i + SK_D - 1);
+                xa = ah[i % SK_D];
+                xl = al[i % SK_D];
+            }
 #pragma unroll
             for (int p = 0; p < BP::NPASS; p++) {
-                const h8 a = BP::pa(p) ? al[i % SK_D] : ah[i % SK_D];
+                const h8 a = BP::pa(p) ? xl : xa;
                 P = mfma(a, BP::pb(p) ? B1 : B0, (i == 0 && p == 0) ? zero : P);
             }
         };
@@ -869,7 +990,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
 #pragma unroll
                 for (int t = 0; t < 4; t++) kstep(4 * s + t, B[t], B[t], P);
             }
-            // the block's min term and C += d * P (d*P is exact in f64)
+            // the block's min term and C += (d s) * P, s * (min term) (exact products in f64)
             const float dmin = f16_hi(h.x), d = f16_lo(h.x);
             h8 bh, bl;
 #pragma unroll
@@ -878,10 +999,14 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
                 bh[g] = (_Float16)v;
                 bl[g] = (_Float16)(v - (float)bh[g]);
             }
-            Cm = mfma(gcur, bh, Cm);
+            f16x Cm = mfma(gcur, bh, zero);
             Cm = mfma(gcur, bl, Cm);
 #pragma unroll
-            for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+            for (int r = 0; r < 16; r++) {
+                const double sr = (double)sv[r];
+                C[r] = fma((double)d * sr, (double)P[r], C[r]);
+                C[r] = fma(sr, (double)Cm[r], C[r]);
+            }
         } else if constexpr (std::is_same<BP, GQ6K>::value) {
             // the lane's half (8 of 16 elements) of each k-step: ql bytes
             // 64 hb + 16 c + 8 lh, qh bytes 128 + 32 hb + 16 (c & 1) + 8 lh
@@ -924,7 +1049,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 16; r++) C[r] = fma((double)d, (double)P[r], C[r]);
+            for (int r = 0; r < 16; r++) C[r] = fma((double)d * (double)sv[r], (double)P[r], C[r]);
         } else {
             // Q8_0: k-step i = 4 s + c is elements 16 (c & 1).. of Q8_0 block
             // bi = 2 s + c / 2 (34 bytes at 34 bi); the lane's 8 q bytes sit
@@ -964,20 +1089,24 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
                 kstep(i, __builtin_bit_cast(h8, bh), __builtin_bit_cast(h8, bl), P);
             }
 #pragma unroll
-            for (int r = 0; r < 16; r++) C[r] += (double)P[r];
+            for (int r = 0; r < 16; r++) C[r] = fma((double)sv[r], (double)P[r], C[r]);
         }
         lds_barrier();  // barrier b+1: this wave is done with the slot of block b
     }
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the end land before the wave leaves
 
-    // lane holds column n0 + lr, rows 8*(r/4) + 4*lh + r%4
+    // lane holds column n0 + lr, rows 8*(r/4) + 4*lh + r%4; a split K
+    // stores the f64 partial
     const int n = n0 + lr;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int m = 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float rs = __shfl(rs_lane, min(m, M - 1));  // lane m holds row m's scale (m < 32)
-        const float v = (float)((C[r] + (double)Cm[r]) * (double)rs);
-        if (m < M && n < N) Yo[(size_t)m * N + n] = v;
+        if (m < M && n < N) {
+            if (ks > 1)
+                Ypart[(size_t)kidx * part_stride + (size_t)m * N + n] = C[r];
+            else
+                Y[(size_t)m * N + n] = (float)C[r];
+        }
     }
 }
 
@@ -1015,7 +1144,7 @@ Plan plan_for(uq_dtype dt, int M, int N, int K) {
 }
 
 template <class BP, int WM, int WN, int NT, bool C64, int D>
-hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
+hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, double *part, int ks, hipStream_t s) {
     constexpr int TM = 32 * WM, TN = 32 * NT * WN;
     const int K = w.dim_in, N = w.dim_out;
     const int ntm = (M + TM - 1) / TM, ntn = (N + TN - 1) / TN;
@@ -1031,7 +1160,7 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
     if ((e = hipGetLastError()) != hipSuccess || ks == 1) return e;
     const size_t MN = (size_t)M * N;
     const int rgrid = (int)std::min<size_t>((MN + 255) / 256, 4096);
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const float *)part, ks, ps, MN, Y);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const double *)part, ks, ps, MN, Y);
     return hipGetLastError();
 }
 
@@ -1039,23 +1168,27 @@ hipError_t gemm_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, 
 // small tiles, whose k-steps are short, 8 or 4 for the others (what the
 // registers allow; the 128 x 192 tile measured the same at 2, 4 and 8).
 template <class BP, int CW>
-hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, float *part, int ks, hipStream_t s) {
+hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y, double *part, int ks, hipStream_t s) {
     const int K = w.dim_in, N = w.dim_out;
-    const int ncg = (N + SkShape<BP, CW>::COLS - 1) / SkShape<BP, CW>::COLS;
+    const int ncg = (N + SkShape<BP, CW, false>::COLS - 1) / SkShape<BP, CW, false>::COLS;
     const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
-    hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
-                       (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
+    if (M <= SK_MA)
+        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, true>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
+                           (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
+    else
+        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, false>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
+                           (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ks == 1) return e;
     const size_t MN = (size_t)M * N;
     const int rgrid = (int)std::min<size_t>((MN + 255) / 256, 4096);
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const float *)part, ks, ps, MN, Y);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, s, (const double *)part, ks, ps, MN, Y);
     return hipGetLastError();
 }
 
 template <class BP>
-hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &ws, float *Y, float *part,
+hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &ws, float *Y, double *part,
                       hipStream_t s) {
     if constexpr (std::is_same<BP, GQ4K>::value) {
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 128 x 192
@@ -1085,7 +1218,7 @@ bool gemm_mfma_ok(const WeightsView &w, int M) {
 size_t gemm_ws_bytes(const WeightsView &w, int M) {
     if (M == 0 || w.dim_out == 0 || w.dim_in == 0 || M == 1 || !gemm_mfma_ok(w, M)) return 0;
     const Plan p = plan_for(w.dtype, M, w.dim_out, w.dim_in);
-    return prep_bytes(M, w.dim_in) + (p.ks > 1 ? (size_t)p.ks * part_stride(M, w.dim_out) * 4 : 0);
+    return prep_bytes(M, w.dim_in) + (p.ks > 1 ? (size_t)p.ks * part_stride(M, w.dim_out) * 8 : 0);
 }
 
 hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y, void *wsp, size_t wsb, hipStream_t s) {
@@ -1107,9 +1240,13 @@ hipError_t launch_gemm_ws(const WeightsView &w, int M, const float *X, float *Y,
     const Plan p = plan_for(w.dtype, M, N, K);
     if (wsb < gemm_ws_bytes(w, M) || !wsp) return hipErrorInvalidValue;
     const GemmWs ws = ws_carve((uint8_t *)wsp, M, K);
-    float *part = p.ks > 1 ? (float *)((uint8_t *)wsp + prep_bytes(M, K)) : nullptr;
-    hipLaunchKernelGGL(gemm_scale_kernel, dim3(M), dim3(64 * SCALE_WAVES), 0, s, X, K, M, ws.scale);
-    hipLaunchKernelGGL(gemm_convert_kernel, dim3((M + 7) / 8, K / 256), dim3(256), 0, s, X, K, M, ws);
+    double *part = p.ks > 1 ? (double *)((uint8_t *)wsp + prep_bytes(M, K)) : nullptr;
+    if (M <= 32) {  // per-(block, row) scales, one launch
+        hipLaunchKernelGGL(gemm_block_prep_kernel, dim3((M + 7) / 8, K / 256), dim3(256), 0, s, X, K, M, ws);
+    } else {
+        hipLaunchKernelGGL(gemm_scale_kernel, dim3(M), dim3(64 * SCALE_WAVES), 0, s, X, K, M, ws.scale);
+        hipLaunchKernelGGL(gemm_convert_kernel, dim3((M + 7) / 8, K / 256), dim3(256), 0, s, X, K, M, ws);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (w.dtype) {

@@ -387,7 +387,7 @@ def gemm_static(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=N
     _check(lib().uq_gemm_static(w.h, m, d_x.ptr, d_y.ptr, stream))
 
 
-GEMM_SCRATCH_BYTES = 32 << 20
+GEMM_SCRATCH_BYTES = 64 << 20
 
 
 def ffn_swiglu(gate: Weights, up: Weights, down: Weights, d_x: DeviceArray, d_h: DeviceArray,
