@@ -497,10 +497,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) __attribute__((amdgpu_waves_per_eu
     // at compile time) of block blk.
     auto dequant = [&](int blk, int sv, int i) {
         // where TN is not a multiple of 64 QW (192 on eight waves), the
-        // upper-half waves have no last task (a wave-uniform branch)
+        // upper-half waves have no last task (a wave-uniform branch); where
+        // it is not a multiple of 64 either (96), the lanes past TN idle
         if constexpr (TN % (64 * QW) != 0)
             if (64 * (wv >> 2) + 64 * QW * i >= TN) return;
         const int col = dq_col0 + 64 * QW * i;
+        if constexpr (TN % 64 != 0)
+            if (col >= TN) return;
         const uint8_t *rc = lds + Lay::RAW + (blk & 1) * Lay::RAWSLOT + col * (16 * BP::CPR);
         uint8_t *bt = lds + Lay::BT + (sv & 1) * Lay::BTSLOT;
         if constexpr (Lay::SUB) {
@@ -785,19 +788,25 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *__restrict__ Y, s
 // f64, s_bm the block's row scale (gemm_block_prep_kernel), and the Q4_K
 // min term as two MFMAs per block added as s_bm * (min term). A split K
 // writes f64 partial tiles that gemm_splitk_reduce sums in range order.
-constexpr int SK_D = 4, SK_RING = 3, SK_MA = 16;  // LA: rows staged in LDS (M <= SK_MA)
+// SK_LW loader waves share a block's loads (a wave keeps at most 63 loads
+// outstanding, and one loader wave held barely one block in flight).
+constexpr int SK_D = 4, SK_RING = 3, SK_MA = 16, SK_LW = 2;  // LA: rows staged in LDS (M <= SK_MA)
 template <class BP, int CW, bool LA>
 struct SkShape {
     static constexpr int COLS = 32 * CW;
     static constexpr int CHUNKS = COLS * BP::CPR;                     // 16-byte chunks of raw weights per block
-    static constexpr int ROUNDS = CHUNKS / 64;                        // loader loads of raw weights per block
+    static constexpr int ROUNDS = CHUNKS / 64;                        // loads of raw weights per block
     static constexpr int RAW = CHUNKS * 16;
     static constexpr int AHI = RAW, ALO = RAW + 512 * SK_MA, SC = RAW + 1024 * SK_MA;  // LA
     static constexpr int SLOT = LA ? SC + 128 : RAW;
-    static constexpr int NA = LA ? 1024 * SK_MA / 1024 : 0;          // activation loads per block (16 KB)
-    static constexpr int LOADS = ROUNDS + (LA ? NA + 1 : 0);          // loader loads per block
+    static constexpr int NA = LA ? SK_MA / 2 : 0;                     // activation load pairs (hi, lo) per block
+    // loads per block of loader wave li: raw rounds r = li (mod SK_LW), activation
+    // pairs j = li (mod SK_LW), and (li == 0) the row scales
+    static constexpr int loads(int li) {
+        return (ROUNDS - li + SK_LW - 1) / SK_LW + (LA ? 2 * ((NA - li + SK_LW - 1) / SK_LW) + (li == 0) : 0);
+    }
     static_assert(CHUNKS % 64 == 0, "every loader round is a full wave");
-    static_assert((SK_RING - 2) * LOADS <= 63, "vmcnt immediate");
+    static_assert((SK_RING - 2) * loads(0) <= 63, "vmcnt immediate");
     static_assert(SK_RING * SLOT <= 160 * 1024, "LDS");
 };
 
@@ -826,15 +835,16 @@ __device__ __forceinline__ void sk_dequant(uint2 q, h2 lsc, h2 loff, h2 hsc, h2 
 // last 16 bytes) and its M row scales (64 bytes; the workspace is padded).
 // It meets barrier 0 once block 0 has landed and barrier b+1 once block b+1
 // has.
-template <class BP, int CW, bool LA>
+template <class BP, int CW, bool LA, int LI>
 __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_t row_bytes, int N, int M,
                                           const GemmWs &ws, int cg, int kb0, int nblk, int lane, uint8_t *ring) {
     using Sh = SkShape<BP, CW, LA>;
-    uint32_t goff[Sh::ROUNDS];
+    constexpr int NR = (Sh::ROUNDS - LI + SK_LW - 1) / SK_LW, LOADS = Sh::loads(LI);
+    uint32_t goff[NR];
 #pragma unroll
-    for (int r = 0; r < Sh::ROUNDS; r++) {
-        const int c = 64 * r + lane, col = c / BP::CPR, part = c - col * BP::CPR;
-        goff[r] = (uint32_t)min(cg * Sh::COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
+    for (int i = 0; i < NR; i++) {
+        const int c = 64 * (LI + SK_LW * i) + lane, col = c / BP::CPR, part = c - col * BP::CPR;
+        goff[i] = (uint32_t)min(cg * Sh::COLS + col, N - 1) * row_bytes + 16u * (uint32_t)part;
     }
     const uint8_t *wb = W + (size_t)kb0 * BP::RB;
     const uint32_t abytes = 512u * (uint32_t)M;  // one plane of one block
@@ -842,23 +852,24 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
         const uint8_t *g = wb + (size_t)b * BP::RB;
         uint8_t *dst = ring + (b % SK_RING) * Sh::SLOT;
 #pragma unroll
-        for (int r = 0; r < Sh::ROUNDS; r++) dma16(g + goff[r], dst + 1024 * r);
+        for (int i = 0; i < NR; i++) dma16(g + goff[i], dst + 1024 * (LI + SK_LW * i));
         if constexpr (LA) {
             const size_t ab = (size_t)(kb0 + b) * abytes;
 #pragma unroll
-            for (int j = 0; j < Sh::NA / 2; j++) {
+            for (int j = LI; j < Sh::NA; j += SK_LW) {
                 const uint32_t o = min((uint32_t)(1024 * j + 16 * lane), abytes - 16u);
                 dma16(ws.ahi + ab + o, dst + Sh::AHI + 1024 * j);
                 dma16(ws.alo + ab + o, dst + Sh::ALO + 1024 * j);
             }
-            if (lane < 4) dma16(ws.scale + (size_t)(kb0 + b) * M + 4 * lane, dst + Sh::SC);
+            if constexpr (LI == 0)
+                if (lane < 4) dma16(ws.scale + (size_t)(kb0 + b) * M + 4 * lane, dst + Sh::SC);
         }
     };
     // barrier 0: block 0 landed (blocks 1..SK_RING-2 may be in flight)
     for (int j = 0; j < SK_RING - 1; j++)
         if (j < nblk) issue(j);
     if (nblk >= SK_RING - 1)
-        wait_vm_barrier<(SK_RING - 2) * Sh::LOADS>();
+        wait_vm_barrier<(SK_RING - 2) * LOADS>();
     else
         wait_vm_barrier<0>();
     for (int b = 0; b < nblk; b++) {
@@ -868,7 +879,7 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
         // wait for everything.
         if (b + SK_RING - 1 < nblk) {
             issue(b + SK_RING - 1);
-            wait_vm_barrier<(SK_RING - 2) * Sh::LOADS>();
+            wait_vm_barrier<(SK_RING - 2) * LOADS>();
         } else {
             wait_vm_barrier<0>();
         }
@@ -876,7 +887,7 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
 }
 
 template <class BP, int CW, bool LA>
-__global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((CW + 4) / 4))) void gemm_skinny_kernel(
+__global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_eu((CW + SK_LW + 3) / 4))) void gemm_skinny_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
     float *__restrict__ Y, double *__restrict__ Ypart, size_t part_stride) {
     using Sh = SkShape<BP, CW, LA>;
@@ -891,8 +902,12 @@ __global__ __launch_bounds__(64 * (CW + 1)) __attribute__((amdgpu_waves_per_eu((
     const int cg = L % ncg, kidx = L / ncg;
     const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
 
-    if (wv == SK_CW) {
-        sk_loader<BP, CW, LA>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+    if (wv >= SK_CW) {
+        static_assert(SK_LW == 2, "loader instantiations");
+        if (wv == SK_CW)
+            sk_loader<BP, CW, LA, 0>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+        else
+            sk_loader<BP, CW, LA, 1>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
         return;
     }
 
@@ -1131,13 +1146,17 @@ struct Plan {
 Plan plan_for(uq_dtype dt, int M, int N, int K) {
     Plan p;
     // rows per tile: 128 beyond M = 64, else 64, else (Q4_K) 32; columns:
-    // Q4_K 192 (128-row tiles) or 256, Q6_K / Q8_0 128. M <= 32 runs the
-    // loader-wave kernel over the same column groups (256 for Q4_K, 128
-    // otherwise), so the K split below holds for it too.
+    // Q4_K 192 (128-row tiles) or 256, Q6_K / Q8_0 128; Q8_0 beyond M = 128
+    // takes 256 x 96 tiles (eight waves down the rows, all on the same
+    // 96 columns), so that M = 512, N = 12288 makes 256 tiles, one per CU,
+    // where 128 x 128 made 384 (a second round on half the chip). M <= 32
+    // runs the loader-wave kernel over the same column groups (256 for
+    // Q4_K, 128 otherwise), so the K split below holds for it too.
     const bool q4 = dt == UQ_Q4_K;
     p.wm = M > 64 ? 4 : (M > 32 || !q4) ? 2 : 1;
+    if (dt == UQ_Q8_0 && M > 128) p.wm = 8;  // 256 x 96: 256 tiles at M = 512, N = 12288
     p.tm = 32 * p.wm;
-    p.tn = q4 ? (p.wm == 4 ? 192 : 256) : 128;
+    p.tn = q4 ? (p.wm == 4 ? 192 : 256) : p.wm == 8 ? 96 : 128;
     const int tiles = ((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
     p.ks = std::max(1, std::min(K / 256, gemm_cus() / std::max(tiles, 1)));
     return p;
@@ -1174,10 +1193,10 @@ hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y
     const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
     if (M <= SK_MA)
-        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, true>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
+        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, true>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
                            (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     else
-        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, false>), dim3(grid), dim3(64 * (CW + 1)), 0, s, w.bytes,
+        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, false>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
                            (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ks == 1) return e;
@@ -1195,6 +1214,8 @@ hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &
         if (p.wm == 2) return gemm_launch<BP, 2, 4, 2, true, 4>(w, M, ws, Y, part, p.ks, s);   // 64 x 256
         return skinny_launch<BP, 8>(w, M, ws, Y, part, p.ks, s);                                // M <= 32
     } else {
+        if constexpr (std::is_same<BP, GQ80>::value)
+            if (p.wm == 8) return gemm_launch<BP, 8, 1, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 256 x 96
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
         if (M <= 32) return skinny_launch<BP, 4>(w, M, ws, Y, part, p.ks, s);                 // M <= 32
         return gemm_launch<BP, 2, 4, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 64 x 128
