@@ -1125,6 +1125,239 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
     }
 }
 
+// ------------------------------------------------------------ GEMM, M <= 16
+// The loader waves and the LDS ring of gemm_skinny_kernel (LA: each block's
+// activation fragments and row scales in the ring), with 16-row tiles on
+// v_mfma_f32_16x16x32_f16: a compute wave owns 16 rows x 32 columns (two
+// 16-column tiles, two independent accumulator chains) instead of 32 x 32,
+// so at M = 8 half the matrix work is padding rows instead of three
+// quarters. A lane holds column i % 16 of each tile and k-octet i / 16 of a
+// 32-k step (k-step t: the block's octets 4t .. 4t + 3, the prep's layout),
+// and its outputs are rows 4 (i / 16) .. + 3. Per block the arithmetic is
+// the skinny kernel's: P over the block on the MFMA (the same exact f16
+// operands and passes), C += (d s_bm) * P (Q4_K, Q6_K) or s_bm * P (Q8_0)
+// in f64, the Q4_K min term on v_mfma_f32_16x16x16_f16.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4x __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4x mfma16(h8 a, h8 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ f4x mfma16k16(h4 a, h4 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+
+template <class BP, int CW>
+__global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_eu((CW + SK_LW + 3) / 4))) void gemm_m16_kernel(
+    const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
+    float *__restrict__ Y, double *__restrict__ Ypart, size_t part_stride) {
+    using Sh = SkShape<BP, CW, true>;
+    constexpr int SK_SLOT = Sh::SLOT;
+    __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
+    const int lane = threadIdx.x & 63, lc = lane & 15, lq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int T = ncg * ks, per = (T + 7) / 8;
+    const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if ((blockIdx.x >> 3) >= per || L >= T) return;  // the whole workgroup
+    const int cg = L % ncg, kidx = L / ncg;
+    const int nbt = K / 256, kb0 = kidx * nbt / ks, nblk = (kidx + 1) * nbt / ks - kb0;
+
+    if (wv >= CW) {
+        if (wv == CW)
+            sk_loader<BP, CW, true, 0>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+        else
+            sk_loader<BP, CW, true, 1>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+        return;
+    }
+
+    // compute wave wv: columns n0 + 16 j + lc (j = 0, 1)
+    const int n0 = (cg * CW + wv) * 32;
+    const int ar = min(lc, M - 1);
+    const auto rg = buf_rsrc(ws.g, (uint32_t)((size_t)M * (K / 256) * 32));
+    const uint32_t goff = (uint32_t)ar * 32u + 8u * lq;
+    auto g_load = [&](int b) {
+        typedef int i2 __attribute__((ext_vector_type(2)));
+        const i2 v = __builtin_amdgcn_raw_buffer_load_b64(rg, (int)goff, (int)((uint32_t)(kb0 + min(b, nblk - 1)) * (uint32_t)M * 32u), 0);
+        return __builtin_bit_cast(h4, v);
+    };
+    const f4x zero4 = {};
+    double C[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) C[j][r] = 0.0;
+    h4 gm = {};
+    if constexpr (BP::kMin) gm = g_load(0);
+    lds_barrier();  // barrier 0
+
+    for (int b = 0; b < nblk; b++) {
+        const uint8_t *slot = ring + (b % SK_RING) * SK_SLOT;
+        const uint8_t *rc[2] = {slot + (wv * 32 + lc) * (16 * BP::CPR), slot + (wv * 32 + 16 + lc) * (16 * BP::CPR)};
+        // the lane's rows 4 lq .. 4 lq + 3: block scales (rows past M read a
+        // neighbour's value; those outputs are not stored)
+        const float4 sv4 = *(const float4 *)(slot + Sh::SC + 16 * lq);
+        const float sv[4] = {sv4.x, sv4.y, sv4.z, sv4.w};
+        auto afrag = [&](int t, h8 &xa, h8 &xl) {
+            const uint32_t o = (uint32_t)((4 * t + lq) * M + ar) * 16u;
+            xa = *(const h8 *)(slot + Sh::AHI + o);
+            xl = *(const h8 *)(slot + Sh::ALO + o);
+        };
+        f4x P[2] = {zero4, zero4};
+        if constexpr (std::is_same<BP, GQ4K>::value) {
+            u4 h[2];
+            uint2 q[2][4];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                h[j] = *(const u4 *)rc[j];
+#pragma unroll
+                for (int st = 0; st < 4; st++) q[j][st] = *(const uint2 *)(rc[j] + 16 + 32 * st + 8 * lq);
+            }
+            const h4 gcur = gm;
+            gm = g_load(b + 1);
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                // sub-step st: groups 2 st (low nibbles: 32-k step 2 st) and 2 st + 1 (high: 2 st + 1)
+                h8 Blo[2], Bhi[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float sa = (float)GQ4K::sc_of(h[j].y, h[j].w, 2 * st), sb = (float)GQ4K::sc_of(h[j].y, h[j].w, 2 * st + 1);
+                    sk_dequant(q[j][st], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), Blo[j], Bhi[j]);
+                }
+                h8 xa, xl;
+                afrag(2 * st, xa, xl);
+#pragma unroll
+                for (int j = 0; j < 2; j++) P[j] = mfma16(xl, Blo[j], mfma16(xa, Blo[j], P[j]));
+                afrag(2 * st + 1, xa, xl);
+#pragma unroll
+                for (int j = 0; j < 2; j++) P[j] = mfma16(xl, Bhi[j], mfma16(xa, Bhi[j], P[j]));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                // min term: group sums g = (4 lq + 0..3) % 8 (hi for lq < 2, lo after) times -dmin*m_g hi, then lo
+                const float dmin = f16_hi(h[j].x), d = f16_lo(h[j].x);
+                h4 bh, bl;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int g = (4 * lq + k) & 7;
+                    const float v = -(dmin * (float)GQ4K::m_of(h[j].z, h[j].w, g));
+                    bh[k] = (_Float16)v;
+                    bl[k] = (_Float16)(v - (float)bh[k]);
+                }
+                const f4x Cm = mfma16k16(gcur, bl, mfma16k16(gcur, bh, zero4));
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const double sr = (double)sv[r];
+                    C[j][r] = fma((double)d * sr, (double)P[j][r], C[j][r]);
+                    C[j][r] = fma(sr, (double)Cm[r], C[j][r]);
+                }
+            }
+        } else if constexpr (std::is_same<BP, GQ6K>::value) {
+            // 32-k step t = 2u + v: the lane's octet lq is 16-k step i = 2t + (lq >> 1)
+            // (sub-step u, half lq & 1): ql bytes 64 (u >> 1) + 16 c + 8 (lq & 1) with
+            // c = 2v + (lq >> 1), qh bytes 128 + 32 (u >> 1) + 16 (lq >> 1) + 8 (lq & 1),
+            // the nibble of sub-step parity u & 1, qh field 2 (2 (u & 1) + v), scale sc[i]
+            const int q1 = lq >> 1, q0 = lq & 1;
+            const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+            const h2 off = hh(-1056.0f);
+            u4 scv[2];
+            float dv[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                scv[j] = *(const u4 *)(rc[j] + 192);
+                dv[j] = f16_lo(*(const uint16_t *)(rc[j] + 208));
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int u = t >> 1, v = t & 1, hb = u >> 1, jj = u & 1, shift = 2 * (2 * jj + v);
+                h8 xa, xl;
+                afrag(t, xa, xl);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint2 A = *(const uint2 *)(rc[j] + 64 * hb + 32 * v + 16 * q1 + 8 * q0);
+                    const uint2 Cq = *(const uint2 *)(rc[j] + 128 + 32 * hb + 16 * q1 + 8 * q0);
+                    const uint32_t scw = (&scv[j].x)[t >> 1] >> (16 * (t & 1));  // sc[2t], sc[2t + 1]
+                    const int sc = (int)(int8_t)((scw >> (8 * q1)) & 0xFF);
+                    const h2 se = hh((float)(sc & ~1)), so = hh((float)(sc & 1));
+                    u4 b1, b2;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t Ad = e ? A.y : A.x, Cd = e ? Cq.y : Cq.x;
+                        const uint32_t raw = (jj ? (Ad >> 4) & 0x0F0F0F0Fu : Ad & 0x0F0F0F0Fu) | (((Cd >> shift) & 0x03030303u) << 4);
+                        const h2 q0v = as_h2(bfi(bm, raw, mag)) + off, q1v = as_h2(bfi(bm, raw >> 8, mag)) + off;
+                        (&b1.x)[2 * e] = as_u(q0v * se);
+                        (&b1.x)[2 * e + 1] = as_u(q1v * se);
+                        (&b2.x)[2 * e] = as_u(q0v * so);
+                        (&b2.x)[2 * e + 1] = as_u(q1v * so);
+                    }
+                    const h8 B1 = __builtin_bit_cast(h8, b1), B2 = __builtin_bit_cast(h8, b2);
+                    P[j] = mfma16(xl, B2, mfma16(xa, B2, mfma16(xl, B1, mfma16(xa, B1, P[j]))));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) C[j][r] = fma((double)dv[j] * (double)sv[r], (double)P[j][r], C[j][r]);
+        } else {
+            // Q8_0: 32-k step t is Q8_0 block t (34 bytes at 34 t); the lane's 8 q
+            // bytes at 2 + 8 lq sit at 2 (mod 4) for even t and are realigned
+            const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
+            const h2 off = hh(-1152.0f);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                h8 xa, xl;
+                afrag(t, xa, xl);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint8_t *blk = rc[j] + 34 * t;
+                    const _Float16 df = __builtin_bit_cast(_Float16, *(const uint16_t *)blk);
+                    const h2 d2 = h2{df, df};
+                    const uint8_t *qp = blk + 2 + 8 * lq;
+                    uint32_t w[2];
+                    if (t & 1) {
+                        w[0] = ((const uint32_t *)qp)[0];
+                        w[1] = ((const uint32_t *)qp)[1];
+                    } else {
+                        const uint32_t *pp = (const uint32_t *)(qp - 2);
+                        const uint32_t r0 = pp[0], r1 = pp[1], r2 = pp[2];
+                        w[0] = __builtin_amdgcn_alignbyte(r1, r0, 2);
+                        w[1] = __builtin_amdgcn_alignbyte(r2, r1, 2);
+                    }
+                    u4 bh, bl;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t u = w[e] ^ 0x80808080u;
+                        const h2 q0v = as_h2(bfi(bm, u, mag)) + off, q1v = as_h2(bfi(bm, u >> 8, mag)) + off;
+                        const h2 h0 = q0v * d2, h1 = q1v * d2;
+                        const h2 l0 = __builtin_elementwise_fma(q0v, d2, -h0), l1 = __builtin_elementwise_fma(q1v, d2, -h1);
+                        (&bh.x)[2 * e] = as_u(h0);
+                        (&bh.x)[2 * e + 1] = as_u(h1);
+                        (&bl.x)[2 * e] = as_u(l0);
+                        (&bl.x)[2 * e + 1] = as_u(l1);
+                    }
+                    const h8 BH = __builtin_bit_cast(h8, bh), BL = __builtin_bit_cast(h8, bl);
+                    P[j] = mfma16(xa, BL, mfma16(xl, BH, mfma16(xa, BH, P[j])));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) C[j][r] = fma((double)sv[r], (double)P[j][r], C[j][r]);
+        }
+        lds_barrier();  // barrier b+1: this wave is done with the slot of block b
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + 16 * j + lc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 4 * lq + r;
+            if (m < M && n < N) {
+                if (ks > 1)
+                    Ypart[(size_t)kidx * part_stride + (size_t)m * N + n] = C[j][r];
+                else
+                    Y[(size_t)m * N + n] = (float)C[j][r];
+            }
+        }
+    }
+}
+
 int gemm_cus() {
     static int n = 0;
     if (!n) {
@@ -1193,7 +1426,7 @@ hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y
     const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
     if (M <= SK_MA)
-        hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, true>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
+        hipLaunchKernelGGL((gemm_m16_kernel<BP, CW>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
                            (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     else
         hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, false>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
