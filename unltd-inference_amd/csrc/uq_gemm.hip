@@ -795,7 +795,7 @@ template <class BP, int CW, bool LA>
 struct SkShape {
     static constexpr int COLS = 32 * CW;
     static constexpr int CHUNKS = COLS * BP::CPR;                     // 16-byte chunks of raw weights per block
-    static constexpr int ROUNDS = CHUNKS / 64;                        // loads of raw weights per block
+    static constexpr int ROUNDS = (CHUNKS + 63) / 64;                 // loads of raw weights per block (the last may be partial)
     static constexpr int RAW = CHUNKS * 16;
     static constexpr int AHI = RAW, ALO = RAW + 512 * SK_MA, SC = RAW + 1024 * SK_MA;  // LA
     static constexpr int SLOT = LA ? SC + 128 : RAW;
@@ -805,7 +805,7 @@ struct SkShape {
     static constexpr int loads(int li) {
         return (ROUNDS - li + SK_LW - 1) / SK_LW + (LA ? 2 * ((NA - li + SK_LW - 1) / SK_LW) + (li == 0) : 0);
     }
-    static_assert(CHUNKS % 64 == 0, "every loader round is a full wave");
+    static_assert(CHUNKS % 64 == 0 || CHUNKS % 64 >= 32, "a partial last round still has active lanes in each loader");
     static_assert((SK_RING - 2) * loads(0) <= 63, "vmcnt immediate");
     static_assert(SK_RING * SLOT <= 160 * 1024, "LDS");
 };
@@ -852,7 +852,8 @@ __device__ __forceinline__ void sk_loader(const uint8_t *__restrict__ W, uint32_
         const uint8_t *g = wb + (size_t)b * BP::RB;
         uint8_t *dst = ring + (b % SK_RING) * Sh::SLOT;
 #pragma unroll
-        for (int i = 0; i < NR; i++) dma16(g + goff[i], dst + 1024 * (LI + SK_LW * i));
+        for (int i = 0; i < NR; i++)
+            if (64 * (LI + SK_LW * i) + lane < Sh::CHUNKS) dma16(g + goff[i], dst + 1024 * (LI + SK_LW * i));
         if constexpr (LA) {
             const size_t ab = (size_t)(kb0 + b) * abytes;
 #pragma unroll
