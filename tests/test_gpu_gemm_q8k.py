@@ -5,8 +5,9 @@ The reference forward prefills token by token through gemv_quant_q8k
 (greedy.rs:55-65; qwen35_forward.rs:365-401), so every row of the batched
 call must carry exactly the bits of that token's call. The shapes cover the
 prefill workload itself (Q4_K 12288 x 4096 at M = 512), the Q6_K FFN-down
-shape (4096 x 12288), each workgroup width the launcher picks (8, 4, 2 and
-1 waves: large M, M around 128, small M), ragged M (padding rows) and N
+shape (4096 x 12288), each tile the launcher picks (64-row waves in
+eight-wave workgroups for M > 128, 32-row waves in six, two or one-wave
+workgroups, 16-row waves for M <= 16), ragged M (padding rows) and N
 (columns past the end), one block, many blocks, and the edge cases of the
 quantizer and of the block scales.
 """
@@ -59,8 +60,8 @@ def assert_rows(Y, R, what):
 
 
 def test_gemm_q8k_prefill_config_every_row():
-    """The prefill workload: Q4_K N = 12288, K = 4096, M = 512 (eight-wave
-    workgroups, 16 blocks each), every row against the oracle."""
+    """The prefill workload: Q4_K N = 12288, K = 4096, M = 512 (64 x 128
+    workgroup tiles, 16 blocks each), every row against the oracle."""
     K, N, M = 4096, 12288, 512
     log(f"gemm_q8k q4k K={K} N={N} M={M}")
     w = S.weights(S.Q4_K, N, K, seed=S.seed_for(3))
@@ -81,7 +82,8 @@ def test_gemm_q8k_q6k_down_shape_every_row():
 
 
 SHAPES = [
-    # (K, N, M): waves per workgroup from the tile count (8 at many tiles, then 4, 2, 1)
+    # (K, N, M): row tile 16 (M <= 16), 64 (M = 200 at N = 8192: 256 tiles of
+    # 64 x 128), else 32 with six, two or one waves per workgroup
     (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
     (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
 ]

@@ -21,15 +21,16 @@
 // fragment order, plus per (block, row) the f32 d and the f16 bsums.
 // Rows are padded to a multiple of 32 with zero blocks.
 //
-// Main kernel: a workgroup owns 32 rows x 32 NC columns, two waves per
-// 32 x 32 output tile, and walks the blocks in order (the f32 epilogue is
-// sequential over blocks, so K is never split). Per block, the activation
-// octets of its 32 rows (16 KB), the raw weight blocks of its columns and
+// Main kernel: a workgroup owns 32 rows (16 for M <= 16) x 16 NW columns,
+// one wave per 16-column tile, and walks the blocks in order (the f32
+// epilogue is sequential over blocks, so K is never split). Per block, the
+// activation octets of its rows, the raw weight blocks of its columns and
 // the rows' d / bsums stream into a two-slot LDS ring with direct-to-LDS
 // loads, issued one block ahead; one barrier per block. Each wave decodes
-// its own column tile's weights for its four lane sums into B operands in
-// registers: a lane holds column lane % 32 and octet lane / 32 of every
-// operand.
+// its columns' weights into B operands in registers (a lane holds column
+// lane % 16 and one octet of all eight lane sums) and keeps the eight lane
+// sums of its outputs in registers: 32 x 16 outputs fit three waves per
+// SIMD.
 #include <algorithm>
 #include <type_traits>
 
@@ -42,7 +43,7 @@ namespace uq {
 namespace {
 
 // ------------------------------------------------------------ workspace
-// Rows padded to Mp (a multiple of 32). a: octet o of fragment F = 16 b +
+// Rows padded to Mp (a multiple of the row tile: 64 for M > 128, else 32). a: octet o of fragment F = 16 b +
 // 2 l + h of row m at ((2 F + o) * Mp + m) * 16; bs: the 16 bsums of (b, m)
 // as f16 at (b * Mp + m) * 32; d8: q8.d of (b, m) at b * Mp + m.
 struct Q8Ws {
@@ -52,14 +53,14 @@ struct Q8Ws {
 };
 
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-int pad32(int M) { return (M + 31) & ~31; }
+int q8k_mp(int M) { return M > 128 ? (M + 63) & ~63 : (M + 31) & ~31; }
 size_t q8_a_bytes(int Mp, int K) { return al256((size_t)Mp * K * 2); }
 size_t q8_bs_bytes(int Mp, int K) { return al256((size_t)Mp * (K / 256) * 32); }
 size_t q8_d8_bytes(int Mp, int K) { return al256((size_t)Mp * (K / 256) * 4); }
 
 Q8Ws q8_carve(uint8_t *base, int M, int K) {
     Q8Ws w;
-    w.Mp = pad32(M);
+    w.Mp = q8k_mp(M);
     w.a = base;
     w.bs = base + q8_a_bytes(w.Mp, K);
     w.d8 = (float *)(w.bs + q8_bs_bytes(w.Mp, K));
@@ -151,68 +152,67 @@ struct Q8Fmt {
     static constexpr int CPR = Q6 ? 14 : 9;    // 16-byte chunks per column and block in LDS
 };
 
-// A workgroup: NC column tiles of 32, two waves per tile (2 NC waves).
-template <bool Q6, int NC>
+// A workgroup: NW waves of 16 columns, TM = 16 RT rows. LDS slot of one
+// block: the activation fragments (fragment f = 2 l + h of the prep: octet
+// o' of row r at f * 32 TM + (o' TM + r) * 16), the raw weight blocks, the
+// rows' bsums (32 B each) and q8.d.
+template <bool Q6, int NW, int RT>
 struct Q8Lay {
-    static constexpr int NW = 2 * NC, TN = 32 * NC;
-    static constexpr int A = 0, ASZ = 16 * 1024;                       // 16 fragments of 64 lanes x 16 bytes
+    static constexpr int TN = 16 * NW, TM = 16 * RT;
+    static constexpr int A = 0, ASZ = 16 * 32 * TM;
     static constexpr int B = ASZ, BSZ = TN * Q8Fmt<Q6>::CPR * 16;      // raw blocks, column-major
-    static constexpr int BS = B + BSZ, D8 = BS + 32 * 32;              // bsums [32 rows][32 B], d8 [32 rows]
-    static constexpr int SLOT = D8 + 32 * 4;
+    static constexpr int BS = B + BSZ, D8 = BS + 32 * TM;
+    static constexpr int SLOT = D8 + 4 * TM;
     static constexpr int BYTES = 2 * SLOT;
     static constexpr int BROUNDS = (TN * Q8Fmt<Q6>::CPR + 64 * NW - 1) / (64 * NW);
     static_assert(BYTES <= 160 * 1024, "LDS");
-    static_assert(NC * 2 * 64 * 16 * 4 <= BYTES, "the end-of-tile exchange fits the ring");
 };
 
 __device__ __forceinline__ h2 h2_of(float a, float b) { return h2{(_Float16)a, (_Float16)b}; }
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4x __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4x mfma16(h8 a, h8 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ f4x mfma16k16(h4 a, h4 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-// Scale of Q4_K group 2c + hi (hi = 0, 1) of qs chunk c = 2h + cc, h known
-// at compile time (scale_min_k4, quants.rs:92-102).
-template <int H>
-__device__ __forceinline__ float q4k_chunk_sc(uint32_t S0, uint32_t S2, int cc, int hi) {
-    const int g4 = 2 * cc + hi;  // group - 4 H
-    if constexpr (H == 0) return (float)((S0 >> (8 * g4)) & 63);
-    return (float)(((S2 >> (8 * g4)) & 0xF) | (((S0 >> (8 * g4 + 6)) & 3) << 4));
-}
-
-// Wave (c, half) of a workgroup owns the 32 x 32 output tile of column tile
-// c and the lane sums l = 4 half .. 4 half + 3 of it (the reference's
-// sums[l] accumulators), so a wave holds 64 accumulator registers and
-// dequantizes only the weights of its four lanes. Per lane: the two MFMAs
-// of the next lane are issued before this lane's epilogue. The block's
-// d = q8.d * f16(d) products are formed by both waves; the Q4_K min term by
-// half 0 for rows r < 8 of the lane's 16 and by half 1 for the rest. At the
-// end half 1 hands its sumf to half 0, half 0 forms sumf + sums[0..3] and
-// hands it back, and half 1 adds sums[4..7] in order and stores.
-template <bool Q6, int NC>
-__global__ __launch_bounds__(128 * NC) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q8k_kernel(
+// Wave wv owns columns n0 + 16 wv .. + 15 of the workgroup's TM rows: RT
+// output tiles of 16 x 16 on v_mfma_f32_16x16x32_f16, all eight lane sums
+// of each output (the reference's sums[8]) in its registers. Per block and
+// lane sum l: one MFMA per row tile, K = 32 = the lane's 32 elements of the
+// block (uq_q8k_tiles.h); a lane holds column lane % 16 and octet q = lane
+// / 16 (= 2h + o' of the prep's octets), so it decodes one qs chunk (Q4_K:
+// c = q) or one ql / qh run pair (Q6_K) for all eight lane sums. The next
+// lane sum's MFMAs are issued before this one's epilogue. The Q4_K min sum
+// is one v_mfma_f32_16x16x16_f16 per row tile (bsums times m[g / 2]).
+template <bool Q6, int NW, int RT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(RT > 2 ? 2 : 3))) void gemm_q8k_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, Q8Ws ws, int ntm, int ntn,
     float *__restrict__ Y) {
     using F = Q8Fmt<Q6>;
-    using Lay = Q8Lay<Q6, NC>;
-    constexpr int NW = Lay::NW, TN = Lay::TN, CPR = F::CPR;
+    using Lay = Q8Lay<Q6, NW, RT>;
+    constexpr int TN = Lay::TN, TM = Lay::TM, CPR = F::CPR;
     extern __shared__ __align__(16) uint8_t lds[];
-    const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
-    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), ct = wv >> 1, half = wv & 1;
+    const int t = threadIdx.x, lane = t & 63, lc = lane & 15, lq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int hq = lq >> 1, oq = lq & 1;  // the lane's octet q = 2 h + o'
 
     // tiles (M fastest) dealt to the 8 XCDs in contiguous runs
     const int T = ntm * ntn, per = (T + 7) / 8;
     const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if ((blockIdx.x >> 3) >= per || L >= T) return;  // the whole workgroup
     const int mt = L % ntm, nt = L / ntm;
-    const int m0 = 32 * mt, n0 = TN * nt;
+    const int m0 = TM * mt, n0 = TN * nt;
     const int nblk = K >> 8, Mp = ws.Mp;
+    static_assert(64 % TM == 0, "row tile");
+    const size_t lane_a = ((size_t)(lane / TM) * Mp + lane % TM) * 16;
 
     // ---- loads of block b into slot b & 1 (direct-to-LDS, 16 bytes a lane)
     auto issue = [&](int b) {
         uint8_t *sl = lds + (b & 1) * Lay::SLOT;
-        // activation fragments f = wv, wv + NW, ...: lane i is row m0 + i % 32, octet i / 32
-        for (int f = wv; f < 16; f += NW) {
-            const size_t Fg = (size_t)16 * b + f;
-            dma16(ws.a + ((2 * Fg + lh) * Mp + m0 + lr) * 16, sl + Lay::A + 1024 * f);
-        }
-        // raw blocks: chunk c = 64 NW r + t is 16 bytes (part c % CPR) of column c / CPR
+        // activation fragments: TM / 2 instructions; lane i of instruction p
+        // loads octet-row j = 64 p + i (row j % TM of octet (j / TM) % 2 of
+        // fragment j / (2 TM)) to LDS offset 16 j
+        for (int p = wv; p < TM / 2; p += NW)
+            dma16(ws.a + ((size_t)(32 * b + (64 / TM) * p) * Mp + m0) * 16 + lane_a, sl + Lay::A + 1024 * p);
 #pragma unroll
         for (int r = 0; r < Lay::BROUNDS; r++) {
             const int c = 64 * NW * r + t;
@@ -223,229 +223,211 @@ __global__ __launch_bounds__(128 * NC) __attribute__((amdgpu_waves_per_eu(2))) v
             }
         }
         if (wv == NW - 1) {
-            dma16(ws.bs + ((size_t)b * Mp + m0) * 32 + 16 * lane, sl + Lay::BS);
-            if (lane < 8) dma16(ws.d8 + (size_t)b * Mp + m0 + 4 * lane, sl + Lay::D8);
+#pragma unroll
+            for (int i = 0; i < 2 * TM; i += 64)
+                if (i + lane < 2 * TM) dma16(ws.bs + ((size_t)b * Mp + m0) * 32 + 16 * (i + lane), sl + Lay::BS + 16 * i);
+            if (lane < TM / 4) dma16(ws.d8 + (size_t)b * Mp + m0 + 4 * lane, sl + Lay::D8);
         }
     };
 
-    // the wave's half of the lane sums is a compile-time constant of the
-    // loop below (its gathers and accumulators are indexed by it)
-    auto run = [&](auto half_c) {
-        constexpr int HALF = decltype(half_c)::value;
-        float sums[4][16];
-        float sumf[8];  // rows 8 half .. 8 half + 7 of the lane's 16 (Q4_K)
+    float sums[8][RT][4];
+    float sumf[RT][4];
 #pragma unroll
-        for (int r = 0; r < 16; r++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) sums[k][r] = 0.0f;
+        for (int r = 0; r < 4; r++) {
+            sumf[rt][r] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 8; r++) sumf[r] = 0.0f;
-        const f16x zero = {};
+            for (int k = 0; k < 8; k++) sums[k][rt][r] = 0.0f;
+        }
+    const f4x zero4 = {};
 
-        issue(0);
-        wait_vm_barrier<0>();
-        for (int b = 0; b < nblk; b++) {
-            if (b + 1 < nblk) issue(b + 1);
-            fence();
-            const uint8_t *sl = lds + (b & 1) * Lay::SLOT;
-            const uint8_t *rc = sl + Lay::B + (32 * ct + lr) * (CPR * 16);  // this lane's column
-            const uint8_t *ab = sl + Lay::A + 16 * lane;
-            // the lane's rows 8 (r / 4) + 4 lh + r % 4: their q8.d
-            float d8v[16];
+    issue(0);
+    wait_vm_barrier<0>();
+    for (int b = 0; b < nblk; b++) {
+        if (b + 1 < nblk) issue(b + 1);
+        fence();
+        const uint8_t *sl = lds + (b & 1) * Lay::SLOT;
+        const uint8_t *rc = sl + Lay::B + (16 * wv + lc) * (CPR * 16);  // this lane's column
+        // A operand of lane sum l, row tile rt: fragment 2 l + h, octet o', row 16 rt + lc
+        auto afrag = [&](int l, int rt) {
+            return *(const h8 *)(sl + Lay::A + (2 * l + hq) * 32 * TM + (oq * TM + 16 * rt + lc) * 16);
+        };
+        // q8.d of the lane's rows 16 rt + 4 lq + r
+        float d8v[RT][4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 v = *(const float4 *)(sl + Lay::D8 + (8 * q + 4 * lh) * 4);
-                d8v[4 * q] = v.x, d8v[4 * q + 1] = v.y, d8v[4 * q + 2] = v.z, d8v[4 * q + 3] = v.w;
+        for (int rt = 0; rt < RT; rt++) {
+            const float4 v = *(const float4 *)(sl + Lay::D8 + (16 * rt + 4 * lq) * 4);
+            d8v[rt][0] = v.x, d8v[rt][1] = v.y, d8v[rt][2] = v.z, d8v[rt][3] = v.w;
+        }
+        float dd[RT][4];
+        f4x S[2][RT];
+        // B operand of lane sum l (eight f16, the lane's octet), then the lane
+        // sum's MFMA per row tile
+        auto lane_mfma = [&](int l, const h8 &Bv, f4x (&acc)[RT]) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) acc[rt] = mfma16(afrag(l, rt), Bv, zero4);
+        };
+        auto epilogue = [&](int l, const f4x (&acc)[RT]) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) sums[l][rt][r] = __fadd_rn(sums[l][rt][r], __fmul_rn(dd[rt][r], acc[rt][r]));
+        };
+        if constexpr (!Q6) {
+            const u4 hd = *(const u4 *)rc;
+            const float dw = f16_lo(hd.x), dmw = f16_hi(hd.x);
+            const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
+            // qs chunk c = lq (groups 2 lq, 2 lq + 1) and its scale constants
+            const u4 qa = *(const u4 *)(rc + 16 + 32 * lq), qb = *(const u4 *)(rc + 32 + 32 * lq);
+            const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            uint32_t T[8];
+            q8k_gather(w, 0, *(uint32_t(*)[4])T);
+            q8k_gather(w, 1, *(uint32_t(*)[4])(T + 4));
+            // groups 2 lq and 2 lq + 1: the low form for lq < 2, the high form after
+            const int g4 = 2 * (lq & 1);
+            const uint32_t loA = (S0 >> (8 * (2 * lq))) & 63, loB = (S0 >> (8 * (2 * lq + 1))) & 63;
+            const uint32_t hiA = ((S2 >> (8 * g4)) & 0xF) | (((S0 >> (8 * g4 + 6)) & 3) << 4);
+            const uint32_t hiB = ((S2 >> (8 * (g4 + 1))) & 0xF) | (((S0 >> (8 * (g4 + 1) + 6)) & 3) << 4);
+            const float fa = (float)(lq < 2 ? loA : hiA), fb = (float)(lq < 2 ? loB : hiB);
+            const h2 lsc = h2_of(fa, fa), loff = h2_of(-1024.0f * fa, -1024.0f * fa);
+            const h2 hsc = h2_of(fb * 0.0625f, fb * 0.0625f), hoff = h2_of(-64.0f * fb, -64.0f * fb);
+            auto bop = [&](int l) {
+                uint32_t p[4];
+                q4k_pairs(T[l], p);
+                const h2 u0 = __builtin_elementwise_fma(as_h2(p[0]), lsc, loff);
+                const h2 u1 = __builtin_elementwise_fma(as_h2(p[1]), lsc, loff);
+                const h2 u2 = __builtin_elementwise_fma(as_h2(p[2]), hsc, hoff);
+                const h2 u3 = __builtin_elementwise_fma(as_h2(p[3]), hsc, hoff);
+                return h8{u0.x, u0.y, u1.x, u1.y, u2.x, u2.y, u3.x, u3.y};
+            };
+            lane_mfma(0, bop(0), S[0]);
+            // min sum: bsums g = 4 lq .. 4 lq + 3 of row 16 rt + lc times m[g / 2]
+            h4 mB;
+            {
+                const _Float16 m0v = (_Float16)(float)q4k_m(S1, S2, 2 * lq), m1v = (_Float16)(float)q4k_m(S1, S2, 2 * lq + 1);
+                mB = h4{m0v, m0v, m1v, m1v};
             }
-            float dd[16];
-            f16x S[2];
-            if constexpr (!Q6) {
-                const u4 hd = *(const u4 *)rc;
-                const float dw = f16_lo(hd.x), dmw = f16_hi(hd.x);
-                const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
-                // qs chunks c = 2 h + lh: the dwords HALF + 2i (bytes 8i + l of
-                // the wave's lanes l), and the chunk's groups' scale constants
-                uint32_t T0[4], T1[4];
-                h2 lsc[2], loff[2], hsc[2], hoff[2];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int c = 2 * h + lh;
-                    const uint32_t *q = (const uint32_t *)(rc + 16 + 32 * c) + HALF;
-                    transpose4(q[0], q[2], q[4], q[6], h ? T1 : T0);
-                    const float sa = h ? q4k_chunk_sc<1>(S0, S2, lh, 0) : q4k_chunk_sc<0>(S0, S2, lh, 0);
-                    const float sb = h ? q4k_chunk_sc<1>(S0, S2, lh, 1) : q4k_chunk_sc<0>(S0, S2, lh, 1);
-                    lsc[h] = h2_of(sa, sa);
-                    loff[h] = h2_of(-1024.0f * sa, -1024.0f * sa);
-                    hsc[h] = h2_of(sb * 0.0625f, sb * 0.0625f);
-                    hoff[h] = h2_of(-64.0f * sb, -64.0f * sb);
+            for (int rt = 0; rt < RT; rt++) {
+                const h4 bsA = *(const h4 *)(sl + Lay::BS + (16 * rt + lc) * 32 + 8 * lq);
+                const f4x mt = mfma16k16(bsA, mB, zero4);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    dd[rt][r] = __fmul_rn(d8v[rt][r], dw);
+                    sumf[rt][r] = __fsub_rn(sumf[rt][r], __fmul_rn(__fmul_rn(dmw, d8v[rt][r]), mt[r]));
                 }
-                // min sum on the MFMA: bsums g = 8 lh .. 8 lh + 7 of the lane's row times m[g / 2]
-                const h8 bsA = *(const h8 *)(sl + Lay::BS + lr * 32 + 16 * lh);
-                h8 mB;
+            }
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                if (l < 7) lane_mfma(l + 1, bop(l + 1), S[(l + 1) & 1]);
+                epilogue(l, S[l & 1]);
+            }
+        } else {
+            const float dw = f16_lo(*(const uint16_t *)(rc + 208));
+            // ql run 64 h + 32 o' = 32 q and qh run 32 h of the lane's octet q
+            const u4 la = *(const u4 *)(rc + 32 * lq), lb = *(const u4 *)(rc + 32 * lq + 16);
+            const u4 ha = *(const u4 *)(rc + 128 + 32 * hq), hb = *(const u4 *)(rc + 128 + 32 * hq + 16);
+            const uint32_t wl[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+            const uint32_t wq[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+            uint32_t QL[8], QH[8];
+            q8k_gather(wl, 0, *(uint32_t(*)[4])QL);
+            q8k_gather(wl, 1, *(uint32_t(*)[4])(QL + 4));
+            q8k_gather(wq, 0, *(uint32_t(*)[4])QH);
+            q8k_gather(wq, 1, *(uint32_t(*)[4])(QH + 4));
+            // pair scales: low-nibble slots sc[8h + 2o' + (0, 1)], high +4; split
+            // into (sc & ~1) and (sc & 1)
+            const uint2 scw = *(const uint2 *)(rc + 192 + 8 * hq);
+            h2 se[2], so[2];
+#pragma unroll
+            for (int part = 0; part < 2; part++) {
+                const uint32_t v = (part ? scw.y : scw.x) >> (16 * oq);
+                const int s0 = (int)(int8_t)(v & 0xFF), s1 = (int)(int8_t)((v >> 8) & 0xFF);
+                se[part] = h2_of((float)(s0 & ~1), (float)(s1 & ~1));
+                so[part] = h2_of((float)(s0 & 1), (float)(s1 & 1));
+            }
+            const h2 off = h2_of(-1056.0f, -1056.0f);
+            auto lane6 = [&](int l, f4x (&acc)[RT]) {
+                uint32_t ra, rb, p[4];
+                q6k_raw(QL[l], QH[l], oq, ra, rb);
+                q6k_pairs(ra, p);
+                q6k_pairs(rb, p + 2);
+                h8 B1, B2;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const _Float16 mv = (_Float16)(float)q4k_m(S1, S2, 4 * lh + k);
-                    mB[2 * k] = mv;
-                    mB[2 * k + 1] = mv;
-                }
-                const f16x mt = mfma(bsA, mB, zero);
-                auto lane_mfma = [&](int li, f16x &acc) {
-                    const int l = 4 * HALF + li;
-                    const h8 A0 = *(const h8 *)(ab + (2 * l) * 1024), A1 = *(const h8 *)(ab + (2 * l + 1) * 1024);
-                    uint32_t p0[4], p1[4];
-                    q4k_pairs(T0[li], p0);
-                    q4k_pairs(T1[li], p1);
-                    h8 B0, B1;
-#pragma unroll
-                    for (int k = 0; k < 2; k++) {
-                        const h2 u0 = __builtin_elementwise_fma(as_h2(p0[k]), lsc[0], loff[0]);
-                        const h2 u1 = __builtin_elementwise_fma(as_h2(p0[2 + k]), hsc[0], hoff[0]);
-                        const h2 v0 = __builtin_elementwise_fma(as_h2(p1[k]), lsc[1], loff[1]);
-                        const h2 v1 = __builtin_elementwise_fma(as_h2(p1[2 + k]), hsc[1], hoff[1]);
-                        B0[2 * k] = u0.x, B0[2 * k + 1] = u0.y, B0[4 + 2 * k] = u1.x, B0[4 + 2 * k + 1] = u1.y;
-                        B1[2 * k] = v0.x, B1[2 * k + 1] = v0.y, B1[4 + 2 * k] = v1.x, B1[4 + 2 * k + 1] = v1.y;
-                    }
-                    acc = mfma(A0, B0, zero);
-                    acc = mfma(A1, B1, acc);
-                };
-                lane_mfma(0, S[0]);
-#pragma unroll
-                for (int r = 0; r < 16; r++) dd[r] = __fmul_rn(d8v[r], dw);
-#pragma unroll
-                for (int r = 0; r < 8; r++) {
-                    const int rr = 8 * HALF + r;
-                    sumf[r] = __fsub_rn(sumf[r], __fmul_rn(__fmul_rn(dmw, d8v[rr]), mt[rr]));
+                    const h2 q = as_h2(p[k]) + off;  // raw - 32, exact
+                    const h2 e1 = q * se[k >> 1], e2 = q * so[k >> 1];
+                    B1[2 * k] = e1.x, B1[2 * k + 1] = e1.y;
+                    B2[2 * k] = e2.x, B2[2 * k + 1] = e2.y;
                 }
 #pragma unroll
-                for (int li = 0; li < 4; li++) {
-                    if (li < 3) lane_mfma(li + 1, S[(li + 1) & 1]);
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        sums[li][r] = __fadd_rn(sums[li][r], __fmul_rn(dd[r], S[li & 1][r]));
+                for (int rt = 0; rt < RT; rt++) {
+                    const h8 A = afrag(l, rt);
+                    acc[rt] = mfma16(A, B2, mfma16(A, B1, zero4));
                 }
-            } else {
-                const float dw = f16_lo(*(const uint16_t *)(rc + 208));
-                // ql run 64 h + 32 lh and qh run 32 h (both 32 bytes) of each half h,
-                // and the pair scales: low-nibble slots sc[8h + 2lh + (0, 1)], high +4,
-                // split into (sc & ~1) and (sc & 1)
-                uint32_t QL[2][4], QH[2][4];
-                h2 se[2][2], so[2][2];  // [h][low / high]
+            };
+            lane6(0, S[0]);
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const uint32_t *ql = (const uint32_t *)(rc + 64 * h + 32 * lh) + HALF;
-                    const uint32_t *qh = (const uint32_t *)(rc + 128 + 32 * h) + HALF;
-                    transpose4(ql[0], ql[2], ql[4], ql[6], QL[h]);
-                    transpose4(qh[0], qh[2], qh[4], qh[6], QH[h]);
-                    const uint2 scw = *(const uint2 *)(rc + 192 + 8 * h);
-                    const uint32_t lo = scw.x >> (16 * lh), hi = scw.y >> (16 * lh);
+            for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-                    for (int part = 0; part < 2; part++) {
-                        const uint32_t v = part ? hi : lo;
-                        const int s0 = (int)(int8_t)(v & 0xFF), s1 = (int)(int8_t)((v >> 8) & 0xFF);
-                        se[h][part] = h2_of((float)(s0 & ~1), (float)(s1 & ~1));
-                        so[h][part] = h2_of((float)(s0 & 1), (float)(s1 & 1));
-                    }
-                }
-                const h2 off = h2_of(-1056.0f, -1056.0f);
-                auto lane_mfma = [&](int li, f16x &acc) {
-                    const int l = 4 * HALF + li;
-                    acc = zero;
+                for (int r = 0; r < 4; r++) dd[rt][r] = __fmul_rn(d8v[rt][r], dw);
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const h8 A = *(const h8 *)(ab + (2 * l + h) * 1024);
-                        uint32_t ra, rb, p[4];
-                        q6k_raw(QL[h][li], QH[h][li], lh, ra, rb);
-                        q6k_pairs(ra, p);
-                        q6k_pairs(rb, p + 2);
-                        h8 B1, B2;
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            const h2 q = as_h2(p[k]) + off;  // raw - 32, exact
-                            const h2 e1 = q * se[h][k >> 1], e2 = q * so[h][k >> 1];
-                            B1[2 * k] = e1.x, B1[2 * k + 1] = e1.y;
-                            B2[2 * k] = e2.x, B2[2 * k + 1] = e2.y;
-                        }
-                        acc = mfma(A, B1, acc);
-                        acc = mfma(A, B2, acc);
-                    }
-                };
-                lane_mfma(0, S[0]);
-#pragma unroll
-                for (int r = 0; r < 16; r++) dd[r] = __fmul_rn(d8v[r], dw);
-#pragma unroll
-                for (int li = 0; li < 4; li++) {
-                    if (li < 3) lane_mfma(li + 1, S[(li + 1) & 1]);
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        sums[li][r] = __fadd_rn(sums[li][r], __fmul_rn(dd[r], S[li & 1][r]));
-                }
+            for (int l = 0; l < 8; l++) {
+                if (l < 7) lane6(l + 1, S[(l + 1) & 1]);
+                epilogue(l, S[l & 1]);
             }
-            // this wave's own loads of block b + 1 landed, then every wave's; the
-            // slot of block b is free for block b + 2
-            wait_vm_barrier<0>();
         }
+        // this wave's own loads of block b + 1 landed, then every wave's; the
+        // slot of block b is free for block b + 2
+        wait_vm_barrier<0>();
+    }
 
-        // s = sumf + sums[0] + ... + sums[7] (Q6_K: sumf is 0), in that order,
-        // exchanged through the (now idle) ring: X[c][w][r][lane], w = 0 the
-        // sumf rows of half 1, w = 1 the partial sum of half 0
-        float *X = (float *)lds;
-        auto xat = [&](int w, int r) { return X + (((ct * 2 + w) * 16 + r) * 64 + lane); };
-        if constexpr (HALF == 1)
+    // s = sumf + sums[0] + ... + sums[7] (Q6_K: sumf is 0), in that order
+    const int n = n0 + 16 * wv + lc;
 #pragma unroll
-            for (int r = 0; r < 8; r++) *xat(0, 8 + r) = sumf[r];
-        lds_barrier();
-        if constexpr (HALF == 0) {
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float s = r < 8 ? sumf[r] : *xat(0, r);
+        for (int r = 0; r < 4; r++) {
+            float s = sumf[rt][r];
 #pragma unroll
-                for (int k = 0; k < 4; k++) s = __fadd_rn(s, sums[k][r]);
-                *xat(1, r) = s;
-            }
+            for (int k = 0; k < 8; k++) s = __fadd_rn(s, sums[k][rt][r]);
+            const int m = m0 + 16 * rt + 4 * lq + r;
+            if (m < M && n < N) Y[(size_t)m * N + n] = s;
         }
-        lds_barrier();
-        if constexpr (HALF == 1) {
-            const int n = n0 + 32 * ct + lr;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float s = *xat(1, r);
-#pragma unroll
-                for (int k = 0; k < 4; k++) s = __fadd_rn(s, sums[k][r]);
-                const int m = m0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m < M && n < N) Y[(size_t)m * N + n] = s;
-            }
-        }
-
-    };
-    if (half)
-        run(std::integral_constant<int, 1>{});
-    else
-        run(std::integral_constant<int, 0>{});
 }
 
-template <bool Q6, int NC>
+template <bool Q6, int NW, int RT>
 hipError_t q8k_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
+    using Lay = Q8Lay<Q6, NW, RT>;
     const int K = w.dim_in, N = w.dim_out;
-    const int ntm = ws.Mp / 32, ntn = (N + 32 * NC - 1) / (32 * NC);
+    const int ntm = (M + Lay::TM - 1) / Lay::TM, ntn = (N + Lay::TN - 1) / Lay::TN;
     const int grid = 8 * ((ntm * ntn + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
-    const void *k = (const void *)gemm_q8k_kernel<Q6, NC>;
-    constexpr int lds = Q8Lay<Q6, NC>::BYTES;
-    hipError_t e = allow_lds(k, lds);
+    const void *k = (const void *)gemm_q8k_kernel<Q6, NW, RT>;
+    hipError_t e = allow_lds(k, Lay::BYTES);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemm_q8k_kernel<Q6, NC>), dim3(grid), dim3(128 * NC), lds, s, w.bytes, (uint32_t)w.row_bytes,
-                       K, N, M, ws, ntm, ntn, Y);
+    hipLaunchKernelGGL((gemm_q8k_kernel<Q6, NW, RT>), dim3(grid), dim3(64 * NW), Lay::BYTES, s, w.bytes,
+                       (uint32_t)w.row_bytes, K, N, M, ws, ntm, ntn, Y);
     return hipGetLastError();
 }
 
-// Column tiles per workgroup: four (eight waves) where the workgroups still
-// number at least one per CU, else fewer.
+// Rows per wave (and workgroup): 16 for M <= 16; 64 for M > 128 while the
+// 64 x 128 workgroup tiles number at least one per CU (eight waves, two per
+// SIMD: the B operands decoded once for 64 rows); else 32. Waves (16-column
+// tiles) per 32-row workgroup: six while the workgroups number two per CU,
+// else two while they number one per CU, else one.
+template <bool Q6, int RT>
+hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
+    const int N = w.dim_out, cus = 256, ntm = (M + 16 * RT - 1) / (16 * RT);
+    if (ntm * ((N + 95) / 96) >= 2 * cus) return q8k_launch<Q6, 6, RT>(w, M, ws, Y, s);
+    if (ntm * ((N + 31) / 32) >= cus) return q8k_launch<Q6, 2, RT>(w, M, ws, Y, s);
+    return q8k_launch<Q6, 1, RT>(w, M, ws, Y, s);
+}
 template <bool Q6>
 hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
-    const int ntm = ws.Mp / 32, N = w.dim_out, cus = 256;
-    auto groups = [&](int nc) { return ntm * ((N + 32 * nc - 1) / (32 * nc)); };
-    if (groups(4) >= cus) return q8k_launch<Q6, 4>(w, M, ws, Y, s);
-    if (groups(2) >= cus) return q8k_launch<Q6, 2>(w, M, ws, Y, s);
-    return q8k_launch<Q6, 1>(w, M, ws, Y, s);
+    const int N = w.dim_out, cus = 256;
+    if (M <= 16) return q8k_width<Q6, 1>(w, M, ws, Y, s);
+    if (M > 128 && ((M + 63) / 64) * ((N + 127) / 128) >= cus) return q8k_launch<Q6, 8, 4>(w, M, ws, Y, s);
+    return q8k_width<Q6, 2>(w, M, ws, Y, s);
 }
 
 __global__ __launch_bounds__(256) void q8k_fill_zero_kernel(float *__restrict__ Y, size_t n) {
@@ -456,7 +438,7 @@ __global__ __launch_bounds__(256) void q8k_fill_zero_kernel(float *__restrict__ 
 
 size_t gemm_q8k_ws_bytes(const WeightsView &w, int M) {
     if (M <= 1 || w.dim_out == 0 || w.dim_in == 0) return 0;
-    const int Mp = pad32(M), K = w.dim_in;
+    const int Mp = q8k_mp(M), K = w.dim_in;
     return q8_a_bytes(Mp, K) + q8_bs_bytes(Mp, K) + q8_d8_bytes(Mp, K);
 }
 
