@@ -120,6 +120,11 @@ def test_gemm_q6k_full_int8_scales():
     check_rows(S.Q6_K, w, K, N, X, run_gemm(S.Q6_K, w, K, N, X), "q6k int8 scales")
 
 
+# Outputs of test_gemm_dynamic_range that need the accumulation term (miss
+# 1e-4 + 1e-3|r| alone), per (format, M); every other case has none.
+STRICT_MISSES = {(S.Q6_K, 70): 1}
+
+
 @pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0])
 @pytest.mark.parametrize("M", [70, 12])
 def test_gemm_dynamic_range(dtype, M):
@@ -155,6 +160,10 @@ def test_gemm_dynamic_range(dtype, M):
     strict = np.argwhere(~(err <= 1e-4 + 1e-3 * np.abs(R)))
     log(f"dtype {dtype}: {len(strict)} of {err.size} outputs need the accumulation term; "
         f"worst err / sum|xw| = {float(np.max(err / np.maximum(A, 1e-300))):.3g}")
+    # every other output meets the strict gemv_quant bound: the exact count
+    # measured on these inputs (the kernels are deterministic) is the ceiling
+    ceiling = STRICT_MISSES.get((dtype, M), 0)
+    assert len(strict) <= ceiling, f"{len(strict)} outputs outside 1e-4 + 1e-3|r| (ceiling {ceiling})"
 
 
 @pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0])
