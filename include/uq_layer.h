@@ -136,6 +136,43 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
                                float *d_v_cache, size_t n_ctx_max, size_t pos, const float *d_x_in, float *d_l_out,
                                float *d_ws, size_t ws_floats, void *stream);
 
+/* Prefill: n_tokens tokens through a layer in one call, with the same
+ * results as n_tokens successive step calls, bit for bit (layer outputs,
+ * conv window, recurrent state, KV cache rows). The reference prefills token
+ * by token (crates/unltd-generation/src/greedy.rs:55-65); here every
+ * projection of the layer runs once over all the tokens as uq_gemm_q8k (each
+ * row equals the token's gemv_quant_q8k, quants.rs:474-515), the norms and
+ * the FFN's swiglu and residual adds over all the rows, and the recurrent
+ * part (conv, gdn_fused_step) or the attention core (q / k norms, IMROPE,
+ * causal attention) token by token with the step's own launches, since
+ * token t depends on tokens before it there. d_x_in and d_l_out are
+ * [n_tokens][n_embd]. The workspace (uq_layer_prefill_ws_floats; 256-byte
+ * aligned, as hipMalloc returns) holds the step's nodes (after the call:
+ * the last token's), n_tokens rows of each batched value and the q8k GEMM's
+ * workspace: nothing is allocated. n_tokens == 0 is a no-op.
+ * uq_layer_prefill_ws_floats takes the layer's weights (either kind, or
+ * both for a workspace shared by the two; the other may be NULL) and
+ * returns 0 for bad dims or n_tokens == 0. */
+size_t uq_layer_prefill_ws_floats(const uq_qwen35_dims *d, const uq_gdn_layer_w *gdn, const uq_attn_layer_w *attn,
+                                  size_t n_ctx_max, size_t n_tokens);
+
+/* n_tokens successive uq_gdn_layer_step_d calls (recr_layer,
+ * qwen35_forward.rs:333-543): tokens t = 0 .. n_tokens - 1 of d_x_in, the
+ * window and state carried through them as the step carries them. Errors as
+ * uq_gdn_layer_step_d. */
+uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, float *d_conv_win, float *d_state,
+                                 size_t n_tokens, const float *d_x_in, float *d_l_out, float *d_ws, size_t ws_floats,
+                                 void *stream);
+
+/* n_tokens successive uq_attn_layer_step_d calls (attn_layer, :546-710) at
+ * positions pos0 .. pos0 + n_tokens - 1: their cache rows are written and
+ * token t attends over rows 0 .. pos0 + t. A last position at or beyond
+ * n_ctx_max is UQ_ERR_ARG (the reference's "context full", :298-303);
+ * other errors as uq_attn_layer_step_d. */
+uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w, float *d_k_cache,
+                                  float *d_v_cache, size_t n_ctx_max, size_t pos0, size_t n_tokens,
+                                  const float *d_x_in, float *d_l_out, float *d_ws, size_t ws_floats, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,7 +5,12 @@
 // projections run as gemv_quant_q8k (the projections of one input share a
 // batched launch per format, bit-identical to separate ones); the glue is
 // uq_ops.hip. No allocation, no host copy, so a step can be captured in a
-// HIP graph.
+// HIP graph. The prefill forms take n_tokens tokens at once: their
+// projections run as uq_gemm_q8k over all the tokens (each row bit-identical
+// to the token's gemv_quant_q8k), the recurrent / attention cores per token
+// with the step's own launches, so the results equal n_tokens successive
+// steps bit for bit.
+#include <algorithm>
 #include <cmath>
 #include <climits>
 
@@ -201,6 +206,105 @@ uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const
                                   at(UQ_NODE_FFN_SWIGLU), at(UQ_NODE_FFN_OUT), at(UQ_NODE_RESIDUAL), l_out, s);
 }
 
+// The prefill workspace: the step's nodes (one token's, reused token by
+// token), then n_tokens rows of each batched array, then the q8k GEMM's
+// workspace; every part at a 64-float boundary.
+enum PrefillArr { P_XN, P_QKV, P_Z, P_BR, P_AL, P_FIN, P_QF, P_KR, P_GT, P_AO, P_RES, P_PN, P_G, P_U, P_H, P_FO, P_COUNT };
+size_t prefill_row(const Dims &D, int a) {
+    switch (a) {
+        case P_QKV: return D.ch;
+        case P_Z:
+        case P_FIN: return D.nv * D.hd;
+        case P_BR:
+        case P_AL: return D.nv;
+        case P_QF: return 2 * D.nh * D.ahd;
+        case P_KR: return D.nkv * D.ahd;
+        case P_GT: return D.nh * D.ahd;
+        case P_G:
+        case P_U:
+        case P_H: return D.nff;
+        default: return D.n;  // XN, AO, RES, PN, FO
+    }
+}
+size_t prefill_arr_offset(const Dims &D, size_t n_ctx_max, size_t nt, int a) {
+    size_t off = node_offset(D, n_ctx_max, UQ_NODE_COUNT);
+    for (int i = 0; i < a; i++) off += (prefill_row(D, i) * nt + 63) & ~(size_t)63;
+    return off;
+}
+// bytes of the q8k GEMM workspace for any projection of the layer at nt rows
+size_t prefill_gemm_bytes(const Dims &D, size_t nt, std::initializer_list<uq_weights> ws) {
+    size_t b = 0;
+    for (uq_weights w : ws)
+        if (wh(w)) b = std::max(b, uq::gemm_q8k_ws_bytes(uq::view(*wh(w)), (int)nt));
+    return b;
+}
+size_t prefill_floats(const Dims &D, size_t n_ctx_max, size_t nt, size_t gemm_bytes) {
+    return prefill_arr_offset(D, n_ctx_max, nt, P_COUNT) + ((gemm_bytes / 4 + 63) & ~(size_t)63);
+}
+
+// Projections of the prefill: Y[t] = gemv_quant_q8k(W, X[t]) for t < nt, on
+// the q8k GEMM kernels with the workspace carved from the layer workspace.
+struct PrefillCtx {
+    const char *fn;
+    hipStream_t s;
+    uint8_t *gws;
+    size_t gws_bytes;
+    uq_status gemm(uq_weights w, int nt, const float *X, float *Y) const {
+        return hip_st(uq::launch_gemm_q8k_ws(uq::view(*wh(w)), nt, X, Y, gws, gws_bytes, s), fn);
+    }
+};
+
+// residual = x_in + attn_out and its post_attention_norm, the FFN and l_out
+// = residual + ffn_out for nt tokens (the step's ffn_tail, its projections
+// as q8k GEMMs; swiglu and the adds are the same f32 operations)
+uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_dims *d, int nt, const float *x_in,
+                           uq_weights g, uq_weights u, uq_weights dn, const float *post_norm, float *const *A,
+                           float *l_out) {
+    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(A[P_PN], (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, nt, d->rms_eps, c.s,
+                                          A[P_AO], A[P_RES]),
+                  c.fn));
+    UQ_TRY(c.gemm(g, nt, A[P_PN], A[P_G]));
+    UQ_TRY(c.gemm(u, nt, A[P_PN], A[P_U]));
+    UQ_TRY(hip_st(uq::launch_swiglu(A[P_G], A[P_U], (size_t)nt * D.nff, A[P_H], c.s), c.fn));
+    UQ_TRY(c.gemm(dn, nt, A[P_H], A[P_FO]));
+    return hip_st(uq::launch_add(l_out, A[P_RES], A[P_FO], (size_t)nt * D.n, c.s), c.fn);
+}
+
+// Steps 4-6 of recr_layer for one token whose qkv projection is in the
+// window's last row: beta = sigmoid(beta_raw), gate = softplus(alpha +
+// dt_bias) * a (:405-419); the depthwise conv over [ring; qkv], silu, the
+// ring's shift (:427-454); the q and k parts l2-normalised per head
+// (:463-464); gdn_fused_step per v head, q/k head h % n_qk, the scale on the
+// output (:470-492); rmsnorm per head with ssm_norm times silu(z) into fin
+// (:495-511). Nodes of one token in ws.
+uq_status gdn_core(const char *fn, const Dims &D, const uq_qwen35_dims *d, const uq_gdn_layer_w *w, float *d_conv_win,
+                   float *d_state, float *ws, const float *beta_raw, const float *alpha, const float *z, float *fin,
+                   hipStream_t s) {
+    auto at = [&](int node) { return ws + node_offset(D, 0, node); };
+    const int hd = (int)D.hd, nv = (int)D.nv, nqk = (int)D.nqk, ch = (int)D.ch;
+    float *qc = at(UQ_NODE_CONV_SILU), *kc = qc + D.nqk * D.hd, *vc = kc + D.nqk * D.hd;
+    if (uq::conv_norm_ok(hd)) {  // one launch
+        UQ_TRY(hip_st(uq::launch_gdn_conv_norm(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, hd,
+                                               nqk, d->rms_eps, beta_raw, alpha, w->ssm_dt_bias, w->ssm_a,
+                                               at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s),
+                      fn));
+    } else {
+        UQ_TRY(hip_st(uq::launch_gdn_gates(beta_raw, alpha, w->ssm_dt_bias, w->ssm_a, at(UQ_NODE_BETA),
+                                           at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s),
+                      fn));
+        UQ_TRY(hip_st(uq::launch_conv_step(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, s),
+                      fn));
+        UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
+    }
+    const float scale = 1.0f / sqrtf((float)D.hd);
+    UQ_TRY(hip_st(uq::launch_gdn_step(d_state, at(UQ_NODE_GDN_OUT), qc, kc, vc, at(UQ_NODE_GATE), at(UQ_NODE_BETA), hd,
+                                      nv, scale, s, nqk),
+                  fn));
+    return hip_st(uq::launch_rmsnorm_rows(fin, hd, at(UQ_NODE_GDN_OUT), hd, w->ssm_norm, hd, nv, d->rms_eps, s, nullptr,
+                                          nullptr, z),
+                  fn);
+}
+
 }  // namespace
 
 extern "C" {
@@ -242,7 +346,6 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
     UQ_TRY(check_proj(fn, "ffn_down", w->ffn_down, D.nff, D.n));
     const hipStream_t s = (hipStream_t)stream;
     auto at = [&](int node) { return d_ws + node_offset(D, 0, node); };
-    const int hd = (int)D.hd, nv = (int)D.nv, nqk = (int)D.nqk, ch = (int)D.ch;
     float *qkv = d_conv_win + (D.ck - 1) * D.ch;  // the window's last row
 
     // 1-3) attn_norm (:352-360); qkv, z, beta, alpha: four q8k projections of
@@ -252,33 +355,8 @@ uq_status uq_gdn_layer_step_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, 
         float *const ys[4] = {qkv, at(UQ_NODE_Z), at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA)};
         UQ_TRY(norm_project_q8k(fn, D, w->attn_norm, d->rms_eps, d_x_in, at(UQ_NODE_ATTN_NORM), ws4, ys, 4, s));
     }
-    // beta = sigmoid(beta_raw); gate = softplus(alpha + dt_bias) * a (:405-419);
-    // 4) depthwise conv over [ring; qkv], silu, the ring's shift (:427-454);
-    // the q and k parts l2-normalised per head (:463-464)
-    float *qc = at(UQ_NODE_CONV_SILU), *kc = qc + D.nqk * D.hd, *vc = kc + D.nqk * D.hd;
-    if (uq::conv_norm_ok(hd)) {  // one launch
-        UQ_TRY(hip_st(uq::launch_gdn_conv_norm(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, hd,
-                                               nqk, d->rms_eps, at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA),
-                                               w->ssm_dt_bias, w->ssm_a, at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS),
-                                               at(UQ_NODE_GATE), nv, s),
-                      fn));
-    } else {
-        UQ_TRY(hip_st(uq::launch_gdn_gates(at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), w->ssm_dt_bias, w->ssm_a,
-                                           at(UQ_NODE_BETA), at(UQ_NODE_A_SOFTPLUS), at(UQ_NODE_GATE), nv, s),
-                      fn));
-        UQ_TRY(hip_st(uq::launch_conv_step(d_conv_win, w->ssm_conv1d, at(UQ_NODE_CONV_RAW), qc, (int)D.ck, ch, s),
-                      fn));
-        UQ_TRY(hip_st(uq::launch_l2norm(qc, hd, 2 * nqk, d->rms_eps, s), fn));
-    }
-    // 5) gdn_fused_step per v head, q/k head h % n_qk, scale on the output (:470-492)
-    const float scale = 1.0f / sqrtf((float)D.hd);
-    UQ_TRY(hip_st(uq::launch_gdn_step(d_state, at(UQ_NODE_GDN_OUT), qc, kc, vc, at(UQ_NODE_GATE), at(UQ_NODE_BETA), hd,
-                                      nv, scale, s, nqk),
-                  fn));
-    // 6) rmsnorm per head with ssm_norm, times silu(z): one launch (:495-511)
-    UQ_TRY(hip_st(uq::launch_rmsnorm_rows(at(UQ_NODE_FINAL), hd, at(UQ_NODE_GDN_OUT), hd, w->ssm_norm, hd, nv,
-                                          d->rms_eps, s, nullptr, nullptr, at(UQ_NODE_Z)),
-                  fn));
+    UQ_TRY(gdn_core(fn, D, d, w, d_conv_win, d_state, d_ws, at(UQ_NODE_BETA_RAW), at(UQ_NODE_ALPHA), at(UQ_NODE_Z),
+                    at(UQ_NODE_FINAL), s));
     // 7) ssm_out (:514-521); the residual is formed with the next norm
     UQ_TRY(uq_gemv_q8k(w->ssm_out, at(UQ_NODE_FINAL), at(UQ_NODE_ATTN_OUT), stream));
     // 8) residual, FFN and l_out (:524-536)
@@ -339,6 +417,126 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
     UQ_TRY(uq_gemv_q8k(w->attn_output, at(UQ_NODE_GATED), at(UQ_NODE_ATTN_OUT), stream));
     return ffn_tail(fn, D, d, d_x_in, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, d_ws, n_ctx_max,
                     d_l_out, s);
+}
+
+size_t uq_layer_prefill_ws_floats(const uq_qwen35_dims *d, const uq_gdn_layer_w *gdn, const uq_attn_layer_w *attn,
+                                  size_t n_ctx_max, size_t n_tokens) {
+    Dims D;
+    if (check_dims("layer_prefill_ws_floats", d, &D) != UQ_OK || n_tokens == 0 || n_tokens > (size_t)INT_MAX) return 0;
+    size_t b = 0;
+    if (gdn)
+        b = std::max(b, prefill_gemm_bytes(D, n_tokens, {gdn->attn_qkv, gdn->attn_gate, gdn->ssm_beta, gdn->ssm_alpha,
+                                                         gdn->ssm_out, gdn->ffn_gate, gdn->ffn_up, gdn->ffn_down}));
+    if (attn)
+        b = std::max(b, prefill_gemm_bytes(D, n_tokens, {attn->attn_q, attn->attn_k, attn->attn_v, attn->attn_output,
+                                                         attn->ffn_gate, attn->ffn_up, attn->ffn_down}));
+    return prefill_floats(D, n_ctx_max, n_tokens, b);
+}
+
+uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *w, float *d_conv_win, float *d_state,
+                                 size_t n_tokens, const float *d_x_in, float *d_l_out, float *d_ws, size_t ws_floats,
+                                 void *stream) {
+    const char *fn = "gdn_layer_prefill_d";
+    Dims D;
+    UQ_TRY(check_dims(fn, d, &D));
+    if (!w || !d_conv_win || !d_state || !d_x_in || !d_l_out || !d_ws || !w->attn_norm || !w->ssm_dt_bias ||
+        !w->ssm_a || !w->ssm_conv1d || !w->ssm_norm || !w->post_attention_norm)
+        return set_error(UQ_ERR_ARG, "%s: null pointer", fn);
+    if (n_tokens == 0) return UQ_OK;
+    if (n_tokens > (size_t)INT_MAX) return set_error(UQ_ERR_ARG, "%s: n_tokens %zu above INT_MAX", fn, n_tokens);
+    UQ_TRY(check_proj(fn, "attn_qkv", w->attn_qkv, D.n, D.ch));
+    UQ_TRY(check_proj(fn, "attn_gate", w->attn_gate, D.n, D.nv * D.hd));
+    UQ_TRY(check_proj(fn, "ssm_beta", w->ssm_beta, D.n, D.nv));
+    UQ_TRY(check_proj(fn, "ssm_alpha", w->ssm_alpha, D.n, D.nv));
+    UQ_TRY(check_proj(fn, "ssm_out", w->ssm_out, D.nv * D.hd, D.n));
+    UQ_TRY(check_proj(fn, "ffn_gate", w->ffn_gate, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_up", w->ffn_up, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_down", w->ffn_down, D.nff, D.n));
+    const size_t need = uq_layer_prefill_ws_floats(d, w, nullptr, 0, n_tokens);
+    if (ws_floats < need) return set_error(UQ_ERR_ARG, "%s: workspace of %zu floats below %zu", fn, ws_floats, need);
+    const int nt = (int)n_tokens;
+    float *A[P_COUNT];
+    for (int a = 0; a < P_COUNT; a++) A[a] = d_ws + prefill_arr_offset(D, 0, n_tokens, a);
+    const PrefillCtx c{fn, (hipStream_t)stream, (uint8_t *)(d_ws + prefill_arr_offset(D, 0, n_tokens, P_COUNT)),
+                       (need - prefill_arr_offset(D, 0, n_tokens, P_COUNT)) * 4};
+    // 1-3) attn_norm of every token (:352-360), then qkv, z, beta, alpha of all
+    // of them (:363-403)
+    UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
+    UQ_TRY(c.gemm(w->attn_qkv, nt, A[P_XN], A[P_QKV]));
+    UQ_TRY(c.gemm(w->attn_gate, nt, A[P_XN], A[P_Z]));
+    UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR]));
+    UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL]));
+    // 4-6) the recurrent part token by token: the token's qkv into the
+    // window's last row, then the step's launches
+    float *qkv = d_conv_win + (D.ck - 1) * D.ch;
+    const size_t vw = D.nv * D.hd;
+    for (int t = 0; t < nt; t++) {
+        UQ_TRY(hip_st(hipMemcpyAsync(qkv, A[P_QKV] + (size_t)t * D.ch, D.ch * 4, hipMemcpyDeviceToDevice, c.s), fn));
+        UQ_TRY(gdn_core(fn, D, d, w, d_conv_win, d_state, d_ws, A[P_BR] + (size_t)t * D.nv, A[P_AL] + (size_t)t * D.nv,
+                        A[P_Z] + t * vw, A[P_FIN] + t * vw, c.s));
+    }
+    // 7) ssm_out of all tokens (:514-521); 8) residual, FFN, l_out (:524-536)
+    UQ_TRY(c.gemm(w->ssm_out, nt, A[P_FIN], A[P_AO]));
+    return ffn_tail_prefill(c, D, d, nt, d_x_in, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, A,
+                            d_l_out);
+}
+
+uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w, float *d_k_cache,
+                                  float *d_v_cache, size_t n_ctx_max, size_t pos0, size_t n_tokens,
+                                  const float *d_x_in, float *d_l_out, float *d_ws, size_t ws_floats, void *stream) {
+    const char *fn = "attn_layer_prefill_d";
+    Dims D;
+    UQ_TRY(check_dims(fn, d, &D));
+    if (!w || !d_k_cache || !d_v_cache || !d_x_in || !d_l_out || !d_ws || !w->attn_norm || !w->attn_q_norm ||
+        !w->attn_k_norm || !w->post_attention_norm)
+        return set_error(UQ_ERR_ARG, "%s: null pointer", fn);
+    if (n_tokens == 0) return UQ_OK;
+    if (n_tokens > (size_t)INT_MAX || pos0 >= n_ctx_max || n_tokens > n_ctx_max - pos0)
+        return set_error(UQ_ERR_ARG, "%s: context full: positions %zu..%zu, n_ctx_max %zu", fn, pos0,
+                         pos0 + n_tokens - 1, n_ctx_max);
+    if (n_ctx_max > (size_t)uq::softmax_max_len() || n_ctx_max * D.nh > ((size_t)1 << 31))
+        return set_error(UQ_ERR_ARG, "%s: n_ctx_max %zu above the attention's limit", fn, n_ctx_max);
+    const size_t kv_len = D.nkv * D.ahd;
+    UQ_TRY(check_proj(fn, "attn_q", w->attn_q, D.n, 2 * D.nh * D.ahd));
+    UQ_TRY(check_proj(fn, "attn_k", w->attn_k, D.n, kv_len));
+    UQ_TRY(check_proj(fn, "attn_v", w->attn_v, D.n, kv_len));
+    UQ_TRY(check_proj(fn, "attn_output", w->attn_output, D.nh * D.ahd, D.n));
+    UQ_TRY(check_proj(fn, "ffn_gate", w->ffn_gate, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_up", w->ffn_up, D.n, D.nff));
+    UQ_TRY(check_proj(fn, "ffn_down", w->ffn_down, D.nff, D.n));
+    const size_t need = uq_layer_prefill_ws_floats(d, nullptr, w, n_ctx_max, n_tokens);
+    if (ws_floats < need) return set_error(UQ_ERR_ARG, "%s: workspace of %zu floats below %zu", fn, ws_floats, need);
+    const int nt = (int)n_tokens, ahd = (int)D.ahd, nh = (int)D.nh, nkv = (int)D.nkv;
+    float *A[P_COUNT];
+    for (int a = 0; a < P_COUNT; a++) A[a] = d_ws + prefill_arr_offset(D, n_ctx_max, n_tokens, a);
+    const PrefillCtx c{fn, (hipStream_t)stream,
+                       (uint8_t *)(d_ws + prefill_arr_offset(D, n_ctx_max, n_tokens, P_COUNT)),
+                       (need - prefill_arr_offset(D, n_ctx_max, n_tokens, P_COUNT)) * 4};
+    auto at = [&](int node) { return d_ws + node_offset(D, n_ctx_max, node); };
+    // 1-3) attn_norm of every token (:563-571); q|gate, k of all of them, and
+    // v straight into the cache rows pos0 .. pos0 + n_tokens - 1 (:625-632)
+    UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
+    UQ_TRY(c.gemm(w->attn_q, nt, A[P_XN], A[P_QF]));
+    UQ_TRY(c.gemm(w->attn_k, nt, A[P_XN], A[P_KR]));
+    UQ_TRY(c.gemm(w->attn_v, nt, A[P_XN], d_v_cache + pos0 * kv_len));
+    // 4-6) token by token, as the step: q / k norms and IMROPE (k into its
+    // cache row), then attention over rows 0..pos and the gate (:585-684)
+    const size_t qf = 2 * D.nh * D.ahd, gw = D.nh * D.ahd;
+    for (int t = 0; t < nt; t++) {
+        const size_t pos = pos0 + t;
+        UQ_TRY(hip_st(uq::launch_attn_qk_prep(A[P_QF] + t * qf, at(UQ_NODE_Q), A[P_KR] + t * kv_len,
+                                              d_k_cache + pos * kv_len, w->attn_q_norm, w->attn_k_norm, ahd, nh, nkv,
+                                              (int)d->n_rot, d->theta_scale, pos, d->rms_eps, c.s),
+                      fn));
+        UQ_TRY(hip_st(uq::launch_attn_decode(at(UQ_NODE_ATTN), at(UQ_NODE_SOFT), at(UQ_NODE_Q), d_k_cache, d_v_cache,
+                                             (int)pos + 1, nkv, ahd, nh / nkv, d->kq_scale, c.s,
+                                             A[P_QF] + t * qf + ahd, 2 * ahd, A[P_GT] + t * gw),
+                      fn));
+    }
+    // 7) attn_output of all tokens (:686-693); residual, FFN, l_out (:696-704)
+    UQ_TRY(c.gemm(w->attn_output, nt, A[P_GT], A[P_AO]));
+    return ffn_tail_prefill(c, D, d, nt, d_x_in, w->ffn_gate, w->ffn_up, w->ffn_down, w->post_attention_norm, A,
+                            d_l_out);
 }
 
 }  // extern "C"

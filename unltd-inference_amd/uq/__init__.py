@@ -138,6 +138,9 @@ SIGNATURES = {
     "uq_layer_node_at": ([_P, _S, C.c_int, _P, _P], _I),
     "uq_gdn_layer_step_d": ([_P, _P, _P, _P, _P, _P, _P, _S, _P], _I),
     "uq_attn_layer_step_d": ([_P, _P, _P, _P, _S, _S, _P, _P, _P, _S, _P], _I),
+    "uq_layer_prefill_ws_floats": ([_P, _P, _P, _S, _S], _S),
+    "uq_gdn_layer_prefill_d": ([_P, _P, _P, _P, _S, _P, _P, _P, _S, _P], _I),
+    "uq_attn_layer_prefill_d": ([_P, _P, _P, _P, _S, _S, _S, _P, _P, _P, _S, _P], _I),
 }
 
 

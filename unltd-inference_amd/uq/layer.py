@@ -1,7 +1,8 @@
 """Device-resident Qwen3.5 layers of libuq (include/uq_layer.h): one token
 through a GatedDeltaNet layer (Qwen35Forward::recr_layer,
 qwen35_forward.rs:333-543) or a full-attention layer (attn_layer,
-:546-710), each with its FFN, on device buffers and a stream."""
+:546-710), each with its FFN, on device buffers and a stream; and the
+prefill forms, n tokens in one call with the results of n steps."""
 from __future__ import annotations
 
 import ctypes as C
@@ -106,3 +107,28 @@ def attn_step(d: Dims, w: AttnWeights, k_cache: DeviceArray, v_cache: DeviceArra
     cw = w._c()
     _check(lib().uq_attn_layer_step_d(C.addressof(d), C.addressof(cw), k_cache.ptr, v_cache.ptr, n_ctx_max, pos,
                                       x_in.ptr, l_out.ptr, ws.ptr, ws.nbytes // 4, stream))
+
+
+def prefill_ws_floats(d: Dims, n_tokens: int, gdn: GdnWeights | None = None, attn: AttnWeights | None = None,
+                      n_ctx_max: int = 0) -> int:
+    """uq_layer_prefill_ws_floats: floats of a prefill workspace for n_tokens."""
+    g = gdn._c() if gdn is not None else None
+    a = attn._c() if attn is not None else None
+    return lib().uq_layer_prefill_ws_floats(C.addressof(d), C.addressof(g) if g is not None else None,
+                                            C.addressof(a) if a is not None else None, n_ctx_max, n_tokens)
+
+
+def gdn_prefill(d: Dims, w: GdnWeights, conv_win: DeviceArray, state: DeviceArray, n_tokens: int, x_in: DeviceArray,
+                l_out: DeviceArray, ws: DeviceArray, stream=None) -> None:
+    """uq_gdn_layer_prefill_d: x_in, l_out are [n_tokens][n_embd]"""
+    cw = w._c()
+    _check(lib().uq_gdn_layer_prefill_d(C.addressof(d), C.addressof(cw), conv_win.ptr, state.ptr, n_tokens, x_in.ptr,
+                                        l_out.ptr, ws.ptr, ws.nbytes // 4, stream))
+
+
+def attn_prefill(d: Dims, w: AttnWeights, k_cache: DeviceArray, v_cache: DeviceArray, n_ctx_max: int, pos0: int,
+                 n_tokens: int, x_in: DeviceArray, l_out: DeviceArray, ws: DeviceArray, stream=None) -> None:
+    """uq_attn_layer_prefill_d: positions pos0 .. pos0 + n_tokens - 1"""
+    cw = w._c()
+    _check(lib().uq_attn_layer_prefill_d(C.addressof(d), C.addressof(cw), k_cache.ptr, v_cache.ptr, n_ctx_max, pos0,
+                                         n_tokens, x_in.ptr, l_out.ptr, ws.ptr, ws.nbytes // 4, stream))
