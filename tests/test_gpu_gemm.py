@@ -92,14 +92,15 @@ def test_gemm_q4k_shapes(K, N, M):
 
 @pytest.mark.parametrize("dtype", [S.Q6_K, S.Q8_0])
 @pytest.mark.parametrize("K,N,M", [(4096, 12288, 512), (12288, 4096, 300), (12288, 4096, 100), (12288, 4096, 8),
-                                   (4096, 1000, 70),
+                                   (4096, 12288, 8), (4096, 12288, 20), (4096, 1000, 70),
                                    (256, 200, 3), (1024, 130, 65), (4352, 384, 33), (12288, 1000, 29)])
 def test_gemm_q6k_q8_0(dtype, K, N, M):
     """Q6_K and Q8_0 on the MFMA: the prefill shape (N = 12288, K = 4096,
     M = 512; Q8_0 on 256 x 96 tiles), the down-projection shape (K = 12288)
     at M = 300, 100 and 8, and small / ragged shapes (M <= 32 runs the
-    loader-wave kernel: 128-column workgroups, tiles past N, K split into
-    ranges of one or two blocks at 12288 x 1000)."""
+    loader-wave kernels: 128- or 96-column workgroups, 96 at N = 12288 and
+    K = 4096 for M = 8 and 20, tiles past N, K split into ranges of one or
+    two blocks at 12288 x 1000)."""
     log(f"gemm dtype={dtype} K={K} N={N} M={M}")
     w = S.weights(dtype, N, K, seed=K + N + M + dtype)
     X = S.activations(K, seed=M + dtype, rows=M).reshape(M, K)

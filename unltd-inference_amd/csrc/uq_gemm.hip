@@ -1143,11 +1143,16 @@ typedef float f4x __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f4x mfma16(h8 a, h8 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 __device__ __forceinline__ f4x mfma16k16(h4 a, h4 b, f4x c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-template <class BP, int CW>
+// JT 16-column tiles per compute wave (2, or 1 with twice the compute waves
+// over the same columns: two waves per SIMD where the LDS ring allows one
+// workgroup per CU).
+template <class BP, int CW, int JT>
 __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_eu((CW + SK_LW + 3) / 4))) void gemm_m16_kernel(
     const uint8_t *__restrict__ W, uint32_t row_bytes, int K, int N, int M, GemmWs ws, int ncg, int ks,
     float *__restrict__ Y, double *__restrict__ Ypart, size_t part_stride) {
-    using Sh = SkShape<BP, CW, true>;
+    static_assert(JT == 1 || JT == 2, "tiles per wave");
+    constexpr int CG = CW * JT / 2;  // 32-column groups of the workgroup (the loader's shape)
+    using Sh = SkShape<BP, CG, true>;
     constexpr int SK_SLOT = Sh::SLOT;
     __shared__ __align__(16) uint8_t ring[SK_RING * SK_SLOT];
     const int lane = threadIdx.x & 63, lc = lane & 15, lq = lane >> 4;
@@ -1160,14 +1165,14 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
 
     if (wv >= CW) {
         if (wv == CW)
-            sk_loader<BP, CW, true, 0>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+            sk_loader<BP, CG, true, 0>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
         else
-            sk_loader<BP, CW, true, 1>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
+            sk_loader<BP, CG, true, 1>(W, row_bytes, N, M, ws, cg, kb0, nblk, lane, ring);
         return;
     }
 
-    // compute wave wv: columns n0 + 16 j + lc (j = 0, 1)
-    const int n0 = (cg * CW + wv) * 32;
+    // compute wave wv: columns n0 + 16 j + lc (j < JT)
+    const int n0 = (cg * CW + wv) * 16 * JT;
     const int ar = min(lc, M - 1);
     const auto rg = buf_rsrc(ws.g, (uint32_t)((size_t)M * (K / 256) * 32));
     const uint32_t goff = (uint32_t)ar * 32u + 8u * lq;
@@ -1177,9 +1182,9 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
         return __builtin_bit_cast(h4, v);
     };
     const f4x zero4 = {};
-    double C[2][4];
+    double C[JT][4];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < JT; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++) C[j][r] = 0.0;
     h4 gm = {};
@@ -1188,7 +1193,9 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
 
     for (int b = 0; b < nblk; b++) {
         const uint8_t *slot = ring + (b % SK_RING) * SK_SLOT;
-        const uint8_t *rc[2] = {slot + (wv * 32 + lc) * (16 * BP::CPR), slot + (wv * 32 + 16 + lc) * (16 * BP::CPR)};
+        const uint8_t *rc[JT];
+#pragma unroll
+        for (int j = 0; j < JT; j++) rc[j] = slot + (wv * 16 * JT + 16 * j + lc) * (16 * BP::CPR);
         // the lane's rows 4 lq .. 4 lq + 3: block scales (rows past M read a
         // neighbour's value; those outputs are not stored)
         const float4 sv4 = *(const float4 *)(slot + Sh::SC + 16 * lq);
@@ -1198,12 +1205,14 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
             xa = *(const h8 *)(slot + Sh::AHI + o);
             xl = *(const h8 *)(slot + Sh::ALO + o);
         };
-        f4x P[2] = {zero4, zero4};
-        if constexpr (std::is_same<BP, GQ4K>::value) {
-            u4 h[2];
-            uint2 q[2][4];
+        f4x P[JT];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < JT; j++) P[j] = zero4;
+        if constexpr (std::is_same<BP, GQ4K>::value) {
+            u4 h[JT];
+            uint2 q[JT][4];
+#pragma unroll
+            for (int j = 0; j < JT; j++) {
                 h[j] = *(const u4 *)rc[j];
 #pragma unroll
                 for (int st = 0; st < 4; st++) q[j][st] = *(const uint2 *)(rc[j] + 16 + 32 * st + 8 * lq);
@@ -1213,22 +1222,22 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 // sub-step st: groups 2 st (low nibbles: 32-k step 2 st) and 2 st + 1 (high: 2 st + 1)
-                h8 Blo[2], Bhi[2];
+                h8 Blo[JT], Bhi[JT];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < JT; j++) {
                     const float sa = (float)GQ4K::sc_of(h[j].y, h[j].w, 2 * st), sb = (float)GQ4K::sc_of(h[j].y, h[j].w, 2 * st + 1);
                     sk_dequant(q[j][st], hh(sa), hh(-1024.0f * sa), hh(sb * 0.0625f), hh(-64.0f * sb), Blo[j], Bhi[j]);
                 }
                 h8 xa, xl;
                 afrag(2 * st, xa, xl);
 #pragma unroll
-                for (int j = 0; j < 2; j++) P[j] = mfma16(xl, Blo[j], mfma16(xa, Blo[j], P[j]));
+                for (int j = 0; j < JT; j++) P[j] = mfma16(xl, Blo[j], mfma16(xa, Blo[j], P[j]));
                 afrag(2 * st + 1, xa, xl);
 #pragma unroll
-                for (int j = 0; j < 2; j++) P[j] = mfma16(xl, Bhi[j], mfma16(xa, Bhi[j], P[j]));
+                for (int j = 0; j < JT; j++) P[j] = mfma16(xl, Bhi[j], mfma16(xa, Bhi[j], P[j]));
             }
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
+            for (int j = 0; j < JT; j++) {
                 // min term: group sums g = (4 lq + 0..3) % 8 (hi for lq < 2, lo after) times -dmin*m_g hi, then lo
                 const float dmin = f16_hi(h[j].x), d = f16_lo(h[j].x);
                 h4 bh, bl;
@@ -1255,10 +1264,10 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
             const int q1 = lq >> 1, q0 = lq & 1;
             const uint32_t bm = 0x00FF00FFu, mag = 0x64006400u;
             const h2 off = hh(-1056.0f);
-            u4 scv[2];
-            float dv[2];
+            u4 scv[JT];
+            float dv[JT];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
+            for (int j = 0; j < JT; j++) {
                 scv[j] = *(const u4 *)(rc[j] + 192);
                 dv[j] = f16_lo(*(const uint16_t *)(rc[j] + 208));
             }
@@ -1268,7 +1277,7 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
                 h8 xa, xl;
                 afrag(t, xa, xl);
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < JT; j++) {
                     const uint2 A = *(const uint2 *)(rc[j] + 64 * hb + 32 * v + 16 * q1 + 8 * q0);
                     const uint2 Cq = *(const uint2 *)(rc[j] + 128 + 32 * hb + 16 * q1 + 8 * q0);
                     const uint32_t scw = (&scv[j].x)[t >> 1] >> (16 * (t & 1));  // sc[2t], sc[2t + 1]
@@ -1290,7 +1299,7 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < JT; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) C[j][r] = fma((double)dv[j] * (double)sv[r], (double)P[j][r], C[j][r]);
         } else {
@@ -1303,7 +1312,7 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
                 h8 xa, xl;
                 afrag(t, xa, xl);
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < JT; j++) {
                     const uint8_t *blk = rc[j] + 34 * t;
                     const _Float16 df = __builtin_bit_cast(_Float16, *(const uint16_t *)blk);
                     const h2 d2 = h2{df, df};
@@ -1335,7 +1344,7 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < JT; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) C[j][r] = fma((double)sv[r], (double)P[j][r], C[j][r]);
         }
@@ -1344,7 +1353,7 @@ __global__ __launch_bounds__(64 * (CW + SK_LW)) __attribute__((amdgpu_waves_per_
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < JT; j++) {
         const int n = n0 + 16 * j + lc;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -1384,13 +1393,22 @@ Plan plan_for(uq_dtype dt, int M, int N, int K) {
     // takes 256 x 96 tiles (eight waves down the rows, all on the same
     // 96 columns), so that M = 512, N = 12288 makes 256 tiles, one per CU,
     // where 128 x 128 made 384 (a second round on half the chip). M <= 32
-    // runs the loader-wave kernel over the same column groups (256 for
-    // Q4_K, 128 otherwise), so the K split below holds for it too.
+    // runs the loader-wave kernels over the same column groups (256 for
+    // Q4_K, 128 or 96 otherwise), so the K split below holds for them too.
     const bool q4 = dt == UQ_Q4_K;
     p.wm = M > 64 ? 4 : (M > 32 || !q4) ? 2 : 1;
     if (dt == UQ_Q8_0 && M > 128) p.wm = 8;  // 256 x 96: 256 tiles at M = 512, N = 12288
     p.tm = 32 * p.wm;
     p.tn = q4 ? (p.wm == 4 ? 192 : 256) : p.wm == 8 ? 96 : 128;
+    if (M <= 32 && !q4) {
+        // the loader-wave kernels on 128 or 96 columns per workgroup, whichever
+        // puts more workgroups (column groups x K ranges) on the CUs
+        auto wgs = [&](int tn) {
+            const int t = (N + tn - 1) / tn;
+            return std::min(t * std::max(1, std::min(K / 256, gemm_cus() / t)), gemm_cus());
+        };
+        if (wgs(96) > wgs(128)) p.tn = 96;
+    }
     const int tiles = ((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
     p.ks = std::max(1, std::min(K / 256, gemm_cus() / std::max(tiles, 1)));
     return p;
@@ -1426,8 +1444,11 @@ hipError_t skinny_launch(const WeightsView &w, int M, const GemmWs &ws, float *Y
     const int ncg = (N + SkShape<BP, CW, false>::COLS - 1) / SkShape<BP, CW, false>::COLS;
     const int grid = 8 * ((ncg * ks + 7) / 8);  // whole rounds of 8 XCDs; surplus slots exit
     const size_t ps = part_stride(M, N);
+    // M <= 16: the 16-row kernel over the same columns; with four 32-column
+    // groups (Q6_K, Q8_0) as eight waves of one 16-column tile each
+    constexpr int CW16 = CW >= 8 ? CW : 2 * CW, JT16 = CW >= 8 ? 2 : 1;
     if (M <= SK_MA)
-        hipLaunchKernelGGL((gemm_m16_kernel<BP, CW>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
+        hipLaunchKernelGGL((gemm_m16_kernel<BP, CW16, JT16>), dim3(grid), dim3(64 * (CW16 + SK_LW)), 0, s, w.bytes,
                            (uint32_t)w.row_bytes, K, N, M, ws, ncg, ks, Y, part, ps);
     else
         hipLaunchKernelGGL((gemm_skinny_kernel<BP, CW, false>), dim3(grid), dim3(64 * (CW + SK_LW)), 0, s, w.bytes,
@@ -1451,7 +1472,8 @@ hipError_t gemm_shape(const WeightsView &w, const Plan &p, int M, const GemmWs &
         if constexpr (std::is_same<BP, GQ80>::value)
             if (p.wm == 8) return gemm_launch<BP, 8, 1, 3, false, 4>(w, M, ws, Y, part, p.ks, s);  // 256 x 96
         if (p.wm == 4) return gemm_launch<BP, 4, 2, 2, true, 8>(w, M, ws, Y, part, p.ks, s);   // 128 x 128
-        if (M <= 32) return skinny_launch<BP, 4>(w, M, ws, Y, part, p.ks, s);                 // M <= 32
+        if (M <= 32)  // M <= 32: 128 or 96 columns per workgroup
+            return p.tn == 96 ? skinny_launch<BP, 3>(w, M, ws, Y, part, p.ks, s) : skinny_launch<BP, 4>(w, M, ws, Y, part, p.ks, s);
         return gemm_launch<BP, 2, 4, 1, true, 16>(w, M, ws, Y, part, p.ks, s);                 // 64 x 128
     }
 }
