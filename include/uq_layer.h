@@ -143,13 +143,16 @@ uq_status uq_attn_layer_step_d(const uq_qwen35_dims *d, const uq_attn_layer_w *w
  * projection of the layer runs once over all the tokens as uq_gemm_q8k (each
  * row equals the token's gemv_quant_q8k, quants.rs:474-515), the norms and
  * the FFN's swiglu and residual adds over all the rows, and the recurrent
- * part (conv, gdn_fused_step) or the attention core (q / k norms, IMROPE,
- * causal attention) token by token with the step's own launches, since
- * token t depends on tokens before it there. d_x_in and d_l_out are
- * [n_tokens][n_embd]. The workspace (uq_layer_prefill_ws_floats; 256-byte
- * aligned, as hipMalloc returns) holds the step's nodes (after the call:
- * the last token's), n_tokens rows of each batched value and the q8k GEMM's
- * workspace: nothing is allocated. n_tokens == 0 is a no-op.
+ * part (conv, norms, gates, gdn_fused_step, gated norm) or the attention
+ * core (q / k norms, IMROPE, causal attention) token after token, since
+ * token t depends on tokens before it there: the recurrent part in one
+ * launch over all the tokens for head_dim_linear 64 or 128 (else with the
+ * step's launches per token), the attention core with the step's launches.
+ * d_x_in and d_l_out are [n_tokens][n_embd]. The workspace
+ * (uq_layer_prefill_ws_floats; 256-byte aligned, as hipMalloc returns) holds
+ * the step's node space (its contents after the call unspecified), n_tokens
+ * rows of each batched value and the q8k GEMM's workspace: nothing is
+ * allocated. n_tokens == 0 is a no-op.
  * uq_layer_prefill_ws_floats takes the layer's weights (either kind, or
  * both for a workspace shared by the two; the other may be NULL) and
  * returns 0 for bad dims or n_tokens == 0. */

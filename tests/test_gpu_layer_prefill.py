@@ -7,10 +7,13 @@ The reference prefills token by token (greedy.rs:55-65), so the step
 (itself checked node by node against the oracle's recr_layer / attn_layer in
 tests/test_gpu_layers.py) is the reference here. The prefill runs every
 projection once over all tokens as uq_gemm_q8k and the norms, swiglu and
-residual adds over all rows; the counts cover the q8k GEMM's tile shapes
+residual adds over all rows, and the GatedDeltaNet's recurrent part in one
+launch over the tokens (head dims 64 and 128) or the step's launches per
+token (other head dims); the counts cover the q8k GEMM's tile shapes
 (1 token: the decode kernel; 5 and 16: 16-row tiles; 17-128: 32-row tiles;
-130: 64-row tiles), the attention starting at a position past earlier
-tokens, the small model and the 9B shapes of the decode benchmark.
+130: 64-row tiles), windows and states carried from earlier tokens, conv
+kernels of 2, 3, 4 and 9 taps, the attention starting at a position past
+earlier tokens, the small model and the 9B shapes of the decode benchmark.
 """
 import sys
 
@@ -33,11 +36,10 @@ def tokens(n_embd, nt, seed):
     return np.random.default_rng(seed).standard_normal((nt, n_embd)).astype(np.float32)
 
 
-def gdn_by_steps(m, X):
+def gdn_by_steps(m, X, win0, state0):
     c, d = m.cfg, m.d
     nt, n = X.shape
-    win = uq.DeviceArray.from_numpy(np.zeros(c.conv_kernel * d.channels, np.float32))
-    state = uq.DeviceArray.from_numpy(np.zeros(c.n_v_heads * c.head_dim_linear ** 2, np.float32))
+    win, state = uq.DeviceArray.from_numpy(win0), uq.DeviceArray.from_numpy(state0)
     ws = uq.DeviceArray(4 * L.ws_floats(d))
     dl = uq.DeviceArray(4 * n)
     out = np.empty_like(X)
@@ -52,11 +54,10 @@ def gdn_by_steps(m, X):
     return res
 
 
-def gdn_by_prefill(m, X):
+def gdn_by_prefill(m, X, win0, state0):
     c, d = m.cfg, m.d
     nt, n = X.shape
-    win = uq.DeviceArray.from_numpy(np.zeros(c.conv_kernel * d.channels, np.float32))
-    state = uq.DeviceArray.from_numpy(np.zeros(c.n_v_heads * c.head_dim_linear ** 2, np.float32))
+    win, state = uq.DeviceArray.from_numpy(win0), uq.DeviceArray.from_numpy(state0)
     ws = uq.DeviceArray(4 * L.prefill_ws_floats(d, nt, gdn=m.gw))
     dx, dl = uq.DeviceArray.from_numpy(X), uq.DeviceArray(4 * nt * n)
     L.gdn_prefill(d, m.gw, win, state, nt, dx, dl, ws)
@@ -67,16 +68,39 @@ def gdn_by_prefill(m, X):
     return res
 
 
-def check_gdn(m, nt, seed, what):
-    X = tokens(m.cfg.n_embd, nt, seed)
-    ref_out, ref_win, ref_state = gdn_by_steps(m, X)
-    out, win, state = gdn_by_prefill(m, X)
+def check_gdn(m, nt, seed, what, carried=False):
+    """nt tokens from an empty window and state, or (carried) from a random
+    window and state as earlier tokens leave them"""
+    c = m.cfg
+    X = tokens(c.n_embd, nt, seed)
+    rng = np.random.default_rng(seed + 100)
+    nwin, nstate = c.conv_kernel * m.d.channels, c.n_v_heads * c.head_dim_linear ** 2
+    win0 = rng.standard_normal(nwin).astype(np.float32) if carried else np.zeros(nwin, np.float32)
+    state0 = (0.05 * rng.standard_normal(nstate)).astype(np.float32) if carried else np.zeros(nstate, np.float32)
+    ref_out, ref_win, ref_state = gdn_by_steps(m, X, win0, state0)
+    out, win, state = gdn_by_prefill(m, X, win0, state0)
     for t in range(nt):
         assert_bitwise(out[t], ref_out[t], f"{what} token {t} l_out")
     assert_bitwise(win, ref_win, f"{what} conv window")
     assert_bitwise(state, ref_state, f"{what} state")
     assert np.all(np.isfinite(out))
     log(f"{what}: {nt} tokens bit-identical to {nt} steps")
+
+
+# other GatedDeltaNet shapes: head_dim_linear 32 (the per-token launches)
+# and 64 with the shortest and longest conv kernels (the one-launch scan;
+# with 9 taps a short prefill keeps rows of the earlier window)
+OTHER = dict(n_embd=256, n_ff=512, n_qk_heads=4, n_v_heads=8, head_dim_linear=32, conv_kernel=3, n_head=2,
+             n_head_kv=1, head_dim=128, n_rot=32)
+
+
+@pytest.mark.parametrize("hd,ck", [(32, 3), (64, 2), (64, 9)])
+@pytest.mark.parametrize("nt", [1, 3, 11, 40])
+def test_gdn_prefill_other_shapes_equal_steps(hd, ck, nt):
+    shape = dict(OTHER, head_dim_linear=hd, conv_kernel=ck, n_embd=8 * hd, n_head=8 * hd // 128)
+    m = Model(shape, seed=49 + hd + ck)
+    check_gdn(m, nt, seed=nt + 3, what=f"gdn hd={hd} ck={ck}", carried=True)
+    m.free()
 
 
 def attn_run(m, X, n_ctx_max, pos0, prefill, warm):
@@ -129,7 +153,7 @@ def check_attn(m, nt, pos0, n_ctx_max, seed, what):
 @pytest.mark.parametrize("nt", [1, 5, 16, 17, 40, 130])
 def test_gdn_prefill_small_equals_steps(nt, q6):
     m = Model(SMALL, seed=41 + q6)
-    check_gdn(m, nt, seed=nt, what=f"gdn small q6={q6}")
+    check_gdn(m, nt, seed=nt, what=f"gdn small q6={q6}", carried=nt in (5, 40))
     m.free()
 
 
@@ -146,6 +170,7 @@ def test_prefill_9b_shapes_equal_steps():
     layer and 12 through an attention layer after 5 earlier positions."""
     m = Model(FULL, seed=45)
     check_gdn(m, 20, seed=7, what="gdn 9b")
+    check_gdn(m, 9, seed=9, what="gdn 9b carried", carried=True)
     check_attn(m, 12, 5, n_ctx_max=64, seed=8, what="attn 9b")
     m.free()
 

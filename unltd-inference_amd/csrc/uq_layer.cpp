@@ -466,11 +466,18 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
     UQ_TRY(c.gemm(w->attn_gate, nt, A[P_XN], A[P_Z]));
     UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR]));
     UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL]));
-    // 4-6) the recurrent part token by token: the token's qkv into the
-    // window's last row, then the step's launches
+    // 4-6) the recurrent part, token after token: for head dims 64 and 128
+    // one launch over all the tokens (the state held on chip between them),
+    // else the token's qkv into the window's last row and the step's launches
+    if (uq::gdn_scan_ok((int)D.hd, (int)D.ck))
+        UQ_TRY(hip_st(uq::launch_gdn_scan(d_conv_win, w->ssm_conv1d, A[P_QKV], A[P_BR], A[P_AL], w->ssm_dt_bias,
+                                          w->ssm_a, A[P_Z], w->ssm_norm, d_state, A[P_FIN], nt, (int)D.ck, (int)D.ch,
+                                          (int)D.hd, (int)D.nqk, (int)D.nv, d->rms_eps, 1.0f / sqrtf((float)D.hd),
+                                          c.s),
+                      fn));
     float *qkv = d_conv_win + (D.ck - 1) * D.ch;
     const size_t vw = D.nv * D.hd;
-    for (int t = 0; t < nt; t++) {
+    for (int t = 0; t < nt && !uq::gdn_scan_ok((int)D.hd, (int)D.ck); t++) {
         UQ_TRY(hip_st(hipMemcpyAsync(qkv, A[P_QKV] + (size_t)t * D.ch, D.ch * 4, hipMemcpyDeviceToDevice, c.s), fn));
         UQ_TRY(gdn_core(fn, D, d, w, d_conv_win, d_state, d_ws, A[P_BR] + (size_t)t * D.nv, A[P_AL] + (size_t)t * D.nv,
                         A[P_Z] + t * vw, A[P_FIN] + t * vw, c.s));

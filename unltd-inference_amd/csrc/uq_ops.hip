@@ -345,6 +345,183 @@ __global__ __launch_bounds__(64 * kGdnWaves) void gdn_step_wg_kernel(float *__re
     if (live && wv == 0) out[(size_t)h * dim + j] = __fmul_rn(o, scale);
 }
 
+// The recurrent part of a GatedDeltaNet layer over nt tokens in one launch
+// (the prefill of qwen35_forward.rs:405-511, token after token): workgroup h
+// is v head h, its dim x dim state in VGPRs for all the tokens (column j =
+// 64 (w / 8) + lane, rows 16 (w % 8) .. + 15 of wave w, as two
+// gdn_step_wg_kernel workgroups). Per token, the arithmetic of the step's
+// launches: the conv of the head's q, k (of q/k head h % n_qk) and v
+// channels over its ring (conv_step_kernel; the ring in registers), silu,
+// the l2 norms of q and k (l2norm_kernel), the gates (gdn_gates_kernel),
+// the delta rule (gdn_step_wg_kernel) and the rmsnorm of the output with
+// ssm_norm times silu(z) (rmsnorm_kernel). Every f64 sum is the
+// reference's sequential one: a sum of the same terms in another order
+// decides it when the bound allows, otherwise one thread (norms) or every
+// column (dots) replays the reference's order, so each token's values equal
+// the step's bit for bit. dim is 64 or 128 (each of q, k, v one or two
+// waves). At the end the state is stored; the window is not written (the
+// workgroups of one q/k head all read its q / k rows): conv_window_kernel
+// shifts it after this launch.
+constexpr int kScanWaves = 16, kScanMaxConv = 9;
+__global__ __launch_bounds__(64 * kScanWaves) void gdn_scan_kernel(
+    float *__restrict__ win, const float *__restrict__ kern, const float *__restrict__ qkv,
+    const float *__restrict__ beta_raw, const float *__restrict__ alpha, const float *__restrict__ dt_bias,
+    const float *__restrict__ a, const float *__restrict__ z, const float *__restrict__ snorm,
+    float *__restrict__ state, float *__restrict__ fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v,
+    float eps, float scale) {
+    __shared__ double ps[kScanWaves][64], pa[kScanWaves][64];
+    __shared__ float col[128][128];  // columns of the state, for an ordered replay of a dot
+    __shared__ float vec[4][128];    // q, k (then normalised), v, the head's output
+    __shared__ double wsum[kScanWaves];
+    __shared__ float bc[3], gb[2];
+    __shared__ float taps[3 * 128][kScanMaxConv], ring[3 * 128][kScanMaxConv];  // odd row stride: no bank conflicts
+    const int h = blockIdx.x, hq = h % n_qk, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nvw = n_v * dim;
+    // conv role: thread tid < 3 dim owns channel c of part p (0 q, 1 k, 2 v)
+    const bool convt = tid < 3 * dim;
+    const int p = convt ? tid / dim : 0, pi = tid - p * dim;
+    const int c = p == 0 ? hq * dim + pi : p == 1 ? (n_qk + hq) * dim + pi : 2 * n_qk * dim + h * dim + pi;
+    // the channel's taps and its ring (window rows 0 .. d_conv - 2, oldest
+    // first from entry t % (d_conv - 1) at token t) in LDS
+    const int nr = d_conv - 1;
+    if (convt)
+        for (int r = 0; r < d_conv; r++) {
+            taps[tid][r] = kern[(size_t)c * d_conv + r];
+            if (r < nr) ring[tid][r] = win[(size_t)r * channels + c];
+        }
+    // state role
+    const int j = 64 * (wv >> 3) + lane, i0 = 16 * (wv & 7), half = wv >> 3;
+    const bool live = j < dim;
+    float cs[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+        cs[r] = (live && i0 + r < dim) ? state[(size_t)h * dim * dim + (size_t)(i0 + r) * dim + j] : 0.0f;
+    const float dtb = dt_bias[h], ah = a[h], wn = tid < dim ? snorm[tid] : 0.0f;
+    const int nparts = dim / 64;  // waves per part
+
+    // (float) of the sequential f64 sum over i < dim of cs_i * vec[sel][i], for
+    // column j (every thread of the column gets it)
+    auto dot = [&](int sel) {
+        double s = 0.0, ab = 0.0;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (i0 + r < dim) {
+                const double t = (double)__fmul_rn(cs[r], vec[sel][i0 + r]);
+                s += t;
+                ab += fabs(t);
+            }
+        ps[wv][lane] = s;
+        pa[wv][lane] = ab;
+        __syncthreads();
+        double S8 = 0.0, A8 = 0.0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            S8 += ps[8 * half + u][lane];
+            A8 += pa[8 * half + u][lane];
+        }
+        __syncthreads();
+        const double e = (double)(dim + 66) * 0x1p-52 * A8;
+        const float lo = (float)(S8 - e), hi = (float)(S8 + e);
+        const int undecided = __syncthreads_or(live && __float_as_uint(lo) != __float_as_uint(hi));
+        if (!undecided) return lo;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (i0 + r < dim && live) col[i0 + r][j] = cs[r];
+        __syncthreads();
+        double qq = 0.0;
+        if (live)
+            for (int i = 0; i < dim; i++) qq += (double)__fmul_rn(col[i][j], vec[sel][i]);
+        __syncthreads();
+        return (float)qq;
+    };
+    // the sum of the squares of part q (vec[q][0..dim)) held as per-thread
+    // terms sq: wave sums, then the part's waves in order
+    auto part_sum = [&](double sq, int q) {
+        const double ws = wave_sum_d(sq);
+        if (lane == 0) wsum[wv] = ws;
+        __syncthreads();
+        double S = 0.0;
+        for (int u = 0; u < nparts; u++) S += wsum[q * nparts + u];
+        __syncthreads();
+        return S;
+    };
+
+    for (int t = 0; t < nt; t++) {
+        // conv over [ring; qkv_t], silu; the ring shifts
+        float v = 0.0f;
+        if (convt) {
+            const float xn = qkv[(size_t)t * channels + c];
+            const int h0 = t % nr;
+            float s = 0.0f;
+            for (int tau = 0, e = h0; tau < nr; tau++, e = e + 1 == nr ? 0 : e + 1)
+                s = __fadd_rn(s, __fmul_rn(ring[tid][e], taps[tid][tau]));
+            s = __fadd_rn(s, __fmul_rn(xn, taps[tid][nr]));
+            v = silu1(s);
+            ring[tid][h0] = xn;  // the oldest entry: the ring's shift
+            vec[p][pi] = v;
+        }
+        // l2 norms of q and k (their sums of squares in parts 0 and 1)
+        const double Sq = part_sum(convt && p == 0 ? (double)__fmul_rn(v, v) : 0.0, 0);
+        const double Sk = part_sum(convt && p == 1 ? (double)__fmul_rn(v, v) : 0.0, 1);
+        const float sq = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[0][i]; }, dim, Sq,
+                                                      [](double u) { return (float)u; }, &bc[0]);
+        const float sk = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[1][i]; }, dim, Sk,
+                                                      [](double u) { return (float)u; }, &bc[1]);
+        if (convt && p < 2) vec[p][pi] = __fmul_rn(v, __fdiv_rn(1.0f, fmaxf(sqrtf_cr(p == 0 ? sq : sk), eps)));
+        if (tid == 0) {
+            gb[1] = sigmoid1(beta_raw[(size_t)t * n_v + h]);
+            const float sp = softplus1(__fadd_rn(alpha[(size_t)t * n_v + h], dtb));
+            gb[0] = __fmul_rn(sp, ah);
+        }
+        __syncthreads();
+        // the delta rule
+        const float g_exp = expf_cr(gb[0]), bt = gb[1];
+#pragma unroll
+        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], g_exp);
+        const float sum = dot(1);
+        const float d = __fmul_rn(__fsub_rn(live ? vec[2][j] : 0.0f, sum), bt);
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (i0 + r < dim) cs[r] = __fadd_rn(cs[r], __fmul_rn(vec[1][i0 + r], d));
+        const float o = dot(0);
+        if (live && (wv & 7) == 0) vec[3][j] = __fmul_rn(o, scale);
+        __syncthreads();
+        // rmsnorm of the head's output with ssm_norm, times silu(z)
+        const float ov = tid < dim ? vec[3][tid] : 0.0f;
+        const double So = part_sum(tid < dim ? (double)__fmul_rn(ov, ov) : 0.0, 0);
+        const double dn = (double)dim;
+        const float mean = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[3][i]; }, dim, So,
+                                                        [dn](double u) { return (float)(u / dn); }, &bc[2]);
+        const float rs = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
+        if (tid < dim) {
+            const float zi = z[(size_t)t * nvw + (size_t)h * dim + tid];
+            fin[(size_t)t * nvw + (size_t)h * dim + tid] = __fmul_rn(__fmul_rn(__fmul_rn(ov, rs), wn), silu1(zi));
+        }
+        __syncthreads();  // vec is rewritten by the next token
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+        if (live && i0 + r < dim) state[(size_t)h * dim * dim + (size_t)(i0 + r) * dim + j] = cs[r];
+}
+
+// The conv window after nt steps, in place, one thread per channel: the
+// sequence is the window's rows 0 .. d_conv - 2 followed by the nt qkv rows;
+// rows 0 .. d_conv - 2 become its last d_conv - 1 entries and row d_conv - 1
+// the last qkv row (as each step writes the token's qkv to the last row,
+// then shifts rows 1 .. d_conv - 1 up). Row r's source is at index nt + r
+// > r, so ascending r reads every old row before it is overwritten.
+__global__ void conv_window_kernel(float *__restrict__ win, const float *__restrict__ qkv, int nt, int d_conv,
+                                   int channels) {
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < channels; c += gridDim.x * blockDim.x) {
+        for (int r = 0; r < d_conv - 1; r++) {
+            const int u = nt + r;
+            win[(size_t)r * channels + c] =
+                u < d_conv - 1 ? win[(size_t)u * channels + c] : qkv[(size_t)(u - (d_conv - 1)) * channels + c];
+        }
+        win[(size_t)(d_conv - 1) * channels + c] = qkv[(size_t)(nt - 1) * channels + c];
+    }
+}
+
 // The rope rotation (kernels.rs:121-123): f64 sin/cos, fma, rounded to f32.
 __device__ __forceinline__ void rotate_pair(float *a, float *b, double angle) {
     double s, c;
@@ -846,6 +1023,24 @@ hipError_t launch_gdn_step(float *state, float *out, const float *q, const float
     }
     const int tpb = dim >= 256 ? 256 : ((dim + 63) / 64) * 64;
     hipLaunchKernelGGL(gdn_step_kernel, dim3(heads), dim3(tpb), 0, s, state, out, q, k, v, gate, beta, dim, scale, nq);
+    return hipGetLastError();
+}
+
+bool gdn_scan_ok(int dim, int d_conv) { return (dim == 64 || dim == 128) && d_conv >= 2 && d_conv <= kScanMaxConv; }
+
+hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, const float *beta_raw, const float *alpha,
+                           const float *dt_bias, const float *a, const float *z, const float *snorm, float *state,
+                           float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v, float eps,
+                           float scale, hipStream_t s) {
+    if (!gdn_scan_ok(dim, d_conv) || n_qk < 1 || channels != (2 * n_qk + n_v) * dim)
+        return hipErrorInvalidValue;
+    if (nt == 0 || n_v == 0) return hipSuccess;
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v), dim3(64 * kScanWaves), 0, s, win, kern, qkv, beta_raw, alpha,
+                       dt_bias, a, z, snorm, state, fin, nt, d_conv, channels, dim, n_qk, n_v, eps, scale);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(conv_window_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, qkv, nt, d_conv,
+                       channels);
     return hipGetLastError();
 }
 
