@@ -93,14 +93,16 @@ hipError_t launch_gdn_conv_norm(float *win, const float *kern_gguf, float *raw, 
                                 hipStream_t s);
 bool conv_norm_ok(int hd);
 // The recurrent part of a GatedDeltaNet layer (conv, norms, gates, delta
-// rule, gated rmsnorm) over nt tokens in one launch: qkv, beta_raw, alpha,
-// z and fin are [nt] rows of the step's nodes; the state and the window
-// carried as nt steps carry them (dim 64 or 128: gdn_scan_ok)
+// rule, gated rmsnorm) of nt tokens: qkv, beta, gexp, z, out and fin are
+// [nt] rows of the step's nodes (beta and gexp hold beta_raw and alpha on
+// entry, are overwritten), cv [nt][channels] scratch; out receives the
+// head outputs before the gated norm, fin after it; the state and the
+// window carried as nt steps carry them (dim 64 or 128: gdn_scan_ok)
 bool gdn_scan_ok(int dim, int d_conv);
-hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, const float *beta_raw, const float *alpha,
+hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, float *cv, float *beta, float *gexp,
                            const float *dt_bias, const float *a, const float *z, const float *snorm, float *state,
-                           float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v, float eps,
-                           float scale, hipStream_t s);
+                           float *out, float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v,
+                           float eps, float scale, hipStream_t s);
 // q and k rmsnorm + IMROPE of the attention layer in one launch (hd <= 512)
 hipError_t launch_attn_qk_prep(const float *qfull, float *q_out, const float *k_raw, float *k_out, const float *wq,
                                const float *wk, int hd, int n_head, int n_head_kv, int n_rot, double theta_scale,

@@ -209,10 +209,12 @@ uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const
 // The prefill workspace: the step's nodes (one token's, reused token by
 // token), then n_tokens rows of each batched array, then the q8k GEMM's
 // workspace; every part at a 64-float boundary.
-enum PrefillArr { P_XN, P_QKV, P_Z, P_BR, P_AL, P_FIN, P_QF, P_KR, P_GT, P_AO, P_RES, P_PN, P_G, P_U, P_H, P_FO, P_COUNT };
+enum PrefillArr { P_XN, P_QKV, P_Z, P_BR, P_AL, P_FIN, P_QF, P_KR, P_GT, P_AO, P_RES, P_PN, P_G, P_U, P_H, P_FO, P_CV,
+                  P_COUNT };
 size_t prefill_row(const Dims &D, int a) {
     switch (a) {
-        case P_QKV: return D.ch;
+        case P_QKV:
+        case P_CV: return D.ch;
         case P_Z:
         case P_FIN: return D.nv * D.hd;
         case P_BR:
@@ -466,14 +468,16 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
     UQ_TRY(c.gemm(w->attn_gate, nt, A[P_XN], A[P_Z]));
     UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR]));
     UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL]));
-    // 4-6) the recurrent part, token after token: for head dims 64 and 128
-    // one launch over all the tokens (the state held on chip between them),
-    // else the token's qkv into the window's last row and the step's launches
+    // 4-6) the recurrent part: for head dims 64 and 128 the conv, norms and
+    // gates of all tokens at once, the delta rule over the tokens in one
+    // launch (the state held in registers between them), the gated norms of
+    // all outputs at once; else per token, its qkv into the window's last
+    // row and the step's launches
     if (uq::gdn_scan_ok((int)D.hd, (int)D.ck))
-        UQ_TRY(hip_st(uq::launch_gdn_scan(d_conv_win, w->ssm_conv1d, A[P_QKV], A[P_BR], A[P_AL], w->ssm_dt_bias,
-                                          w->ssm_a, A[P_Z], w->ssm_norm, d_state, A[P_FIN], nt, (int)D.ck, (int)D.ch,
-                                          (int)D.hd, (int)D.nqk, (int)D.nv, d->rms_eps, 1.0f / sqrtf((float)D.hd),
-                                          c.s),
+        UQ_TRY(hip_st(uq::launch_gdn_scan(d_conv_win, w->ssm_conv1d, A[P_QKV], A[P_CV], A[P_BR], A[P_AL],
+                                          w->ssm_dt_bias, w->ssm_a, A[P_Z], w->ssm_norm, d_state, A[P_AO], A[P_FIN],
+                                          nt, (int)D.ck, (int)D.ch, (int)D.hd, (int)D.nqk, (int)D.nv, d->rms_eps,
+                                          1.0f / sqrtf((float)D.hd), c.s),
                       fn));
     float *qkv = d_conv_win + (D.ck - 1) * D.ch;
     const size_t vw = D.nv * D.hd;

@@ -345,163 +345,154 @@ __global__ __launch_bounds__(64 * kGdnWaves) void gdn_step_wg_kernel(float *__re
     if (live && wv == 0) out[(size_t)h * dim + j] = __fmul_rn(o, scale);
 }
 
-// The recurrent part of a GatedDeltaNet layer over nt tokens in one launch
-// (the prefill of qwen35_forward.rs:405-511, token after token): workgroup h
-// is v head h, its dim x dim state in VGPRs for all the tokens (column j =
-// 64 (w / 8) + lane, rows 16 (w % 8) .. + 15 of wave w, as two
-// gdn_step_wg_kernel workgroups). Per token, the arithmetic of the step's
-// launches: the conv of the head's q, k (of q/k head h % n_qk) and v
-// channels over its ring (conv_step_kernel; the ring in registers), silu,
-// the l2 norms of q and k (l2norm_kernel), the gates (gdn_gates_kernel),
-// the delta rule (gdn_step_wg_kernel) and the rmsnorm of the output with
-// ssm_norm times silu(z) (rmsnorm_kernel). Every f64 sum is the
-// reference's sequential one: a sum of the same terms in another order
-// decides it when the bound allows, otherwise one thread (norms) or every
-// column (dots) replays the reference's order, so each token's values equal
-// the step's bit for bit. dim is 64 or 128 (each of q, k, v one or two
-// waves). At the end the state is stored; the window is not written (the
-// workgroups of one q/k head all read its q / k rows): conv_window_kernel
-// shifts it after this launch.
-constexpr int kScanWaves = 16, kScanMaxConv = 9;
-__global__ __launch_bounds__(64 * kScanWaves) void gdn_scan_kernel(
-    float *__restrict__ win, const float *__restrict__ kern, const float *__restrict__ qkv,
-    const float *__restrict__ beta_raw, const float *__restrict__ alpha, const float *__restrict__ dt_bias,
-    const float *__restrict__ a, const float *__restrict__ z, const float *__restrict__ snorm,
-    float *__restrict__ state, float *__restrict__ fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v,
-    float eps, float scale) {
-    __shared__ double ps[kScanWaves][64], pa[kScanWaves][64];
-    __shared__ float col[128][128];  // columns of the state, for an ordered replay of a dot
-    __shared__ float vec[4][128];    // q, k (then normalised), v, the head's output
-    __shared__ double wsum[kScanWaves];
-    __shared__ float bc[3], gb[2];
-    __shared__ float taps[3 * 128][kScanMaxConv], ring[3 * 128][kScanMaxConv];  // odd row stride: no bank conflicts
-    const int h = blockIdx.x, hq = h % n_qk, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nvw = n_v * dim;
-    // conv role: thread tid < 3 dim owns channel c of part p (0 q, 1 k, 2 v)
-    const bool convt = tid < 3 * dim;
-    const int p = convt ? tid / dim : 0, pi = tid - p * dim;
-    const int c = p == 0 ? hq * dim + pi : p == 1 ? (n_qk + hq) * dim + pi : 2 * n_qk * dim + h * dim + pi;
-    // the channel's taps and its ring (window rows 0 .. d_conv - 2, oldest
-    // first from entry t % (d_conv - 1) at token t) in LDS
-    const int nr = d_conv - 1;
-    if (convt)
-        for (int r = 0; r < d_conv; r++) {
-            taps[tid][r] = kern[(size_t)c * d_conv + r];
-            if (r < nr) ring[tid][r] = win[(size_t)r * channels + c];
+// ---- the GatedDeltaNet prefill: the recurrent part of nt tokens ----------
+// Of the step's work per token only the delta rule carries state from token
+// to token; the conv over [window; qkv rows], silu, the q / k l2 norms and
+// the gates of every token, and the gated rmsnorm of every output, are
+// independent per token and run as row-parallel launches around the scan.
+
+// Conv, silu and l2 norm of nt tokens (gdn_conv_norm_kernel per token):
+// workgroup (b, t) for b < n_chunks forms chunk b of token t into cv[t] (the
+// q and k chunks normalised); the window seen by token t is entries t ..
+// t + d_conv - 1 of the sequence [win rows 0 .. d_conv - 2; qkv rows 0 ..
+// nt - 1]. Workgroup (n_chunks, t) forms token t's gates per v head in
+// place: beta_raw becomes beta = sigmoid(beta_raw), alpha becomes exp(gate),
+// gate = softplus(alpha + dt_bias) * a (gdn_gates_kernel, then the step's
+// exp of the gate).
+__global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_rows_kernel(
+    const float *__restrict__ win, const float *__restrict__ kern, const float *__restrict__ qkv,
+    float *__restrict__ cv, int d_conv, int channels, int hd, int n_qk, float eps, float *__restrict__ beta,
+    float *__restrict__ gexp, const float *__restrict__ dt_bias, const float *__restrict__ a, int n_v) {
+    __shared__ float vals[128];  // hd <= 128 (gdn_scan_ok)
+    __shared__ double red[OPS_TPB / 64];
+    __shared__ float bc;
+    const int b = blockIdx.x, t = blockIdx.y, n_chunks = channels / hd;
+    if (b == n_chunks) {
+        for (int h = threadIdx.x; h < n_v; h += OPS_TPB) {
+            const size_t i = (size_t)t * n_v + h;
+            const float br = beta[i], al = gexp[i];
+            beta[i] = sigmoid1(br);
+            gexp[i] = expf_cr(__fmul_rn(softplus1(__fadd_rn(al, dt_bias[h])), a[h]));
         }
-    // state role
-    const int j = 64 * (wv >> 3) + lane, i0 = 16 * (wv & 7), half = wv >> 3;
-    const bool live = j < dim;
+        return;
+    }
+    const bool norm = b < 2 * n_qk;  // workgroup-uniform
+    double s = 0.0;
+    for (int j = threadIdx.x; j < hd; j += OPS_TPB) {
+        const int c = b * hd + j;
+        float x = 0.0f;
+        for (int tau = 0; tau < d_conv; tau++) {
+            const int u = t + tau;
+            const float xv = u < d_conv - 1 ? win[(size_t)u * channels + c] : qkv[(size_t)(u - d_conv + 1) * channels + c];
+            x = __fadd_rn(x, __fmul_rn(xv, kern[(size_t)c * d_conv + tau]));
+        }
+        const float v = silu1(x);
+        if (norm) {
+            vals[j] = v;
+            s += (double)__fmul_rn(v, v);
+        } else {
+            cv[(size_t)t * channels + c] = v;
+        }
+    }
+    if (!norm) return;
+    const double S = block_sum_d<OPS_TPB>(s, red);  // its barrier also publishes vals
+    const float sum32 = seq_sum_f32<OPS_TPB>([](int i) { return vals[i]; }, hd, S, [](double v) { return (float)v; },
+                                             &bc);
+    const float scale = __fdiv_rn(1.0f, fmaxf(sqrtf_cr(sum32), eps));
+    for (int j = threadIdx.x; j < hd; j += OPS_TPB) cv[(size_t)t * channels + b * hd + j] = __fmul_rn(vals[j], scale);
+}
+
+// The delta rule (gdn_step_wg_kernel) of nt tokens, token after token, one
+// wave per workgroup and no exchange between waves: lane l holds rows
+// [16 m, 16 m + 16), m = l % RB (RB = dim / 16 lanes per column), of column
+// j = (64 / RB) blockIdx.x + l / RB of v head blockIdx.y's state, in VGPRs
+// for all the tokens. Each f64 dot is the lane's 16 terms in row order,
+// then an xor tree over the column's RB lanes, with the bound of the step
+// kernel: when both ends of [S - e, S + e] round to one f32 that is the
+// reference's (float) of its sequential sum; otherwise the column's products
+// go through LDS and every lane of it sums them in the reference's order.
+// Token t's q and k (normalised) and v are row t of cv, its beta and
+// exp(gate) row t of beta / gexp; the next token's are loaded while this
+// one is processed. out[t] receives o * scale (before the gated rmsnorm).
+template <int RB>
+__device__ __forceinline__ double col_sum_d(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    if constexpr (RB == 8) v += dpp_d<0x141>(v);
+    return v;
+}
+template <int RB>
+__global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ cv, const float *__restrict__ beta,
+                                                      const float *__restrict__ gexp, float *__restrict__ state,
+                                                      float *__restrict__ out, int nt, int channels, int n_qk,
+                                                      int n_v, float scale) {
+    constexpr int dim = 16 * RB, CPW = 64 / RB;  // columns per wave
+    __shared__ float prod[CPW][dim];             // a column's products, for the ordered replay
+    const int lane = threadIdx.x, m = lane % RB, jc = lane / RB, h = blockIdx.y, hq = h % n_qk;
+    const int j = blockIdx.x * CPW + jc, i0 = 16 * m;
+    float *S = state + (size_t)h * dim * dim + (size_t)i0 * dim + j;
     float cs[16];
 #pragma unroll
-    for (int r = 0; r < 16; r++)
-        cs[r] = (live && i0 + r < dim) ? state[(size_t)h * dim * dim + (size_t)(i0 + r) * dim + j] : 0.0f;
-    const float dtb = dt_bias[h], ah = a[h], wn = tid < dim ? snorm[tid] : 0.0f;
-    const int nparts = dim / 64;  // waves per part
-
-    // (float) of the sequential f64 sum over i < dim of cs_i * vec[sel][i], for
-    // column j (every thread of the column gets it)
-    auto dot = [&](int sel) {
+    for (int r = 0; r < 16; r++) cs[r] = S[(size_t)r * dim];
+    const size_t oq = (size_t)hq * dim + i0, ok = (size_t)(n_qk + hq) * dim + i0, ov = (size_t)(2 * n_qk + h) * dim + j;
+    float qn[16], kn[16], vn, gn, bn;  // the next token's inputs
+    auto fetch = [&](int t) {
+        const float4 *q4 = (const float4 *)(cv + (size_t)t * channels + oq);
+        const float4 *k4 = (const float4 *)(cv + (size_t)t * channels + ok);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float4 a = q4[u], b = k4[u];
+            qn[4 * u] = a.x, qn[4 * u + 1] = a.y, qn[4 * u + 2] = a.z, qn[4 * u + 3] = a.w;
+            kn[4 * u] = b.x, kn[4 * u + 1] = b.y, kn[4 * u + 2] = b.z, kn[4 * u + 3] = b.w;
+        }
+        vn = cv[(size_t)t * channels + ov];
+        gn = gexp[(size_t)t * n_v + h];
+        bn = beta[(size_t)t * n_v + h];
+    };
+    // (float) of the reference's sequential f64 sum over i < dim of cs_i x_i
+    auto dot = [&](const float *x) {
         double s = 0.0, ab = 0.0;
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            if (i0 + r < dim) {
-                const double t = (double)__fmul_rn(cs[r], vec[sel][i0 + r]);
-                s += t;
-                ab += fabs(t);
-            }
-        ps[wv][lane] = s;
-        pa[wv][lane] = ab;
-        __syncthreads();
-        double S8 = 0.0, A8 = 0.0;
+        for (int r = 0; r < 16; r++) {
+            const double t = (double)__fmul_rn(cs[r], x[r]);
+            s += t;
+            ab += fabs(t);
+        }
+        const double Sc = col_sum_d<RB>(s), Ac = col_sum_d<RB>(ab);
+        const double e = (double)(dim + 66) * 0x1p-52 * Ac;
+        const float lo = (float)(Sc - e), hi = (float)(Sc + e);
+        const bool undecided = __float_as_uint(lo) != __float_as_uint(hi);
+        if (!__builtin_amdgcn_ballot_w64(undecided)) return lo;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            S8 += ps[8 * half + u][lane];
-            A8 += pa[8 * half + u][lane];
+        for (int r = 0; r < 16; r++) prod[jc][i0 + r] = __fmul_rn(cs[r], x[r]);
+        __syncthreads();
+        float res = lo;
+        if (undecided) {
+            double q = 0.0;
+            for (int i = 0; i < dim; i++) q += (double)prod[jc][i];
+            res = (float)q;
         }
         __syncthreads();
-        const double e = (double)(dim + 66) * 0x1p-52 * A8;
-        const float lo = (float)(S8 - e), hi = (float)(S8 + e);
-        const int undecided = __syncthreads_or(live && __float_as_uint(lo) != __float_as_uint(hi));
-        if (!undecided) return lo;
-#pragma unroll
-        for (int r = 0; r < 16; r++)
-            if (i0 + r < dim && live) col[i0 + r][j] = cs[r];
-        __syncthreads();
-        double qq = 0.0;
-        if (live)
-            for (int i = 0; i < dim; i++) qq += (double)__fmul_rn(col[i][j], vec[sel][i]);
-        __syncthreads();
-        return (float)qq;
+        return res;
     };
-    // the sum of the squares of part q (vec[q][0..dim)) held as per-thread
-    // terms sq: wave sums, then the part's waves in order
-    auto part_sum = [&](double sq, int q) {
-        const double ws = wave_sum_d(sq);
-        if (lane == 0) wsum[wv] = ws;
-        __syncthreads();
-        double S = 0.0;
-        for (int u = 0; u < nparts; u++) S += wsum[q * nparts + u];
-        __syncthreads();
-        return S;
-    };
-
+    fetch(0);
     for (int t = 0; t < nt; t++) {
-        // conv over [ring; qkv_t], silu; the ring shifts
-        float v = 0.0f;
-        if (convt) {
-            const float xn = qkv[(size_t)t * channels + c];
-            const int h0 = t % nr;
-            float s = 0.0f;
-            for (int tau = 0, e = h0; tau < nr; tau++, e = e + 1 == nr ? 0 : e + 1)
-                s = __fadd_rn(s, __fmul_rn(ring[tid][e], taps[tid][tau]));
-            s = __fadd_rn(s, __fmul_rn(xn, taps[tid][nr]));
-            v = silu1(s);
-            ring[tid][h0] = xn;  // the oldest entry: the ring's shift
-            vec[p][pi] = v;
-        }
-        // l2 norms of q and k (their sums of squares in parts 0 and 1)
-        const double Sq = part_sum(convt && p == 0 ? (double)__fmul_rn(v, v) : 0.0, 0);
-        const double Sk = part_sum(convt && p == 1 ? (double)__fmul_rn(v, v) : 0.0, 1);
-        const float sq = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[0][i]; }, dim, Sq,
-                                                      [](double u) { return (float)u; }, &bc[0]);
-        const float sk = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[1][i]; }, dim, Sk,
-                                                      [](double u) { return (float)u; }, &bc[1]);
-        if (convt && p < 2) vec[p][pi] = __fmul_rn(v, __fdiv_rn(1.0f, fmaxf(sqrtf_cr(p == 0 ? sq : sk), eps)));
-        if (tid == 0) {
-            gb[1] = sigmoid1(beta_raw[(size_t)t * n_v + h]);
-            const float sp = softplus1(__fadd_rn(alpha[(size_t)t * n_v + h], dtb));
-            gb[0] = __fmul_rn(sp, ah);
-        }
-        __syncthreads();
-        // the delta rule
-        const float g_exp = expf_cr(gb[0]), bt = gb[1];
+        float qc[16], kc[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], g_exp);
-        const float sum = dot(1);
-        const float d = __fmul_rn(__fsub_rn(live ? vec[2][j] : 0.0f, sum), bt);
+        for (int r = 0; r < 16; r++) qc[r] = qn[r], kc[r] = kn[r];
+        const float vj = vn, g = gn, bt = bn;
+        if (t + 1 < nt) fetch(t + 1);
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            if (i0 + r < dim) cs[r] = __fadd_rn(cs[r], __fmul_rn(vec[1][i0 + r], d));
-        const float o = dot(0);
-        if (live && (wv & 7) == 0) vec[3][j] = __fmul_rn(o, scale);
-        __syncthreads();
-        // rmsnorm of the head's output with ssm_norm, times silu(z)
-        const float ov = tid < dim ? vec[3][tid] : 0.0f;
-        const double So = part_sum(tid < dim ? (double)__fmul_rn(ov, ov) : 0.0, 0);
-        const double dn = (double)dim;
-        const float mean = seq_sum_f32<64 * kScanWaves>([&](int i) { return vec[3][i]; }, dim, So,
-                                                        [dn](double u) { return (float)(u / dn); }, &bc[2]);
-        const float rs = __fdiv_rn(1.0f, sqrtf_cr(__fadd_rn(mean, eps)));
-        if (tid < dim) {
-            const float zi = z[(size_t)t * nvw + (size_t)h * dim + tid];
-            fin[(size_t)t * nvw + (size_t)h * dim + tid] = __fmul_rn(__fmul_rn(__fmul_rn(ov, rs), wn), silu1(zi));
-        }
-        __syncthreads();  // vec is rewritten by the next token
+        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], g);
+        const float sum = dot(kc);
+        const float d = __fmul_rn(__fsub_rn(vj, sum), bt);
+#pragma unroll
+        for (int r = 0; r < 16; r++) cs[r] = __fadd_rn(cs[r], __fmul_rn(kc[r], d));
+        const float o = dot(qc);
+        if (m == 0) out[(size_t)t * n_v * dim + (size_t)h * dim + j] = __fmul_rn(o, scale);
     }
 #pragma unroll
-    for (int r = 0; r < 16; r++)
-        if (live && i0 + r < dim) state[(size_t)h * dim * dim + (size_t)(i0 + r) * dim + j] = cs[r];
+    for (int r = 0; r < 16; r++) S[(size_t)r * dim] = cs[r];
 }
 
 // The conv window after nt steps, in place, one thread per channel: the
@@ -1026,22 +1017,30 @@ hipError_t launch_gdn_step(float *state, float *out, const float *q, const float
     return hipGetLastError();
 }
 
-bool gdn_scan_ok(int dim, int d_conv) { return (dim == 64 || dim == 128) && d_conv >= 2 && d_conv <= kScanMaxConv; }
+bool gdn_scan_ok(int dim, int d_conv) { return (dim == 64 || dim == 128) && d_conv >= 2 && d_conv <= 9; }
 
-hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, const float *beta_raw, const float *alpha,
+hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, float *cv, float *beta, float *gexp,
                            const float *dt_bias, const float *a, const float *z, const float *snorm, float *state,
-                           float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v, float eps,
-                           float scale, hipStream_t s) {
-    if (!gdn_scan_ok(dim, d_conv) || n_qk < 1 || channels != (2 * n_qk + n_v) * dim)
-        return hipErrorInvalidValue;
+                           float *out, float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v,
+                           float eps, float scale, hipStream_t s) {
+    if (!gdn_scan_ok(dim, d_conv) || n_qk < 1 || channels != (2 * n_qk + n_v) * dim) return hipErrorInvalidValue;
     if (nt == 0 || n_v == 0) return hipSuccess;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v), dim3(64 * kScanWaves), 0, s, win, kern, qkv, beta_raw, alpha,
-                       dt_bias, a, z, snorm, state, fin, nt, d_conv, channels, dim, n_qk, n_v, eps, scale);
-    const hipError_t e = hipGetLastError();
+    hipLaunchKernelGGL(gdn_conv_norm_rows_kernel, dim3(channels / dim + 1, nt), dim3(OPS_TPB), 0, s, win, kern, qkv,
+                       cv, d_conv, channels, dim, n_qk, eps, beta, gexp, dt_bias, a, n_v);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(conv_window_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, qkv, nt, d_conv,
                        channels);
-    return hipGetLastError();
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (dim == 128)
+        hipLaunchKernelGGL(gdn_scan_kernel<8>, dim3(16, n_v), dim3(64), 0, s, cv, beta, gexp, state, out, nt, channels,
+                           n_qk, n_v, scale);
+    else
+        hipLaunchKernelGGL(gdn_scan_kernel<4>, dim3(4, n_v), dim3(64), 0, s, cv, beta, gexp, state, out, nt, channels,
+                           n_qk, n_v, scale);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // the gated rmsnorm of every token's head outputs (rmsnorm_kernel with z)
+    return launch_rmsnorm_rows(fin, dim, out, dim, snorm, dim, nt * n_v, eps, s, nullptr, nullptr, z);
 }
 
 hipError_t launch_rope_freq(int mode, float *x, int rows, int n, const float *freqs, size_t pos, hipStream_t s) {
