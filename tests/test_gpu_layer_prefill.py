@@ -165,6 +165,15 @@ def test_attn_prefill_small_equals_steps(nt, pos0, q6):
     m.free()
 
 
+def test_attn_prefill_chunked_equals_steps():
+    """A context so long that the scores of 40 tokens exceed the prefill's
+    2^24-float scores area: the attention runs in chunks of 15, 15 and 10
+    tokens (n_head 4 x n_ctx_max 262145 floats per token)."""
+    m = Model(SMALL, seed=51)
+    check_attn(m, 40, 3, n_ctx_max=262145, seed=11, what="attn small chunked")
+    m.free()
+
+
 def test_prefill_9b_shapes_equal_steps():
     """The decode benchmark's 9B shapes: 20 tokens through a GatedDeltaNet
     layer and 12 through an attention layer after 5 earlier positions."""

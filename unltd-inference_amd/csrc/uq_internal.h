@@ -85,6 +85,13 @@ bool attn_shape_ok(int hd, int group);
 hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
                               int n_head_kv, int hd, int group, float kq_scale, hipStream_t s,
                               const float *gz = nullptr, int gzs = 0, float *gated = nullptr);
+// The same attention for rows consecutive queries (a prefill): query z sees
+// n_ctx + z positions; its q, soft, out, gz and gated are z times the
+// given strides (floats) on. soft_st >= n_head (n_ctx + rows - 1).
+hipError_t launch_attn_rows(float *out, size_t out_st, float *soft, size_t soft_st, const float *q, size_t q_st,
+                            const float *kc, const float *vc, int n_ctx, int rows, int n_head_kv, int hd, int group,
+                            float kq_scale, hipStream_t s, const float *gz, int gzs, size_t gz_st, float *gated,
+                            size_t gated_st);
 // The GatedDeltaNet conv step, the l2 norms of the q / k heads and the gates
 // in one launch (hd <= 1024, conv_norm_ok)
 hipError_t launch_gdn_conv_norm(float *win, const float *kern_gguf, float *raw, float *act, int d_conv, int channels,
@@ -103,10 +110,12 @@ hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, floa
                            const float *dt_bias, const float *a, const float *z, const float *snorm, float *state,
                            float *out, float *fin, int nt, int d_conv, int channels, int dim, int n_qk, int n_v,
                            float eps, float scale, hipStream_t s);
-// q and k rmsnorm + IMROPE of the attention layer in one launch (hd <= 512)
+// q and k rmsnorm + IMROPE of the attention layer in one launch (hd <= 512),
+// for rows consecutive tokens at positions pos .. pos + rows - 1 (their
+// rows of qfull, q_out, k_raw and k_out consecutive)
 hipError_t launch_attn_qk_prep(const float *qfull, float *q_out, const float *k_raw, float *k_out, const float *wq,
                                const float *wk, int hd, int n_head, int n_head_kv, int n_rot, double theta_scale,
-                               size_t pos, float eps, hipStream_t s);
+                               size_t pos, float eps, hipStream_t s, int rows = 1);
 
 // For host-pointer entry points: checks for a gfx950 device and returns the
 // calling thread's stream (uq_abi.cpp).

@@ -210,7 +210,14 @@ uq_status ffn_tail(const char *fn, const Dims &D, const uq_qwen35_dims *d, const
 // token), then n_tokens rows of each batched array, then the q8k GEMM's
 // workspace; every part at a 64-float boundary.
 enum PrefillArr { P_XN, P_QKV, P_Z, P_BR, P_AL, P_FIN, P_QF, P_KR, P_GT, P_AO, P_RES, P_PN, P_G, P_U, P_H, P_FO, P_CV,
-                  P_COUNT };
+                  P_SC, P_COUNT };
+// The attention of a prefill runs in chunks of tokens whose scores, each
+// token n_head * n_ctx_max floats at most, fit in 2^24 floats (64 MiB;
+// at least one token). P_SC holds one chunk's.
+size_t attn_chunk(const Dims &D, size_t n_ctx_max, size_t nt) {
+    if (n_ctx_max == 0) return 0;
+    return std::max<size_t>(1, std::min({nt, ((size_t)1 << 24) / (D.nh * n_ctx_max), (size_t)65535}));
+}
 size_t prefill_row(const Dims &D, int a) {
     switch (a) {
         case P_QKV:
@@ -230,7 +237,10 @@ size_t prefill_row(const Dims &D, int a) {
 }
 size_t prefill_arr_offset(const Dims &D, size_t n_ctx_max, size_t nt, int a) {
     size_t off = node_offset(D, n_ctx_max, UQ_NODE_COUNT);
-    for (int i = 0; i < a; i++) off += (prefill_row(D, i) * nt + 63) & ~(size_t)63;
+    for (int i = 0; i < a; i++) {
+        const size_t len = i == P_SC ? attn_chunk(D, n_ctx_max, nt) * D.nh * n_ctx_max : prefill_row(D, i) * nt;
+        off += (len + 63) & ~(size_t)63;
+    }
     return off;
 }
 // bytes of the q8k GEMM workspace for any projection of the layer at nt rows
@@ -530,18 +540,26 @@ uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w
     UQ_TRY(c.gemm(w->attn_q, nt, A[P_XN], A[P_QF]));
     UQ_TRY(c.gemm(w->attn_k, nt, A[P_XN], A[P_KR]));
     UQ_TRY(c.gemm(w->attn_v, nt, A[P_XN], d_v_cache + pos0 * kv_len));
-    // 4-6) token by token, as the step: q / k norms and IMROPE (k into its
-    // cache row), then attention over rows 0..pos and the gate (:585-684)
+    // By chunks of tokens: 4) q / k norms and IMROPE of each token
+    // (:585-642), k into its cache row, q into P_XN (free after the
+    // projections; n_head * head_dim = n_embd); 5-6) attention of token t over
+    // rows 0 .. pos0 + t and the gate (:647-684) in one launch per kernel for
+    // the chunk (causal: a token reads no row past its own). The pre-gate
+    // output goes to P_AO, written again by attn_output below.
     const size_t qf = 2 * D.nh * D.ahd, gw = D.nh * D.ahd;
-    for (int t = 0; t < nt; t++) {
-        const size_t pos = pos0 + t;
-        UQ_TRY(hip_st(uq::launch_attn_qk_prep(A[P_QF] + t * qf, at(UQ_NODE_Q), A[P_KR] + t * kv_len,
-                                              d_k_cache + pos * kv_len, w->attn_q_norm, w->attn_k_norm, ahd, nh, nkv,
-                                              (int)d->n_rot, d->theta_scale, pos, d->rms_eps, c.s),
+    const size_t chunk = attn_chunk(D, n_ctx_max, n_tokens);
+    for (size_t t0 = 0; t0 < n_tokens; t0 += chunk) {
+        const int rows = (int)std::min(chunk, n_tokens - t0);
+        const size_t n_last = pos0 + t0 + rows;  // positions seen by the chunk's last token
+        UQ_TRY(hip_st(uq::launch_attn_qk_prep(A[P_QF] + t0 * qf, A[P_XN] + t0 * gw, A[P_KR] + t0 * kv_len,
+                                              d_k_cache + (pos0 + t0) * kv_len, w->attn_q_norm, w->attn_k_norm, ahd,
+                                              nh, nkv, (int)d->n_rot, d->theta_scale, pos0 + t0, d->rms_eps, c.s,
+                                              rows),
                       fn));
-        UQ_TRY(hip_st(uq::launch_attn_decode(at(UQ_NODE_ATTN), at(UQ_NODE_SOFT), at(UQ_NODE_Q), d_k_cache, d_v_cache,
-                                             (int)pos + 1, nkv, ahd, nh / nkv, d->kq_scale, c.s,
-                                             A[P_QF] + t * qf + ahd, 2 * ahd, A[P_GT] + t * gw),
+        UQ_TRY(hip_st(uq::launch_attn_rows(A[P_AO] + t0 * gw, gw, A[P_SC], D.nh * n_last, A[P_XN] + t0 * gw, gw,
+                                           d_k_cache, d_v_cache, (int)(pos0 + t0 + 1), rows, nkv, ahd, nh / nkv,
+                                           d->kq_scale, c.s, A[P_QF] + t0 * qf + ahd, 2 * ahd, qf, A[P_GT] + t0 * gw,
+                                           gw),
                       fn));
     }
     // 7) attn_output of all tokens (:686-693); residual, FFN, l_out (:696-704)

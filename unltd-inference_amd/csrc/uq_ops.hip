@@ -154,12 +154,17 @@ __device__ double lds_tree(double *lv, int len) {
 constexpr int kSmChunk = 2 * OPS_TPB * kTreeRegs;  // 8192
 constexpr int kSmMaxChunks = 2048;
 static_assert((kSmChunk & (kSmChunk - 1)) == 0, "chunk trees must be nodes of the row tree");
-__global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const float *x, int n, float scale) {
+// Rows of token z = blockIdx.y (the attention of a prefill) are n + z dn
+// long and start zst floats after token z - 1's.
+__global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const float *x, int n, float scale, int dn,
+                                                          size_t zst) {
     __shared__ double lv[kSmChunk / 2];
     __shared__ double cs[kSmMaxChunks];
     __shared__ float red[OPS_TPB / 64];
-    const float *xr = x + (size_t)blockIdx.x * n;
-    float *yr = out + (size_t)blockIdx.x * n;
+    n += (int)blockIdx.y * dn;
+    const size_t row0 = (size_t)blockIdx.y * zst + (size_t)blockIdx.x * n;
+    const float *xr = x + row0;
+    float *yr = out + row0;
     float m = -INFINITY;
     for (int i = threadIdx.x; i < n; i += OPS_TPB) m = fmaxf(m, xr[i]);
     m = block_max_f(m, red);
@@ -628,13 +633,19 @@ constexpr int kAttnMaxGroup = 8;
 constexpr int kScoresPPB = 8;  // positions per workgroup (2 per wave)
 
 // scores[h][p] = (f32) dot_f32(q_h, K[p][kv]) for the group's heads; one
-// wave per position, E = hd / 64 values per lane.
+// wave per position, E = hd / 64 values per lane. Query z = blockIdx.z (of
+// a prefill) sees n_ctx + z positions; its q and scores are z q_st and
+// z sc_st floats on.
 template <int E>
 __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict__ scores, const float *__restrict__ q,
                                                               const float *__restrict__ kc, int n_ctx, int n_head_kv,
-                                                              int group) {
+                                                              int group, size_t q_st, size_t sc_st) {
     constexpr int HD = 64 * E;
     __shared__ float qs[kAttnMaxGroup * HD];
+    n_ctx += (int)blockIdx.z;
+    if (blockIdx.x * kScoresPPB >= (unsigned)n_ctx) return;  // the whole workgroup: past this query's positions
+    q += blockIdx.z * q_st;
+    scores += blockIdx.z * sc_st;
     const int kv = blockIdx.y, lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int t = threadIdx.x; t < group * HD; t += OPS_TPB) qs[t] = q[(size_t)kv * group * HD + t];
     __syncthreads();
@@ -676,16 +687,28 @@ constexpr int kPvCoop = 4;    // at most this many replays per wave run one colu
 constexpr int kPvChunk = 8;   // positions per lane loaded at once in such a replay
 template <int G>
 constexpr int pv_waves() { return G <= 4 ? 16 : 8; }  // the LDS partials stay within 64 KB
-// G: q heads per kv head, compile-time so that a batch's loads issue back to back
+// G: q heads per kv head, compile-time so that a batch's loads issue back to
+// back. Query z = blockIdx.z (of a prefill) sees n_ctx + z positions; its
+// soft, out, gz and gated rows are z times the strides in st on.
+struct PvStrides {
+    size_t soft, out, gz, gated;
+};
 template <int G>
 __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__restrict__ out,
                                                                     const float *__restrict__ soft,
                                                                     const float *__restrict__ vc, int n_ctx,
                                                                     int n_head_kv, int hd,
                                                                     const float *__restrict__ gz, int gzs,
-                                                                    float *__restrict__ gated) {
+                                                                    float *__restrict__ gated, PvStrides zs) {
     constexpr int group = G, kPvWaves = pv_waves<G>();
     __shared__ double part[2][kPvWaves][G][64];
+    n_ctx += (int)blockIdx.z;
+    soft += blockIdx.z * zs.soft;
+    out += blockIdx.z * zs.out;
+    if (gated) {
+        gz += blockIdx.z * zs.gz;
+        gated += blockIdx.z * zs.gated;
+    }
     const int kv = blockIdx.y, lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = blockIdx.x * 64 + lane;
     const size_t kv_len = (size_t)n_head_kv * hd;
@@ -899,17 +922,26 @@ __global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_kernel(
 // half of q head h (rmsnorm with attn_q_norm, as rmsnorm_kernel) into q_out
 // row h, workgroup n_head + j the raw k row of kv head j (attn_k_norm) into
 // k_out row j; then IMROPE rotates the row (as rope_imrope_kernel) before
-// it is stored.
+// it is stored. Token z = blockIdx.y (of a prefill) is at position pos + z,
+// its rows st[0..3] floats (qfull, q_out, k_raw, k_out) times z on.
 constexpr int kQkMaxHd = 512;
+struct QkStrides {
+    size_t qfull, q_out, k_raw, k_out;
+};
 __global__ __launch_bounds__(OPS_TPB) void attn_qk_prep_kernel(const float *__restrict__ qfull, float *__restrict__ q_out,
                                                              const float *__restrict__ k_raw, float *__restrict__ k_out,
                                                              const float *__restrict__ wq, const float *__restrict__ wk,
                                                              int hd, int n_head, int n_rot, double theta_scale,
-                                                             double pos, float eps) {
+                                                             double pos, float eps, QkStrides st) {
     __shared__ float rowv[kQkMaxHd];
     __shared__ double red[OPS_TPB / 64];
     __shared__ float bc;
     const int b = blockIdx.x;
+    qfull += blockIdx.y * st.qfull;
+    q_out += blockIdx.y * st.q_out;
+    k_raw += blockIdx.y * st.k_raw;
+    k_out += blockIdx.y * st.k_out;
+    pos += (double)blockIdx.y;
     const bool isq = b < n_head;
     const float *xr = isq ? qfull + (size_t)b * 2 * hd : k_raw + (size_t)(b - n_head) * hd;
     const float *w = isq ? wq : wk;
@@ -985,7 +1017,7 @@ int softmax_max_len() { return kSmChunk * kSmMaxChunks; }
 hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (n > softmax_max_len()) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale);
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale, 0, (size_t)0);
     return hipGetLastError();
 }
 
@@ -1062,25 +1094,29 @@ bool attn_shape_ok(int hd, int group) {
     return (hd == 64 || hd == 128 || hd == 256 || hd == 512) && group >= 1 && group <= kAttnMaxGroup;
 }
 
-hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
-                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s, const float *gz,
-                              int gzs, float *gated) {
-    if (n_ctx <= 0 || n_head_kv <= 0) return hipSuccess;
-    if (!attn_shape_ok(hd, group) || n_ctx > softmax_max_len()) return hipErrorInvalidValue;
-    const dim3 gs((n_ctx + kScoresPPB - 1) / kScoresPPB, n_head_kv);
+hipError_t launch_attn_rows(float *out, size_t out_st, float *soft, size_t soft_st, const float *q, size_t q_st,
+                            const float *kc, const float *vc, int n_ctx, int rows, int n_head_kv, int hd, int group,
+                            float kq_scale, hipStream_t s, const float *gz, int gzs, size_t gz_st, float *gated,
+                            size_t gated_st) {
+    if (n_ctx <= 0 || n_head_kv <= 0 || rows <= 0) return hipSuccess;
+    const int n_last = n_ctx + rows - 1;
+    if (!attn_shape_ok(hd, group) || n_last > softmax_max_len() || rows > 65535) return hipErrorInvalidValue;
+    const dim3 gs((n_last + kScoresPPB - 1) / kScoresPPB, n_head_kv, rows);
     switch (hd) {
-        case 64: hipLaunchKernelGGL(attn_scores_kernel<1>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
-        case 128: hipLaunchKernelGGL(attn_scores_kernel<2>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
-        case 256: hipLaunchKernelGGL(attn_scores_kernel<4>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
-        default: hipLaunchKernelGGL(attn_scores_kernel<8>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group); break;
+        case 64: hipLaunchKernelGGL(attn_scores_kernel<1>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+        case 128: hipLaunchKernelGGL(attn_scores_kernel<2>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+        case 256: hipLaunchKernelGGL(attn_scores_kernel<4>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+        default: hipLaunchKernelGGL(attn_scores_kernel<8>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale);
+    hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group, rows), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale,
+                       1, soft_st);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const dim3 gp(hd / 64, n_head_kv);
+    const dim3 gp(hd / 64, n_head_kv, rows);
+    const PvStrides pst{soft_st, out_st, gz_st, gated_st};
 #define UQ_PV(G) hipLaunchKernelGGL(attn_pv_kernel<G>, gp, dim3(pv_waves<G>() * 64), 0, s, out, soft, vc, n_ctx, \
-                                    n_head_kv, hd, gz, gzs, gated)
+                                    n_head_kv, hd, gz, gzs, gated, pst)
     switch (group) {
         case 1: UQ_PV(1); break;
         case 2: UQ_PV(2); break;
@@ -1093,6 +1129,13 @@ hipError_t launch_attn_decode(float *out, float *soft, const float *q, const flo
     }
 #undef UQ_PV
     return hipGetLastError();
+}
+
+hipError_t launch_attn_decode(float *out, float *soft, const float *q, const float *kc, const float *vc, int n_ctx,
+                              int n_head_kv, int hd, int group, float kq_scale, hipStream_t s, const float *gz,
+                              int gzs, float *gated) {
+    return launch_attn_rows(out, 0, soft, 0, q, 0, kc, vc, n_ctx, 1, n_head_kv, hd, group, kq_scale, s, gz, gzs, 0,
+                            gated, 0);
 }
 
 hipError_t launch_gdn_gates(const float *beta_raw, const float *alpha, const float *dt_bias, const float *a,
@@ -1134,11 +1177,14 @@ bool conv_norm_ok(int hd) { return hd >= 1 && hd <= kConvNormMaxHd; }
 
 hipError_t launch_attn_qk_prep(const float *qfull, float *q_out, const float *k_raw, float *k_out, const float *wq,
                                const float *wk, int hd, int n_head, int n_head_kv, int n_rot, double theta_scale,
-                               size_t pos, float eps, hipStream_t s) {
-    if (hd < 1 || hd > kQkMaxHd || n_rot > hd || n_rot % 2) return hipErrorInvalidValue;
-    if (n_head + n_head_kv == 0) return hipSuccess;
-    hipLaunchKernelGGL(attn_qk_prep_kernel, dim3(n_head + n_head_kv), dim3(OPS_TPB), 0, s, qfull, q_out, k_raw, k_out,
-                       wq, wk, hd, n_head, n_rot, theta_scale, (double)pos, eps);
+                               size_t pos, float eps, hipStream_t s, int rows) {
+    if (hd < 1 || hd > kQkMaxHd || n_rot > hd || n_rot % 2 || rows > 65535) return hipErrorInvalidValue;
+    if (n_head + n_head_kv == 0 || rows <= 0) return hipSuccess;
+    // rows of consecutive tokens: qfull [2 n_head hd], q_out [n_head hd],
+    // k_raw and k_out (cache rows) [n_head_kv hd]
+    const QkStrides st{(size_t)2 * n_head * hd, (size_t)n_head * hd, (size_t)n_head_kv * hd, (size_t)n_head_kv * hd};
+    hipLaunchKernelGGL(attn_qk_prep_kernel, dim3(n_head + n_head_kv, rows), dim3(OPS_TPB), 0, s, qfull, q_out, k_raw,
+                       k_out, wq, wk, hd, n_head, n_rot, theta_scale, (double)pos, eps, st);
     return hipGetLastError();
 }
 
