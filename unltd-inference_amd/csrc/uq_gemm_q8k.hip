@@ -449,7 +449,7 @@ size_t gemm_q8k_ws_bytes(const WeightsView &w, int M) {
 }
 
 hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *wsp, size_t wsb,
-                              hipStream_t s) {
+                              hipStream_t s, bool prepped) {
     if (M == 0 || w.dim_out == 0) return hipSuccess;
     if (w.dim_in == 0) {  // no blocks: every row's sum is sumf + sums[..] = 0
         const size_t MN = (size_t)M * w.dim_out;
@@ -462,13 +462,15 @@ hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float
     const int K = w.dim_in;
     const Q8Ws ws = q8_carve((uint8_t *)wsp, M, K);
     const bool q6 = w.dtype == UQ_Q6_K;
-    const dim3 pgrid(ws.Mp / 8, K / 256);
-    if (q6)
-        hipLaunchKernelGGL(gemm_q8k_prep_kernel<true>, pgrid, dim3(512), 0, s, X, K, M, ws);
-    else
-        hipLaunchKernelGGL(gemm_q8k_prep_kernel<false>, pgrid, dim3(512), 0, s, X, K, M, ws);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (!prepped) {
+        const dim3 pgrid(ws.Mp / 8, K / 256);
+        if (q6)
+            hipLaunchKernelGGL(gemm_q8k_prep_kernel<true>, pgrid, dim3(512), 0, s, X, K, M, ws);
+        else
+            hipLaunchKernelGGL(gemm_q8k_prep_kernel<false>, pgrid, dim3(512), 0, s, X, K, M, ws);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     return q6 ? q8k_shape<true>(w, M, ws, Y, s) : q8k_shape<false>(w, M, ws, Y, s);
 }
 

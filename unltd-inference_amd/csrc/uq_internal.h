@@ -214,7 +214,10 @@ hipError_t gemm_workspace(size_t need, hipStream_t s, uint8_t **buf, size_t *hav
 // workspace of wsb >= gemm_q8k_ws_bytes(w, M) bytes.
 hipError_t launch_gemm_q8k(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s);
 size_t gemm_q8k_ws_bytes(const WeightsView &w, int M);
+// prepped: ws already holds X quantized by the previous launch_gemm_q8k_ws
+// call on it (same X contents, M, K, and Q6_K-ness of the weights), so the
+// quantization is skipped.
 hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
-                              hipStream_t s);
+                              hipStream_t s, bool prepped = false);
 
 }  // namespace uq

@@ -256,13 +256,24 @@ size_t prefill_floats(const Dims &D, size_t n_ctx_max, size_t nt, size_t gemm_by
 
 // Projections of the prefill: Y[t] = gemv_quant_q8k(W, X[t]) for t < nt, on
 // the q8k GEMM kernels with the workspace carved from the layer workspace.
+// same_x: X is the previous call's input, unchanged since; its quantization
+// in the workspace is reused when the weights' format quantizes alike
+// (Q6_K or not) and K matches.
 struct PrefillCtx {
     const char *fn;
     hipStream_t s;
     uint8_t *gws;
     size_t gws_bytes;
-    uq_status gemm(uq_weights w, int nt, const float *X, float *Y) const {
-        return hip_st(uq::launch_gemm_q8k_ws(uq::view(*wh(w)), nt, X, Y, gws, gws_bytes, s), fn);
+    mutable const float *last_x = nullptr;
+    mutable size_t last_k = 0;
+    mutable int last_m = 0;
+    mutable bool last_q6 = false;
+    uq_status gemm(uq_weights w, int nt, const float *X, float *Y, bool same_x = false) const {
+        const uq::WeightsView v = uq::view(*wh(w));
+        const bool q6 = v.dtype == UQ_Q6_K;
+        const bool prepped = same_x && X == last_x && v.dim_in == last_k && nt == last_m && q6 == last_q6;
+        last_x = X, last_k = v.dim_in, last_m = nt, last_q6 = q6;
+        return hip_st(uq::launch_gemm_q8k_ws(v, nt, X, Y, gws, gws_bytes, s, prepped), fn);
     }
 };
 
@@ -276,7 +287,7 @@ uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_d
                                           A[P_AO], A[P_RES]),
                   c.fn));
     UQ_TRY(c.gemm(g, nt, A[P_PN], A[P_G]));
-    UQ_TRY(c.gemm(u, nt, A[P_PN], A[P_U]));
+    UQ_TRY(c.gemm(u, nt, A[P_PN], A[P_U], true));
     UQ_TRY(hip_st(uq::launch_swiglu(A[P_G], A[P_U], (size_t)nt * D.nff, A[P_H], c.s), c.fn));
     UQ_TRY(c.gemm(dn, nt, A[P_H], A[P_FO]));
     return hip_st(uq::launch_add(l_out, A[P_RES], A[P_FO], (size_t)nt * D.n, c.s), c.fn);
@@ -474,10 +485,10 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
     // 1-3) attn_norm of every token (:352-360), then qkv, z, beta, alpha of all
     // of them (:363-403)
     UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
-    UQ_TRY(c.gemm(w->attn_qkv, nt, A[P_XN], A[P_QKV]));
     UQ_TRY(c.gemm(w->attn_gate, nt, A[P_XN], A[P_Z]));
-    UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR]));
-    UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL]));
+    UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR], true));
+    UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL], true));
+    UQ_TRY(c.gemm(w->attn_qkv, nt, A[P_XN], A[P_QKV], true));
     // 4-6) the recurrent part: for head dims 64 and 128 the conv, norms and
     // gates of all tokens at once, the delta rule over the tokens in one
     // launch (the state held in registers between them), the gated norms of
@@ -538,8 +549,8 @@ uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w
     // v straight into the cache rows pos0 .. pos0 + n_tokens - 1 (:625-632)
     UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
     UQ_TRY(c.gemm(w->attn_q, nt, A[P_XN], A[P_QF]));
-    UQ_TRY(c.gemm(w->attn_k, nt, A[P_XN], A[P_KR]));
-    UQ_TRY(c.gemm(w->attn_v, nt, A[P_XN], d_v_cache + pos0 * kv_len));
+    UQ_TRY(c.gemm(w->attn_k, nt, A[P_XN], A[P_KR], true));
+    UQ_TRY(c.gemm(w->attn_v, nt, A[P_XN], d_v_cache + pos0 * kv_len, true));
     // By chunks of tokens: 4) q / k norms and IMROPE of each token
     // (:585-642), k into its cache row, q into P_XN (free after the
     // projections; n_head * head_dim = n_embd); 5-6) attention of token t over
