@@ -469,38 +469,42 @@ def bench_forward(hip, steps, warmup, st, ctx=512):
 
     # prefill: P tokens through the same 32 layers, one prefill call per layer
     # (projections and FFNs as q8k GEMMs over the P tokens, bit-identical to P
-    # steps); launched eagerly from the host
-    P = 128
-    xp = uq.DeviceArray.from_numpy(rng.standard_normal(P * n).astype(np.float32))
-    pa, pb = uq.DeviceArray(4 * P * n), uq.DeviceArray(4 * P * n)
-    pws = uq.DeviceArray(4 * max(L.prefill_ws_floats(d, P, gdn=w, n_ctx_max=0) if kind == "gdn" else
-                                 L.prefill_ws_floats(d, P, attn=w, n_ctx_max=ctx) for kind, w, _, _ in layers))
+    # steps); launched eagerly from the host. P = 128 and P = ctx (512).
+    def prefill_run(P):
+        xp = uq.DeviceArray.from_numpy(rng.standard_normal(P * n).astype(np.float32))
+        pa, pb = uq.DeviceArray(4 * P * n), uq.DeviceArray(4 * P * n)
+        pws = uq.DeviceArray(4 * max(L.prefill_ws_floats(d, P, gdn=w, n_ctx_max=0) if kind == "gdn" else
+                                     L.prefill_ws_floats(d, P, attn=w, n_ctx_max=ctx) for kind, w, _, _ in layers))
 
-    def prefill():
-        x = xp
-        for i, (kind, w, a, b) in enumerate(layers):
-            y = pa if i % 2 == 0 else pb
-            if kind == "gdn":
-                L.gdn_prefill(d, w, a, b, P, x, y, pws, s)
-            else:
-                L.attn_prefill(d, w, a, b, ctx, 0, P, x, y, pws, s)
-            x = y
+        def prefill():
+            x = xp
+            for i, (kind, w, a, b) in enumerate(layers):
+                y = pa if i % 2 == 0 else pb
+                if kind == "gdn":
+                    L.gdn_prefill(d, w, a, b, P, x, y, pws, s)
+                else:
+                    L.attn_prefill(d, w, a, b, ctx, 0, P, x, y, pws, s)
+                x = y
 
-    _, evp = timed(hip, prefill, 3, 1, s)
-    tp = evp * 1e-3 / 3
-    for a in keep + [ws, xa, xb, xn, xp, pa, pb, pws]:
+        _, evp = timed(hip, prefill, 3, 1, s)
+        tp = evp * 1e-3 / 3
+        for a in (xp, pa, pb, pws):
+            a.free()
+        return {"config": f"{P} tokens at positions 0..{P - 1} through the 32 layers (no head), one "
+                          f"uq_gdn_layer_prefill_d / uq_attn_layer_prefill_d call per layer, launched "
+                          f"eagerly; every output equals {P} one-token steps bit for bit",
+                "tokens": P, "ms": tp * 1e3, "tok_s": P / tp, "token_serial_ms_estimate": P * t * 1e3,
+                "speedup_vs_token_serial": P * t / tp}
+
+    pre = prefill_run(128)
+    pre512 = prefill_run(ctx)
+    for a in keep + [ws, xa, xb, xn]:
         a.free()
     return {"config": f"one decode token through the device-resident forward: 24 GatedDeltaNet + 8 attention "
                       f"layers of the synthetic hybrid 9B with their FFNs, result_norm and the Q6_K head, "
                       f"gemv_quant_q8k projections, attention at position {ctx - 1}; one HIP graph",
             "ms_per_token": t * 1e3, "tok_s": 1.0 / t, "weight_bytes_per_token": st.total,
-            "gbs": st.total / t / 1e9,
-            "prefill": {"config": f"{P} tokens at positions 0..{P - 1} through the 32 layers (no head), one "
-                                  f"uq_gdn_layer_prefill_d / uq_attn_layer_prefill_d call per layer, launched "
-                                  f"eagerly; every output equals {P} one-token steps bit for bit",
-                        "tokens": P, "ms": tp * 1e3, "tok_s": P / tp,
-                        "token_serial_ms_estimate": P * t * 1e3,
-                        "speedup_vs_token_serial": P * t / tp}}
+            "gbs": st.total / t / 1e9, "prefill": pre, f"prefill_{ctx}": pre512}
 
 
 def cpu_baseline(w, x):

@@ -440,29 +440,34 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
 #pragma unroll
     for (int r = 0; r < 16; r++) cs[r] = S[(size_t)r * dim];
     const size_t oq = (size_t)hq * dim + i0, ok = (size_t)(n_qk + hq) * dim + i0, ov = (size_t)(2 * n_qk + h) * dim + j;
-    float qn[16], kn[16], vn, gn, bn;  // the next token's inputs
-    auto fetch = [&](int t) {
+    // inputs of two tokens (ping-pong: token t in buffer t & 1, so the
+    // next token's loads land in registers no instruction of this token reads)
+    float qn[2][16], kn[2][16], vn[2], gn[2], bn[2];
+    auto fetch = [&](int t, int bsel) {
         const float4 *q4 = (const float4 *)(cv + (size_t)t * channels + oq);
         const float4 *k4 = (const float4 *)(cv + (size_t)t * channels + ok);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float4 a = q4[u], b = k4[u];
-            qn[4 * u] = a.x, qn[4 * u + 1] = a.y, qn[4 * u + 2] = a.z, qn[4 * u + 3] = a.w;
-            kn[4 * u] = b.x, kn[4 * u + 1] = b.y, kn[4 * u + 2] = b.z, kn[4 * u + 3] = b.w;
+            qn[bsel][4 * u] = a.x, qn[bsel][4 * u + 1] = a.y, qn[bsel][4 * u + 2] = a.z, qn[bsel][4 * u + 3] = a.w;
+            kn[bsel][4 * u] = b.x, kn[bsel][4 * u + 1] = b.y, kn[bsel][4 * u + 2] = b.z, kn[bsel][4 * u + 3] = b.w;
         }
-        vn = cv[(size_t)t * channels + ov];
-        gn = gexp[(size_t)t * n_v + h];
-        bn = beta[(size_t)t * n_v + h];
+        vn[bsel] = cv[(size_t)t * channels + ov];
+        gn[bsel] = gexp[(size_t)t * n_v + h];
+        bn[bsel] = beta[(size_t)t * n_v + h];
     };
     // (float) of the reference's sequential f64 sum over i < dim of cs_i x_i
     auto dot = [&](const float *x) {
-        double s = 0.0, ab = 0.0;
+        // four interleaved partial sums (the bound covers any order), then
+        // a fixed tree
+        double s4[4] = {0.0, 0.0, 0.0, 0.0}, a4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const double t = (double)__fmul_rn(cs[r], x[r]);
-            s += t;
-            ab += fabs(t);
+            s4[r & 3] += t;
+            a4[r & 3] += fabs(t);
         }
+        const double s = (s4[0] + s4[1]) + (s4[2] + s4[3]), ab = (a4[0] + a4[1]) + (a4[2] + a4[3]);
         const double Sc = col_sum_d<RB>(s), Ac = col_sum_d<RB>(ab);
         const double e = (double)(dim + 66) * 0x1p-52 * Ac;
         const float lo = (float)(Sc - e), hi = (float)(Sc + e);
@@ -470,31 +475,39 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         if (!__builtin_amdgcn_ballot_w64(undecided)) return lo;
 #pragma unroll
         for (int r = 0; r < 16; r++) prod[jc][i0 + r] = __fmul_rn(cs[r], x[r]);
-        __syncthreads();
+        // the workgroup is this one wave: wave-scope ordering of the LDS
+        // writes before the reads (a workgroup barrier would also wait for
+        // the next token's global loads)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float res = lo;
         if (undecided) {
             double q = 0.0;
             for (int i = 0; i < dim; i++) q += (double)prod[jc][i];
             res = (float)q;
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         return res;
     };
-    fetch(0);
-    for (int t = 0; t < nt; t++) {
-        float qc[16], kc[16];
+    auto step = [&](int t, int bsel) {
+        if (t + 1 < nt) fetch(t + 1, bsel ^ 1);
+        const float *kc = kn[bsel], *qc = qn[bsel];
 #pragma unroll
-        for (int r = 0; r < 16; r++) qc[r] = qn[r], kc[r] = kn[r];
-        const float vj = vn, g = gn, bt = bn;
-        if (t + 1 < nt) fetch(t + 1);
-#pragma unroll
-        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], g);
+        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], gn[bsel]);
         const float sum = dot(kc);
-        const float d = __fmul_rn(__fsub_rn(vj, sum), bt);
+        const float d = __fmul_rn(__fsub_rn(vn[bsel], sum), bn[bsel]);
 #pragma unroll
         for (int r = 0; r < 16; r++) cs[r] = __fadd_rn(cs[r], __fmul_rn(kc[r], d));
         const float o = dot(qc);
         if (m == 0) out[(size_t)t * n_v * dim + (size_t)h * dim + j] = __fmul_rn(o, scale);
+    };
+    fetch(0, 0);
+    for (int t = 0; t < nt; t += 2) {
+        step(t, 0);
+        if (t + 1 < nt) step(t + 1, 1);
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) S[(size_t)r * dim] = cs[r];
