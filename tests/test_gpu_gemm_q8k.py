@@ -84,9 +84,13 @@ def test_gemm_q8k_q6k_down_shape_every_row():
 SHAPES = [
     # (K, N, M): row tile 16 (M <= 16, and M = 31, 33, 65, 100 here, whose
     # 32-row grids are small), 64 (M = 200 at N = 8192: 256 tiles of 64 x
-    # 128), else 32 with six, two or one waves per workgroup
+    # 128), else 32 with six, two or one waves per workgroup. Where the
+    # 16 x 16 tiles number at most one per CU and K >= 2048 the K-parallel
+    # kernel runs (M = 31, 33, 65 here, and the FFN down shape at M = 8:
+    # 48 blocks over four waves)
     (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
     (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
+    (12288, 4096, 8), (2304, 48, 16),
 ]
 
 

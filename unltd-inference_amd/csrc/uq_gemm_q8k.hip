@@ -410,6 +410,267 @@ hipError_t q8k_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hip
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------ K-parallel kernel
+// For launches whose (16-row tile, 16 columns) grid leaves most SIMDs idle
+// (small M; the Q6_K down projection, N = 4096, K = 12288, at M <= 16 is
+// 256 single-wave workgroups each walking 48 blocks): KS waves per tile,
+// wave w forming the integer lane sums of blocks w, w + KS, w + 2 KS, ...
+// from its own two-slot LDS ring. The reference's epilogue is a chain over
+// the blocks per output and lane sum, sums[l] += d * sumi[l], but its terms
+// (d * sumi[l], rounded; the Q4_K min term) depend on one block each. So a
+// wave forms its block's terms, a round of KS blocks meets in LDS, and the
+// chains add the round's terms in block order, wave w running lane sums
+// w * 8 / KS .. + 8 / KS - 1 (wave 0 also the min-term chain). At the end
+// s = sumf + sums[0] + .. + sums[7] is added in that order. Each operation
+// is the main kernel's, so the bits are the same.
+template <int N>
+__device__ __forceinline__ void wait_vm_wave() {
+    static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <bool Q6, int KS>
+struct KparLay {
+    using L1 = Q8Lay<Q6, 1, 1>;  // one 16 x 16 tile: the slot of a wave's ring
+    static constexpr int RING = 2 * L1::SLOT;
+    static constexpr int TERMS = KS * 2 * L1::SLOT;  // terms [KS][9][64 lanes][4] floats
+    static constexpr int BYTES = TERMS + KS * 9 * 1024;
+    // loads one block issues (every one with lane 0 active, so each counts)
+    static constexpr int LOADS = L1::TM / 2 + L1::BROUNDS + (2 * L1::TM + 63) / 64 + 1;
+    static_assert(BYTES <= 160 * 1024, "LDS");
+};
+
+template <bool Q6, int KS>
+__global__ __launch_bounds__(64 * KS) void gemm_q8k_kpar_kernel(const uint8_t *__restrict__ W, uint32_t row_bytes,
+                                                                 int K, int N, int M, Q8Ws ws, int ntm, int ntn,
+                                                                 float *__restrict__ Y) {
+    using F = Q8Fmt<Q6>;
+    using KL = KparLay<Q6, KS>;
+    using Lay = typename KL::L1;
+    constexpr int TM = Lay::TM, CPR = F::CPR, LPW = 8 / KS;
+    static_assert(8 % KS == 0 && TM == 16, "lane sums split over the waves; 16-row tiles");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int t = threadIdx.x, lane = t & 63, lc = lane & 15, lq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int hq = lq >> 1, oq = lq & 1;
+
+    const int T = ntm * ntn, per = (T + 7) / 8;
+    const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if ((blockIdx.x >> 3) >= per || L >= T) return;  // the whole workgroup
+    const int mt = L % ntm, nt = L / ntm;
+    const int m0 = TM * mt, n0 = 16 * nt;
+    const int nblk = K >> 8, Mp = ws.Mp;
+    const size_t lane_a = ((size_t)(lane / TM) * Mp + lane % TM) * 16;
+    uint8_t *ring = lds + (size_t)wv * KL::RING;
+    float *terms = (float *)(lds + KL::TERMS);
+    auto tslot = [&](int w, int l) { return terms + ((size_t)(w * 9 + l) * 64 + lane) * 4; };
+
+    // this wave's loads of block b into slot (b / KS) & 1 of its ring
+    auto issue = [&](int b) {
+        uint8_t *sl = ring + ((b / KS) & 1) * Lay::SLOT;
+#pragma unroll
+        for (int p = 0; p < TM / 2; p++)
+            dma16(ws.a + ((size_t)(32 * b + (64 / TM) * p) * Mp + m0) * 16 + lane_a, sl + Lay::A + 1024 * p);
+#pragma unroll
+        for (int r = 0; r < Lay::BROUNDS; r++) {
+            const int c = 64 * r + lane;
+            if (c < 16 * CPR) {
+                const int col = c / CPR, part = c - col * CPR;
+                dma16(W + (size_t)min(n0 + col, N - 1) * row_bytes + (size_t)b * F::RB + 16 * part,
+                      sl + Lay::B + 1024 * r);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * TM; i += 64)
+            if (i + lane < 2 * TM) dma16(ws.bs + ((size_t)b * Mp + m0) * 32 + 16 * (i + lane), sl + Lay::BS + 16 * i);
+        if (lane < TM / 4) dma16(ws.d8 + (size_t)b * Mp + m0 + 4 * lane, sl + Lay::D8);
+    };
+
+    // the terms of block b (this wave's), into its terms slots: l = 0..7 the
+    // lane sums' d * sumi[l], 8 the Q4_K min term
+    const f4x zero4 = {};
+    auto block_terms = [&](int b) {
+        const uint8_t *sl = ring + ((b / KS) & 1) * Lay::SLOT;
+        const uint8_t *rc = sl + Lay::B + lc * (CPR * 16);  // this lane's column
+        auto afrag = [&](int l) { return *(const h8 *)(sl + Lay::A + (2 * l + hq) * 32 * TM + (oq * TM + lc) * 16); };
+        const float4 d8q = *(const float4 *)(sl + Lay::D8 + (4 * lq) * 4);
+        const float d8v[4] = {d8q.x, d8q.y, d8q.z, d8q.w};
+        float dd[4];
+        auto put = [&](int l, const f4x &acc) {
+            float4 o;
+            o.x = __fmul_rn(dd[0], acc[0]);
+            o.y = __fmul_rn(dd[1], acc[1]);
+            o.z = __fmul_rn(dd[2], acc[2]);
+            o.w = __fmul_rn(dd[3], acc[3]);
+            *(float4 *)tslot(wv, l) = o;
+        };
+        if constexpr (!Q6) {
+            const u4 hd = *(const u4 *)rc;
+            const float dw = f16_lo(hd.x), dmw = f16_hi(hd.x);
+            const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;
+            const u4 qa = *(const u4 *)(rc + 16 + 32 * lq), qb = *(const u4 *)(rc + 32 + 32 * lq);
+            const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            uint32_t Tg[8];
+            q8k_gather(w, 0, *(uint32_t(*)[4])Tg);
+            q8k_gather(w, 1, *(uint32_t(*)[4])(Tg + 4));
+            const int g4 = 2 * (lq & 1);
+            const uint32_t loA = (S0 >> (8 * (2 * lq))) & 63, loB = (S0 >> (8 * (2 * lq + 1))) & 63;
+            const uint32_t hiA = ((S2 >> (8 * g4)) & 0xF) | (((S0 >> (8 * g4 + 6)) & 3) << 4);
+            const uint32_t hiB = ((S2 >> (8 * (g4 + 1))) & 0xF) | (((S0 >> (8 * (g4 + 1) + 6)) & 3) << 4);
+            const float fa = (float)(lq < 2 ? loA : hiA), fb = (float)(lq < 2 ? loB : hiB);
+            const h2 lsc = h2_of(fa, fa), loff = h2_of(-1024.0f * fa, -1024.0f * fa);
+            const h2 hsc = h2_of(fb * 0.0625f, fb * 0.0625f), hoff = h2_of(-64.0f * fb, -64.0f * fb);
+            auto bop = [&](int l) {
+                uint32_t pp[4];
+                q4k_pairs(Tg[l], pp);
+                const h2 u0 = __builtin_elementwise_fma(as_h2(pp[0]), lsc, loff);
+                const h2 u1 = __builtin_elementwise_fma(as_h2(pp[1]), lsc, loff);
+                const h2 u2 = __builtin_elementwise_fma(as_h2(pp[2]), hsc, hoff);
+                const h2 u3 = __builtin_elementwise_fma(as_h2(pp[3]), hsc, hoff);
+                return h8{u0.x, u0.y, u1.x, u1.y, u2.x, u2.y, u3.x, u3.y};
+            };
+            h4 mB;
+            {
+                const _Float16 m0v = (_Float16)(float)q4k_m(S1, S2, 2 * lq), m1v = (_Float16)(float)q4k_m(S1, S2, 2 * lq + 1);
+                mB = h4{m0v, m0v, m1v, m1v};
+            }
+            const h4 bsA = *(const h4 *)(sl + Lay::BS + lc * 32 + 8 * lq);
+            const f4x mt4 = mfma16k16(bsA, mB, zero4);
+            float4 mo;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                dd[r] = __fmul_rn(d8v[r], dw);
+                (&mo.x)[r] = __fmul_rn(__fmul_rn(dmw, d8v[r]), mt4[r]);
+            }
+            *(float4 *)tslot(wv, 8) = mo;
+            f4x acc[2];
+            acc[0] = mfma16(afrag(0), bop(0), zero4);
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                if (l < 7) acc[(l + 1) & 1] = mfma16(afrag(l + 1), bop(l + 1), zero4);
+                put(l, acc[l & 1]);
+            }
+        } else {
+            const float dw = f16_lo(*(const uint16_t *)(rc + 208));
+            const u4 la = *(const u4 *)(rc + 32 * lq), lb = *(const u4 *)(rc + 32 * lq + 16);
+            const u4 ha = *(const u4 *)(rc + 128 + 32 * hq), hb = *(const u4 *)(rc + 128 + 32 * hq + 16);
+            const uint32_t wl[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+            const uint32_t wq[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+            uint32_t QL[8], QH[8];
+            q8k_gather(wl, 0, *(uint32_t(*)[4])QL);
+            q8k_gather(wl, 1, *(uint32_t(*)[4])(QL + 4));
+            q8k_gather(wq, 0, *(uint32_t(*)[4])QH);
+            q8k_gather(wq, 1, *(uint32_t(*)[4])(QH + 4));
+            const uint2 scw = *(const uint2 *)(rc + 192 + 8 * hq);
+            h2 se[2], so[2];
+#pragma unroll
+            for (int part = 0; part < 2; part++) {
+                const uint32_t v = (part ? scw.y : scw.x) >> (16 * oq);
+                const int s0 = (int)(int8_t)(v & 0xFF), s1 = (int)(int8_t)((v >> 8) & 0xFF);
+                se[part] = h2_of((float)(s0 & ~1), (float)(s1 & ~1));
+                so[part] = h2_of((float)(s0 & 1), (float)(s1 & 1));
+            }
+            const h2 off = h2_of(-1056.0f, -1056.0f);
+            auto lane6 = [&](int l) {
+                uint32_t ra, rb, pp[4];
+                q6k_raw(QL[l], QH[l], oq, ra, rb);
+                q6k_pairs(ra, pp);
+                q6k_pairs(rb, pp + 2);
+                h8 B1, B2;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const h2 q = as_h2(pp[k]) + off;
+                    const h2 e1 = q * se[k >> 1], e2 = q * so[k >> 1];
+                    B1[2 * k] = e1.x, B1[2 * k + 1] = e1.y;
+                    B2[2 * k] = e2.x, B2[2 * k + 1] = e2.y;
+                }
+                const h8 A = afrag(l);
+                return mfma16(A, B2, mfma16(A, B1, zero4));
+            };
+#pragma unroll
+            for (int r = 0; r < 4; r++) dd[r] = __fmul_rn(d8v[r], dw);
+            f4x acc[2];
+            acc[0] = lane6(0);
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                if (l < 7) acc[(l + 1) & 1] = lane6(l + 1);
+                put(l, acc[l & 1]);
+            }
+        }
+    };
+
+    float sums[LPW][4], sumf[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sumf[r] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LPW; k++) sums[k][r] = 0.0f;
+    }
+    const int nround = (nblk + KS - 1) / KS;
+    if (wv < nblk) issue(wv);
+    for (int r = 0; r < nround; r++) {
+        const int b = r * KS + wv;  // this wave's block of the round
+        if (b + KS < nblk) {
+            issue(b + KS);
+            wait_vm_wave<KL::LOADS>();  // block b landed (loads retire in issue order)
+        } else {
+            wait_vm_wave<0>();
+        }
+        if (b < nblk) block_terms(b);
+        __syncthreads();  // the round's terms are in LDS
+        const int nb = min(KS, nblk - r * KS);
+        for (int j = 0; j < nb; j++) {  // blocks in order
+#pragma unroll
+            for (int k = 0; k < LPW; k++) {
+                const float4 tv = *(const float4 *)tslot(j, wv * LPW + k);
+                sums[k][0] = __fadd_rn(sums[k][0], tv.x);
+                sums[k][1] = __fadd_rn(sums[k][1], tv.y);
+                sums[k][2] = __fadd_rn(sums[k][2], tv.z);
+                sums[k][3] = __fadd_rn(sums[k][3], tv.w);
+            }
+            if (!Q6 && wv == 0) {
+                const float4 tv = *(const float4 *)tslot(j, 8);
+                sumf[0] = __fsub_rn(sumf[0], tv.x);
+                sumf[1] = __fsub_rn(sumf[1], tv.y);
+                sumf[2] = __fsub_rn(sumf[2], tv.z);
+                sumf[3] = __fsub_rn(sumf[3], tv.w);
+            }
+        }
+        __syncthreads();  // every chain has read the round's terms
+    }
+
+    // s = sumf + sums[0] + ... + sums[7] (Q6_K: sumf is 0), in that order:
+    // each wave's lane sums to the terms area (slot (0, l)), then wave 0 adds
+#pragma unroll
+    for (int k = 0; k < LPW; k++)
+        *(float4 *)tslot(0, wv * LPW + k) = float4{sums[k][0], sums[k][1], sums[k][2], sums[k][3]};
+    __syncthreads();
+    if (wv != 0) return;
+    const int n = n0 + lc;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float sv = sumf[r];
+#pragma unroll
+        for (int l = 0; l < 8; l++) sv = __fadd_rn(sv, tslot(0, l)[r]);
+        const int m = m0 + 4 * lq + r;
+        if (m < M && n < N) Y[(size_t)m * N + n] = sv;
+    }
+}
+
+template <bool Q6, int KS>
+hipError_t q8k_kpar_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
+    using KL = KparLay<Q6, KS>;
+    const int K = w.dim_in, N = w.dim_out;
+    const int ntm = (M + 15) / 16, ntn = (N + 15) / 16;
+    const int grid = 8 * ((ntm * ntn + 7) / 8);
+    const void *k = (const void *)gemm_q8k_kpar_kernel<Q6, KS>;
+    hipError_t e = allow_lds(k, KL::BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemm_q8k_kpar_kernel<Q6, KS>), dim3(grid), dim3(64 * KS), KL::BYTES, s, w.bytes,
+                       (uint32_t)w.row_bytes, K, N, M, ws, ntm, ntn, Y);
+    return hipGetLastError();
+}
+
 // Rows per wave (and workgroup): 16 for M <= 16; 64 for M > 128 while the
 // 64 x 128 workgroup tiles number at least one per CU (eight waves, two per
 // SIMD: the B operands decoded once for 64 rows); 16 where 32-row tiles of
@@ -422,6 +683,9 @@ hipError_t q8k_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hip
 template <bool Q6, int RT>
 hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256, ntm = (M + 16 * RT - 1) / (16 * RT);
+    // 16-row tiles of 16 columns numbering at most one per CU, and K long
+    // enough to split: the K-parallel kernel, four waves per tile
+    if (RT == 1 && ntm * ((N + 15) / 16) <= cus && w.dim_in >= 8 * 256) return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     if (ntm * ((N + 95) / 96) >= 2 * cus) return q8k_launch<Q6, 6, RT>(w, M, ws, Y, s);
     if (ntm * ((N + 31) / 32) >= cus) return q8k_launch<Q6, 2, RT>(w, M, ws, Y, s);
     return q8k_launch<Q6, 1, RT>(w, M, ws, Y, s);
