@@ -87,10 +87,11 @@ SHAPES = [
     # 128), else 32 with six, two or one waves per workgroup. Where the
     # 16 x 16 tiles number at most one per CU and K >= 2048 the K-parallel
     # kernel runs (M = 31, 33, 65 here, and the FFN down shape at M = 8:
-    # 48 blocks over four waves)
+    # 48 blocks over four waves), and for M <= 32 at K > 8192 up to two per
+    # CU (M = 24 at K = 12288)
     (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
     (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
-    (12288, 4096, 8), (2304, 48, 16),
+    (12288, 4096, 8), (2304, 48, 16), (12288, 4096, 24),
 ]
 
 

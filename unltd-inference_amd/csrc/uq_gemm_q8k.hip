@@ -693,6 +693,10 @@ hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipS
 template <bool Q6>
 hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256;
+    // M <= 32 at long K (K > 8192: a 16- or 32-row wave would walk over 32
+    // blocks alone), up to two workgroups per CU: the K-parallel kernel
+    if (M <= 32 && ((M + 15) / 16) * ((N + 15) / 16) <= 2 * cus && w.dim_in > 8192)
+        return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     if (M <= 16) return q8k_width<Q6, 1>(w, M, ws, Y, s);
     if (M <= 128 && ((M + 31) / 32) * ((N + 31) / 32) <= 2 * cus && w.dim_in <= 8192)
         return q8k_width<Q6, 1>(w, M, ws, Y, s);
