@@ -165,6 +165,16 @@ def test_attn_prefill_small_equals_steps(nt, pos0, q6):
     m.free()
 
 
+@pytest.mark.parametrize("head_dim,n_head,n_head_kv", [(64, 8, 2), (512, 1, 1)])
+def test_attn_prefill_head_dims_equal_steps(head_dim, n_head, n_head_kv):
+    """Attention heads of 64 (the one-lane-per-position scores kernel at its
+    smallest tree) and of 512 (beyond it: the step's scores kernel over the
+    token dimension)."""
+    m = Model(dict(SMALL, n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim, n_rot=32), seed=53 + head_dim)
+    check_attn(m, 70, 4, n_ctx_max=128, seed=head_dim, what=f"attn head_dim={head_dim}")
+    m.free()
+
+
 def test_attn_prefill_chunked_equals_steps():
     """A context so long that the scores of 40 tokens exceed the prefill's
     2^24-float scores area: the attention runs in chunks of 15, 15 and 10

@@ -688,6 +688,66 @@ __global__ __launch_bounds__(OPS_TPB) void attn_scores_kernel(float *__restrict_
     }
 }
 
+// The pairwise tree (kernels.rs:21-42) of the N products x_i * y_i (exact
+// in f64), i in [B, B + N), N a power of two: both halves, then their sum,
+// the reference's adjacent-pair levels (it carries no odd tail at a power
+// of two). x a broadcast row in LDS, y the lane's row in LDS.
+template <int N, int B>
+__device__ __forceinline__ double tree_dot(const float *__restrict__ x, const float *__restrict__ y) {
+    if constexpr (N == 1)
+        return (double)x[B] * (double)y[B];
+    else
+        return tree_dot<N / 2, B>(x, y) + tree_dot<N / 2, B + N / 2>(x, y);
+}
+
+// Scores of a prefill chunk with one lane per position: the workgroup holds
+// the K rows of 64 positions (one kv head) in LDS and the q rows of up to qb
+// queries of the group's heads (at most 80 KB in all, so two workgroups
+// share a CU); wave w takes the (query, head)
+// pairs w, w + 4, ..., and each lane forms its position's whole dot as the
+// pairwise tree, with no exchange between lanes. Query z0 + zz sees n_ctx +
+// z0 + zz positions (causal). Each dot is the same tree of the same exact
+// products as attn_scores_kernel's, so the same bits; the lane butterflies
+// that bound that kernel are gone.
+constexpr int kLaneScoresPos = 64;
+template <int HD>
+__global__ __launch_bounds__(OPS_TPB) void attn_scores_lane_kernel(float *__restrict__ scores,
+                                                                   const float *__restrict__ q,
+                                                                   const float *__restrict__ kc, int n_ctx,
+                                                                   int n_head_kv, int group, size_t q_st,
+                                                                   size_t sc_st, int rows, int qb) {
+    constexpr int KP = HD + 1;  // K row pitch in floats: an odd pitch, no bank conflicts
+    extern __shared__ __align__(16) float qd[];  // [qb * group][HD], then K [64][KP]
+    const int p0 = blockIdx.x * kLaneScoresPos, kv = blockIdx.y, z0 = blockIdx.z * qb;
+    const int nz = min(qb, rows - z0), n_hi = n_ctx + z0 + nz - 1;  // positions of the block's last query
+    if (p0 >= n_hi) return;  // the whole workgroup
+    float *ks = qd + (size_t)qb * group * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gh = group * HD;
+    const size_t kv_len = (size_t)n_head_kv * HD;
+    for (int idx = tid; idx < kLaneScoresPos * (HD / 4); idx += OPS_TPB) {
+        const int r = idx / (HD / 4), c4 = idx - r * (HD / 4);
+        const int p = min(p0 + r, n_hi - 1);
+        const float4 v = *(const float4 *)(kc + (size_t)p * kv_len + (size_t)kv * HD + 4 * c4);
+        float *d = ks + r * KP + 4 * c4;
+        d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+    }
+    for (int idx = tid; idx < nz * gh; idx += OPS_TPB) {
+        const int zz = idx / gh, rr = idx - zz * gh;
+        qd[idx] = q[(size_t)(z0 + zz) * q_st + (size_t)kv * gh + rr];
+    }
+    __syncthreads();
+    const int p = p0 + lane;
+    const float *kr = ks + lane * KP;
+    for (int pair = wv; pair < nz * group; pair += OPS_TPB / 64) {
+        const int zz = pair / group, g = pair - zz * group;
+        const int nzc = n_ctx + z0 + zz;
+        if (p0 >= nzc) continue;  // no position of the tile for this query (wave-uniform)
+        const double sc = tree_dot<HD, 0>(qd + (size_t)pair * HD, kr);
+        if (p < nzc) scores[(size_t)(z0 + zz) * sc_st + (size_t)(kv * group + g) * nzc + p] = (float)sc;
+    }
+}
+
 // out[h][i] = (f32) of the sequential f64 sum over p of soft[h][p] * V[p][i]
 // (every product exact in f64). Lane = column i, the waves split p; the
 // partial sums S and absolute sums A meet in LDS. Any summation order of
@@ -1114,12 +1174,31 @@ hipError_t launch_attn_rows(float *out, size_t out_st, float *soft, size_t soft_
     if (n_ctx <= 0 || n_head_kv <= 0 || rows <= 0) return hipSuccess;
     const int n_last = n_ctx + rows - 1;
     if (!attn_shape_ok(hd, group) || n_last > softmax_max_len() || rows > 65535) return hipErrorInvalidValue;
-    const dim3 gs((n_last + kScoresPPB - 1) / kScoresPPB, n_head_kv, rows);
-    switch (hd) {
-        case 64: hipLaunchKernelGGL(attn_scores_kernel<1>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
-        case 128: hipLaunchKernelGGL(attn_scores_kernel<2>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
-        case 256: hipLaunchKernelGGL(attn_scores_kernel<4>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
-        default: hipLaunchKernelGGL(attn_scores_kernel<8>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+    if (rows > 1 && hd <= 256) {
+        // a prefill chunk: lane-per-position dots, blocks of qb queries whose
+        // q rows and the 64 K rows fit 80 KB of LDS
+        const size_t kbytes = (size_t)kLaneScoresPos * (hd + 1) * 4;
+        const int qb = (int)std::max<size_t>(1, std::min<size_t>(8, (80 * 1024 - kbytes) / ((size_t)group * hd * 4)));
+        const size_t lds = (size_t)qb * group * hd * 4 + kbytes;
+        const dim3 gl((n_last + kLaneScoresPos - 1) / kLaneScoresPos, n_head_kv, (rows + qb - 1) / qb);
+        hipError_t e = hipSuccess;
+        auto go = [&](const void *k, auto launch) {
+            if ((e = allow_lds(k, lds)) == hipSuccess) launch();
+        };
+        switch (hd) {
+            case 64: go((const void *)attn_scores_lane_kernel<64>, [&] { hipLaunchKernelGGL(attn_scores_lane_kernel<64>, gl, dim3(OPS_TPB), lds, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st, rows, qb); }); break;
+            case 128: go((const void *)attn_scores_lane_kernel<128>, [&] { hipLaunchKernelGGL(attn_scores_lane_kernel<128>, gl, dim3(OPS_TPB), lds, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st, rows, qb); }); break;
+            default: go((const void *)attn_scores_lane_kernel<256>, [&] { hipLaunchKernelGGL(attn_scores_lane_kernel<256>, gl, dim3(OPS_TPB), lds, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st, rows, qb); }); break;
+        }
+        if (e != hipSuccess) return e;
+    } else {
+        const dim3 gs((n_last + kScoresPPB - 1) / kScoresPPB, n_head_kv, rows);
+        switch (hd) {
+            case 64: hipLaunchKernelGGL(attn_scores_kernel<1>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+            case 128: hipLaunchKernelGGL(attn_scores_kernel<2>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+            case 256: hipLaunchKernelGGL(attn_scores_kernel<4>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+            default: hipLaunchKernelGGL(attn_scores_kernel<8>, gs, dim3(OPS_TPB), 0, s, soft, q, kc, n_ctx, n_head_kv, group, q_st, soft_st); break;
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
