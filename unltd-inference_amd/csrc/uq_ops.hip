@@ -493,7 +493,10 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         return res;
     };
     auto step = [&](int t, int bsel) {
-        if (t + 1 < nt) fetch(t + 1, bsel ^ 1);
+        // unconditional (the last token fetches itself again): a fetch under
+        // a branch makes the compiler's load counters assume the branch not
+        // taken, and this token's reads then wait for the next token's loads
+        fetch(min(t + 1, nt - 1), bsel ^ 1);
         const float *kc = kn[bsel], *qc = qn[bsel];
 #pragma unroll
         for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], gn[bsel]);
@@ -502,7 +505,9 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
 #pragma unroll
         for (int r = 0; r < 16; r++) cs[r] = __fadd_rn(cs[r], __fmul_rn(kc[r], d));
         const float o = dot(qc);
-        if (m == 0) out[(size_t)t * n_v * dim + (size_t)h * dim + j] = __fmul_rn(o, scale);
+        // every lane of the column holds o: all store it (the same value to
+        // the same address), with no branch around the store
+        out[(size_t)t * n_v * dim + (size_t)h * dim + j] = __fmul_rn(o, scale);
     };
     fetch(0, 0);
     for (int t = 0; t < nt; t += 2) {
