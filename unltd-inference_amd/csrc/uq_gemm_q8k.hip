@@ -683,9 +683,6 @@ hipError_t q8k_kpar_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y
 template <bool Q6, int RT>
 hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256, ntm = (M + 16 * RT - 1) / (16 * RT);
-    // 16-row tiles of 16 columns numbering at most one per CU, and K long
-    // enough to split: the K-parallel kernel, four waves per tile
-    if (RT == 1 && ntm * ((N + 15) / 16) <= cus && w.dim_in >= 8 * 256) return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     if (ntm * ((N + 95) / 96) >= 2 * cus) return q8k_launch<Q6, 6, RT>(w, M, ws, Y, s);
     if (ntm * ((N + 31) / 32) >= cus) return q8k_launch<Q6, 2, RT>(w, M, ws, Y, s);
     return q8k_launch<Q6, 1, RT>(w, M, ws, Y, s);
@@ -693,6 +690,10 @@ hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipS
 template <bool Q6>
 hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256;
+    // 16-row tiles of 16 columns numbering at most one per CU, and K long
+    // enough to split (the 32-wide projections of a prefill, for one): the
+    // K-parallel kernel, four waves per tile
+    if (((M + 15) / 16) * ((N + 15) / 16) <= cus && w.dim_in >= 8 * 256) return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     // M <= 32 at long K (K > 8192: a 16- or 32-row wave would walk over 32
     // blocks alone), up to two workgroups per CU: the K-parallel kernel
     if (M <= 32 && ((M + 15) / 16) * ((N + 15) / 16) <= 2 * cus && w.dim_in > 8192)
