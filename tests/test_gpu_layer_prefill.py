@@ -175,6 +175,19 @@ def test_attn_prefill_head_dims_equal_steps(head_dim, n_head, n_head_kv):
     m.free()
 
 
+@pytest.mark.parametrize("shape,nt", [
+    (dict(n_embd=768, n_v_heads=12, n_head=6, n_head_kv=2, head_dim=128), 37),
+    (dict(n_head=8, n_head_kv=1, head_dim=64), 19),
+    (dict(n_embd=1280, n_v_heads=20, n_head=5, n_head_kv=1, head_dim=256), 23)])
+def test_attn_prefill_head_groups_equal_steps(shape, nt):
+    """Head groups of 3, 8 and 5 q heads per kv head: the prefill's pv
+    kernel takes 16 / group queries per workgroup (5, 2 and 3 here), the
+    last block of each run partly filled."""
+    m = Model(dict(SMALL, **shape), seed=61 + shape["n_head"])
+    check_attn(m, nt, 5, n_ctx_max=96, seed=shape["n_head"], what=f"attn {shape}")
+    m.free()
+
+
 def test_attn_prefill_chunked_equals_steps():
     """A context so long that the scores of 40 tokens exceed the prefill's
     2^24-float scores area: the attention runs in chunks of 15, 15 and 10

@@ -911,6 +911,169 @@ __global__ __launch_bounds__(pv_waves<G>() * 64) void attn_pv_kernel(float *__re
     }
 }
 
+// attn_pv_kernel for a prefill chunk: a workgroup takes the NP = (16 / G) *
+// G (query, head) pairs of QB = 16 / G consecutive queries and the G heads
+// of kv head blockIdx.y, lane = column blockIdx.x * 64 + lane, so each V
+// load serves all NP pairs. Wave w takes the 16-position batches w, w + 4,
+// ...; a pair's soft values of a batch are uniform (scalar) loads. Each
+// product is exact in f64, so S += s * v and A += |s * v| are single fused
+// multiply-adds with the values of the separate multiply and add. The four
+// waves' S and A meet in LDS, then the bound decides each output as in
+// attn_pv_kernel, or the lane replays the sequential sum.
+constexpr int kPvRowsWaves = 4, kPvRowsBatch = 16;
+template <int G>
+__global__ __launch_bounds__(kPvRowsWaves * 64) void attn_pv_rows_kernel(
+    float *__restrict__ out, const float *__restrict__ soft, const float *__restrict__ vc, int n_ctx, int n_head_kv,
+    int hd, int rows, const float *__restrict__ gz, int gzs, float *__restrict__ gated, PvStrides zs) {
+    constexpr int QB = 16 / G, NP = QB * G;
+    __shared__ double part[kPvRowsWaves][NP][64];
+    static_assert(NP >= kPvChunk, "a wave's part rows hold its replay chunk");
+    const int kv = blockIdx.y, lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int z0 = blockIdx.z * QB, nz = min(QB, rows - z0);
+    const int i = blockIdx.x * 64 + lane;
+    const size_t kv_len = (size_t)n_head_kv * hd;
+    const float *vcol = vc + (size_t)kv * hd + i;
+    const int n_hi = n_ctx + z0 + nz - 1;  // positions of the block's last query
+    // soft row of pair q: query z0 + q / G, head kv * G + q % G
+    auto srow = [&](int q) {
+        const int zz = q / G, nzc = n_ctx + z0 + zz;
+        return soft + (size_t)(z0 + zz) * zs.soft + (size_t)(kv * G + q % G) * nzc;
+    };
+    double S[NP], A[NP];
+#pragma unroll
+    for (int q = 0; q < NP; q++) S[q] = A[q] = 0.0;
+    for (int pb = w * kPvRowsBatch; pb < n_hi; pb += kPvRowsWaves * kPvRowsBatch) {
+        double vd[kPvRowsBatch];
+#pragma unroll
+        for (int u = 0; u < kPvRowsBatch; u++) vd[u] = (double)vcol[(size_t)min(pb + u, n_hi - 1) * kv_len];
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int zz = q / G, nzc = n_ctx + z0 + zz;
+            if (zz >= nz || pb >= nzc) continue;  // wave-uniform
+            const float *sr = srow(q) + pb;
+            if (pb + kPvRowsBatch <= nzc) {
+#pragma unroll
+                for (int u = 0; u < kPvRowsBatch; u++) {
+                    const double sv = (double)sr[u];
+                    S[q] = fma(sv, vd[u], S[q]);
+                    A[q] = fma(fabs(sv), fabs(vd[u]), A[q]);
+                }
+            } else {
+                const int m = nzc - pb;
+#pragma unroll
+                for (int u = 0; u < kPvRowsBatch; u++)
+                    if (u < m) {
+                        const double sv = (double)sr[u];
+                        S[q] = fma(sv, vd[u], S[q]);
+                        A[q] = fma(fabs(sv), fabs(vd[u]), A[q]);
+                    }
+            }
+        }
+    }
+    // the waves' partials: S, then A, through the one LDS array
+    double st[(NP + kPvRowsWaves - 1) / kPvRowsWaves], at[(NP + kPvRowsWaves - 1) / kPvRowsWaves];
+#pragma unroll
+    for (int ph = 0; ph < 2; ph++) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) part[w][q][lane] = ph == 0 ? S[q] : A[q];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < (NP + kPvRowsWaves - 1) / kPvRowsWaves; k++) {
+            const int q = w + kPvRowsWaves * k;
+            double t = 0.0;
+            if (q < NP)
+#pragma unroll
+                for (int u = 0; u < kPvRowsWaves; u++) t += part[u][q][lane];
+            (ph == 0 ? st : at)[k] = t;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < (NP + kPvRowsWaves - 1) / kPvRowsWaves; k++) {
+        const int q = w + kPvRowsWaves * k;
+        if (q >= NP) break;
+        const int zz = q / G, g = q % G, nzc = n_ctx + z0 + zz;
+        if (zz >= nz) break;  // wave-uniform; later k only higher zz
+        const double e = (double)(nzc + 66) * 0x1p-52 * at[k];
+        const float lo = (float)(st[k] - e), hi = (float)(st[k] + e);
+        float r = lo;
+        // the reference's sequential sum where the bound cannot decide
+        const bool need = __float_as_uint(lo) != __float_as_uint(hi);
+        unsigned long long mask = __ballot(need);
+        const float *sr = srow(q);
+        if (__popcll(mask) > kPvCoop) {
+            // many columns: each lane replays its own
+            if (need) {
+                double qs = 0.0;
+                for (int p0 = 0; p0 < nzc; p0 += 16) {
+                    float vb[16], sb[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        const int p = min(p0 + u, nzc - 1);
+                        vb[u] = vcol[(size_t)p * kv_len];
+                        sb[u] = sr[p];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; u++)
+                        if (p0 + u < nzc) qs += (double)sb[u] * (double)vb[u];
+                }
+                r = (float)qs;
+            }
+        } else {
+            // a few columns, one at a time: every lane forms the products of
+            // its positions (loads in parallel) into the wave's LDS scratch
+            // (part is free after the reductions), then all lanes add them in
+            // position order (broadcast reads; the same sum in each lane)
+            double *buf = &part[w][0][0];
+            while (mask) {
+                const int l = __ffsll(mask) - 1;
+                mask &= mask - 1;
+                const float *vl = vc + (size_t)kv * hd + blockIdx.x * 64 + l;
+                double qs = 0.0;
+                for (int p0 = 0; p0 < nzc; p0 += 64 * kPvChunk) {
+#pragma unroll
+                    for (int c = 0; c < kPvChunk; c++) {
+                        const int p = min(p0 + 64 * c + lane, nzc - 1);
+                        buf[64 * c + lane] = (double)sr[p] * (double)vl[(size_t)p * kv_len];
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    const int m = min(64 * kPvChunk, nzc - p0);
+                    // the reads of the next eight values issue before the adds of these eight
+                    int p = 0;
+                    double bb[8];
+                    if (m >= 8) {
+#pragma unroll
+                        for (int u = 0; u < 8; u++) bb[u] = buf[u];
+                    }
+                    for (; p + 8 <= m; p += 8) {
+                        double nb[8];
+                        const int pn = p + 16 <= m ? p + 8 : p;  // the last group rereads itself
+#pragma unroll
+                        for (int u = 0; u < 8; u++) nb[u] = buf[pn + u];
+#pragma unroll
+                        for (int u = 0; u < 8; u++) qs += bb[u];
+#pragma unroll
+                        for (int u = 0; u < 8; u++) bb[u] = nb[u];
+                    }
+                    for (; p < m; p++) qs += buf[p];
+                    // every lane's reads are done before the next chunk's writes
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+                if (lane == l) r = (float)qs;
+            }
+        }
+        float *o = out + (size_t)(z0 + zz) * zs.out;
+        o[(size_t)(kv * G + g) * hd + i] = r;
+        if (gated)
+            gated[(size_t)(z0 + zz) * zs.gated + (size_t)(kv * G + g) * hd + i] =
+                __fmul_rn(r, sigmoid1(gz[(size_t)(z0 + zz) * zs.gz + (size_t)(kv * G + g) * gzs + i]));
+    }
+}
+
 // ---- glue of the layer forward (qwen35_forward.rs:333-710) ----------------
 // GatedDeltaNet gates (:405-419): beta = sigmoid(beta_raw), sp =
 // softplus(alpha + dt_bias), gate = sp * a, per v head.
@@ -1210,8 +1373,26 @@ hipError_t launch_attn_rows(float *out, size_t out_st, float *soft, size_t soft_
     hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group, rows), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale,
                        1, soft_st);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const dim3 gp(hd / 64, n_head_kv, rows);
     const PvStrides pst{soft_st, out_st, gz_st, gated_st};
+    if (rows > 1) {
+        // a prefill chunk: 16 / group queries per workgroup
+#define UQ_PVR(G) hipLaunchKernelGGL(attn_pv_rows_kernel<G>, dim3(hd / 64, n_head_kv, (rows + 16 / G - 1) / (16 / G)), \
+                                     dim3(kPvRowsWaves * 64), 0, s, out, soft, vc, n_ctx, n_head_kv, hd, rows, gz, gzs, \
+                                     gated, pst)
+        switch (group) {
+            case 1: UQ_PVR(1); break;
+            case 2: UQ_PVR(2); break;
+            case 3: UQ_PVR(3); break;
+            case 4: UQ_PVR(4); break;
+            case 5: UQ_PVR(5); break;
+            case 6: UQ_PVR(6); break;
+            case 7: UQ_PVR(7); break;
+            default: UQ_PVR(8); break;
+        }
+#undef UQ_PVR
+        return hipGetLastError();
+    }
+    const dim3 gp(hd / 64, n_head_kv, rows);
 #define UQ_PV(G) hipLaunchKernelGGL(attn_pv_kernel<G>, gp, dim3(pv_waves<G>() * 64), 0, s, out, soft, vc, n_ctx, \
                                     n_head_kv, hd, gz, gzs, gated, pst)
     switch (group) {
