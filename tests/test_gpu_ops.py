@@ -70,6 +70,51 @@ def test_rmsnorm_rows_on_device_and_the_boundary_replay():
                    "rmsnorm midpoint")
 
 
+def undecided_row(rng, n, above):
+    """A row of n random values whose sequential f64 sum of f32 squares (the
+    reference's order) lies a few ulps from n times an f32 midpoint, well
+    inside the device's bound, so the tree-sum bound cannot decide the mean
+    and the device replays the sequential loop; above: the sum lands on the
+    side of the midpoint that rounds up (a replay that is skipped, or drops
+    or repeats a term, gives the wrong bits). The last two values steer the
+    sum."""
+    x = rng.standard_normal(n).astype(np.float32)
+    P = 0.0
+    for v in x[:n - 2]:
+        P += float(np.float32(v) * np.float32(v))
+    a = np.float32(P / n * (1 + 2.0 ** -16))
+    mid = (float(a) + float(np.nextafter(a, np.float32(np.inf)))) / 2  # exact in f64
+    T = mid * n
+    e = (n + 66) * 2.0 ** -52 * T
+    target = T + (3 if above else -3) * 2.0 ** -52 * T
+    v = np.float32(np.sqrt((target - P) * (1 - 2.0 ** -20)))
+    P1 = P + float(v * v)
+    w = np.float32(np.sqrt(target - P1))
+    x[n - 2], x[n - 1] = v, w
+    S = P1 + float(w * w)
+    assert abs(S - T) < e / 4 and (S > T) == above, (S, T, e)
+    return x
+
+
+@pytest.mark.parametrize("n", [4096, 5000, 12288])
+def test_rmsnorm_rows_replay_the_sequential_sum(n):
+    """Rows whose mean the bound cannot decide, the sum over thousands of
+    random squares: the replay's result must be the reference's bit for bit
+    (both sides of the midpoint; decided rows between them)."""
+    rng = np.random.default_rng(n + 17)
+    X = np.stack([undecided_row(rng, n, above=r % 2 == 0) if r % 3 != 2 else rng.standard_normal(n).astype(np.float32)
+                  for r in range(6)])
+    w = rng.standard_normal(n).astype(np.float32)
+    dx, dw, dy = dev(X), dev(w), uq.DeviceArray(4 * n * len(X))
+    ops.rmsnorm_d(dy, dx, dw, n, len(X), 1e-30)
+    uq.synchronize()
+    got = dy.download(np.float32, n * len(X)).reshape(len(X), n)
+    for r in range(len(X)):
+        assert_bitwise(got[r], O.rmsnorm(X[r], w, 1e-30), f"rmsnorm replay row {r} n={n}")
+    for a in (dx, dw, dy):
+        a.free()
+
+
 def test_l2_norm_rows_bit_exact_and_boundary():
     rng = np.random.default_rng(6)
     dim, rows = 128, 64

@@ -348,20 +348,36 @@ __device__ double block_sum_d(double v, double *red) {
 
 // The f32 result of a sequential f64 sum of the n non-negative values
 // sq[i] (f32 squares), mapped through finish(): finish(lo) == finish(hi)
-// proves the result; otherwise thread 0 replays the loop. Every thread
-// returns the same value.
+// proves the result; otherwise wave 0 replays the loop: its lanes load 64
+// values at a time (the next 64 in flight while these are added) and every
+// lane adds them in order, each taken from its lane by readlane, so the
+// only serial part is the chain of adds. Every thread returns the same
+// value.
 template <int TPB, class Val, class Finish>
 __device__ float seq_sum_f32(Val val, int n, double S, Finish finish, float *bcast) {
     const double e = (double)(n + 66) * 0x1p-52 * S;  // twice the bound, covering the roundings of S +- e
     const float a = finish(S - e), b = finish(S + e);
     if (__float_as_uint(a) == __float_as_uint(b)) return a;  // -0 and +0 differ: replay
-    if (threadIdx.x == 0) {
-        double s = 0.0;
-        for (int i = 0; i < n; i++) {
+    if (threadIdx.x < 64) {  // wave 0, all of it
+        const int lane = threadIdx.x;
+        auto sq = [&](int i) {
+            if (i >= n) return 0.0f;
             const float v = val(i);
-            s += (double)__fmul_rn(v, v);
+            return __fmul_rn(v, v);
+        };
+        double s = 0.0;
+        float nx = sq(lane);
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int cur = __float_as_int(nx);
+            nx = sq(c0 + 64 + lane);
+            if (n - c0 >= 64) {
+#pragma unroll
+                for (int k = 0; k < 64; k++) s += (double)__int_as_float(__builtin_amdgcn_readlane(cur, k));
+            } else {
+                for (int k = 0; k < n - c0; k++) s += (double)__int_as_float(__builtin_amdgcn_readlane(cur, k));
+            }
         }
-        *bcast = finish(s);
+        if (lane == 0) *bcast = finish(s);
     }
     __syncthreads();
     const float r = *bcast;

@@ -9,7 +9,7 @@
 // both lie within (n + log2 n + 2) * 2^-53 * S of the exact sum, so when
 // both ends of [S - e, S + e] round to the same f32 result (rounding is
 // monotonic), that is the reference's result. Otherwise (probability about
-// n * 2^-29 per row) one lane replays the sequential loop.
+// n * 2^-29 per row) one wave replays the sequential loop.
 //
 // Transcendentals: f32 exp / log are evaluated in f64 and rounded once
 // (correctly rounded but for rare near-midpoint arguments), and the rope
