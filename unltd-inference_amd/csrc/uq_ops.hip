@@ -407,47 +407,57 @@ __global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_rows_kernel(
     for (int j = threadIdx.x; j < hd; j += OPS_TPB) cv[(size_t)t * channels + b * hd + j] = __fmul_rn(vals[j], scale);
 }
 
-// The delta rule (gdn_step_wg_kernel) of nt tokens, token after token, one
-// wave per workgroup and no exchange between waves: lane l holds rows
-// [16 m, 16 m + 16), m = l % RB (RB = dim / 16 lanes per column), of column
-// j = (64 / RB) blockIdx.x + l / RB of v head blockIdx.y's state, in VGPRs
-// for all the tokens. Each f64 dot is the lane's 16 terms in row order,
-// then an xor tree over the column's RB lanes, with the bound of the step
-// kernel: when both ends of [S - e, S + e] round to one f32 that is the
-// reference's (float) of its sequential sum; otherwise the column's products
-// go through LDS and every lane of it sums them in the reference's order.
-// Token t's q and k (normalised) and v are row t of cv, its beta and
-// exp(gate) row t of beta / gexp; the next token's are loaded while this
-// one is processed. out[t] receives o * scale (before the gated rmsnorm).
+// The delta rule (gdn_step_wg_kernel) of nt tokens, token after token, with
+// no exchange between waves: lane l of wave w holds rows [R m, R m + R),
+// m = l % RB (RB = dim / R lanes per column), of column j = (64 / RB)
+// (kScanWaves blockIdx.x + w) + l / RB of v head blockIdx.y's state, in
+// VGPRs for all the tokens. Each f64 dot is the lane's R terms, then a
+// fixed tree over the column's RB lanes, with the bound of the step kernel: when
+// both ends of [S - e, S + e] round to one f32 that is the reference's
+// (float) of its sequential sum; otherwise the column's products go through
+// the wave's LDS rows and every lane of the column sums them in the
+// reference's order. Token t's q and k (normalised) and v are row t of cv,
+// its beta and exp(gate) row t of beta / gexp; the next token's are loaded
+// while this one is processed. out[t] receives o * scale (before the gated
+// rmsnorm). The waves of a workgroup share nothing but are four to a
+// workgroup so that they sit on the CU's four SIMDs: eight rows per lane
+// (twice the waves of sixteen, half the instructions each) measured 294 us
+// for 512 tokens of a 128-dim head as single-wave workgroups, which the
+// hardware doubled up on SIMDs, as sixteen rows per lane did (288 us), and
+// 226 us four to a workgroup.
+constexpr int kScanWaves = 4;
 template <int RB>
 __device__ __forceinline__ double col_sum_d(double v) {
     v += dpp_d<0xB1>(v);
     v += dpp_d<0x4E>(v);
-    if constexpr (RB == 8) v += dpp_d<0x141>(v);
+    if constexpr (RB >= 8) v += dpp_d<0x141>(v);
+    if constexpr (RB == 16) v += dpp_d<0x140>(v);
     return v;
 }
-template <int RB>
-__global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ cv, const float *__restrict__ beta,
+template <int RB, int R>
+__global__ __launch_bounds__(64 * kScanWaves) void gdn_scan_kernel(const float *__restrict__ cv, const float *__restrict__ beta,
                                                       const float *__restrict__ gexp, float *__restrict__ state,
                                                       float *__restrict__ out, int nt, int channels, int n_qk,
                                                       int n_v, float scale) {
-    constexpr int dim = 16 * RB, CPW = 64 / RB;  // columns per wave
-    __shared__ float prod[CPW][dim];             // a column's products, for the ordered replay
-    const int lane = threadIdx.x, m = lane % RB, jc = lane / RB, h = blockIdx.y, hq = h % n_qk;
-    const int j = blockIdx.x * CPW + jc, i0 = 16 * m;
+    constexpr int dim = R * RB, CPW = 64 / RB;  // columns per wave
+    __shared__ float prodw[kScanWaves][CPW][dim];  // per wave: a column's products, for the ordered replay
+    const int wv = (int)(threadIdx.x >> 6);
+    float (*prod)[dim] = prodw[wv];
+    const int lane = threadIdx.x & 63, m = lane % RB, jc = lane / RB, h = blockIdx.y, hq = h % n_qk;
+    const int j = (blockIdx.x * kScanWaves + wv) * CPW + jc, i0 = R * m;
     float *S = state + (size_t)h * dim * dim + (size_t)i0 * dim + j;
-    float cs[16];
+    float cs[R];
 #pragma unroll
-    for (int r = 0; r < 16; r++) cs[r] = S[(size_t)r * dim];
+    for (int r = 0; r < R; r++) cs[r] = S[(size_t)r * dim];
     const size_t oq = (size_t)hq * dim + i0, ok = (size_t)(n_qk + hq) * dim + i0, ov = (size_t)(2 * n_qk + h) * dim + j;
     // inputs of two tokens (ping-pong: token t in buffer t & 1, so the
     // next token's loads land in registers no instruction of this token reads)
-    float qn[2][16], kn[2][16], vn[2], gn[2], bn[2];
+    float qn[2][R], kn[2][R], vn[2], gn[2], bn[2];
     auto fetch = [&](int t, int bsel) {
         const float4 *q4 = (const float4 *)(cv + (size_t)t * channels + oq);
         const float4 *k4 = (const float4 *)(cv + (size_t)t * channels + ok);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < R / 4; u++) {
             const float4 a = q4[u], b = k4[u];
             qn[bsel][4 * u] = a.x, qn[bsel][4 * u + 1] = a.y, qn[bsel][4 * u + 2] = a.z, qn[bsel][4 * u + 3] = a.w;
             kn[bsel][4 * u] = b.x, kn[bsel][4 * u + 1] = b.y, kn[bsel][4 * u + 2] = b.z, kn[bsel][4 * u + 3] = b.w;
@@ -462,7 +472,7 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         // a fixed tree
         double s4[4] = {0.0, 0.0, 0.0, 0.0}, a4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = 0; r < R; r++) {
             const double t = (double)__fmul_rn(cs[r], x[r]);
             s4[r & 3] += t;
             a4[r & 3] += fabs(t);
@@ -474,10 +484,10 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         const bool undecided = __float_as_uint(lo) != __float_as_uint(hi);
         if (!__builtin_amdgcn_ballot_w64(undecided)) return lo;
 #pragma unroll
-        for (int r = 0; r < 16; r++) prod[jc][i0 + r] = __fmul_rn(cs[r], x[r]);
-        // the workgroup is this one wave: wave-scope ordering of the LDS
+        for (int r = 0; r < R; r++) prod[jc][i0 + r] = __fmul_rn(cs[r], x[r]);
+        // the rows are this wave's own: wave-scope ordering of the LDS
         // writes before the reads (a workgroup barrier would also wait for
-        // the next token's global loads)
+        // the other waves and the next token's global loads)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -499,11 +509,11 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         fetch(min(t + 1, nt - 1), bsel ^ 1);
         const float *kc = kn[bsel], *qc = qn[bsel];
 #pragma unroll
-        for (int r = 0; r < 16; r++) cs[r] = __fmul_rn(cs[r], gn[bsel]);
+        for (int r = 0; r < R; r++) cs[r] = __fmul_rn(cs[r], gn[bsel]);
         const float sum = dot(kc);
         const float d = __fmul_rn(__fsub_rn(vn[bsel], sum), bn[bsel]);
 #pragma unroll
-        for (int r = 0; r < 16; r++) cs[r] = __fadd_rn(cs[r], __fmul_rn(kc[r], d));
+        for (int r = 0; r < R; r++) cs[r] = __fadd_rn(cs[r], __fmul_rn(kc[r], d));
         const float o = dot(qc);
         // every lane of the column holds o: all store it (the same value to
         // the same address), with no branch around the store
@@ -515,7 +525,7 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float *__restrict__ 
         if (t + 1 < nt) step(t + 1, 1);
     }
 #pragma unroll
-    for (int r = 0; r < 16; r++) S[(size_t)r * dim] = cs[r];
+    for (int r = 0; r < R; r++) S[(size_t)r * dim] = cs[r];
 }
 
 // The conv window after nt steps, in place, one thread per channel: the
@@ -1305,12 +1315,14 @@ hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, floa
     hipLaunchKernelGGL(conv_window_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, qkv, nt, d_conv,
                        channels);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    // eight rows per lane: a 128-dim head on 16 lanes per column (32 waves),
+    // a 64-dim one on 8 (8 waves)
     if (dim == 128)
-        hipLaunchKernelGGL(gdn_scan_kernel<8>, dim3(16, n_v), dim3(64), 0, s, cv, beta, gexp, state, out, nt, channels,
-                           n_qk, n_v, scale);
+        hipLaunchKernelGGL((gdn_scan_kernel<16, 8>), dim3(32 / kScanWaves, n_v), dim3(64 * kScanWaves), 0, s, cv, beta,
+                           gexp, state, out, nt, channels, n_qk, n_v, scale);
     else
-        hipLaunchKernelGGL(gdn_scan_kernel<4>, dim3(4, n_v), dim3(64), 0, s, cv, beta, gexp, state, out, nt, channels,
-                           n_qk, n_v, scale);
+        hipLaunchKernelGGL((gdn_scan_kernel<8, 8>), dim3(8 / kScanWaves, n_v), dim3(64 * kScanWaves), 0, s, cv, beta,
+                           gexp, state, out, nt, channels, n_qk, n_v, scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // the gated rmsnorm of every token's head outputs (rmsnorm_kernel with z)
     return launch_rmsnorm_rows(fin, dim, out, dim, snorm, dim, nt * n_v, eps, s, nullptr, nullptr, z);
