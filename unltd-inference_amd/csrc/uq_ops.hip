@@ -356,24 +356,27 @@ __global__ __launch_bounds__(64 * kGdnWaves) void gdn_step_wg_kernel(float *__re
 // the gates of every token, and the gated rmsnorm of every output, are
 // independent per token and run as row-parallel launches around the scan.
 
-// Conv, silu and l2 norm of nt tokens (gdn_conv_norm_kernel per token):
-// workgroup (b, t) for b < n_chunks forms chunk b of token t into cv[t] (the
-// q and k chunks normalised); the window seen by token t is entries t ..
-// t + d_conv - 1 of the sequence [win rows 0 .. d_conv - 2; qkv rows 0 ..
-// nt - 1]. Workgroup (n_chunks, t) forms token t's gates per v head in
-// place: beta_raw becomes beta = sigmoid(beta_raw), alpha becomes exp(gate),
-// gate = softplus(alpha + dt_bias) * a (gdn_gates_kernel, then the step's
-// exp of the gate).
-__global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_rows_kernel(
+// Conv, silu and l2 norm of nt tokens (gdn_conv_norm_kernel per token),
+// one wave per unit (b, t), four units a workgroup: for b < n_chunks the
+// wave forms chunk b of token t into cv[t] (the q and k chunks normalised),
+// lane l its channels l and l + 64 (hd <= 128); the window seen by token t
+// is entries t .. t + d_conv - 1 of the sequence [win rows 0 .. d_conv - 2;
+// qkv rows 0 .. nt - 1]. The norm's sum of squares is the wave's tree with
+// the bound of seq_sum_f32, or, undecided, the sequential loop with each
+// value taken from its lane by readlane. Unit (n_chunks, t) forms token t's
+// gates per v head in place: beta_raw becomes beta = sigmoid(beta_raw),
+// alpha becomes exp(gate), gate = softplus(alpha + dt_bias) * a
+// (gdn_gates_kernel, then the step's exp of the gate).
+constexpr int kConvUnits = 4;  // units (waves) per workgroup
+__global__ __launch_bounds__(64 * kConvUnits) void gdn_conv_norm_rows_kernel(
     const float *__restrict__ win, const float *__restrict__ kern, const float *__restrict__ qkv,
     float *__restrict__ cv, int d_conv, int channels, int hd, int n_qk, float eps, float *__restrict__ beta,
     float *__restrict__ gexp, const float *__restrict__ dt_bias, const float *__restrict__ a, int n_v) {
-    __shared__ float vals[128];  // hd <= 128 (gdn_scan_ok)
-    __shared__ double red[OPS_TPB / 64];
-    __shared__ float bc;
-    const int b = blockIdx.x, t = blockIdx.y, n_chunks = channels / hd;
+    const int lane = threadIdx.x & 63, t = blockIdx.y, n_chunks = channels / hd;
+    const int b = blockIdx.x * kConvUnits + (int)(threadIdx.x >> 6);
+    if (b > n_chunks) return;  // the whole wave
     if (b == n_chunks) {
-        for (int h = threadIdx.x; h < n_v; h += OPS_TPB) {
+        for (int h = lane; h < n_v; h += 64) {
             const size_t i = (size_t)t * n_v + h;
             const float br = beta[i], al = gexp[i];
             beta[i] = sigmoid1(br);
@@ -381,9 +384,13 @@ __global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_rows_kernel(
         }
         return;
     }
-    const bool norm = b < 2 * n_qk;  // workgroup-uniform
+    const bool norm = b < 2 * n_qk;  // wave-uniform
+    float v[2] = {0.0f, 0.0f};
     double s = 0.0;
-    for (int j = threadIdx.x; j < hd; j += OPS_TPB) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int j = lane + 64 * k;
+        if (j >= hd) break;
         const int c = b * hd + j;
         float x = 0.0f;
         for (int tau = 0; tau < d_conv; tau++) {
@@ -391,20 +398,31 @@ __global__ __launch_bounds__(OPS_TPB) void gdn_conv_norm_rows_kernel(
             const float xv = u < d_conv - 1 ? win[(size_t)u * channels + c] : qkv[(size_t)(u - d_conv + 1) * channels + c];
             x = __fadd_rn(x, __fmul_rn(xv, kern[(size_t)c * d_conv + tau]));
         }
-        const float v = silu1(x);
-        if (norm) {
-            vals[j] = v;
-            s += (double)__fmul_rn(v, v);
-        } else {
-            cv[(size_t)t * channels + c] = v;
-        }
+        v[k] = silu1(x);
+        if (norm)
+            s += (double)__fmul_rn(v[k], v[k]);
+        else
+            cv[(size_t)t * channels + c] = v[k];
     }
     if (!norm) return;
-    const double S = block_sum_d<OPS_TPB>(s, red);  // its barrier also publishes vals
-    const float sum32 = seq_sum_f32<OPS_TPB>([](int i) { return vals[i]; }, hd, S, [](double v) { return (float)v; },
-                                             &bc);
+    // l2_norm_rows of the chunk: (float) of the sequential f64 sum of squares
+    const double S = wave_sum_d(s);  // the same in every lane
+    const double e = (double)(hd + 66) * 0x1p-52 * S;
+    float sum32 = (float)(S - e);
+    if (__float_as_uint(sum32) != __float_as_uint((float)(S + e))) {  // wave-uniform; -0 and +0 replay too
+        double q = 0.0;
+        for (int i = 0; i < hd; i++) {
+            const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(i < 64 ? v[0] : v[1]), i & 63));
+            q += (double)__fmul_rn(x, x);
+        }
+        sum32 = (float)q;
+    }
     const float scale = __fdiv_rn(1.0f, fmaxf(sqrtf_cr(sum32), eps));
-    for (int j = threadIdx.x; j < hd; j += OPS_TPB) cv[(size_t)t * channels + b * hd + j] = __fmul_rn(vals[j], scale);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int j = lane + 64 * k;
+        if (j < hd) cv[(size_t)t * channels + b * hd + j] = __fmul_rn(v[k], scale);
+    }
 }
 
 // The delta rule (gdn_step_wg_kernel) of nt tokens, token after token, with
@@ -1308,8 +1326,9 @@ hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, floa
                            float eps, float scale, hipStream_t s) {
     if (!gdn_scan_ok(dim, d_conv) || n_qk < 1 || channels != (2 * n_qk + n_v) * dim) return hipErrorInvalidValue;
     if (nt == 0 || n_v == 0) return hipSuccess;
-    hipLaunchKernelGGL(gdn_conv_norm_rows_kernel, dim3(channels / dim + 1, nt), dim3(OPS_TPB), 0, s, win, kern, qkv,
-                       cv, d_conv, channels, dim, n_qk, eps, beta, gexp, dt_bias, a, n_v);
+    hipLaunchKernelGGL(gdn_conv_norm_rows_kernel, dim3((channels / dim + kConvUnits) / kConvUnits, nt),
+                       dim3(64 * kConvUnits), 0, s, win, kern, qkv, cv, d_conv, channels, dim, n_qk, eps, beta, gexp,
+                       dt_bias, a, n_v);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(conv_window_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, qkv, nt, d_conv,
