@@ -186,6 +186,49 @@ __global__ __launch_bounds__(OPS_TPB) void softmax_kernel(float *out, const floa
     for (int i = threadIdx.x; i < n; i += OPS_TPB) yr[i] = (float)((double)ex(i) / sum);
 }
 
+// softmax_kernel for rows of at most kSmWaveMax (the attention of a short
+// context or of a prefill chunk): one wave per row, four rows a workgroup,
+// no barrier. Lane l holds elements [16 l, 16 l + 16); the row's pairwise
+// tree (kernels.rs:21-42) is the lanes' 16-element trees, then the wave's
+// fixed tree over the lanes (wave_sum_d), with the missing elements as
+// zeros: every term is an exponential (>= +0), so a zero added where the
+// tree carries an odd tail up leaves the same value. Row r of token z =
+// blockIdx.y (r < nr) is n + z dn long, token z's rows start zst floats
+// after token z - 1's.
+constexpr int kSmWaveMax = 1024;
+__global__ __launch_bounds__(OPS_TPB) void softmax_wave_kernel(float *out, const float *x, int n, float scale, int dn,
+                                                               size_t zst, int nr) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * (OPS_TPB / 64) + (int)(threadIdx.x >> 6);
+    if (r >= nr) return;  // the whole wave
+    n += (int)blockIdx.y * dn;
+    const size_t row0 = (size_t)blockIdx.y * zst + (size_t)r * n;
+    const float *xr = x + row0;
+    float *yr = out + row0;
+    const int i0 = 16 * lane;
+    float v[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        v[k] = i0 + k < n ? xr[i0 + k] : -INFINITY;
+        m = fmaxf(m, v[k]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = i0 + k < n ? expf_cr(__fmul_rn(__fsub_rn(v[k], m), scale)) : 0.0f;
+    double t[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) t[k] = (double)v[2 * k] + (double)v[2 * k + 1];
+#pragma unroll
+    for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int k = 0; k < w; k++) t[k] = t[2 * k] + t[2 * k + 1];
+    const double sum = wave_sum_d(t[0]);
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        if (i0 + k < n) yr[i0 + k] = (float)((double)v[k] / sum);
+}
+
 // sigmoid, silu, softplus, gelu_tanh (kernels.rs:185-194)
 __global__ void unary_kernel(int op, const float *__restrict__ x, size_t n, float *__restrict__ out) {
     for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
@@ -1286,7 +1329,11 @@ int softmax_max_len() { return kSmChunk * kSmMaxChunks; }
 hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (n > softmax_max_len()) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale, 0, (size_t)0);
+    if (n <= kSmWaveMax)
+        hipLaunchKernelGGL(softmax_wave_kernel, dim3((rows + OPS_TPB / 64 - 1) / (OPS_TPB / 64)), dim3(OPS_TPB), 0, s,
+                           out, x, n, scale, 0, (size_t)0, rows);
+    else
+        hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(OPS_TPB), 0, s, out, x, n, scale, 0, (size_t)0);
     return hipGetLastError();
 }
 
@@ -1401,8 +1448,12 @@ hipError_t launch_attn_rows(float *out, size_t out_st, float *soft, size_t soft_
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group, rows), dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale,
-                       1, soft_st);
+    if (n_last <= kSmWaveMax)
+        hipLaunchKernelGGL(softmax_wave_kernel, dim3((n_head_kv * group + OPS_TPB / 64 - 1) / (OPS_TPB / 64), rows),
+                           dim3(OPS_TPB), 0, s, soft, soft, n_ctx, kq_scale, 1, soft_st, n_head_kv * group);
+    else
+        hipLaunchKernelGGL(softmax_kernel, dim3(n_head_kv * group, rows), dim3(OPS_TPB), 0, s, soft, soft, n_ctx,
+                           kq_scale, 1, soft_st);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const PvStrides pst{soft_st, out_st, gz_st, gated_st};
     if (rows > 1) {
