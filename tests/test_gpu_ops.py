@@ -148,6 +148,37 @@ def test_softmax_reference_case_and_device_rows():
         assert_ulp(got[r], O.softmax(X[r], 0.5), 2, 0.99, f"softmax row {r}")
 
 
+def softmax_model(x, scale):
+    """The device's method for softmax: f32 steps, each exp the f64 function
+    rounded once to f32, the denominator the reference's pairwise tree
+    (kernels.rs:21-42: pairs (2i, 2i+1), an odd tail carried up) in f64."""
+    f = np.float32
+    x = np.asarray(x, f)
+    e = np.exp(((x - x.max()) * f(scale)).astype(np.float64)).astype(f)
+    lv = [float(v) for v in e]
+    while len(lv) > 1:
+        lv = [lv[i] + lv[i + 1] if i + 1 < len(lv) else lv[i] for i in range(0, len(lv), 2)]
+    return (e.astype(np.float64) / lv[0]).astype(f)
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 100, 777, 1024, 1025, 3000])
+def test_softmax_rows_equal_the_pairwise_model(n):
+    """Rows of up to 1024 take one wave each (16-element lane trees, then
+    the wave's tree), longer rows the workgroup's LDS tree: both give the
+    reference's pairwise denominator, bit for bit against the model."""
+    rng = np.random.default_rng(n + 3)
+    rows = 5
+    X = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
+    dx, dy = dev(X), uq.DeviceArray(4 * n * rows)
+    ops.softmax_d(dy, dx, n, rows, 0.25)
+    uq.synchronize()
+    got = dy.download(np.float32, n * rows).reshape(rows, n)
+    for r in range(rows):
+        assert_bitwise(got[r], softmax_model(X[r], 0.25), f"softmax n={n} row {r}")
+    for a_ in (dx, dy):
+        a_.free()
+
+
 def unary_cr(name, x):
     """The device's method: each f32 exp / log is the f64 function rounded
     once to f32; the other steps are single f32 operations."""
