@@ -772,6 +772,8 @@ template <int N, int B>
 __device__ __forceinline__ double tree_dot(const float *__restrict__ x, const float *__restrict__ y) {
     if constexpr (N == 1)
         return (double)x[B] * (double)y[B];
+    else if constexpr (N == 2)  // x1 y1 + x0 y0, both exact, rounded once: one fma
+        return fma((double)x[B + 1], (double)y[B + 1], (double)x[B] * (double)y[B]);
     else
         return tree_dot<N / 2, B>(x, y) + tree_dot<N / 2, B + N / 2>(x, y);
 }
