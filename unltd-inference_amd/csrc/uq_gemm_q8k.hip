@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "uq_device.h"
 #include "uq_internal.h"
 #include "uq_mfma.h"
 #include "uq_q8k_tiles.h"
@@ -50,6 +51,7 @@ struct Q8Ws {
     uint8_t *a, *bs;
     float *d8;
     int Mp;
+    const float *res;  // non-null: each output is res + the dot (one f32 add, res in Y's layout)
 };
 
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -64,6 +66,7 @@ Q8Ws q8_carve(uint8_t *base, int M, int K) {
     w.a = base;
     w.bs = base + q8_a_bytes(w.Mp, K);
     w.d8 = (float *)(w.bs + q8_bs_bytes(w.Mp, K));
+    w.res = nullptr;
     return w;
 }
 
@@ -76,7 +79,8 @@ Q8Ws q8_carve(uint8_t *base, int M, int K) {
 // the 256 quants in LDS, then lane t < 32 writes octet (l, h, o) = (t / 4,
 // t / 2 % 2, t % 2) as eight f16, lanes 32-33 the bsums, lane 34 d.
 template <bool Q6>
-__global__ __launch_bounds__(512) void gemm_q8k_prep_kernel(const float *__restrict__ X, int K, int M, Q8Ws ws) {
+__global__ __launch_bounds__(512) void gemm_q8k_prep_kernel(const float *__restrict__ X, const float *__restrict__ U,
+                                                            int K, int M, Q8Ws ws) {
     __shared__ int8_t qs[8][256];
     __shared__ int bsum[8][16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -85,6 +89,10 @@ __global__ __launch_bounds__(512) void gemm_q8k_prep_kernel(const float *__restr
     if (m < M) {
         const float4 f = *(const float4 *)(X + (size_t)m * K + 256 * b + 4 * lane);
         v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+        if (U) {  // the row is swiglu(X, U), as swiglu_kernel forms it
+            const float4 u = *(const float4 *)(U + (size_t)m * K + 256 * b + 4 * lane);
+            v[0] = swiglu1(v[0], u.x), v[1] = swiglu1(v[1], u.y), v[2] = swiglu1(v[2], u.z), v[3] = swiglu1(v[3], u.w);
+        }
     }
     float am = 0.0f, mx = 0.0f;
     int idx = 0x7FFFFFFF;
@@ -392,7 +400,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(RT > 2 
 #pragma unroll
             for (int k = 0; k < 8; k++) s = __fadd_rn(s, sums[k][rt][r]);
             const int m = m0 + 16 * rt + 4 * lq + r;
-            if (m < M && n < N) Y[(size_t)m * N + n] = s;
+            if (m < M && n < N) Y[(size_t)m * N + n] = ws.res ? __fadd_rn(ws.res[(size_t)m * N + n], s) : s;
         }
 }
 
@@ -653,7 +661,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_q8k_kpar_kernel(const uint8_t *_
 #pragma unroll
         for (int l = 0; l < 8; l++) sv = __fadd_rn(sv, tslot(0, l)[r]);
         const int m = m0 + 4 * lq + r;
-        if (m < M && n < N) Y[(size_t)m * N + n] = sv;
+        if (m < M && n < N) Y[(size_t)m * N + n] = ws.res ? __fadd_rn(ws.res[(size_t)m * N + n], sv) : sv;
     }
 }
 
@@ -718,7 +726,8 @@ size_t gemm_q8k_ws_bytes(const WeightsView &w, int M) {
 }
 
 hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *wsp, size_t wsb,
-                              hipStream_t s, bool prepped) {
+                              hipStream_t s, bool prepped, const float *up, const float *res) {
+    if ((up || res) && (M < 2 || w.dim_in == 0)) return hipErrorInvalidValue;  // the fused forms: tile kernels only
     if (M == 0 || w.dim_out == 0) return hipSuccess;
     if (w.dim_in == 0) {  // no blocks: every row's sum is sumf + sums[..] = 0
         const size_t MN = (size_t)M * w.dim_out;
@@ -729,14 +738,15 @@ hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float
     if (M == 1) return launch_gemv_q8k(w, X, Y, s);  // the decode kernel, bit-identical
     if (wsb < gemm_q8k_ws_bytes(w, M) || !wsp) return hipErrorInvalidValue;
     const int K = w.dim_in;
-    const Q8Ws ws = q8_carve((uint8_t *)wsp, M, K);
+    Q8Ws ws = q8_carve((uint8_t *)wsp, M, K);
+    ws.res = res;
     const bool q6 = w.dtype == UQ_Q6_K;
     if (!prepped) {
         const dim3 pgrid(ws.Mp / 8, K / 256);
         if (q6)
-            hipLaunchKernelGGL(gemm_q8k_prep_kernel<true>, pgrid, dim3(512), 0, s, X, K, M, ws);
+            hipLaunchKernelGGL(gemm_q8k_prep_kernel<true>, pgrid, dim3(512), 0, s, X, up, K, M, ws);
         else
-            hipLaunchKernelGGL(gemm_q8k_prep_kernel<false>, pgrid, dim3(512), 0, s, X, K, M, ws);
+            hipLaunchKernelGGL(gemm_q8k_prep_kernel<false>, pgrid, dim3(512), 0, s, X, up, K, M, ws);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -216,8 +216,12 @@ hipError_t launch_gemm_q8k(const WeightsView &w, int M, const float *X, float *Y
 size_t gemm_q8k_ws_bytes(const WeightsView &w, int M);
 // prepped: ws already holds X quantized by the previous launch_gemm_q8k_ws
 // call on it (same X contents, M, K, and Q6_K-ness of the weights), so the
-// quantization is skipped.
+// quantization is skipped. Two fused forms for M >= 2 (hipErrorInvalidValue
+// otherwise): up, the input rows are swiglu(X, up) as swiglu_kernel forms
+// them (X the gate rows); res, Y = res + the products, one f32 add per
+// output (res M x dim_out like Y).
 hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
-                              hipStream_t s, bool prepped = false);
+                              hipStream_t s, bool prepped = false, const float *up = nullptr,
+                              const float *res = nullptr);
 
 }  // namespace uq

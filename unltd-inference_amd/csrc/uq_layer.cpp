@@ -268,12 +268,15 @@ struct PrefillCtx {
     mutable size_t last_k = 0;
     mutable int last_m = 0;
     mutable bool last_q6 = false;
-    uq_status gemm(uq_weights w, int nt, const float *X, float *Y, bool same_x = false) const {
+    // up / res (nt >= 2): the fused forms of launch_gemm_q8k_ws, the input
+    // swiglu(X, up), the output res + the product
+    uq_status gemm(uq_weights w, int nt, const float *X, float *Y, bool same_x = false, const float *up = nullptr,
+                   const float *res = nullptr) const {
         const uq::WeightsView v = uq::view(*wh(w));
         const bool q6 = v.dtype == UQ_Q6_K;
-        const bool prepped = same_x && X == last_x && v.dim_in == last_k && nt == last_m && q6 == last_q6;
-        last_x = X, last_k = v.dim_in, last_m = nt, last_q6 = q6;
-        return hip_st(uq::launch_gemm_q8k_ws(v, nt, X, Y, gws, gws_bytes, s, prepped), fn);
+        const bool prepped = !up && same_x && X == last_x && v.dim_in == last_k && nt == last_m && q6 == last_q6;
+        last_x = up ? nullptr : X, last_k = v.dim_in, last_m = nt, last_q6 = q6;
+        return hip_st(uq::launch_gemm_q8k_ws(v, nt, X, Y, gws, gws_bytes, s, prepped, up, res), fn);
     }
 };
 
@@ -288,6 +291,8 @@ uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_d
                   c.fn));
     UQ_TRY(c.gemm(g, nt, A[P_PN], A[P_G]));
     UQ_TRY(c.gemm(u, nt, A[P_PN], A[P_U], true));
+    if (nt >= 2)  // swiglu formed in the down projection's activation prep, l_out in its store
+        return c.gemm(dn, nt, A[P_G], l_out, false, A[P_U], A[P_RES]);
     UQ_TRY(hip_st(uq::launch_swiglu(A[P_G], A[P_U], (size_t)nt * D.nff, A[P_H], c.s), c.fn));
     UQ_TRY(c.gemm(dn, nt, A[P_H], A[P_FO]));
     return hip_st(uq::launch_add(l_out, A[P_RES], A[P_FO], (size_t)nt * D.n, c.s), c.fn);

@@ -468,6 +468,24 @@ __global__ __launch_bounds__(64 * kConvUnits) void gdn_conv_norm_rows_kernel(
     }
 }
 
+// The conv window after nt steps, in place, one thread per channel: the
+// sequence is the window's rows 0 .. d_conv - 2 followed by the nt qkv rows;
+// rows 0 .. d_conv - 2 become its last d_conv - 1 entries and row d_conv - 1
+// the last qkv row (as each step writes the token's qkv to the last row,
+// then shifts rows 1 .. d_conv - 1 up). Row r's source is at index nt + r
+// > r, so ascending r reads every old row before it is overwritten.
+// Channel c of it; the workgroups of gdn_scan_kernel past the scan's own
+// run it (the scan reads no window, and the conv before it is done with it).
+__device__ __forceinline__ void conv_window_channel(float *__restrict__ win, const float *__restrict__ qkv, int nt,
+                                                    int d_conv, int channels, int c) {
+    for (int r = 0; r < d_conv - 1; r++) {
+        const int u = nt + r;
+        win[(size_t)r * channels + c] =
+            u < d_conv - 1 ? win[(size_t)u * channels + c] : qkv[(size_t)(u - (d_conv - 1)) * channels + c];
+    }
+    win[(size_t)(d_conv - 1) * channels + c] = qkv[(size_t)(nt - 1) * channels + c];
+}
+
 // The delta rule (gdn_step_wg_kernel) of nt tokens, token after token, with
 // no exchange between waves: lane l of wave w holds rows [R m, R m + R),
 // m = l % RB (RB = dim / R lanes per column), of column j = (64 / RB)
@@ -499,7 +517,13 @@ template <int RB, int R>
 __global__ __launch_bounds__(64 * kScanWaves) void gdn_scan_kernel(const float *__restrict__ cv, const float *__restrict__ beta,
                                                       const float *__restrict__ gexp, float *__restrict__ state,
                                                       float *__restrict__ out, int nt, int channels, int n_qk,
-                                                      int n_v, float scale) {
+                                                      int n_v, float scale, float *__restrict__ win,
+                                                      const float *__restrict__ qkv, int d_conv) {
+    if ((int)blockIdx.y >= n_v) {  // the window's workgroups, dispatched after the scan's (the whole workgroup)
+        const int c = (((int)blockIdx.y - n_v) * (int)gridDim.x + (int)blockIdx.x) * 64 * kScanWaves + (int)threadIdx.x;
+        if (c < channels) conv_window_channel(win, qkv, nt, d_conv, channels, c);
+        return;
+    }
     constexpr int dim = R * RB, CPW = 64 / RB;  // columns per wave
     __shared__ float prodw[kScanWaves][CPW][dim];  // per wave: a column's products, for the ordered replay
     const int wv = (int)(threadIdx.x >> 6);
@@ -587,24 +611,6 @@ __global__ __launch_bounds__(64 * kScanWaves) void gdn_scan_kernel(const float *
     }
 #pragma unroll
     for (int r = 0; r < R; r++) S[(size_t)r * dim] = cs[r];
-}
-
-// The conv window after nt steps, in place, one thread per channel: the
-// sequence is the window's rows 0 .. d_conv - 2 followed by the nt qkv rows;
-// rows 0 .. d_conv - 2 become its last d_conv - 1 entries and row d_conv - 1
-// the last qkv row (as each step writes the token's qkv to the last row,
-// then shifts rows 1 .. d_conv - 1 up). Row r's source is at index nt + r
-// > r, so ascending r reads every old row before it is overwritten.
-__global__ void conv_window_kernel(float *__restrict__ win, const float *__restrict__ qkv, int nt, int d_conv,
-                                   int channels) {
-    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < channels; c += gridDim.x * blockDim.x) {
-        for (int r = 0; r < d_conv - 1; r++) {
-            const int u = nt + r;
-            win[(size_t)r * channels + c] =
-                u < d_conv - 1 ? win[(size_t)u * channels + c] : qkv[(size_t)(u - (d_conv - 1)) * channels + c];
-        }
-        win[(size_t)(d_conv - 1) * channels + c] = qkv[(size_t)(nt - 1) * channels + c];
-    }
 }
 
 // The rope rotation (kernels.rs:121-123): f64 sin/cos, fma, rounded to f32.
@@ -1380,17 +1386,19 @@ hipError_t launch_gdn_scan(float *win, const float *kern, const float *qkv, floa
                        dt_bias, a, n_v);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(conv_window_kernel, dim3(ops_grid(channels)), dim3(OPS_TPB), 0, s, win, qkv, nt, d_conv,
-                       channels);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     // eight rows per lane: a 128-dim head on 16 lanes per column (32 waves),
-    // a 64-dim one on 8 (8 waves)
+    // a 64-dim one on 8 (8 waves); then, as rows of the grid after the v
+    // heads' (dispatched last, so the scan's workgroups spread over the CUs
+    // first), the window's workgroups, a channel per thread
+    const int scan_bx = (dim == 128 ? 32 : 8) / kScanWaves, tpb = 64 * kScanWaves;
+    const int win_by = ((channels + tpb - 1) / tpb + scan_bx - 1) / scan_bx;
+    const dim3 grid(scan_bx, n_v + win_by);
     if (dim == 128)
-        hipLaunchKernelGGL((gdn_scan_kernel<16, 8>), dim3(32 / kScanWaves, n_v), dim3(64 * kScanWaves), 0, s, cv, beta,
-                           gexp, state, out, nt, channels, n_qk, n_v, scale);
+        hipLaunchKernelGGL((gdn_scan_kernel<16, 8>), grid, dim3(tpb), 0, s, cv, beta, gexp, state, out, nt, channels,
+                           n_qk, n_v, scale, win, qkv, d_conv);
     else
-        hipLaunchKernelGGL((gdn_scan_kernel<8, 8>), dim3(8 / kScanWaves, n_v), dim3(64 * kScanWaves), 0, s, cv, beta,
-                           gexp, state, out, nt, channels, n_qk, n_v, scale);
+        hipLaunchKernelGGL((gdn_scan_kernel<8, 8>), grid, dim3(tpb), 0, s, cv, beta, gexp, state, out, nt, channels,
+                           n_qk, n_v, scale, win, qkv, d_conv);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // the gated rmsnorm of every token's head outputs (rmsnorm_kernel with z)
     return launch_rmsnorm_rows(fin, dim, out, dim, snorm, dim, nt * n_v, eps, s, nullptr, nullptr, z);
