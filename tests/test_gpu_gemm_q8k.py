@@ -89,10 +89,10 @@ SHAPES = [
     # kernel runs (M = 31, 33, 65 here, the FFN down shape at M = 8: 48
     # blocks over four waves, and the 32-wide projections of a 512- or
     # 300-token prefill), and for M <= 32 at K > 8192 up to two per CU
-    # (M = 24 at K = 12288)
+    # (M = 24 at K = 12288); 16-row tiles at K = 12288 for M > 64 (M = 100)
     (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
     (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
-    (12288, 4096, 8), (2304, 48, 16), (12288, 4096, 24), (4096, 32, 512), (4096, 40, 300),
+    (12288, 4096, 8), (2304, 48, 16), (12288, 4096, 24), (4096, 32, 512), (4096, 40, 300), (12288, 4096, 100),
 ]
 
 

@@ -682,10 +682,12 @@ hipError_t q8k_kpar_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y
 // Rows per wave (and workgroup): 16 for M <= 16; 64 for M > 128 while the
 // 64 x 128 workgroup tiles number at least one per CU (eight waves, two per
 // SIMD: the B operands decoded once for 64 rows); 16 where 32-row tiles of
-// 32 columns would number at most two per CU and K <= 8192 (such launches
-// run one wave per SIMD, latency-bound: twice the waves at twice the
-// decode per output measured faster, e.g. 4096 x 4096 at M = 128 29 us
-// against 32, 1024 x 4096 22 against 27); else 32. Waves (16-column
+// 32 columns would number at most two per CU and K <= 8192 or M > 64 (such
+// launches run one wave per SIMD, latency-bound: twice the waves at twice
+// the decode per output measured faster, e.g. 4096 x 4096 at M = 128 29 us
+// against 32, 1024 x 4096 22 against 27, the K = 12288 down projections at
+// M = 100 to 128 72-73 against 82 us (Q4_K) and 97 against 105-107 us
+// (Q6_K); at M = 64 the Q6_K one took 88 against 73 us); else 32. Waves (16-column
 // tiles) per workgroup: six while the workgroups number two per CU, else
 // two while they number one per CU, else one.
 template <bool Q6, int RT>
@@ -707,7 +709,7 @@ hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipS
     if (M <= 32 && ((M + 15) / 16) * ((N + 15) / 16) <= 2 * cus && w.dim_in > 8192)
         return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     if (M <= 16) return q8k_width<Q6, 1>(w, M, ws, Y, s);
-    if (M <= 128 && ((M + 31) / 32) * ((N + 31) / 32) <= 2 * cus && w.dim_in <= 8192)
+    if (M <= 128 && ((M + 31) / 32) * ((N + 31) / 32) <= 2 * cus && (w.dim_in <= 8192 || M > 64))
         return q8k_width<Q6, 1>(w, M, ws, Y, s);
     if (M > 128 && ((M + 63) / 64) * ((N + 127) / 128) >= cus) return q8k_launch<Q6, 8, 4>(w, M, ws, Y, s);
     return q8k_width<Q6, 2>(w, M, ws, Y, s);
