@@ -688,12 +688,16 @@ hipError_t q8k_kpar_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y
 // against 32, 1024 x 4096 22 against 27, the K = 12288 down projections at
 // M = 100 to 128 72-73 against 82 us (Q4_K) and 97 against 105-107 us
 // (Q6_K); at M = 64 the Q6_K one took 88 against 73 us); else 32. Waves (16-column
-// tiles) per workgroup: six while the workgroups number two per CU, else
-// two while they number one per CU, else one.
+// tiles) per workgroup: four while the workgroups number two per CU, else
+// two while they number one per CU, else one. Four waves hold a two-slot
+// ring small enough for three workgroups per CU, where six waves' held two:
+// at M = 128 Q4_K 8192 x 4096 35 against 54 us, 12288 x 4096 46 against
+// 59, Q6_K 8192 x 4096 44 against 71; at M = 256, 4096 x 4096 37 against
+// 55 and Q6_K 4096 x 12288 130 against 180.
 template <bool Q6, int RT>
 hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256, ntm = (M + 16 * RT - 1) / (16 * RT);
-    if (ntm * ((N + 95) / 96) >= 2 * cus) return q8k_launch<Q6, 6, RT>(w, M, ws, Y, s);
+    if (ntm * ((N + 63) / 64) >= 2 * cus) return q8k_launch<Q6, 4, RT>(w, M, ws, Y, s);
     if (ntm * ((N + 31) / 32) >= cus) return q8k_launch<Q6, 2, RT>(w, M, ws, Y, s);
     return q8k_launch<Q6, 1, RT>(w, M, ws, Y, s);
 }
