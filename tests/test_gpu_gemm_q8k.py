@@ -82,17 +82,19 @@ def test_gemm_q8k_q6k_down_shape_every_row():
 
 
 SHAPES = [
-    # (K, N, M): row tile 16 (M <= 16, and M = 31, 33, 65, 100 here, whose
-    # 32-row grids are small), 64 (M = 200 at N = 8192: 256 tiles of 64 x
-    # 128), else 32 with six, two or one waves per workgroup. Where the
-    # 16 x 16 tiles number at most one per CU and K >= 2048 the K-parallel
-    # kernel runs (M = 31, 33, 65 here, the FFN down shape at M = 8: 48
-    # blocks over four waves, and the 32-wide projections of a 512- or
-    # 300-token prefill), and for M <= 32 at K > 8192 up to two per CU
-    # (M = 24 at K = 12288); 16-row tiles at K = 12288 for M > 64 (M = 100)
+    # (K, N, M): 16-row tiles for M <= 16 (one wave per workgroup at these
+    # N) and where 32 x 64 tiles would number under one per CU (M = 64 at
+    # N = 4096: four waves a workgroup; M = 128 at N = 1024: two); 32-row
+    # tiles of four waves (M = 64, 100, 128 at N >= 4096); 64-row tiles past
+    # M = 128 where they fill the CUs (M = 200 at N = 8192). The K-parallel
+    # kernel where 16 x 16 tiles number at most one per CU and K >= 2048 (M =
+    # 31, 33, 65, M = 8 at K = 12288, the 32-wide projections of a 512- or
+    # 300-token prefill), and for M <= 32 at K > 8192 up to two per CU (M =
+    # 24 at K = 12288)
     (256, 300, 2), (768, 1000, 3), (1024, 256, 8), (4096, 2048, 31), (2048, 777, 33),
     (4096, 12288, 64), (4096, 12288, 128), (1280, 4096, 100), (512, 8192, 200), (4096, 640, 65),
     (12288, 4096, 8), (2304, 48, 16), (12288, 4096, 24), (4096, 32, 512), (4096, 40, 300), (12288, 4096, 100),
+    (4096, 4096, 64), (4096, 1024, 128),
 ]
 
 

@@ -681,23 +681,21 @@ hipError_t q8k_kpar_launch(const WeightsView &w, int M, const Q8Ws &ws, float *Y
 
 // Rows per wave (and workgroup): 16 for M <= 16; 64 for M > 128 while the
 // 64 x 128 workgroup tiles number at least one per CU (eight waves, two per
-// SIMD: the B operands decoded once for 64 rows); 16 where 32-row tiles of
-// 32 columns would number at most two per CU and K <= 8192 or M > 64 (such
-// launches run one wave per SIMD, latency-bound: twice the waves at twice
-// the decode per output measured faster, e.g. 4096 x 4096 at M = 128 29 us
-// against 32, 1024 x 4096 22 against 27, the K = 12288 down projections at
-// M = 100 to 128 72-73 against 82 us (Q4_K) and 97 against 105-107 us
-// (Q6_K); at M = 64 the Q6_K one took 88 against 73 us); else 32. Waves (16-column
-// tiles) per workgroup: four while the workgroups number two per CU, else
-// two while they number one per CU, else one. Four waves hold a two-slot
-// ring small enough for three workgroups per CU, where six waves' held two:
-// at M = 128 Q4_K 8192 x 4096 35 against 54 us, 12288 x 4096 46 against
-// 59, Q6_K 8192 x 4096 44 against 71; at M = 256, 4096 x 4096 37 against
-// 55 and Q6_K 4096 x 12288 130 against 180.
+// SIMD: the B operands decoded once for 64 rows); 32 while 32 x 64 tiles
+// (four 16-column waves) number at least one per CU; else 16. Waves
+// (16-column tiles) per workgroup: four while the workgroups number at
+// least one per CU, else two while they do, else one. Four waves hold a
+// two-slot ring small enough for three workgroups per CU, where six waves'
+// held two. Measured over the prefill's projections (a sweep of every
+// wave count and tile height): at M = 128 the rule is the best shape or
+// within a few percent of it, e.g. Q4_K 8192 x 4096 35 us (six waves: 54),
+// Q6_K 4096 x 12288 75 us (16-row tiles: 96); at M = 512 the 64-row tiles
+// stay best for N >= 4096 (Q4_K 12288 x 4096 144 against 155 on 32-row
+// ones) and N = 1024 takes 32-row tiles (34 against 47 us).
 template <bool Q6, int RT>
 hipError_t q8k_width(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipStream_t s) {
     const int N = w.dim_out, cus = 256, ntm = (M + 16 * RT - 1) / (16 * RT);
-    if (ntm * ((N + 63) / 64) >= 2 * cus) return q8k_launch<Q6, 4, RT>(w, M, ws, Y, s);
+    if (ntm * ((N + 63) / 64) >= cus) return q8k_launch<Q6, 4, RT>(w, M, ws, Y, s);
     if (ntm * ((N + 31) / 32) >= cus) return q8k_launch<Q6, 2, RT>(w, M, ws, Y, s);
     return q8k_launch<Q6, 1, RT>(w, M, ws, Y, s);
 }
@@ -713,10 +711,9 @@ hipError_t q8k_shape(const WeightsView &w, int M, const Q8Ws &ws, float *Y, hipS
     if (M <= 32 && ((M + 15) / 16) * ((N + 15) / 16) <= 2 * cus && w.dim_in > 8192)
         return q8k_kpar_launch<Q6, 4>(w, M, ws, Y, s);
     if (M <= 16) return q8k_width<Q6, 1>(w, M, ws, Y, s);
-    if (M <= 128 && ((M + 31) / 32) * ((N + 31) / 32) <= 2 * cus && (w.dim_in <= 8192 || M > 64))
-        return q8k_width<Q6, 1>(w, M, ws, Y, s);
     if (M > 128 && ((M + 63) / 64) * ((N + 127) / 128) >= cus) return q8k_launch<Q6, 8, 4>(w, M, ws, Y, s);
-    return q8k_width<Q6, 2>(w, M, ws, Y, s);
+    if (((M + 31) / 32) * ((N + 63) / 64) >= cus) return q8k_width<Q6, 2>(w, M, ws, Y, s);
+    return q8k_width<Q6, 1>(w, M, ws, Y, s);
 }
 
 __global__ __launch_bounds__(256) void q8k_fill_zero_kernel(float *__restrict__ Y, size_t n) {
