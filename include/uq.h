@@ -202,6 +202,20 @@ uq_status uq_gemm(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
 uq_status uq_gemm_q8k(uq_weights w, size_t m_rows, const float *d_x, float *d_y,
                       void *stream);
 
+/* uq_gemm_q8k of several weights over the same rows in one launch: d_y[i] =
+ * uq_gemm_q8k(W[i], m_rows, d_x) bit for bit, for i < count (count <=
+ * UQ_GEMM_Q8K_BATCH_MAX), e.g. the qkv, gate, beta and alpha projections of
+ * a GatedDeltaNet layer's tokens. All W[i] share dtype (Q4_K or Q6_K) and
+ * dim_in; each d_y[i] is [m_rows][dim_out of W[i]]. The rows are quantized
+ * once and one grid covers every weight's column tiles (above 128 rows the
+ * weights under 128 columns run in a second grid). No reference
+ * counterpart (one gemv_quant_q8k call per projection and token,
+ * qwen35_forward.rs:365-401, greedy.rs:55-65). Workspace as uq_gemm_q8k's.
+ * m_rows == 1 runs uq_gemv_q8k_batch. */
+#define UQ_GEMM_Q8K_BATCH_MAX 4
+uq_status uq_gemm_q8k_batch(const uq_weights *w, float *const *d_y, size_t count,
+                            size_t m_rows, const float *d_x, void *stream);
+
 /* uq_gemm that allocates nothing: no reference counterpart. For callers that
  * cannot allocate device memory inside the call (HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels

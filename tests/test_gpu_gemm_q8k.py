@@ -207,3 +207,85 @@ def test_gemm_q8k_one_row_is_gemv_q8k_and_errors():
         uq.gemm_q8k(W, 2, dx, dy)
     assert e.value.kind == "DTYPE"
     W.free()
+
+
+BATCH_CASES = [
+    # (K, segment widths, M): the GatedDeltaNet projections (qkv, z, beta,
+    # alpha) at 128 tokens (32-row tiles of four waves) and 512 (64 x 128
+    # tiles for qkv and z, the K-parallel kernel for the two 32-wide ones);
+    # ragged widths over and under 128 columns at 200 rows; widths that end
+    # inside a tile in every segment, at 37 rows; a
+    # zero-width segment; two 32-wide segments on the K-parallel kernel (128
+    # and 300 rows); M = 16 (16-row tiles); M = 1 (the batched decode
+    # kernel); one segment
+    (4096, (8192, 4096, 32, 32), 128),
+    (4096, (8192, 4096, 32, 32), 512),
+    (1024, (300, 100, 1100, 17), 200),
+    (2048, (1000, 17, 300, 65), 37),
+    (1024, (48, 0, 200), 70),
+    (4096, (32, 32), 128),
+    (4096, (32, 32), 300),
+    (1536, (640, 96, 33), 16),
+    (1024, (777, 40, 5), 1),
+    (256, (300,), 2),
+]
+
+
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
+@pytest.mark.parametrize("K,widths,M", BATCH_CASES)
+def test_gemm_q8k_batch_equals_each_gemm(dtype, K, widths, M):
+    """uq_gemm_q8k_batch: one launch over every weight's column tiles; each
+    output equals uq_gemm_q8k of its weight alone, bit for bit, and no
+    output is written past its own columns."""
+    log(f"gemm_q8k_batch dtype={dtype} K={K} widths={widths} M={M}")
+    X = S.activations(K, seed=M * 3 + dtype, rows=M).reshape(M, K)
+    dx = uq.DeviceArray.from_numpy(np.ascontiguousarray(X, np.float32))
+    Ws, ys = [], []
+    for i, N in enumerate(widths):
+        Ws.append(uq.Weights(S.weights(dtype, N, K, seed=K + 31 * i + N + dtype), dtype, K, N))
+        y = uq.DeviceArray(4 * (M * N + 64))  # 64 guard floats past each output
+        y.upload(np.full(M * N + 64, np.nan, np.float32))
+        ys.append(y)
+    uq.gemm_q8k_batch(Ws, M, dx, ys)
+    for i, (W, N) in enumerate(zip(Ws, widths)):
+        got = ys[i].download(np.float32, M * N + 64)
+        assert np.all(np.isnan(got[M * N:])), f"segment {i}: written past its outputs"
+        ref = uq.DeviceArray(4 * max(M * N, 1))
+        uq.gemm_q8k(W, M, dx, ref)
+        want = ref.download(np.float32, M * N)
+        assert not np.isnan(want).any()
+        assert_bitwise(got[:M * N], want, f"segment {i} ({N} columns)")
+        W.free()
+
+
+def test_gemm_q8k_batch_rows_against_the_oracle():
+    """Rows of a three-segment launch against the oracle's gemv_quant_q8k."""
+    K, widths, M = 2048, (700, 40, 129), 50
+    X = S.activations(K, seed=77, rows=M).reshape(M, K)
+    dx = uq.DeviceArray.from_numpy(np.ascontiguousarray(X, np.float32))
+    ws = [S.weights(S.Q4_K, N, K, seed=80 + N) for N in widths]
+    Ws = [uq.Weights(w, S.Q4_K, K, N) for w, N in zip(ws, widths)]
+    ys = [uq.DeviceArray(4 * M * N) for N in widths]
+    uq.gemm_q8k_batch(Ws, M, dx, ys)
+    for w, N, y in zip(ws, widths, ys):
+        Y = y.download(np.float32, M * N).reshape(M, N)
+        assert_rows(Y, oracle_rows(S.Q4_K, w, K, N, X, [0, 17, M - 1]), f"batch segment of {N}")
+    for W in Ws:
+        W.free()
+
+
+def test_gemm_q8k_batch_errors():
+    """More than four weights, or weights that differ in dtype or dim_in, are
+    refused before anything is launched; Q8_0 is refused as in uq_gemm_q8k."""
+    K = 512
+    a = uq.Weights(S.weights(S.Q4_K, 64, K, seed=1), S.Q4_K, K, 64)
+    b = uq.Weights(S.weights(S.Q6_K, 64, K, seed=2), S.Q6_K, K, 64)
+    c = uq.Weights(S.weights(S.Q4_K, 64, 2 * K, seed=3), S.Q4_K, 2 * K, 64)
+    q = uq.Weights(S.weights(S.Q8_0, 64, K, seed=4), S.Q8_0, K, 64)
+    dx, dy = uq.DeviceArray(4 * 4 * 2 * K), uq.DeviceArray(4 * 4 * 64)
+    for ws, kind in (([a] * 5, "ARG"), ([a, b], "LEN"), ([a, c], "LEN"), ([q], "DTYPE")):
+        with pytest.raises(uq.UqError) as e:
+            uq.gemm_q8k_batch(ws, 4, dx, [dy] * len(ws))
+        assert e.value.kind == kind
+    for W in (a, b, c, q):
+        W.free()

@@ -575,6 +575,21 @@ uq_status uq_gemm_q8k(uq_weights wh, size_t m_rows, const float *d_x, float *d_y
     return UQ_OK;
 }
 
+uq_status uq_gemm_q8k_batch(const uq_weights *whs, float *const *d_y, size_t count, size_t m_rows, const float *d_x,
+                            void *stream) {
+    static_assert(UQ_GEMM_Q8K_BATCH_MAX == uq::kGemmQ8kBatchMax, "batch bound");
+    if (count > UQ_GEMM_Q8K_BATCH_MAX)
+        return fail(UQ_ERR_ARG, "gemm_q8k_batch: count %zu above %d", count, UQ_GEMM_Q8K_BATCH_MAX);
+    uq::WeightsView v[UQ_GEMV_BATCH_MAX];
+    uq_status st = batch_views("gemm_q8k_batch", whs, d_y, count, d_x, true, v);
+    if (st != UQ_OK || count == 0 || m_rows == 0) return st;
+    if (m_rows > (size_t)INT_MAX / 2) return fail(UQ_ERR_ARG, "gemm_q8k_batch: m_rows above INT_MAX / 2");
+    if (v[0].dim_in / 256 > 65535) return fail(UQ_ERR_ARG, "gemm_q8k_batch: dim_in above 65535 blocks of 256");
+    UQ_HIP(uq::launch_gemm_q8k_batch(v, (int)count, (int)m_rows, d_x, d_y, (hipStream_t)stream),
+           "gemm_q8k_batch launch");
+    return UQ_OK;
+}
+
 uq_status uq_gemm_static(uq_weights wh, size_t m_rows, const float *d_x, float *d_y, void *stream) {
     uq_weights_s *w = handle(wh);
     if (!w) return fail(UQ_ERR_ARG, "gemm_static: invalid handle");

@@ -223,5 +223,15 @@ size_t gemm_q8k_ws_bytes(const WeightsView &w, int M);
 hipError_t launch_gemm_q8k_ws(const WeightsView &w, int M, const float *X, float *Y, void *ws, size_t wsb,
                               hipStream_t s, bool prepped = false, const float *up = nullptr,
                               const float *res = nullptr);
+// Up to kGemmQ8kBatchMax weights sharing dtype and dim_in over the same X:
+// one prep, one grid over all their column tiles (past M = 128 the weights
+// under 128 columns in a second grid); Y[i] = the launch_gemm_q8k_ws product
+// of w[i], bit for bit. res needs n == 1.
+constexpr int kGemmQ8kBatchMax = 4;
+hipError_t launch_gemm_q8k_batch(const WeightsView *w, int n, int M, const float *X, float *const *Y,
+                                 hipStream_t s);
+hipError_t launch_gemm_q8k_batch_ws(const WeightsView *w, int n, int M, const float *X, float *const *Y, void *ws,
+                                    size_t wsb, hipStream_t s, bool prepped = false, const float *up = nullptr,
+                                    const float *res = nullptr);
 
 }  // namespace uq

@@ -278,6 +278,23 @@ struct PrefillCtx {
         last_x = up ? nullptr : X, last_k = v.dim_in, last_m = nt, last_q6 = q6;
         return hip_st(uq::launch_gemm_q8k_ws(v, nt, X, Y, gws, gws_bytes, s, prepped, up, res), fn);
     }
+    // The projections w[0..n) of the same rows X: one launch over all their
+    // column tiles when they share dtype and dim_in (each Y[i] the bits of its
+    // own gemm), else one gemm each
+    uq_status gemm_group(const uq_weights *w, int n, int nt, const float *X, float *const *Y) const {
+        uq::WeightsView v[uq::kGemmQ8kBatchMax];
+        bool one = n <= uq::kGemmQ8kBatchMax;
+        for (int i = 0; one && i < n; i++) {
+            v[i] = uq::view(*wh(w[i]));
+            one = v[i].dtype == v[0].dtype && v[i].dim_in == v[0].dim_in && v[i].row_bytes == v[0].row_bytes;
+        }
+        if (!one) {
+            for (int i = 0; i < n; i++) UQ_TRY(gemm(w[i], nt, X, Y[i], i > 0));
+            return UQ_OK;
+        }
+        last_x = X, last_k = v[0].dim_in, last_m = nt, last_q6 = v[0].dtype == UQ_Q6_K;
+        return hip_st(uq::launch_gemm_q8k_batch_ws(v, n, nt, X, Y, gws, gws_bytes, s), fn);
+    }
 };
 
 // residual = x_in + attn_out and its post_attention_norm, the FFN and l_out
@@ -289,8 +306,11 @@ uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_d
     UQ_TRY(hip_st(uq::launch_rmsnorm_rows(A[P_PN], (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, nt, d->rms_eps, c.s,
                                           A[P_AO], A[P_RES]),
                   c.fn));
-    UQ_TRY(c.gemm(g, nt, A[P_PN], A[P_G]));
-    UQ_TRY(c.gemm(u, nt, A[P_PN], A[P_U], true));
+    {
+        const uq_weights gu[2] = {g, u};
+        float *const gy[2] = {A[P_G], A[P_U]};
+        UQ_TRY(c.gemm_group(gu, 2, nt, A[P_PN], gy));
+    }
     if (nt >= 2)  // swiglu formed in the down projection's activation prep, l_out in its store
         return c.gemm(dn, nt, A[P_G], l_out, false, A[P_U], A[P_RES]);
     UQ_TRY(hip_st(uq::launch_swiglu(A[P_G], A[P_U], (size_t)nt * D.nff, A[P_H], c.s), c.fn));
@@ -490,10 +510,11 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
     // 1-3) attn_norm of every token (:352-360), then qkv, z, beta, alpha of all
     // of them (:363-403)
     UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
-    UQ_TRY(c.gemm(w->attn_gate, nt, A[P_XN], A[P_Z]));
-    UQ_TRY(c.gemm(w->ssm_beta, nt, A[P_XN], A[P_BR], true));
-    UQ_TRY(c.gemm(w->ssm_alpha, nt, A[P_XN], A[P_AL], true));
-    UQ_TRY(c.gemm(w->attn_qkv, nt, A[P_XN], A[P_QKV], true));
+    {
+        const uq_weights pw[4] = {w->attn_qkv, w->attn_gate, w->ssm_beta, w->ssm_alpha};
+        float *const py[4] = {A[P_QKV], A[P_Z], A[P_BR], A[P_AL]};
+        UQ_TRY(c.gemm_group(pw, 4, nt, A[P_XN], py));
+    }
     // 4-6) the recurrent part: for head dims 64 and 128 the conv, norms and
     // gates of all tokens at once, the delta rule over the tokens in one
     // launch (the state held in registers between them), the gated norms of
@@ -553,9 +574,11 @@ uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w
     // 1-3) attn_norm of every token (:563-571); q|gate, k of all of them, and
     // v straight into the cache rows pos0 .. pos0 + n_tokens - 1 (:625-632)
     UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
-    UQ_TRY(c.gemm(w->attn_q, nt, A[P_XN], A[P_QF]));
-    UQ_TRY(c.gemm(w->attn_k, nt, A[P_XN], A[P_KR], true));
-    UQ_TRY(c.gemm(w->attn_v, nt, A[P_XN], d_v_cache + pos0 * kv_len, true));
+    {
+        const uq_weights pw[3] = {w->attn_q, w->attn_k, w->attn_v};
+        float *const py[3] = {A[P_QF], A[P_KR], d_v_cache + pos0 * kv_len};
+        UQ_TRY(c.gemm_group(pw, 3, nt, A[P_XN], py));
+    }
     // By chunks of tokens: 4) q / k norms and IMROPE of each token
     // (:585-642), k into its cache row, q into P_XN (free after the
     // projections; n_head * head_dim = n_embd); 5-6) attention of token t over

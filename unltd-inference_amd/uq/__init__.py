@@ -75,6 +75,7 @@ SIGNATURES = {
     "uq_gemm": ([_P, _S, _P, _P, _P], _I),
     "uq_gemm_static": ([_P, _S, _P, _P, _P], _I),
     "uq_gemm_q8k": ([_P, _S, _P, _P, _P], _I),
+    "uq_gemm_q8k_batch": ([_P, _P, _S, _S, _P, _P], _I),
     "uq_ffn_swiglu": ([_P, _P, _P, _P, _P, _P, _P], _I),
     "uq_dequantize": ([_P, _P, _P], _I),
     "uq_embed": ([_P, _P, _S, _P, _P], _I),
@@ -383,6 +384,15 @@ def gemm(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) ->
 def gemm_q8k(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
     """d_y[r] = gemv_quant_q8k(w, d_x[r]) for r < m, bit-exact (uq_gemm_q8k)."""
     _check(lib().uq_gemm_q8k(w.h, m, d_x.ptr, d_y.ptr, stream))
+
+
+def gemm_q8k_batch(ws, m: int, d_x: DeviceArray, d_ys, stream=None) -> None:
+    """d_ys[i][r] = gemv_quant_q8k(ws[i], d_x[r]) for r < m and every i, in one
+    launch (same dtype and dim_in; uq_gemm_q8k_batch)."""
+    n = len(ws)
+    hs = (_P * max(n, 1))(*[w.h for w in ws])
+    ys = (_P * max(n, 1))(*[y.ptr for y in d_ys])
+    _check(lib().uq_gemm_q8k_batch(hs, ys, n, m, d_x.ptr, stream))
 
 
 def gemm_static(w: Weights, m: int, d_x: DeviceArray, d_y: DeviceArray, stream=None) -> None:
