@@ -38,6 +38,7 @@
 #include "uq_device.h"
 #include "uq_internal.h"
 #include "uq_mfma.h"
+#include "uq_q8k_quant.h"
 #include "uq_q8k_tiles.h"
 
 namespace uq {
@@ -127,12 +128,9 @@ Q8Ws q8_carve(uint8_t *base, int M, int K) {
 
 // ------------------------------------------------------------ prep
 // Workgroup (g, b): rows 8g..8g+7 (one wave each) of block b. The wave
-// quantizes its row's block as quantize_q8k_kernel does (quantize_q8_k,
-// quants.rs:250-290: first strict argmax of |x| with its sign, iscale =
-// -127/max, nearest_int by the 12582912 add, min(127), bsums, d = 1/iscale;
-// an all-zero block, or a padding row, is d = 0, qs = 0, bsums = 0), puts
-// the 256 quants in LDS, then lane t < 32 writes octet (l, h, o) = (t / 4,
-// t / 2 % 2, t % 2) as eight f16, lanes 32-33 the bsums, lane 34 d.
+// quantizes its row's block as quantize_q8k_kernel does (q8k_quantize_wave:
+// quantize_q8_k, quants.rs:250-290); a padding row is an all-zero block
+// (d = 0, qs = 0, bsums = 0).
 template <bool Q6>
 __global__ __launch_bounds__(512) void gemm_q8k_prep_kernel(const float *__restrict__ X, const float *__restrict__ U,
                                                             int K, int M, Q8Ws ws) {
@@ -149,63 +147,7 @@ __global__ __launch_bounds__(512) void gemm_q8k_prep_kernel(const float *__restr
             v[0] = swiglu1(v[0], u.x), v[1] = swiglu1(v[1], u.y), v[2] = swiglu1(v[2], u.z), v[3] = swiglu1(v[3], u.w);
         }
     }
-    float am = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = fabsf(v[i]);
-        if (a > am) {
-            am = a;
-            mx = v[i];
-            idx = lane * 4 + i;
-        }
-    }
-    // wave argmax: larger |x| wins; equal |x|, the smaller index
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oam = __shfl_xor(am, off), omx = __shfl_xor(mx, off);
-        const int oidx = __shfl_xor(idx, off);
-        if (oam > am || (oam == am && oidx < idx)) {
-            am = oam;
-            mx = omx;
-            idx = oidx;
-        }
-    }
-    float d = 0.0f;
-    int s = 0;
-    if (am != 0.0f) {
-        const float iscale = __fdiv_rn(-127.0f, mx);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float val = __fadd_rn(__fmul_rn(iscale, v[i]), 12582912.0f);
-            int qv = (int)(__float_as_uint(val) & 0x007FFFFFu) - 0x00400000;
-            qv = qv < 127 ? qv : 127;
-            qs[wv][lane * 4 + i] = (int8_t)qv;
-            s += (int8_t)qv;
-        }
-        d = __fdiv_rn(1.0f, iscale);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) qs[wv][lane * 4 + i] = 0;
-    }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    if ((lane & 3) == 0) bsum[wv][lane >> 2] = s;
-    __syncthreads();
-    if (lane < 32) {
-        const int l = lane >> 2, h = (lane >> 1) & 1, o = lane & 1;
-        h8 q;
-#pragma unroll
-        for (int sl = 0; sl < 8; sl++) q[sl] = (_Float16)(float)qs[wv][q8k_slot_elem<Q6>(l, h, o, sl)];
-        const size_t F = (size_t)16 * b + 2 * l + h;
-        *(h8 *)(ws.a + ((2 * F + o) * ws.Mp + m) * 16) = q;
-    } else if (lane < 34) {
-        h8 q;
-#pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = (_Float16)(float)bsum[wv][8 * (lane - 32) + i];
-        *(h8 *)(ws.bs + ((size_t)b * ws.Mp + m) * 32 + 16 * (lane - 32)) = q;
-    } else if (lane == 34) {
-        ws.d8[(size_t)b * ws.Mp + m] = d;
-    }
+    q8k_quantize_wave<Q6>(v, lane, qs[wv], bsum[wv], Q8Planes{ws.a, ws.bs, ws.d8, ws.Mp}, m, b);
 }
 
 // ------------------------------------------------------------ main kernel
@@ -778,6 +720,11 @@ __global__ __launch_bounds__(256) void q8k_fill_zero_kernel(float *__restrict__ 
 }
 
 }  // namespace
+
+Q8Planes gemm_q8k_planes(void *wsp, int M, int K) {
+    const Q8Ws w = q8_carve((uint8_t *)wsp, M, K);
+    return Q8Planes{w.a, w.bs, w.d8, w.Mp};
+}
 
 size_t gemm_q8k_ws_bytes(const WeightsView &w, int M) {
     if (M <= 1 || w.dim_out == 0 || w.dim_in == 0) return 0;

@@ -47,13 +47,27 @@ struct RelaxedCapture {
     RelaxedCapture &operator=(const RelaxedCapture &) = delete;
 };
 
+// The activation planes of the q8k GEMM's workspace for M rows of dim_in K,
+// rows padded to Mp: octet o of fragment F = 16 b + 2 l + h of row m at
+// a + ((2 F + o) Mp + m) 16 (eight f16); the 16 bsums of (block b, row m) as
+// f16 at bs + (b Mp + m) 32; q8.d of (b, m) at d8[b Mp + m].
+struct Q8Planes {
+    uint8_t *a, *bs;
+    float *d8;
+    int Mp;
+};
+
 // Per-layer non-linear ops (uq_ops.hip).
 hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int rows, float eps, hipStream_t s);
 // rows of n, xs / ys floats apart in x / out; xb: normalise x + xb, written
-// to xsum when given; z: multiply the output by silu(z) (z laid out as out)
+// to xsum when given; z: multiply the output by silu(z) (z laid out as out);
+// q8: the outputs also quantized into these planes (all q8->Mp rows, the
+// padding rows as zero blocks; the Q6_K operand order when q6), as the q8k
+// GEMM's prep would quantize them, where rmsnorm_q8k_fits(n, rows)
 hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const float *w, int n, int rows, float eps,
                                hipStream_t s, const float *xb = nullptr, float *xsum = nullptr,
-                               const float *z = nullptr);
+                               const float *z = nullptr, const Q8Planes *q8 = nullptr, bool q6 = false);
+inline bool rmsnorm_q8k_fits(int n, int rows) { return rows >= 1 && n >= 256 && n <= 4096 && n % 256 == 0; }
 hipError_t launch_l2norm(float *data, int dim, int rows, float eps, hipStream_t s);
 int softmax_max_len();
 hipError_t launch_softmax(float *out, const float *x, int n, int rows, float scale, hipStream_t s);
@@ -214,6 +228,7 @@ hipError_t gemm_workspace(size_t need, hipStream_t s, uint8_t **buf, size_t *hav
 // workspace of wsb >= gemm_q8k_ws_bytes(w, M) bytes.
 hipError_t launch_gemm_q8k(const WeightsView &w, int M, const float *X, float *Y, hipStream_t s);
 size_t gemm_q8k_ws_bytes(const WeightsView &w, int M);
+Q8Planes gemm_q8k_planes(void *ws, int M, int K);
 // prepped: ws already holds X quantized by the previous launch_gemm_q8k_ws
 // call on it (same X contents, M, K, and Q6_K-ness of the weights), so the
 // quantization is skipped. Two fused forms for M >= 2 (hipErrorInvalidValue

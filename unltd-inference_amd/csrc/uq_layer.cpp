@@ -280,8 +280,9 @@ struct PrefillCtx {
     }
     // The projections w[0..n) of the same rows X: one launch over all their
     // column tiles when they share dtype and dim_in (each Y[i] the bits of its
-    // own gemm), else one gemm each
-    uq_status gemm_group(const uq_weights *w, int n, int nt, const float *X, float *const *Y) const {
+    // own gemm), else one gemm each; same_x as for gemm
+    uq_status gemm_group(const uq_weights *w, int n, int nt, const float *X, float *const *Y,
+                         bool same_x = false) const {
         uq::WeightsView v[uq::kGemmQ8kBatchMax];
         bool one = n <= uq::kGemmQ8kBatchMax;
         for (int i = 0; one && i < n; i++) {
@@ -289,11 +290,31 @@ struct PrefillCtx {
             one = v[i].dtype == v[0].dtype && v[i].dim_in == v[0].dim_in && v[i].row_bytes == v[0].row_bytes;
         }
         if (!one) {
-            for (int i = 0; i < n; i++) UQ_TRY(gemm(w[i], nt, X, Y[i], i > 0));
+            for (int i = 0; i < n; i++) UQ_TRY(gemm(w[i], nt, X, Y[i], same_x || i > 0));
             return UQ_OK;
         }
-        last_x = X, last_k = v[0].dim_in, last_m = nt, last_q6 = v[0].dtype == UQ_Q6_K;
-        return hip_st(uq::launch_gemm_q8k_batch_ws(v, n, nt, X, Y, gws, gws_bytes, s), fn);
+        const bool q6 = v[0].dtype == UQ_Q6_K;
+        const bool prepped = same_x && X == last_x && v[0].dim_in == last_k && nt == last_m && q6 == last_q6;
+        last_x = X, last_k = v[0].dim_in, last_m = nt, last_q6 = q6;
+        return hip_st(uq::launch_gemm_q8k_batch_ws(v, n, nt, X, Y, gws, gws_bytes, s, prepped), fn);
+    }
+    // The planes of the q8k workspace that the norm producing X (nt rows of
+    // n) can quantize its outputs into for the projection w that reads X next
+    // (then called with same_x): none where the GEMM's own prep runs (one
+    // row, rows the fused norm does not take, other dim_in)
+    struct NormQ8 {
+        uq::Q8Planes P;
+        bool on = false, q6 = false;
+        const uq::Q8Planes *ptr() const { return on ? &P : nullptr; }
+    };
+    NormQ8 norm_q8(uq_weights w, int nt, const float *X, int n) const {
+        NormQ8 r;
+        const uq::WeightsView v = uq::view(*wh(w));
+        if (nt < 2 || v.dim_in != n || !uq::rmsnorm_q8k_fits(n, nt) || gws_bytes < uq::gemm_q8k_ws_bytes(v, nt))
+            return r;
+        r.P = uq::gemm_q8k_planes(gws, nt, n), r.on = true, r.q6 = v.dtype == UQ_Q6_K;
+        last_x = X, last_k = v.dim_in, last_m = nt, last_q6 = r.q6;
+        return r;
     }
 };
 
@@ -303,13 +324,14 @@ struct PrefillCtx {
 uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_dims *d, int nt, const float *x_in,
                            uq_weights g, uq_weights u, uq_weights dn, const float *post_norm, float *const *A,
                            float *l_out) {
+    const PrefillCtx::NormQ8 q = c.norm_q8(g, nt, A[P_PN], (int)D.n);
     UQ_TRY(hip_st(uq::launch_rmsnorm_rows(A[P_PN], (int)D.n, x_in, (int)D.n, post_norm, (int)D.n, nt, d->rms_eps, c.s,
-                                          A[P_AO], A[P_RES]),
+                                          A[P_AO], A[P_RES], nullptr, q.ptr(), q.q6),
                   c.fn));
     {
         const uq_weights gu[2] = {g, u};
         float *const gy[2] = {A[P_G], A[P_U]};
-        UQ_TRY(c.gemm_group(gu, 2, nt, A[P_PN], gy));
+        UQ_TRY(c.gemm_group(gu, 2, nt, A[P_PN], gy, true));
     }
     if (nt >= 2)  // swiglu formed in the down projection's activation prep, l_out in its store
         return c.gemm(dn, nt, A[P_G], l_out, false, A[P_U], A[P_RES]);
@@ -509,11 +531,14 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
                        (need - prefill_arr_offset(D, 0, n_tokens, P_COUNT)) * 4};
     // 1-3) attn_norm of every token (:352-360), then qkv, z, beta, alpha of all
     // of them (:363-403)
-    UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
     {
+        const PrefillCtx::NormQ8 q = c.norm_q8(w->attn_qkv, nt, A[P_XN], (int)D.n);
+        UQ_TRY(hip_st(uq::launch_rmsnorm_rows(A[P_XN], (int)D.n, d_x_in, (int)D.n, w->attn_norm, (int)D.n, nt,
+                                              d->rms_eps, c.s, nullptr, nullptr, nullptr, q.ptr(), q.q6),
+                      fn));
         const uq_weights pw[4] = {w->attn_qkv, w->attn_gate, w->ssm_beta, w->ssm_alpha};
         float *const py[4] = {A[P_QKV], A[P_Z], A[P_BR], A[P_AL]};
-        UQ_TRY(c.gemm_group(pw, 4, nt, A[P_XN], py));
+        UQ_TRY(c.gemm_group(pw, 4, nt, A[P_XN], py, true));
     }
     // 4-6) the recurrent part: for head dims 64 and 128 the conv, norms and
     // gates of all tokens at once, the delta rule over the tokens in one
@@ -573,11 +598,14 @@ uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w
     auto at = [&](int node) { return d_ws + node_offset(D, n_ctx_max, node); };
     // 1-3) attn_norm of every token (:563-571); q|gate, k of all of them, and
     // v straight into the cache rows pos0 .. pos0 + n_tokens - 1 (:625-632)
-    UQ_TRY(hip_st(uq::launch_rmsnorm(A[P_XN], d_x_in, w->attn_norm, (int)D.n, nt, d->rms_eps, c.s), fn));
     {
+        const PrefillCtx::NormQ8 q = c.norm_q8(w->attn_q, nt, A[P_XN], (int)D.n);
+        UQ_TRY(hip_st(uq::launch_rmsnorm_rows(A[P_XN], (int)D.n, d_x_in, (int)D.n, w->attn_norm, (int)D.n, nt,
+                                              d->rms_eps, c.s, nullptr, nullptr, nullptr, q.ptr(), q.q6),
+                      fn));
         const uq_weights pw[3] = {w->attn_q, w->attn_k, w->attn_v};
         float *const py[3] = {A[P_QF], A[P_KR], d_v_cache + pos0 * kv_len};
-        UQ_TRY(c.gemm_group(pw, 3, nt, A[P_XN], py));
+        UQ_TRY(c.gemm_group(pw, 3, nt, A[P_XN], py, true));
     }
     // By chunks of tokens: 4) q / k norms and IMROPE of each token
     // (:585-642), k into its cache row, q into P_XN (free after the

@@ -17,6 +17,7 @@
 // the platform libm, so those results agree within about 1 ulp.
 #include "uq_device.h"
 #include "uq_internal.h"
+#include "uq_q8k_quant.h"
 
 namespace uq {
 
@@ -47,18 +48,41 @@ __device__ __forceinline__ float softplus1(float v) { return v > 20.0f ? v : log
 // the row normalised is x + xb (an f32 add), also written to xsum (the
 // residual and the norm after it, qwen35_forward.rs:525-530); with z the
 // output is multiplied by silu(z) (the gated norm, :495-511; z in the
-// output's layout). PT > 0 (n <= PT * TPB): a thread's elements are
+// output's layout). Q8 (PT * TPB >= n, n a multiple of 256): the outputs
+// also go to LDS and each wave quantizes 256-blocks of them into the q8k
+// GEMM's planes q8 (q8k_quantize_wave, as the GEMM's prep would from the
+// stored rows: the same f32 values); workgroups rows .. q8.Mp - 1 write the
+// padding rows' all-zero blocks. PT > 0 (n <= PT * TPB): a thread's elements are
 // loaded once, all before the sum, and kept in registers. Rows up to 4096
 // run on 1024 threads (four elements each: the per-thread chains of loads
 // and f64 adds are a quarter as long; 3.2 us per 4096-row in a graph against
 // 5.0 us on 256 threads).
-template <int PT, int TPB = OPS_TPB>
+template <int PT, int TPB = OPS_TPB, bool Q8 = false>
 __global__ __launch_bounds__(TPB) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
                                                       const float *__restrict__ w, int n, float eps, int xs,
                                                       int ys, const float *__restrict__ xb,
-                                                      float *__restrict__ xsum, const float *__restrict__ z) {
+                                                      float *__restrict__ xsum, const float *__restrict__ z,
+                                                      Q8Planes q8 = {}, int rows = 0, bool q6 = false) {
     __shared__ double red[TPB / 64];
     __shared__ float bc;
+    constexpr int QE = Q8 ? PT * TPB : 1, QW = Q8 ? TPB / 64 : 1;
+    __shared__ float yq[QE];
+    __shared__ int8_t qsw[QW][256];
+    __shared__ int bsw[QW][16];
+    const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;
+    auto quantize = [&](int b, const float (&v)[4]) {
+        if (q6)
+            q8k_quantize_wave<true>(v, lane, qsw[wq], bsw[wq], q8, blockIdx.x, b);
+        else
+            q8k_quantize_wave<false>(v, lane, qsw[wq], bsw[wq], q8, blockIdx.x, b);
+    };
+    if constexpr (Q8) {
+        if ((int)blockIdx.x >= rows) {  // a padding row of the planes
+            const float v0[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = wq; b < n / 256; b += TPB / 64) quantize(b, v0);
+            return;
+        }
+    }
     const float *xr = x + (size_t)blockIdx.x * xs;
     const float *xbr = xb ? xb + (size_t)blockIdx.x * xs : nullptr;
     float *yr = out + (size_t)blockIdx.x * ys;
@@ -98,6 +122,7 @@ __global__ __launch_bounds__(TPB) void rmsnorm_kernel(float *__restrict__ out, c
         float y = __fmul_rn(__fmul_rn(t, scale), wi);
         if (z) y = __fmul_rn(y, silu1(zi));
         yr[i] = y;
+        if constexpr (Q8) yq[i] = y;
     };
     if constexpr (PT > 0) {
 #pragma unroll
@@ -108,6 +133,15 @@ __global__ __launch_bounds__(TPB) void rmsnorm_kernel(float *__restrict__ out, c
     } else {
         for (int i = threadIdx.x; i < n; i += TPB)
             emit(i, val(i), w[i], z ? z[(size_t)blockIdx.x * ys + i] : 0.0f);
+    }
+    if constexpr (Q8) {
+        static_assert(PT > 0, "the row is held in LDS");
+        __syncthreads();  // every output in yq
+        for (int b = wq; b < n / 256; b += TPB / 64) {
+            const float4 f = *(const float4 *)(yq + 256 * b + 4 * lane);
+            const float v[4] = {f.x, f.y, f.z, f.w};
+            quantize(b, v);
+        }
     }
 }
 
@@ -1312,8 +1346,15 @@ hipError_t launch_rmsnorm(float *out, const float *x, const float *w, int n, int
 }
 
 hipError_t launch_rmsnorm_rows(float *out, int ys, const float *x, int xs, const float *w, int n, int rows, float eps,
-                               hipStream_t s, const float *xb, float *xsum, const float *z) {
+                               hipStream_t s, const float *xb, float *xsum, const float *z, const Q8Planes *q8,
+                               bool q6) {
     if (rows == 0 || n == 0) return hipSuccess;
+    if (q8) {  // rows quantized into the q8k GEMM's planes in the same launch
+        if (!rmsnorm_q8k_fits(n, rows) || q8->Mp < rows) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((rmsnorm_kernel<4, 1024, true>), dim3(q8->Mp), dim3(1024), 0, s, out, x, w, n, eps, xs, ys,
+                           xb, xsum, z, *q8, rows, q6);
+        return hipGetLastError();
+    }
     if (n <= OPS_TPB)
         hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(OPS_TPB), 0, s, out, x, w, n, eps, xs, ys, xb, xsum, z);
     else if (n <= 4 * 1024)  // wider rows: 1024 threads, four elements each
