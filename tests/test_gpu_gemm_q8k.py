@@ -171,7 +171,8 @@ def test_gemm_q8k_special_block_scales(dtype):
 @pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K])
 def test_gemm_q8k_edge_activations(dtype):
     """Rows of the quantizer's edge cases: zero rows and blocks, a negative
-    maximum, ties in |x|, subnormals, rows of very different magnitude, a
+    maximum, ties in |x| (within a lane's four elements and across lanes of
+    one block, either sign first), subnormals, rows of very different magnitude, a
     NaN (quantized to 0: the row stays finite) and an infinity (d = -inf:
     the row is NaN in the reference and here)."""
     K, N, M = 1024, 200, 36
@@ -186,6 +187,9 @@ def test_gemm_q8k_edge_activations(dtype):
     X[5, 17] = np.nan
     X[6, 600] = np.inf
     X[7, 1] = -np.inf
+    X[8, 10], X[8, 100] = -5.0e3, 5.0e3
+    X[9, 40], X[9, 200] = -7.0e3, 7.0e3
+    X[10, 300], X[10, 301], X[10, 509] = 9.0e3, -9.0e3, -9.0e3
     w = S.weights(dtype, N, K, seed=31 + dtype)
     Y = run(dtype, w, K, N, X)
     R = oracle_rows(dtype, w, K, N, X)

@@ -184,7 +184,6 @@ __global__ void quantize_q8k_kernel(const float *__restrict__ x, size_t nblocks,
     const float *c = x + b * 256;
     float v[4];
     float am = 0.0f;
-    int idx = 0x7FFFFFFF;
     float mx = 0.0f;
     for (int i = 0; i < 4; i++) {
         v[i] = c[lane * 4 + i];
@@ -192,20 +191,9 @@ __global__ void quantize_q8k_kernel(const float *__restrict__ x, size_t nblocks,
         if (a > am) {
             am = a;
             mx = v[i];
-            idx = lane * 4 + i;
         }
     }
-    // wave argmax: larger |x| wins; equal |x| -> smaller index wins
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oam = __shfl_xor(am, off);
-        const float omx = __shfl_xor(mx, off);
-        const int oidx = __shfl_xor(idx, off);
-        if (oam > am || (oam == am && oidx < idx)) {
-            am = oam;
-            mx = omx;
-            idx = oidx;
-        }
-    }
+    wave_first_absmax(am, mx);  // larger |x| wins; equal |x| -> smaller index wins
     uq_q8k_block *o = out + b;
     if (am == 0.0f) {
         for (int i = 0; i < 4; i++) o->qs[lane * 4 + i] = 0;

@@ -933,25 +933,14 @@ Segs one_seg(const WeightsView &w, const uint8_t *w2, float *y) {
 // v: the lane's four values of the block (elements 4 lane .. 4 lane + 3).
 __device__ __forceinline__ void quantize_vals_lds(const float (&v)[4], int lane, uint32_t *q, int *bs, float *dq) {
     float am = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
     for (int i = 0; i < 4; i++) {
         const float a = fabsf(v[i]);
         if (a > am) {
             am = a;
             mx = v[i];
-            idx = lane * 4 + i;
         }
     }
-    for (int off = 32; off >= 1; off >>= 1) {  // first strict argmax of |x|
-        const float oam = __shfl_xor(am, off);
-        const float omx = __shfl_xor(mx, off);
-        const int oidx = __shfl_xor(idx, off);
-        if (oam > am || (oam == am && oidx < idx)) {
-            am = oam;
-            mx = omx;
-            idx = oidx;
-        }
-    }
+    wave_first_absmax(am, mx);  // first strict argmax of |x|
     uint32_t packed = 0;
     int s = 0;
     if (am != 0.0f) {

@@ -7,6 +7,7 @@
 
 #include <cstdint>
 
+#include "uq_device.h"
 #include "uq_internal.h"
 #include "uq_mfma.h"
 #include "uq_q8k_tiles.h"
@@ -29,26 +30,15 @@ __device__ __forceinline__ void q8k_quantize_wave(const float (&v)[4], int lane,
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float am = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float a = fabsf(v[i]);
         if (a > am) {
             am = a;
             mx = v[i];
-            idx = lane * 4 + i;
         }
     }
-    // wave argmax: larger |x| wins; equal |x|, the smaller index
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oam = __shfl_xor(am, off), omx = __shfl_xor(mx, off);
-        const int oidx = __shfl_xor(idx, off);
-        if (oam > am || (oam == am && oidx < idx)) {
-            am = oam;
-            mx = omx;
-            idx = oidx;
-        }
-    }
+    wave_first_absmax(am, mx);  // larger |x| wins; equal |x|, the smaller index
     float d = 0.0f;
     int s = 0;
     if (am != 0.0f) {
