@@ -93,18 +93,6 @@ __device__ __forceinline__ void q8k_replay(const uint32_t *rr, int nblk, int k, 
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float expf_cr(float v) { return (float)exp((double)v); }
 
-// quantize_q8_k's argmax over a 256-block held four elements a lane
-// (quants.rs:250-290: the first strict maximum of |x| and its signed value):
-// from each lane's own first strict maximum am = |mx| over its elements
-// 4 lane .. 4 lane + 3, the largest am and the mx of the lowest lane that
-// holds it (its elements come first). am is never NaN (NaN > am is false).
-__device__ __forceinline__ void wave_first_absmax(float &am, float &mx) {
-    float wm = am;
-    for (int off = 32; off >= 1; off >>= 1) wm = fmaxf(wm, __shfl_xor(wm, off));
-    const int src = __builtin_ctzll(__ballot(am == wm));  // some lane holds wm
-    am = wm;
-    mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), src));
-}
 __device__ __forceinline__ float swiglu1(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_cr(-g))), u);
 }
@@ -166,6 +154,20 @@ __device__ __forceinline__ int group4_sum_i(int v) {
     v += dpp_int<0xB1>(v);
     v += dpp_int<0x4E>(v);
     return v;
+}
+
+// quantize_q8_k's argmax over a 256-block held four elements a lane
+// (quants.rs:250-290: the first strict maximum of |x| and its signed value):
+// from each lane's own first strict maximum am = |mx| over its elements
+// 4 lane .. 4 lane + 3, the largest am and the mx of the lowest lane that
+// holds it (its elements come first). am is never NaN (NaN > am is false)
+// and never negative, so its bit pattern orders like the value.
+__device__ __forceinline__ void wave_first_absmax(float &am, float &mx) {
+    const uint32_t g = group32_max_bits(__float_as_uint(am));
+    const float wm = __uint_as_float(max(__builtin_amdgcn_readlane(g, 0), __builtin_amdgcn_readlane(g, 32)));
+    const int src = __builtin_ctzll(__ballot(am == wm));  // some lane holds wm
+    am = wm;
+    mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), src));
 }
 
 // f64 DPP: the two halves move together

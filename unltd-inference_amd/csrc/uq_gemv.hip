@@ -957,8 +957,7 @@ __device__ __forceinline__ void quantize_vals_lds(const float (&v)[4], int lane,
         *dq = 0.0f;
     }
     q[lane] = packed;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s = group4_sum_i(s);
     if ((lane & 3) == 0) bs[lane >> 2] = s;
 }
 

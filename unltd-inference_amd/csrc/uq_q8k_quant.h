@@ -56,8 +56,7 @@ __device__ __forceinline__ void q8k_quantize_wave(const float (&v)[4], int lane,
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[lane * 4 + i] = 0;
     }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s = group4_sum_i(s);  // the bsum of the lane's quad: 16 elements
     if ((lane & 3) == 0) bsum[lane >> 2] = s;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
