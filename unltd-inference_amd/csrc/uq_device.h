@@ -156,6 +156,20 @@ __device__ __forceinline__ int group4_sum_i(int v) {
     return v;
 }
 
+// s + v[8g] + v[8g + 1] + ... + v[8g + 7] in that order (f32 adds), valid in
+// lane 8g of each group of eight (row_shl:k brings lane 8g + k, inside its
+// 16-lane row); other lanes get a value no one reads.
+__device__ __forceinline__ float group8_chain_first(float s, float v) {
+    s = __fadd_rn(s, v);
+    s = __fadd_rn(s, dpp_f<0x101>(v));
+    s = __fadd_rn(s, dpp_f<0x102>(v));
+    s = __fadd_rn(s, dpp_f<0x103>(v));
+    s = __fadd_rn(s, dpp_f<0x104>(v));
+    s = __fadd_rn(s, dpp_f<0x105>(v));
+    s = __fadd_rn(s, dpp_f<0x106>(v));
+    return __fadd_rn(s, dpp_f<0x107>(v));
+}
+
 // quantize_q8_k's argmax over a 256-block held four elements a lane
 // (quants.rs:250-290: the first strict maximum of |x| and its signed value):
 // from each lane's own first strict maximum am = |mx| over its elements

@@ -1131,9 +1131,8 @@ __global__ __launch_bounds__(TPB) void gemv_q8k_kernel(const Segs S, size_t row_
             const int r = lane >> 3, k = lane & 7;
             float sums = 0.0f, sumf = 0.0f;
             if (r < slot) q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, nblk, k, sums, sumf);
-            float s = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
-#pragma unroll
-            for (int kk = 0; kk < 8; kk++) s = __fadd_rn(s, __shfl(sums, (lane & ~7) + kk));
+            // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`; lane k = 0 holds s
+            const float s = group8_chain_first(sumf, sums);
             if (k == 0 && r < slot) {
                 const int Rr = row - (slot - 1 - r) * nwave, so = MULTI ? seg_of(S, Rr) : 0;
                 S.y[so][Rr - S.start[so]] = s;
@@ -1313,9 +1312,8 @@ gemv_q8k_stream_kernel(const Segs Sg, size_t row_bytes, int K, const float *__re
             for (int u = 0; u < NT; u++) {
                 float sums = 0.0f, sumf = 0.0f;
                 if (r < slot) q8k_replay<F::kMin>(rec + ((size_t)(u * R + r)) * nblk * 10, nblk, k, sums, sumf);
-                float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
-#pragma unroll
-                for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
+                // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`; lane k = 0 holds it
+                const float sv = group8_chain_first(sumf, sums);
                 out[u] = sv;
             }
             if (k == 0 && r < slot) {  // lane 0 always stores: NT == 1: one store, else three
@@ -1447,9 +1445,8 @@ __global__ __launch_bounds__(64 * KS * NG) void gemv_q8k_ks_kernel(const Segs Sg
                 const int r = lane >> 3, k = lane & 7;
                 float sums = 0.0f, sumf = 0.0f;
                 if (r < nr) q8k_replay<F::kMin>(rec + (size_t)(r) * nblk * 10, nblk, k, sums, sumf);
-                float sv = sumf;  // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`
-#pragma unroll
-                for (int kk = 0; kk < 8; kk++) sv = __fadd_rn(sv, __shfl(sums, (lane & ~7) + kk));
+                // Q6_K: sumf stays 0.0f, matching `let mut s = 0.0f32`; lane k = 0 holds it
+                const float sv = group8_chain_first(sumf, sums);
                 if (k == 0 && r < nr) {  // lane 0 always stores: one store instruction
                     const int Rr = G + (i + 1 - slot + r) * nG;
                     Sg.y[0][Rr] = sv;
