@@ -300,8 +300,8 @@ struct PrefillCtx {
     }
     // The planes of the q8k workspace that the norm producing X (nt rows of
     // n) can quantize its outputs into for the projection w that reads X next
-    // (then called with same_x): none where the GEMM's own prep runs (one
-    // row, rows the fused norm does not take, other dim_in)
+    // (then called with same_x = on): none where the GEMM's own prep runs
+    // (one row, rows the fused norm does not take, other dim_in)
     struct NormQ8 {
         uq::Q8Planes P;
         bool on = false, q6 = false;
@@ -331,7 +331,7 @@ uq_status ffn_tail_prefill(const PrefillCtx &c, const Dims &D, const uq_qwen35_d
     {
         const uq_weights gu[2] = {g, u};
         float *const gy[2] = {A[P_G], A[P_U]};
-        UQ_TRY(c.gemm_group(gu, 2, nt, A[P_PN], gy, true));
+        UQ_TRY(c.gemm_group(gu, 2, nt, A[P_PN], gy, q.on));
     }
     if (nt >= 2)  // swiglu formed in the down projection's activation prep, l_out in its store
         return c.gemm(dn, nt, A[P_G], l_out, false, A[P_U], A[P_RES]);
@@ -538,7 +538,7 @@ uq_status uq_gdn_layer_prefill_d(const uq_qwen35_dims *d, const uq_gdn_layer_w *
                       fn));
         const uq_weights pw[4] = {w->attn_qkv, w->attn_gate, w->ssm_beta, w->ssm_alpha};
         float *const py[4] = {A[P_QKV], A[P_Z], A[P_BR], A[P_AL]};
-        UQ_TRY(c.gemm_group(pw, 4, nt, A[P_XN], py, true));
+        UQ_TRY(c.gemm_group(pw, 4, nt, A[P_XN], py, q.on));
     }
     // 4-6) the recurrent part: for head dims 64 and 128 the conv, norms and
     // gates of all tokens at once, the delta rule over the tokens in one
@@ -605,7 +605,7 @@ uq_status uq_attn_layer_prefill_d(const uq_qwen35_dims *d, const uq_attn_layer_w
                       fn));
         const uq_weights pw[3] = {w->attn_q, w->attn_k, w->attn_v};
         float *const py[3] = {A[P_QF], A[P_KR], d_v_cache + pos0 * kv_len};
-        UQ_TRY(c.gemm_group(pw, 3, nt, A[P_XN], py, true));
+        UQ_TRY(c.gemm_group(pw, 3, nt, A[P_XN], py, q.on));
     }
     // By chunks of tokens: 4) q / k norms and IMROPE of each token
     // (:585-642), k into its cache row, q into P_XN (free after the
